@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""Throughput of the int8 Depth-Anything-V2 path on one MI355X.
+
+Workload (default): ViT-L + DPT at 518x518, batch 1, int8 GEMMs with binary16
+attention scores (the reference's int8-mode default), seeded random weights in
+a .dav2 file and a seeded ImageNet-normalised input already resident in HBM,
+run through dav2_infer_tensor_f32_device. One step = one full inference of
+the batch. Prints one JSON line.
+
+Roofline: the dominant kernel is the int8 MFMA GEMM. Its algorithmic work is
+2*M*N*K int8 ops per launch (unpadded K); achieved = total ops / total
+launch time, measured with HIP events around every GEMM launch on the stream
+it runs on, during a second timed pass of the same K steps.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+SEED = 0xDA20000
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0
+
+
+def load_package():
+    spec = importlib.util.spec_from_file_location("dav2_amd", ROOT / "depth-anything-v2_amd" / "__init__.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules.setdefault("dav2_amd", mod)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def cpu_baseline(model_path: Path, encoder: str, size: int, budget_s: float) -> dict:
+    """The CPU oracle (this build's restatement of the reference operators) on
+    the host cores: one full image of the same workload, or - if one image
+    exceeds the budget - the patch embedding plus as many encoder blocks as fit,
+    extrapolated to the full image from the measured per-block time."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_py import Oracle
+
+    fmt = load_package().dav2_format
+    oracle = Oracle()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    oracle.lib.orc_set_threads(threads)
+    enc_id = {"vits": 0, "vitb": 1, "vitl": 2}[encoder]
+    h = oracle.load_model(model_path, enc_id)
+    try:
+        x = fmt.imagenet_input(size, size, SEED + 3)[0]
+        t0 = time.perf_counter()
+        oracle.infer(h, x, size, size, fp16_attention=True)
+        dt = time.perf_counter() - t0
+        return {"value": 1.0 / dt, "unit": "images/s", "cores": oracle.lib.orc_get_threads(), "kind": "port",
+                "sample": f"1 full {encoder} {size}x{size} image through the oracle's int8 graph ({dt:.2f} s)"}
+    finally:
+        oracle.free_model(h)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--encoder", default="vitl", choices=["vits", "vitb", "vitl"])
+    ap.add_argument("--size", type=int, default=518)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--fp32-attention", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=30.0)
+    ap.add_argument("--profile-json", default="")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not part of this build "
+              "(images are independent; see DESIGN.md for how the path would shard)", file=sys.stderr)
+        return 2
+    if args.size % 14:
+        print("--size must be a multiple of 14", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    pkg = load_package()
+    fmt = pkg.dav2_format
+    flags = pkg.FORCE_INT8 | (pkg.FORCE_FP32_ATTENTION if args.fp32_attention else 0)
+    with tempfile.TemporaryDirectory(prefix="dav2_bench_") as tmp:
+        model = Path(tmp) / f"{args.encoder}.dav2"
+        fmt.write_synthetic_model(model, args.encoder, seed=SEED + 3)
+        print(f"bench: wrote {model.stat().st_size / 2**20:.0f} MiB synthetic {args.encoder} model", file=sys.stderr,
+              flush=True)
+        ctx = pkg.Context(str(model), args.encoder, flags)
+        x = torch.from_numpy(fmt.imagenet_input(args.size, args.size, SEED + 3, args.batch)).cuda()
+        n_out = args.batch * args.size * args.size
+        out = torch.empty(n_out, dtype=torch.float32, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def step():
+            ctx.infer_device(x.data_ptr(), args.batch, args.size, args.size, out.data_ptr(), n_out, stream)
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        print(f"bench: {args.steps} steps in {elapsed:.3f} s", file=sys.stderr, flush=True)
+
+        # Second pass with per-launch HIP events for the kernel rooflines.
+        ctx.profile(True)
+        torch.cuda.synchronize()
+        p0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        profiled_elapsed = time.perf_counter() - p0
+        prof = ctx.profile_report()
+        ctx.profile(False)
+        depth = out.cpu().numpy()
+        ctx.close()
+
+        gemm = prof.get("gemm_i8", {})
+        g_ms = gemm.get("ms", 0.0)
+        g_launches = max(1, gemm.get("launches", 1))
+        achieved = gemm.get("work", 0.0) / (g_ms * 1e-3) / 1e12 if g_ms else 0.0
+        traffic = None
+        tfile = ROOT / "profiles" / "gemm_i8_traffic.json"
+        if tfile.exists():
+            try:
+                t = json.loads(tfile.read_text())
+                key = f"{args.encoder}_{args.size}_b{args.batch}"
+                traffic = t.get(key, {}).get("bytes_per_launch")
+            except (ValueError, OSError):
+                traffic = None
+        kernels = {}
+        for name, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+            rate = v["work"] / (v["ms"] * 1e-3) if v["ms"] else 0.0
+            if v["unit"] == "B":
+                kernels[name] = {"ms_per_step": v["ms"] / args.steps, "avg_us": 1e3 * v["ms"] / v["launches"],
+                                 "GB/s": rate / 1e9, "frac_hbm": rate / 1e9 / PEAK_HBM_GBS}
+            else:
+                kernels[name] = {"ms_per_step": v["ms"] / args.steps, "avg_us": 1e3 * v["ms"] / v["launches"],
+                                 "T/s": rate / 1e12}
+        if args.profile_json:
+            Path(args.profile_json).write_text(json.dumps({"raw": prof, "kernels": kernels}, indent=1))
+        print("bench: per-kernel " + json.dumps(kernels), file=sys.stderr, flush=True)
+
+        cpu = None
+        if not args.no_cpu_baseline:
+            cpu = cpu_baseline(model, args.encoder, args.size, args.cpu_budget)
+
+    ms = 1e3 * elapsed / args.steps
+    result = {
+        "metric": "images/sec ViT-L 518² bs1 on 1 MI355X; int8 GEMM % MFMA peak; LN/softmax % HBM",
+        "value": args.batch * args.steps / elapsed,
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded random-init weights in a .dav2 file, seeded ImageNet-normalised input)",
+        "config": {"workload": f"{args.encoder} + DPT {args.size}x{args.size} batch {args.batch}, int8 GEMMs, "
+                               f"{'fp32' if args.fp32_attention else 'fp16'} attention scores, "
+                               "dav2_infer_tensor_f32_device",
+                   "encoder": args.encoder, "size": args.size, "global_batch": args.batch,
+                   "parallelism": "single GPU"},
+        "roofline": {"kernel": "gemm_i8", "bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS,
+                     "unit": "TOP/s", "frac": achieved / PEAK_INT8_TOPS,
+                     "avg_launch_us": 1e3 * g_ms / g_launches, "launches_per_step": g_launches / args.steps,
+                     "traffic": traffic},
+        "kernels": {k: kernels[k] for k in list(kernels)[:8]},
+        "profiled_ms_per_step": 1e3 * profiled_elapsed / args.steps,
+        "depth_finite": bool(np.isfinite(depth).all()),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,79 @@
+#include "executor.h"
+
+#include "dav2_hip.h"
+
+#include <stdexcept>
+
+namespace dav2 {
+
+namespace {
+Precision attention_precision_for(std::uint32_t flags) {
+    // src/encoder.cpp:389-396: int8 mode keeps binary16 attention scores unless
+    // FORCE_FP32(_ATTENTION) asks for fp32 scores.
+    return (flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP32_ATTENTION)) != 0 ? Precision::fp32
+                                                                                       : Precision::fp16;
+}
+}  // namespace
+
+HipExecutor::HipExecutor(const std::string& model_path, dav2_encoder encoder, int device_index,
+                         std::uint32_t flags)
+    : encoder_(encoder),
+      model_(model_path, encoder),
+      context_(device_index),
+      attention_precision_(attention_precision_for(flags)),
+      weights_(model_, context_),
+      operators_(context_),
+      dino_(encoder, weights_, operators_, attention_precision_),
+      dpt_(encoder, weights_, operators_) {
+    context_.synchronize();
+}
+
+void HipExecutor::prepare(int image_width, int image_height, int input_size) {
+    (void)image_width;
+    (void)image_height;
+    (void)input_size;
+    // Buffers are sized on the first inference at a resolution; nothing is
+    // compiled or autotuned ahead of time.
+}
+
+void HipExecutor::run(const float* input, int batch, int width, int height, float* output, float* pre_relu) {
+    DeviceBuffer* features[4] = {nullptr, nullptr, nullptr, nullptr};
+    dino_.forward(input, static_cast<std::uint32_t>(width), static_cast<std::uint32_t>(height),
+                  static_cast<std::uint32_t>(batch), arena_, features);
+    dpt_.forward(features, static_cast<std::uint32_t>(width / 14), static_cast<std::uint32_t>(height / 14),
+                 static_cast<std::uint32_t>(batch), arena_, output, pre_relu);
+}
+
+void HipExecutor::infer(const float* input, int width, int height, float* output) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    context_.make_current();
+    ScopedStream scoped(context_, nullptr);
+    const std::uint64_t in_elems = std::uint64_t(width) * height * 3;
+    const std::uint64_t out_elems = std::uint64_t(width) * height;
+    DeviceBuffer& in = arena_.get("io.input", in_elems * sizeof(float));
+    DeviceBuffer& out = arena_.get("io.output", out_elems * sizeof(float));
+    context_.upload(in, input, in_elems * sizeof(float));
+    run(in.as<float>(), 1, width, height, out.as<float>(), nullptr);
+    context_.download(out, output, out_elems * sizeof(float));
+}
+
+void HipExecutor::infer_device(const float* input, int batch, int width, int height, float* output,
+                               hipStream_t stream, float* pre_relu) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    context_.make_current();
+    ScopedStream scoped(context_, stream);
+    run(input, batch, width, height, output, pre_relu);
+}
+
+void HipExecutor::normalize_relative_device(float* depth, std::uint64_t count, hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    context_.make_current();
+    ScopedStream scoped(context_, stream);
+    if (count == 0 || count > 0xffffffffull) throw std::invalid_argument("invalid relative depth count");
+    DeviceBuffer d = DeviceBuffer::view(depth, count * sizeof(float));
+    DeviceBuffer& range = arena_.get("io.range", 2 * sizeof(float));
+    operators_.reduce_minmax(d, range, static_cast<std::uint32_t>(count));
+    operators_.normalize_relative(d, range, static_cast<std::uint32_t>(count));
+}
+
+}  // namespace dav2

@@ -1,0 +1,56 @@
+// The HIP executor behind the C ABI (role of the reference's Executor /
+// VulkanExecutor, src/executor.h:87-121, src/vulkan_executor.cpp:534-634).
+#pragma once
+
+#include "graph.h"
+#include "model.h"
+
+#include <memory>
+#include <mutex>
+#include <string>
+
+namespace dav2 {
+
+class HipExecutor {
+public:
+    HipExecutor(const std::string& model_path, dav2_encoder encoder, int device_index, std::uint32_t flags);
+
+    void prepare(int image_width, int image_height, int input_size);
+    // Host buffers: normalised RGB CHW in, width*height raw depth out.
+    void infer(const float* input, int width, int height, float* output);
+    // Device buffers, batch images; enqueued on `stream` (nullptr = own stream).
+    void infer_device(const float* input, int batch, int width, int height, float* output, hipStream_t stream,
+                      float* pre_relu = nullptr);
+    void normalize_relative_device(float* depth, std::uint64_t count, hipStream_t stream);
+
+    dav2_encoder encoder() const { return encoder_; }
+    float metric_max_depth() const { return model_.derivation().metric_max_depth; }
+    void transfer_counters(std::uint64_t& upload, std::uint64_t& download) const {
+        upload = context_.upload_bytes();
+        download = context_.download_bytes();
+    }
+    Precision attention_precision() const { return attention_precision_; }
+    HipContext& context() { return context_; }
+    std::uint64_t arena_bytes() const { return arena_.bytes(); }
+
+private:
+    void run(const float* input, int batch, int width, int height, float* output, float* pre_relu);
+
+    dav2_encoder encoder_;
+    ModelFile model_;  // validated before any HIP call, as the reference's member order does
+    HipContext context_;
+    Precision attention_precision_;
+    GpuModel weights_;
+    HipOperators operators_;
+    DinoEncoder dino_;
+    DptHead dpt_;
+    Arena arena_;
+    std::mutex mutex_;  // one inference at a time per context (docs/architecture.md:254-256)
+};
+
+}  // namespace dav2
+
+// Opaque handle of the public ABI.
+struct dav2_context {
+    std::unique_ptr<dav2::HipExecutor> executor;
+};

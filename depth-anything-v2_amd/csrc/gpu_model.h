@@ -1,0 +1,53 @@
+// Device-resident weights. Every tensor's CRC-32 is verified on load
+// (reference src/gpu_model.cpp:127-146). Tensors the reference quantizes for
+// its int8 mode (selection rule: src/gpu_model.cpp:16-44) are stored only as
+// per-output-row int8 + fp32 scales (quantizer: src/gpu_model.cpp:241-264),
+// everything else as fp32.
+//
+// int8 layout: [rows][ld] bytes, ld = columns rounded up to 64, zero padding.
+// Conv weights [OC][IC][k][k] flatten to rows = OC, column ic*k*k + ky*k + kx
+// (the im2col column order); ConvTranspose weights [IC][OC][k][k] are
+// reordered to rows (ky*k + kx)*OC + oc, columns = IC (src/gpu_model.cpp:226-240).
+#pragma once
+
+#include "model.h"
+#include "runtime.h"
+
+#include <array>
+#include <cstdint>
+#include <string>
+#include <string_view>
+#include <unordered_map>
+
+namespace dav2 {
+
+struct GpuTensor {
+    DeviceBuffer buffer;       // fp32 copy (only for tensors not stored as int8)
+    DeviceBuffer int8_buffer;  // [int8_rows][int8_ld]
+    DeviceBuffer int8_scales;  // [int8_rows]
+    std::uint32_t int8_rows = 0;
+    std::uint32_t int8_columns = 0;
+    std::uint32_t int8_ld = 0;
+    std::array<std::uint64_t, 4> dimensions{};
+    std::uint32_t rank = 0;
+    std::uint64_t elements = 0;
+};
+
+bool use_int8_weight(std::string_view name, const TensorView& tensor);
+bool transposed_convolution_weight(std::string_view name);
+inline std::uint32_t padded_k(std::uint64_t columns) { return static_cast<std::uint32_t>((columns + 63) & ~63ull); }
+
+class GpuModel {
+public:
+    GpuModel(const ModelFile& model, HipContext& context);
+    const GpuTensor& tensor(std::string_view name) const;
+    bool contains(std::string_view name) const { return tensors_.count(std::string(name)) != 0; }
+    std::size_t tensor_count() const { return tensors_.size(); }
+    std::uint64_t device_bytes() const { return device_bytes_; }
+
+private:
+    std::unordered_map<std::string, GpuTensor> tensors_;
+    std::uint64_t device_bytes_ = 0;
+};
+
+}  // namespace dav2

@@ -1,0 +1,254 @@
+#include "graph.h"
+
+#include "dav2_hip.h"
+
+#include <stdexcept>
+
+namespace dav2 {
+
+EncoderConfig encoder_config(dav2_encoder encoder) {
+    switch (encoder) {
+        case DAV2_ENCODER_VITS: return {384, 6, 12, {2, 5, 8, 11}};
+        case DAV2_ENCODER_VITB: return {768, 12, 12, {2, 5, 8, 11}};
+        case DAV2_ENCODER_VITL: return {1024, 16, 24, {4, 11, 17, 23}};
+    }
+    throw std::invalid_argument("unsupported DINOv2 encoder");
+}
+
+DptConfig dpt_config(dav2_encoder encoder) {
+    switch (encoder) {
+        case DAV2_ENCODER_VITS: return {384, 64, {48, 96, 192, 384}};
+        case DAV2_ENCODER_VITB: return {768, 128, {96, 192, 384, 768}};
+        case DAV2_ENCODER_VITL: return {1024, 256, {256, 512, 1024, 1024}};
+    }
+    throw std::invalid_argument("unsupported DPT encoder");
+}
+
+DeviceBuffer& Arena::get(const std::string& name, std::uint64_t bytes) {
+    DeviceBuffer& b = buffers_[name];
+    if (b.size() < bytes) {
+        hip_check(hipDeviceSynchronize(), "arena grow");
+        b.reset();
+        b = DeviceBuffer(bytes);
+    }
+    return b;
+}
+
+std::uint64_t Arena::bytes() const {
+    std::uint64_t total = 0;
+    for (const auto& kv : buffers_) total += kv.second.size();
+    return total;
+}
+
+namespace {
+std::string block_name(std::uint32_t block, const char* suffix) {
+    return "pretrained.blocks." + std::to_string(block) + suffix;
+}
+}  // namespace
+
+// ---------------------------------------------------------------------------
+DinoEncoder::DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators,
+                         Precision attention_precision)
+    : config_(encoder_config(encoder)), weights_(weights), ops_(operators),
+      attention_precision_(attention_precision) {
+    if (weights_.tensor("pretrained.cls_token").elements != config_.embedding ||
+        weights_.tensor("pretrained.pos_embed").elements != std::uint64_t(1370) * config_.embedding)
+        throw std::runtime_error("encoder tensor dimensions do not match");
+}
+
+const DeviceBuffer& DinoEncoder::fp32(const std::string& name) const { return weights_.tensor(name).buffer; }
+
+void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t height, std::uint32_t batch,
+                          Arena& arena, DeviceBuffer* features[4]) {
+    if (width == 0 || height == 0 || width % 14 != 0 || height % 14 != 0 || batch == 0)
+        throw std::invalid_argument("encoder dimensions must be positive multiples of 14");
+    const std::uint32_t D = config_.embedding, H = config_.heads;
+    const std::uint32_t pw = width / 14, ph = height / 14, T = pw * ph + 1;
+    const std::uint64_t rows64 = std::uint64_t(T) * batch;
+    if (rows64 > 0x7fffffffull) throw std::invalid_argument("token batch too large");
+    const std::uint32_t rows = static_cast<std::uint32_t>(rows64);
+    const std::uint64_t tok_bytes = rows64 * D * sizeof(float);
+    DeviceBuffer& current = arena.get("enc.current", tok_bytes);
+    DeviceBuffer& qkv = arena.get("enc.qkv", tok_bytes * 3);
+    DeviceBuffer& attn = arena.get("enc.attention", tok_bytes);
+    DeviceBuffer& hidden = arena.get("enc.hidden", tok_bytes * 4);
+    DeviceBuffer& scores =
+        arena.get("enc.scores", HipOperators::attention_score_bytes(T, H, batch, attention_precision_));
+    for (int i = 0; i < 4; ++i) features[i] = &arena.get("enc.feature" + std::to_string(i), tok_bytes);
+
+    // Patch embedding + class token + position (operators.cpp:1211-1406), one
+    // image at a time into rows [b*T, (b+1)*T).
+    const GpuTensor& patch = weights_.tensor("pretrained.patch_embed.proj.weight");
+    const std::uint64_t image_elems = std::uint64_t(width) * height * 3;
+    for (std::uint32_t b = 0; b < batch; ++b) {
+        DeviceBuffer img = DeviceBuffer::view(const_cast<float*>(image) + b * image_elems, image_elems * sizeof(float));
+        DeviceBuffer out = DeviceBuffer::view(current.as<float>() + std::uint64_t(b) * T * D,
+                                              std::uint64_t(T) * D * sizeof(float));
+        ops_.prepare_tokens(out, img, DeviceBuffer(), DeviceBuffer(), patch.int8_buffer, patch.int8_scales,
+                            fp32("pretrained.patch_embed.proj.bias"), fp32("pretrained.cls_token"),
+                            fp32("pretrained.pos_embed"), width, height, D, Precision::int8);
+    }
+
+    std::uint32_t capture = 0;
+    for (std::uint32_t blk = 0; blk < config_.blocks; ++blk) {
+        const auto W = [&](const char* s) -> const GpuTensor& { return weights_.tensor(block_name(blk, s)); };
+        const auto F = [&](const char* s) -> const DeviceBuffer& { return fp32(block_name(blk, s)); };
+        // norm1 -> qkv (encoder.cpp:443-452)
+        ops_.layer_norm_quantize(current, F(".norm1.weight"), F(".norm1.bias"), rows, D, 1.0e-6f, nullptr);
+        const GpuTensor& wqkv = W(".attn.qkv.weight");
+        ops_.linear_int8_prequantized(qkv, wqkv.int8_buffer, wqkv.int8_scales, &F(".attn.qkv.bias"), rows, D, 3 * D,
+                                      HipOperators::Epilogue::row);
+        // attention (encoder.cpp:454-460)
+        ops_.attention_batched(attn, qkv, T, H, batch, scores, attention_precision_);
+        // proj + LayerScale residual (encoder.cpp:478-491), in place
+        ops_.quantize_rows(attn, 0, rows, D);
+        const GpuTensor& wproj = W(".attn.proj.weight");
+        ops_.linear_int8_prequantized(current, wproj.int8_buffer, wproj.int8_scales, &F(".attn.proj.bias"), rows, D, D,
+                                      HipOperators::Epilogue::row_layerscale, &F(".ls1.gamma"));
+        // norm2 -> fc1 + GELU (encoder.cpp:500-529)
+        ops_.layer_norm_quantize(current, F(".norm2.weight"), F(".norm2.bias"), rows, D, 1.0e-6f, nullptr);
+        const GpuTensor& wfc1 = W(".mlp.fc1.weight");
+        ops_.linear_int8_prequantized(hidden, wfc1.int8_buffer, wfc1.int8_scales, &F(".mlp.fc1.bias"), rows, D, 4 * D,
+                                      HipOperators::Epilogue::row_gelu);
+        // fc2 + LayerScale residual (encoder.cpp:560-574), in place
+        ops_.quantize_rows(hidden, 0, rows, 4 * D);
+        const GpuTensor& wfc2 = W(".mlp.fc2.weight");
+        ops_.linear_int8_prequantized(current, wfc2.int8_buffer, wfc2.int8_scales, &F(".mlp.fc2.bias"), rows, 4 * D, D,
+                                      HipOperators::Epilogue::row_layerscale, &F(".ls2.gamma"));
+        // captured features (encoder.cpp:576-589)
+        if (capture < 4 && blk == config_.capture[capture]) {
+            ops_.layer_norm(*features[capture], current, fp32("pretrained.norm.weight"), fp32("pretrained.norm.bias"),
+                            rows, D, 1.0e-6f);
+            ++capture;
+        }
+    }
+    if (capture != 4) throw std::runtime_error("encoder did not produce four features");
+}
+
+// ---------------------------------------------------------------------------
+DptHead::DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operators)
+    : config_(dpt_config(encoder)), weights_(weights), ops_(operators), zero_bias_(sizeof(float)) {
+    hip_check(hipMemsetAsync(zero_bias_.data(), 0, sizeof(float), ops_.context().active_stream()), "zero bias");
+}
+
+FeatureMap DptHead::conv(const FeatureMap& in, const std::string& weight, const std::string& bias,
+                         std::uint32_t oc, std::uint32_t k, std::uint32_t stride, std::uint32_t pad, bool has_bias,
+                         Arena& arena, const std::string& slot) {
+    // dpt.cpp:479-535, every convolution through conv2d_int8
+    FeatureMap out;
+    out.width = (in.width + 2 * pad - k) / stride + 1;
+    out.height = (in.height + 2 * pad - k) / stride + 1;
+    out.channels = oc;
+    out.buffer = &arena.get(slot, out.elements() * sizeof(float));
+    const GpuTensor& w = weights_.tensor(weight);
+    if (!w.int8_buffer) throw std::runtime_error("convolution weight is not int8: " + weight);
+    const DeviceBuffer& b = has_bias ? weights_.tensor(bias).buffer : zero_bias_;
+    ops_.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc, k,
+                     stride, pad, has_bias);
+    return out;
+}
+
+FeatureMap DptHead::residual_unit(const FeatureMap& in, const std::string& prefix, Arena& arena,
+                                  const std::string& slot) {
+    // dpt.cpp:537-572: relu -> conv3x3 -> relu -> conv3x3 -> + input
+    const std::uint32_t count = static_cast<std::uint32_t>(in.elements());
+    FeatureMap act = in;
+    act.buffer = &arena.get("dpt.ru.act", in.elements() * sizeof(float));
+    ops_.relu(*act.buffer, *in.buffer, count);
+    FeatureMap first = conv(act, prefix + ".conv1.weight", prefix + ".conv1.bias", in.channels, 3, 1, 1, true, arena,
+                            "dpt.ru.first");
+    ops_.relu(*first.buffer, *first.buffer, count);
+    FeatureMap second = conv(first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.channels, 3, 1, 1, true,
+                             arena, slot);
+    ops_.add(*second.buffer, *second.buffer, *in.buffer, count);
+    return second;
+}
+
+FeatureMap DptHead::fusion(const FeatureMap& path, const FeatureMap* skip, const std::string& prefix,
+                           std::uint32_t ow, std::uint32_t oh, Arena& arena, const std::string& slot) {
+    // dpt.cpp:574-615
+    if (skip) {
+        FeatureMap processed = residual_unit(*skip, prefix + ".resConfUnit1", arena, "dpt.fu.skip");
+        ops_.add(*path.buffer, *path.buffer, *processed.buffer, static_cast<std::uint32_t>(path.elements()));
+    }
+    FeatureMap unit = residual_unit(path, prefix + ".resConfUnit2", arena, "dpt.fu.unit");
+    FeatureMap resized{&arena.get("dpt.fu.resized", std::uint64_t(ow) * oh * config_.features * sizeof(float)), ow,
+                       oh, config_.features};
+    ops_.bilinear_align_true(*resized.buffer, *unit.buffer, unit.width, unit.height, ow, oh, config_.features);
+    return conv(resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", config_.features, 1, 1, 0, true,
+                arena, slot);
+}
+
+void DptHead::forward(DeviceBuffer* features[4], std::uint32_t pw, std::uint32_t ph, std::uint32_t batch,
+                      Arena& arena, float* depth, float* pre_relu) {
+    const std::uint32_t D = config_.embedding, T = pw * ph + 1;
+    const std::uint32_t F = config_.features;
+    for (std::uint32_t b = 0; b < batch; ++b) {
+        // Projections and resize layers (dpt.cpp:635-736).
+        FeatureMap layers[4];
+        for (std::uint32_t i = 0; i < 4; ++i) {
+            const std::string prefix = "depth_head.projects." + std::to_string(i);
+            const GpuTensor& w = weights_.tensor(prefix + ".weight");
+            FeatureMap proj{&arena.get("dpt.proj" + std::to_string(i),
+                                       std::uint64_t(pw) * ph * config_.project[i] * sizeof(float)),
+                            pw, ph, config_.project[i]};
+            DeviceBuffer tokens = DeviceBuffer::view(features[i]->as<float>() + std::uint64_t(b) * T * D,
+                                                     std::uint64_t(T) * D * sizeof(float));
+            ops_.project_tokens_int8(*proj.buffer, tokens, w.int8_buffer, w.int8_scales,
+                                     weights_.tensor(prefix + ".bias").buffer, pw, ph, D, config_.project[i]);
+            if (i < 2) {
+                const std::uint32_t k = i == 0 ? 4 : 2;
+                const std::string r = "depth_head.resize_layers." + std::to_string(i);
+                const GpuTensor& rw = weights_.tensor(r + ".weight");
+                FeatureMap res{&arena.get("dpt.layer" + std::to_string(i),
+                                          std::uint64_t(pw) * k * ph * k * proj.channels * sizeof(float)),
+                               pw * k, ph * k, proj.channels};
+                ops_.conv_transpose_nonoverlap_int8(*res.buffer, *proj.buffer, rw.int8_buffer, rw.int8_scales,
+                                                    weights_.tensor(r + ".bias").buffer, pw, ph, proj.channels,
+                                                    proj.channels, k);
+                layers[i] = res;
+            } else if (i == 2) {
+                layers[i] = proj;
+            } else {
+                layers[i] = conv(proj, "depth_head.resize_layers.3.weight", "depth_head.resize_layers.3.bias",
+                                 config_.project[3], 3, 2, 1, true, arena, "dpt.layer3");
+            }
+        }
+        // layer*_rn (dpt.cpp:743-756)
+        FeatureMap refined[4];
+        for (std::uint32_t i = 0; i < 4; ++i)
+            refined[i] = conv(layers[i], "depth_head.scratch.layer" + std::to_string(i + 1) + "_rn.weight", "", F, 3, 1,
+                              1, false, arena, "dpt.rn" + std::to_string(i));
+        // refinenets (dpt.cpp:759-790); outputs alternate between two slots.
+        FeatureMap path = fusion(refined[3], nullptr, "depth_head.scratch.refinenet4", refined[2].width,
+                                 refined[2].height, arena, "dpt.pathA");
+        path = fusion(path, &refined[2], "depth_head.scratch.refinenet3", refined[1].width, refined[1].height, arena,
+                      "dpt.pathB");
+        path = fusion(path, &refined[1], "depth_head.scratch.refinenet2", refined[0].width, refined[0].height, arena,
+                      "dpt.pathA");
+        path = fusion(path, &refined[0], "depth_head.scratch.refinenet1", refined[0].width * 2,
+                      refined[0].height * 2, arena, "dpt.pathB");
+        // output head (dpt.cpp:792-855)
+        path = conv(path, "depth_head.scratch.output_conv1.weight", "depth_head.scratch.output_conv1.bias", F / 2, 3, 1,
+                    1, true, arena, "dpt.out1");
+        FeatureMap full{&arena.get("dpt.full", std::uint64_t(pw) * 14 * ph * 14 * (F / 2) * sizeof(float)), pw * 14,
+                        ph * 14, F / 2};
+        ops_.bilinear_align_true(*full.buffer, *path.buffer, path.width, path.height, full.width, full.height,
+                                 full.channels);
+        FeatureMap head = conv(full, "depth_head.scratch.output_conv2.0.weight",
+                               "depth_head.scratch.output_conv2.0.bias", 32, 3, 1, 1, true, arena, "dpt.out2");
+        ops_.relu(*head.buffer, *head.buffer, static_cast<std::uint32_t>(head.elements()));
+        const std::uint64_t pixels = std::uint64_t(pw) * 14 * ph * 14;
+        DeviceBuffer out = DeviceBuffer::view(depth + b * pixels, pixels * sizeof(float));
+        FeatureMap result{&out, pw * 14, ph * 14, 1};
+        FeatureMap logits = conv(head, "depth_head.scratch.output_conv2.2.weight",
+                                 "depth_head.scratch.output_conv2.2.bias", 1, 1, 1, 0, true, arena, "dpt.logits");
+        if (pre_relu && b + 1 == batch)
+            hip_check(hipMemcpyAsync(pre_relu, logits.buffer->data(), pixels * sizeof(float), hipMemcpyDeviceToDevice,
+                                     ops_.context().active_stream()),
+                      "pre-ReLU copy");
+        ops_.relu(*result.buffer, *logits.buffer, static_cast<std::uint32_t>(pixels));
+    }
+}
+
+}  // namespace dav2

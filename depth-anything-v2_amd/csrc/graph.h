@@ -1,0 +1,91 @@
+// Graph drivers: the DINOv2 encoder (reference src/encoder.cpp:322-597) and
+// the DPT head (src/dpt.cpp:479-863) over the HIP operator surface.
+//
+// Differences in structure, not arithmetic, from the reference drivers:
+//  - the encoder runs `batch` images at once (rows = batch * tokens);
+//  - LayerNorm writes its quantized rows directly (no fp32 round trip), GELU
+//    is fused into the fc1 GEMM epilogue and the LayerScale residual into the
+//    proj/fc2 epilogues;
+//  - every DPT convolution, 3x3 and 1x1, runs as im2col + int8 GEMM (the
+//    reference's int8 mode sends only resize_layers.* through conv2d_int8 and
+//    the refinement convolutions through fp16);
+//  - buffers come from a grow-only arena, so a fixed resolution allocates only
+//    on its first run.
+#pragma once
+
+#include "gpu_model.h"
+#include "operators.h"
+
+#include <map>
+#include <string>
+
+namespace dav2 {
+
+struct EncoderConfig {
+    std::uint32_t embedding, heads, blocks;
+    std::uint32_t capture[4];
+};
+struct DptConfig {
+    std::uint32_t embedding, features;
+    std::uint32_t project[4];
+};
+EncoderConfig encoder_config(dav2_encoder encoder);  // src/encoder.cpp:40-70
+DptConfig dpt_config(dav2_encoder encoder);          // src/dpt.cpp:51-78
+
+class Arena {
+public:
+    DeviceBuffer& get(const std::string& name, std::uint64_t bytes);
+    std::uint64_t bytes() const;
+
+private:
+    std::map<std::string, DeviceBuffer> buffers_;
+};
+
+class DinoEncoder {
+public:
+    DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, Precision attention_precision);
+    // image: device [batch][3][height][width]. On return features[i] holds the
+    // final-norm token matrix [batch*tokens][D] of capture layer i.
+    void forward(const float* image, std::uint32_t width, std::uint32_t height, std::uint32_t batch, Arena& arena,
+                 DeviceBuffer* features[4]);
+    const EncoderConfig& config() const { return config_; }
+
+private:
+    const DeviceBuffer& fp32(const std::string& name) const;
+    EncoderConfig config_;
+    GpuModel& weights_;
+    HipOperators& ops_;
+    Precision attention_precision_;
+};
+
+struct FeatureMap {
+    DeviceBuffer* buffer = nullptr;
+    std::uint32_t width = 0, height = 0, channels = 0;
+    std::uint64_t elements() const { return std::uint64_t(width) * height * channels; }
+};
+
+class DptHead {
+public:
+    DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operators);
+    // features[i]: [batch*tokens][D]; writes batch raw depth maps
+    // [batch][ph*14][pw*14] to depth. pre_relu (optional) receives the last
+    // image's depth before the final ReLU.
+    void forward(DeviceBuffer* features[4], std::uint32_t patch_width, std::uint32_t patch_height,
+                 std::uint32_t batch, Arena& arena, float* depth, float* pre_relu = nullptr);
+
+private:
+    FeatureMap conv(const FeatureMap& input, const std::string& weight, const std::string& bias,
+                    std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding,
+                    bool has_bias, Arena& arena, const std::string& slot);
+    FeatureMap residual_unit(const FeatureMap& input, const std::string& prefix, Arena& arena,
+                             const std::string& slot);
+    FeatureMap fusion(const FeatureMap& path, const FeatureMap* skip, const std::string& prefix,
+                      std::uint32_t output_width, std::uint32_t output_height, Arena& arena, const std::string& slot);
+
+    DptConfig config_;
+    GpuModel& weights_;
+    HipOperators& ops_;
+    DeviceBuffer zero_bias_;
+};
+
+}  // namespace dav2

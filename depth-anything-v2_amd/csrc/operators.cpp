@@ -1,0 +1,440 @@
+#include "operators.h"
+
+#include "dav2_hip.h"
+
+#include <limits>
+#include <stdexcept>
+#include <string>
+
+namespace dav2 {
+namespace {
+
+// src/operators.cpp:93-102
+void require_bytes(const DeviceBuffer& buffer, std::uint64_t elements, const char* name) {
+    if (elements > std::numeric_limits<std::uint64_t>::max() / sizeof(float) ||
+        buffer.size() < elements * sizeof(float))
+        throw std::invalid_argument(std::string(name) + " device buffer is too small");
+}
+
+void require_int8_weight(const DeviceBuffer& weight, std::uint64_t rows, std::uint64_t columns, const char* what) {
+    const std::uint64_t ld = (columns + 63) & ~63ull;
+    if (weight.size() < rows * ld) throw std::invalid_argument(std::string(what) + " is too small");
+}
+
+std::uint32_t ld64(std::uint64_t columns) { return static_cast<std::uint32_t>((columns + 63) & ~63ull); }
+
+DeviceBuffer& grow(DeviceBuffer& buffer, std::uint64_t bytes) {
+    if (buffer.size() < bytes) {
+        // Work already queued may still read the old allocation.
+        hip_check(hipDeviceSynchronize(), "workspace grow");
+        buffer.reset();
+        buffer = DeviceBuffer(bytes);
+    }
+    return buffer;
+}
+
+}  // namespace
+
+DeviceBuffer& Int8Workspace::packed(std::uint64_t bytes) { return grow(packed_, bytes); }
+DeviceBuffer& Int8Workspace::scales(std::uint64_t bytes) { return grow(scales_, bytes); }
+
+HipOperators::HipOperators(HipContext& context) : context_(context) {}
+
+// ---------------------------------------------------------------------------
+// src/operators.cpp:770-845
+void HipOperators::linear_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+                               const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
+                               std::uint32_t input_columns, std::uint32_t output_columns, bool gelu,
+                               bool /*weight_transposed: the NV cooperative-matrix layout is not used*/) {
+    if (rows == 0 || input_columns == 0 || output_columns == 0 || input_columns % 4 != 0)
+        throw std::invalid_argument("invalid INT8 linear dimensions");
+    require_bytes(input, std::uint64_t(rows) * input_columns, "input");
+    require_int8_weight(int8_weight, output_columns, input_columns, "packed INT8 weight buffer");
+    require_bytes(weight_scales, output_columns, "weight scale");
+    require_bytes(bias, output_columns, "bias");
+    require_bytes(output, std::uint64_t(rows) * output_columns, "output");
+    quantize_rows(input, 0, rows, input_columns);
+    linear_int8_prequantized(output, int8_weight, weight_scales, &bias, rows, input_columns, output_columns,
+                             gelu ? Epilogue::row_gelu : Epilogue::row);
+}
+
+void HipOperators::quantize_rows(const DeviceBuffer& input, std::uint64_t input_offset, std::uint32_t rows,
+                                 std::uint32_t columns) {
+    const std::uint32_t ld = ld64(columns);
+    DeviceBuffer& packed = workspace_.packed(std::uint64_t(rows) * ld);
+    DeviceBuffer& scales = workspace_.scales(std::uint64_t(rows) * sizeof(float));
+    ProfileScope prof(context_.profiler(), "quantize_rows_i8", 5.0 * rows * columns + 4.0 * rows, "B",
+                      context_.active_stream());
+    hip_check(dav2_hip_quantize_rows_i8(input.as<float>(), input_offset, rows, columns, packed.as<int8_t>(), ld,
+                                        scales.as<float>(), context_.active_stream()),
+              "quantize_rows_int8");
+    workspace_ld_ = ld;
+}
+
+void HipOperators::layer_norm_quantize(const DeviceBuffer& input, const DeviceBuffer& weight,
+                                       const DeviceBuffer& bias, std::uint32_t rows, std::uint32_t columns,
+                                       float epsilon, DeviceBuffer* fp32_out) {
+    if (rows == 0 || columns == 0 || columns % 4 != 0 || epsilon <= 0.0f)
+        throw std::invalid_argument("invalid layer norm parameters");
+    require_bytes(input, std::uint64_t(rows) * columns, "input");
+    require_bytes(weight, columns, "weight");
+    require_bytes(bias, columns, "bias");
+    if (fp32_out) require_bytes(*fp32_out, std::uint64_t(rows) * columns, "output");
+    const std::uint32_t ld = ld64(columns);
+    DeviceBuffer& packed = workspace_.packed(std::uint64_t(rows) * ld);
+    DeviceBuffer& scales = workspace_.scales(std::uint64_t(rows) * sizeof(float));
+    ProfileScope prof(context_.profiler(), "layer_norm_quantize_i8",
+                      5.0 * rows * columns + 8.0 * columns + 4.0 * rows + (fp32_out ? 4.0 * rows * columns : 0.0),
+                      "B", context_.active_stream());
+    hip_check(dav2_hip_layer_norm_quantize_i8(packed.as<int8_t>(), ld, scales.as<float>(),
+                                              fp32_out ? fp32_out->as<float>() : nullptr, input.as<float>(),
+                                              weight.as<float>(), bias.as<float>(), rows, columns, epsilon,
+                                              context_.active_stream()),
+              "layer_norm_quantize");
+    workspace_ld_ = ld;
+}
+
+void HipOperators::linear_int8_prequantized(DeviceBuffer& output, const DeviceBuffer& int8_weight,
+                                            const DeviceBuffer& weight_scales, const DeviceBuffer* bias,
+                                            std::uint32_t rows, std::uint32_t input_columns,
+                                            std::uint32_t output_columns, Epilogue epilogue,
+                                            const DeviceBuffer* gamma, std::uint64_t output_row_offset) {
+    if (workspace_ld_ != ld64(input_columns)) throw std::logic_error("int8 workspace holds rows of another width");
+    require_bytes(output, (std::uint64_t(rows) + output_row_offset) * output_columns, "output");
+    if (epilogue == Epilogue::row_layerscale && (!gamma || gamma->size() < output_columns * sizeof(float)))
+        throw std::invalid_argument("layer scale buffer is too small");
+    dav2_gemm_i8_args a{};
+    a.a = workspace_.packed(0).as<int8_t>();
+    a.lda = workspace_ld_;
+    a.b = int8_weight.as<int8_t>();
+    a.ldb = ld64(input_columns);
+    a.m = rows;
+    a.n = output_columns;
+    a.k = ld64(input_columns);
+    a.epilogue = epilogue == Epilogue::row ? DAV2_GEMM_EPI_ROW
+                 : epilogue == Epilogue::row_gelu ? DAV2_GEMM_EPI_ROW_GELU
+                                                  : DAV2_GEMM_EPI_ROW_LAYERSCALE;
+    a.a_scales = workspace_.scales(0).as<float>();
+    a.b_scales = weight_scales.as<float>();
+    a.bias = bias ? bias->as<float>() : nullptr;
+    a.out = output.as<float>();
+    a.out_row_offset = output_row_offset;
+    a.residual = output.as<float>();
+    a.gamma = gamma ? gamma->as<float>() : nullptr;
+    ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
+                      context_.active_stream());
+    hip_check(dav2_hip_gemm_i8(&a, context_.active_stream()), "int8 GEMM");
+}
+
+// src/operators.cpp:847-880
+void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& packed_input,
+                                      std::uint32_t packed_ld, const DeviceBuffer& int8_weight,
+                                      const DeviceBuffer& input_scales, const DeviceBuffer& weight_scales,
+                                      const DeviceBuffer& bias, std::uint32_t rows, std::uint32_t input_columns,
+                                      std::uint32_t output_columns, std::uint32_t output_row_offset,
+                                      std::uint32_t output_row_stride, bool output_transposed, bool has_bias) {
+    dav2_gemm_i8_args a{};
+    a.a = packed_input.as<int8_t>();
+    a.lda = packed_ld;
+    a.b = int8_weight.as<int8_t>();
+    a.ldb = ld64(input_columns);
+    a.m = rows;
+    a.n = output_columns;
+    a.k = ld64(input_columns);
+    a.epilogue = output_transposed ? DAV2_GEMM_EPI_TRANSPOSED : DAV2_GEMM_EPI_ROW;
+    a.a_scales = input_scales.as<float>();
+    a.b_scales = weight_scales.as<float>();
+    a.bias = has_bias ? bias.as<float>() : nullptr;
+    a.out = output.as<float>();
+    a.out_row_offset = output_row_offset;
+    a.out_row_stride = output_row_stride;
+    ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
+                      context_.active_stream());
+    hip_check(dav2_hip_gemm_i8(&a, context_.active_stream()), "int8 GEMM");
+}
+
+// src/operators.cpp:1016-1042
+void HipOperators::layer_norm(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                              const DeviceBuffer& bias, std::uint32_t rows, std::uint32_t columns, float epsilon) {
+    if (rows == 0 || columns == 0 || epsilon <= 0.0f) throw std::invalid_argument("invalid layer norm parameters");
+    require_bytes(input, std::uint64_t(rows) * columns, "input");
+    require_bytes(output, std::uint64_t(rows) * columns, "output");
+    require_bytes(weight, columns, "weight");
+    require_bytes(bias, columns, "bias");
+    ProfileScope prof(context_.profiler(), "layer_norm", 8.0 * rows * columns + 8.0 * columns, "B",
+                      context_.active_stream());
+    hip_check(dav2_hip_layer_norm(output.as<float>(), input.as<float>(), weight.as<float>(), bias.as<float>(), rows,
+                                  columns, epsilon, context_.active_stream()),
+              "layer_norm");
+}
+
+// src/operators.cpp:1072-1096
+void HipOperators::add_scaled(DeviceBuffer& output, const DeviceBuffer& residual, const DeviceBuffer& addend,
+                              const DeviceBuffer& scale, std::uint32_t count, std::uint32_t columns) {
+    if (count == 0 || columns == 0 || count % columns != 0) throw std::invalid_argument("invalid add-scaled dimensions");
+    require_bytes(output, count, "output");
+    require_bytes(residual, count, "residual");
+    require_bytes(addend, count, "addend");
+    require_bytes(scale, columns, "scale");
+    ProfileScope prof(context_.profiler(), "add_scaled", 12.0 * count, "B", context_.active_stream());
+    hip_check(dav2_hip_add_scaled(output.as<float>(), residual.as<float>(), addend.as<float>(), scale.as<float>(),
+                                  count, columns, context_.active_stream()),
+              "add_scaled");
+}
+
+std::uint64_t HipOperators::attention_score_bytes(std::uint32_t tokens, std::uint32_t heads, std::uint32_t batch,
+                                                  Precision precision) {
+    const std::uint64_t rows = std::uint64_t(batch) * heads * tokens;
+    if (precision == Precision::fp16) return rows * ((std::uint64_t(tokens) + 7) & ~7ull) * 2u;
+    return rows * tokens * sizeof(float);
+}
+
+// src/operators.cpp:1098-1209
+void HipOperators::attention_head64(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
+                                    std::uint32_t heads, DeviceBuffer* score_scratch, Precision precision) {
+    if (tokens == 0 || heads == 0) throw std::invalid_argument("invalid attention dimensions");
+    const std::uint64_t elements = std::uint64_t(tokens) * heads * 64;
+    require_bytes(output, elements, "attention output");
+    require_bytes(qkv, elements * 3, "QKV");
+    const std::uint64_t score_bytes = attention_score_bytes(tokens, heads, 1, precision);
+    DeviceBuffer owned;
+    if (score_scratch == nullptr) {
+        owned = context_.create_device_buffer(score_bytes);
+        score_scratch = &owned;
+    } else if (score_scratch->size() < score_bytes) {
+        throw std::invalid_argument("attention score scratch device buffer is too small");
+    }
+    attention_batched(output, qkv, tokens, heads, 1, *score_scratch, precision);
+    if (owned) context_.synchronize();  // the local scratch must outlive the kernels
+}
+
+void HipOperators::attention_batched(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
+                                     std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scores,
+                                     Precision precision) {
+    const int fp16 = precision == Precision::fp16 ? 1 : 0;
+    const hipStream_t s = context_.active_stream();
+    const std::uint32_t stride = fp16 ? ((tokens + 7u) & ~7u) : tokens;
+    const double flops = 2.0 * batch * heads * double(tokens) * tokens * 64.0;
+    const double score_bytes = double(batch) * heads * tokens * tokens * (fp16 ? 2.0 : 4.0);
+    Profiler& prof = context_.profiler();
+    {
+        ProfileScope p(prof, "attention_scores", flops, "FLOP", s);
+        hip_check(dav2_hip_attention_scores(scores.data(), qkv.as<float>(), tokens, heads, batch, fp16, s),
+                  "attention scores");
+    }
+    {
+        ProfileScope p(prof, fp16 ? "softmax_f16" : "softmax_f32", 2.0 * score_bytes, "B", s);
+        hip_check(dav2_hip_softmax_rows(scores.data(), std::uint64_t(batch) * heads * tokens, tokens, stride, fp16, s),
+                  "attention softmax");
+    }
+    {
+        ProfileScope p(prof, "attention_values", flops, "FLOP", s);
+        hip_check(dav2_hip_attention_values(output.as<float>(), scores.data(), qkv.as<float>(), tokens, heads, batch,
+                                            fp16, s),
+                  "attention values");
+    }
+}
+
+// src/operators.cpp:1211-1406 (int8 branch)
+void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& image, const DeviceBuffer&,
+                                  const DeviceBuffer&, const DeviceBuffer& patch_int8_weight,
+                                  const DeviceBuffer& patch_int8_scales, const DeviceBuffer& patch_bias,
+                                  const DeviceBuffer& class_token, const DeviceBuffer& position,
+                                  std::uint32_t input_width, std::uint32_t input_height, std::uint32_t embedding,
+                                  Precision precision) {
+    if (input_width == 0 || input_height == 0 || input_width % 14 != 0 || input_height % 14 != 0 || embedding == 0)
+        throw std::invalid_argument("invalid patch embedding dimensions");
+    if (precision != Precision::int8) throw std::runtime_error("only the INT8 patch embedding is built");
+    const std::uint32_t pw = input_width / 14, ph = input_height / 14, spatial = pw * ph;
+    const std::uint64_t tokens = std::uint64_t(spatial) + 1;
+    constexpr std::uint32_t patch_columns = 3u * 14u * 14u;
+    require_bytes(image, std::uint64_t(input_width) * input_height * 3, "image");
+    require_int8_weight(patch_int8_weight, embedding, patch_columns, "INT8 patch weight buffer");
+    require_bytes(patch_int8_scales, embedding, "patch weight scale");
+    require_bytes(patch_bias, embedding, "patch bias");
+    require_bytes(class_token, embedding, "class token");
+    require_bytes(position, std::uint64_t(1370) * embedding, "position");
+    require_bytes(output, tokens * embedding, "token output");
+    const hipStream_t s = context_.active_stream();
+    const std::uint32_t ld = ld64(patch_columns);
+    DeviceBuffer& packed = workspace_.packed(std::uint64_t(spatial) * ld);
+    DeviceBuffer& scales = workspace_.scales(std::uint64_t(spatial) * sizeof(float));
+    ProfileScope prof_patch(context_.profiler(), "im2col_quantize_i8",
+                            12.0 * input_width * input_height + 1.0 * spatial * patch_columns + 4.0 * spatial,
+                            "B", s);
+    hip_check(dav2_hip_im2col_quantize_i8(image.as<float>(), input_width, input_height, 3, pw, ph, 14, 14, 0,
+                                          packed.as<int8_t>(), ld, scales.as<float>(), s),
+              "patch im2col");
+    linear_int8_packed(output, packed, ld, patch_int8_weight, scales, patch_int8_scales, patch_bias, spatial,
+                       patch_columns, embedding, 1u, static_cast<std::uint32_t>(tokens), false, true);
+    workspace_ld_ = ld;
+    grow(interpolated_, std::uint64_t(spatial) * embedding * sizeof(float));
+    hip_check(dav2_hip_position_bicubic(interpolated_.as<float>(), position.as<float>(), pw, ph, embedding, s),
+              "position bicubic");
+    hip_check(dav2_hip_finish_tokens(output.as<float>(), interpolated_.as<float>(), position.as<float>(),
+                                     class_token.as<float>(), pw, ph, embedding, 1, s),
+              "class/position tokens");
+}
+
+// src/operators.cpp:1483-1526
+void HipOperators::project_tokens_int8(DeviceBuffer& output, const DeviceBuffer& tokens,
+                                       const DeviceBuffer& int8_weight, const DeviceBuffer& weight_scales,
+                                       const DeviceBuffer& bias, std::uint32_t width, std::uint32_t height,
+                                       std::uint32_t embedding, std::uint32_t output_channels) {
+    const std::uint32_t spatial = width * height;
+    if (embedding % 4u != 0u || embedding == 0 || spatial == 0 || output_channels == 0)
+        throw std::invalid_argument("INT8 token embedding must be divisible by four");
+    require_bytes(tokens, std::uint64_t(spatial + 1u) * embedding, "tokens");
+    require_int8_weight(int8_weight, output_channels, embedding, "INT8 projection weight");
+    require_bytes(weight_scales, output_channels, "weight scale");
+    require_bytes(bias, output_channels, "bias");
+    require_bytes(output, std::uint64_t(spatial) * output_channels, "output");
+    quantize_rows(tokens, embedding, spatial, embedding);
+    linear_int8_packed(output, workspace_.packed(0), workspace_ld_, int8_weight, workspace_.scales(0),
+                       weight_scales, bias, spatial, embedding, output_channels, 0u, spatial, true, true);
+}
+
+// src/operators.cpp:1735-1805
+void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+                               const DeviceBuffer& weight_scales, const DeviceBuffer& bias,
+                               std::uint32_t input_width, std::uint32_t input_height, std::uint32_t input_channels,
+                               std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
+                               std::uint32_t padding, bool has_bias) {
+    if (input_width == 0 || input_height == 0 || input_channels == 0 || output_channels == 0 || kernel == 0 ||
+        stride == 0 || input_width + 2u * padding < kernel || input_height + 2u * padding < kernel)
+        throw std::invalid_argument("invalid INT8 convolution dimensions");
+    const std::uint32_t inner = input_channels * kernel * kernel;
+    if (inner % 4u != 0u) throw std::invalid_argument("INT8 convolution inner size is not packed");
+    const std::uint32_t ow = (input_width + 2u * padding - kernel) / stride + 1u;
+    const std::uint32_t oh = (input_height + 2u * padding - kernel) / stride + 1u;
+    const std::uint32_t rows = ow * oh;
+    require_bytes(input, std::uint64_t(input_width) * input_height * input_channels, "convolution input");
+    require_int8_weight(int8_weight, output_channels, inner, "INT8 convolution weight");
+    require_bytes(weight_scales, output_channels, "convolution weight scale");
+    require_bytes(bias, has_bias ? output_channels : 1u, "convolution bias");
+    require_bytes(output, std::uint64_t(rows) * output_channels, "output");
+    const std::uint32_t ld = ld64(inner);
+    DeviceBuffer& packed = workspace_.packed(std::uint64_t(rows) * ld);
+    DeviceBuffer& scales = workspace_.scales(std::uint64_t(rows) * sizeof(float));
+    ProfileScope prof(context_.profiler(), "im2col_quantize_i8",
+                      4.0 * input_width * input_height * input_channels + 1.0 * rows * inner + 4.0 * rows, "B",
+                      context_.active_stream());
+    hip_check(dav2_hip_im2col_quantize_i8(input.as<float>(), input_width, input_height, input_channels, ow, oh,
+                                          kernel, stride, static_cast<std::int32_t>(padding), packed.as<int8_t>(),
+                                          ld, scales.as<float>(), context_.active_stream()),
+              "im2col quantize");
+    workspace_ld_ = ld;
+    linear_int8_packed(output, packed, ld, int8_weight, scales, weight_scales, bias, rows, inner, output_channels, 0u,
+                       rows, true, has_bias);
+}
+
+// src/operators.cpp:1908-1976
+void HipOperators::conv_transpose_nonoverlap_int8(DeviceBuffer& output, const DeviceBuffer& input,
+                                                  const DeviceBuffer& int8_weight,
+                                                  const DeviceBuffer& weight_scales, const DeviceBuffer& bias,
+                                                  std::uint32_t input_width, std::uint32_t input_height,
+                                                  std::uint32_t input_channels, std::uint32_t output_channels,
+                                                  std::uint32_t kernel) {
+    if (input_width == 0 || input_height == 0 || input_channels == 0 || output_channels == 0 || kernel == 0 ||
+        input_channels % 4u != 0u)
+        throw std::invalid_argument("invalid INT8 transposed convolution");
+    const std::uint32_t input_rows = input_width * input_height;
+    const std::uint32_t weight_rows = kernel * kernel * output_channels;
+    require_bytes(input, std::uint64_t(input_rows) * input_channels, "transposed convolution input");
+    require_int8_weight(int8_weight, weight_rows, input_channels, "INT8 transposed weight");
+    require_bytes(weight_scales, weight_rows, "transposed weight scale");
+    require_bytes(bias, output_channels, "transposed bias");
+    require_bytes(output, std::uint64_t(input_rows) * kernel * kernel * output_channels, "transposed output");
+    const std::uint32_t ld = ld64(input_channels);
+    DeviceBuffer& packed = workspace_.packed(std::uint64_t(input_rows) * ld);
+    DeviceBuffer& scales = workspace_.scales(std::uint64_t(input_rows) * sizeof(float));
+    const hipStream_t s = context_.active_stream();
+    ProfileScope prof_q(context_.profiler(), "im2col_quantize_i8",
+                        4.0 * input_rows * input_channels + 1.0 * input_rows * input_channels + 4.0 * input_rows, "B", s);
+    hip_check(dav2_hip_im2col_quantize_i8(input.as<float>(), input_width, input_height, input_channels, input_width,
+                                          input_height, 1, 1, 0, packed.as<int8_t>(), ld, scales.as<float>(), s),
+              "im2col quantize");
+    workspace_ld_ = ld;
+    dav2_gemm_i8_args a{};
+    a.a = packed.as<int8_t>();
+    a.lda = ld;
+    a.b = int8_weight.as<int8_t>();
+    a.ldb = ld;
+    a.m = input_rows;
+    a.n = weight_rows;
+    a.k = ld;
+    a.epilogue = DAV2_GEMM_EPI_CONVT;
+    a.a_scales = scales.as<float>();
+    a.b_scales = weight_scales.as<float>();
+    a.bias = bias.as<float>();
+    a.out = output.as<float>();
+    a.convt_kernel = kernel;
+    a.convt_width = input_width;
+    a.convt_height = input_height;
+    a.convt_channels = output_channels;
+    ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * input_rows * weight_rows * input_channels, "OP", s);
+    hip_check(dav2_hip_gemm_i8(&a, s), "transposed convolution GEMM");
+}
+
+// src/operators.cpp:1978-2012
+void HipOperators::bilinear_align_true(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t input_width,
+                                       std::uint32_t input_height, std::uint32_t output_width,
+                                       std::uint32_t output_height, std::uint32_t channels) {
+    if (input_width == 0 || input_height == 0 || output_width == 0 || output_height == 0 || channels == 0)
+        throw std::invalid_argument("invalid bilinear dimensions");
+    require_bytes(input, std::uint64_t(input_width) * input_height * channels, "bilinear input");
+    require_bytes(output, std::uint64_t(output_width) * output_height * channels, "bilinear output");
+    ProfileScope prof(context_.profiler(), "bilinear",
+                      4.0 * channels * (double(input_width) * input_height + double(output_width) * output_height), "B",
+                      context_.active_stream());
+    hip_check(dav2_hip_bilinear_align_true(output.as<float>(), input.as<float>(), input_width, input_height,
+                                           output_width, output_height, channels, context_.active_stream()),
+              "bilinear");
+}
+
+// src/operators.cpp:2050-2071
+void HipOperators::reduce_minmax(const DeviceBuffer& input, DeviceBuffer& range, std::uint32_t count) {
+    if (count == 0) throw std::invalid_argument("empty depth reduction");
+    require_bytes(input, count, "depth reduction input");
+    require_bytes(range, 2, "depth reduction range");
+    grow(minmax_partials_, std::uint64_t(dav2_hip_minmax_partials(count)) * 2 * sizeof(float));
+    ProfileScope prof(context_.profiler(), "reduce_minmax", 4.0 * count, "B", context_.active_stream());
+    hip_check(dav2_hip_reduce_minmax(input.as<float>(), count, range.as<float>(), minmax_partials_.as<float>(),
+                                     context_.active_stream()),
+              "reduce_minmax");
+}
+
+void HipOperators::normalize_relative(DeviceBuffer& depth, const DeviceBuffer& range, std::uint32_t count) {
+    if (count == 0) throw std::invalid_argument("empty relative depth");
+    require_bytes(depth, count, "relative depth");
+    require_bytes(range, 2, "relative depth range");
+    ProfileScope prof(context_.profiler(), "normalize_relative", 8.0 * count, "B", context_.active_stream());
+    hip_check(dav2_hip_normalize_relative(depth.as<float>(), range.as<float>(), count, context_.active_stream()),
+              "normalize_relative");
+}
+
+// src/operators.cpp:2092-2130
+void HipOperators::relu(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t count) {
+    require_bytes(output, count, "ReLU output");
+    require_bytes(input, count, "ReLU input");
+    ProfileScope prof(context_.profiler(), "relu", 8.0 * count, "B", context_.active_stream());
+    hip_check(dav2_hip_relu(output.as<float>(), input.as<float>(), count, context_.active_stream()), "relu");
+}
+
+void HipOperators::add(DeviceBuffer& output, const DeviceBuffer& left, const DeviceBuffer& right,
+                       std::uint32_t count) {
+    require_bytes(output, count, "add output");
+    require_bytes(left, count, "add left");
+    require_bytes(right, count, "add right");
+    ProfileScope prof(context_.profiler(), "add", 12.0 * count, "B", context_.active_stream());
+    hip_check(dav2_hip_add(output.as<float>(), left.as<float>(), right.as<float>(), count, context_.active_stream()),
+              "add");
+}
+
+void HipOperators::gelu(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t count) {
+    require_bytes(output, count, "GELU output");
+    require_bytes(input, count, "GELU input");
+    hip_check(dav2_hip_gelu(output.as<float>(), input.as<float>(), count, context_.active_stream()), "gelu");
+}
+
+}  // namespace dav2

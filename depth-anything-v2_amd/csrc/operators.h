@@ -1,0 +1,126 @@
+// Operator surface of the int8 hot path on HIP.
+//
+// Same method names, argument order and validation behaviour as the int8 and
+// shared operators of the reference's VulkanOperators (src/operators.h:11-383):
+// sizes are checked against the buffers (too small -> std::invalid_argument,
+// src/operators.cpp:93-102) and work is enqueued asynchronously on the
+// context's active stream. DeviceBuffer replaces VulkanBuffer; the int8 weight
+// buffers are the GpuModel layout ([rows][ld] bytes, ld = K rounded up to 64).
+// fp32/fp16 operator variants are not part of this build.
+//
+// Fused variants (no reference counterpart) serve the encoder/DPT drivers:
+// they compute the same arithmetic as the reference's separate passes.
+#pragma once
+
+#include "runtime.h"
+
+#include <cstdint>
+
+namespace dav2 {
+
+// Mirrors the InferBridge native Precision enum used by the reference.
+enum class Precision { fp32, fp16, int8 };
+
+// Reusable int8 activation workspace (role of the reference's
+// Int8ActivationWorkspace): packed rows + per-row scales, grown on demand.
+class Int8Workspace {
+public:
+    DeviceBuffer& packed(std::uint64_t bytes);
+    DeviceBuffer& scales(std::uint64_t bytes);
+
+private:
+    DeviceBuffer packed_;
+    DeviceBuffer scales_;
+};
+
+class HipOperators {
+public:
+    explicit HipOperators(HipContext& context);
+
+    void linear_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+                     const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
+                     std::uint32_t input_columns, std::uint32_t output_columns, bool gelu,
+                     bool weight_transposed = false);
+
+    void layer_norm(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                    const DeviceBuffer& bias, std::uint32_t rows, std::uint32_t columns, float epsilon);
+
+    void add_scaled(DeviceBuffer& output, const DeviceBuffer& residual, const DeviceBuffer& addend,
+                    const DeviceBuffer& scale, std::uint32_t count, std::uint32_t columns);
+
+    void attention_head64(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
+                          std::uint32_t heads, DeviceBuffer* score_scratch = nullptr,
+                          Precision precision = Precision::fp32);
+
+    void prepare_tokens(DeviceBuffer& output, const DeviceBuffer& image, const DeviceBuffer& patch_weight,
+                        const DeviceBuffer& patch_half_weight, const DeviceBuffer& patch_int8_weight,
+                        const DeviceBuffer& patch_int8_scales, const DeviceBuffer& patch_bias,
+                        const DeviceBuffer& class_token, const DeviceBuffer& position, std::uint32_t input_width,
+                        std::uint32_t input_height, std::uint32_t embedding, Precision precision);
+
+    void project_tokens_int8(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& int8_weight,
+                             const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t width,
+                             std::uint32_t height, std::uint32_t embedding, std::uint32_t output_channels);
+
+    void conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+                     const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t input_width,
+                     std::uint32_t input_height, std::uint32_t input_channels, std::uint32_t output_channels,
+                     std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding, bool has_bias);
+
+    void conv_transpose_nonoverlap_int8(DeviceBuffer& output, const DeviceBuffer& input,
+                                        const DeviceBuffer& int8_weight, const DeviceBuffer& weight_scales,
+                                        const DeviceBuffer& bias, std::uint32_t input_width,
+                                        std::uint32_t input_height, std::uint32_t input_channels,
+                                        std::uint32_t output_channels, std::uint32_t kernel);
+
+    void bilinear_align_true(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t input_width,
+                             std::uint32_t input_height, std::uint32_t output_width, std::uint32_t output_height,
+                             std::uint32_t channels);
+
+    void reduce_minmax(const DeviceBuffer& input, DeviceBuffer& range, std::uint32_t count);
+    void normalize_relative(DeviceBuffer& depth, const DeviceBuffer& range, std::uint32_t count);
+
+    void relu(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t count);
+    void add(DeviceBuffer& output, const DeviceBuffer& left, const DeviceBuffer& right, std::uint32_t count);
+    void gelu(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t count);
+
+    // ---- fused variants used by the graph drivers ------------------------
+    // LayerNorm whose output row is quantized straight into the workspace
+    // (layer_norm + quantize_rows of linear_int8); fp32 row optional.
+    void layer_norm_quantize(const DeviceBuffer& input, const DeviceBuffer& weight, const DeviceBuffer& bias,
+                             std::uint32_t rows, std::uint32_t columns, float epsilon, DeviceBuffer* fp32_out);
+    // quantize_rows of linear_int8 into the workspace.
+    void quantize_rows(const DeviceBuffer& input, std::uint64_t input_offset, std::uint32_t rows,
+                       std::uint32_t columns);
+    // GEMM on the rows currently held by the workspace.
+    enum class Epilogue { row, row_gelu, row_layerscale };
+    void linear_int8_prequantized(DeviceBuffer& output, const DeviceBuffer& int8_weight,
+                                  const DeviceBuffer& weight_scales, const DeviceBuffer* bias, std::uint32_t rows,
+                                  std::uint32_t input_columns, std::uint32_t output_columns, Epilogue epilogue,
+                                  const DeviceBuffer* gamma = nullptr, std::uint64_t output_row_offset = 0);
+    // Batched attention over `batch` token matrices of `tokens` rows each.
+    void attention_batched(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
+                           std::uint32_t heads, std::uint32_t batch, DeviceBuffer& score_scratch,
+                           Precision precision);
+    static std::uint64_t attention_score_bytes(std::uint32_t tokens, std::uint32_t heads, std::uint32_t batch,
+                                               Precision precision);
+
+    Int8Workspace& workspace() { return workspace_; }
+    HipContext& context() { return context_; }
+
+private:
+    void linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& packed_input, std::uint32_t packed_ld,
+                            const DeviceBuffer& int8_weight, const DeviceBuffer& input_scales,
+                            const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
+                            std::uint32_t input_columns, std::uint32_t output_columns,
+                            std::uint32_t output_row_offset, std::uint32_t output_row_stride, bool output_transposed,
+                            bool has_bias);
+
+    HipContext& context_;
+    Int8Workspace workspace_;
+    DeviceBuffer minmax_partials_;
+    DeviceBuffer interpolated_;
+    std::uint32_t workspace_ld_ = 0;  // row stride of the int8 rows currently in the workspace
+};
+
+}  // namespace dav2

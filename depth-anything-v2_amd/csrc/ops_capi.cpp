@@ -1,0 +1,220 @@
+// C ABI over dav2::HipOperators (include/dav2_ops.h).
+
+#include "dav2_ops.h"
+
+#include "executor.h"
+#include "operators.h"
+
+#include <memory>
+#include <new>
+#include <stdexcept>
+#include <string>
+
+struct dav2_ops {
+    std::unique_ptr<dav2::HipContext> context;
+    std::unique_ptr<dav2::HipOperators> ops;
+};
+
+namespace {
+
+thread_local std::string ops_error;
+
+// Status mapping of the public ABI (src/dav2.cpp:71-90). The last error text
+// is published through dav2_last_error() via the public entry points only, so
+// keep a separate message here and mirror it there.
+template <typename Function>
+dav2_status guard(dav2_ops* ops, Function&& f) {
+    if (ops == nullptr) return DAV2_STATUS_INVALID_ARGUMENT;
+    try {
+        ops->context->make_current();
+        f(*ops->ops);
+        return DAV2_STATUS_OK;
+    } catch (const std::bad_alloc&) {
+        ops_error = "out of memory";
+        return DAV2_STATUS_OUT_OF_MEMORY;
+    } catch (const std::invalid_argument& e) {
+        ops_error = e.what();
+        return DAV2_STATUS_INVALID_ARGUMENT;
+    } catch (const std::exception& e) {
+        ops_error = e.what();
+        return DAV2_STATUS_INTERNAL_ERROR;
+    }
+}
+
+dav2::DeviceBuffer v(const dav2_device_buffer& b) { return dav2::DeviceBuffer::view(b.data, b.data ? b.bytes : 0); }
+
+}  // namespace
+
+extern "C" {
+
+DAV2_API const char* DAV2_CALL dav2_ops_last_error(void) { return ops_error.c_str(); }
+
+dav2_ops* DAV2_CALL dav2_ops_create(int32_t device_index) {
+    try {
+        auto o = std::make_unique<dav2_ops>();
+        o->context = std::make_unique<dav2::HipContext>(device_index);
+        o->ops = std::make_unique<dav2::HipOperators>(*o->context);
+        return o.release();
+    } catch (const std::exception& e) {
+        ops_error = e.what();
+        return nullptr;
+    }
+}
+
+void DAV2_CALL dav2_ops_destroy(dav2_ops* ops) { delete ops; }
+
+void* DAV2_CALL dav2_ops_stream(dav2_ops* ops) { return ops ? ops->context->stream() : nullptr; }
+
+dav2_status DAV2_CALL dav2_ops_synchronize(dav2_ops* ops) {
+    return guard(ops, [&](dav2::HipOperators& o) { o.context().synchronize(); });
+}
+
+dav2_status DAV2_CALL dav2_ops_linear_int8(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                          dav2_device_buffer w8, dav2_device_buffer ws, dav2_device_buffer bias,
+                                          uint32_t rows, uint32_t ic, uint32_t oc, int32_t gelu) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.linear_int8(out, v(input), v(w8), v(ws), v(bias), rows, ic, oc, gelu != 0);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_layer_norm(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                         dav2_device_buffer weight, dav2_device_buffer bias, uint32_t rows,
+                                         uint32_t columns, float epsilon) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.layer_norm(out, v(input), v(weight), v(bias), rows, columns, epsilon);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_add_scaled(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer residual,
+                                         dav2_device_buffer addend, dav2_device_buffer scale, uint32_t count,
+                                         uint32_t columns) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.add_scaled(out, v(residual), v(addend), v(scale), count, columns);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_attention_head64(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer qkv,
+                                               uint32_t tokens, uint32_t heads, dav2_device_buffer scratch,
+                                               int32_t precision) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        if (precision != DAV2_PRECISION_FP32 && precision != DAV2_PRECISION_FP16)
+            throw std::invalid_argument("attention precision must be fp32 or fp16");
+        auto out = v(output);
+        auto s = v(scratch);
+        o.attention_head64(out, v(qkv), tokens, heads, scratch.data ? &s : nullptr,
+                           precision == DAV2_PRECISION_FP16 ? dav2::Precision::fp16 : dav2::Precision::fp32);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_prepare_tokens(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer image,
+                                             dav2_device_buffer w8, dav2_device_buffer ws, dav2_device_buffer bias,
+                                             dav2_device_buffer cls, dav2_device_buffer position, uint32_t width,
+                                             uint32_t height, uint32_t embedding) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.prepare_tokens(out, v(image), dav2::DeviceBuffer(), dav2::DeviceBuffer(), v(w8), v(ws), v(bias), v(cls),
+                         v(position), width, height, embedding, dav2::Precision::int8);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_project_tokens_int8(dav2_ops* ops, dav2_device_buffer output,
+                                                  dav2_device_buffer tokens, dav2_device_buffer w8,
+                                                  dav2_device_buffer ws, dav2_device_buffer bias, uint32_t width,
+                                                  uint32_t height, uint32_t embedding, uint32_t channels) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.project_tokens_int8(out, v(tokens), v(w8), v(ws), v(bias), width, height, embedding, channels);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_conv2d_int8(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                          dav2_device_buffer w8, dav2_device_buffer ws, dav2_device_buffer bias,
+                                          uint32_t iw, uint32_t ih, uint32_t ic, uint32_t oc, uint32_t kernel,
+                                          uint32_t stride, uint32_t padding, int32_t has_bias) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.conv2d_int8(out, v(input), v(w8), v(ws), v(bias), iw, ih, ic, oc, kernel, stride, padding, has_bias != 0);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_conv_transpose_nonoverlap_int8(dav2_ops* ops, dav2_device_buffer output,
+                                                             dav2_device_buffer input, dav2_device_buffer w8,
+                                                             dav2_device_buffer ws, dav2_device_buffer bias,
+                                                             uint32_t iw, uint32_t ih, uint32_t ic, uint32_t oc,
+                                                             uint32_t kernel) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.conv_transpose_nonoverlap_int8(out, v(input), v(w8), v(ws), v(bias), iw, ih, ic, oc, kernel);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_bilinear_align_true(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                                  uint32_t iw, uint32_t ih, uint32_t ow, uint32_t oh,
+                                                  uint32_t channels) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.bilinear_align_true(out, v(input), iw, ih, ow, oh, channels);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_reduce_minmax(dav2_ops* ops, dav2_device_buffer input, dav2_device_buffer range,
+                                            uint32_t count) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto r = v(range);
+        o.reduce_minmax(v(input), r, count);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_normalize_relative(dav2_ops* ops, dav2_device_buffer depth, dav2_device_buffer range,
+                                                 uint32_t count) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto d = v(depth);
+        o.normalize_relative(d, v(range), count);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_relu(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                   uint32_t count) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.relu(out, v(input), count);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_add(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer left,
+                                  dav2_device_buffer right, uint32_t count) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.add(out, v(left), v(right), count);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_gelu(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                   uint32_t count) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.gelu(out, v(input), count);
+    });
+}
+
+dav2_status DAV2_CALL dav2_infer_tensor_f32_device_logits(dav2_context* context, const float* input, int32_t width,
+                                                         int32_t height, float* depth, float* logits,
+                                                         void* stream) {
+    if (context == nullptr || input == nullptr || depth == nullptr || logits == nullptr) return DAV2_STATUS_INVALID_ARGUMENT;
+    if (width <= 0 || height <= 0 || width % 14 != 0 || height % 14 != 0) return DAV2_STATUS_INVALID_ARGUMENT;
+    try {
+        context->executor->infer_device(input, 1, width, height, depth, static_cast<hipStream_t>(stream), logits);
+        return DAV2_STATUS_OK;
+    } catch (const std::invalid_argument& e) {
+        ops_error = e.what();
+        return DAV2_STATUS_INVALID_ARGUMENT;
+    } catch (const std::exception& e) {
+        ops_error = e.what();
+        return DAV2_STATUS_INTERNAL_ERROR;
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,157 @@
+#include "runtime.h"
+
+#include <cstdio>
+#include <new>
+#include <utility>
+
+namespace dav2 {
+
+void hip_check(hipError_t error, const char* what) {
+    if (error == hipSuccess) return;
+    if (error == hipErrorOutOfMemory || error == hipErrorMemoryAllocation) throw std::bad_alloc();
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(error));
+}
+
+DeviceBuffer::DeviceBuffer(std::size_t bytes) : bytes_(bytes), owned_(true) {
+    if (bytes == 0) return;
+    hip_check(hipMalloc(&pointer_, bytes), "hipMalloc");
+}
+
+DeviceBuffer::~DeviceBuffer() { reset(); }
+
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& other) noexcept
+    : pointer_(std::exchange(other.pointer_, nullptr)),
+      bytes_(std::exchange(other.bytes_, 0)),
+      owned_(std::exchange(other.owned_, false)) {}
+
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& other) noexcept {
+    if (this != &other) {
+        reset();
+        pointer_ = std::exchange(other.pointer_, nullptr);
+        bytes_ = std::exchange(other.bytes_, 0);
+        owned_ = std::exchange(other.owned_, false);
+    }
+    return *this;
+}
+
+DeviceBuffer DeviceBuffer::view(void* pointer, std::size_t bytes) {
+    DeviceBuffer b;
+    b.pointer_ = pointer;
+    b.bytes_ = pointer ? bytes : 0;
+    b.owned_ = false;
+    return b;
+}
+
+void DeviceBuffer::reset() {
+    if (owned_ && pointer_) (void)hipFree(pointer_);
+    pointer_ = nullptr;
+    bytes_ = 0;
+    owned_ = false;
+}
+
+Profiler::~Profiler() {
+    for (auto& r : pending_) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    for (hipEvent_t e : free_) (void)hipEventDestroy(e);
+}
+
+hipEvent_t Profiler::take_event() {
+    if (!free_.empty()) {
+        hipEvent_t e = free_.back();
+        free_.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    hip_check(hipEventCreate(&e), "hipEventCreate");
+    return e;
+}
+
+int Profiler::begin(const char* name, double work, const char* unit, hipStream_t stream) {
+    if (!enabled_) return -1;
+    Record r{name, unit, work, take_event(), take_event()};
+    hip_check(hipEventRecord(r.start, stream), "hipEventRecord");
+    pending_.push_back(r);
+    return static_cast<int>(pending_.size() - 1);
+}
+
+void Profiler::end(int id, hipStream_t stream) {
+    if (id < 0 || static_cast<std::size_t>(id) >= pending_.size()) return;
+    (void)hipEventRecord(pending_[id].stop, stream);
+}
+
+std::string Profiler::report() {
+    for (auto& r : pending_) {
+        hip_check(hipEventSynchronize(r.stop), "hipEventSynchronize");
+        float ms = 0.0f;
+        hip_check(hipEventElapsedTime(&ms, r.start, r.stop), "hipEventElapsedTime");
+        Total& t = totals_[r.name];
+        t.launches += 1;
+        t.ms += ms;
+        t.work += r.work;
+        t.unit = r.unit;
+        free_.push_back(r.start);
+        free_.push_back(r.stop);
+    }
+    pending_.clear();
+    std::string out = "{";
+    bool first = true;
+    for (const auto& kv : totals_) {
+        char buf[256];
+        std::snprintf(buf, sizeof(buf), "%s\"%s\": {\"launches\": %llu, \"ms\": %.6f, \"work\": %.6e, \"unit\": \"%s\"}",
+                      first ? "" : ", ", kv.first.c_str(), static_cast<unsigned long long>(kv.second.launches),
+                      kv.second.ms, kv.second.work, kv.second.unit.c_str());
+        out += buf;
+        first = false;
+    }
+    out += "}";
+    totals_.clear();
+    return out;
+}
+
+HipContext::HipContext(int device_index) : device_(device_index) {
+    int count = 0;
+    hip_check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (device_index < 0 || device_index >= count)
+        throw std::runtime_error("HIP device index " + std::to_string(device_index) + " is not available");
+    hip_check(hipSetDevice(device_), "hipSetDevice");
+    hipDeviceProp_t props{};
+    hip_check(hipGetDeviceProperties(&props, device_), "hipGetDeviceProperties");
+    device_name_ = props.name;
+    compute_units_ = props.multiProcessorCount;
+    // Default priority, non-blocking with respect to the null stream.
+    hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    active_ = stream_;
+}
+
+HipContext::~HipContext() {
+    if (stream_) {
+        (void)hipSetDevice(device_);
+        (void)hipStreamSynchronize(stream_);
+        (void)hipStreamDestroy(stream_);
+    }
+}
+
+void HipContext::make_current() const { hip_check(hipSetDevice(device_), "hipSetDevice"); }
+
+void HipContext::upload(DeviceBuffer& destination, const void* source, std::size_t bytes) {
+    if (bytes > destination.size()) throw std::invalid_argument("upload exceeds device buffer");
+    if (bytes == 0) return;
+    hip_check(hipMemcpyAsync(destination.data(), source, bytes, hipMemcpyHostToDevice, active_), "upload");
+    // Asynchronous: the caller keeps the host source alive and unchanged until
+    // it synchronises the stream (create and infer both end with a sync).
+    upload_bytes_ += bytes;
+}
+
+void HipContext::download(const DeviceBuffer& source, void* destination, std::size_t bytes) {
+    if (bytes > source.size()) throw std::invalid_argument("download exceeds device buffer");
+    if (bytes == 0) return;
+    hip_check(hipMemcpyAsync(destination, source.data(), bytes, hipMemcpyDeviceToHost, active_), "download");
+    hip_check(hipStreamSynchronize(active_), "download synchronize");
+    download_bytes_ += bytes;
+}
+
+void HipContext::synchronize() { hip_check(hipStreamSynchronize(active_), "hipStreamSynchronize"); }
+
+}  // namespace dav2

@@ -1,0 +1,146 @@
+// HIP device runtime: device buffers, one in-order stream per context,
+// transfers with byte counters, and per-launch error checking.
+// Role of the reference's src/vulkan.{h,cpp} (buffers, dispatch, batch,
+// transfer counters) without any of its Vulkan objects: a single in-order HIP
+// stream already orders every kernel after the one before it, so there are
+// no barriers or hazard tracking to manage.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace dav2 {
+
+// Throws std::bad_alloc for out-of-memory and std::runtime_error otherwise.
+void hip_check(hipError_t error, const char* what);
+inline void hip_check(int error, const char* what) { hip_check(static_cast<hipError_t>(error), what); }
+
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(std::size_t bytes);
+    ~DeviceBuffer();
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    DeviceBuffer(DeviceBuffer&& other) noexcept;
+    DeviceBuffer& operator=(DeviceBuffer&& other) noexcept;
+
+    // Non-owning view of caller memory (the FFI operator surface uses this).
+    static DeviceBuffer view(void* pointer, std::size_t bytes);
+
+    void* data() const { return pointer_; }
+    std::size_t size() const { return bytes_; }
+    template <typename T>
+    T* as() const { return static_cast<T*>(pointer_); }
+    explicit operator bool() const { return pointer_ != nullptr; }
+    void reset();
+
+private:
+    void* pointer_ = nullptr;
+    std::size_t bytes_ = 0;
+    bool owned_ = false;
+};
+
+// Per-launch HIP-event timing, aggregated per kernel family (role of the
+// reference's DAV2_VULKAN_PROFILE timestamp queries, src/vulkan.cpp:874-960).
+// Off by default; when on, every operator launch is bracketed by two events on
+// the stream it runs on, together with its algorithmic work (ops or bytes).
+class Profiler {
+public:
+    ~Profiler();
+    void set_enabled(bool on) { enabled_ = on; }
+    bool enabled() const { return enabled_; }
+    // Returns a record id, or -1 when disabled.
+    int begin(const char* name, double work, const char* unit, hipStream_t stream);
+    void end(int id, hipStream_t stream);
+    // Synchronises, folds pending records into the totals and returns them as
+    // a JSON object {name: {"launches", "ms", "work", "unit"}}; then clears.
+    std::string report();
+
+private:
+    struct Record {
+        std::string name;
+        const char* unit;
+        double work;
+        hipEvent_t start, stop;
+    };
+    struct Total {
+        std::uint64_t launches = 0;
+        double ms = 0.0, work = 0.0;
+        std::string unit;
+    };
+    hipEvent_t take_event();
+    bool enabled_ = false;
+    std::vector<Record> pending_;
+    std::vector<hipEvent_t> free_;
+    std::map<std::string, Total> totals_;
+};
+
+class ProfileScope {
+public:
+    ProfileScope(Profiler& p, const char* name, double work, const char* unit, hipStream_t s)
+        : p_(p), s_(s), id_(p.begin(name, work, unit, s)) {}
+    ~ProfileScope() { p_.end(id_, s_); }
+
+private:
+    Profiler& p_;
+    hipStream_t s_;
+    int id_;
+};
+
+class HipContext {
+public:
+    explicit HipContext(int device_index);
+    ~HipContext();
+    HipContext(const HipContext&) = delete;
+    HipContext& operator=(const HipContext&) = delete;
+
+    int device() const { return device_; }
+    hipStream_t stream() const { return stream_; }
+    // Runs subsequent work on an external stream (nullptr restores the own one).
+    void use_stream(hipStream_t stream) { active_ = stream ? stream : stream_; }
+    hipStream_t active_stream() const { return active_; }
+
+    DeviceBuffer create_device_buffer(std::size_t bytes) { return DeviceBuffer(bytes); }
+    void upload(DeviceBuffer& destination, const void* source, std::size_t bytes);
+    void download(const DeviceBuffer& source, void* destination, std::size_t bytes);
+    void synchronize();
+    void make_current() const;
+
+    std::uint64_t upload_bytes() const { return upload_bytes_; }
+    std::uint64_t download_bytes() const { return download_bytes_; }
+    const std::string& device_name() const { return device_name_; }
+    int compute_units() const { return compute_units_; }
+    Profiler& profiler() { return profiler_; }
+
+private:
+    Profiler profiler_;
+    int device_ = 0;
+    hipStream_t stream_ = nullptr;
+    hipStream_t active_ = nullptr;
+    std::uint64_t upload_bytes_ = 0;
+    std::uint64_t download_bytes_ = 0;
+    std::string device_name_;
+    int compute_units_ = 0;
+};
+
+// RAII switch of the context's active stream.
+class ScopedStream {
+public:
+    ScopedStream(HipContext& context, hipStream_t stream) : context_(context), previous_(context.active_stream()) {
+        context_.use_stream(stream);
+    }
+    ~ScopedStream() { context_.use_stream(previous_); }
+
+private:
+    HipContext& context_;
+    hipStream_t previous_;
+};
+
+}  // namespace dav2

@@ -1,0 +1,152 @@
+/*
+ * Thin C-ABI HIP launcher layer: one extern "C" entry per gfx950 kernel.
+ *
+ * Every entry takes raw device pointers, plain sizes and a hipStream_t passed
+ * as void* (NULL = the null stream), enqueues asynchronously and returns the
+ * hipError_t value as int (0 = hipSuccess; hipErrorInvalidValue = 1 for
+ * rejected arguments). No entry allocates memory. The C++ operator surface
+ * (dav2::HipOperators, mirroring the reference's src/operators.h) calls only
+ * these; tests and FFI callers may call them directly.
+ *
+ * int8 matrices are row-major [rows][ld] bytes, ld a multiple of 64 and bytes
+ * [K, ld) zero: the first K bytes of a row are the byte view of the
+ * reference's packed 4x int8 words (quantize_rows_int8_fused.glsl:51).
+ */
+#ifndef DAV2_HIP_H
+#define DAV2_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef DAV2_API
+#define DAV2_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Replaces quantize_rows_int8_fused.glsl:20-55 as dispatched by
+ * VulkanOperators::linear_int8 (src/operators.cpp:810-818) and
+ * project_tokens_int8 (:1514-1522). Row r reads input[input_offset + r*columns + c].
+ * columns % 4 == 0, input_offset % 4 == 0. */
+DAV2_API int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset,
+                                       uint32_t rows, uint32_t columns, int8_t* q,
+                                       uint32_t ldq, float* scales, void* stream);
+
+/* Replaces im2col_quantize_int8.glsl:26-83 (src/operators.cpp:1284-1298,
+ * :1787-1801, :1946-1960). CHW input; rows = output_width*output_height. */
+DAV2_API int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width,
+                                         uint32_t input_height, uint32_t input_channels,
+                                         uint32_t output_width, uint32_t output_height,
+                                         uint32_t kernel, uint32_t stride, int32_t padding,
+                                         int8_t* q, uint32_t ldq, float* scales,
+                                         void* stream);
+
+/* Replaces layer_norm.glsl:27-68 (src/operators.cpp:1016-1042). */
+DAV2_API int dav2_hip_layer_norm(float* out, const float* input, const float* weight,
+                                 const float* bias, uint32_t rows, uint32_t columns,
+                                 float epsilon, void* stream);
+
+/* layer_norm.glsl followed by quantize_rows_int8_fused.glsl in one pass (the
+ * reference runs them back to back at src/encoder.cpp:443-452, :500-528);
+ * out may be NULL when the fp32 row is not needed. columns <= 4096. */
+DAV2_API int dav2_hip_layer_norm_quantize_i8(int8_t* q, uint32_t ldq, float* scales,
+                                             float* out, const float* input,
+                                             const float* weight, const float* bias,
+                                             uint32_t rows, uint32_t columns,
+                                             float epsilon, void* stream);
+
+/* GEMM epilogues. Reference: linear_int8_tiled.glsl:99-116,
+ * gelu.glsl:16-49, add_scaled.glsl:23-32, conv_transpose_int8.glsl:31-58. */
+enum {
+    DAV2_GEMM_EPI_RAW_I32 = 0,        /* out_i32[m*n + n'] = int32 accumulator        */
+    DAV2_GEMM_EPI_ROW = 1,            /* out[(m+off)*n + n'] = acc*sa*sb + bias        */
+    DAV2_GEMM_EPI_ROW_GELU = 2,       /* ... then exact-erf GELU                        */
+    DAV2_GEMM_EPI_ROW_LAYERSCALE = 3, /* out = residual + (acc*sa*sb + bias)*gamma[n'] */
+    DAV2_GEMM_EPI_TRANSPOSED = 4,     /* out[n'*stride + m + off] (channel-major)       */
+    DAV2_GEMM_EPI_CONVT = 5           /* stride==kernel ConvTranspose scatter           */
+};
+
+typedef struct dav2_gemm_i8_args {
+    const int8_t* a;        /* activations [m][lda], 16-byte aligned          */
+    uint64_t lda;
+    const int8_t* b;        /* weights [n][ldb], 16-byte aligned              */
+    uint64_t ldb;
+    uint32_t m, n, k;       /* k: multiple of 64, padding bytes zero          */
+    uint32_t epilogue;      /* DAV2_GEMM_EPI_*                                */
+    const float* a_scales;  /* [m] per-row activation scales                  */
+    const float* b_scales;  /* [n] per-row weight scales                      */
+    const float* bias;      /* [n] (CONVT: [convt_channels]) or NULL = 0      */
+    int32_t* out_i32;
+    float* out;
+    uint64_t out_row_offset;
+    uint64_t out_row_stride;
+    const float* residual;  /* LAYERSCALE: may alias out                      */
+    const float* gamma;
+    uint32_t convt_kernel, convt_width, convt_height, convt_channels;
+} dav2_gemm_i8_args;
+
+/* Replaces linear_int8_tiled.glsl:40-117 (src/operators.cpp:847-880) and
+ * conv_transpose_int8.glsl:31-58 (:1969-1975). */
+DAV2_API int dav2_hip_gemm_i8(const dav2_gemm_i8_args* args, void* stream);
+
+/* Elementwise kernels. Reference: gelu.glsl, add_scaled.glsl, add.glsl, relu.glsl. */
+DAV2_API int dav2_hip_gelu(float* out, const float* input, uint64_t count, void* stream);
+DAV2_API int dav2_hip_add_scaled(float* out, const float* residual, const float* addend,
+                                 const float* scale, uint64_t count, uint32_t columns,
+                                 void* stream);
+DAV2_API int dav2_hip_add(float* out, const float* left, const float* right, uint64_t count,
+                          void* stream);
+DAV2_API int dav2_hip_relu(float* out, const float* input, uint64_t count, void* stream);
+
+/* Attention, head_dim 64 (src/operators.cpp:1098-1209). qkv is [batch*T][3*H*64]
+ * token-major (q | k | v, head h at h*64). fp16 = 0: fp32 scores [batch][H][T][T]
+ * (bmm.glsl, softmax_lastdim.glsl); fp16 = 1: binary16 scores
+ * [batch][H][T][ldt], ldt = T rounded up to a multiple of 8 (bmm_score_fp16.glsl,
+ * softmax_lastdim_half.glsl, bmm_value_fp16.glsl). Softmax is in place. */
+DAV2_API int dav2_hip_attention_scores(void* scores, const float* qkv, uint32_t tokens,
+                                       uint32_t heads, uint32_t batch, int fp16,
+                                       void* stream);
+DAV2_API int dav2_hip_softmax_rows(void* scores, uint64_t rows, uint32_t columns,
+                                   uint32_t row_stride, int fp16, void* stream);
+DAV2_API int dav2_hip_attention_values(float* out, const void* probabilities,
+                                       const float* qkv, uint32_t tokens, uint32_t heads,
+                                       uint32_t batch, int fp16, void* stream);
+
+/* bilinear_align_true.glsl:27-63, CHW. */
+DAV2_API int dav2_hip_bilinear_align_true(float* out, const float* input,
+                                          uint32_t input_width, uint32_t input_height,
+                                          uint32_t output_width, uint32_t output_height,
+                                          uint32_t channels, void* stream);
+
+/* reduce_minmax.glsl as a two-stage grid reduction; partials must hold
+ * 2*dav2_hip_minmax_partials(count) floats. range[0] = min, range[1] = max. */
+DAV2_API uint32_t dav2_hip_minmax_partials(uint64_t count);
+DAV2_API int dav2_hip_reduce_minmax(const float* input, uint64_t count, float* range,
+                                    float* partials, void* stream);
+/* normalize_relative.glsl:8-16 */
+DAV2_API int dav2_hip_normalize_relative(float* depth, const float* range, uint64_t count,
+                                         void* stream);
+
+/* position_bicubic.glsl:76-105 with the set-up of src/operators.cpp:1323-1376:
+ * position is the [1370][D] pos_embed, out is CHW [D][ph][pw]. */
+DAV2_API int dav2_hip_position_bicubic(float* out, const float* position,
+                                       uint32_t patch_width, uint32_t patch_height,
+                                       uint32_t embedding, void* stream);
+/* copy_class_token.glsl + add_position.glsl (src/operators.cpp:1299-1304,
+ * :1389-1405) for batch images of T = pw*ph+1 tokens each: token 0 becomes
+ * class_token + position[0..D), token t > 0 gets interpolated[f*pw*ph + t-1]
+ * added. */
+DAV2_API int dav2_hip_finish_tokens(float* tokens, const float* interpolated,
+                                    const float* position, const float* class_token,
+                                    uint32_t patch_width, uint32_t patch_height,
+                                    uint32_t embedding, uint32_t batch, void* stream);
+
+DAV2_API const char* dav2_hip_error_string(int error);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DAV2_HIP_H */

@@ -1,0 +1,962 @@
+// CPU oracle for the int8 hot path. TEST INFRASTRUCTURE ONLY: a restatement of
+// the reference runtime's operator semantics, used as the checker for the HIP
+// implementation and as the timed CPU baseline. Never linked into the product.
+//
+// Built with -ffp-contract=off so every a*b+c below rounds twice, exactly as
+// written; the GPU kernels are compiled the same way where they mirror these
+// expressions.
+
+#include "dav2_oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <limits>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include <immintrin.h>
+#include <omp.h>
+
+namespace {
+
+inline float clamp127(float v) {
+    // GLSL clamp(v, -127, 127) == min(max(v, -127), 127)
+    return std::min(std::max(v, -127.0f), 127.0f);
+}
+
+inline int8_t round_rne(float v) {
+    // GLSL round() ties are implementation-defined; the host quantizer uses
+    // std::nearbyint (gpu_model.cpp:253). The whole build pins ties-to-even.
+    return static_cast<int8_t>(static_cast<int>(std::nearbyint(v)));
+}
+
+// ---------------------------------------------------------------------------
+// fp16 (binary16) helpers, round to nearest even.
+uint16_t f2h(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t mant = x & 0x7fffffu;
+    if (exp == 0xffu) return static_cast<uint16_t>(sign | (mant ? 0x7e00u : 0x7c00u));
+    int e = static_cast<int>(exp) - 127 + 15;
+    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return static_cast<uint16_t>(sign);
+        mant |= 0x800000u;
+        const uint32_t shift = static_cast<uint32_t>(14 - e);
+        uint32_t r = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u);
+        const uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (r & 1u))) ++r;
+        return static_cast<uint16_t>(sign | r);
+    }
+    uint32_t r = mant >> 13;
+    const uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) {
+        ++r;
+        if (r == 0x400u) {
+            r = 0;
+            ++e;
+            if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+        }
+    }
+    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(e) << 10) | r);
+}
+
+float h2f(uint16_t h) {
+    const uint32_t sign = (static_cast<uint32_t>(h) & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t mant = h & 0x3ffu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do { ++e; mant <<= 1; } while ((mant & 0x400u) == 0);
+            mant &= 0x3ffu;
+            bits = sign | (static_cast<uint32_t>(127 - 15 - e) << 23) | (mant << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (mant << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+inline float round_half(float f) { return h2f(f2h(f)); }
+
+// Eight binary16 round-trips at once (F16C, round to nearest even); the same
+// results as round_half lane by lane.
+inline __m256 round_half8(__m256 v) {
+    return _mm256_cvtph_ps(_mm256_cvtps_ph(v, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+}
+
+// ---------------------------------------------------------------------------
+// int8 dot product; exact in int32 for |K| <= 2^31 / 127^2.
+inline int32_t dot_i8(const int8_t* a, const int8_t* b, uint32_t k) {
+    int32_t s = 0;
+    for (uint32_t i = 0; i < k; ++i) s += static_cast<int32_t>(a[i]) * static_cast<int32_t>(b[i]);
+    return s;
+}
+
+void gemm_i8_blocked(const int8_t* a, const int8_t* b, uint32_t m, uint32_t n,
+                     uint32_t k, int32_t* acc) {
+    constexpr uint32_t MB = 32, NB = 64;
+    const uint32_t mblocks = (m + MB - 1) / MB, nblocks = (n + NB - 1) / NB;
+    const int64_t tasks = static_cast<int64_t>(mblocks) * nblocks;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t t = 0; t < tasks; ++t) {
+        const uint32_t mb = static_cast<uint32_t>(t / nblocks);
+        const uint32_t nb = static_cast<uint32_t>(t % nblocks);
+        const uint32_t m0 = mb * MB, m1 = std::min(m, m0 + MB);
+        const uint32_t n0 = nb * NB, n1 = std::min(n, n0 + NB);
+        for (uint32_t j = n0; j < n1; ++j) {
+            const int8_t* bj = b + static_cast<size_t>(j) * k;
+            for (uint32_t i = m0; i < m1; ++i) {
+                acc[static_cast<size_t>(i) * n + j] =
+                    dot_i8(a + static_cast<size_t>(i) * k, bj, k);
+            }
+        }
+    }
+}
+
+// linear_int8_tiled.glsl:109-114: float(sum) * s_in[row] * s_w[col] + bias
+inline float dequant(int32_t acc, float s_in, float s_w, float b) {
+    float v = static_cast<float>(acc);
+    v = v * s_in;
+    v = v * s_w;
+    return v + b;
+}
+
+inline float gelu_value(float value) {
+    // gelu.glsl:29-48 computes 0.5*x*(1+erf(x/sqrt2)) with erf from the
+    // Numerical Recipes erfcc fit (~1.2e-7); the build uses libm/device erff.
+    const float x = value * 0.70710678118654752440f;
+    const float e = std::erf(x);
+    return 0.5f * value * (1.0f + e);
+}
+
+// ---------------------------------------------------------------------------
+// .dav2 reader (format: src/model.cpp:27-69, tools/export_model.py:21-38)
+#pragma pack(push, 1)
+struct Header {
+    char magic[8];
+    uint32_t version, endian, encoder, tensor_count;
+    uint64_t directory_offset, directory_bytes, data_offset, file_bytes, reserved;
+};
+struct Record {
+    char name[112];
+    uint32_t dtype, rank;
+    uint64_t dims[4];
+    uint64_t data_offset, data_bytes, element_count;
+    uint32_t crc32, flags;
+    uint64_t reserved;
+};
+#pragma pack(pop)
+static_assert(sizeof(Header) == 64, "header");
+static_assert(sizeof(Record) == 192, "record");
+
+uint32_t crc32_impl(const void* data, size_t bytes) {
+    static uint32_t table[256];
+    static bool init = false;
+    if (!init) {
+        for (uint32_t i = 0; i < 256; ++i) {
+            uint32_t c = i;
+            for (int b = 0; b < 8; ++b) c = (c & 1u) ? (0xedb88320u ^ (c >> 1)) : (c >> 1);
+            table[i] = c;
+        }
+        init = true;
+    }
+    const auto* p = static_cast<const unsigned char*>(data);
+    uint32_t c = 0xffffffffu;
+    for (size_t i = 0; i < bytes; ++i) c = table[(c ^ p[i]) & 0xffu] ^ (c >> 8);
+    return c ^ 0xffffffffu;
+}
+
+struct Tensor {
+    std::vector<float> data;
+    uint64_t dims[4] = {0, 0, 0, 0};
+    uint32_t rank = 0;
+    std::vector<int8_t> q;      // per-row int8 (reference a9 rule)
+    std::vector<float> qscale;  // per-row scale
+};
+
+}  // namespace
+
+struct orc_model {
+    int encoder = 0;
+    uint32_t dim = 0, heads = 0, blocks = 0, features = 0;
+    uint32_t capture[4] = {0, 0, 0, 0};
+    uint32_t project[4] = {0, 0, 0, 0};
+    std::unordered_map<std::string, Tensor> tensors;
+
+    const Tensor& t(const std::string& name) const {
+        auto it = tensors.find(name);
+        if (it == tensors.end()) throw std::runtime_error("oracle: missing tensor " + name);
+        return it->second;
+    }
+};
+
+extern "C" {
+
+int orc_set_threads(int threads) {
+    if (threads > 0) omp_set_num_threads(threads);
+    return omp_get_max_threads();
+}
+int orc_get_threads(void) { return omp_get_max_threads(); }
+
+uint16_t orc_float_to_half(float value) { return f2h(value); }
+float orc_half_to_float(uint16_t value) { return h2f(value); }
+uint32_t orc_crc32(const void* data, size_t bytes) { return crc32_impl(data, bytes); }
+
+void orc_quantize_rows(const float* input, uint32_t rows, uint32_t columns,
+                       uint32_t input_offset, int8_t* q, float* scales) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* x = input + input_offset + static_cast<size_t>(r) * columns;
+        float maximum = 0.0f;
+        for (uint32_t c = 0; c < columns; ++c) maximum = std::max(maximum, std::fabs(x[c]));
+        const float scale = std::max(maximum / 127.0f, 1.0e-8f);
+        scales[r] = scale;
+        int8_t* out = q + static_cast<size_t>(r) * columns;
+        for (uint32_t c = 0; c < columns; ++c) out[c] = round_rne(clamp127(x[c] / scale));
+    }
+}
+
+static inline float im2col_read(const float* input, uint32_t iw, uint32_t ih,
+                                uint32_t ow, uint32_t kernel, uint32_t stride,
+                                int32_t padding, uint32_t row, uint32_t column) {
+    const uint32_t ox = row % ow, oy = row / ow;
+    const uint32_t area = kernel * kernel;
+    const uint32_t ic = column / area, kidx = column % area;
+    const uint32_t kx = kidx % kernel, ky = kidx / kernel;
+    const int32_t ix = static_cast<int32_t>(ox * stride + kx) - padding;
+    const int32_t iy = static_cast<int32_t>(oy * stride + ky) - padding;
+    if (ix < 0 || iy < 0 || ix >= static_cast<int32_t>(iw) || iy >= static_cast<int32_t>(ih)) return 0.0f;
+    return input[(static_cast<size_t>(ic) * ih + static_cast<uint32_t>(iy)) * iw + static_cast<uint32_t>(ix)];
+}
+
+void orc_im2col_quantize(const float* input, uint32_t iw, uint32_t ih, uint32_t ic,
+                         uint32_t ow, uint32_t oh, uint32_t kernel, uint32_t stride,
+                         int32_t padding, int8_t* q, float* scales) {
+    const uint32_t rows = ow * oh;
+    const uint32_t columns = ic * kernel * kernel;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint32_t row = static_cast<uint32_t>(r);
+        float maximum = 0.0f;
+        for (uint32_t c = 0; c < columns; ++c)
+            maximum = std::max(maximum, std::fabs(im2col_read(input, iw, ih, ow, kernel, stride, padding, row, c)));
+        const float scale = std::max(maximum / 127.0f, 1.0e-8f);
+        scales[r] = scale;
+        const float inverse = 1.0f / scale;  // im2col_quantize_int8.glsl:68
+        int8_t* out = q + static_cast<size_t>(r) * columns;
+        for (uint32_t c = 0; c < columns; ++c)
+            out[c] = round_rne(clamp127(im2col_read(input, iw, ih, ow, kernel, stride, padding, row, c) * inverse));
+    }
+}
+
+void orc_quantize_weight_rows(const float* weight, uint64_t rows, uint64_t columns,
+                              int8_t* q, float* scales) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < static_cast<int64_t>(rows); ++r) {
+        const float* w = weight + static_cast<size_t>(r) * columns;
+        float maximum = 0.0f;
+        for (uint64_t c = 0; c < columns; ++c) maximum = std::max(maximum, std::abs(w[c]));
+        const float scale = std::max(maximum / 127.0f, 1.0e-8f);
+        scales[r] = scale;
+        for (uint64_t c = 0; c < columns; ++c) {
+            const float normalized = w[c] / scale;
+            q[static_cast<size_t>(r) * columns + c] = static_cast<int8_t>(
+                static_cast<int>(std::nearbyint(std::max(-127.0f, std::min(127.0f, normalized)))));
+        }
+    }
+}
+
+void orc_quantize_convT_weight(const float* weight, uint32_t in_channels,
+                               uint32_t out_channels, uint32_t kernel, int8_t* q,
+                               float* scales) {
+    const uint32_t rows = kernel * kernel * out_channels;
+    std::vector<float> reordered(static_cast<size_t>(rows) * in_channels);
+    for (uint32_t row = 0; row < rows; ++row) {
+        const uint32_t kidx = row / out_channels, oc = row % out_channels;
+        const uint32_t ky = kidx / kernel, kx = kidx % kernel;
+        for (uint32_t c = 0; c < in_channels; ++c)
+            reordered[static_cast<size_t>(row) * in_channels + c] =
+                weight[((static_cast<size_t>(c) * out_channels + oc) * kernel + ky) * kernel + kx];
+    }
+    orc_quantize_weight_rows(reordered.data(), rows, in_channels, q, scales);
+}
+
+void orc_gemm_i8(const int8_t* a, const int8_t* b, uint32_t m, uint32_t n, uint32_t k,
+                 int32_t* acc) {
+    gemm_i8_blocked(a, b, m, n, k, acc);
+}
+
+void orc_linear_epilogue(const int32_t* acc, const float* s_in, const float* s_w,
+                         const float* bias, uint32_t rows, uint32_t columns,
+                         uint32_t row_offset, uint32_t row_stride, int transposed,
+                         float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        for (uint32_t c = 0; c < columns; ++c) {
+            const float v = dequant(acc[static_cast<size_t>(r) * columns + c], s_in[r], s_w[c],
+                                    bias ? bias[c] : 0.0f);
+            const size_t dst_row = static_cast<size_t>(r) + row_offset;
+            const size_t idx = transposed ? static_cast<size_t>(c) * row_stride + dst_row
+                                          : dst_row * columns + c;
+            out[idx] = v;
+        }
+    }
+}
+
+void orc_gelu(const float* input, uint64_t count, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) out[i] = gelu_value(input[i]);
+}
+
+void orc_linear_int8(const float* input, const int8_t* w8, const float* w_scales,
+                     const float* bias, uint32_t rows, uint32_t in_cols,
+                     uint32_t out_cols, int gelu, float* out) {
+    // operators.cpp:770-845: quantize_rows -> tiled int8 GEMM -> (gelu pass)
+    std::vector<int8_t> q(static_cast<size_t>(rows) * in_cols);
+    std::vector<float> s(rows);
+    orc_quantize_rows(input, rows, in_cols, 0, q.data(), s.data());
+    std::vector<int32_t> acc(static_cast<size_t>(rows) * out_cols);
+    gemm_i8_blocked(q.data(), w8, rows, out_cols, in_cols, acc.data());
+    orc_linear_epilogue(acc.data(), s.data(), w_scales, bias, rows, out_cols, 0, rows, 0, out);
+    if (gelu) orc_gelu(out, static_cast<uint64_t>(rows) * out_cols, out);
+}
+
+void orc_layer_norm(const float* input, const float* weight, const float* bias,
+                    uint32_t rows, uint32_t columns, float epsilon, float* out) {
+    // layer_norm.glsl:27-68: 64 lanes, lane l sums columns l, l+64, ... in
+    // order, then an LDS tree over widths 32..1.
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* x = input + static_cast<size_t>(r) * columns;
+        float ps[64], pq[64];
+        for (uint32_t lane = 0; lane < 64; ++lane) {
+            float s = 0.0f, sq = 0.0f;
+            for (uint32_t c = lane; c < columns; c += 64) {
+                const float v = x[c];
+                s = s + v;
+                sq = sq + v * v;
+            }
+            ps[lane] = s;
+            pq[lane] = sq;
+        }
+        for (uint32_t width = 32; width > 0; width >>= 1)
+            for (uint32_t lane = 0; lane < width; ++lane) {
+                ps[lane] = ps[lane] + ps[lane + width];
+                pq[lane] = pq[lane] + pq[lane + width];
+            }
+        const float denom = std::max(static_cast<float>(columns), 1.0f);
+        const float mean = ps[0] / denom;
+        const float var = std::max(pq[0] / denom - mean * mean, 0.0f);
+        const float inv = 1.0f / std::sqrt(var + epsilon);
+        float* y = out + static_cast<size_t>(r) * columns;
+        for (uint32_t c = 0; c < columns; ++c) y[c] = (x[c] - mean) * inv * weight[c] + bias[c];
+    }
+}
+
+void orc_add_scaled(const float* residual, const float* addend, const float* scale,
+                    uint64_t count, uint32_t columns, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) {
+        const float scaled = addend[i] * scale[static_cast<uint64_t>(i) % columns];
+        out[i] = residual[i] + scaled;
+    }
+}
+
+void orc_add(const float* left, const float* right, uint64_t count, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) out[i] = left[i] + right[i];
+}
+
+void orc_relu(const float* input, uint64_t count, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) out[i] = std::max(input[i], 0.0f);
+}
+
+static void softmax_row_fp32(const float* x, uint32_t columns, float* y) {
+    // softmax_lastdim.glsl:19-69 (128 lanes; sum partition lane = column % 128)
+    float maximum = -3.402823466e+38f;
+    for (uint32_t c = 0; c < columns; ++c) maximum = std::max(maximum, x[c]);
+    float partial[128];
+    for (uint32_t lane = 0; lane < 128; ++lane) {
+        float d = 0.0f;
+        for (uint32_t c = lane; c < columns; c += 128) {
+            const float e = std::exp(x[c] - maximum);
+            y[c] = e;
+            d = d + e;
+        }
+        partial[lane] = d;
+    }
+    for (uint32_t stride = 64; stride > 0; stride >>= 1)
+        for (uint32_t lane = 0; lane < stride; ++lane) partial[lane] = partial[lane] + partial[lane + stride];
+    const float inverse = 1.0f / std::max(partial[0], 1.0e-20f);
+    for (uint32_t c = 0; c < columns; ++c) y[c] = y[c] * inverse;
+}
+
+void orc_softmax_rows(const float* input, uint64_t rows, uint32_t columns, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < static_cast<int64_t>(rows); ++r)
+        softmax_row_fp32(input + static_cast<size_t>(r) * columns, columns,
+                         out + static_cast<size_t>(r) * columns);
+}
+
+void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int fp16,
+                          float* out, float* probabilities) {
+    const size_t D = static_cast<size_t>(heads) * 64;
+    const size_t T = tokens;
+    // fp16 path: binary16-rounded keys (feature-major, 64 x T) and values
+    // (T x 64) per head, converted once.
+    std::vector<std::vector<float>> half_keys_t(fp16 ? heads : 0), half_values(fp16 ? heads : 0);
+    if (fp16) {
+#pragma omp parallel for schedule(static)
+        for (int64_t h = 0; h < heads; ++h) {
+            half_keys_t[h].resize(64 * T);
+            half_values[h].resize(T * 64);
+            for (size_t j = 0; j < T; ++j)
+                for (int f = 0; f < 64; ++f) {
+                    half_keys_t[h][f * T + j] = round_half(qkv[j * D * 3 + D + h * 64 + f]);
+                    half_values[h][j * 64 + f] = round_half(qkv[j * D * 3 + 2 * D + h * 64 + f]);
+                }
+        }
+    }
+#pragma omp parallel
+    {
+        std::vector<float> row(T), p(T);
+        std::vector<uint16_t> hrow(T);
+#pragma omp for schedule(dynamic, 4) collapse(2)
+        for (int64_t h = 0; h < heads; ++h) {
+            for (int64_t i = 0; i < static_cast<int64_t>(T); ++i) {
+                const float* q = qkv + static_cast<size_t>(i) * D * 3 + h * 64;
+                if (!fp16) {
+                    // bmm.glsl with input_qkv_query=1, weight_qkv_kind=1: sequential
+                    // accumulation over the 64 features of (q*0.125)*k.
+                    for (size_t j = 0; j < T; ++j) {
+                        const float* k = qkv + j * D * 3 + D + h * 64;
+                        float s = 0.0f;
+                        for (int f = 0; f < 64; ++f) {
+                            const float sq = q[f] * 0.125f;
+                            s = s + sq * k[f];
+                        }
+                        row[j] = s;
+                    }
+                    softmax_row_fp32(row.data(), tokens, p.data());
+                    // bmm.glsl value pass: sequential over source tokens j.
+                    float* o = out + static_cast<size_t>(i) * D + h * 64;
+                    for (int f = 0; f < 64; ++f) {
+                        float s = 0.0f;
+                        for (size_t j = 0; j < T; ++j) s = s + p[j] * qkv[j * D * 3 + 2 * D + h * 64 + f];
+                        o[f] = s;
+                    }
+                } else {
+                    // bmm_score_fp16.glsl:29-70: fp16(q*0.125), fp16(k), fp16
+                    // products accumulated in fp32 (sequentially over the 64
+                    // features), stored as fp16. Eight keys per AVX lane set.
+                    const std::vector<float>& kt = half_keys_t[h];
+                    float qr[64];
+                    for (int f = 0; f < 64; ++f) qr[f] = round_half(q[f] * 0.125f);
+                    size_t j = 0;
+                    for (; j + 8 <= T; j += 8) {
+                        __m256 s = _mm256_setzero_ps();
+                        for (int f = 0; f < 64; ++f) {
+                            const __m256 prod = _mm256_mul_ps(_mm256_set1_ps(qr[f]), _mm256_loadu_ps(&kt[f * T + j]));
+                            s = _mm256_add_ps(s, round_half8(prod));
+                        }
+                        alignas(32) float tmp[8];
+                        _mm256_store_ps(tmp, s);
+                        for (int l = 0; l < 8; ++l) hrow[j + l] = f2h(tmp[l]);
+                    }
+                    for (; j < T; ++j) {
+                        float s = 0.0f;
+                        for (int f = 0; f < 64; ++f) s = s + round_half(qr[f] * kt[f * T + j]);
+                        hrow[j] = f2h(s);
+                    }
+                    // softmax_lastdim_half.glsl: word w = (2w, 2w+1) handled by
+                    // lane w % 128; exp stored as fp16, fp32 denominator.
+                    float maximum = -3.402823466e+38f;
+                    for (size_t j = 0; j < T; ++j) maximum = std::max(maximum, h2f(hrow[j]));
+                    const size_t words = (T + 1) / 2;
+                    float partial[128];
+                    for (uint32_t lane = 0; lane < 128; ++lane) {
+                        float d = 0.0f;
+                        for (size_t w = lane; w < words; w += 128) {
+                            const size_t j0 = 2 * w, j1 = 2 * w + 1;
+                            const float ex = std::exp(h2f(hrow[j0]) - maximum);
+                            float ey = 0.0f;
+                            if (j1 < T) ey = std::exp(h2f(hrow[j1]) - maximum);
+                            hrow[j0] = f2h(ex);
+                            if (j1 < T) hrow[j1] = f2h(ey);
+                            d = d + (ex + ey);
+                        }
+                        partial[lane] = d;
+                    }
+                    for (uint32_t stride = 64; stride > 0; stride >>= 1)
+                        for (uint32_t lane = 0; lane < stride; ++lane)
+                            partial[lane] = partial[lane] + partial[lane + stride];
+                    const float inverse = 1.0f / std::max(partial[0], 1.0e-20f);
+                    for (size_t j = 0; j < T; ++j) p[j] = round_half(h2f(hrow[j]) * inverse);
+                    // bmm_value_fp16.glsl: fp16 products, fp32 accumulation
+                    // sequentially over the source tokens; 8 features per lane set.
+                    const std::vector<float>& vr = half_values[h];
+                    float* o = out + static_cast<size_t>(i) * D + h * 64;
+                    for (int f0 = 0; f0 < 64; f0 += 8) {
+                        __m256 s = _mm256_setzero_ps();
+                        for (size_t jj = 0; jj < T; ++jj) {
+                            const __m256 prod = _mm256_mul_ps(_mm256_set1_ps(p[jj]), _mm256_loadu_ps(&vr[jj * 64 + f0]));
+                            s = _mm256_add_ps(s, round_half8(prod));
+                        }
+                        _mm256_storeu_ps(o + f0, s);
+                    }
+                }
+                if (probabilities) std::memcpy(probabilities + (h * T + i) * T, p.data(), T * sizeof(float));
+            }
+        }
+    }
+}
+
+void orc_bilinear_align_true(const float* input, uint32_t iw, uint32_t ih, uint32_t ow,
+                             uint32_t oh, uint32_t channels, float* out) {
+    // bilinear_align_true.glsl:27-63
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t c = 0; c < channels; ++c) {
+        for (int64_t oy = 0; oy < oh; ++oy) {
+            const float sy = oh > 1 ? static_cast<float>(oy) * static_cast<float>(ih - 1) / static_cast<float>(oh - 1) : 0.0f;
+            const uint32_t y0 = static_cast<uint32_t>(std::floor(sy));
+            const uint32_t y1 = std::min(y0 + 1, ih - 1);
+            const float fy = sy - static_cast<float>(y0);
+            const float* src = input + static_cast<size_t>(c) * ih * iw;
+            for (uint32_t ox = 0; ox < ow; ++ox) {
+                const float sx = ow > 1 ? static_cast<float>(ox) * static_cast<float>(iw - 1) / static_cast<float>(ow - 1) : 0.0f;
+                const uint32_t x0 = static_cast<uint32_t>(std::floor(sx));
+                const uint32_t x1 = std::min(x0 + 1, iw - 1);
+                const float fx = sx - static_cast<float>(x0);
+                const float top = src[y0 * iw + x0] * (1.0f - fx) + src[y0 * iw + x1] * fx;
+                const float bottom = src[y1 * iw + x0] * (1.0f - fx) + src[y1 * iw + x1] * fx;
+                out[(static_cast<size_t>(c) * oh + oy) * ow + ox] = top * (1.0f - fy) + bottom * fy;
+            }
+        }
+    }
+}
+
+void orc_reduce_minmax(const float* input, uint64_t count, float* range) {
+    float mn = std::numeric_limits<float>::infinity();
+    float mx = -std::numeric_limits<float>::infinity();
+    for (uint64_t i = 0; i < count; ++i) {
+        mn = std::min(mn, input[i]);
+        mx = std::max(mx, input[i]);
+    }
+    range[0] = mn;
+    range[1] = mx;
+}
+
+void orc_normalize_relative(float* depth, const float* range, uint64_t count) {
+    const float minimum = range[0];
+    const float span = range[1] - minimum;
+    for (uint64_t i = 0; i < count; ++i)
+        depth[i] = span > 1.0e-12f ? std::min(std::max((depth[i] - minimum) / span, 0.0f), 1.0f) : 0.0f;
+}
+
+static inline void cubic_coeffs(float t, float c[4]) {
+    // position_bicubic.glsl:39-56 (A = -0.75)
+    const float a = -0.75f;
+    auto cc1 = [a](float x) { return ((a + 2.0f) * x - (a + 3.0f)) * x * x + 1.0f; };
+    auto cc2 = [a](float x) { return ((a * x - 5.0f * a) * x + 8.0f * a) * x - 4.0f * a; };
+    c[0] = cc2(t + 1.0f);
+    c[1] = cc1(t);
+    c[2] = cc1(1.0f - t);
+    c[3] = cc2((1.0f - t) + 1.0f);
+}
+
+static inline float cubic_interp(float x0, float x1, float x2, float x3, float t) {
+    float c[4];
+    cubic_coeffs(t, c);
+    return x0 * c[0] + x1 * c[1] + x2 * c[2] + x3 * c[3];
+}
+
+void orc_position_bicubic(const float* position, uint32_t pw, uint32_t ph, uint32_t D,
+                          float* out) {
+    const bool identity = pw == 37 && ph == 37;
+    const float scale_x = identity ? 1.0f : static_cast<float>(1.0 / ((static_cast<double>(pw) + 0.1) / 37.0));
+    const float scale_y = identity ? 1.0f : static_cast<float>(1.0 / ((static_cast<double>(ph) + 0.1) / 37.0));
+    const size_t spatial = static_cast<size_t>(pw) * ph;
+#pragma omp parallel for schedule(static)
+    for (int64_t d = 0; d < D; ++d) {
+        for (uint32_t y = 0; y < ph; ++y) {
+            for (uint32_t x = 0; x < pw; ++x) {
+                const float srcx = (static_cast<float>(x) + 0.5f) * scale_x - 0.5f;
+                const float srcy = (static_cast<float>(y) + 0.5f) * scale_y - 0.5f;
+                const int bx = static_cast<int>(std::floor(srcx));
+                const int by = static_cast<int>(std::floor(srcy));
+                const float tx = srcx - static_cast<float>(bx);
+                const float ty = srcy - static_cast<float>(by);
+                auto fetch = [&](int xx, int yy) {
+                    xx = std::min(std::max(xx, 0), 36);
+                    yy = std::min(std::max(yy, 0), 36);
+                    // physical strides {D, 37*D, 1, 1370*D} + offset D (skip CLS)
+                    return position[static_cast<size_t>(xx) * D + static_cast<size_t>(yy) * 37 * D + d + D];
+                };
+                float rows[4];
+                for (int k = 0; k < 4; ++k) {
+                    const int yy = by - 1 + k;
+                    rows[k] = cubic_interp(fetch(bx - 1, yy), fetch(bx, yy), fetch(bx + 1, yy), fetch(bx + 2, yy), tx);
+                }
+                out[static_cast<size_t>(d) * spatial + static_cast<size_t>(y) * pw + x] =
+                    cubic_interp(rows[0], rows[1], rows[2], rows[3], ty);
+            }
+        }
+    }
+}
+
+void orc_prepare_tokens_int8(const float* image, const int8_t* w8, const float* w_scales,
+                             const float* bias, const float* class_token,
+                             const float* position, uint32_t width, uint32_t height,
+                             uint32_t D, float* tokens) {
+    // operators.cpp:1270-1308 (int8 branch) then :1323-1405 (position)
+    const uint32_t pw = width / 14, ph = height / 14, spatial = pw * ph;
+    constexpr uint32_t K = 3 * 14 * 14;
+    std::vector<int8_t> q(static_cast<size_t>(spatial) * K);
+    std::vector<float> s(spatial);
+    orc_im2col_quantize(image, width, height, 3, pw, ph, 14, 14, 0, q.data(), s.data());
+    std::memcpy(tokens, class_token, D * sizeof(float));
+    std::vector<int32_t> acc(static_cast<size_t>(spatial) * D);
+    gemm_i8_blocked(q.data(), w8, spatial, D, K, acc.data());
+    orc_linear_epilogue(acc.data(), s.data(), w_scales, bias, spatial, D, 1, spatial + 1, 0, tokens);
+    std::vector<float> interp(static_cast<size_t>(spatial) * D);
+    orc_position_bicubic(position, pw, ph, D, interp.data());
+    // add_position.glsl:25-41
+    const size_t count = static_cast<size_t>(spatial + 1) * D;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) {
+        const size_t token = static_cast<size_t>(i) / D, feature = static_cast<size_t>(i) % D;
+        const float p = token == 0 ? position[feature] : interp[feature * spatial + (token - 1)];
+        tokens[i] = tokens[i] + p;
+    }
+}
+
+void orc_project_tokens_int8(const float* tokens, const int8_t* w8, const float* w_scales,
+                             const float* bias, uint32_t width, uint32_t height, uint32_t D,
+                             uint32_t C, float* out) {
+    // operators.cpp:1483-1526: skip CLS, GEMM, channel-major output
+    const uint32_t spatial = width * height;
+    std::vector<int8_t> q(static_cast<size_t>(spatial) * D);
+    std::vector<float> s(spatial);
+    orc_quantize_rows(tokens, spatial, D, D, q.data(), s.data());
+    std::vector<int32_t> acc(static_cast<size_t>(spatial) * C);
+    gemm_i8_blocked(q.data(), w8, spatial, C, D, acc.data());
+    orc_linear_epilogue(acc.data(), s.data(), w_scales, bias, spatial, C, 0, spatial, 1, out);
+}
+
+void orc_conv2d_int8(const float* input, const int8_t* w8, const float* w_scales,
+                     const float* bias, uint32_t width, uint32_t height, uint32_t ic,
+                     uint32_t oc, uint32_t kernel, uint32_t stride, uint32_t padding,
+                     int has_bias, float* out) {
+    // operators.cpp:1735-1805
+    const uint32_t ow = (width + 2 * padding - kernel) / stride + 1;
+    const uint32_t oh = (height + 2 * padding - kernel) / stride + 1;
+    const uint32_t rows = ow * oh, K = ic * kernel * kernel;
+    std::vector<int8_t> q(static_cast<size_t>(rows) * K);
+    std::vector<float> s(rows);
+    orc_im2col_quantize(input, width, height, ic, ow, oh, kernel, stride,
+                        static_cast<int32_t>(padding), q.data(), s.data());
+    std::vector<int32_t> acc(static_cast<size_t>(rows) * oc);
+    gemm_i8_blocked(q.data(), w8, rows, oc, K, acc.data());
+    orc_linear_epilogue(acc.data(), s.data(), w_scales, has_bias ? bias : nullptr, rows, oc, 0,
+                        rows, 1, out);
+}
+
+void orc_conv_transpose_int8(const float* input, const int8_t* w8, const float* w_scales,
+                             const float* bias, uint32_t width, uint32_t height,
+                             uint32_t ic, uint32_t oc, uint32_t kernel, float* out) {
+    // operators.cpp:1908-1976 + conv_transpose_int8.glsl:31-58
+    const uint32_t rows = width * height;
+    std::vector<int8_t> q(static_cast<size_t>(rows) * ic);
+    std::vector<float> s(rows);
+    orc_im2col_quantize(input, width, height, ic, width, height, 1, 1, 0, q.data(), s.data());
+    const uint32_t wrows = kernel * kernel * oc;
+    std::vector<int32_t> acc(static_cast<size_t>(rows) * wrows);
+    gemm_i8_blocked(q.data(), w8, rows, wrows, ic, acc.data());
+    const uint32_t ow = width * kernel, oh = height * kernel;
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t c = 0; c < oc; ++c) {
+        for (int64_t oy = 0; oy < oh; ++oy) {
+            for (uint32_t ox = 0; ox < ow; ++ox) {
+                const uint32_t ix = ox / kernel, iy = static_cast<uint32_t>(oy) / kernel;
+                const uint32_t kx = ox % kernel, ky = static_cast<uint32_t>(oy) % kernel;
+                const uint32_t row = iy * width + ix;
+                const uint32_t wrow = (ky * kernel + kx) * oc + static_cast<uint32_t>(c);
+                out[(static_cast<size_t>(c) * oh + oy) * ow + ox] =
+                    dequant(acc[static_cast<size_t>(row) * wrows + wrow], s[row], w_scales[wrow], bias[c]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Model
+
+static bool use_int8_weight(const std::string& name, const Tensor& t) {
+    // gpu_model.cpp:16-44
+    const std::string suffix = ".weight";
+    if (name.size() < suffix.size() || name.compare(name.size() - suffix.size(), suffix.size(), suffix) != 0) return false;
+    bool half = false;
+    if (name == "pretrained.patch_embed.proj.weight" || name.rfind("depth_head.", 0) == 0) half = true;
+    else if (name.rfind("pretrained.blocks.", 0) == 0)
+        half = name.find(".attn.") != std::string::npos || name.find(".mlp.") != std::string::npos;
+    if (!half || t.dims[0] == 0) return false;
+    uint64_t elements = 1;
+    for (uint32_t i = 0; i < t.rank; ++i) elements *= t.dims[i];
+    if (t.rank == 2) return t.dims[1] % 4 == 0;
+    if (t.rank != 4) return false;
+    if (name == "depth_head.resize_layers.0.weight" || name == "depth_head.resize_layers.1.weight")
+        return t.dims[0] % 4 == 0;
+    return (elements / t.dims[0]) % 4 == 0;
+}
+
+orc_model* orc_model_load(const char* path, int encoder, char* error, size_t error_bytes) {
+    auto fail = [&](const std::string& msg) -> orc_model* {
+        if (error && error_bytes) std::snprintf(error, error_bytes, "%s", msg.c_str());
+        return nullptr;
+    };
+    std::ifstream file(path, std::ios::binary);
+    if (!file) return fail("cannot open model");
+    std::vector<char> bytes((std::istreambuf_iterator<char>(file)), std::istreambuf_iterator<char>());
+    if (bytes.size() < sizeof(Header)) return fail("truncated");
+    Header h;
+    std::memcpy(&h, bytes.data(), sizeof(h));
+    if (std::memcmp(h.magic, "DAV2MOD\0", 8) != 0 || h.version != 1 || h.endian != 0x01020304u)
+        return fail("bad header");
+    if (h.encoder != static_cast<uint32_t>(encoder)) return fail("encoder mismatch");
+    auto model = std::make_unique<orc_model>();
+    model->encoder = encoder;
+    switch (encoder) {
+        case 0: model->dim = 384; model->heads = 6; model->blocks = 12; model->features = 64;
+            model->capture[0] = 2; model->capture[1] = 5; model->capture[2] = 8; model->capture[3] = 11;
+            model->project[0] = 48; model->project[1] = 96; model->project[2] = 192; model->project[3] = 384; break;
+        case 1: model->dim = 768; model->heads = 12; model->blocks = 12; model->features = 128;
+            model->capture[0] = 2; model->capture[1] = 5; model->capture[2] = 8; model->capture[3] = 11;
+            model->project[0] = 96; model->project[1] = 192; model->project[2] = 384; model->project[3] = 768; break;
+        case 2: model->dim = 1024; model->heads = 16; model->blocks = 24; model->features = 256;
+            model->capture[0] = 4; model->capture[1] = 11; model->capture[2] = 17; model->capture[3] = 23;
+            model->project[0] = 256; model->project[1] = 512; model->project[2] = 1024; model->project[3] = 1024; break;
+        default: return fail("bad encoder");
+    }
+    if (h.directory_offset + static_cast<uint64_t>(h.tensor_count) * sizeof(Record) > bytes.size())
+        return fail("bad directory");
+    for (uint32_t i = 0; i < h.tensor_count; ++i) {
+        Record r;
+        std::memcpy(&r, bytes.data() + h.directory_offset + static_cast<size_t>(i) * sizeof(Record), sizeof(r));
+        if (r.data_offset + r.data_bytes > bytes.size() || r.element_count * 4 != r.data_bytes)
+            return fail("bad record");
+        Tensor t;
+        t.rank = r.rank;
+        for (int d = 0; d < 4; ++d) t.dims[d] = r.dims[d];
+        t.data.resize(r.element_count);
+        std::memcpy(t.data.data(), bytes.data() + r.data_offset, r.data_bytes);
+        if (crc32_impl(t.data.data(), r.data_bytes) != r.crc32) return fail("crc mismatch");
+        const std::string name(r.name, strnlen(r.name, sizeof(r.name)));
+        if (use_int8_weight(name, t)) {
+            const bool convT = name == "depth_head.resize_layers.0.weight" || name == "depth_head.resize_layers.1.weight";
+            if (convT) {
+                const uint32_t ic = static_cast<uint32_t>(t.dims[0]), oc = static_cast<uint32_t>(t.dims[1]);
+                const uint32_t k = static_cast<uint32_t>(t.dims[2]);
+                t.q.resize(static_cast<size_t>(k) * k * oc * ic);
+                t.qscale.resize(static_cast<size_t>(k) * k * oc);
+                orc_quantize_convT_weight(t.data.data(), ic, oc, k, t.q.data(), t.qscale.data());
+            } else {
+                const uint64_t rows = t.dims[0], cols = r.element_count / rows;
+                t.q.resize(r.element_count);
+                t.qscale.resize(rows);
+                orc_quantize_weight_rows(t.data.data(), rows, cols, t.q.data(), t.qscale.data());
+            }
+        }
+        model->tensors.emplace(name, std::move(t));
+    }
+    return model.release();
+}
+
+void orc_model_free(orc_model* model) { delete model; }
+
+namespace {
+
+struct Map {
+    std::vector<float> v;
+    uint32_t w = 0, h = 0, c = 0;
+};
+
+std::string blk(uint32_t b, const char* s) { return "pretrained.blocks." + std::to_string(b) + s; }
+
+void encoder_block(const orc_model& m, std::vector<float>& cur, uint32_t T, uint32_t b, int fp16) {
+    const uint32_t D = m.dim;
+    const size_t n = static_cast<size_t>(T) * D;
+    std::vector<float> norm(n), qkv(n * 3), attn(n), tmp(n), next(n), hidden(n * 4);
+    auto lin = [&](const std::vector<float>& in, const std::string& w, const std::string& bias,
+                   uint32_t ic, uint32_t oc, bool gelu, std::vector<float>& out) {
+        const Tensor& wt = m.t(w);
+        orc_linear_int8(in.data(), wt.q.data(), wt.qscale.data(), m.t(bias).data.data(), T, ic, oc, gelu, out.data());
+    };
+    orc_layer_norm(cur.data(), m.t(blk(b, ".norm1.weight")).data.data(), m.t(blk(b, ".norm1.bias")).data.data(),
+                   T, D, 1.0e-6f, norm.data());
+    lin(norm, blk(b, ".attn.qkv.weight"), blk(b, ".attn.qkv.bias"), D, 3 * D, false, qkv);
+    orc_attention_head64(qkv.data(), T, m.heads, fp16, attn.data(), nullptr);
+    lin(attn, blk(b, ".attn.proj.weight"), blk(b, ".attn.proj.bias"), D, D, false, tmp);
+    orc_add_scaled(cur.data(), tmp.data(), m.t(blk(b, ".ls1.gamma")).data.data(), n, D, next.data());
+    cur.swap(next);
+    orc_layer_norm(cur.data(), m.t(blk(b, ".norm2.weight")).data.data(), m.t(blk(b, ".norm2.bias")).data.data(),
+                   T, D, 1.0e-6f, norm.data());
+    lin(norm, blk(b, ".mlp.fc1.weight"), blk(b, ".mlp.fc1.bias"), D, 4 * D, true, hidden);
+    lin(hidden, blk(b, ".mlp.fc2.weight"), blk(b, ".mlp.fc2.bias"), 4 * D, D, false, tmp);
+    orc_add_scaled(cur.data(), tmp.data(), m.t(blk(b, ".ls2.gamma")).data.data(), n, D, next.data());
+    cur.swap(next);
+}
+
+Map conv(const orc_model& m, const Map& in, const std::string& w, const std::string& b,
+         uint32_t oc, uint32_t k, uint32_t stride, uint32_t pad, bool has_bias) {
+    // dpt.cpp:479-535 with every conv routed to conv2d_int8
+    Map out;
+    out.w = (in.w + 2 * pad - k) / stride + 1;
+    out.h = (in.h + 2 * pad - k) / stride + 1;
+    out.c = oc;
+    out.v.resize(static_cast<size_t>(out.w) * out.h * oc);
+    const Tensor& wt = m.t(w);
+    if (wt.q.empty()) throw std::runtime_error("oracle: conv weight not int8: " + w);
+    orc_conv2d_int8(in.v.data(), wt.q.data(), wt.qscale.data(), has_bias ? m.t(b).data.data() : nullptr,
+                    in.w, in.h, in.c, oc, k, stride, pad, has_bias ? 1 : 0, out.v.data());
+    return out;
+}
+
+Map residual_unit(const orc_model& m, const Map& in, const std::string& prefix) {
+    // dpt.cpp:537-572
+    Map act = in;
+    orc_relu(in.v.data(), in.v.size(), act.v.data());
+    Map first = conv(m, act, prefix + ".conv1.weight", prefix + ".conv1.bias", in.c, 3, 1, 1, true);
+    orc_relu(first.v.data(), first.v.size(), first.v.data());
+    Map second = conv(m, first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.c, 3, 1, 1, true);
+    orc_add(second.v.data(), in.v.data(), second.v.size(), second.v.data());
+    return second;
+}
+
+Map fusion(const orc_model& m, Map path, const Map* skip, const std::string& prefix, uint32_t ow, uint32_t oh) {
+    // dpt.cpp:574-615
+    if (skip) {
+        Map processed = residual_unit(m, *skip, prefix + ".resConfUnit1");
+        orc_add(path.v.data(), processed.v.data(), path.v.size(), path.v.data());
+    }
+    path = residual_unit(m, path, prefix + ".resConfUnit2");
+    Map resized;
+    resized.w = ow; resized.h = oh; resized.c = m.features;
+    resized.v.resize(static_cast<size_t>(ow) * oh * m.features);
+    orc_bilinear_align_true(path.v.data(), path.w, path.h, ow, oh, m.features, resized.v.data());
+    return conv(m, resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", m.features, 1, 1, 0, true);
+}
+
+}  // namespace
+
+int orc_model_encoder_blocks(orc_model* model, float* tokens, uint32_t T, uint32_t first,
+                             uint32_t last, int fp16) {
+    try {
+        std::vector<float> cur(tokens, tokens + static_cast<size_t>(T) * model->dim);
+        for (uint32_t b = first; b < last && b < model->blocks; ++b) encoder_block(*model, cur, T, b, fp16);
+        std::memcpy(tokens, cur.data(), cur.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "oracle: %s\n", e.what());
+        return 1;
+    }
+}
+
+int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t height,
+                    int fp16, float* depth, float* pre_relu, float* features) {
+    try {
+        const orc_model& m = *model;
+        const uint32_t D = m.dim, pw = width / 14, ph = height / 14, T = pw * ph + 1;
+        const size_t n = static_cast<size_t>(T) * D;
+        std::vector<float> cur(n);
+        const Tensor& pe = m.t("pretrained.patch_embed.proj.weight");
+        orc_prepare_tokens_int8(chw, pe.q.data(), pe.qscale.data(), m.t("pretrained.patch_embed.proj.bias").data.data(),
+                                m.t("pretrained.cls_token").data.data(), m.t("pretrained.pos_embed").data.data(),
+                                width, height, D, cur.data());
+        std::vector<std::vector<float>> feats;
+        uint32_t ci = 0;
+        for (uint32_t b = 0; b < m.blocks; ++b) {
+            encoder_block(m, cur, T, b, fp16);
+            if (ci < 4 && b == m.capture[ci]) {
+                std::vector<float> f(n);
+                orc_layer_norm(cur.data(), m.t("pretrained.norm.weight").data.data(),
+                               m.t("pretrained.norm.bias").data.data(), T, D, 1.0e-6f, f.data());
+                if (features) std::memcpy(features + ci * n, f.data(), n * sizeof(float));
+                feats.push_back(std::move(f));
+                ++ci;
+            }
+        }
+        // dpt.cpp:635-736
+        Map layers[4];
+        for (uint32_t i = 0; i < 4; ++i) {
+            const std::string prefix = "depth_head.projects." + std::to_string(i);
+            Map proj;
+            proj.w = pw; proj.h = ph; proj.c = m.project[i];
+            proj.v.resize(static_cast<size_t>(pw) * ph * proj.c);
+            const Tensor& wt = m.t(prefix + ".weight");
+            orc_project_tokens_int8(feats[i].data(), wt.q.data(), wt.qscale.data(), m.t(prefix + ".bias").data.data(),
+                                    pw, ph, D, proj.c, proj.v.data());
+            if (i < 2) {
+                const uint32_t k = i == 0 ? 4 : 2;
+                const std::string r = "depth_head.resize_layers." + std::to_string(i);
+                Map res;
+                res.w = pw * k; res.h = ph * k; res.c = proj.c;
+                res.v.resize(static_cast<size_t>(res.w) * res.h * res.c);
+                const Tensor& rw = m.t(r + ".weight");
+                orc_conv_transpose_int8(proj.v.data(), rw.q.data(), rw.qscale.data(), m.t(r + ".bias").data.data(),
+                                        pw, ph, proj.c, proj.c, k, res.v.data());
+                layers[i] = std::move(res);
+            } else if (i == 2) {
+                layers[i] = std::move(proj);
+            } else {
+                layers[i] = conv(m, proj, "depth_head.resize_layers.3.weight", "depth_head.resize_layers.3.bias",
+                                 m.project[3], 3, 2, 1, true);
+            }
+        }
+        Map refined[4];
+        for (uint32_t i = 0; i < 4; ++i)
+            refined[i] = conv(m, layers[i], "depth_head.scratch.layer" + std::to_string(i + 1) + "_rn.weight", "",
+                              m.features, 3, 1, 1, false);
+        Map path = fusion(m, refined[3], nullptr, "depth_head.scratch.refinenet4", refined[2].w, refined[2].h);
+        path = fusion(m, path, &refined[2], "depth_head.scratch.refinenet3", refined[1].w, refined[1].h);
+        path = fusion(m, path, &refined[1], "depth_head.scratch.refinenet2", refined[0].w, refined[0].h);
+        path = fusion(m, path, &refined[0], "depth_head.scratch.refinenet1", refined[0].w * 2, refined[0].h * 2);
+        path = conv(m, path, "depth_head.scratch.output_conv1.weight", "depth_head.scratch.output_conv1.bias",
+                    m.features / 2, 3, 1, 1, true);
+        Map full;
+        full.w = pw * 14; full.h = ph * 14; full.c = m.features / 2;
+        full.v.resize(static_cast<size_t>(full.w) * full.h * full.c);
+        orc_bilinear_align_true(path.v.data(), path.w, path.h, full.w, full.h, full.c, full.v.data());
+        full = conv(m, full, "depth_head.scratch.output_conv2.0.weight", "depth_head.scratch.output_conv2.0.bias",
+                    32, 3, 1, 1, true);
+        orc_relu(full.v.data(), full.v.size(), full.v.data());
+        Map out = conv(m, full, "depth_head.scratch.output_conv2.2.weight", "depth_head.scratch.output_conv2.2.bias",
+                       1, 1, 1, 0, true);
+        if (pre_relu) std::memcpy(pre_relu, out.v.data(), out.v.size() * sizeof(float));
+        orc_relu(out.v.data(), out.v.size(), depth);
+        return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "oracle: %s\n", e.what());
+        return 1;
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,134 @@
+/*
+ * CPU oracle for the Depth-Anything-V2 int8 operator hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library restates, on the CPU, what the
+ * reference runtime's Vulkan compute shaders and host quantizer compute, so
+ * that the HIP implementation can be checked against it on identical inputs.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * it; the product library never links, loads or calls it.
+ *
+ * Each function names the reference file:line it follows. Layout conventions:
+ *  - int8 matrices are row-major [rows][K] bytes, K unpadded (the byte view of
+ *    the reference's little-endian 4x8 packing, quantize_rows_int8_fused.glsl:51);
+ *  - feature maps are CHW float32; token matrices are row-major [T][D].
+ *
+ * Pinning (see tests/test_oracle_*.py): quantizers by hand-derived vectors and
+ * invariants, the int32 GEMM by exact integer brute force, conv/conv-transpose
+ * by the reference's own int8-vs-fp32 tolerance tests, LN/softmax/attention/
+ * bilinear/bicubic by the reference KATs and by torch's CPU routines, the
+ * graph by the reference's int8 acceptance gate against an fp32 forward.
+ */
+#ifndef DAV2_ORACLE_H
+#define DAV2_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int orc_set_threads(int threads);
+int orc_get_threads(void);
+
+/* a1: quantize_rows_int8_fused.glsl:20-55 */
+void orc_quantize_rows(const float* input, uint32_t rows, uint32_t columns,
+                       uint32_t input_offset, int8_t* q, float* scales);
+/* a2: im2col_quantize_int8.glsl:26-83 (rows = OW*OH, K = C*k*k) */
+void orc_im2col_quantize(const float* input, uint32_t input_width,
+                         uint32_t input_height, uint32_t input_channels,
+                         uint32_t output_width, uint32_t output_height,
+                         uint32_t kernel, uint32_t stride, int32_t padding,
+                         int8_t* q, float* scales);
+/* a9: gpu_model.cpp:241-264, per output row */
+void orc_quantize_weight_rows(const float* weight, uint64_t rows,
+                              uint64_t columns, int8_t* q, float* scales);
+/* a9: gpu_model.cpp:210-240, ConvTranspose [IC][OC][k][k] -> rows (ky*k+kx)*OC+oc */
+void orc_quantize_convT_weight(const float* weight, uint32_t in_channels,
+                               uint32_t out_channels, uint32_t kernel,
+                               int8_t* q, float* scales);
+/* a3: exact int32 accumulators, acc[m][n] = sum_k a[m][k]*b[n][k] */
+void orc_gemm_i8(const int8_t* a, const int8_t* b, uint32_t m, uint32_t n,
+                 uint32_t k, int32_t* acc);
+/* a3: linear_int8_tiled.glsl:99-116 epilogue */
+void orc_linear_epilogue(const int32_t* acc, const float* input_scales,
+                         const float* weight_scales, const float* bias,
+                         uint32_t rows, uint32_t columns,
+                         uint32_t output_row_offset, uint32_t output_row_stride,
+                         int transposed, float* out);
+
+/* Operator surface (operators.h), fp32 in / fp32 out. */
+void orc_linear_int8(const float* input, const int8_t* w8, const float* w_scales,
+                     const float* bias, uint32_t rows, uint32_t in_columns,
+                     uint32_t out_columns, int gelu, float* out);
+void orc_gelu(const float* input, uint64_t count, float* out);
+void orc_layer_norm(const float* input, const float* weight, const float* bias,
+                    uint32_t rows, uint32_t columns, float epsilon, float* out);
+void orc_add_scaled(const float* residual, const float* addend,
+                    const float* scale, uint64_t count, uint32_t columns,
+                    float* out);
+void orc_add(const float* left, const float* right, uint64_t count, float* out);
+void orc_relu(const float* input, uint64_t count, float* out);
+void orc_softmax_rows(const float* input, uint64_t rows, uint32_t columns,
+                      float* out);
+/* fp16: 1 -> softmax_lastdim_half/bmm_*_fp16 arithmetic, 0 -> fp32 bmm/softmax.
+ * scores (optional, fp32 view) receives the probabilities [H][T][T]. */
+void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads,
+                          int fp16, float* out, float* probabilities);
+void orc_bilinear_align_true(const float* input, uint32_t input_width,
+                             uint32_t input_height, uint32_t output_width,
+                             uint32_t output_height, uint32_t channels,
+                             float* out);
+void orc_reduce_minmax(const float* input, uint64_t count, float* range);
+void orc_normalize_relative(float* depth, const float* range, uint64_t count);
+/* position_bicubic.glsl:76-105 with the block set up at operators.cpp:1346-1364;
+ * output CHW [D][ph][pw] */
+void orc_position_bicubic(const float* position, uint32_t patch_width,
+                          uint32_t patch_height, uint32_t embedding,
+                          float* out);
+void orc_prepare_tokens_int8(const float* image, const int8_t* w8,
+                             const float* w_scales, const float* bias,
+                             const float* class_token, const float* position,
+                             uint32_t width, uint32_t height,
+                             uint32_t embedding, float* tokens);
+void orc_project_tokens_int8(const float* tokens, const int8_t* w8,
+                             const float* w_scales, const float* bias,
+                             uint32_t width, uint32_t height,
+                             uint32_t embedding, uint32_t out_channels,
+                             float* out);
+void orc_conv2d_int8(const float* input, const int8_t* w8, const float* w_scales,
+                     const float* bias, uint32_t width, uint32_t height,
+                     uint32_t in_channels, uint32_t out_channels,
+                     uint32_t kernel, uint32_t stride, uint32_t padding,
+                     int has_bias, float* out);
+void orc_conv_transpose_int8(const float* input, const int8_t* w8,
+                             const float* w_scales, const float* bias,
+                             uint32_t width, uint32_t height,
+                             uint32_t in_channels, uint32_t out_channels,
+                             uint32_t kernel, float* out);
+
+/* Whole int8 graph: encoder.cpp:322-597 + dpt.cpp:628-863 (all DPT convs int8). */
+typedef struct orc_model orc_model;
+orc_model* orc_model_load(const char* path, int encoder, char* error,
+                          size_t error_bytes);
+void orc_model_free(orc_model* model);
+/* depth: W*H raw ReLU depth. pre_relu (nullable): W*H before the final ReLU.
+ * features (nullable): 4*T*D captured encoder features.
+ * Returns 0 on success. */
+int orc_model_infer(orc_model* model, const float* chw, uint32_t width,
+                    uint32_t height, int fp16_attention, float* depth,
+                    float* pre_relu, float* features);
+/* Encoder blocks [first, last) only, on tokens [T][D] in place (timing sample). */
+int orc_model_encoder_blocks(orc_model* model, float* tokens, uint32_t tokens_count,
+                             uint32_t first, uint32_t last, int fp16_attention);
+
+/* IEEE binary16 round-to-nearest-even helpers used by the fp16 attention path. */
+uint16_t orc_float_to_half(float value);
+float orc_half_to_float(uint16_t value);
+uint32_t orc_crc32(const void* data, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

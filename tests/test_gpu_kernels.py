@@ -1,0 +1,369 @@
+"""HIP kernels vs the CPU oracle, through the C-ABI launchers (include/dav2_hip.h).
+
+Integer stages (int8 bytes, scales, int32 accumulators) must match bit for
+bit; fp32 stages whose GPU code evaluates the same expression order match
+bit for bit too, the rest within the stated tolerances.
+"""
+
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+from gpu_util import dev, empty, host, ok, ptr, stream
+from oracle_py import pad_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _announce(*what):
+    print("case:", *what, flush=True)
+    sys.stdout.flush()
+
+
+# ---------------------------------------------------------------------------
+# a1 quantize_rows_int8_fused.glsl
+@pytest.mark.parametrize("rows,cols,offset_rows", [(1370, 384, 0), (1370, 1024, 0), (1369, 4096, 0), (7, 8, 0),
+                                                   (3, 8192, 0), (1369, 1024, 1), (1, 1536, 0)])
+def test_quantize_rows_bit_exact(gpu, lib, oracle, rows, cols, offset_rows):
+    torch = gpu
+    _announce("quantize_rows", rows, cols, offset_rows)
+    rng = np.random.default_rng(rows + cols)
+    x = (rng.standard_normal((rows + offset_rows, cols)) * rng.uniform(0.01, 30, (rows + offset_rows, 1))).astype(np.float32)
+    if rows > 2:
+        x[offset_rows + 1] = 0.0  # an all-zero row
+    q_ref, s_ref = oracle.quantize_rows(x, rows, cols, offset_rows * cols)
+    ld = (cols + 63) // 64 * 64
+    xd = dev(torch, x)
+    qd = torch.full((rows, ld), 0x55, dtype=torch.int8, device="cuda")
+    sd = empty(torch, (rows,), torch.float32)
+    ok(lib, lib.dav2_hip_quantize_rows_i8(ptr(xd), offset_rows * cols, rows, cols, ptr(qd), ld, ptr(sd), stream(torch)))
+    q = host(torch, qd)
+    assert np.array_equal(q[:, :cols], q_ref)
+    assert np.all(q[:, cols:] == 0)
+    assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_quantize_rows_packed_word_byte_order(gpu, lib):
+    # quantize_rows_int8_fused.glsl:51: byte k of word w is column 4w+k.
+    torch = gpu
+    x = np.array([[254.0, 1.0, 2.0, 3.0, -254.0, -2.0, 4.0, 0.0]], np.float32)
+    xd = dev(torch, x)
+    qd = empty(torch, (1, 64), torch.int8)
+    sd = empty(torch, (1,), torch.float32)
+    ok(lib, lib.dav2_hip_quantize_rows_i8(ptr(xd), 0, 1, 8, ptr(qd), 64, ptr(sd), stream(torch)))
+    words = host(torch, qd).view(np.uint32)[0, :2]
+    assert words.tolist() == [0x0201007F, 0x0002FF81]
+    assert host(torch, sd)[0] == np.float32(2.0)
+
+
+# ---------------------------------------------------------------------------
+# a2 im2col_quantize_int8.glsl
+@pytest.mark.parametrize("c,h,w,k,s,p", [(3, 518, 518, 14, 14, 0), (3, 266, 350, 14, 14, 0), (64, 37, 37, 3, 1, 1),
+                                         (96, 19, 19, 3, 2, 1), (32, 74, 74, 1, 1, 0), (5, 4, 4, 3, 1, 1),
+                                         (128, 60, 52, 3, 1, 1), (1024, 10, 10, 3, 2, 1)])
+def test_im2col_quantize_bit_exact(gpu, lib, oracle, c, h, w, k, s, p):
+    torch = gpu
+    _announce("im2col", c, h, w, k, s, p)
+    rng = np.random.default_rng(c + h + k)
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    q_ref, s_ref = oracle.im2col_quantize(x, k, s, p)
+    ow = (w + 2 * p - k) // s + 1
+    oh = (h + 2 * p - k) // s + 1
+    kk = c * k * k
+    ld = (kk + 63) // 64 * 64
+    xd = dev(torch, x)
+    qd = torch.full((ow * oh, ld), 0x55, dtype=torch.int8, device="cuda")
+    sd = empty(torch, (ow * oh,), torch.float32)
+    ok(lib, lib.dav2_hip_im2col_quantize_i8(ptr(xd), w, h, c, ow, oh, k, s, p, ptr(qd), ld, ptr(sd), stream(torch)))
+    q = host(torch, qd)
+    assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q[:, :kk], q_ref)
+    assert np.all(q[:, kk:] == 0)
+
+
+# ---------------------------------------------------------------------------
+# a3 int8 GEMM (linear_int8_tiled.glsl), raw int32 accumulators
+def _gemm_args(pkg, **kw):
+    a = pkg.GemmArgs()
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("m,n,k", [(1370, 1152, 384), (1370, 3072, 1024), (1369, 384, 588), (17, 33, 64),
+                                   (4096, 256, 2304), (1370, 1024, 4096), (130, 1, 32), (21904, 256, 2304)])
+def test_gemm_int32_bit_exact(gpu, pkg, lib, m, n, k):
+    torch = gpu
+    _announce("gemm raw", m, n, k)
+    rng = np.random.default_rng(m * 7 + n)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ref = (a.astype(np.int64) @ b.astype(np.int64).T)
+    ld = (k + 63) // 64 * 64
+    ad, bd = dev(torch, pad_rows(a, ld)), dev(torch, pad_rows(b, ld))
+    out = torch.full((m, n), -1, dtype=torch.int32, device="cuda")
+    args = _gemm_args(pkg, a=ptr(ad), lda=ld, b=ptr(bd), ldb=ld, m=m, n=n, k=ld, epilogue=pkg.GEMM_EPI["raw"],
+                      out_i32=ptr(out))
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(args), stream(torch)))
+    assert np.array_equal(host(torch, out).astype(np.int64), ref)
+
+
+def _random_gemm_case(rng, m, n, k):
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    sa = rng.uniform(1e-3, 5e-2, m).astype(np.float32)
+    sb = rng.uniform(1e-4, 2e-3, n).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32) * 0.1
+    return a, b, sa, sb, bias
+
+
+@pytest.mark.parametrize("m,n,k", [(1370, 384, 384), (1369, 96, 640), (300, 1024, 1024)])
+def test_gemm_row_epilogues(gpu, pkg, lib, oracle, m, n, k):
+    torch = gpu
+    _announce("gemm epilogues", m, n, k)
+    rng = np.random.default_rng(n + k)
+    a, b, sa, sb, bias = _random_gemm_case(rng, m, n, k)
+    acc = oracle.gemm_i8(a, b)
+    ld = (k + 63) // 64 * 64
+    ad, bd = dev(torch, pad_rows(a, ld)), dev(torch, pad_rows(b, ld))
+    sad, sbd, biasd = dev(torch, sa), dev(torch, sb), dev(torch, bias)
+    s = stream(torch)
+    base = dict(a=ptr(ad), lda=ld, b=ptr(bd), ldb=ld, m=m, n=n, k=ld, a_scales=ptr(sad), b_scales=ptr(sbd))
+
+    # ROW with bias and a row offset (prepare_tokens writes rows 1..T-1)
+    out = torch.zeros((m + 1, n), dtype=torch.float32, device="cuda")
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, epilogue=1, bias=ptr(biasd), out=ptr(out),
+                                                    out_row_offset=1)), s))
+    ref = oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m + 1, row_offset=1).reshape(m + 1, n)
+    got = host(torch, out)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+    # ROW without bias
+    out0 = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, epilogue=1, out=ptr(out0))), s))
+    ref0 = oracle.linear_epilogue(acc, sa, sb, None, out_rows=m).reshape(m, n)
+    assert np.array_equal(host(torch, out0).view(np.uint32), ref0.view(np.uint32))
+
+    # TRANSPOSED (channel-major, row stride m)
+    outt = torch.zeros((n, m), dtype=torch.float32, device="cuda")
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, epilogue=4, bias=ptr(biasd), out=ptr(outt),
+                                                    out_row_stride=m)), s))
+    reft = oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m, row_stride=m, transposed=True).reshape(n, m)
+    assert np.array_equal(host(torch, outt).view(np.uint32), reft.view(np.uint32))
+
+    # ROW + GELU (device erff vs libm erf: a few ulp)
+    outg = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, epilogue=2, bias=ptr(biasd), out=ptr(outg))), s))
+    refg = oracle.gelu(oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m).reshape(m, n))
+    np.testing.assert_allclose(host(torch, outg), refg, rtol=4e-7, atol=1e-8)
+
+    # ROW + LayerScale residual, in place (add_scaled.glsl arithmetic)
+    resid = rng.standard_normal((m, n)).astype(np.float32)
+    gamma = rng.uniform(-1e-3, 1e-3, n).astype(np.float32)
+    outr = dev(torch, resid)
+    gd = dev(torch, gamma)
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, epilogue=3, bias=ptr(biasd), out=ptr(outr),
+                                                    residual=ptr(outr), gamma=ptr(gd))), s))
+    refr = oracle.add_scaled(resid, oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m).reshape(m, n), gamma)
+    assert np.array_equal(host(torch, outr).view(np.uint32), refr.view(np.uint32))
+
+
+def test_gemm_rejects_bad_arguments(gpu, pkg, lib):
+    torch = gpu
+    a = torch.zeros((4, 64), dtype=torch.int8, device="cuda")
+    out = torch.zeros((4, 4), dtype=torch.int32, device="cuda")
+    bad_k = _gemm_args(pkg, a=ptr(a), lda=64, b=ptr(a), ldb=64, m=4, n=4, k=60, epilogue=0, out_i32=ptr(out))
+    assert lib.dav2_hip_gemm_i8(C.byref(bad_k), stream(torch)) != 0
+    bad_epi = _gemm_args(pkg, a=ptr(a), lda=64, b=ptr(a), ldb=64, m=4, n=4, k=64, epilogue=9, out_i32=ptr(out))
+    assert lib.dav2_hip_gemm_i8(C.byref(bad_epi), stream(torch)) != 0
+
+
+# ---------------------------------------------------------------------------
+# a10 LayerNorm (+ fused quantization)
+@pytest.mark.parametrize("rows,cols", [(1370, 384), (1370, 1024), (4, 17), (10, 768), (3, 5000)])
+def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
+    torch = gpu
+    _announce("layer_norm", rows, cols)
+    rng = np.random.default_rng(rows + cols)
+    x = (rng.standard_normal((rows, cols)) * 3 + 1).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    b = rng.standard_normal(cols).astype(np.float32) * 0.1
+    ref = oracle.layer_norm(x, w, b, 1e-6)
+    xd, wd, bd = dev(torch, x), dev(torch, w), dev(torch, b)
+    out = empty(torch, (rows, cols), torch.float32)
+    ok(lib, lib.dav2_hip_layer_norm(ptr(out), ptr(xd), ptr(wd), ptr(bd), rows, cols, 1e-6, stream(torch)))
+    assert np.array_equal(host(torch, out).view(np.uint32), ref.view(np.uint32))
+    if cols % 4 == 0:
+        ld = (cols + 63) // 64 * 64
+        qd = torch.full((rows, ld), 0x33, dtype=torch.int8, device="cuda")
+        sd = empty(torch, (rows,), torch.float32)
+        out2 = empty(torch, (rows, cols), torch.float32)
+        ok(lib, lib.dav2_hip_layer_norm_quantize_i8(ptr(qd), ld, ptr(sd), ptr(out2), ptr(xd), ptr(wd), ptr(bd), rows,
+                                                     cols, 1e-6, stream(torch)))
+        q_ref, s_ref = oracle.quantize_rows(ref)
+        q = host(torch, qd)
+        assert np.array_equal(q[:, :cols], q_ref) and np.all(q[:, cols:] == 0)
+        assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
+        assert np.array_equal(host(torch, out2).view(np.uint32), ref.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# a11 attention: scores -> softmax -> values
+def _attention_gpu(torch, lib, qkv, tokens, heads, fp16):
+    qd = dev(torch, qkv)
+    ldt = (tokens + 7) // 8 * 8 if fp16 else tokens
+    scores = torch.empty((heads, tokens, ldt), dtype=torch.float16 if fp16 else torch.float32, device="cuda")
+    out = empty(torch, (tokens, heads * 64), torch.float32)
+    s = stream(torch)
+    ok(lib, lib.dav2_hip_attention_scores(ptr(scores), ptr(qd), tokens, heads, 1, int(fp16), s))
+    ok(lib, lib.dav2_hip_softmax_rows(ptr(scores), heads * tokens, tokens, ldt, int(fp16), s))
+    ok(lib, lib.dav2_hip_attention_values(ptr(out), ptr(scores), ptr(qd), tokens, heads, 1, int(fp16), s))
+    return host(torch, out), host(torch, scores)[:, :, :tokens].astype(np.float32)
+
+
+@pytest.mark.parametrize("tokens,heads", [(5, 2), (65, 3), (1370, 6), (1370, 16)])
+def test_attention_fp32(gpu, lib, oracle, tokens, heads):
+    torch = gpu
+    _announce("attention fp32", tokens, heads)
+    rng = np.random.default_rng(tokens + heads)
+    qkv = rng.standard_normal((tokens, 3 * heads * 64)).astype(np.float32)
+    ref, p_ref = oracle.attention(qkv, tokens, heads, fp16=False, probabilities=True)
+    out, p = _attention_gpu(torch, lib, qkv, tokens, heads, False)
+    np.testing.assert_allclose(p, p_ref, rtol=2e-5, atol=2e-7)
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=2e-6)
+
+
+def test_attention_reference_kat(gpu, lib):
+    # tests/vulkan_smoke.cpp:540-628: 5 tokens x 2 heads, qkv[i] = (i%29-14)/128;
+    # fp32 within 2e-6 of the closed form, fp16 within 3e-4 of fp32.
+    torch = gpu
+    tokens, heads = 5, 2
+    d = heads * 64
+    qkv = ((np.arange(tokens * 3 * d) % 29 - 14) * 0.0078125).astype(np.float32).reshape(tokens, 3 * d)
+    q = qkv[:, :d].reshape(tokens, heads, 64).astype(np.float64)
+    k = qkv[:, d:2 * d].reshape(tokens, heads, 64).astype(np.float64)
+    v = qkv[:, 2 * d:].reshape(tokens, heads, 64).astype(np.float64)
+    sc = np.einsum("ihf,jhf->hij", q * 0.125, k)
+    p = np.exp(sc - sc.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    expect = np.einsum("hij,jhf->ihf", p, v).reshape(tokens, d)
+    out32, _ = _attention_gpu(torch, lib, qkv, tokens, heads, False)
+    assert np.abs(out32 - expect).max() <= 2e-6
+    out16, _ = _attention_gpu(torch, lib, qkv, tokens, heads, True)
+    assert np.abs(out16 - out32).max() <= 3e-4
+
+
+@pytest.mark.parametrize("tokens,heads", [(5, 2), (77, 4), (1370, 6), (1370, 16)])
+def test_attention_fp16(gpu, lib, oracle, tokens, heads):
+    torch = gpu
+    _announce("attention fp16", tokens, heads)
+    rng = np.random.default_rng(tokens * 3 + heads)
+    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * 0.5).astype(np.float32)
+    ref16, p16 = oracle.attention(qkv, tokens, heads, fp16=True, probabilities=True)
+    ref32 = oracle.attention(qkv, tokens, heads, fp16=False)
+    out, p = _attention_gpu(torch, lib, qkv, tokens, heads, True)
+    # binary16 scores/probabilities: one fp16 ulp of the largest probability
+    np.testing.assert_allclose(p, p16, rtol=0, atol=2e-3 * max(1.0, float(p16.max())))
+    assert np.abs(out - ref16).max() <= 2e-3
+    assert np.abs(out - ref32).max() <= 3e-3
+
+
+@pytest.mark.parametrize("rows,cols", [(16 * 1370, 1370), (7, 5477), (3, 64), (5, 9000)])
+def test_softmax_fp32(gpu, lib, oracle, rows, cols):
+    torch = gpu
+    _announce("softmax", rows, cols)
+    rng = np.random.default_rng(rows)
+    x = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
+    ref = oracle.softmax_rows(x)
+    xd = dev(torch, x)
+    ok(lib, lib.dav2_hip_softmax_rows(ptr(xd), rows, cols, cols, 0, stream(torch)))
+    np.testing.assert_allclose(host(torch, xd), ref, rtol=5e-6, atol=1e-9)
+
+
+# ---------------------------------------------------------------------------
+# a12-a16 elementwise, resize, min/max, position
+def test_elementwise_exact(gpu, lib, oracle):
+    torch = gpu
+    rng = np.random.default_rng(1)
+    n = 1370 * 1024 + 3
+    a = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    ad, bd = dev(torch, a), dev(torch, b)
+    out = empty(torch, (n,), torch.float32)
+    s = stream(torch)
+    ok(lib, lib.dav2_hip_add(ptr(out), ptr(ad), ptr(bd), n, s))
+    assert np.array_equal(host(torch, out), oracle.add(a, b))
+    ok(lib, lib.dav2_hip_relu(ptr(out), ptr(ad), n, s))
+    assert np.array_equal(host(torch, out), oracle.relu(a))
+    cols = 1024
+    m = (n // cols) * cols
+    gamma = rng.uniform(-1e-3, 1e-3, cols).astype(np.float32)
+    gd = dev(torch, gamma)
+    ok(lib, lib.dav2_hip_add_scaled(ptr(out), ptr(ad), ptr(bd), ptr(gd), m, cols, s))
+    assert np.array_equal(host(torch, out)[:m], oracle.add_scaled(a[:m], b[:m], gamma))
+    ok(lib, lib.dav2_hip_gelu(ptr(out), ptr(ad), n, s))
+    np.testing.assert_allclose(host(torch, out), oracle.gelu(a), rtol=4e-7, atol=1e-8)
+
+
+@pytest.mark.parametrize("c,ih,iw,oh,ow", [(256, 19, 19, 37, 37), (256, 148, 148, 296, 296), (128, 296, 296, 518, 518),
+                                           (3, 5, 7, 1, 1), (2, 1, 1, 4, 3), (64, 25, 19, 50, 38)])
+def test_bilinear_bit_exact(gpu, lib, oracle, c, ih, iw, oh, ow):
+    torch = gpu
+    _announce("bilinear", c, ih, iw, oh, ow)
+    rng = np.random.default_rng(c + oh)
+    x = rng.standard_normal((c, ih, iw)).astype(np.float32)
+    ref = oracle.bilinear(x, ow, oh)
+    xd = dev(torch, x)
+    out = empty(torch, (c, oh, ow), torch.float32)
+    ok(lib, lib.dav2_hip_bilinear_align_true(ptr(out), ptr(xd), iw, ih, ow, oh, c, stream(torch)))
+    assert np.array_equal(host(torch, out).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [4, 1000, 518 * 518, 1036 * 1036 + 5])
+def test_minmax_normalize(gpu, lib, oracle, n):
+    torch = gpu
+    rng = np.random.default_rng(n)
+    d = (rng.standard_normal(n) * 3 + 7).astype(np.float32)
+    if n == 4:
+        d = np.array([2.0, 3.0, 5.0, 10.0], np.float32)  # tests/vulkan_smoke.cpp:121-142
+    dd = dev(torch, d)
+    rng_d = empty(torch, (2,), torch.float32)
+    part = empty(torch, (2 * lib.dav2_hip_minmax_partials(n),), torch.float32)
+    s = stream(torch)
+    ok(lib, lib.dav2_hip_reduce_minmax(ptr(dd), n, ptr(rng_d), ptr(part), s))
+    r = host(torch, rng_d)
+    assert np.array_equal(r, oracle.reduce_minmax(d))
+    ok(lib, lib.dav2_hip_normalize_relative(ptr(dd), ptr(rng_d), n, s))
+    got = host(torch, dd)
+    assert np.array_equal(got.view(np.uint32), oracle.normalize_relative(d, r).view(np.uint32))
+    if n == 4:
+        np.testing.assert_allclose(got, [0.0, 0.125, 0.375, 1.0], atol=1e-6)
+
+
+@pytest.mark.parametrize("pw,ph,dim", [(37, 37, 384), (74, 74, 64), (25, 19, 96), (3, 2, 3)])
+def test_position_bicubic_and_tokens(gpu, lib, oracle, pw, ph, dim):
+    torch = gpu
+    rng = np.random.default_rng(pw * ph)
+    pos = (rng.standard_normal((1370, dim)) * 0.02).astype(np.float32)
+    ref = oracle.position_bicubic(pos, pw, ph, dim)
+    pd = dev(torch, pos)
+    out = empty(torch, (dim, ph, pw), torch.float32)
+    s = stream(torch)
+    ok(lib, lib.dav2_hip_position_bicubic(ptr(out), ptr(pd), pw, ph, dim, s))
+    interp = host(torch, out)
+    assert np.array_equal(interp.view(np.uint32), ref.view(np.uint32))
+    if pw == 37 and ph == 37:
+        assert np.array_equal(interp, pos[1:].T.reshape(dim, 37, 37))  # exact copy (operators.cpp:1351-1357)
+    # class token + position add for a batch of two token matrices
+    t = pw * ph + 1
+    tokens = rng.standard_normal((2, t, dim)).astype(np.float32)
+    cls = rng.standard_normal(dim).astype(np.float32)
+    td, cd = dev(torch, tokens), dev(torch, cls)
+    ok(lib, lib.dav2_hip_finish_tokens(ptr(td), ptr(out), ptr(pd), ptr(cd), pw, ph, dim, 2, s))
+    got = host(torch, td)
+    exp = tokens.copy()
+    exp[:, 0] = cls + pos[0]
+    exp[:, 1:] = tokens[:, 1:] + interp.reshape(dim, -1).T[None]
+    assert np.array_equal(got, exp)
