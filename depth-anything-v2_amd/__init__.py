@@ -130,7 +130,8 @@ PROTOTYPES = {
     "dav2_profile_report": (C.c_int, [vp, C.c_char_p, sz]),
     # HIP launcher layer
     "dav2_hip_quantize_rows_i8": (C.c_int, [vp, u64, u32, u32, vp, u32, vp, vp]),
-    "dav2_hip_im2col_quantize_i8": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, vp, u32, vp, vp]),
+    "dav2_hip_im2col_scratch_floats": (u64, [u32, u32, u32]),
+    "dav2_hip_im2col_quantize_i8": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, vp, u32, vp, vp, u64, vp]),
     "dav2_hip_layer_norm": (C.c_int, [vp, vp, vp, vp, u32, u32, f32, vp]),
     "dav2_hip_layer_norm_quantize_i8": (C.c_int, [vp, u32, vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "dav2_hip_gemm_i8": (C.c_int, [C.POINTER(GemmArgs), vp]),
@@ -141,6 +142,7 @@ PROTOTYPES = {
     "dav2_hip_attention_scores": (C.c_int, [vp, vp, u32, u32, u32, C.c_int, vp]),
     "dav2_hip_softmax_rows": (C.c_int, [vp, u64, u32, u32, C.c_int, vp]),
     "dav2_hip_attention_values": (C.c_int, [vp, vp, vp, u32, u32, u32, C.c_int, vp]),
+    "dav2_hip_attention_scratch_bytes": (u64, [u32, u32, u32, C.c_int]),
     "dav2_hip_bilinear_align_true": (C.c_int, [vp, vp, u32, u32, u32, u32, u32, vp]),
     "dav2_hip_minmax_partials": (u32, [u64]),
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),

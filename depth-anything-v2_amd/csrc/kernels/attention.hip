@@ -119,20 +119,41 @@ __global__ __launch_bounds__(256) void attention_scores_kernel(
     }
 
     const uint64_t plane = static_cast<uint64_t>(bh) * tokens;
+    if (HALF) {
+        // Stage the 64x64 binary16 tile in LDS (reusing the Q tile, same
+        // shape) and write it as 16-byte row segments. Columns in [T, ldt)
+        // come from zero key rows; the softmax overwrites them with zeros.
+        __syncthreads();
+        _Float16* st = reinterpret_cast<_Float16*>(qt);
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
+        for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const uint32_t j = j0 + wc + c * 16 + fr;
-            if (j >= tokens) continue;
+            for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t i = i0 + wr + a * 16 + 4 * g + r;
-                if (i >= tokens) continue;
-                if (HALF)
-                    static_cast<_Float16*>(scores_out)[(plane + i) * ldt + j] = static_cast<_Float16>(acc[a][c][r]);
-                else
-                    static_cast<float*>(scores_out)[(plane + i) * tokens + j] = acc[a][c][r];
+                for (int r = 0; r < 4; ++r)
+                    st[(wr + a * 16 + 4 * g + r) * S + wc + c * 16 + fr] = static_cast<_Float16>(acc[a][c][r]);
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int idx = tid + it * 256;  // 64 rows x 8 chunks of 8 halves
+            const int row = idx >> 3, chunk = idx & 7;
+            const uint32_t i = i0 + row, j = j0 + chunk * 8;
+            if (i < tokens && j < ldt)
+                *reinterpret_cast<v8h*>(static_cast<_Float16*>(scores_out) + (plane + i) * ldt + j) =
+                    *reinterpret_cast<const v8h*>(st + row * S + chunk * 8);
+        }
+    } else {
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint32_t j = j0 + wc + c * 16 + fr;
+                if (j >= tokens) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t i = i0 + wr + a * 16 + 4 * g + r;
+                    if (i < tokens) static_cast<float*>(scores_out)[(plane + i) * tokens + j] = acc[a][c][r];
+                }
             }
         }
     }
@@ -314,9 +335,188 @@ __global__ __launch_bounds__(256) void attention_values_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// binary16 path, tuned kernels.
+//
+// V is first packed to binary16, feature-major: vt[bh][f][j], j padded with
+// zeros to ldv = T rounded up to 32, so a PV operand fragment (8 consecutive
+// tokens of one feature) is one 16-byte load.
+inline uint32_t value_ld(uint32_t tokens) { return (tokens + 31u) & ~31u; }
+
+__global__ __launch_bounds__(256) void pack_values_half_kernel(const float* __restrict__ qkv,
+                                                               _Float16* __restrict__ vt, uint32_t tokens,
+                                                               uint32_t heads, uint32_t ldv) {
+    __shared__ float tile[64][65];
+    const uint32_t bh = blockIdx.z;
+    const uint32_t b = bh / heads, h = bh - b * heads;
+    const uint32_t D = heads * 64u;
+    const uint32_t j0 = blockIdx.x * 64u;
+    const int tid = threadIdx.x;
+    const float* vbase = qkv + static_cast<uint64_t>(b) * tokens * 3u * D + 2u * D + h * 64u;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {  // 64 tokens x 16 float4
+        const int c = tid + it * 256;
+        const int jr = c >> 4, f4 = (c & 15) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j0 + jr < tokens) v = *reinterpret_cast<const float4*>(vbase + static_cast<uint64_t>(j0 + jr) * 3u * D + f4);
+        tile[jr][f4 + 0] = v.x;
+        tile[jr][f4 + 1] = v.y;
+        tile[jr][f4 + 2] = v.z;
+        tile[jr][f4 + 3] = v.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {  // 64 features x 8 chunks of 8 tokens
+        const int c = tid + it * 256;
+        const int f = c >> 3, jc = (c & 7) * 8;
+        if (j0 + jc >= ldv) continue;
+        v8h out;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) out[k] = static_cast<_Float16>(tile[jc + k][f]);
+        *reinterpret_cast<v8h*>(vt + (static_cast<uint64_t>(bh) * 64u + f) * ldv + j0 + jc) = out;
+    }
+}
+
+// out = P v for 64 query rows of one (batch, head): the four waves split the
+// key axis (wave w takes every fourth 32-token step), each accumulating a
+// 64x64 partial on 4x4 MFMA blocks with operands loaded straight from global
+// memory (P rows: 16 bytes per lane; vt: 16 bytes per lane). The partials are
+// summed through LDS.
+__global__ __launch_bounds__(256) void attention_values_half_kernel(const _Float16* __restrict__ p,
+                                                                    const _Float16* __restrict__ vt,
+                                                                    float* __restrict__ out, uint32_t tokens,
+                                                                    uint32_t heads, uint32_t ldt, uint32_t ldv) {
+    extern __shared__ float red[];  // [waves 1..3][64 rows][64 features]
+    const uint32_t bh = blockIdx.z;
+    const uint32_t b = bh / heads, h = bh - b * heads;
+    const uint32_t D = heads * 64u;
+    const uint32_t i0 = blockIdx.x * 64u;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int fr = lane & 15, g = lane >> 4;
+    const _Float16* prow = p + static_cast<uint64_t>(bh) * tokens * ldt;
+    const _Float16* vrow = vt + static_cast<uint64_t>(bh) * 64u * ldv;
+    v4f acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
+    const uint32_t steps = (tokens + 31u) / 32u;
+    for (uint32_t st = wave; st < steps; st += 4) {
+        const uint32_t j = st * 32u + g * 8u;
+        v8h af[4], bf[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const uint32_t i = i0 + a * 16 + fr;
+            v8h v = {};
+            if (i < tokens && j < ldt) v = *reinterpret_cast<const v8h*>(prow + static_cast<uint64_t>(i) * ldt + j);
+            af[a] = v;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bf[c] = *reinterpret_cast<const v8h*>(vrow + static_cast<uint64_t>(c * 16 + fr) * ldv + j);
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[c], acc[a][c], 0, 0, 0);
+    }
+    // 16x16 result layout: lane holds rows 4*g + r of column fr. Waves 1-3
+    // park their partials in LDS; wave 0 adds them to its own and stores.
+    if (wave > 0) {
+        float* mine = red + (wave - 1) * 4096;
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mine[(a * 16 + 4 * g + r) * 64 + c * 16 + fr] = acc[a][c][r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = a * 16 + 4 * g + r;
+                const uint32_t i = i0 + row;
+                if (i >= tokens) continue;
+                float* o = out + (static_cast<uint64_t>(b) * tokens + i) * D + h * 64u;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int idx = row * 64 + c * 16 + fr;
+                    o[c * 16 + fr] = ((acc[a][c][r] + red[idx]) + red[4096 + idx]) + red[8192 + idx];
+                }
+            }
+    }
+}
+
+// binary16 softmax, one wave per row, 16-byte loads: lane l owns the 8-column
+// chunks l, l+64, ... (CPL chunks per lane). Same arithmetic as softmax_kernel.
+template <int CPL>
+__global__ __launch_bounds__(256) void softmax_half_kernel(_Float16* data, uint64_t rows, uint32_t columns,
+                                                           uint32_t row_stride) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 4u + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    _Float16* hr = data + row * row_stride;
+    const uint32_t chunks = row_stride / 8u;
+    float v[CPL][8];
+    float maximum = -3.402823466e+38f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        const uint32_t c = lane + 64u * k;
+        v8h raw = {};
+        if (c < chunks) raw = *reinterpret_cast<const v8h*>(hr + 8u * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const bool ok = c < chunks && 8u * c + e < columns;
+            v[k][e] = ok ? static_cast<float>(raw[e]) : -3.402823466e+38f;
+            maximum = fmaxf(maximum, v[k][e]);
+        }
+    }
+    maximum = wave_max(maximum);
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        const uint32_t c = lane + 64u * k;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const bool ok = c < chunks && 8u * c + e < columns;
+            const float ex = ok ? expf(v[k][e] - maximum) : 0.0f;
+            sum = sum + ex;
+            v[k][e] = static_cast<float>(static_cast<_Float16>(ex));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum = sum + __shfl_xor(sum, o, kWave);
+    const float inverse = 1.0f / fmaxf(sum, 1.0e-20f);
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        const uint32_t c = lane + 64u * k;
+        if (c >= chunks) continue;
+        v8h o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = static_cast<_Float16>(v[k][e] * inverse);  // padding: 0 * inverse
+        *reinterpret_cast<v8h*>(hr + 8u * c) = o;
+    }
+}
+
 template <bool HALF>
 void launch_softmax(void* data, uint64_t rows, uint32_t columns, uint32_t stride, hipStream_t s) {
     const unsigned grid = ceil_div(rows, 4);
+    if (HALF && stride % 8u == 0) {
+        const uint32_t cpl = (stride / 8u + 63u) / 64u;
+        _Float16* d = static_cast<_Float16*>(data);
+#define DAV2_SMH_CASE(N) \
+    hipLaunchKernelGGL((softmax_half_kernel<N>), dim3(grid), dim3(256), 0, s, d, rows, columns, stride)
+        if (cpl <= 1) { DAV2_SMH_CASE(1); return; }
+        if (cpl <= 2) { DAV2_SMH_CASE(2); return; }
+        if (cpl <= 3) { DAV2_SMH_CASE(3); return; }
+        if (cpl <= 4) { DAV2_SMH_CASE(4); return; }
+        if (cpl <= 6) { DAV2_SMH_CASE(6); return; }
+        if (cpl <= 8) { DAV2_SMH_CASE(8); return; }
+        if (cpl <= 12) { DAV2_SMH_CASE(12); return; }
+#undef DAV2_SMH_CASE
+    }
     const uint32_t ch = (columns + 63u) / 64u;
 #define DAV2_SM_CASE(N) \
     hipLaunchKernelGGL((softmax_kernel<N, HALF>), dim3(grid), dim3(256), 0, s, data, rows, columns, stride)
@@ -368,14 +568,30 @@ int dav2_hip_attention_values(float* out, const void* probabilities, const float
     if (!out || !probabilities || !qkv || (reinterpret_cast<uintptr_t>(qkv) & 15) || heads > 65535u / batch)
         return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(ceil_div(tokens, 128), 1, heads * batch);
-    if (fp16)
-        hipLaunchKernelGGL(attention_values_kernel<true>, grid, dim3(256), 0, s, probabilities, qkv, out, tokens,
-                           heads, half_ld(tokens));
-    else
+    if (fp16) {
+        // The packed binary16 copy of v lives right after the scores.
+        const uint32_t ldt = half_ld(tokens), ldv = value_ld(tokens);
+        const uint64_t score_bytes = static_cast<uint64_t>(batch) * heads * tokens * ldt * 2u;
+        _Float16* vt = reinterpret_cast<_Float16*>(const_cast<char*>(static_cast<const char*>(probabilities)) +
+                                                   ((score_bytes + 255u) & ~255ull));
+        hipLaunchKernelGGL(pack_values_half_kernel, dim3(ceil_div(ldv, 64), 1, heads * batch), dim3(256), 0, s, qkv,
+                           vt, tokens, heads, ldv);
+        hipLaunchKernelGGL(attention_values_half_kernel, dim3(ceil_div(tokens, 64), 1, heads * batch), dim3(256),
+                           3 * 64 * 64 * sizeof(float), s, static_cast<const _Float16*>(probabilities), vt, out,
+                           tokens, heads, ldt, ldv);
+    } else {
+        const dim3 grid(ceil_div(tokens, 128), 1, heads * batch);
         hipLaunchKernelGGL(attention_values_kernel<false>, grid, dim3(256), 0, s, probabilities, qkv, out, tokens,
                            heads, tokens);
+    }
     return hipGetLastError();
+}
+
+uint64_t dav2_hip_attention_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch, int fp16) {
+    const uint64_t bh = static_cast<uint64_t>(batch) * heads;
+    if (!fp16) return bh * tokens * tokens * sizeof(float);
+    const uint64_t score_bytes = bh * tokens * half_ld(tokens) * 2u;
+    return ((score_bytes + 255u) & ~255ull) + bh * 64u * value_ld(tokens) * 2u;
 }
 
 }  // extern "C"

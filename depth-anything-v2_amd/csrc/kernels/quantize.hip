@@ -6,6 +6,8 @@
 // steps. The first K bytes of each row are exactly the reference's packed
 // 4x int8 words (little-endian byte c%4 of word c/4 = column c).
 
+#include <algorithm>
+
 #include "common.h"
 #include "dav2_hip.h"
 
@@ -161,6 +163,171 @@ __global__ __launch_bounds__(256) void im2col_quantize_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Fast paths of a2 for the DPT shapes (same bytes as the generic kernels).
+//
+// 3x3, stride 1, pad 1 (C % 16 == 0): a workgroup owns 64 consecutive output
+// pixels of one row and a range of 16-channel chunks. Pass 1 folds the
+// per-channel-group |x| maxima (channel_group_absmax_kernel) of the 3 x 66
+// input window; the 3x3 window maximum of that map is the im2col row's absmax
+// (zero padding never raises it, and max is order-free, so the scale is
+// bit-identical to the generic kernel's). Pass 2 stages each chunk's 16 x 3 x 66
+// window in LDS and writes the chunk's 144 bytes of every row with consecutive
+// lanes on consecutive words, i.e. one 144-byte segment per output row.
+constexpr int kTile = 64;     // output pixels per workgroup
+constexpr int kChunk = 16;    // input channels per chunk (16 * 9 = 144 bytes)
+constexpr int kHalo = kTile + 2;
+
+// Per-pixel maxima of |x| over channel groups of kGroupChannels:
+// partial[g][p] = max over c in group g of |x[c][p]|.
+constexpr uint32_t kGroupChannels = 32;
+
+__global__ __launch_bounds__(256) void channel_group_absmax_kernel(const float* __restrict__ x, uint32_t C,
+                                                                   uint64_t plane, float* __restrict__ partial) {
+    const uint64_t p = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    if (p >= plane) return;
+    const uint32_t c0 = blockIdx.y * kGroupChannels;
+    const uint32_t c1 = min(C, c0 + kGroupChannels);
+    const float* src = x + c0 * plane + p;
+    float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
+    uint32_t c = c0;
+    for (; c + 4 <= c1; c += 4, src += 4 * plane) {
+        m0 = fmaxf(m0, fabsf(src[0]));
+        m1 = fmaxf(m1, fabsf(src[plane]));
+        m2 = fmaxf(m2, fabsf(src[2 * plane]));
+        m3 = fmaxf(m3, fabsf(src[3 * plane]));
+    }
+    for (; c < c1; ++c, src += plane) m0 = fmaxf(m0, fabsf(src[0]));
+    partial[blockIdx.y * plane + p] = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+}
+
+__global__ __launch_bounds__(256) void im2col3x3_kernel(const float* __restrict__ x, const float* __restrict__ partial,
+                                                        uint32_t groups, uint32_t C, uint32_t H, uint32_t W,
+                                                        uint32_t chunks_per_block, int8_t* __restrict__ q,
+                                                        uint32_t ldq, float* __restrict__ scales) {
+    __shared__ float amax[3 * kHalo];
+    __shared__ float inv[kTile];
+    __shared__ float tile[kChunk * 3 * kHalo];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t x0 = blockIdx.x * kTile, y = blockIdx.y;
+    const uint64_t plane = static_cast<uint64_t>(H) * W;
+
+    // Pass 1: channel absmax of rows y-1..y+1, columns x0-1..x0+64, folded
+    // from the per-channel-group maxima of channel_group_absmax_kernel.
+    if (tid < 3 * kHalo) {
+        const int r = static_cast<int>(tid) / kHalo, col = static_cast<int>(tid) % kHalo;
+        const int gy = static_cast<int>(y) + r - 1, gx = static_cast<int>(x0) + col - 1;
+        float m = 0.0f;
+        if (gy >= 0 && gy < static_cast<int>(H) && gx >= 0 && gx < static_cast<int>(W)) {
+            const float* src = partial + static_cast<uint64_t>(gy) * W + gx;
+            for (uint32_t g = 0; g < groups; ++g) m = fmaxf(m, src[g * plane]);
+        }
+        amax[tid] = m;
+    }
+    __syncthreads();
+    if (tid < kTile) {
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+#pragma unroll
+            for (int dx = 0; dx < 3; ++dx) m = fmaxf(m, amax[r * kHalo + tid + dx]);
+        const float s = row_scale(m);
+        inv[tid] = 1.0f / s;
+        if (blockIdx.z == 0 && x0 + tid < W) scales[static_cast<uint64_t>(y) * W + x0 + tid] = s;
+    }
+
+    const uint32_t chunks = C / kChunk;
+    const uint32_t first = blockIdx.z * chunks_per_block;
+    const uint32_t last = min(chunks, first + chunks_per_block);
+    const uint32_t valid = min(static_cast<uint32_t>(kTile), W - x0);
+    uint8_t* row_base = reinterpret_cast<uint8_t*>(q) + (static_cast<uint64_t>(y) * W + x0) * ldq;
+    for (uint32_t chunk = first; chunk < last; ++chunk) {
+        __syncthreads();  // previous chunk's readers are done with `tile`
+        const uint32_t c0 = chunk * kChunk;
+        for (uint32_t idx = tid; idx < kChunk * 3 * kHalo; idx += 256) {
+            const uint32_t ch = idx / (3 * kHalo), rem = idx - ch * (3 * kHalo);
+            const int r = static_cast<int>(rem) / kHalo, col = static_cast<int>(rem) % kHalo;
+            const int gy = static_cast<int>(y) + r - 1, gx = static_cast<int>(x0) + col - 1;
+            float v = 0.0f;
+            if (gy >= 0 && gy < static_cast<int>(H) && gx >= 0 && gx < static_cast<int>(W))
+                v = x[(c0 + ch) * plane + static_cast<uint64_t>(gy) * W + gx];
+            tile[idx] = v;
+        }
+        __syncthreads();
+        // 36 words (144 bytes) per pixel; word w of pixel p covers chunk
+        // columns 4w..4w+3, column j -> channel j/9, tap j%9 = 3*ky + kx.
+        for (uint32_t idx = tid; idx < valid * 36u; idx += 256) {
+            const uint32_t p = idx / 36u, w = idx - p * 36u;
+            const float sc = inv[p];
+            int b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t j = 4u * w + i;
+                const uint32_t ch = j / 9u, t = j - ch * 9u;
+                const uint32_t ky = t / 3u, kx = t - ky * 3u;
+                b[i] = quantize_rne(tile[ch * (3 * kHalo) + ky * kHalo + p + kx] * sc);
+            }
+            *reinterpret_cast<uint32_t*>(row_base + static_cast<uint64_t>(p) * ldq + c0 * 9u + 4u * w) =
+                pack4(b[0], b[1], b[2], b[3]);
+        }
+    }
+    // Zero the row padding [9C, ldq) once.
+    if (blockIdx.z == 0) {
+        const uint32_t pad_words = (ldq - 9u * C) / 4u;
+        for (uint32_t idx = tid; idx < valid * pad_words; idx += 256) {
+            const uint32_t p = idx / pad_words, w = idx - p * pad_words;
+            *reinterpret_cast<uint32_t*>(row_base + static_cast<uint64_t>(p) * ldq + 9u * C + 4u * w) = 0u;
+        }
+    }
+}
+
+// 1x1 (rows = pixels, K = C): a workgroup owns 64 consecutive pixels of the
+// flattened map and a range of 64-channel chunks; chunks are staged as
+// [64 channels][64 pixels] (coalesced along pixels) and written back as one
+// 64-byte segment per output row. Columns beyond C (the row padding) are zero.
+constexpr int kChunk1 = 64;
+
+__global__ __launch_bounds__(256) void im2col1x1_kernel(const float* __restrict__ x, const float* __restrict__ partial,
+                                                        uint32_t groups, uint32_t C, uint64_t plane,
+                                                        uint32_t chunks_per_block, int8_t* __restrict__ q,
+                                                        uint32_t ldq, float* __restrict__ scales) {
+    __shared__ float inv[kTile];
+    __shared__ float tile[kChunk1 * (kTile + 1)];
+    const uint32_t tid = threadIdx.x;
+    const uint64_t p0 = static_cast<uint64_t>(blockIdx.x) * kTile;
+    const uint32_t valid = static_cast<uint32_t>(min<uint64_t>(kTile, plane - p0));
+    if (tid < kTile) {
+        float m = 0.0f;
+        if (tid < valid)
+            for (uint32_t g = 0; g < groups; ++g) m = fmaxf(m, partial[g * plane + p0 + tid]);
+        const float s = row_scale(m);
+        inv[tid] = 1.0f / s;
+        if (blockIdx.y == 0 && tid < valid) scales[p0 + tid] = s;
+    }
+    const uint32_t chunks = ldq / kChunk1;  // covers the padding as well
+    const uint32_t first = blockIdx.y * chunks_per_block;
+    const uint32_t last = min(chunks, first + chunks_per_block);
+    uint8_t* row_base = reinterpret_cast<uint8_t*>(q) + p0 * ldq;
+    for (uint32_t chunk = first; chunk < last; ++chunk) {
+        __syncthreads();
+        const uint32_t c0 = chunk * kChunk1;
+        for (uint32_t idx = tid; idx < kChunk1 * kTile; idx += 256) {
+            const uint32_t ch = idx / kTile, p = idx - ch * kTile;
+            tile[ch * (kTile + 1) + p] = (c0 + ch < C && p < valid) ? x[(c0 + ch) * plane + p0 + p] : 0.0f;
+        }
+        __syncthreads();
+        for (uint32_t idx = tid; idx < valid * 16u; idx += 256) {
+            const uint32_t p = idx / 16u, w = idx - p * 16u;
+            const float sc = inv[p];
+            int b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b[i] = quantize_rne(tile[(4u * w + i) * (kTile + 1) + p] * sc);
+            *reinterpret_cast<uint32_t*>(row_base + static_cast<uint64_t>(p) * ldq + c0 + 4u * w) =
+                pack4(b[0], b[1], b[2], b[3]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // a10: layer_norm.glsl:27-68. One wave per row; lane l accumulates columns
 // l, l+64, ... in order and the wave reduction reproduces the 64-entry LDS
 // tree, so sums, mean and variance match the reference order exactly.
@@ -297,11 +464,15 @@ int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset, uint32_
     return hipGetLastError();
 }
 
+uint64_t dav2_hip_im2col_scratch_floats(uint32_t input_width, uint32_t input_height, uint32_t input_channels) {
+    return static_cast<uint64_t>(input_width) * input_height * ((input_channels + kGroupChannels - 1) / kGroupChannels);
+}
+
 int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32_t input_height,
                                 uint32_t input_channels, uint32_t output_width,
                                 uint32_t output_height, uint32_t kernel, uint32_t stride,
                                 int32_t padding, int8_t* q, uint32_t ldq, float* scales,
-                                void* stream) {
+                                float* scratch, uint64_t scratch_floats, void* stream) {
     const uint64_t rows64 = static_cast<uint64_t>(output_width) * output_height;
     const uint64_t cols64 = static_cast<uint64_t>(input_channels) * kernel * kernel;
     if (rows64 == 0) return hipSuccess;
@@ -327,6 +498,35 @@ int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32
     g.div_k = make_div(kernel);
     g.plane = static_cast<uint64_t>(input_width) * input_height;
     const uint32_t rows = static_cast<uint32_t>(rows64);
+    const uint64_t plane = static_cast<uint64_t>(input_width) * input_height;
+    const uint32_t groups = (input_channels + kGroupChannels - 1) / kGroupChannels;
+    const bool fast3 = kernel == 3 && stride == 1 && padding == 1 && input_channels % kChunk == 0 &&
+                       output_width == input_width && output_height == input_height;
+    const bool fast1 = kernel == 1 && stride == 1 && padding == 0 && output_width == input_width &&
+                       output_height == input_height;
+    if ((fast3 || fast1) && scratch && scratch_floats >= plane * groups && input_height <= 65535u) {
+        hipLaunchKernelGGL(channel_group_absmax_kernel, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s, input,
+                           input_channels, plane, scratch);
+        // Enough workgroups to fill the chip: split the channel chunks of
+        // small maps over blockIdx.z (each split recomputes the 64 scales).
+        if (fast3) {
+            const unsigned tiles = ceil_div(input_width, kTile) * input_height;
+            const uint32_t chunks = input_channels / kChunk;
+            const uint32_t splits = std::max(1u, std::min(chunks, static_cast<uint32_t>(2048u / tiles)));
+            const uint32_t per = (chunks + splits - 1) / splits;
+            hipLaunchKernelGGL(im2col3x3_kernel, dim3(ceil_div(input_width, kTile), input_height, ceil_div(chunks, per)),
+                               dim3(256), 0, s, input, scratch, groups, input_channels, input_height, input_width, per,
+                               q, ldq, scales);
+        } else {
+            const unsigned tiles = ceil_div(plane, kTile);
+            const uint32_t chunks = ldq / kChunk1;
+            const uint32_t splits = std::max(1u, std::min(chunks, static_cast<uint32_t>(2048u / tiles)));
+            const uint32_t per = (chunks + splits - 1) / splits;
+            hipLaunchKernelGGL(im2col1x1_kernel, dim3(tiles, ceil_div(chunks, per)), dim3(256), 0, s, input, scratch,
+                               groups, input_channels, plane, per, q, ldq, scales);
+        }
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(im2col_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
                        s, g, rows, scales);
     const uint32_t ldq_words = ldq / 4u;

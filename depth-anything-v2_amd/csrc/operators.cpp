@@ -184,9 +184,7 @@ void HipOperators::add_scaled(DeviceBuffer& output, const DeviceBuffer& residual
 
 std::uint64_t HipOperators::attention_score_bytes(std::uint32_t tokens, std::uint32_t heads, std::uint32_t batch,
                                                   Precision precision) {
-    const std::uint64_t rows = std::uint64_t(batch) * heads * tokens;
-    if (precision == Precision::fp16) return rows * ((std::uint64_t(tokens) + 7) & ~7ull) * 2u;
-    return rows * tokens * sizeof(float);
+    return dav2_hip_attention_scratch_bytes(tokens, heads, batch, precision == Precision::fp16 ? 1 : 0);
 }
 
 // src/operators.cpp:1098-1209
@@ -263,7 +261,7 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
                             12.0 * input_width * input_height + 1.0 * spatial * patch_columns + 4.0 * spatial,
                             "B", s);
     hip_check(dav2_hip_im2col_quantize_i8(image.as<float>(), input_width, input_height, 3, pw, ph, 14, 14, 0,
-                                          packed.as<int8_t>(), ld, scales.as<float>(), s),
+                                          packed.as<int8_t>(), ld, scales.as<float>(), nullptr, 0, s),
               "patch im2col");
     linear_int8_packed(output, packed, ld, patch_int8_weight, scales, patch_int8_scales, patch_bias, spatial,
                        patch_columns, embedding, 1u, static_cast<std::uint32_t>(tokens), false, true);
@@ -319,9 +317,12 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     ProfileScope prof(context_.profiler(), "im2col_quantize_i8",
                       4.0 * input_width * input_height * input_channels + 1.0 * rows * inner + 4.0 * rows, "B",
                       context_.active_stream());
+    const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
+    grow(im2col_scratch_, scratch_floats * sizeof(float));
     hip_check(dav2_hip_im2col_quantize_i8(input.as<float>(), input_width, input_height, input_channels, ow, oh,
                                           kernel, stride, static_cast<std::int32_t>(padding), packed.as<int8_t>(),
-                                          ld, scales.as<float>(), context_.active_stream()),
+                                          ld, scales.as<float>(), im2col_scratch_.as<float>(), scratch_floats,
+                                          context_.active_stream()),
               "im2col quantize");
     workspace_ld_ = ld;
     linear_int8_packed(output, packed, ld, int8_weight, scales, weight_scales, bias, rows, inner, output_channels, 0u,
@@ -351,8 +352,11 @@ void HipOperators::conv_transpose_nonoverlap_int8(DeviceBuffer& output, const De
     const hipStream_t s = context_.active_stream();
     ProfileScope prof_q(context_.profiler(), "im2col_quantize_i8",
                         4.0 * input_rows * input_channels + 1.0 * input_rows * input_channels + 4.0 * input_rows, "B", s);
+    const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
+    grow(im2col_scratch_, scratch_floats * sizeof(float));
     hip_check(dav2_hip_im2col_quantize_i8(input.as<float>(), input_width, input_height, input_channels, input_width,
-                                          input_height, 1, 1, 0, packed.as<int8_t>(), ld, scales.as<float>(), s),
+                                          input_height, 1, 1, 0, packed.as<int8_t>(), ld, scales.as<float>(),
+                                          im2col_scratch_.as<float>(), scratch_floats, s),
               "im2col quantize");
     workspace_ld_ = ld;
     dav2_gemm_i8_args a{};

@@ -120,6 +120,7 @@ private:
     Int8Workspace workspace_;
     DeviceBuffer minmax_partials_;
     DeviceBuffer interpolated_;
+    DeviceBuffer im2col_scratch_;  // per-channel-group maxima for the tiled im2col kernels
     std::uint32_t workspace_ld_ = 0;  // row stride of the int8 rows currently in the workspace
 };
 

@@ -35,13 +35,18 @@ DAV2_API int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset
                                        uint32_t ldq, float* scales, void* stream);
 
 /* Replaces im2col_quantize_int8.glsl:26-83 (src/operators.cpp:1284-1298,
- * :1787-1801, :1946-1960). CHW input; rows = output_width*output_height. */
+ * :1787-1801, :1946-1960). CHW input; rows = output_width*output_height.
+ * scratch (optional, dav2_hip_im2col_scratch_floats() floats) enables the
+ * tiled 3x3-stride-1 and 1x1 kernels; without it the generic gather runs.
+ * Both produce the same bytes. */
+DAV2_API uint64_t dav2_hip_im2col_scratch_floats(uint32_t input_width, uint32_t input_height,
+                                                 uint32_t input_channels);
 DAV2_API int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width,
                                          uint32_t input_height, uint32_t input_channels,
                                          uint32_t output_width, uint32_t output_height,
                                          uint32_t kernel, uint32_t stride, int32_t padding,
                                          int8_t* q, uint32_t ldq, float* scales,
-                                         void* stream);
+                                         float* scratch, uint64_t scratch_floats, void* stream);
 
 /* Replaces layer_norm.glsl:27-68 (src/operators.cpp:1016-1042). */
 DAV2_API int dav2_hip_layer_norm(float* out, const float* input, const float* weight,
@@ -104,7 +109,12 @@ DAV2_API int dav2_hip_relu(float* out, const float* input, uint64_t count, void*
  * token-major (q | k | v, head h at h*64). fp16 = 0: fp32 scores [batch][H][T][T]
  * (bmm.glsl, softmax_lastdim.glsl); fp16 = 1: binary16 scores
  * [batch][H][T][ldt], ldt = T rounded up to a multiple of 8 (bmm_score_fp16.glsl,
- * softmax_lastdim_half.glsl, bmm_value_fp16.glsl). Softmax is in place. */
+ * softmax_lastdim_half.glsl, bmm_value_fp16.glsl), followed (at the next
+ * 256-byte boundary) by a packed binary16 copy of v that attention_values
+ * writes and reads. Softmax is in place. The whole score buffer holds
+ * dav2_hip_attention_scratch_bytes() bytes. */
+DAV2_API uint64_t dav2_hip_attention_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch,
+                                                   int fp16);
 DAV2_API int dav2_hip_attention_scores(void* scores, const float* qkv, uint32_t tokens,
                                        uint32_t heads, uint32_t batch, int fp16,
                                        void* stream);

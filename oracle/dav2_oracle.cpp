@@ -96,12 +96,6 @@ float h2f(uint16_t h) {
 
 inline float round_half(float f) { return h2f(f2h(f)); }
 
-// Eight binary16 round-trips at once (F16C, round to nearest even); the same
-// results as round_half lane by lane.
-inline __m256 round_half8(__m256 v) {
-    return _mm256_cvtph_ps(_mm256_cvtps_ph(v, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
-}
-
 // ---------------------------------------------------------------------------
 // int8 dot product; exact in int32 for |K| <= 2^31 / 127^2.
 inline int32_t dot_i8(const int8_t* a, const int8_t* b, uint32_t k) {
@@ -465,9 +459,11 @@ void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int
                         o[f] = s;
                     }
                 } else {
-                    // bmm_score_fp16.glsl:29-70: fp16(q*0.125), fp16(k), fp16
-                    // products accumulated in fp32 (sequentially over the 64
-                    // features), stored as fp16. Eight keys per AVX lane set.
+                    // bmm_score_fp16.glsl:29-70 operands: fp16(q*0.125), fp16(k),
+                    // score stored as fp16. Products of two binary16 values are
+                    // exact in fp32 and are accumulated in fp32 without the
+                    // shader's per-product fp16 rounding (the matrix-core
+                    // semantics of the HIP path). Eight keys per AVX lane set.
                     const std::vector<float>& kt = half_keys_t[h];
                     float qr[64];
                     for (int f = 0; f < 64; ++f) qr[f] = round_half(q[f] * 0.125f);
@@ -476,7 +472,7 @@ void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int
                         __m256 s = _mm256_setzero_ps();
                         for (int f = 0; f < 64; ++f) {
                             const __m256 prod = _mm256_mul_ps(_mm256_set1_ps(qr[f]), _mm256_loadu_ps(&kt[f * T + j]));
-                            s = _mm256_add_ps(s, round_half8(prod));
+                            s = _mm256_add_ps(s, prod);
                         }
                         alignas(32) float tmp[8];
                         _mm256_store_ps(tmp, s);
@@ -484,7 +480,7 @@ void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int
                     }
                     for (; j < T; ++j) {
                         float s = 0.0f;
-                        for (int f = 0; f < 64; ++f) s = s + round_half(qr[f] * kt[f * T + j]);
+                        for (int f = 0; f < 64; ++f) s = s + qr[f] * kt[f * T + j];
                         hrow[j] = f2h(s);
                     }
                     // softmax_lastdim_half.glsl: word w = (2w, 2w+1) handled by
@@ -511,15 +507,16 @@ void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int
                             partial[lane] = partial[lane] + partial[lane + stride];
                     const float inverse = 1.0f / std::max(partial[0], 1.0e-20f);
                     for (size_t j = 0; j < T; ++j) p[j] = round_half(h2f(hrow[j]) * inverse);
-                    // bmm_value_fp16.glsl: fp16 products, fp32 accumulation
-                    // sequentially over the source tokens; 8 features per lane set.
+                    // bmm_value_fp16.glsl operands fp16(p), fp16(v); exact
+                    // products, fp32 accumulation over the source tokens;
+                    // 8 features per lane set.
                     const std::vector<float>& vr = half_values[h];
                     float* o = out + static_cast<size_t>(i) * D + h * 64;
                     for (int f0 = 0; f0 < 64; f0 += 8) {
                         __m256 s = _mm256_setzero_ps();
                         for (size_t jj = 0; jj < T; ++jj) {
                             const __m256 prod = _mm256_mul_ps(_mm256_set1_ps(p[jj]), _mm256_loadu_ps(&vr[jj * 64 + f0]));
-                            s = _mm256_add_ps(s, round_half8(prod));
+                            s = _mm256_add_ps(s, prod);
                         }
                         _mm256_storeu_ps(o + f0, s);
                     }

@@ -62,7 +62,9 @@ def test_quantize_rows_packed_word_byte_order(gpu, lib):
 # a2 im2col_quantize_int8.glsl
 @pytest.mark.parametrize("c,h,w,k,s,p", [(3, 518, 518, 14, 14, 0), (3, 266, 350, 14, 14, 0), (64, 37, 37, 3, 1, 1),
                                          (96, 19, 19, 3, 2, 1), (32, 74, 74, 1, 1, 0), (5, 4, 4, 3, 1, 1),
-                                         (128, 60, 52, 3, 1, 1), (1024, 10, 10, 3, 2, 1)])
+                                         (128, 60, 52, 3, 1, 1), (1024, 10, 10, 3, 2, 1), (1024, 19, 19, 3, 1, 1),
+                                         (128, 130, 141, 3, 1, 1), (16, 3, 70, 3, 1, 1), (512, 37, 37, 1, 1, 0),
+                                         (48, 5, 7, 1, 1, 0), (256, 150, 150, 3, 1, 1)])
 def test_im2col_quantize_bit_exact(gpu, lib, oracle, c, h, w, k, s, p):
     torch = gpu
     _announce("im2col", c, h, w, k, s, p)
@@ -74,13 +76,18 @@ def test_im2col_quantize_bit_exact(gpu, lib, oracle, c, h, w, k, s, p):
     kk = c * k * k
     ld = (kk + 63) // 64 * 64
     xd = dev(torch, x)
-    qd = torch.full((ow * oh, ld), 0x55, dtype=torch.int8, device="cuda")
-    sd = empty(torch, (ow * oh,), torch.float32)
-    ok(lib, lib.dav2_hip_im2col_quantize_i8(ptr(xd), w, h, c, ow, oh, k, s, p, ptr(qd), ld, ptr(sd), stream(torch)))
-    q = host(torch, qd)
-    assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
-    assert np.array_equal(q[:, :kk], q_ref)
-    assert np.all(q[:, kk:] == 0)
+    n_scratch = lib.dav2_hip_im2col_scratch_floats(w, h, c)
+    scratch = empty(torch, (n_scratch,), torch.float32)
+    # generic gather kernels (no scratch), then the tiled 3x3 / 1x1 kernels
+    for sp, sn in ((None, 0), (ptr(scratch), n_scratch)):
+        qd = torch.full((ow * oh, ld), 0x55, dtype=torch.int8, device="cuda")
+        sd = empty(torch, (ow * oh,), torch.float32)
+        ok(lib, lib.dav2_hip_im2col_quantize_i8(ptr(xd), w, h, c, ow, oh, k, s, p, ptr(qd), ld, ptr(sd), sp, sn,
+                                                stream(torch)))
+        q = host(torch, qd)
+        assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
+        assert np.array_equal(q[:, :kk], q_ref)
+        assert np.all(q[:, kk:] == 0)
 
 
 # ---------------------------------------------------------------------------
@@ -215,13 +222,19 @@ def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
 def _attention_gpu(torch, lib, qkv, tokens, heads, fp16):
     qd = dev(torch, qkv)
     ldt = (tokens + 7) // 8 * 8 if fp16 else tokens
-    scores = torch.empty((heads, tokens, ldt), dtype=torch.float16 if fp16 else torch.float32, device="cuda")
+    nbytes = lib.dav2_hip_attention_scratch_bytes(tokens, heads, 1, int(fp16))
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     out = empty(torch, (tokens, heads * 64), torch.float32)
     s = stream(torch)
-    ok(lib, lib.dav2_hip_attention_scores(ptr(scores), ptr(qd), tokens, heads, 1, int(fp16), s))
-    ok(lib, lib.dav2_hip_softmax_rows(ptr(scores), heads * tokens, tokens, ldt, int(fp16), s))
-    ok(lib, lib.dav2_hip_attention_values(ptr(out), ptr(scores), ptr(qd), tokens, heads, 1, int(fp16), s))
-    return host(torch, out), host(torch, scores)[:, :, :tokens].astype(np.float32)
+    ok(lib, lib.dav2_hip_attention_scores(ptr(buf), ptr(qd), tokens, heads, 1, int(fp16), s))
+    ok(lib, lib.dav2_hip_softmax_rows(ptr(buf), heads * tokens, tokens, ldt, int(fp16), s))
+    ok(lib, lib.dav2_hip_attention_values(ptr(out), ptr(buf), ptr(qd), tokens, heads, 1, int(fp16), s))
+    n = heads * tokens * ldt
+    scores = buf[: n * (2 if fp16 else 4)].view(torch.float16 if fp16 else torch.float32).reshape(heads, tokens, ldt)
+    probs = host(torch, scores)
+    if fp16:
+        assert np.all(probs[:, :, tokens:] == 0)  # padding columns are zero after the softmax
+    return host(torch, out), probs[:, :, :tokens].astype(np.float32)
 
 
 @pytest.mark.parametrize("tokens,heads", [(5, 2), (65, 3), (1370, 6), (1370, 16)])

@@ -205,9 +205,11 @@ def test_prepare_tokens_reference_kat(gpu, pkg, lib, oracle, ops):
     image = np.zeros((3, height, width), np.float32)
     wq, ws = oracle.quantize_weight_rows(np.zeros((dim, 3, 14, 14), np.float32))
     out = empty(torch, (7, dim), torch.float32)
-    run(lib, lib.dav2_ops_prepare_tokens(ops, db(pkg, out), db(pkg, dev(torch, image)), db(pkg, dev(torch, pad_rows(wq))),
-                                         db(pkg, dev(torch, ws)), db(pkg, dev(torch, bias)), db(pkg, dev(torch, cls)),
-                                         db(pkg, dev(torch, pos)), width, height, dim))
+    # Every device tensor stays referenced until the call is synchronised: a
+    # temporary would go back to torch's caching allocator and the next
+    # upload could reuse its memory.
+    held = [dev(torch, a) for a in (image, pad_rows(wq), ws, bias, cls, pos)]
+    run(lib, lib.dav2_ops_prepare_tokens(ops, db(pkg, out), *[db(pkg, t) for t in held], width, height, dim))
     sync(lib, ops)
     tokens = host(torch, out)
     assert np.array_equal(tokens[0], cls + pos[0])
@@ -247,8 +249,8 @@ def test_layer_norm_add_scaled_kats(gpu, pkg, lib, ops):
     x = ((np.arange(rows * cols) % 23 - 10) * 0.125).astype(np.float32).reshape(rows, cols)
     w, b = np.ones(cols, np.float32), np.zeros(cols, np.float32)
     out = empty(torch, (rows, cols), torch.float32)
-    run(lib, lib.dav2_ops_layer_norm(ops, db(pkg, out), db(pkg, dev(torch, x)), db(pkg, dev(torch, w)),
-                                     db(pkg, dev(torch, b)), rows, cols, 1e-6))
+    held = [dev(torch, a) for a in (x, w, b)]
+    run(lib, lib.dav2_ops_layer_norm(ops, db(pkg, out), *[db(pkg, t) for t in held], rows, cols, 1e-6))
     sync(lib, ops)
     mean = x.mean(axis=1, keepdims=True)
     var = np.maximum((x * x).mean(axis=1, keepdims=True) - mean * mean, 0)
@@ -257,8 +259,8 @@ def test_layer_norm_add_scaled_kats(gpu, pkg, lib, ops):
     addend = ((np.arange(15) + 2) * -0.0625).astype(np.float32)
     scale = ((np.arange(5) + 1) * 0.25).astype(np.float32)
     o2 = empty(torch, (15,), torch.float32)
-    run(lib, lib.dav2_ops_add_scaled(ops, db(pkg, o2), db(pkg, dev(torch, residual)), db(pkg, dev(torch, addend)),
-                                     db(pkg, dev(torch, scale)), 15, 5))
+    held2 = [dev(torch, a) for a in (residual, addend, scale)]
+    run(lib, lib.dav2_ops_add_scaled(ops, db(pkg, o2), *[db(pkg, t) for t in held2], 15, 5))
     sync(lib, ops)
     assert np.array_equal(host(torch, o2), residual + addend * scale[np.arange(15) % 5])
     assert lib.dav2_ops_add_scaled(ops, db(pkg, o2), db(pkg, o2), db(pkg, o2), db(pkg, o2), 15, 4) == 1
@@ -270,13 +272,14 @@ def test_attention_head64_surface(gpu, pkg, lib, oracle, ops, tokens, heads, pre
     rng = np.random.default_rng(tokens + heads)
     qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * 0.5).astype(np.float32)
     out = empty(torch, (tokens, heads * 64), torch.float32)
-    run(lib, lib.dav2_ops_attention_head64(ops, db(pkg, out), db(pkg, dev(torch, qkv)), tokens, heads, db(pkg, None),
+    qkv_d = dev(torch, qkv)
+    run(lib, lib.dav2_ops_attention_head64(ops, db(pkg, out), db(pkg, qkv_d), tokens, heads, db(pkg, None),
                                            precision))
     sync(lib, ops)
     ref = oracle.attention(qkv, tokens, heads, fp16=bool(precision))
     np.testing.assert_allclose(host(torch, out), ref, atol=2e-3 if precision else 2e-6, rtol=1e-4)
     small = empty(torch, (16,), torch.float32)
-    assert lib.dav2_ops_attention_head64(ops, db(pkg, out), db(pkg, dev(torch, qkv)), tokens, heads, db(pkg, small),
+    assert lib.dav2_ops_attention_head64(ops, db(pkg, out), db(pkg, qkv_d), tokens, heads, db(pkg, small),
                                          precision) == 1
 
 
@@ -285,7 +288,8 @@ def test_bilinear_minmax_normalize_surface(gpu, pkg, lib, oracle, ops):
     rng = np.random.default_rng(2)
     x = rng.standard_normal((1, 296, 296)).astype(np.float32)
     out = empty(torch, (1, 518, 518), torch.float32)
-    run(lib, lib.dav2_ops_bilinear_align_true(ops, db(pkg, out), db(pkg, dev(torch, x)), 296, 296, 518, 518, 1))
+    x_d = dev(torch, x)
+    run(lib, lib.dav2_ops_bilinear_align_true(ops, db(pkg, out), db(pkg, x_d), 296, 296, 518, 518, 1))
     rng_d = empty(torch, (2,), torch.float32)
     run(lib, lib.dav2_ops_reduce_minmax(ops, db(pkg, out), db(pkg, rng_d), 518 * 518))
     run(lib, lib.dav2_ops_normalize_relative(ops, db(pkg, out), db(pkg, rng_d), 518 * 518))
