@@ -75,6 +75,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=30.0)
     ap.add_argument("--profile-json", default="")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run one device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not part of this build "
@@ -86,6 +88,19 @@ def main() -> int:
 
     import numpy as np
     import torch
+
+    if args.copy_calibration:
+        # A plain copy kernel of known size: reads and writes exactly
+        # MIB MiB, so FETCH_SIZE / WRITE_SIZE of its dispatch give the
+        # factor between those counters and HBM bytes.
+        n = args.copy_calibration * 2**20 // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4}))
+        return 0
 
     pkg = load_package()
     fmt = pkg.dav2_format
@@ -174,10 +189,11 @@ def main() -> int:
         "config": {"workload": f"{args.encoder} + DPT {args.size}x{args.size} batch {args.batch}, int8 GEMMs, "
                                f"{'fp32' if args.fp32_attention else 'fp16'} attention scores, "
                                "dav2_infer_tensor_f32_device",
-                   "encoder": args.encoder, "size": args.size, "global_batch": args.batch,
+                   "size": args.size, "global_batch": args.batch,
                    "parallelism": "single GPU"},
         "roofline": {"kernel": "gemm_i8", "bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS,
-                     "unit": "TOP/s", "frac": achieved / PEAK_INT8_TOPS,
+                     "unit": "TFLOP/s", "work": "int8 ops, 2*M*N*K per GEMM",
+                     "frac": achieved / PEAK_INT8_TOPS,
                      "avg_launch_us": 1e3 * g_ms / g_launches, "launches_per_step": g_launches / args.steps,
                      "traffic": traffic},
         "kernels": {k: kernels[k] for k in list(kernels)[:8]},

@@ -143,6 +143,8 @@ PROTOTYPES = {
     "dav2_hip_softmax_rows": (C.c_int, [vp, u64, u32, u32, C.c_int, vp]),
     "dav2_hip_attention_values": (C.c_int, [vp, vp, vp, u32, u32, u32, C.c_int, vp]),
     "dav2_hip_attention_scratch_bytes": (u64, [u32, u32, u32, C.c_int]),
+    "dav2_hip_attention_fused_scratch_bytes": (u64, [u32, u32, u32]),
+    "dav2_hip_attention_fused": (C.c_int, [vp, vp, u32, u32, u32, vp, u64, vp]),
     "dav2_hip_bilinear_align_true": (C.c_int, [vp, vp, u32, u32, u32, u32, u32, vp]),
     "dav2_hip_minmax_partials": (u32, [u64]),
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),

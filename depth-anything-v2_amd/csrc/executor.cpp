@@ -8,8 +8,8 @@ namespace dav2 {
 
 namespace {
 Precision attention_precision_for(std::uint32_t flags) {
-    // src/encoder.cpp:389-396: int8 mode keeps binary16 attention scores unless
-    // FORCE_FP32(_ATTENTION) asks for fp32 scores.
+    // src/encoder.cpp:389-396: int8 mode uses binary16 attention operands
+    // (the fused kernel) unless FORCE_FP32(_ATTENTION) asks for fp32 scores.
     return (flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP32_ATTENTION)) != 0 ? Precision::fp32
                                                                                        : Precision::fp16;
 }

@@ -72,8 +72,10 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
     DeviceBuffer& qkv = arena.get("enc.qkv", tok_bytes * 3);
     DeviceBuffer& attn = arena.get("enc.attention", tok_bytes);
     DeviceBuffer& hidden = arena.get("enc.hidden", tok_bytes * 4);
+    const bool fused = attention_precision_ == Precision::fp16;
     DeviceBuffer& scores =
-        arena.get("enc.scores", HipOperators::attention_score_bytes(T, H, batch, attention_precision_));
+        arena.get("enc.scores", fused ? HipOperators::attention_fused_scratch_bytes(T, H, batch)
+                                      : HipOperators::attention_score_bytes(T, H, batch, attention_precision_));
     for (int i = 0; i < 4; ++i) features[i] = &arena.get("enc.feature" + std::to_string(i), tok_bytes);
 
     // Patch embedding + class token + position (operators.cpp:1211-1406), one
@@ -98,8 +100,12 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
         const GpuTensor& wqkv = W(".attn.qkv.weight");
         ops_.linear_int8_prequantized(qkv, wqkv.int8_buffer, wqkv.int8_scales, &F(".attn.qkv.bias"), rows, D, 3 * D,
                                       HipOperators::Epilogue::row);
-        // attention (encoder.cpp:454-460)
-        ops_.attention_batched(attn, qkv, T, H, batch, scores, attention_precision_);
+        // attention (encoder.cpp:454-460): fused binary16-operand kernel in
+        // int8 mode, materialised fp32 scores under FORCE_FP32(_ATTENTION)
+        if (fused)
+            ops_.attention_fused(attn, qkv, T, H, batch, scores);
+        else
+            ops_.attention_batched(attn, qkv, T, H, batch, scores, attention_precision_);
         // proj + LayerScale residual (encoder.cpp:478-491), in place
         ops_.quantize_rows(attn, 0, rows, D);
         const GpuTensor& wproj = W(".attn.proj.weight");

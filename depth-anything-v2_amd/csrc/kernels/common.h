@@ -56,4 +56,48 @@ DAV2_DEV float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
 inline unsigned ceil_div(uint64_t a, uint64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
+// e^a by Cody-Waite range reduction (a = n ln2 + r, |r| <= ln2/2, ln2 split
+// into a 16-bit head and a tail) and the degree-7 Taylor polynomial of e^r in
+// Horner form with explicit fmaf; error below 1 ulp of float over the range.
+// Every step is a correctly rounded IEEE operation, so the CPU oracle's
+// restatement of the same sequence returns the same bits. Results below
+// e^-86 (about 2^-124) are flushed to zero, above FLT_MAX they are +inf.
+DAV2_DEV float exp_cw(float a) {
+    if (!(a > -86.0f)) return a != a ? a : 0.0f;
+    if (a > 88.72f) return __builtin_inff();
+    const float n = __builtin_rintf(a * 1.44269504f);
+    float r = fmaf(-n, 0.693145751953125f, a);  // ln2 head, exact product
+    r = fmaf(-n, 1.42860677e-6f, r);             // ln2 - head
+    float p = 1.98412698e-4f;                    // 1/7!
+    p = fmaf(p, r, 1.38888889e-3f);              // 1/6!
+    p = fmaf(p, r, 8.33333333e-3f);              // 1/5!
+    p = fmaf(p, r, 4.16666667e-2f);              // 1/4!
+    p = fmaf(p, r, 1.66666667e-1f);              // 1/3!
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, static_cast<int>(n));
+}
+
+// gelu.glsl:29-48: 0.5 x (1 + erf(x / sqrt 2)) with erf from the
+// Numerical Recipes erfc fit, the shader's operation order and exp_cw.
+DAV2_DEV float gelu_erfcc(float value) {
+    const float x = value * 0.70710678118654752440f;
+    const float magnitude = fabsf(x);
+    const float t = 1.0f / (1.0f + 0.5f * magnitude);
+    float poly = t * 0.17087277f;
+    poly = t * (-0.82215223f + poly);
+    poly = t * (1.48851587f + poly);
+    poly = t * (-1.13520398f + poly);
+    poly = t * (0.27886807f + poly);
+    poly = t * (-0.18628806f + poly);
+    poly = t * (0.09678418f + poly);
+    poly = t * (0.37409196f + poly);
+    poly = t * (1.00002368f + poly);
+    poly = -1.26551223f + poly;
+    const float erfc_magnitude = t * exp_cw(-magnitude * magnitude + poly);
+    const float erf_value = x >= 0.0f ? 1.0f - erfc_magnitude : erfc_magnitude - 1.0f;
+    return 0.5f * value * (1.0f + erf_value);
+}
+
 }  // namespace dav2k

@@ -18,12 +18,12 @@ unsigned grid_for(uint64_t items) {
     return static_cast<unsigned>(g < 65536u ? (g == 0 ? 1 : g) : 65536u);
 }
 
-// gelu.glsl:16-49: 0.5 x (1 + erf(x / sqrt 2)), erf from the device libm.
+// gelu.glsl:16-49 (erfc fit and operation order of the shader).
 __global__ __launch_bounds__(kBlock) void gelu_kernel(float* out, const float* in, uint64_t n) {
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
          i += static_cast<uint64_t>(gridDim.x) * kBlock) {
         const float v = in[i];
-        out[i] = 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+        out[i] = gelu_erfcc(v);
     }
 }
 

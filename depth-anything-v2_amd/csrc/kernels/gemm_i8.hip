@@ -49,7 +49,7 @@ DAV2_DEV float dequant(int32_t acc, float s_in, float s_w, float b) {
 }
 
 DAV2_DEV float gelu_erf(float v) {
-    return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+    return gelu_erfcc(v);
 }
 
 template <int EPI>

@@ -233,6 +233,28 @@ void HipOperators::attention_batched(DeviceBuffer& output, const DeviceBuffer& q
     }
 }
 
+std::uint64_t HipOperators::attention_fused_scratch_bytes(std::uint32_t tokens, std::uint32_t heads,
+                                                          std::uint32_t batch) {
+    return dav2_hip_attention_fused_scratch_bytes(tokens, heads, batch);
+}
+
+void HipOperators::attention_fused(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
+                                   std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scratch) {
+    if (tokens == 0 || heads == 0 || batch == 0) throw std::invalid_argument("invalid attention dimensions");
+    const std::uint64_t elements = std::uint64_t(batch) * tokens * heads * 64;
+    require_bytes(output, elements, "attention output");
+    require_bytes(qkv, elements * 3, "QKV");
+    const std::uint64_t need = attention_fused_scratch_bytes(tokens, heads, batch);
+    if (scratch.size() < need) throw std::invalid_argument("attention scratch device buffer is too small");
+    const hipStream_t s = context_.active_stream();
+    // QK^T and PV: 4*T*T*64 flops per head.
+    const double flops = 4.0 * batch * heads * double(tokens) * tokens * 64.0;
+    ProfileScope p(context_.profiler(), "attention_fused", flops, "FLOP", s);
+    hip_check(dav2_hip_attention_fused(output.as<float>(), qkv.as<float>(), tokens, heads, batch, scratch.data(),
+                                       scratch.size(), s),
+              "fused attention");
+}
+
 // src/operators.cpp:1211-1406 (int8 branch)
 void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& image, const DeviceBuffer&,
                                   const DeviceBuffer&, const DeviceBuffer& patch_int8_weight,

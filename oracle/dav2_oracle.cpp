@@ -133,12 +133,47 @@ inline float dequant(int32_t acc, float s_in, float s_w, float b) {
     return v + b;
 }
 
+// e^a: Cody-Waite reduction a = n ln2 + r (ln2 as a 16-bit head plus tail),
+// degree-7 Taylor polynomial of e^r by Horner with fused multiply-adds,
+// scaling by 2^n. Each step is one correctly rounded IEEE operation, the
+// sequence the GPU kernels evaluate; results below e^-86 are zero.
+float exp_cw(float a) {
+    if (!(a > -86.0f)) return a != a ? a : 0.0f;
+    if (a > 88.72f) return std::numeric_limits<float>::infinity();
+    const float n = std::nearbyint(a * 1.44269504f);
+    float r = std::fmaf(-n, 0.693145751953125f, a);
+    r = std::fmaf(-n, 1.42860677e-6f, r);
+    float p = 1.98412698e-4f;
+    p = std::fmaf(p, r, 1.38888889e-3f);
+    p = std::fmaf(p, r, 8.33333333e-3f);
+    p = std::fmaf(p, r, 4.16666667e-2f);
+    p = std::fmaf(p, r, 1.66666667e-1f);
+    p = std::fmaf(p, r, 0.5f);
+    p = std::fmaf(p, r, 1.0f);
+    p = std::fmaf(p, r, 1.0f);
+    return std::ldexp(p, static_cast<int>(n));
+}
+
 inline float gelu_value(float value) {
-    // gelu.glsl:29-48 computes 0.5*x*(1+erf(x/sqrt2)) with erf from the
-    // Numerical Recipes erfcc fit (~1.2e-7); the build uses libm/device erff.
+    // gelu.glsl:29-48: 0.5*x*(1+erf(x/sqrt2)), erf = 1 - erfc from the
+    // Numerical Recipes fit (coefficients and Horner order of the shader),
+    // its exp evaluated by exp_cw.
     const float x = value * 0.70710678118654752440f;
-    const float e = std::erf(x);
-    return 0.5f * value * (1.0f + e);
+    const float magnitude = std::fabs(x);
+    const float t = 1.0f / (1.0f + 0.5f * magnitude);
+    float poly = t * 0.17087277f;
+    poly = t * (-0.82215223f + poly);
+    poly = t * (1.48851587f + poly);
+    poly = t * (-1.13520398f + poly);
+    poly = t * (0.27886807f + poly);
+    poly = t * (-0.18628806f + poly);
+    poly = t * (0.09678418f + poly);
+    poly = t * (0.37409196f + poly);
+    poly = t * (1.00002368f + poly);
+    poly = -1.26551223f + poly;
+    const float erfc_magnitude = t * exp_cw(-magnitude * magnitude + poly);
+    const float erf_value = x >= 0.0f ? 1.0f - erfc_magnitude : erfc_magnitude - 1.0f;
+    return 0.5f * value * (1.0f + erf_value);
 }
 
 // ---------------------------------------------------------------------------
@@ -213,6 +248,9 @@ int orc_get_threads(void) { return omp_get_max_threads(); }
 uint16_t orc_float_to_half(float value) { return f2h(value); }
 float orc_half_to_float(uint16_t value) { return h2f(value); }
 uint32_t orc_crc32(const void* data, size_t bytes) { return crc32_impl(data, bytes); }
+void orc_exp(const float* input, uint64_t count, float* out) {
+    for (uint64_t i = 0; i < count; ++i) out[i] = exp_cw(input[i]);
+}
 
 void orc_quantize_rows(const float* input, uint32_t rows, uint32_t columns,
                        uint32_t input_offset, int8_t* q, float* scales) {
@@ -411,10 +449,111 @@ void orc_softmax_rows(const float* input, uint64_t rows, uint32_t columns, float
                          out + static_cast<size_t>(r) * columns);
 }
 
-void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int fp16,
-                          float* out, float* probabilities) {
+namespace {
+
+// 15-bit block floating point: x[i*stride] ~= X[i] * 2^exponent with
+// |X| <= 16383. a = max|x| = m * 2^e (frexp, m in [0.5, 1)), exponent = e - 14,
+// X = clamp(rint(x * 2^(14 - e)), -16383, 16383); an all-zero vector gets
+// X = 0, exponent 0.
+void block_fixed15(const float* x, size_t n, size_t stride, int32_t* X, int* exponent) {
+    float a = 0.0f;
+    for (size_t i = 0; i < n; ++i) a = std::max(a, std::fabs(x[i * stride]));
+    if (a == 0.0f) {
+        for (size_t i = 0; i < n; ++i) X[i] = 0;
+        *exponent = 0;
+        return;
+    }
+    int e = 0;
+    std::frexp(a, &e);
+    for (size_t i = 0; i < n; ++i) {
+        const float v = std::nearbyint(std::ldexp(x[i * stride], 14 - e));
+        X[i] = static_cast<int32_t>(std::min(std::max(v, -16383.0f), 16383.0f));
+    }
+    *exponent = e - 14;
+}
+
+// Integer-exact attention (the int8-mode kernel): q*0.125 and k in 15-bit
+// block floating point per token row, v per feature column over the tokens.
+//   s_ij = fp32(Q_i . K_j * 2^(eq_i + ek_j))         (exact dot, one rounding)
+//   E_ij = min(rint(exp_cw(s_ij - max_j s_ij) * 2^21), 2^21 - 1)
+//   o_if = ldexp(fp32(sum_j E_ij V_jf) / fp32(sum_j E_ij), ev_f)
+// Every sum is an exact integer, so no result depends on summation order.
+void attention_exact(const float* qkv, uint32_t tokens, uint32_t heads, float* out,
+                     float* probabilities) {
     const size_t D = static_cast<size_t>(heads) * 64;
     const size_t T = tokens;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t h = 0; h < heads; ++h) {
+        std::vector<double> qd(T * 64), kd(T * 64), vd(T * 64);
+        std::vector<int> qe(T), ke(T), ve(64);
+        std::vector<int32_t> X(std::max<size_t>(T, 64));
+        std::vector<float> row(64);
+        for (size_t t = 0; t < T; ++t) {
+            const float* q = qkv + t * D * 3 + h * 64;
+            for (int f = 0; f < 64; ++f) row[f] = q[f] * 0.125f;
+            block_fixed15(row.data(), 64, 1, X.data(), &qe[t]);
+            for (int f = 0; f < 64; ++f) qd[t * 64 + f] = X[f];
+            block_fixed15(q + D, 64, 1, X.data(), &ke[t]);
+            for (int f = 0; f < 64; ++f) kd[t * 64 + f] = X[f];
+        }
+        for (int f = 0; f < 64; ++f) {
+            block_fixed15(qkv + 2 * D + h * 64 + f, T, D * 3, X.data(), &ve[f]);
+            for (size_t t = 0; t < T; ++t) vd[t * 64 + f] = X[t];
+        }
+        std::vector<float> s(T);
+        std::vector<double> E(T);
+        for (size_t i = 0; i < T; ++i) {
+            const double* qi = &qd[i * 64];
+            float maximum = -std::numeric_limits<float>::infinity();
+            for (size_t j = 0; j < T; ++j) {
+                // products < 2^28, sums < 2^34: every double operation is exact
+                const double* kj = &kd[j * 64];
+                __m256d acc = _mm256_setzero_pd();
+                for (int f = 0; f < 64; f += 4)
+                    acc = _mm256_fmadd_pd(_mm256_loadu_pd(qi + f), _mm256_loadu_pd(kj + f), acc);
+                alignas(32) double lanes[4];
+                _mm256_store_pd(lanes, acc);
+                const double dot = (lanes[0] + lanes[1]) + (lanes[2] + lanes[3]);
+                s[j] = static_cast<float>(std::ldexp(dot, qe[i] + ke[j]));
+                maximum = std::max(maximum, s[j]);
+            }
+            double L = 0.0;
+            for (size_t j = 0; j < T; ++j) {
+                const float e = exp_cw(s[j] - maximum) * 2097152.0f;
+                E[j] = std::min(std::nearbyint(e), 2097151.0f);
+                L += E[j];
+            }
+            // E < 2^21, |V| < 2^14, T < 2^17: sums stay below 2^52 (exact)
+            __m256d o[16];
+            for (int c = 0; c < 16; ++c) o[c] = _mm256_setzero_pd();
+            for (size_t j = 0; j < T; ++j) {
+                const __m256d e = _mm256_set1_pd(E[j]);
+                const double* vj = &vd[j * 64];
+                for (int c = 0; c < 16; ++c) o[c] = _mm256_fmadd_pd(e, _mm256_loadu_pd(vj + 4 * c), o[c]);
+            }
+            alignas(32) double ov[64];
+            for (int c = 0; c < 16; ++c) _mm256_store_pd(ov + 4 * c, o[c]);
+            const float Lf = static_cast<float>(L);
+            float* dst = out + i * D + h * 64;
+            for (int f = 0; f < 64; ++f) dst[f] = std::ldexp(static_cast<float>(ov[f]) / Lf, ve[f]);
+            if (probabilities)
+                for (size_t j = 0; j < T; ++j)
+                    probabilities[(h * T + i) * T + j] = static_cast<float>(E[j]) / Lf;
+        }
+    }
+}
+
+}  // namespace
+
+void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int mode,
+                          float* out, float* probabilities) {
+    if (mode == 2) {
+        attention_exact(qkv, tokens, heads, out, probabilities);
+        return;
+    }
+    const size_t D = static_cast<size_t>(heads) * 64;
+    const size_t T = tokens;
+    const int fp16 = mode != 0;
     // fp16 path: binary16-rounded keys (feature-major, 64 x T) and values
     // (T x 64) per head, converted once.
     std::vector<std::vector<float>> half_keys_t(fp16 ? heads : 0), half_values(fp16 ? heads : 0);
@@ -810,7 +949,8 @@ void encoder_block(const orc_model& m, std::vector<float>& cur, uint32_t T, uint
     orc_layer_norm(cur.data(), m.t(blk(b, ".norm1.weight")).data.data(), m.t(blk(b, ".norm1.bias")).data.data(),
                    T, D, 1.0e-6f, norm.data());
     lin(norm, blk(b, ".attn.qkv.weight"), blk(b, ".attn.qkv.bias"), D, 3 * D, false, qkv);
-    orc_attention_head64(qkv.data(), T, m.heads, fp16, attn.data(), nullptr);
+    // int8 default: fused attention (binary16 operands, fp32 scores)
+    orc_attention_head64(qkv.data(), T, m.heads, fp16 ? 2 : 0, attn.data(), nullptr);
     lin(attn, blk(b, ".attn.proj.weight"), blk(b, ".attn.proj.bias"), D, D, false, tmp);
     orc_add_scaled(cur.data(), tmp.data(), m.t(blk(b, ".ls1.gamma")).data.data(), n, D, next.data());
     cur.swap(next);

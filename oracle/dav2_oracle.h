@@ -61,7 +61,10 @@ void orc_linear_epilogue(const int32_t* acc, const float* input_scales,
 void orc_linear_int8(const float* input, const int8_t* w8, const float* w_scales,
                      const float* bias, uint32_t rows, uint32_t in_columns,
                      uint32_t out_columns, int gelu, float* out);
+/* gelu.glsl:16-49 (Numerical Recipes erfc fit, shader operation order). */
 void orc_gelu(const float* input, uint64_t count, float* out);
+/* e^x as the kernels evaluate it (Cody-Waite reduction, degree-7 Taylor). */
+void orc_exp(const float* input, uint64_t count, float* out);
 void orc_layer_norm(const float* input, const float* weight, const float* bias,
                     uint32_t rows, uint32_t columns, float epsilon, float* out);
 void orc_add_scaled(const float* residual, const float* addend,
@@ -71,10 +74,16 @@ void orc_add(const float* left, const float* right, uint64_t count, float* out);
 void orc_relu(const float* input, uint64_t count, float* out);
 void orc_softmax_rows(const float* input, uint64_t rows, uint32_t columns,
                       float* out);
-/* fp16: 1 -> softmax_lastdim_half/bmm_*_fp16 arithmetic, 0 -> fp32 bmm/softmax.
- * scores (optional, fp32 view) receives the probabilities [H][T][T]. */
+/* mode 0: fp32 bmm/softmax (bmm.glsl, softmax_lastdim.glsl).
+ * mode 1: materialised binary16 scores and probabilities
+ *         (bmm_score_fp16.glsl, softmax_lastdim_half.glsl, bmm_value_fp16.glsl)
+ *         with exact products accumulated in fp32.
+ * mode 2: integer-exact (the int8-mode kernel): 15-bit block floating point
+ *         q*0.125, k (per token) and v (per feature), exact integer dot
+ *         products, one rounding per score, 21-bit softmax numerators.
+ * probabilities (optional) receives [H][T][T]. */
 void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads,
-                          int fp16, float* out, float* probabilities);
+                          int mode, float* out, float* probabilities);
 void orc_bilinear_align_true(const float* input, uint32_t input_width,
                              uint32_t input_height, uint32_t output_width,
                              uint32_t output_height, uint32_t channels,
@@ -112,7 +121,8 @@ typedef struct orc_model orc_model;
 orc_model* orc_model_load(const char* path, int encoder, char* error,
                           size_t error_bytes);
 void orc_model_free(orc_model* model);
-/* depth: W*H raw ReLU depth. pre_relu (nullable): W*H before the final ReLU.
+/* fp16_attention != 0 runs attention in mode 2 (the int8 default), else mode 0.
+ * depth: W*H raw ReLU depth. pre_relu (nullable): W*H before the final ReLU.
  * features (nullable): 4*T*D captured encoder features.
  * Returns 0 on success. */
 int orc_model_infer(orc_model* model, const float* chw, uint32_t width,

@@ -173,11 +173,15 @@ class Oracle:
         self.lib.orc_softmax_rows(x.ctypes.data, x.shape[0], x.shape[1], out.ctypes.data)
         return out
 
-    def attention(self, qkv, tokens: int, heads: int, fp16: bool = False, probabilities: bool = False):
+    def attention(self, qkv, tokens: int, heads: int, fp16: bool = False, probabilities: bool = False,
+                  fused: bool = False):
+        """fp16=False: fp32 path; fp16=True: materialised binary16 scores;
+        fused=True: binary16 operands with fp32 scores (the int8 default)."""
         qkv = _f32(qkv)
         out = np.empty((tokens, heads * 64), np.float32)
         p = np.empty((heads, tokens, tokens), np.float32) if probabilities else None
-        self.lib.orc_attention_head64(qkv.ctypes.data, tokens, heads, int(fp16), out.ctypes.data, _p(p))
+        mode = 2 if fused else int(fp16)
+        self.lib.orc_attention_head64(qkv.ctypes.data, tokens, heads, mode, out.ctypes.data, _p(p))
         return (out, p) if probabilities else out
 
     def bilinear(self, x, ow: int, oh: int):

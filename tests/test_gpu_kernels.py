@@ -160,12 +160,11 @@ def test_gemm_row_epilogues(gpu, pkg, lib, oracle, m, n, k):
     reft = oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m, row_stride=m, transposed=True).reshape(n, m)
     assert np.array_equal(host(torch, outt).view(np.uint32), reft.view(np.uint32))
 
-    # ROW + GELU: device erff vs libm erff differ by an ulp or two; where
-    # 1 + erf(x) cancels (x << 0) that is ~1e-7 absolute.
+    # ROW + GELU (erfc fit and exp evaluated by the same IEEE sequence): exact
     outg = torch.zeros((m, n), dtype=torch.float32, device="cuda")
     ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, epilogue=2, bias=ptr(biasd), out=ptr(outg))), s))
     refg = oracle.gelu(oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m).reshape(m, n))
-    np.testing.assert_allclose(host(torch, outg), refg, rtol=1e-6, atol=3e-7)
+    assert np.array_equal(host(torch, outg).view(np.uint32), refg.view(np.uint32))
 
     # ROW + LayerScale residual, in place (add_scaled.glsl arithmetic)
     resid = rng.standard_normal((m, n)).astype(np.float32)
@@ -284,6 +283,60 @@ def test_attention_fp16(gpu, lib, oracle, tokens, heads):
     assert np.abs(out - ref32).max() <= 3e-3
 
 
+def _attention_fused_gpu(torch, lib, qkv, tokens, heads, batch):
+    qd = dev(torch, qkv)
+    nbytes = lib.dav2_hip_attention_fused_scratch_bytes(tokens, heads, batch)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    out = empty(torch, (batch * tokens, heads * 64), torch.float32)
+    ok(lib, lib.dav2_hip_attention_fused(ptr(out), ptr(qd), tokens, heads, batch, ptr(buf), nbytes, stream(torch)))
+    # one byte short of the packed operands is rejected before any launch
+    assert lib.dav2_hip_attention_fused(ptr(out), ptr(qd), tokens, heads, batch, ptr(buf), nbytes - 1,
+                                        stream(torch)) == 1
+    return host(torch, out)
+
+
+@pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (5, 2, 1), (64, 3, 1), (77, 4, 2), (257, 6, 1),
+                                                (1370, 16, 1), (1370, 6, 3), (2000, 2, 1)])
+def test_attention_fused(gpu, lib, oracle, tokens, heads, batch):
+    # Integer-exact kernel vs the oracle's restatement: every sum is an exact
+    # integer and every rounding the same IEEE operation, so bit for bit; and
+    # within 2e-4 of float64 attention.
+    torch = gpu
+    _announce("attention fused", tokens, heads, batch)
+    rng = np.random.default_rng(tokens * 7 + heads + batch)
+    qkv = (rng.standard_normal((batch * tokens, 3 * heads * 64)) * 0.5).astype(np.float32)
+    out = _attention_fused_gpu(torch, lib, qkv, tokens, heads, batch)
+    for b in range(batch):
+        rows = slice(b * tokens, (b + 1) * tokens)
+        ref = oracle.attention(qkv[rows], tokens, heads, fused=True)
+        assert np.array_equal(out[rows].view(np.uint32), ref.view(np.uint32))
+        q = qkv[rows, :heads * 64].reshape(tokens, heads, 64).astype(np.float64)
+        k = qkv[rows, heads * 64:2 * heads * 64].reshape(tokens, heads, 64).astype(np.float64)
+        v = qkv[rows, 2 * heads * 64:].reshape(tokens, heads, 64).astype(np.float64)
+        sc = np.einsum("ihf,jhf->hij", q * 0.125, k)
+        p = np.exp(sc - sc.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        exact = np.einsum("hij,jhf->ihf", p, v).reshape(tokens, heads * 64)
+        assert np.abs(out[rows] - exact).max() <= 2e-4
+
+
+def test_attention_fused_peaked_and_zero_rows(gpu, lib, oracle):
+    # Peaked rows (|s| up to ~60, most numerators underflow to 0), an all-zero
+    # query row, an all-zero key row and an all-zero value column.
+    torch = gpu
+    tokens, heads = 300, 2
+    rng = np.random.default_rng(11)
+    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * 2.0).astype(np.float32)
+    qkv[7, :64] = 0.0
+    qkv[9, heads * 64:heads * 64 + 64] = 0.0
+    qkv[:, 2 * heads * 64 + 5] = 0.0
+    out = _attention_fused_gpu(torch, lib, qkv, tokens, heads, 1)
+    ref = oracle.attention(qkv, tokens, heads, fused=True)
+    assert np.isfinite(out).all()
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    assert np.all(out[:, 5] == 0.0)
+
+
 @pytest.mark.parametrize("rows,cols", [(16 * 1370, 1370), (7, 5477), (3, 64), (5, 9000)])
 def test_softmax_fp32(gpu, lib, oracle, rows, cols):
     torch = gpu
@@ -318,7 +371,14 @@ def test_elementwise_exact(gpu, lib, oracle):
     ok(lib, lib.dav2_hip_add_scaled(ptr(out), ptr(ad), ptr(bd), ptr(gd), m, cols, s))
     assert np.array_equal(host(torch, out)[:m], oracle.add_scaled(a[:m], b[:m], gamma))
     ok(lib, lib.dav2_hip_gelu(ptr(out), ptr(ad), n, s))
-    np.testing.assert_allclose(host(torch, out), oracle.gelu(a), rtol=1e-6, atol=3e-7)
+    assert np.array_equal(host(torch, out).view(np.uint32), oracle.gelu(a).view(np.uint32))
+    # wide sweep through every branch of the exp and erfc evaluation
+    w = np.concatenate([np.linspace(-40, 40, 200001, dtype=np.float32),
+                        (rng.standard_normal(100000) * 10).astype(np.float32),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 13.5, -13.5, 1e4, -1e4], np.float32)])
+    wd, wo = dev(torch, w), empty(torch, w.shape, torch.float32)
+    ok(lib, lib.dav2_hip_gelu(ptr(wo), ptr(wd), w.size, s))
+    assert np.array_equal(host(torch, wo).view(np.uint32), oracle.gelu(w).view(np.uint32))
 
 
 @pytest.mark.parametrize("c,ih,iw,oh,ow", [(256, 19, 19, 37, 37), (256, 148, 148, 296, 296), (128, 296, 296, 518, 518),

@@ -50,10 +50,7 @@ def test_linear_int8(gpu, pkg, lib, oracle, ops, rows, ic, oc, gelu):
     sync(lib, ops)
     ref = oracle.linear_int8(x, q, s, b, gelu=gelu)
     got = host(torch, out)
-    if gelu:
-        np.testing.assert_allclose(got, ref, rtol=1e-6, atol=3e-7)
-    else:
-        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
 def test_linear_int8_validation(gpu, pkg, lib, ops):
