@@ -6,23 +6,30 @@
 // integer, so the result does not depend on summation order and a CPU
 // restatement reproduces it bit for bit:
 //
-//   q*0.125 and k per token row, v per feature column (over the tokens), in
+//   q*0.125 per token row, k per (batch, head) and v per feature column, in
 //   15-bit block floating point: x ~= X * 2^e, |X| <= 16383, X = 128*d1 + d0
 //   with digits d1 in [-128, 127] and d0 in [0, 127] (two int8 planes);
-//   s_ij = fp32(Q_i . K_j * 2^(eq_i + ek_j))        exact dot, one rounding
-//   E_ij = min(rint(exp_cw(s_ij - max_j s_ij) * 2^21), 2^21 - 1)
+//   u_ij = fma(H, 2^14, fp32(R)) with the exact digit sums
+//          H = sum_f d1(q) d1(k) and R = Q_i . K_j - 2^14 H
+//   (the score is u_ij * 2^(eq_i + ek): one exponent per query row)
+//   x_ij = (u_ij - max_j u_ij) * (log2(e) * 2^(eq_i + ek))
+//   E_ij = min(rint(pow2(x_ij) * 2^21), 2^21 - 1)
 //        = 2^14 e2 + 2^7 e1 + e0 (three 7-bit digits)
 //   o_if = ldexp(fp32(sum_j E_ij V_jf) / fp32(sum_j E_ij), ev_f)
+//   pow2: n = rint(x), f = x - n, degree-6 Taylor polynomial of 2^f, * 2^n.
 //
 // Digit products run on v_mfma_i32_16x16x64_i8 (exact int32 sums); the
-// partial sums are recombined in double precision, where they are exact.
+// output sums are recombined in double precision, where they are exact.
 //
-// Kernels: zero the column maxima; pack q/k rows into digit planes and
-// take column maxima of v; pack v into digit planes (key-permuted, see
-// below); attention. Attention: one workgroup = 4 waves = 64 queries of one
-// (batch, head), wave w owns 16 queries. Key blocks of 64 are staged through
-// LDS (double buffered, one barrier per block). Pass 1 computes the row
-// maxima, pass 2 recomputes the same scores and accumulates E V.
+// Kernels: pack (q rows into digit planes, per-block maxima of |k| and of
+// |v| per column), pack k and v (reduce the block maxima, digit planes, v
+// key-permuted as below), attention.
+//
+// Attention: one workgroup = 4 waves = 2 query groups of 16 x 2 key halves.
+// The two waves of a key half share its key blocks of 64, staged through LDS
+// (double buffered, one barrier per block). Pass 1 computes the row maxima,
+// pass 2 recomputes the same scores and accumulates E and E V; the halves
+// combine their maxima and their (exact integer) sums through LDS.
 //
 // The wave computes S^T = K Q^T (keys x queries), so after the score MFMAs
 // lane l holds, for its query l%16, keys 16j + 4g + r of the block (j, r in
@@ -32,6 +39,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "dav2_hip.h"
 
@@ -39,34 +48,42 @@ using namespace dav2k;
 
 namespace {
 
-constexpr uint32_t kBlock = 64;   // keys per LDS block, queries per workgroup
-constexpr int kRow = 80;          // LDS bytes per 64-byte digit row (16 padding)
-constexpr int kPlane = 64 * kRow; // one digit plane of a block in LDS
-constexpr float kE = 2097152.0f;  // 2^21
-constexpr int kEMax = 2097151;
+constexpr uint32_t kBlock = 64;    // keys per LDS block, tokens per pack workgroup
+constexpr int kPlane = 64 * 64;   // one digit plane of a block in LDS (64 rows x 64 B)
+constexpr int kTile = 4 * kPlane;  // K1 | K0 | V1 | V0
+constexpr int kEMax = 2097151;     // 2^21 - 1
+constexpr int kAttnThreads = 256;  // 2 query groups x 2 key halves
+constexpr size_t kAttnLds = 2 * 2 * kTile;  // [key half][buffer] tiles
 
 inline uint32_t padded_tokens(uint32_t tokens) { return (tokens + kBlock - 1u) / kBlock * kBlock; }
 
 // Block position p (0..63) of the value planes holds key perm64(p).
 DAV2_DEV uint32_t perm64(uint32_t p) { return ((p >> 2) & 3u) * 16u + 4u * (p >> 4) + (p & 3u); }
 
+// LDS byte offset of 16-byte chunk c (0..3) of digit row r: chunks are XOR
+// swizzled with bits 2..3 of the row, so the 16 rows one MFMA operand load
+// touches (same logical chunk) fall on 16 distinct 16-byte bank groups.
+DAV2_DEV uint32_t lds_chunk(uint32_t r, uint32_t c) { return r * 64u + ((c ^ (r >> 2)) & 3u) * 16u; }
+
 struct Layout {
-    uint64_t planes_q, planes_k, planes_v;  // byte offsets of the digit planes
-    uint64_t exp_q, exp_k, exp_v, colmax;   // byte offsets of int32/uint32 arrays
+    uint64_t planes_q, planes_k, planes_v;     // byte offsets of the digit planes
+    uint64_t exp_q, exp_k, exp_v, kmax, vmax;  // int32 exponents, fp32 block maxima
     uint64_t bytes;
 };
 
 inline Layout layout_for(uint32_t tokens, uint32_t heads, uint32_t batch) {
     const uint64_t bh = static_cast<uint64_t>(batch) * heads, tp = padded_tokens(tokens);
+    const uint64_t nblk = tp / kBlock;
     Layout l{};
     l.planes_q = 0;
     l.planes_k = l.planes_q + bh * 2 * tp * 64;
     l.planes_v = l.planes_k + bh * 2 * tp * 64;
     l.exp_q = l.planes_v + bh * 2 * 64 * tp;
     l.exp_k = l.exp_q + bh * tp * 4;
-    l.exp_v = l.exp_k + bh * tp * 4;
-    l.colmax = l.exp_v + bh * 64 * 4;
-    l.bytes = l.colmax + bh * 64 * 4;
+    l.exp_v = l.exp_k + bh * 4;
+    l.kmax = l.exp_v + bh * 64 * 4;  // [bh][nblk]
+    l.vmax = l.kmax + bh * nblk * 4;  // [bh][nblk][64]
+    l.bytes = l.vmax + bh * nblk * 64 * 4;
     return l;
 }
 
@@ -78,246 +95,389 @@ DAV2_DEV void digits15(float x, int shift, int8_t& d1, int8_t& d0) {
     d0 = static_cast<int8_t>(X & 127);
 }
 
-__global__ void zero_colmax_kernel(uint32_t* colmax, uint32_t n) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) colmax[i] = 0u;
-}
-
-// One wave per q or k row (lane = feature): 64 tokens x {q, k} per
-// workgroup. Also folds |v| of the workgroup's tokens into colmax.
-__global__ __launch_bounds__(256) void pack_rows_kernel(const float* __restrict__ qkv, int8_t* __restrict__ qd,
-                                                        int8_t* __restrict__ kd, int* __restrict__ qe,
-                                                        int* __restrict__ ke, uint32_t* __restrict__ colmax,
-                                                        uint32_t tokens, uint32_t heads, uint32_t tp) {
-    __shared__ float vmax[4][64];
-    const uint32_t h = blockIdx.y, b = blockIdx.z, bh = b * heads + h;
-    const uint32_t D = heads * 64u;
-    const uint32_t j0 = blockIdx.x * kBlock;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float* base = qkv + static_cast<uint64_t>(b) * tokens * 3u * D + h * 64u + lane;
-    for (int r = wave; r < 128; r += 4) {
-        const bool is_k = r >= 64;
-        const uint32_t t = j0 + (r & 63);
-        float x = 0.0f;
-        if (t < tokens) {
-            x = base[static_cast<uint64_t>(t) * 3u * D + (is_k ? D : 0u)];
-            if (!is_k) x = x * 0.125f;
-        }
-        const float a = wave_max(fabsf(x));
-        int e = 0;
-        int8_t d1 = 0, d0 = 0;
-        if (a != 0.0f) {
-            frexpf(a, &e);
-            digits15(x, 14 - e, d1, d0);
-        }
-        int8_t* planes = is_k ? kd : qd;
-        const uint64_t o = (static_cast<uint64_t>(bh) * 2u * tp + t) * 64u + lane;
-        planes[o + static_cast<uint64_t>(tp) * 64u] = d1;  // plane 1
-        planes[o] = d0;                                    // plane 0
-        if (lane == 0) (is_k ? ke : qe)[static_cast<uint64_t>(bh) * tp + t] = a != 0.0f ? e - 14 : 0;
-    }
-    float m = 0.0f;
-    for (int i = 0; i < 16; ++i) {
-        const uint32_t t = j0 + wave * 16 + i;
-        if (t < tokens) m = fmaxf(m, fabsf(base[static_cast<uint64_t>(t) * 3u * D + 2u * D]));
-    }
-    vmax[wave][lane] = m;
-    __syncthreads();
-    if (wave == 0) {
-        m = fmaxf(fmaxf(vmax[0][lane], vmax[1][lane]), fmaxf(vmax[2][lane], vmax[3][lane]));
-        // |v| >= 0: the IEEE bit patterns order like the values
-        atomicMax(colmax + static_cast<uint64_t>(bh) * 64u + lane, __float_as_uint(m));
-    }
-}
-
-// v of 64 tokens -> two digit planes [64 features][tp], key-permuted.
-__global__ __launch_bounds__(256) void pack_values_kernel(const float* __restrict__ qkv,
-                                                          const uint32_t* __restrict__ colmax,
-                                                          int8_t* __restrict__ vd, int* __restrict__ ve,
-                                                          uint32_t tokens, uint32_t heads, uint32_t tp) {
-    __shared__ float tile[64][65];  // [token][feature]
-    const uint32_t h = blockIdx.y, b = blockIdx.z, bh = b * heads + h;
-    const uint32_t D = heads * 64u;
-    const uint32_t j0 = blockIdx.x * kBlock;
-    const int tid = threadIdx.x;
-    const float* base = qkv + static_cast<uint64_t>(b) * tokens * 3u * D + 2u * D + h * 64u;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int c = tid + it * 256;
-        const uint32_t jr = static_cast<uint32_t>(c) >> 4, f4 = (static_cast<uint32_t>(c) & 15u) * 4u;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (j0 + jr < tokens) v = *reinterpret_cast<const float4*>(base + static_cast<uint64_t>(j0 + jr) * 3u * D + f4);
-        tile[jr][f4 + 0] = v.x;
-        tile[jr][f4 + 1] = v.y;
-        tile[jr][f4 + 2] = v.z;
-        tile[jr][f4 + 3] = v.w;
-    }
-    __syncthreads();
-    const uint32_t f = static_cast<uint32_t>(tid) >> 2, p0 = (static_cast<uint32_t>(tid) & 3u) * 16u;
-    const float a = __uint_as_float(colmax[static_cast<uint64_t>(bh) * 64u + f]);
-    int e = 0;
-    if (a != 0.0f) frexpf(a, &e);
-    int8_t hi[16], lo[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        hi[i] = 0;
-        lo[i] = 0;
-        if (a != 0.0f) digits15(tile[perm64(p0 + i)][f], 14 - e, hi[i], lo[i]);
-    }
-    int8_t* row1 = vd + ((static_cast<uint64_t>(bh) * 2u + 1u) * 64u + f) * tp + j0 + p0;
-    int8_t* row0 = vd + ((static_cast<uint64_t>(bh) * 2u) * 64u + f) * tp + j0 + p0;
+DAV2_DEV void store_digits16(int8_t* plane1, int8_t* plane0, const int8_t d1[16], const int8_t d0[16]) {
     v4i w1, w0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        w1[q] = static_cast<int>(pack4(hi[4 * q], hi[4 * q + 1], hi[4 * q + 2], hi[4 * q + 3]));
-        w0[q] = static_cast<int>(pack4(lo[4 * q], lo[4 * q + 1], lo[4 * q + 2], lo[4 * q + 3]));
+        w1[q] = static_cast<int>(pack4(d1[4 * q], d1[4 * q + 1], d1[4 * q + 2], d1[4 * q + 3]));
+        w0[q] = static_cast<int>(pack4(d0[4 * q], d0[4 * q + 1], d0[4 * q + 2], d0[4 * q + 3]));
     }
-    *reinterpret_cast<v4i*>(row1) = w1;
-    *reinterpret_cast<v4i*>(row0) = w0;
-    if (blockIdx.x == 0 && (tid & 3) == 0) ve[static_cast<uint64_t>(bh) * 64u + f] = a != 0.0f ? e - 14 : 0;
+    *reinterpret_cast<v4i*>(plane1) = w1;
+    *reinterpret_cast<v4i*>(plane0) = w0;
+}
+
+// 64 tokens per workgroup; thread t owns token row t/4, features 16*(t%4)..
+// q*0.125 rows -> digit planes; maxima of |k| and of |v| per column over the
+// block -> kmax[bh][block], vmax[bh][block][64].
+__global__ __launch_bounds__(256) void pack_q_kernel(const float* __restrict__ qkv, int8_t* __restrict__ qd,
+                                                     int* __restrict__ qe, float* __restrict__ kmax,
+                                                     float* __restrict__ vmax, uint32_t tokens, uint32_t heads,
+                                                     uint32_t tp) {
+    __shared__ float vcol[64][65];
+    __shared__ float kpart[4];
+    const uint32_t h = blockIdx.y, b = blockIdx.z, bh = b * heads + h;
+    const uint32_t D = heads * 64u;
+    const uint32_t nblk = tp / kBlock;
+    const int tid = threadIdx.x, row = tid >> 2, c16 = (tid & 3) * 16;
+    const uint32_t t = blockIdx.x * kBlock + row;
+    float q[16], mk = 0.0f;
+    if (t < tokens) {
+        const float* src = qkv + (static_cast<uint64_t>(b) * tokens + t) * 3u * D + h * 64u + c16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 vq = *reinterpret_cast<const float4*>(src + 4 * i);
+            const float4 vk = *reinterpret_cast<const float4*>(src + D + 4 * i);
+            const float4 vv = *reinterpret_cast<const float4*>(src + 2u * D + 4 * i);
+            q[4 * i + 0] = vq.x * 0.125f;
+            q[4 * i + 1] = vq.y * 0.125f;
+            q[4 * i + 2] = vq.z * 0.125f;
+            q[4 * i + 3] = vq.w * 0.125f;
+            mk = fmaxf(mk, fmaxf(fmaxf(fabsf(vk.x), fabsf(vk.y)), fmaxf(fabsf(vk.z), fabsf(vk.w))));
+            vcol[row][c16 + 4 * i + 0] = fabsf(vv.x);
+            vcol[row][c16 + 4 * i + 1] = fabsf(vv.y);
+            vcol[row][c16 + 4 * i + 2] = fabsf(vv.z);
+            vcol[row][c16 + 4 * i + 3] = fabsf(vv.w);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            q[i] = 0.0f;
+            vcol[row][c16 + i] = 0.0f;
+        }
+    }
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a = fmaxf(a, fabsf(q[i]));
+    a = fmaxf(a, __shfl_xor(a, 1, kWave));
+    a = fmaxf(a, __shfl_xor(a, 2, kWave));
+    int e = 0;
+    if (a != 0.0f) frexpf(a, &e);
+    int8_t d1[16], d0[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        d1[i] = 0;
+        d0[i] = 0;
+        if (a != 0.0f) digits15(q[i], 14 - e, d1[i], d0[i]);
+    }
+    int8_t* p0 = qd + (static_cast<uint64_t>(bh) * 2u * tp + t) * 64u + c16;
+    store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
+    if ((tid & 3) == 0) qe[static_cast<uint64_t>(bh) * tp + t] = a != 0.0f ? e - 14 : 0;
+
+    mk = wave_max(mk);
+    if ((tid & 63) == 0) kpart[tid >> 6] = mk;
+    __syncthreads();
+    if (tid == 0) kmax[static_cast<uint64_t>(bh) * nblk + blockIdx.x] = fmaxf(fmaxf(kpart[0], kpart[1]), fmaxf(kpart[2], kpart[3]));
+    if (tid < 64) {
+        float m = 0.0f;
+        for (int r = 0; r < 64; ++r) m = fmaxf(m, vcol[r][tid]);
+        vmax[(static_cast<uint64_t>(bh) * nblk + blockIdx.x) * 64u + tid] = m;
+    }
+}
+
+// k (per-head exponent) and v (per-column exponent) of 64 tokens into digit
+// planes: k row-major [tp][64], v feature-major [64][tp] and key-permuted.
+__global__ __launch_bounds__(256) void pack_kv_kernel(const float* __restrict__ qkv, const float* __restrict__ kmax,
+                                                      const float* __restrict__ vmax, int8_t* __restrict__ kd,
+                                                      int8_t* __restrict__ vd, int* __restrict__ ke,
+                                                      int* __restrict__ ve, uint32_t tokens, uint32_t heads,
+                                                      uint32_t tp) {
+    __shared__ float tile[64][65];  // v [token][feature]
+    __shared__ float kred[4];
+    __shared__ float vred[4][64];
+    const uint32_t h = blockIdx.y, b = blockIdx.z, bh = b * heads + h;
+    const uint32_t D = heads * 64u;
+    const uint32_t nblk = tp / kBlock;
+    const uint32_t j0 = blockIdx.x * kBlock;
+    const int tid = threadIdx.x, hi4 = tid >> 2, c16 = (tid & 3) * 16;
+
+    // Head maximum of |k| and column maxima of |v| from the block maxima
+    // (wave w folds blocks w, w + 4, ...; lane = feature).
+    float mk = 0.0f, mv = 0.0f;
+    for (uint32_t i = static_cast<uint32_t>(tid); i < nblk; i += 256u) mk = fmaxf(mk, kmax[static_cast<uint64_t>(bh) * nblk + i]);
+    for (uint32_t i = static_cast<uint32_t>(tid >> 6); i < nblk; i += 4u)
+        mv = fmaxf(mv, vmax[(static_cast<uint64_t>(bh) * nblk + i) * 64u + (tid & 63)]);
+    mk = wave_max(mk);
+    if ((tid & 63) == 0) kred[tid >> 6] = mk;
+    vred[tid >> 6][tid & 63] = mv;
+
+    const uint32_t t = j0 + hi4;  // k: token row hi4, features c16..c16+15
+    float k[16];
+    const float* src = qkv + (static_cast<uint64_t>(b) * tokens + t) * 3u * D + D + h * 64u + c16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float4 vk = make_float4(0.f, 0.f, 0.f, 0.f), vv = vk;
+        if (t < tokens) {
+            vk = *reinterpret_cast<const float4*>(src + 4 * i);
+            vv = *reinterpret_cast<const float4*>(src + D + 4 * i);
+        }
+        k[4 * i + 0] = vk.x;
+        k[4 * i + 1] = vk.y;
+        k[4 * i + 2] = vk.z;
+        k[4 * i + 3] = vk.w;
+        tile[hi4][c16 + 4 * i + 0] = vv.x;
+        tile[hi4][c16 + 4 * i + 1] = vv.y;
+        tile[hi4][c16 + 4 * i + 2] = vv.z;
+        tile[hi4][c16 + 4 * i + 3] = vv.w;
+    }
+    __syncthreads();
+    mv = fmaxf(fmaxf(vred[0][hi4], vred[1][hi4]), fmaxf(vred[2][hi4], vred[3][hi4]));
+    int8_t d1[16], d0[16];
+    {
+        const float a = fmaxf(fmaxf(kred[0], kred[1]), fmaxf(kred[2], kred[3]));
+        int e = 0;
+        if (a != 0.0f) frexpf(a, &e);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            d1[i] = 0;
+            d0[i] = 0;
+            if (a != 0.0f) digits15(k[i], 14 - e, d1[i], d0[i]);
+        }
+        int8_t* p0 = kd + ((static_cast<uint64_t>(bh) * 2u) * tp + t) * 64u + c16;
+        store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
+        if (blockIdx.x == 0 && tid == 0) ke[bh] = a != 0.0f ? e - 14 : 0;
+    }
+    {  // v: feature hi4, block positions c16..c16+15
+        int e = 0;
+        if (mv != 0.0f) frexpf(mv, &e);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            d1[i] = 0;
+            d0[i] = 0;
+            if (mv != 0.0f) digits15(tile[perm64(c16 + i)][hi4], 14 - e, d1[i], d0[i]);
+        }
+        int8_t* p0 = vd + ((static_cast<uint64_t>(bh) * 2u) * 64u + hi4) * tp + j0 + c16;
+        store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
+        if (blockIdx.x == 0 && (tid & 3) == 0) ve[static_cast<uint64_t>(bh) * 64u + hi4] = mv != 0.0f ? e - 14 : 0;
+    }
 }
 
 DAV2_DEV v4i mfma8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 
-__global__ __launch_bounds__(256) void attention_exact_kernel(const int8_t* __restrict__ qd,
-                                                              const int8_t* __restrict__ kd,
-                                                              const int8_t* __restrict__ vd,
-                                                              const int* __restrict__ qe,
-                                                              const int* __restrict__ ke,
-                                                              const int* __restrict__ ve,
-                                                              float* __restrict__ out, uint32_t tokens,
-                                                              uint32_t heads, uint32_t tp) {
-    // [buffer][K1 | K0 | V1 | V0] digit rows, then [buffer][64] key exponents
-    __shared__ __attribute__((aligned(16))) int8_t lds[2][4 * kPlane];
-    __shared__ int kexp[2][64];
+// E = min(rint(pow2(x) * 2^21), 2^21 - 1) for x <= 0 (or -inf / NaN: 0).
+// pow2(x) = 2^n * p(x - n), n = rint(x), p the degree-6 Taylor polynomial of
+// 2^f (coefficients ln2^k / k!); x below -100 gives E = 0. The final
+// rounding adds 2^23 (ties to even) and reads the integer from the bits.
+DAV2_DEV int numerator21(float x) {
+    const float xc = fmaxf(x, -100.0f);
+    const float n = __builtin_rintf(xc);
+    const float f = xc - n;
+    float p = 1.54035304e-4f;
+    p = fmaf(p, f, 1.33335581e-3f);
+    p = fmaf(p, f, 9.61812911e-3f);
+    p = fmaf(p, f, 5.55041087e-2f);
+    p = fmaf(p, f, 2.40226507e-1f);
+    p = fmaf(p, f, 6.93147181e-1f);
+    p = fmaf(p, f, 1.0f);
+    const float v = ldexpf(p, static_cast<int>(n) + 21);  // < 2^21 + 1, normal
+    const float r = v + 8388608.0f;
+    return min(static_cast<int>(__float_as_uint(r) - 0x4B000000u), kEMax);
+}
+
+// Wave w: query group w & 1 (16 queries), key half w >> 1.
+__global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
+    const int8_t* __restrict__ qd, const int8_t* __restrict__ kd, const int8_t* __restrict__ vd,
+    const int* __restrict__ qe, const int* __restrict__ ke, const int* __restrict__ ve, float* __restrict__ out,
+    uint32_t tokens, uint32_t heads, uint32_t tp) {
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];  // [half][buffer][kTile]
     const uint32_t h = blockIdx.y, b = blockIdx.z, bh = b * heads + h;
     const uint32_t D = heads * 64u;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave-uniform values kept in scalar registers (uniform branches)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int group = wave & 1, half = wave >> 1;
+    const int htid = tid & 127;  // thread index within the key half
     const int col = lane & 15, g = lane >> 4;
-    const uint32_t q0 = blockIdx.x * kBlock + wave * 16u;
+    const uint32_t q0 = blockIdx.x * 32u + group * 16u;
     const uint64_t plane_qk = static_cast<uint64_t>(tp) * 64u;
+    const uint32_t blocks = tp / kBlock;
+    const uint32_t first_half = (blocks + 1u) / 2u;  // blocks of half 0; half 1 has the rest
+    const uint32_t kb0 = half ? first_half : 0u;
+    const uint32_t nkb = half ? blocks - first_half : first_half;
+    int8_t* tiles = lds + half * 2 * kTile;
 
     const int8_t* kbase = kd + static_cast<uint64_t>(bh) * 2u * plane_qk;
     const int8_t* vbase = vd + static_cast<uint64_t>(bh) * 2u * plane_qk;
-    const int* kebase = ke + static_cast<uint64_t>(bh) * tp;
 
     // B operand of S^T = K Q^T: lane holds features 16g..16g+15 of query col.
     const int8_t* qrow = qd + static_cast<uint64_t>(bh) * 2u * plane_qk + static_cast<uint64_t>(q0 + col) * 64u + g * 16;
     const v4i q1 = *reinterpret_cast<const v4i*>(qrow + plane_qk);
     const v4i q0v = *reinterpret_cast<const v4i*>(qrow);
-    const int qexp = qe[static_cast<uint64_t>(bh) * tp + q0 + col];
+    // log2(e) * 2^(eq + ek): turns u - max u into the exponent of 2
+    const float row_scale = ldexpf(1.44269504f, qe[static_cast<uint64_t>(bh) * tp + q0 + col] + ke[bh]);
 
-    // Staging: K planes (2 x 64 rows x 64 B) and V planes, 16-byte chunks:
-    // chunk c < 512: plane c >> 8, row (c >> 2) & 63, 16-byte column c & 3.
-    v4i stage[4];
-    int kstage = 0;
+    // Staging of one key half: K planes (2 x 64 rows x 64 B) and V planes in
+    // 16-byte chunks c < 512: plane c >> 8, row (c >> 2) & 63, column c & 3.
+    v4i stage[8];
     auto fetch = [&](uint32_t kb, bool values) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t c = static_cast<uint32_t>(tid) + 256u * i;
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = static_cast<uint32_t>(htid) + 128u * i;
             const uint32_t plane = c >> 8, row = (c >> 2) & 63u, c16 = (c & 3u) * 16u;
             stage[i] = *reinterpret_cast<const v4i*>(kbase + plane * plane_qk +
                                                      (static_cast<uint64_t>(kb) * kBlock + row) * 64u + c16);
             if (values)
-                stage[2 + i] = *reinterpret_cast<const v4i*>(vbase + (plane * 64u + row) * static_cast<uint64_t>(tp) +
-                                                             kb * kBlock + c16);
+                stage[4 + i] = *reinterpret_cast<const v4i*>(
+                    vbase + (plane * 64u + row) * static_cast<uint64_t>(tp) + kb * kBlock + c16);
         }
-        if (tid < 64) kstage = kebase[kb * kBlock + tid];
     };
     auto store = [&](int buf, bool values) {
+        int8_t* t = tiles + buf * kTile;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t c = static_cast<uint32_t>(tid) + 256u * i;
-            const uint32_t plane = c >> 8, row = (c >> 2) & 63u, c16 = (c & 3u) * 16u;
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = static_cast<uint32_t>(htid) + 128u * i;
+            const uint32_t plane = c >> 8, row = (c >> 2) & 63u;
             // LDS planes: K1 = 0, K0 = 1, V1 = 2, V0 = 3 (global plane 1 is the high digit)
-            *reinterpret_cast<v4i*>(&lds[buf][(1u - plane) * kPlane + row * kRow + c16]) = stage[i];
-            if (values) *reinterpret_cast<v4i*>(&lds[buf][(3u - plane) * kPlane + row * kRow + c16]) = stage[2 + i];
+            const uint32_t at = lds_chunk(row, c & 3u);
+            *reinterpret_cast<v4i*>(t + (1u - plane) * kPlane + at) = stage[i];
+            if (values) *reinterpret_cast<v4i*>(t + (3u - plane) * kPlane + at) = stage[4 + i];
         }
-        if (tid < 64) kexp[buf][tid] = kstage;
     };
-    // Scores of sub-block j for this lane: keys 16j + 4g + r, query col.
-    auto scores = [&](int buf, int j, uint32_t kb, float s[4]) {
-        const int8_t* k1 = &lds[buf][0 * kPlane + (j * 16 + col) * kRow + g * 16];
-        const int8_t* k0 = &lds[buf][1 * kPlane + (j * 16 + col) * kRow + g * 16];
-        const v4i a1 = *reinterpret_cast<const v4i*>(k1);
-        const v4i a0 = *reinterpret_cast<const v4i*>(k0);
+    // Unscaled scores of the block for this lane: u[j][r] = key 16j + 4g + r,
+    // query col; TAIL masks keys >= tokens. All MFMAs are issued first.
+    auto block_scores = [&](const int8_t* t, uint32_t kb, auto TAIL, float s[4][4]) {
+        v4i hi[4], mid[4], lo[4];
         const v4i zero = {0, 0, 0, 0};
-        const v4i hi = mfma8(a1, q1, zero);
-        const v4i mid = mfma8(a0, q1, mfma8(a1, q0v, zero));
-        const v4i lo = mfma8(a0, q0v, zero);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t key = kb * kBlock + j * 16 + 4 * g + r;
-            // exact: |hi| <= 2^20, |mid| <= 2^21, |lo| <= 2^20
-            const double dot = (static_cast<double>(hi[r]) * 16384.0 + static_cast<double>(mid[r]) * 128.0) +
-                               static_cast<double>(lo[r]);
-            const float v = static_cast<float>(ldexp(dot, qexp + kexp[buf][j * 16 + 4 * g + r]));
-            s[r] = key < tokens ? v : -INFINITY;
-        }
-    };
-
-    const uint32_t blocks = tp / kBlock;
-    // Pass 1: row maxima.
-    float m = -INFINITY;
-    fetch(0, false);
-    store(0, false);
-    __syncthreads();
-    for (uint32_t kb = 0; kb < blocks; ++kb) {
-        const int buf = static_cast<int>(kb & 1u);
-        if (kb + 1 < blocks) fetch(kb + 1, false);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            float s[4];
-            scores(buf, j, kb, s);
-            m = fmaxf(fmaxf(m, fmaxf(s[0], s[1])), fmaxf(s[2], s[3]));
+            const uint32_t at = lds_chunk(j * 16 + col, g);
+            const v4i a1 = *reinterpret_cast<const v4i*>(t + 0 * kPlane + at);
+            const v4i a0 = *reinterpret_cast<const v4i*>(t + 1 * kPlane + at);
+            hi[j] = mfma8(a1, q1, zero);
+            mid[j] = mfma8(a1, q0v, zero);
+            lo[j] = mfma8(a0, q0v, zero);
+            mid[j] = mfma8(a0, q1, mid[j]);
         }
-        if (kb + 1 < blocks) store(buf ^ 1, false);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // |128 mid + lo| < 2^29 (exact in int32); hi * 2^14 is exact in fp32
+                const int rest = mid[j][r] * 128 + lo[j][r];
+                float v = fmaf(static_cast<float>(hi[j][r]), 16384.0f, static_cast<float>(rest));
+                if (decltype(TAIL)::value && kb * kBlock + j * 16 + 4 * g + r >= tokens) v = -INFINITY;
+                s[j][r] = v;
+            }
+    };
+
+    const bool ragged = tokens != tp;
+    // Pass 1: row maxima of u over this key half.
+    float m = -INFINITY;
+    if (nkb > 0) {
+        fetch(kb0, false);
+        store(0, false);
+    }
+    __syncthreads();
+    for (uint32_t it = 0; it < first_half; ++it) {
+        const int buf = static_cast<int>(it & 1u);
+        const uint32_t kb = kb0 + it;
+        const bool have = it < nkb;
+        if (it + 1 < nkb) fetch(kb + 1, false);
+        if (have) {
+            const int8_t* t = tiles + buf * kTile;
+            float s[4][4];
+            if (ragged && kb + 1 == blocks)
+                block_scores(t, kb, std::true_type{}, s);
+            else
+                block_scores(t, kb, std::false_type{}, s);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = fmaxf(fmaxf(m, fmaxf(s[j][0], s[j][1])), fmaxf(s[j][2], s[j][3]));
+        }
+        if (it + 1 < nkb) store(buf ^ 1, false);
         __syncthreads();
     }
     m = fmaxf(m, __shfl_xor(m, 16, kWave));
     m = fmaxf(m, __shfl_xor(m, 32, kWave));
+    // [half][group][query] maxima in the buffer-1 tile of key half 1, which
+    // pass 2 first writes after its opening barrier
+    float* half_max = reinterpret_cast<float*>(lds + 3 * kTile);
+    if (g == 0) half_max[(half * 2 + group) * 16 + col] = m;
+    __syncthreads();
+    m = fmaxf(half_max[group * 16 + col], half_max[(2 + group) * 16 + col]);
 
-    // Pass 2: E = 21-bit softmax numerators, sum_j E, sum_j E V.
+    // Pass 2: E = 21-bit softmax numerators, sum_j E, sum_j E V over this half.
     v4i c0[4], c7[4], c14[4], c21[4];
 #pragma unroll
     for (int fb = 0; fb < 4; ++fb) c0[fb] = c7[fb] = c14[fb] = c21[fb] = v4i{0, 0, 0, 0};
     uint64_t lsum = 0;
-    fetch(0, true);
-    store(0, true);
+    if (nkb > 0) {
+        fetch(kb0, true);
+        store(0, true);
+    }
     __syncthreads();
-    for (uint32_t kb = 0; kb < blocks; ++kb) {
-        const int buf = static_cast<int>(kb & 1u);
-        if (kb + 1 < blocks) fetch(kb + 1, true);
-        v4i e0, e1, e2;
+    for (uint32_t it = 0; it < first_half; ++it) {
+        const int buf = static_cast<int>(it & 1u);
+        const uint32_t kb = kb0 + it;
+        const bool have = it < nkb;
+        if (it + 1 < nkb) fetch(kb + 1, true);
+        if (have) {
+            const int8_t* t = tiles + buf * kTile;
+            float s[4][4];
+            if (ragged && kb + 1 == blocks)
+                block_scores(t, kb, std::true_type{}, s);
+            else
+                block_scores(t, kb, std::false_type{}, s);
+            v4i e0, e1, e2;
+            uint32_t lblock = 0;  // <= 16 * 2^21
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float s[4];
-            scores(buf, j, kb, s);
-            int d0[4], d1[4], d2[4];
+            for (int j = 0; j < 4; ++j) {
+                int E[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    E[r] = numerator21((s[j][r] - m) * row_scale);
+                    lblock += static_cast<uint32_t>(E[r]);
+                }
+                e0[j] = (E[0] & 127) | ((E[1] & 127) << 8) | ((E[2] & 127) << 16) | ((E[3] & 127) << 24);
+                e1[j] = ((E[0] >> 7) & 127) | (((E[1] >> 7) & 127) << 8) | (((E[2] >> 7) & 127) << 16) |
+                        (((E[3] >> 7) & 127) << 24);
+                e2[j] = (E[0] >> 14) | ((E[1] >> 14) << 8) | ((E[2] >> 14) << 16) | ((E[3] >> 14) << 24);
+            }
+            lsum += lblock;
+#pragma unroll
+            for (int fb = 0; fb < 4; ++fb) {
+                const uint32_t at = lds_chunk(fb * 16 + col, g);
+                const v4i v1 = *reinterpret_cast<const v4i*>(t + 2 * kPlane + at);
+                const v4i v0 = *reinterpret_cast<const v4i*>(t + 3 * kPlane + at);
+                c0[fb] = mfma8(v0, e0, c0[fb]);
+                c7[fb] = mfma8(v1, e0, mfma8(v0, e1, c7[fb]));
+                c14[fb] = mfma8(v1, e1, mfma8(v0, e2, c14[fb]));
+                c21[fb] = mfma8(v1, e2, c21[fb]);
+            }
+        }
+        if (it + 1 < nkb) store(buf ^ 1, true);
+        __syncthreads();
+    }
+
+    // Half 1 hands its integer sums to half 0 (exact adds): [group][lane][66].
+    int* red = reinterpret_cast<int*>(lds);
+    if (half == 1) {
+        int* mine = red + (group * 64 + lane) * 66;
+#pragma unroll
+        for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = exp_cw(s[r] - m) * kE;
-                const int E = min(static_cast<int>(__builtin_rintf(e)), kEMax);
-                lsum += static_cast<uint32_t>(E);
-                d0[r] = E & 127;
-                d1[r] = (E >> 7) & 127;
-                d2[r] = E >> 14;
+                mine[fb * 16 + r] = c0[fb][r];
+                mine[fb * 16 + 4 + r] = c7[fb][r];
+                mine[fb * 16 + 8 + r] = c14[fb][r];
+                mine[fb * 16 + 12 + r] = c21[fb][r];
             }
-            e0[j] = static_cast<int>(pack4(d0[0], d0[1], d0[2], d0[3]));
-            e1[j] = static_cast<int>(pack4(d1[0], d1[1], d1[2], d1[3]));
-            e2[j] = static_cast<int>(pack4(d2[0], d2[1], d2[2], d2[3]));
-        }
+        mine[64] = static_cast<int>(static_cast<uint32_t>(lsum));
+        mine[65] = static_cast<int>(static_cast<uint32_t>(lsum >> 32));
+    }
+    __syncthreads();
+    if (half == 1) return;
+    {
+        const int* other = red + (group * 64 + lane) * 66;
 #pragma unroll
-        for (int fb = 0; fb < 4; ++fb) {
-            const v4i v1 = *reinterpret_cast<const v4i*>(&lds[buf][2 * kPlane + (fb * 16 + col) * kRow + g * 16]);
-            const v4i v0 = *reinterpret_cast<const v4i*>(&lds[buf][3 * kPlane + (fb * 16 + col) * kRow + g * 16]);
-            c0[fb] = mfma8(v0, e0, c0[fb]);
-            c7[fb] = mfma8(v1, e0, mfma8(v0, e1, c7[fb]));
-            c14[fb] = mfma8(v1, e1, mfma8(v0, e2, c14[fb]));
-            c21[fb] = mfma8(v1, e2, c21[fb]);
-        }
-        if (kb + 1 < blocks) store(buf ^ 1, true);
-        __syncthreads();
+        for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                c0[fb][r] += other[fb * 16 + r];
+                c7[fb][r] += other[fb * 16 + 4 + r];
+                c14[fb][r] += other[fb * 16 + 8 + r];
+                c21[fb][r] += other[fb * 16 + 12 + r];
+            }
+        lsum += static_cast<uint64_t>(static_cast<uint32_t>(other[64])) |
+                (static_cast<uint64_t>(static_cast<uint32_t>(other[65])) << 32);
     }
     double l = static_cast<double>(lsum);
     l = l + __shfl_xor(l, 16, kWave);
@@ -359,6 +519,10 @@ DAV2_API int dav2_hip_attention_fused(float* out, const float* qkv, uint32_t tok
         return hipErrorInvalidValue;
     const Layout l = layout_for(tokens, heads, batch);
     if (scratch_bytes < l.bytes) return hipErrorInvalidValue;
+    static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_exact_kernel),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         static_cast<int>(kAttnLds));
+    if (lds_ok != hipSuccess) return lds_ok;
     const uint32_t tp = padded_tokens(tokens);
     uint8_t* base = static_cast<uint8_t*>(scratch);
     int8_t* qd = reinterpret_cast<int8_t*>(base + l.planes_q);
@@ -367,14 +531,14 @@ DAV2_API int dav2_hip_attention_fused(float* out, const float* qkv, uint32_t tok
     int* qe = reinterpret_cast<int*>(base + l.exp_q);
     int* ke = reinterpret_cast<int*>(base + l.exp_k);
     int* ve = reinterpret_cast<int*>(base + l.exp_v);
-    uint32_t* colmax = reinterpret_cast<uint32_t*>(base + l.colmax);
+    float* kmax = reinterpret_cast<float*>(base + l.kmax);
+    float* vmax = reinterpret_cast<float*>(base + l.vmax);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint32_t ncol = batch * heads * 64u;
     const dim3 grid(tp / kBlock, heads, batch);
-    hipLaunchKernelGGL(zero_colmax_kernel, dim3(ceil_div(ncol, 256)), dim3(256), 0, s, colmax, ncol);
-    hipLaunchKernelGGL(pack_rows_kernel, grid, dim3(256), 0, s, qkv, qd, kd, qe, ke, colmax, tokens, heads, tp);
-    hipLaunchKernelGGL(pack_values_kernel, grid, dim3(256), 0, s, qkv, colmax, vd, ve, tokens, heads, tp);
-    hipLaunchKernelGGL(attention_exact_kernel, grid, dim3(256), 0, s, qd, kd, vd, qe, ke, ve, out, tokens, heads, tp);
+    hipLaunchKernelGGL(pack_q_kernel, grid, dim3(256), 0, s, qkv, qd, qe, kmax, vmax, tokens, heads, tp);
+    hipLaunchKernelGGL(pack_kv_kernel, grid, dim3(256), 0, s, qkv, kmax, vmax, kd, vd, ke, ve, tokens, heads, tp);
+    hipLaunchKernelGGL(attention_exact_kernel, dim3(tp / 32u, heads, batch), dim3(kAttnThreads), kAttnLds, s, qd,
+                       kd, vd, qe, ke, ve, out, tokens, heads, tp);
     return hipGetLastError();
 }
 

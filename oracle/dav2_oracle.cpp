@@ -472,10 +472,32 @@ void block_fixed15(const float* x, size_t n, size_t stride, int32_t* X, int* exp
     *exponent = e - 14;
 }
 
-// Integer-exact attention (the int8-mode kernel): q*0.125 and k in 15-bit
-// block floating point per token row, v per feature column over the tokens.
-//   s_ij = fp32(Q_i . K_j * 2^(eq_i + ek_j))         (exact dot, one rounding)
-//   E_ij = min(rint(exp_cw(s_ij - max_j s_ij) * 2^21), 2^21 - 1)
+// 2^x scaled to 21 bits: E = min(rint(2^n p(x - n) * 2^21), 2^21 - 1) with
+// n = rint(max(x, -100)), p the degree-6 Taylor polynomial of 2^f
+// (coefficients ln2^k / k!) evaluated by Horner with fused multiply-adds.
+float numerator21(float x) {
+    const float xc = std::fmax(x, -100.0f);
+    const float n = std::nearbyint(xc);
+    const float f = xc - n;
+    float p = 1.54035304e-4f;
+    p = std::fmaf(p, f, 1.33335581e-3f);
+    p = std::fmaf(p, f, 9.61812911e-3f);
+    p = std::fmaf(p, f, 5.55041087e-2f);
+    p = std::fmaf(p, f, 2.40226507e-1f);
+    p = std::fmaf(p, f, 6.93147181e-1f);
+    p = std::fmaf(p, f, 1.0f);
+    const float v = std::ldexp(p, static_cast<int>(n) + 21);
+    return std::min(std::nearbyint(v), 2097151.0f);
+}
+
+// Integer-exact attention (the int8-mode kernel): q*0.125 in 15-bit block
+// floating point per token row, k per head (one exponent over all tokens),
+// v per feature column over the tokens; X = 128 d1 + d0 (d1 in [-128, 127],
+// d0 in [0, 127]).
+//   H_ij = sum_f d1(Q_if) d1(K_jf),  R_ij = Q_i . K_j - 2^14 H_ij  (exact)
+//   u_ij = fmaf(fp32(H), 2^14, fp32(R))      (score = u_ij * 2^(eq_i + ek))
+//   x_ij = (u_ij - max_j u_ij) * ldexp(log2(e), eq_i + ek)
+//   E_ij = numerator21(x_ij)
 //   o_if = ldexp(fp32(sum_j E_ij V_jf) / fp32(sum_j E_ij), ev_f)
 // Every sum is an exact integer, so no result depends on summation order.
 void attention_exact(const float* qkv, uint32_t tokens, uint32_t heads, float* out,
@@ -484,43 +506,58 @@ void attention_exact(const float* qkv, uint32_t tokens, uint32_t heads, float* o
     const size_t T = tokens;
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t h = 0; h < heads; ++h) {
-        std::vector<double> qd(T * 64), kd(T * 64), vd(T * 64);
-        std::vector<int> qe(T), ke(T), ve(64);
-        std::vector<int32_t> X(std::max<size_t>(T, 64));
-        std::vector<float> row(64);
+        std::vector<double> qd(T * 64), kd(T * 64), vd(T * 64), qh(T * 64), kh(T * 64);
+        std::vector<int> qe(T), ve(64);
+        int ke = 0;
+        std::vector<int32_t> X(std::max<size_t>(T * 64, 64));
+        std::vector<float> row(64), kall(T * 64);
         for (size_t t = 0; t < T; ++t) {
             const float* q = qkv + t * D * 3 + h * 64;
             for (int f = 0; f < 64; ++f) row[f] = q[f] * 0.125f;
             block_fixed15(row.data(), 64, 1, X.data(), &qe[t]);
-            for (int f = 0; f < 64; ++f) qd[t * 64 + f] = X[f];
-            block_fixed15(q + D, 64, 1, X.data(), &ke[t]);
-            for (int f = 0; f < 64; ++f) kd[t * 64 + f] = X[f];
+            for (int f = 0; f < 64; ++f) {
+                qd[t * 64 + f] = X[f];
+                qh[t * 64 + f] = X[f] >> 7;  // high digit (arithmetic shift)
+            }
+            for (int f = 0; f < 64; ++f) kall[t * 64 + f] = q[D + f];
+        }
+        block_fixed15(kall.data(), T * 64, 1, X.data(), &ke);
+        for (size_t i = 0; i < T * 64; ++i) {
+            kd[i] = X[i];
+            kh[i] = X[i] >> 7;
         }
         for (int f = 0; f < 64; ++f) {
             block_fixed15(qkv + 2 * D + h * 64 + f, T, D * 3, X.data(), &ve[f]);
             for (size_t t = 0; t < T; ++t) vd[t * 64 + f] = X[t];
         }
-        std::vector<float> s(T);
+        std::vector<float> u(T);
         std::vector<double> E(T);
         for (size_t i = 0; i < T; ++i) {
             const double* qi = &qd[i * 64];
+            const double* qhi = &qh[i * 64];
             float maximum = -std::numeric_limits<float>::infinity();
             for (size_t j = 0; j < T; ++j) {
                 // products < 2^28, sums < 2^34: every double operation is exact
                 const double* kj = &kd[j * 64];
-                __m256d acc = _mm256_setzero_pd();
-                for (int f = 0; f < 64; f += 4)
+                const double* khj = &kh[j * 64];
+                __m256d acc = _mm256_setzero_pd(), acch = _mm256_setzero_pd();
+                for (int f = 0; f < 64; f += 4) {
                     acc = _mm256_fmadd_pd(_mm256_loadu_pd(qi + f), _mm256_loadu_pd(kj + f), acc);
-                alignas(32) double lanes[4];
+                    acch = _mm256_fmadd_pd(_mm256_loadu_pd(qhi + f), _mm256_loadu_pd(khj + f), acch);
+                }
+                alignas(32) double lanes[4], lanesh[4];
                 _mm256_store_pd(lanes, acc);
+                _mm256_store_pd(lanesh, acch);
                 const double dot = (lanes[0] + lanes[1]) + (lanes[2] + lanes[3]);
-                s[j] = static_cast<float>(std::ldexp(dot, qe[i] + ke[j]));
-                maximum = std::max(maximum, s[j]);
+                const double hi = (lanesh[0] + lanesh[1]) + (lanesh[2] + lanesh[3]);
+                const int32_t rest = static_cast<int32_t>(dot - hi * 16384.0);
+                u[j] = std::fmaf(static_cast<float>(hi), 16384.0f, static_cast<float>(rest));
+                maximum = std::max(maximum, u[j]);
             }
+            const float row_scale = std::ldexp(1.44269504f, qe[i] + ke);
             double L = 0.0;
             for (size_t j = 0; j < T; ++j) {
-                const float e = exp_cw(s[j] - maximum) * 2097152.0f;
-                E[j] = std::min(std::nearbyint(e), 2097151.0f);
+                E[j] = numerator21((u[j] - maximum) * row_scale);
                 L += E[j];
             }
             // E < 2^21, |V| < 2^14, T < 2^17: sums stay below 2^52 (exact)

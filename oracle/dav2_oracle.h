@@ -79,8 +79,8 @@ void orc_softmax_rows(const float* input, uint64_t rows, uint32_t columns,
  *         (bmm_score_fp16.glsl, softmax_lastdim_half.glsl, bmm_value_fp16.glsl)
  *         with exact products accumulated in fp32.
  * mode 2: integer-exact (the int8-mode kernel): 15-bit block floating point
- *         q*0.125, k (per token) and v (per feature), exact integer dot
- *         products, one rounding per score, 21-bit softmax numerators.
+ *         q*0.125 (per token), k (per head) and v (per feature), exact
+ *         integer dot products, 21-bit softmax numerators.
  * probabilities (optional) receives [H][T][T]. */
 void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads,
                           int mode, float* out, float* probabilities);
