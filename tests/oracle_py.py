@@ -23,6 +23,7 @@ _PROTO = {
     "orc_linear_epilogue": (None, [vp, vp, vp, vp, u32, u32, u32, u32, C.c_int, vp]),
     "orc_linear_int8": (None, [vp, vp, vp, vp, u32, u32, u32, C.c_int, vp]),
     "orc_gelu": (None, [vp, u64, vp]),
+    "orc_exp": (None, [vp, u64, vp]),
     "orc_layer_norm": (None, [vp, vp, vp, u32, u32, f32, vp]),
     "orc_add_scaled": (None, [vp, vp, vp, u64, u32, vp]),
     "orc_add": (None, [vp, vp, u64, vp]),
@@ -141,6 +142,12 @@ class Oracle:
         self.lib.orc_gelu(x.ctypes.data, x.size, out.ctypes.data)
         return out
 
+    def exp(self, x):
+        x = _f32(x)
+        out = np.empty_like(x)
+        self.lib.orc_exp(x.ctypes.data, x.size, out.ctypes.data)
+        return out
+
     def layer_norm(self, x, w, b, eps=1e-6):
         x, w, b = _f32(x), _f32(w), _f32(b)
         out = np.empty_like(x)
@@ -176,7 +183,7 @@ class Oracle:
     def attention(self, qkv, tokens: int, heads: int, fp16: bool = False, probabilities: bool = False,
                   fused: bool = False):
         """fp16=False: fp32 path; fp16=True: materialised binary16 scores;
-        fused=True: binary16 operands with fp32 scores (the int8 default)."""
+        fused=True: the integer-exact kernel of int8 mode."""
         qkv = _f32(qkv)
         out = np.empty((tokens, heads * 64), np.float32)
         p = np.empty((heads, tokens, tokens), np.float32) if probabilities else None
