@@ -129,6 +129,17 @@ def main() -> int:
         elapsed = time.perf_counter() - t0
         print(f"bench: {args.steps} steps in {elapsed:.3f} s", file=sys.stderr, flush=True)
 
+        # The host-buffer entry (dav2_infer_tensor_f32): PCIe copies included.
+        host_rate = None
+        if args.batch == 1:
+            x_host = fmt.imagenet_input(args.size, args.size, SEED + 3)[0]
+            ctx.infer(x_host, args.size, args.size)
+            h0 = time.perf_counter()
+            host_steps = min(args.steps, 10)
+            for _ in range(host_steps):
+                ctx.infer(x_host, args.size, args.size)
+            host_rate = host_steps / (time.perf_counter() - h0)
+
         # Second pass with per-launch HIP events for the kernel rooflines.
         ctx.profile(True)
         torch.cuda.synchronize()
@@ -198,6 +209,7 @@ def main() -> int:
                      "traffic": traffic},
         "kernels": {k: kernels[k] for k in list(kernels)[:8]},
         "profiled_ms_per_step": 1e3 * profiled_elapsed / args.steps,
+        "host_entry_images_per_s": host_rate,
         "depth_finite": bool(np.isfinite(depth).all()),
         "cpu_baseline": cpu,
     }
