@@ -10,9 +10,13 @@
 // along output pixels and their stores coalesce.
 //
 // Tiling: a workgroup owns a BM x BN output tile, its waves a (BM/WAVES_M) x
-// (BN/WAVES_N) sub-tile of 16x16 MFMA blocks. Each 64-byte K step is staged
-// global -> VGPR -> LDS, double-buffered so the loads of step s+1 overlap the
-// MFMAs of step s, with one workgroup barrier per step.
+// (BN/WAVES_N) sub-tile of 16x16 MFMA blocks. K advances in stages of BK
+// bytes copied straight from global memory into an LDS ring of STAGES slots
+// (global_load_lds_dwordx4, no register staging), XOR-swizzled so the MFMA
+// operand reads are free of bank conflicts; the copies of the next
+// STAGES - 1 stages are in flight while a stage is multiplied, with one
+// workgroup barrier per stage. Workgroups are remapped so that each XCD
+// works on one contiguous band of tiles.
 
 #include "common.h"
 #include "dav2_hip.h"
@@ -21,8 +25,6 @@ using namespace dav2k;
 
 namespace {
 
-constexpr int kBK = 64;              // K bytes per pipeline step
-constexpr int kLdsStride = kBK + 16;  // padded LDS row (bytes): spreads 16 rows over all banks
 
 struct GemmParams {
     const int8_t* p;
@@ -94,62 +96,101 @@ DAV2_DEV void store_one(const GemmParams& g, uint32_t prow, uint32_t qcol, int32
     }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI>
+// Tile index of this workgroup. Workgroups are dealt to the 8 XCDs round
+// robin (id % 8); remap so that each XCD owns one contiguous run of tiles,
+// ordered along M first: the tiles of one weight-column band then share that
+// XCD's L2.
+DAV2_DEV void tile_of(uint32_t& tm, uint32_t& tn) {
+    const uint32_t mt = gridDim.x, total = gridDim.x * gridDim.y;
+    const uint32_t id = blockIdx.y * gridDim.x + blockIdx.x;
+    const uint32_t xcd = id & 7u, idx = id >> 3;
+    const uint32_t base = total >> 3, extra = total & 7u;
+    const uint32_t lin = xcd * base + min(xcd, extra) + idx;
+    tm = lin % mt;
+    tn = lin / mt;
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane l's bytes land at lds_base + 16*l; the
+// base must be the same for the whole wave.
+DAV2_DEV void copy16_to_lds(const int8_t* src, int8_t* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)lds_base, 16, 0, 0);
+}
+
+// LDS byte offset of logical 16-byte chunk c of row r in a stage of BK-byte
+// rows: chunks are XOR-swizzled with the row's 256-byte period index, so the
+// 16 rows that one MFMA operand load reads at the same logical chunk hit 16
+// distinct bank groups (256 bytes = all banks once).
+template <int BK>
+DAV2_DEV uint32_t swz(uint32_t r, uint32_t c) {
+    constexpr uint32_t cpr = BK / 16, rows_per_period = 256 / BK;
+    return r * BK + ((c ^ ((r / rows_per_period) & (cpr - 1))) << 4);
+}
+
+// s_waitcnt with vmcnt = n (expcnt, lgkmcnt not waited on), n < 64.
+#define DAV2_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, int EPI>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmParams g) {
-    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    constexpr int NW = WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int TM = WM / 16, TN = WN / 16;
-    constexpr int P_CHUNKS = BM * (kBK / 16);  // 16-byte chunks per stage
-    constexpr int Q_CHUNKS = BN * (kBK / 16);
-    constexpr int P_PER_T = (P_CHUNKS + NT - 1) / NT;
-    constexpr int Q_PER_T = (Q_CHUNKS + NT - 1) / NT;
+    constexpr int kBK = BK;
+    constexpr int CPR = BK / 16;                  // 16-byte chunks per row
+    constexpr int STAGE_BYTES = (BM + BN) * BK;
+    // one global_load_lds_dwordx4 moves 64 x 16 bytes = 1024 / BK rows
+    constexpr int RPL = 1024 / BK;
+    constexpr int LOADS = (BM + BN) / RPL;        // per stage, all waves
+    constexpr int LOADS_PER_WAVE = LOADS / NW;
+    static_assert(BK == 64 || BK == 128 || BK == 256, "stage depth");
+    static_assert(STAGES >= 2 && STAGES <= 4 && 2 * LOADS_PER_WAVE < 64, "pipeline depth / vmcnt range");
+    static_assert(LOADS % NW == 0 && BM % RPL == 0, "stage rows must split evenly over the waves");
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one MFMA block");
 
-    __shared__ __attribute__((aligned(16))) int8_t smem[2][(BM + BN) * kLdsStride];
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];  // [STAGES][BM + BN][128]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-    const uint32_t row0 = blockIdx.y * BM;
-    const uint32_t col0 = blockIdx.x * BN;
-    const int ksteps = static_cast<int>(g.k / kBK);
+    uint32_t tm, tn;
+    tile_of(tm, tn);
+    const uint32_t row0 = tm * BM;
+    const uint32_t col0 = tn * BN;
+    // K is a multiple of 64: full stages, then possibly a partial one
+    const int ksteps = static_cast<int>((g.k + kBK - 1) / kBK);
 
-    v4i rp[P_PER_T], rq[Q_PER_T];
-
-    auto load_global = [&](int ks) {
-        const uint64_t kofs = static_cast<uint64_t>(ks) * kBK;
+    // Loads of this wave: instruction i covers stage rows RPL*(wave*LPW + i)
+    // .. +RPL-1; lane l brings row +l/CPR, physical chunk l%CPR, i.e. the
+    // logical chunk that swz maps there. Rows past the matrix read a valid
+    // row (their results are never stored); chunks past K are never
+    // multiplied.
+    const int8_t* src[LOADS_PER_WAVE];
+    uint32_t chunk_bytes[LOADS_PER_WAVE];
 #pragma unroll
-        for (int i = 0; i < P_PER_T; ++i) {
-            const int c = tid + i * NT;
-            const uint32_t r = row0 + (c >> 2);
-            v4i v = {0, 0, 0, 0};
-            if (c < P_CHUNKS && r < g.rows_p)
-                v = *reinterpret_cast<const v4i*>(g.p + r * g.ldp + kofs + (c & 3) * 16);
-            rp[i] = v;
+    for (int i = 0; i < LOADS_PER_WAVE; ++i) {
+        const uint32_t srow = RPL * (wave * LOADS_PER_WAVE + i) + lane / CPR;  // stage row
+        chunk_bytes[i] = ((lane % CPR) ^ ((srow / (256 / BK)) & (CPR - 1))) * 16u;
+        if (srow < static_cast<uint32_t>(BM)) {  // uniform per instruction (BM % RPL == 0)
+            const uint32_t r = min(row0 + srow, g.rows_p - 1);
+            src[i] = g.p + r * g.ldp + chunk_bytes[i];
+        } else {
+            const uint32_t r = min(col0 + srow - BM, g.rows_q - 1);
+            src[i] = g.q + r * g.ldq + chunk_bytes[i];
         }
+    }
+    auto issue = [&](int ks) {
+        const int slot = ks % STAGES;
+        const uint32_t kofs = static_cast<uint32_t>(ks) * kBK;
 #pragma unroll
-        for (int i = 0; i < Q_PER_T; ++i) {
-            const int c = tid + i * NT;
-            const uint32_t r = col0 + (c >> 2);
-            v4i v = {0, 0, 0, 0};
-            if (c < Q_CHUNKS && r < g.rows_q)
-                v = *reinterpret_cast<const v4i*>(g.q + r * g.ldq + kofs + (c & 3) * 16);
-            rq[i] = v;
-        }
-    };
-    auto store_lds = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < P_PER_T; ++i) {
-            const int c = tid + i * NT;
-            if (c < P_CHUNKS)
-                *reinterpret_cast<v4i*>(&smem[buf][(c >> 2) * kLdsStride + (c & 3) * 16]) = rp[i];
-        }
-#pragma unroll
-        for (int i = 0; i < Q_PER_T; ++i) {
-            const int c = tid + i * NT;
-            if (c < Q_CHUNKS)
-                *reinterpret_cast<v4i*>(&smem[buf][(BM + (c >> 2)) * kLdsStride + (c & 3) * 16]) = rq[i];
+        for (int i = 0; i < LOADS_PER_WAVE; ++i) {
+            // In a partial stage chunks past K re-read bytes of the same row
+            // inside K (never multiplied).
+            int64_t off = static_cast<int64_t>(kofs);
+            while (off + chunk_bytes[i] >= g.k) off -= 64;
+            copy16_to_lds(src[i] + off, smem + slot * STAGE_BYTES + (wave * LOADS_PER_WAVE + i) * 1024);
         }
     };
 
@@ -159,31 +200,55 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < ksteps) issue(s);
 
     const int frag_row = lane & 15;
-    const int frag_k = (lane >> 4) * 16;
+    const int frag_c = lane >> 4;  // logical chunk within a 64-byte k step
     for (int ks = 0; ks < ksteps; ++ks) {
-        const int cur = ks & 1;
-        if (ks + 1 < ksteps) load_global(ks + 1);
-        v4i af[TM], bf[TN];
+        // stage ks has landed once only the loads of the stages after it are
+        // outstanding
+        // loads complete in order: after stage ks only the stages issued
+        // after it (at most STAGES - 2 of them) may still be in flight
+        const int later = min(STAGES - 2, ksteps - 1 - ks);
+        if (later >= 2) {
+            DAV2_WAIT_VMCNT(2 * LOADS_PER_WAVE);
+        } else if (later == 1) {
+            DAV2_WAIT_VMCNT(LOADS_PER_WAVE);
+        } else {
+            DAV2_WAIT_VMCNT(0);
+        }
+        // Plain barrier: the wait above already covers this wave's copies of
+        // stage ks, and the slot refilled next was last read by operands the
+        // MFMAs of the previous stage consumed. (__syncthreads would also
+        // drain the copies of stage ks + 1.)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + STAGES - 1 < ksteps) issue(ks + STAGES - 1);
+        const int8_t* st = smem + (ks % STAGES) * STAGE_BYTES;
+        const int ksub = min(static_cast<int>((g.k - static_cast<uint32_t>(ks) * kBK) / 64), BK / 64);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-            af[i] = *reinterpret_cast<const v4i*>(
-                &smem[cur][(wm * WM + i * 16 + frag_row) * kLdsStride + frag_k]);
+        for (int kk = 0; kk < BK / 64; ++kk) {
+            if (kk < ksub) {
+                v4i af[TM], bf[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-            bf[j] = *reinterpret_cast<const v4i*>(
-                &smem[cur][(BM + wn * WN + j * 16 + frag_row) * kLdsStride + frag_k]);
+                for (int i = 0; i < TM; ++i) {
+                    const uint32_t r = wm * WM + i * 16 + frag_row;
+                    af[i] = *reinterpret_cast<const v4i*>(st + swz<BK>(r, kk * 4 + frag_c));
+                }
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+                for (int j = 0; j < TN; ++j) {
+                    const uint32_t r = BM + wn * WN + j * 16 + frag_row;
+                    bf[j] = *reinterpret_cast<const v4i*>(st + swz<BK>(r, kk * 4 + frag_c));
+                }
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-        if (ks + 1 < ksteps) store_lds(cur ^ 1);
-        __syncthreads();
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
     }
 
     // 16x16 MFMA result layout: lane l holds rows 4*(l/16)+r (r = 0..3) of
@@ -203,31 +268,26 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
     }
 }
 
-int device_cu_count() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-    }
-    return cus;
-}
-
-template <int BM, int BN, int WMW, int WNW, int EPI>
+template <int BM, int BN, int WMW, int WNW, int BK, int STAGES, int EPI>
 void launch_cfg(const GemmParams& g, hipStream_t s) {
-    const dim3 grid(ceil_div(g.rows_q, BN), ceil_div(g.rows_p, BM));
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WMW, WNW, EPI>), grid, dim3(64 * WMW * WNW), 0, s, g);
+    constexpr size_t lds = static_cast<size_t>(STAGES) * (BM + BN) * BK;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    (void)attr;
+    const dim3 grid(ceil_div(g.rows_p, BM), ceil_div(g.rows_q, BN));
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>), grid, dim3(64 * WMW * WNW), lds, s, g);
 }
 
 template <int EPI>
 void launch_epi(const GemmParams& g, hipStream_t s) {
-    const uint64_t cus = static_cast<uint64_t>(device_cu_count());
-    const uint64_t tiles_l = static_cast<uint64_t>(ceil_div(g.rows_p, 128)) * ceil_div(g.rows_q, 128);
-    const uint64_t tiles_m = static_cast<uint64_t>(ceil_div(g.rows_p, 128)) * ceil_div(g.rows_q, 64);
-    if (tiles_l >= 2 * cus) launch_cfg<128, 128, 2, 2, EPI>(g, s);
-    else if (tiles_m >= cus) launch_cfg<128, 64, 2, 2, EPI>(g, s);
-    else launch_cfg<64, 64, 2, 2, EPI>(g, s);
+    // Measured on MI355X for the ViT-L encoder shapes (M = 1370, K = 1024 /
+    // 4096): 64x64 tiles with four waves, 128-byte stages and a three-stage
+    // ring beat every larger tile (more workgroups in flight hide the load
+    // latency better) and match the vendor int8 GEMM. Channel-major GEMMs
+    // with few output channels use 32-row tiles.
+    if (g.rows_p <= 32) launch_cfg<32, 64, 1, 2, 128, 3, EPI>(g, s);
+    else launch_cfg<64, 64, 2, 2, 128, 3, EPI>(g, s);
 }
 
 }  // namespace
@@ -235,7 +295,7 @@ void launch_epi(const GemmParams& g, hipStream_t s) {
 extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     if (!a) return hipErrorInvalidValue;
     if (a->m == 0 || a->n == 0) return hipSuccess;
-    if (!a->a || !a->b || a->k == 0 || a->k % kBK || a->lda < a->k || a->ldb < a->k ||
+    if (!a->a || !a->b || a->k == 0 || a->k % 64 || a->lda < a->k || a->ldb < a->k ||
         a->lda % 16 || a->ldb % 16 || (reinterpret_cast<uintptr_t>(a->a) & 15) ||
         (reinterpret_cast<uintptr_t>(a->b) & 15))
         return hipErrorInvalidValue;
