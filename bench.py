@@ -1,8 +1,9 @@
 #!/usr/bin/env python3
 """Throughput of the int8 Depth-Anything-V2 path on one MI355X.
 
-Workload (default): ViT-L + DPT at 518x518, batch 1, int8 GEMMs with binary16
-attention scores (the reference's int8-mode default), seeded random weights in
+Workload (default): ViT-L + DPT at 518x518, batch 1, int8 GEMMs and
+convolutions with the integer-exact fused attention (in place of the
+reference's binary16 attention of its int8 mode), seeded random weights in
 a .dav2 file and a seeded ImageNet-normalised input already resident in HBM,
 run through dav2_infer_tensor_f32_device. One step = one full inference of
 the batch. Prints one JSON line.
@@ -79,8 +80,9 @@ def main() -> int:
                     help="only run one device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not part of this build "
-              "(images are independent; see DESIGN.md for how the path would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
+              "(images are independent, so several GPUs would each run their own share of the batch)",
+              file=sys.stderr)
         return 2
     if args.size % 14:
         print("--size must be a multiple of 14", file=sys.stderr)
@@ -197,8 +199,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (seeded random-init weights in a .dav2 file, seeded ImageNet-normalised input)",
-        "config": {"workload": f"{args.encoder} + DPT {args.size}x{args.size} batch {args.batch}, int8 GEMMs, "
-                               f"{'fp32' if args.fp32_attention else 'fp16'} attention scores, "
+        "config": {"workload": f"{args.encoder} + DPT {args.size}x{args.size} batch {args.batch}, int8 GEMMs and "
+                               f"convolutions, {'fp32' if args.fp32_attention else 'integer-exact'} attention, "
                                "dav2_infer_tensor_f32_device",
                    "size": args.size, "global_batch": args.batch,
                    "parallelism": "single GPU"},

@@ -112,6 +112,18 @@ GpuModel::GpuModel(const ModelFile& model, HipContext& context) {
                                                 dst.int8_scales.as<float>(), stream),
                       "weight quantization");
             device_bytes_ += rows * dst.int8_ld + rows * sizeof(float);
+            const std::uint64_t k = src.dimensions[2];
+            if (!convT && src.rank == 4 && src.dimensions[3] == k &&
+                dav2_hip_conv2d_i8_supported(1, 1, static_cast<std::uint32_t>(src.dimensions[1]),
+                                             dst.int8_rows, static_cast<std::uint32_t>(k), 1,
+                                             static_cast<std::uint32_t>((k - 1) / 2))) {
+                dst.int8_tapmajor = context.create_device_buffer(rows * columns);
+                hip_check(dav2_hip_conv_weights_tapmajor(dst.int8_tapmajor.as<int8_t>(), dst.int8_buffer.as<int8_t>(),
+                                                         dst.int8_rows, static_cast<std::uint32_t>(src.dimensions[1]),
+                                                         static_cast<std::uint32_t>(k), dst.int8_ld, stream),
+                          "tap-major conv weights");
+                device_bytes_ += rows * columns;
+            }
         }
         if (!tensors_.emplace(std::string(name), std::move(dst)).second)
             throw std::runtime_error("duplicate GPU tensor name: " + std::string(name));

@@ -25,6 +25,10 @@ struct GpuTensor {
     DeviceBuffer buffer;       // fp32 copy (only for tensors not stored as int8)
     DeviceBuffer int8_buffer;  // [int8_rows][int8_ld]
     DeviceBuffer int8_scales;  // [int8_rows]
+    // Conv weights the implicit-GEMM convolution takes (kernel 1 or 3,
+    // IC % 64 == 0, OC % 32 == 0): the same int8 rows with columns reordered
+    // tap-major, [OC][(ky*k + kx)*IC + ic], no padding. Empty otherwise.
+    DeviceBuffer int8_tapmajor;
     std::uint32_t int8_rows = 0;
     std::uint32_t int8_columns = 0;
     std::uint32_t int8_ld = 0;

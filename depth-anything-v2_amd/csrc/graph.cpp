@@ -150,7 +150,7 @@ FeatureMap DptHead::conv(const FeatureMap& in, const std::string& weight, const 
     if (!w.int8_buffer) throw std::runtime_error("convolution weight is not int8: " + weight);
     const DeviceBuffer& b = has_bias ? weights_.tensor(bias).buffer : zero_bias_;
     ops_.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc, k,
-                     stride, pad, has_bias);
+                     stride, pad, has_bias, &w.int8_tapmajor);
     return out;
 }
 

@@ -56,6 +56,18 @@ DAV2_DEV float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
 inline unsigned ceil_div(uint64_t a, uint64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
+// Scale rule shared by every activation quantizer:
+// quantize_rows_int8_fused.glsl:37 and im2col_quantize_int8.glsl:63.
+DAV2_DEV float row_scale(float absmax) { return fmaxf(absmax / 127.0f, 1.0e-8f); }
+
+// Per-pixel |x| maxima of a CHW map over groups of kGroupChannels channels:
+// partial[g][p] = max over c in group g of |x[c][p]| (quantize.hip). The
+// window maximum of these is the absmax of an im2col row.
+constexpr uint32_t kGroupChannels = 32;
+inline uint32_t channel_groups(uint32_t channels) { return (channels + kGroupChannels - 1) / kGroupChannels; }
+hipError_t launch_channel_group_absmax(const float* x, uint32_t channels, uint64_t plane, float* partial,
+                                       hipStream_t stream);
+
 // e^a by Cody-Waite range reduction (a = n ln2 + r, |r| <= ln2/2, ln2 split
 // into a 16-bit head and a tail) and the degree-7 Taylor polynomial of e^r in
 // Horner form with explicit fmaf; error below 1 ulp of float over the range.

@@ -1,0 +1,446 @@
+// Implicit-GEMM int8 convolution on CDNA4 matrix cores: im2col, per-pixel
+// quantization and the int8 GEMM of the reference's conv2d_int8
+// (src/operators.cpp:1735-1805: im2col_quantize_int8.glsl:26-83 then
+// linear_int8_tiled.glsl:40-117 with the CHW store) in one kernel, without
+// the im2col matrix ever reaching HBM.
+//
+// Scope: kernel 3 (stride 1, padding 1) or kernel 1 (stride 1, no padding),
+// input channels a multiple of 64, output channels a multiple of 32.
+//
+// Arithmetic. Output pixel p's im2col row is quantized with the scale
+// s = max(absmax/127, 1e-8) of that whole row and q = rne(clamp(x * (1/s))),
+// exactly as im2col_quantize_int8.glsl; the int32 dot products are exact, so
+// the order in which K is walked is free. This kernel walks K tap-major
+// (k = tap * C + c, tap = ky * ks + kx) so that one 64-byte K step is 64
+// channels of one tap; the weights are stored in that order
+// (dav2_hip_conv_weights_tapmajor). The epilogue is the GEMM's CHW epilogue,
+// ((float(acc) * s_pixel) * s_weight) + bias, so every output float equals
+// the im2col + GEMM path's bit for bit.
+//
+// Tiling. A workgroup (4 waves) owns 64 output pixels (a segment of one image
+// row for 3x3, 64 consecutive pixels for 1x1) and BN output channels. Per
+// block of 64 input channels it stages the fp32 input window (64 channels x
+// 3 rows x 66 columns for 3x3) in LDS; per tap every thread quantizes 16
+// channels of one pixel into a double-buffered 64 x 64-byte int8 tile
+// (XOR-swizzled rows, conflict-free for the MFMA operand reads), and the
+// waves multiply it against weight fragments read straight from global
+// memory (v_mfma_i32_16x16x64_i8, weights as the row operand so each lane's
+// accumulators run along pixels and the CHW stores coalesce). The next
+// channel block's window is loaded into registers while the nine taps of the
+// current one run, and weight fragments three steps ahead, so global latency
+// hides behind the quantize and MFMA work. One LDS-only barrier per tap.
+
+#include <algorithm>
+
+#include "common.h"
+#include "dav2_hip.h"
+
+using namespace dav2k;
+
+namespace {
+
+constexpr int kPix = 64;  // output pixels per workgroup
+constexpr int kCB = 64;   // input channels per block = one MFMA K step per tap
+
+struct ConvParams {
+    const float* x;        // CHW input
+    const float* partial;  // [groups][plane] channel-group |x| maxima
+    uint32_t groups;
+    uint32_t channels, height, width;
+    uint64_t plane;
+    uint32_t tiles_x;      // 3x3: pixel tiles per image row
+    const int8_t* w;       // [N][taps * channels], tap-major
+    const float* w_scales;
+    const float* bias;     // nullable
+    float* out;            // CHW [N][plane]
+};
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// operations (lgkmcnt) but leaves global loads in flight.
+DAV2_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// rne(clamp(v * inv, -127, 127)) of four values packed little-endian, for
+// |v| <= absmax of the row and inv = 1 / max(absmax / 127, 1e-8): then
+// |v * inv| <= 127 * (1 + 3 * 2^-24) < 127.5 (or below 127 under the 1e-8
+// floor), so rounding alone lands in [-127, 127] and the clamp never acts.
+// Adding 1.5 * 2^23 rounds to an integer (round to nearest even, the ulp
+// there is 1) held in the low mantissa bits, so the low byte of the sum is the
+// two's-complement int8; v_perm gathers the bytes. (Finite inputs: the
+// reference leaves NaN and infinity to the shader's clamp.)
+DAV2_DEV uint32_t quant4(float a, float b, float c, float d, float inv) {
+    constexpr float kMagic = 12582912.0f;
+    const uint32_t qa = __float_as_uint(a * inv + kMagic);
+    const uint32_t qb = __float_as_uint(b * inv + kMagic);
+    const uint32_t qc = __float_as_uint(c * inv + kMagic);
+    const uint32_t qd = __float_as_uint(d * inv + kMagic);
+    const uint32_t lo = __builtin_amdgcn_perm(qb, qa, 0x00000400u);  // bytes: a, b, a, a
+    const uint32_t hi = __builtin_amdgcn_perm(qd, qc, 0x00000400u);  // bytes: c, d, c, c
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);               // bytes: a, b, c, d
+}
+
+// LDS byte offset of 16-byte chunk c (0..3) of pixel row p in a 64 x 64-byte
+// int8 tile: rows are 64 bytes, chunks XOR-swizzled by (p / 4) % 4 so the 16
+// rows one MFMA operand read touches cover all banks once.
+DAV2_DEV uint32_t a_offset(uint32_t p, uint32_t c) { return p * 64u + ((c ^ ((p >> 2) & 3u)) << 4); }
+
+template <int KS, int BN, int WM, int WN>
+__global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
+    constexpr int kRowsT = KS;                   // input rows per channel in the window
+    constexpr int kColsT = kPix + KS - 1;        // input columns per row (halo for 3x3)
+    constexpr int kPlaneT = kRowsT * kColsT;     // floats per channel in LDS
+    constexpr int kLoads = kCB * kRowsT / 4;     // 64-wide row loads per wave per block
+    constexpr int kTaps = KS * KS;
+    constexpr int PW = kPix / WM, NW = BN / WN;  // pixels / channels per wave
+    constexpr int PB = PW / 16, NB = NW / 16;
+    static_assert(WM * WN == 4 && PW % 16 == 0 && NW % 16 == 0, "wave tiling");
+
+    __shared__ float xt[kCB * kPlaneT];
+    __shared__ __attribute__((aligned(16))) int8_t at[2][kPix * 64];
+    __shared__ float sc_lds[kPix];
+    __shared__ float wsc_lds[BN], bias_lds[BN];
+    __shared__ float amax_lds[KS == 3 ? 3 * kColsT : 1];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WN, wn = wave % WN;
+
+    // Workgroups go to the 8 XCDs round robin; give each XCD a contiguous run
+    // of pixel tiles (neighbouring tiles share input rows in that XCD's L2),
+    // with all channel blocks of one pixel tile together.
+    const uint32_t nblk_n = gridDim.y, total = gridDim.x * gridDim.y;
+    const uint32_t id = blockIdx.y * gridDim.x + blockIdx.x;
+    const uint32_t xcd = id & 7u, slot = id >> 3, per = total >> 3, extra = total & 7u;
+    const uint32_t lin = xcd * per + min(xcd, extra) + slot;
+    const uint32_t nb = lin % nblk_n, pt = lin / nblk_n;
+
+    // The image as rows of `rowlen` pixels: 3x3 tiles are row segments, 1x1
+    // tiles are runs of the flattened map (one row of `plane` pixels).
+    const uint32_t rowlen = KS == 3 ? g.width : static_cast<uint32_t>(g.plane);
+    const uint32_t nrows = KS == 3 ? g.height : 1u;
+    const uint32_t y = KS == 3 ? pt / g.tiles_x : 0u;
+    const uint32_t x0 = KS == 3 ? (pt - y * g.tiles_x) * kPix : pt * kPix;
+    const uint64_t mbase = static_cast<uint64_t>(y) * rowlen + x0;
+    const uint32_t valid = min(static_cast<uint32_t>(kPix), rowlen - x0);
+
+    // ---- per-pixel scale: window maximum of the channel-group maxima -----
+    float m = 0.0f;
+    if constexpr (KS == 3) {
+        if (tid < 3u * kColsT) {
+            const int r = static_cast<int>(tid) / kColsT, col = static_cast<int>(tid) % kColsT;
+            const int gy = static_cast<int>(y) + r - 1, gx = static_cast<int>(x0) + col - 1;
+            float t = 0.0f;
+            if (gy >= 0 && gy < static_cast<int>(g.height) && gx >= 0 && gx < static_cast<int>(g.width)) {
+                const float* src = g.partial + static_cast<uint64_t>(gy) * g.width + gx;
+                for (uint32_t k = 0; k < g.groups; ++k) t = fmaxf(t, src[k * g.plane]);
+            }
+            amax_lds[tid] = t;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+#pragma unroll
+            for (int dx = 0; dx < 3; ++dx) m = fmaxf(m, amax_lds[r * kColsT + lane + dx]);
+    } else {
+        if (lane < valid)
+            for (uint32_t k = 0; k < g.groups; ++k) m = fmaxf(m, g.partial[k * g.plane + mbase + lane]);
+    }
+    const float s_pix = row_scale(m);
+    const float inv = 1.0f / s_pix;  // this thread quantizes pixel `lane`
+    if (wave == 0) sc_lds[lane] = s_pix;
+    if (tid < BN) {
+        const uint32_t ch = nb * BN + tid;
+        wsc_lds[tid] = g.w_scales[ch];
+        bias_lds[tid] = g.bias ? g.bias[ch] : 0.0f;
+    }
+
+    // ---- input window staging ---------------------------------------------
+    // Wave w loads LDS rows R = w*kLoads + j (channel R / kRowsT, window row
+    // R % kRowsT), 64 columns per load with lane = column; the two halo
+    // columns of every row (3x3) are loaded by threads 0..383 of the block.
+    // Every load reads a valid address (rows and columns clamped into the
+    // image); the padding zeros are substituted when the window is written to
+    // LDS, so no load sits behind a branch or waits before that point.
+    // Addresses are the tensor base plus a 32-bit byte offset (the host
+    // checks that the input is below 4 GiB): a wave-uniform row offset and
+    // one per-lane column offset. The block index goes through an empty asm
+    // statement so the row arithmetic is redone with scalar instructions in
+    // every block instead of being hoisted into 48 live vector registers.
+    const bool col_ok = x0 + lane < rowlen;
+    const uint32_t col4 = min(x0 + lane, rowlen - 1u) * 4u;
+    const uint32_t plane32 = static_cast<uint32_t>(g.plane);
+    const char* xbase = reinterpret_cast<const char*>(g.x);
+    float xs[kLoads];
+    float xh[2] = {0.0f, 0.0f};
+    // Byte offsets of the window rows within a channel plane (clamped).
+    uint32_t row4[kRowsT];
+#pragma unroll
+    for (int r = 0; r < kRowsT; ++r) {
+        const int gy = static_cast<int>(y) + r - KS / 2;
+        row4[r] = static_cast<uint32_t>(min(max(gy, 0), static_cast<int>(nrows) - 1)) * rowlen * 4u;
+    }
+    // Wave w's rows j = 0..kLoads-1 are channel 16w + j / kRowsT, window row
+    // j % kRowsT. The channel offset advances through an opaque register so
+    // the compiler does not precompute (and keep live) all kLoads offsets.
+    auto issue_rows = [&](uint32_t cb, int j0, int j1) {
+        uint32_t chan = ((cb * kCB + wave * (kCB / 4) + j0 / kRowsT) * plane32) * 4u;
+        asm volatile("" : "+s"(chan));
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            if (j < j0 || j >= j1) continue;
+            if (j > j0 && j % kRowsT == 0) {
+                chan += plane32 * 4u;
+                asm volatile("" : "+s"(chan));
+            }
+            xs[j] = *reinterpret_cast<const float*>(xbase + (chan + row4[j % kRowsT] + col4));
+        }
+    };
+    auto issue_halo = [&](uint32_t cb) {
+        if constexpr (KS == 3) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t idx = min(tid + 256u * h, 2u * kCB * 3u - 1u);  // 2 * 192 halo values
+                const uint32_t R = idx >> 1, c = R / 3u, r = R - 3u * c;
+                const int gy = static_cast<int>(y) + static_cast<int>(r) - 1;
+                const int gx = (idx & 1u) ? static_cast<int>(x0) + kPix : static_cast<int>(x0) - 1;
+                const uint32_t gyc = static_cast<uint32_t>(min(max(gy, 0), static_cast<int>(g.height) - 1));
+                const uint32_t gxc = static_cast<uint32_t>(min(max(gx, 0), static_cast<int>(g.width) - 1));
+                const uint32_t off = ((cb * kCB + c) * plane32 + gyc * g.width + gxc) * 4u;
+                xh[h] = *reinterpret_cast<const float*>(xbase + off);
+            }
+        }
+    };
+    auto write_window = [&]() {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const uint32_t R = wave * kLoads + j;
+            const uint32_t c = R / kRowsT, r = R - c * kRowsT;
+            const int gy = static_cast<int>(y) + static_cast<int>(r) - KS / 2;
+            const bool ok = col_ok && gy >= 0 && gy < static_cast<int>(nrows);
+            xt[c * kPlaneT + r * kColsT + (KS == 3 ? 1u : 0u) + lane] = ok ? xs[j] : 0.0f;
+        }
+        if constexpr (KS == 3) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t idx = tid + 256u * h;
+                if (idx < 2u * kCB * 3u) {
+                    const uint32_t R = idx >> 1, c = R / 3u, r = R - 3u * c;
+                    const int gy = static_cast<int>(y) + static_cast<int>(r) - 1;
+                    const int gx = (idx & 1u) ? static_cast<int>(x0) + kPix : static_cast<int>(x0) - 1;
+                    const bool ok =
+                        gy >= 0 && gy < static_cast<int>(g.height) && gx >= 0 && gx < static_cast<int>(g.width);
+                    xt[c * kPlaneT + r * kColsT + ((idx & 1u) ? kColsT - 1u : 0u)] = ok ? xh[h] : 0.0f;
+                }
+            }
+        }
+    };
+
+    // ---- weight fragments ----------------------------------------------------
+    // Lane l supplies weight row n0 + 16i + l%16, bytes 16*(l/16) of the step.
+    const uint32_t kw = kTaps * g.channels;  // weight row length
+    const uint32_t wrow0 = (nb * BN + wn * NW) * kw;
+    const uint32_t wlane = (lane & 15u) * kw + (lane >> 4) * 16u;
+    auto load_w = [&](v4i (&b)[NB], uint32_t step) {
+        const uint32_t cb = step / kTaps, tap = step - cb * kTaps;
+        const uint32_t k0 = tap * g.channels + cb * kCB;
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            b[i] = *reinterpret_cast<const v4i*>(g.w + ((wrow0 + i * 16u * kw + k0) + wlane));
+    };
+
+    v4i acc[NB][PB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < PB; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    // Weight fragments go through a ring of kRing steps. Global loads retire
+    // in issue order (one vmcnt counter per wave), so the slow input-window
+    // loads of the next block are issued once per block, right after a
+    // weight load: only the weight load kRing steps later queues behind them.
+    constexpr int kRing = kTaps % 3 == 0 ? 3 : 1;
+    const uint32_t nblocks = g.channels / kCB, nsteps = nblocks * kTaps;
+    v4i ring[kRing][NB];
+    issue_rows(0, 0, kLoads);
+    issue_halo(0);
+#pragma unroll
+    for (int d = 0; d < kRing; ++d) load_w(ring[d], min(static_cast<uint32_t>(d), nsteps - 1));
+    write_window();
+    lds_barrier();
+
+    // Operand reads of this wave's pixel blocks: lane l reads pixel
+    // wm*PW + 16j + l%16, chunk l/16.
+    const uint32_t prow = wm * PW + (lane & 15u), pchunk = lane >> 4;
+    // Quantizer: pixel `lane`, channels 16*wave .. +15 of the block.
+    const float* qsrc = xt + (wave * 16u) * kPlaneT + lane;
+    const uint32_t qdst = a_offset(lane, wave);
+
+    // The 16 window values a thread quantizes for a tap are read one step
+    // ahead, before the barrier, so their LDS latency overlaps the barrier
+    // wait instead of following it.
+    float f[16];
+    auto read_tap = [&](int tap) {
+        uint32_t qoff = (tap / KS) * kColsT + (tap % KS);
+        asm volatile("" : "+v"(qoff));  // keep the read bases from being hoisted
+        const float* src = qsrc + qoff;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) f[e] = src[e * kPlaneT];
+    };
+    read_tap(0);
+
+    for (uint32_t cb = 0; cb < nblocks; ++cb) {
+        const bool more = cb + 1 < nblocks;
+        const uint32_t next_cb = more ? cb + 1 : cb;
+#pragma unroll
+        for (int tap = 0; tap < kTaps; ++tap) {
+            const uint32_t step = cb * kTaps + tap;
+            int8_t* abuf = at[step & 1u];
+            {
+                uint32_t w4[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    w4[q] = quant4(f[4 * q + 0], f[4 * q + 1], f[4 * q + 2], f[4 * q + 3], inv);
+                *reinterpret_cast<v4i*>(abuf + qdst) =
+                    v4i{static_cast<int>(w4[0]), static_cast<int>(w4[1]), static_cast<int>(w4[2]),
+                        static_cast<int>(w4[3])};
+            }
+            if (tap + 1 < kTaps) read_tap(tap + 1);
+            lds_barrier();
+            v4i (&bw)[NB] = ring[tap % kRing];
+#pragma unroll
+            for (int j = 0; j < PB; ++j) {
+                const v4i bp = *reinterpret_cast<const v4i*>(abuf + a_offset(prow + 16u * j, pchunk));
+#pragma unroll
+                for (int i = 0; i < NB; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[i], bp, acc[i][j], 0, 0, 0);
+            }
+            // Prefetches are unconditional (a branch around a load makes the
+            // compiler wait for it at the merge); past the end they re-read
+            // the last step / block, which is harmless.
+            load_w(bw, min(step + kRing, nsteps - 1));
+            if (tap == 0) {
+                issue_rows(next_cb, 0, kLoads);
+                issue_halo(next_cb);
+            }
+        }
+        if (more) {
+            // Every wave is past the last tap's barrier, so no quantizer still
+            // reads the window: replace it with the next block's.
+            write_window();
+            lds_barrier();
+            read_tap(0);
+        }
+    }
+
+    // ---- epilogue: out[ch][pixel] = ((acc * s_pixel) * s_weight) + bias ---
+    // Accumulator r of lane l in block (i, j): channel 16i + 4(l/16) + r,
+    // pixel 16j + l%16 of the wave's sub-tile.
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+        const uint32_t p = wm * PW + 16u * j + (lane & 15u);
+        if (p >= valid) continue;
+        const float sp = sc_lds[p];
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t cl = wn * NW + 16u * i + 4u * (lane >> 4) + r;
+                float v = static_cast<float>(acc[i][j][r]);
+                v = v * sp;
+                v = v * wsc_lds[cl];
+                v = v + bias_lds[cl];
+                g.out[static_cast<uint64_t>(nb * BN + cl) * g.plane + mbase + p] = v;
+            }
+    }
+}
+
+// dst[n][tap*C + c] = src[n][c*taps + tap].
+__global__ __launch_bounds__(256) void weights_tapmajor_kernel(int8_t* __restrict__ dst, const int8_t* __restrict__ src,
+                                                               uint32_t n, uint32_t channels, uint32_t taps,
+                                                               uint64_t ldb) {
+    const uint64_t row_len = static_cast<uint64_t>(taps) * channels;
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    if (idx >= row_len * n) return;
+    const uint64_t row = idx / row_len;
+    const uint32_t k = static_cast<uint32_t>(idx - row * row_len);
+    const uint32_t tap = k / channels, c = k - tap * channels;
+    dst[idx] = src[row * ldb + static_cast<uint64_t>(c) * taps + tap];
+}
+
+template <int KS, int BN, int WM, int WN>
+void launch(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
+    hipLaunchKernelGGL((conv_i8_kernel<KS, BN, WM, WN>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+}
+
+template <int KS>
+void launch_ks(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
+    // Measured on the DPT shapes: one channel slice per wave (each wave
+    // reads the whole pixel tile) beats 2x2 wave grids, and the widest
+    // channel tile wins; 32-channel maps use a 2x2 grid.
+    if (n % 256 == 0) launch<KS, 256, 1, 4>(g, tiles, n, s);
+    else if (n % 128 == 0) launch<KS, 128, 1, 4>(g, tiles, n, s);
+    else if (n % 64 == 0) launch<KS, 64, 1, 4>(g, tiles, n, s);
+    else launch<KS, 32, 2, 2>(g, tiles, n, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dav2_hip_conv_weights_tapmajor(int8_t* dst, const int8_t* src, uint32_t out_channels, uint32_t channels,
+                                   uint32_t kernel, uint64_t ldb, void* stream) {
+    if (out_channels == 0) return hipSuccess;
+    const uint64_t taps = static_cast<uint64_t>(kernel) * kernel;
+    if (!dst || !src || kernel == 0 || channels == 0 || ldb < taps * channels) return hipErrorInvalidValue;
+    const uint64_t total = taps * channels * out_channels;
+    hipLaunchKernelGGL(weights_tapmajor_kernel, dim3(ceil_div(total, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), dst, src, out_channels, channels,
+                       static_cast<uint32_t>(taps), ldb);
+    return hipGetLastError();
+}
+
+int dav2_hip_conv2d_i8_supported(uint32_t width, uint32_t height, uint32_t channels, uint32_t out_channels,
+                                 uint32_t kernel, uint32_t stride, uint32_t padding) {
+    return width > 0 && height > 0 && height <= 65535u && (kernel == 3 || kernel == 1) && stride == 1 &&
+           padding == (kernel - 1) / 2 && channels > 0 && channels % kCB == 0 && out_channels > 0 &&
+           out_channels % 32 == 0 && static_cast<uint64_t>(width) * height < (1ull << 31);
+}
+
+int dav2_hip_conv2d_i8(const dav2_conv_i8_args* a, void* stream) {
+    if (!a) return hipErrorInvalidValue;
+    if (!dav2_hip_conv2d_i8_supported(a->width, a->height, a->channels, a->out_channels, a->kernel, 1,
+                                      (a->kernel - 1) / 2))
+        return hipErrorInvalidValue;
+    if (!a->input || !a->weight || !a->weight_scales || !a->out || !a->scratch) return hipErrorInvalidValue;
+    const uint64_t plane = static_cast<uint64_t>(a->width) * a->height;
+    const uint32_t groups = channel_groups(a->channels);
+    if (a->scratch_floats < plane * groups) return hipErrorInvalidValue;
+    // The kernel addresses input and weights with 32-bit byte offsets.
+    if (plane * a->channels * sizeof(float) >= (1ull << 32) ||
+        static_cast<uint64_t>(a->out_channels) * a->kernel * a->kernel * a->channels >= (1ull << 32))
+        return hipErrorInvalidValue;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = launch_channel_group_absmax(a->input, a->channels, plane, a->scratch, s);
+    if (e != hipSuccess) return e;
+    ConvParams g;
+    g.x = a->input;
+    g.partial = a->scratch;
+    g.groups = groups;
+    g.channels = a->channels;
+    g.height = a->height;
+    g.width = a->width;
+    g.plane = plane;
+    g.tiles_x = ceil_div(a->width, kPix);
+    g.w = a->weight;
+    g.w_scales = a->weight_scales;
+    g.bias = a->bias;
+    g.out = a->out;
+    if (a->kernel == 3) launch_ks<3>(g, g.tiles_x * a->height, a->out_channels, s);
+    else launch_ks<1>(g, ceil_div(plane, kPix), a->out_channels, s);
+    return hipGetLastError();
+}
+
+}  // extern "C"

@@ -18,12 +18,8 @@ namespace {
 // Rows are handled one wave each; kRowsPerBlock waves per workgroup.
 constexpr int kRowsPerBlock = 4;
 
-// Scale rule shared by every activation quantizer:
-// quantize_rows_int8_fused.glsl:37 and im2col_quantize_int8.glsl:63.
-DAV2_DEV float row_scale(float absmax) { return fmaxf(absmax / 127.0f, 1.0e-8f); }
-
 // ---------------------------------------------------------------------------
-// a1: quantize_rows_int8_fused.glsl:20-55. q = rne(clamp(x / s)).
+// Per-row quantization, quantize_rows_int8_fused.glsl:20-55. q = rne(clamp(x / s)).
 // Lane l owns float4 chunks at columns 4l + 256j; CH = chunks kept in VGPRs.
 template <int CH>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_kernel(
@@ -85,7 +81,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_long_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// a2: im2col_quantize_int8.glsl:26-83. Column c of output row r reads
+// im2col + quantization, im2col_quantize_int8.glsl:26-83. Column c of output row r reads
 // input[ic][oy*stride+ky-pad][ox*stride+kx-pad] with ic = c / k^2,
 // ky = (c % k^2) / k, kx = c % k, zero outside the image; the row is scaled
 // by s = max(absmax/127, 1e-8) and quantized as rne(clamp(x * (1/s))).
@@ -163,7 +159,7 @@ __global__ __launch_bounds__(256) void im2col_quantize_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Fast paths of a2 for the DPT shapes (same bytes as the generic kernels).
+// Fast im2col paths for the DPT shapes (same bytes as the generic kernels).
 //
 // 3x3, stride 1, pad 1 (C % 16 == 0): a workgroup owns 64 consecutive output
 // pixels of one row and a range of 16-channel chunks. Pass 1 folds the
@@ -179,8 +175,6 @@ constexpr int kHalo = kTile + 2;
 
 // Per-pixel maxima of |x| over channel groups of kGroupChannels:
 // partial[g][p] = max over c in group g of |x[c][p]|.
-constexpr uint32_t kGroupChannels = 32;
-
 __global__ __launch_bounds__(256) void channel_group_absmax_kernel(const float* __restrict__ x, uint32_t C,
                                                                    uint64_t plane, float* __restrict__ partial) {
     const uint64_t p = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
@@ -328,11 +322,11 @@ __global__ __launch_bounds__(256) void im2col1x1_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// a10: layer_norm.glsl:27-68. One wave per row; lane l accumulates columns
+// LayerNorm, layer_norm.glsl:27-68. One wave per row; lane l accumulates columns
 // l, l+64, ... in order and the wave reduction reproduces the 64-entry LDS
 // tree, so sums, mean and variance match the reference order exactly.
 // CH = ceil(columns / 64) values kept per lane (0 = re-read from memory).
-// With QUANT the normalised row is also quantized (a1 rule) into q/scales;
+// With QUANT the normalised row is also quantized (per-row rule above) into q/scales;
 // out may then be null.
 template <int CH, bool QUANT>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
@@ -346,17 +340,26 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
     const uint32_t row = blockIdx.x * kRowsPerBlock + wave;
     if (row >= rows) return;
     const float* x = input + static_cast<uint64_t>(row) * columns;
-    float v[CH > 0 ? CH : 1];
+    constexpr int kKept = CH > 0 ? CH : 1;
+    float v[kKept], wv[kKept], bv[kKept];
     float s = 0.0f, sq = 0.0f;
     if (CH > 0) {
+        // Every load is issued unconditionally (clamped index) before the
+        // first use, so the row, weight and bias arrive in one round trip;
+        // columns past the row end are masked out of the sums by selects.
+        const uint32_t last = columns - 1u;
 #pragma unroll
-        for (int j = 0; j < (CH > 0 ? CH : 1); ++j) {
-            const uint32_t c = lane + 64u * j;
-            v[j] = c < columns ? x[c] : 0.0f;
-            if (c < columns) {
-                s = s + v[j];
-                sq = sq + v[j] * v[j];
-            }
+        for (int j = 0; j < kKept; ++j) v[j] = x[min(lane + 64u * j, last)];
+#pragma unroll
+        for (int j = 0; j < kKept; ++j) {
+            wv[j] = weight[min(lane + 64u * j, last)];
+            bv[j] = bias[min(lane + 64u * j, last)];
+        }
+#pragma unroll
+        for (int j = 0; j < kKept; ++j) {
+            const bool in = lane + 64u * j < columns;
+            s = in ? s + v[j] : s;
+            sq = in ? sq + v[j] * v[j] : sq;
         }
     } else {
         for (uint32_t c = lane; c < columns; c += 64u) {
@@ -376,10 +379,10 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
     float absmax = 0.0f;
     if (CH > 0) {
 #pragma unroll
-        for (int j = 0; j < (CH > 0 ? CH : 1); ++j) {
+        for (int j = 0; j < kKept; ++j) {
             const uint32_t c = lane + 64u * j;
             if (c < columns) {
-                const float r = (v[j] - mean) * inv * weight[c] + bias[c];
+                const float r = (v[j] - mean) * inv * wv[j] + bv[j];
                 if (y) y[c] = r;
                 if (QUANT) {
                     stage[c] = r;
@@ -436,6 +439,13 @@ hipError_t launch_layer_norm(const float* in, const float* w, const float* b, ui
 }
 
 }  // namespace
+
+hipError_t dav2k::launch_channel_group_absmax(const float* x, uint32_t channels, uint64_t plane, float* partial,
+                                              hipStream_t stream) {
+    hipLaunchKernelGGL(channel_group_absmax_kernel, dim3(ceil_div(plane, 256), channel_groups(channels)), dim3(256), 0,
+                       stream, x, channels, plane, partial);
+    return hipGetLastError();
+}
 
 extern "C" {
 

@@ -319,7 +319,7 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
                                const DeviceBuffer& weight_scales, const DeviceBuffer& bias,
                                std::uint32_t input_width, std::uint32_t input_height, std::uint32_t input_channels,
                                std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
-                               std::uint32_t padding, bool has_bias) {
+                               std::uint32_t padding, bool has_bias, const DeviceBuffer* tapmajor_weight) {
     if (input_width == 0 || input_height == 0 || input_channels == 0 || output_channels == 0 || kernel == 0 ||
         stride == 0 || input_width + 2u * padding < kernel || input_height + 2u * padding < kernel)
         throw std::invalid_argument("invalid INT8 convolution dimensions");
@@ -333,18 +333,51 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     require_bytes(weight_scales, output_channels, "convolution weight scale");
     require_bytes(bias, has_bias ? output_channels : 1u, "convolution bias");
     require_bytes(output, std::uint64_t(rows) * output_channels, "output");
+    const hipStream_t s = context_.active_stream();
+    const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
+    // Implicit GEMM: same bits as im2col + GEMM, no im2col matrix. Maps
+    // narrower than its 64-pixel row tiles (37x37, 19x19 in the DPT head) run
+    // faster as im2col + GEMM.
+    if (input_width >= 64 && dav2_hip_conv2d_i8_supported(input_width, input_height, input_channels,
+                                                          output_channels, kernel, stride, padding)) {
+        const DeviceBuffer* tapmajor = tapmajor_weight;
+        if (!tapmajor || !*tapmajor) {
+            grow(conv_weights_, std::uint64_t(output_channels) * inner);
+            hip_check(dav2_hip_conv_weights_tapmajor(conv_weights_.as<int8_t>(), int8_weight.as<int8_t>(),
+                                                     output_channels, input_channels, kernel, ld64(inner), s),
+                      "tap-major conv weights");
+            tapmajor = &conv_weights_;
+        } else {
+            if (tapmajor->size() < std::uint64_t(output_channels) * inner)
+                throw std::invalid_argument("tap-major convolution weight is too small");
+        }
+        grow(im2col_scratch_, scratch_floats * sizeof(float));
+        ProfileScope prof(context_.profiler(), "conv2d_i8", 2.0 * rows * output_channels * inner, "OP", s);
+        dav2_conv_i8_args a{};
+        a.input = input.as<float>();
+        a.width = input_width;
+        a.height = input_height;
+        a.channels = input_channels;
+        a.kernel = kernel;
+        a.weight = tapmajor->as<int8_t>();
+        a.weight_scales = weight_scales.as<float>();
+        a.bias = has_bias ? bias.as<float>() : nullptr;
+        a.out_channels = output_channels;
+        a.out = output.as<float>();
+        a.scratch = im2col_scratch_.as<float>();
+        a.scratch_floats = scratch_floats;
+        hip_check(dav2_hip_conv2d_i8(&a, s), "implicit-GEMM convolution");
+        return;
+    }
     const std::uint32_t ld = ld64(inner);
     DeviceBuffer& packed = workspace_.packed(std::uint64_t(rows) * ld);
     DeviceBuffer& scales = workspace_.scales(std::uint64_t(rows) * sizeof(float));
     ProfileScope prof(context_.profiler(), "im2col_quantize_i8",
-                      4.0 * input_width * input_height * input_channels + 1.0 * rows * inner + 4.0 * rows, "B",
-                      context_.active_stream());
-    const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
+                      4.0 * input_width * input_height * input_channels + 1.0 * rows * inner + 4.0 * rows, "B", s);
     grow(im2col_scratch_, scratch_floats * sizeof(float));
     hip_check(dav2_hip_im2col_quantize_i8(input.as<float>(), input_width, input_height, input_channels, ow, oh,
                                           kernel, stride, static_cast<std::int32_t>(padding), packed.as<int8_t>(),
-                                          ld, scales.as<float>(), im2col_scratch_.as<float>(), scratch_floats,
-                                          context_.active_stream()),
+                                          ld, scales.as<float>(), im2col_scratch_.as<float>(), scratch_floats, s),
               "im2col quantize");
     workspace_ld_ = ld;
     linear_int8_packed(output, packed, ld, int8_weight, scales, weight_scales, bias, rows, inner, output_channels, 0u,

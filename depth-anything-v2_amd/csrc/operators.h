@@ -65,7 +65,8 @@ public:
     void conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
                      const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t input_width,
                      std::uint32_t input_height, std::uint32_t input_channels, std::uint32_t output_channels,
-                     std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding, bool has_bias);
+                     std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding, bool has_bias,
+                     const DeviceBuffer* tapmajor_weight = nullptr);
 
     void conv_transpose_nonoverlap_int8(DeviceBuffer& output, const DeviceBuffer& input,
                                         const DeviceBuffer& int8_weight, const DeviceBuffer& weight_scales,
@@ -127,6 +128,7 @@ private:
     DeviceBuffer minmax_partials_;
     DeviceBuffer interpolated_;
     DeviceBuffer im2col_scratch_;  // per-channel-group maxima for the tiled im2col kernels
+    DeviceBuffer conv_weights_;    // tap-major weights of a conv2d_int8 call that brought none
     std::uint32_t workspace_ld_ = 0;  // row stride of the int8 rows currently in the workspace
 };
 

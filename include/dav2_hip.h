@@ -96,6 +96,36 @@ typedef struct dav2_gemm_i8_args {
  * conv_transpose_int8.glsl:31-58 (:1969-1975). */
 DAV2_API int dav2_hip_gemm_i8(const dav2_gemm_i8_args* args, void* stream);
 
+/* Implicit-GEMM int8 convolution: replaces the im2col_quantize_int8.glsl +
+ * linear_int8_tiled.glsl pair of VulkanOperators::conv2d_int8
+ * (src/operators.cpp:1735-1805) for kernel 3 / stride 1 / padding 1 and
+ * kernel 1 / stride 1 / padding 0, channels % 64 == 0, out_channels % 32 == 0
+ * (dav2_hip_conv2d_i8_supported). Same output bits as
+ * dav2_hip_im2col_quantize_i8 followed by dav2_hip_gemm_i8 with
+ * DAV2_GEMM_EPI_TRANSPOSED; the im2col matrix is never stored. The weights are
+ * the GpuModel int8 rows permuted tap-major by dav2_hip_conv_weights_tapmajor:
+ * dst[n][(ky*k + kx)*channels + c] = src[n][c*k*k + ky*k + kx]. */
+typedef struct dav2_conv_i8_args {
+    const float* input;          /* CHW [channels][height][width]                  */
+    uint32_t width, height, channels;
+    uint32_t kernel;             /* 1 or 3                                         */
+    const int8_t* weight;        /* [out_channels][kernel*kernel*channels], tap-major */
+    const float* weight_scales;  /* [out_channels]                                 */
+    const float* bias;           /* [out_channels] or NULL = 0                     */
+    uint32_t out_channels;
+    float* out;                  /* CHW [out_channels][height][width]              */
+    float* scratch;              /* dav2_hip_im2col_scratch_floats() floats        */
+    uint64_t scratch_floats;
+} dav2_conv_i8_args;
+
+DAV2_API int dav2_hip_conv2d_i8_supported(uint32_t width, uint32_t height, uint32_t channels,
+                                          uint32_t out_channels, uint32_t kernel, uint32_t stride,
+                                          uint32_t padding);
+DAV2_API int dav2_hip_conv_weights_tapmajor(int8_t* dst, const int8_t* src, uint32_t out_channels,
+                                            uint32_t channels, uint32_t kernel, uint64_t ldb,
+                                            void* stream);
+DAV2_API int dav2_hip_conv2d_i8(const dav2_conv_i8_args* args, void* stream);
+
 /* Elementwise kernels. Reference: gelu.glsl, add_scaled.glsl, add.glsl, relu.glsl. */
 DAV2_API int dav2_hip_gelu(float* out, const float* input, uint64_t count, void* stream);
 DAV2_API int dav2_hip_add_scaled(float* out, const float* residual, const float* addend,

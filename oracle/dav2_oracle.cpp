@@ -217,7 +217,7 @@ struct Tensor {
     std::vector<float> data;
     uint64_t dims[4] = {0, 0, 0, 0};
     uint32_t rank = 0;
-    std::vector<int8_t> q;      // per-row int8 (reference a9 rule)
+    std::vector<int8_t> q;      // per-row int8 (reference weight quantizer rule)
     std::vector<float> qscale;  // per-row scale
 };
 

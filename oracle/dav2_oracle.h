@@ -31,26 +31,26 @@ extern "C" {
 int orc_set_threads(int threads);
 int orc_get_threads(void);
 
-/* a1: quantize_rows_int8_fused.glsl:20-55 */
+/* quantize_rows_int8_fused.glsl:20-55 */
 void orc_quantize_rows(const float* input, uint32_t rows, uint32_t columns,
                        uint32_t input_offset, int8_t* q, float* scales);
-/* a2: im2col_quantize_int8.glsl:26-83 (rows = OW*OH, K = C*k*k) */
+/* im2col_quantize_int8.glsl:26-83 (rows = OW*OH, K = C*k*k) */
 void orc_im2col_quantize(const float* input, uint32_t input_width,
                          uint32_t input_height, uint32_t input_channels,
                          uint32_t output_width, uint32_t output_height,
                          uint32_t kernel, uint32_t stride, int32_t padding,
                          int8_t* q, float* scales);
-/* a9: gpu_model.cpp:241-264, per output row */
+/* weight quantizer, gpu_model.cpp:241-264, per output row */
 void orc_quantize_weight_rows(const float* weight, uint64_t rows,
                               uint64_t columns, int8_t* q, float* scales);
-/* a9: gpu_model.cpp:210-240, ConvTranspose [IC][OC][k][k] -> rows (ky*k+kx)*OC+oc */
+/* weight layout, gpu_model.cpp:210-240, ConvTranspose [IC][OC][k][k] -> rows (ky*k+kx)*OC+oc */
 void orc_quantize_convT_weight(const float* weight, uint32_t in_channels,
                                uint32_t out_channels, uint32_t kernel,
                                int8_t* q, float* scales);
-/* a3: exact int32 accumulators, acc[m][n] = sum_k a[m][k]*b[n][k] */
+/* exact int32 accumulators, acc[m][n] = sum_k a[m][k]*b[n][k] */
 void orc_gemm_i8(const int8_t* a, const int8_t* b, uint32_t m, uint32_t n,
                  uint32_t k, int32_t* acc);
-/* a3: linear_int8_tiled.glsl:99-116 epilogue */
+/* linear_int8_tiled.glsl:99-116 epilogue */
 void orc_linear_epilogue(const int32_t* acc, const float* input_scales,
                          const float* weight_scales, const float* bias,
                          uint32_t rows, uint32_t columns,

@@ -23,7 +23,7 @@ def _announce(*what):
 
 
 # ---------------------------------------------------------------------------
-# a1 quantize_rows_int8_fused.glsl
+# quantize_rows_int8_fused.glsl
 @pytest.mark.parametrize("rows,cols,offset_rows", [(1370, 384, 0), (1370, 1024, 0), (1369, 4096, 0), (7, 8, 0),
                                                    (3, 8192, 0), (1369, 1024, 1), (1, 1536, 0)])
 def test_quantize_rows_bit_exact(gpu, lib, oracle, rows, cols, offset_rows):
@@ -59,7 +59,7 @@ def test_quantize_rows_packed_word_byte_order(gpu, lib):
 
 
 # ---------------------------------------------------------------------------
-# a2 im2col_quantize_int8.glsl
+# im2col_quantize_int8.glsl
 @pytest.mark.parametrize("c,h,w,k,s,p", [(3, 518, 518, 14, 14, 0), (3, 266, 350, 14, 14, 0), (64, 37, 37, 3, 1, 1),
                                          (96, 19, 19, 3, 2, 1), (32, 74, 74, 1, 1, 0), (5, 4, 4, 3, 1, 1),
                                          (128, 60, 52, 3, 1, 1), (1024, 10, 10, 3, 2, 1), (1024, 19, 19, 3, 1, 1),
@@ -91,7 +91,96 @@ def test_im2col_quantize_bit_exact(gpu, lib, oracle, c, h, w, k, s, p):
 
 
 # ---------------------------------------------------------------------------
-# a3 int8 GEMM (linear_int8_tiled.glsl), raw int32 accumulators
+# implicit-GEMM convolution == im2col_quantize_int8.glsl + linear_int8_tiled.glsl
+# (CHW store), bit for bit. Shapes cover every channel-tile configuration the
+# launcher picks (256/128/64/32 output channels per workgroup), maps narrower
+# than one 64-pixel tile, one-row maps and 1x1 kernels.
+@pytest.mark.parametrize("c,h,w,n,k,has_bias", [(64, 37, 37, 256, 3, True), (128, 9, 150, 32, 3, True),
+                                                (256, 166, 180, 256, 3, True), (64, 100, 300, 128, 3, False),
+                                                (64, 250, 128, 64, 3, True), (64, 1, 5, 32, 3, True),
+                                                (192, 19, 19, 96, 3, True), (64, 37, 37, 96, 1, True),
+                                                (128, 100, 330, 128, 1, True), (128, 518, 518, 32, 3, True)])
+def test_conv2d_i8_matches_im2col_gemm(gpu, pkg, lib, oracle, c, h, w, n, k, has_bias):
+    torch = gpu
+    _announce("conv2d_i8", c, h, w, n, k, has_bias)
+    assert lib.dav2_hip_conv2d_i8_supported(w, h, c, n, k, 1, (k - 1) // 2)
+    rng = np.random.default_rng(c * 31 + h + n + k)
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    x[:, h // 2, :] *= 40.0  # rows with a larger range, so scales differ between pixels
+    kk = c * k * k
+    ld = (kk + 63) // 64 * 64
+    wq, ws = oracle.quantize_weight_rows(rng.standard_normal((n, kk)).astype(np.float32) * 0.05)
+    bias = rng.standard_normal(n).astype(np.float32)
+    xd, wqd, wsd, bd = dev(torch, x), dev(torch, pad_rows(wq, ld)), dev(torch, ws), dev(torch, bias)
+    s = stream(torch)
+    n_scratch = lib.dav2_hip_im2col_scratch_floats(w, h, c)
+    scratch = empty(torch, (n_scratch,), torch.float32)
+
+    # reference path: tiled im2col + GEMM with the channel-major epilogue
+    rows = h * w
+    qd = empty(torch, (rows, ld), torch.int8)
+    sd = empty(torch, (rows,), torch.float32)
+    ok(lib, lib.dav2_hip_im2col_quantize_i8(ptr(xd), w, h, c, w, h, k, 1, (k - 1) // 2, ptr(qd), ld, ptr(sd),
+                                            ptr(scratch), n_scratch, s))
+    ref = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
+    args = _gemm_args(pkg, a=ptr(qd), lda=ld, b=ptr(wqd), ldb=ld, m=rows, n=n, k=ld, epilogue=pkg.GEMM_EPI["transposed"],
+                      a_scales=ptr(sd), b_scales=ptr(wsd), bias=ptr(bd) if has_bias else None, out=ptr(ref),
+                      out_row_stride=rows)
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(args), s))
+
+    # tap-major weights: dst[o][t*c + ic] = src[o][ic*k*k + t]
+    wt = empty(torch, (n, kk), torch.int8)
+    ok(lib, lib.dav2_hip_conv_weights_tapmajor(ptr(wt), ptr(wqd), n, c, k, ld, s))
+    want_wt = wq.reshape(n, c, k * k).transpose(0, 2, 1).reshape(n, kk)
+    assert np.array_equal(host(torch, wt), want_wt)
+
+    out = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
+    a = pkg.ConvArgs(input=ptr(xd), width=w, height=h, channels=c, kernel=k, weight=ptr(wt), weight_scales=ptr(wsd),
+                     bias=ptr(bd) if has_bias else None, out_channels=n, out=ptr(out), scratch=ptr(scratch),
+                     scratch_floats=n_scratch)
+    ok(lib, lib.dav2_hip_conv2d_i8(C.byref(a), s))
+    got, want = host(torch, out), host(torch, ref)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+        f"{np.count_nonzero(got.view(np.uint32) != want.view(np.uint32))} of {got.size} outputs differ"
+
+
+def test_conv2d_i8_matches_oracle(gpu, pkg, lib, oracle):
+    # the CPU oracle's conv2d_int8 (im2col + int8 GEMM + CHW epilogue)
+    torch = gpu
+    _announce("conv2d_i8 oracle")
+    rng = np.random.default_rng(5)
+    c, h, w, n = 64, 21, 70, 64
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    wq, ws = oracle.quantize_weight_rows(rng.standard_normal((n, c * 9)).astype(np.float32) * 0.05)
+    bias = rng.standard_normal(n).astype(np.float32)
+    want = oracle.conv2d_int8(x, wq, ws, bias, n, 3, 1, 1).reshape(n, h * w)
+    wt = wq.reshape(n, c, 9).transpose(0, 2, 1).reshape(n, c * 9)
+    n_scratch = lib.dav2_hip_im2col_scratch_floats(w, h, c)
+    scratch = empty(torch, (n_scratch,), torch.float32)
+    xd, wtd, wsd, bd = dev(torch, x), dev(torch, wt), dev(torch, ws), dev(torch, bias)
+    out = empty(torch, (n, h * w), torch.float32)
+    a = pkg.ConvArgs(input=ptr(xd), width=w, height=h, channels=c, kernel=3, weight=ptr(wtd), weight_scales=ptr(wsd),
+                     bias=ptr(bd), out_channels=n, out=ptr(out), scratch=ptr(scratch), scratch_floats=n_scratch)
+    ok(lib, lib.dav2_hip_conv2d_i8(C.byref(a), stream(torch)))
+    assert np.array_equal(host(torch, out).view(np.uint32), want.view(np.uint32))
+
+
+def test_conv2d_i8_rejects_unsupported(gpu, pkg, lib):
+    torch = gpu
+    for args in [(10, 10, 48, 32, 3, 1, 1), (10, 10, 64, 48, 3, 1, 1), (10, 10, 64, 32, 3, 2, 1), (10, 10, 64, 32, 5, 1, 2),
+                 (10, 10, 64, 32, 1, 1, 1)]:
+        assert not lib.dav2_hip_conv2d_i8_supported(*args)
+    x = torch.zeros(64 * 100, dtype=torch.float32, device="cuda")
+    a = pkg.ConvArgs(input=ptr(x), width=10, height=10, channels=48, kernel=3, weight=ptr(x), weight_scales=ptr(x),
+                     bias=None, out_channels=32, out=ptr(x), scratch=ptr(x), scratch_floats=100)
+    assert lib.dav2_hip_conv2d_i8(C.byref(a), stream(torch)) != 0
+    a.channels = 64
+    a.scratch_floats = 10  # fewer than width * height * groups
+    assert lib.dav2_hip_conv2d_i8(C.byref(a), stream(torch)) != 0
+
+
+# ---------------------------------------------------------------------------
+# int8 GEMM (linear_int8_tiled.glsl), raw int32 accumulators
 def _gemm_args(pkg, **kw):
     a = pkg.GemmArgs()
     for k, v in kw.items():
@@ -188,7 +277,7 @@ def test_gemm_rejects_bad_arguments(gpu, pkg, lib):
 
 
 # ---------------------------------------------------------------------------
-# a10 LayerNorm (+ fused quantization)
+# LayerNorm (+ fused quantization)
 @pytest.mark.parametrize("rows,cols", [(1370, 384), (1370, 1024), (4, 17), (10, 768), (3, 5000), (2, 4096)])
 def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
     torch = gpu
@@ -217,7 +306,7 @@ def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
 
 
 # ---------------------------------------------------------------------------
-# a11 attention: scores -> softmax -> values
+# attention: scores -> softmax -> values
 def _attention_gpu(torch, lib, qkv, tokens, heads, fp16):
     qd = dev(torch, qkv)
     ldt = (tokens + 7) // 8 * 8 if fp16 else tokens
@@ -350,7 +439,7 @@ def test_softmax_fp32(gpu, lib, oracle, rows, cols):
 
 
 # ---------------------------------------------------------------------------
-# a12-a16 elementwise, resize, min/max, position
+# elementwise, resize, min/max, position
 def test_elementwise_exact(gpu, lib, oracle):
     torch = gpu
     rng = np.random.default_rng(1)
