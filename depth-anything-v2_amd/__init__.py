@@ -96,7 +96,10 @@ class ConvArgs(C.Structure):
     _fields_ = [("input", C.c_void_p), ("width", C.c_uint32), ("height", C.c_uint32), ("channels", C.c_uint32),
                 ("kernel", C.c_uint32), ("weight", C.c_void_p), ("weight_scales", C.c_void_p), ("bias", C.c_void_p),
                 ("out_channels", C.c_uint32), ("out", C.c_void_p), ("scratch", C.c_void_p),
-                ("scratch_floats", C.c_uint64)]
+                ("scratch_floats", C.c_uint64), ("flags", C.c_uint32), ("residual", C.c_void_p)]
+
+
+CONV_RELU_INPUT, CONV_RELU_OUTPUT = 1, 2
 
 
 vp, u32, i32, u64, f32, sz = C.c_void_p, C.c_uint32, C.c_int32, C.c_uint64, C.c_float, C.c_size_t
@@ -142,6 +145,7 @@ PROTOTYPES = {
     "dav2_hip_conv2d_i8_supported": (C.c_int, [u32, u32, u32, u32, u32, u32, u32]),
     "dav2_hip_conv_weights_tapmajor": (C.c_int, [vp, vp, u32, u32, u32, u64, vp]),
     "dav2_hip_conv2d_i8": (C.c_int, [C.POINTER(ConvArgs), vp]),
+    "dav2_hip_conv1x1_narrow_i8": (C.c_int, [vp, u32, u32, u32, vp, u32, vp, vp, u32, vp, vp, u32, vp]),
     "dav2_hip_layer_norm": (C.c_int, [vp, vp, vp, vp, u32, u32, f32, vp]),
     "dav2_hip_layer_norm_quantize_i8": (C.c_int, [vp, u32, vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "dav2_hip_gemm_i8": (C.c_int, [C.POINTER(GemmArgs), vp]),

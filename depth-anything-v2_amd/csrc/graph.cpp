@@ -139,7 +139,7 @@ DptHead::DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operator
 
 FeatureMap DptHead::conv(const FeatureMap& in, const std::string& weight, const std::string& bias,
                          std::uint32_t oc, std::uint32_t k, std::uint32_t stride, std::uint32_t pad, bool has_bias,
-                         Arena& arena, const std::string& slot) {
+                         Arena& arena, const std::string& slot, const ConvFusion& fusion) {
     // dpt.cpp:479-535, every convolution through conv2d_int8
     FeatureMap out;
     out.width = (in.width + 2 * pad - k) / stride + 1;
@@ -150,24 +150,23 @@ FeatureMap DptHead::conv(const FeatureMap& in, const std::string& weight, const 
     if (!w.int8_buffer) throw std::runtime_error("convolution weight is not int8: " + weight);
     const DeviceBuffer& b = has_bias ? weights_.tensor(bias).buffer : zero_bias_;
     ops_.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc, k,
-                     stride, pad, has_bias, &w.int8_tapmajor);
+                     stride, pad, has_bias, &w.int8_tapmajor, fusion);
     return out;
 }
 
 FeatureMap DptHead::residual_unit(const FeatureMap& in, const std::string& prefix, Arena& arena,
                                   const std::string& slot) {
-    // dpt.cpp:537-572: relu -> conv3x3 -> relu -> conv3x3 -> + input
-    const std::uint32_t count = static_cast<std::uint32_t>(in.elements());
-    FeatureMap act = in;
-    act.buffer = &arena.get("dpt.ru.act", in.elements() * sizeof(float));
-    ops_.relu(*act.buffer, *in.buffer, count);
-    FeatureMap first = conv(act, prefix + ".conv1.weight", prefix + ".conv1.bias", in.channels, 3, 1, 1, true, arena,
-                            "dpt.ru.first");
-    ops_.relu(*first.buffer, *first.buffer, count);
-    FeatureMap second = conv(first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.channels, 3, 1, 1, true,
-                             arena, slot);
-    ops_.add(*second.buffer, *second.buffer, *in.buffer, count);
-    return second;
+    // dpt.cpp:537-572: relu -> conv3x3 -> relu -> conv3x3 -> + input, the
+    // ReLUs and the residual add folded into the two convolutions.
+    ConvFusion first_fusion;
+    first_fusion.relu_input = true;
+    first_fusion.relu_output = true;
+    FeatureMap first = conv(in, prefix + ".conv1.weight", prefix + ".conv1.bias", in.channels, 3, 1, 1, true, arena,
+                            "dpt.ru.first", first_fusion);
+    ConvFusion second_fusion;
+    second_fusion.residual = in.buffer;
+    return conv(first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.channels, 3, 1, 1, true, arena, slot,
+                second_fusion);
 }
 
 FeatureMap DptHead::fusion(const FeatureMap& path, const FeatureMap* skip, const std::string& prefix,
@@ -241,19 +240,22 @@ void DptHead::forward(DeviceBuffer* features[4], std::uint32_t pw, std::uint32_t
                         ph * 14, F / 2};
         ops_.bilinear_align_true(*full.buffer, *path.buffer, path.width, path.height, full.width, full.height,
                                  full.channels);
+        ConvFusion relu_after;
+        relu_after.relu_output = true;
         FeatureMap head = conv(full, "depth_head.scratch.output_conv2.0.weight",
-                               "depth_head.scratch.output_conv2.0.bias", 32, 3, 1, 1, true, arena, "dpt.out2");
-        ops_.relu(*head.buffer, *head.buffer, static_cast<std::uint32_t>(head.elements()));
+                               "depth_head.scratch.output_conv2.0.bias", 32, 3, 1, 1, true, arena, "dpt.out2",
+                               relu_after);
+        // output_conv2.2 (1x1, 32 -> 1) and the final ReLU in one pass; the
+        // pre-ReLU logits of the last image go to pre_relu when asked.
         const std::uint64_t pixels = std::uint64_t(pw) * 14 * ph * 14;
         DeviceBuffer out = DeviceBuffer::view(depth + b * pixels, pixels * sizeof(float));
-        FeatureMap result{&out, pw * 14, ph * 14, 1};
-        FeatureMap logits = conv(head, "depth_head.scratch.output_conv2.2.weight",
-                                 "depth_head.scratch.output_conv2.2.bias", 1, 1, 1, 0, true, arena, "dpt.logits");
-        if (pre_relu && b + 1 == batch)
-            hip_check(hipMemcpyAsync(pre_relu, logits.buffer->data(), pixels * sizeof(float), hipMemcpyDeviceToDevice,
-                                     ops_.context().active_stream()),
-                      "pre-ReLU copy");
-        ops_.relu(*result.buffer, *logits.buffer, static_cast<std::uint32_t>(pixels));
+        DeviceBuffer logits;
+        if (pre_relu && b + 1 == batch) logits = DeviceBuffer::view(pre_relu, pixels * sizeof(float));
+        const GpuTensor& w3 = weights_.tensor("depth_head.scratch.output_conv2.2.weight");
+        if (!w3.int8_buffer) throw std::runtime_error("output_conv2.2 weight is not int8");
+        ops_.conv1x1_narrow_int8(out, *head.buffer, w3.int8_buffer, w3.int8_ld, w3.int8_scales,
+                                 weights_.tensor("depth_head.scratch.output_conv2.2.bias").buffer, head.width,
+                                 head.height, head.channels, 1, true, relu_after, logits ? &logits : nullptr);
     }
 }
 

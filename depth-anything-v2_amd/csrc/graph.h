@@ -76,7 +76,7 @@ public:
 private:
     FeatureMap conv(const FeatureMap& input, const std::string& weight, const std::string& bias,
                     std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding,
-                    bool has_bias, Arena& arena, const std::string& slot);
+                    bool has_bias, Arena& arena, const std::string& slot, const ConvFusion& fusion = ConvFusion{});
     FeatureMap residual_unit(const FeatureMap& input, const std::string& prefix, Arena& arena,
                              const std::string& slot);
     FeatureMap fusion(const FeatureMap& path, const FeatureMap* skip, const std::string& prefix,

@@ -66,7 +66,7 @@ DAV2_DEV float row_scale(float absmax) { return fmaxf(absmax / 127.0f, 1.0e-8f);
 constexpr uint32_t kGroupChannels = 32;
 inline uint32_t channel_groups(uint32_t channels) { return (channels + kGroupChannels - 1) / kGroupChannels; }
 hipError_t launch_channel_group_absmax(const float* x, uint32_t channels, uint64_t plane, float* partial,
-                                       hipStream_t stream);
+                                       bool relu, hipStream_t stream);
 
 // e^a by Cody-Waite range reduction (a = n ln2 + r, |r| <= ln2/2, ln2 split
 // into a 16-bit head and a tail) and the degree-7 Taylor polynomial of e^r in

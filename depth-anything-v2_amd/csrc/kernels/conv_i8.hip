@@ -31,6 +31,7 @@
 // hides behind the quantize and MFMA work. One LDS-only barrier per tap.
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "dav2_hip.h"
@@ -53,6 +54,8 @@ struct ConvParams {
     const float* w_scales;
     const float* bias;     // nullable
     float* out;            // CHW [N][plane]
+    const float* residual; // nullable, CHW [N][plane]
+    uint32_t flags;        // DAV2_CONV_*
 };
 
 // Workgroup barrier that orders LDS only: waits for this wave's LDS
@@ -87,7 +90,7 @@ DAV2_DEV uint32_t quant4(float a, float b, float c, float d, float inv) {
 // rows one MFMA operand read touches cover all banks once.
 DAV2_DEV uint32_t a_offset(uint32_t p, uint32_t c) { return p * 64u + ((c ^ ((p >> 2) & 3u)) << 4); }
 
-template <int KS, int BN, int WM, int WN>
+template <int KS, int BN, int WM, int WN, bool RELU_IN>
 __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
     constexpr int kRowsT = KS;                   // input rows per channel in the window
     constexpr int kColsT = kPix + KS - 1;        // input columns per row (halo for 3x3)
@@ -175,6 +178,7 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
     const char* xbase = reinterpret_cast<const char*>(g.x);
     float xs[kLoads];
     float xh[2] = {0.0f, 0.0f};
+    constexpr bool relu_in = RELU_IN;
     // Byte offsets of the window rows within a channel plane (clamped).
     uint32_t row4[kRowsT];
 #pragma unroll
@@ -220,7 +224,8 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
             const uint32_t c = R / kRowsT, r = R - c * kRowsT;
             const int gy = static_cast<int>(y) + static_cast<int>(r) - KS / 2;
             const bool ok = col_ok && gy >= 0 && gy < static_cast<int>(nrows);
-            xt[c * kPlaneT + r * kColsT + (KS == 3 ? 1u : 0u) + lane] = ok ? xs[j] : 0.0f;
+            const float v = ok ? xs[j] : 0.0f;
+            xt[c * kPlaneT + r * kColsT + (KS == 3 ? 1u : 0u) + lane] = relu_in ? fmaxf(v, 0.0f) : v;
         }
         if constexpr (KS == 3) {
 #pragma unroll
@@ -232,7 +237,8 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
                     const int gx = (idx & 1u) ? static_cast<int>(x0) + kPix : static_cast<int>(x0) - 1;
                     const bool ok =
                         gy >= 0 && gy < static_cast<int>(g.height) && gx >= 0 && gx < static_cast<int>(g.width);
-                    xt[c * kPlaneT + r * kColsT + ((idx & 1u) ? kColsT - 1u : 0u)] = ok ? xh[h] : 0.0f;
+                    const float v = ok ? xh[h] : 0.0f;
+                    xt[c * kPlaneT + r * kColsT + ((idx & 1u) ? kColsT - 1u : 0u)] = relu_in ? fmaxf(v, 0.0f) : v;
                 }
             }
         }
@@ -335,25 +341,84 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
         }
     }
 
-    // ---- epilogue: out[ch][pixel] = ((acc * s_pixel) * s_weight) + bias ---
+    // ---- epilogue: out[ch][pixel] = ((acc * s_pixel) * s_weight) + bias,
+    // then + residual (add.glsl) and max(., 0) (relu.glsl) when asked; the
+    // flag tests sit outside the unrolled store loops.
     // Accumulator r of lane l in block (i, j): channel 16i + 4(l/16) + r,
     // pixel 16j + l%16 of the wave's sub-tile.
+    auto epilogue = [&](auto residual_tag, auto relu_tag) {
+        constexpr bool kResidual = decltype(residual_tag)::value, kRelu = decltype(relu_tag)::value;
 #pragma unroll
-    for (int j = 0; j < PB; ++j) {
-        const uint32_t p = wm * PW + 16u * j + (lane & 15u);
-        if (p >= valid) continue;
-        const float sp = sc_lds[p];
+        for (int j = 0; j < PB; ++j) {
+            const uint32_t p = wm * PW + 16u * j + (lane & 15u);
+            if (p >= valid) continue;
+            const float sp = sc_lds[p];
 #pragma unroll
-        for (int i = 0; i < NB; ++i)
+            for (int i = 0; i < NB; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t cl = wn * NW + 16u * i + 4u * (lane >> 4) + r;
-                float v = static_cast<float>(acc[i][j][r]);
-                v = v * sp;
-                v = v * wsc_lds[cl];
-                v = v + bias_lds[cl];
-                g.out[static_cast<uint64_t>(nb * BN + cl) * g.plane + mbase + p] = v;
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t cl = wn * NW + 16u * i + 4u * (lane >> 4) + r;
+                    float v = static_cast<float>(acc[i][j][r]);
+                    v = v * sp;
+                    v = v * wsc_lds[cl];
+                    v = v + bias_lds[cl];
+                    const uint64_t idx = static_cast<uint64_t>(nb * BN + cl) * g.plane + mbase + p;
+                    if (kResidual) v = v + g.residual[idx];
+                    if (kRelu) v = fmaxf(v, 0.0f);
+                    g.out[idx] = v;
+                }
+        }
+    };
+    const bool relu_out = (g.flags & DAV2_CONV_RELU_OUTPUT) != 0;
+    if (g.residual) {
+        if (relu_out) epilogue(std::true_type{}, std::true_type{});
+        else epilogue(std::true_type{}, std::false_type{});
+    } else {
+        if (relu_out) epilogue(std::false_type{}, std::true_type{});
+        else epilogue(std::false_type{}, std::false_type{});
+    }
+}
+
+// 1x1 convolution to at most kNarrowN output channels: one thread per pixel
+// holds its (at most 64) input values, takes their absmax, quantizes them with
+// the im2col rule rne(clamp(x * (1/s))) and forms the dot products on the
+// VALU; the epilogue is the GEMM's ((acc * s) * s_w) + bias.
+constexpr uint32_t kNarrowN = 4, kNarrowC = 64;
+
+__global__ __launch_bounds__(256) void conv1x1_narrow_kernel(const float* __restrict__ x, uint64_t plane,
+                                                             uint32_t channels, const int8_t* __restrict__ w,
+                                                             uint32_t ldw, const float* __restrict__ w_scales,
+                                                             const float* __restrict__ bias, uint32_t n,
+                                                             float* __restrict__ out, float* __restrict__ pre_relu,
+                                                             uint32_t flags) {
+    const uint64_t p = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    if (p >= plane) return;
+    const bool relu_in = (flags & DAV2_CONV_RELU_INPUT) != 0, relu_out = (flags & DAV2_CONV_RELU_OUTPUT) != 0;
+    float v[kNarrowC];
+    float m = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < kNarrowC; ++c) {
+        if (c < channels) {
+            const float t = x[c * plane + p];
+            v[c] = relu_in ? fmaxf(t, 0.0f) : t;
+            m = fmaxf(m, fabsf(v[c]));
+        }
+    }
+    const float s = row_scale(m), inv = 1.0f / s;
+    int q[kNarrowC];
+#pragma unroll
+    for (uint32_t c = 0; c < kNarrowC; ++c) q[c] = c < channels ? quantize_rne(v[c] * inv) : 0;
+    for (uint32_t o = 0; o < n; ++o) {
+        int32_t acc = 0;
+#pragma unroll
+        for (uint32_t c = 0; c < kNarrowC; ++c)
+            if (c < channels) acc += q[c] * static_cast<int32_t>(w[static_cast<uint64_t>(o) * ldw + c]);
+        float r = static_cast<float>(acc);
+        r = r * s;
+        r = r * w_scales[o];
+        r = r + (bias ? bias[o] : 0.0f);
+        if (pre_relu) pre_relu[o * plane + p] = r;
+        out[o * plane + p] = relu_out ? fmaxf(r, 0.0f) : r;
     }
 }
 
@@ -372,7 +437,10 @@ __global__ __launch_bounds__(256) void weights_tapmajor_kernel(int8_t* __restric
 
 template <int KS, int BN, int WM, int WN>
 void launch(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
-    hipLaunchKernelGGL((conv_i8_kernel<KS, BN, WM, WN>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+    if (g.flags & DAV2_CONV_RELU_INPUT)
+        hipLaunchKernelGGL((conv_i8_kernel<KS, BN, WM, WN, true>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+    else
+        hipLaunchKernelGGL((conv_i8_kernel<KS, BN, WM, WN, false>), dim3(tiles, n / BN), dim3(256), 0, s, g);
 }
 
 template <int KS>
@@ -423,7 +491,9 @@ int dav2_hip_conv2d_i8(const dav2_conv_i8_args* a, void* stream) {
         static_cast<uint64_t>(a->out_channels) * a->kernel * a->kernel * a->channels >= (1ull << 32))
         return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e = launch_channel_group_absmax(a->input, a->channels, plane, a->scratch, s);
+    if (a->flags & ~static_cast<uint32_t>(DAV2_CONV_RELU_INPUT | DAV2_CONV_RELU_OUTPUT)) return hipErrorInvalidValue;
+    hipError_t e = launch_channel_group_absmax(a->input, a->channels, plane, a->scratch,
+                                               (a->flags & DAV2_CONV_RELU_INPUT) != 0, s);
     if (e != hipSuccess) return e;
     ConvParams g;
     g.x = a->input;
@@ -438,8 +508,25 @@ int dav2_hip_conv2d_i8(const dav2_conv_i8_args* a, void* stream) {
     g.w_scales = a->weight_scales;
     g.bias = a->bias;
     g.out = a->out;
+    g.residual = a->residual;
+    g.flags = a->flags;
     if (a->kernel == 3) launch_ks<3>(g, g.tiles_x * a->height, a->out_channels, s);
     else launch_ks<1>(g, ceil_div(plane, kPix), a->out_channels, s);
+    return hipGetLastError();
+}
+
+int dav2_hip_conv1x1_narrow_i8(const float* input, uint32_t width, uint32_t height, uint32_t channels,
+                               const int8_t* weight, uint32_t ldw, const float* weight_scales, const float* bias,
+                               uint32_t out_channels, float* out, float* pre_relu, uint32_t flags, void* stream) {
+    const uint64_t plane = static_cast<uint64_t>(width) * height;
+    if (plane == 0 || out_channels == 0) return hipSuccess;
+    if (!input || !weight || !weight_scales || !out || channels == 0 || channels > kNarrowC ||
+        out_channels > kNarrowN || ldw < channels ||
+        (flags & ~static_cast<uint32_t>(DAV2_CONV_RELU_INPUT | DAV2_CONV_RELU_OUTPUT)))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(conv1x1_narrow_kernel, dim3(ceil_div(plane, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), input, plane, channels, weight, ldw, weight_scales, bias,
+                       out_channels, out, pre_relu, flags);
     return hipGetLastError();
 }
 

@@ -175,6 +175,9 @@ constexpr int kHalo = kTile + 2;
 
 // Per-pixel maxima of |x| over channel groups of kGroupChannels:
 // partial[g][p] = max over c in group g of |x[c][p]|.
+// RELU: maxima of |max(x, 0)| = max(x, 0), for a map that a consumer reads
+// through a ReLU.
+template <bool RELU>
 __global__ __launch_bounds__(256) void channel_group_absmax_kernel(const float* __restrict__ x, uint32_t C,
                                                                    uint64_t plane, float* __restrict__ partial) {
     const uint64_t p = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
@@ -182,16 +185,41 @@ __global__ __launch_bounds__(256) void channel_group_absmax_kernel(const float* 
     const uint32_t c0 = blockIdx.y * kGroupChannels;
     const uint32_t c1 = min(C, c0 + kGroupChannels);
     const float* src = x + c0 * plane + p;
+    auto mag = [](float v) { return RELU ? fmaxf(v, 0.0f) : fabsf(v); };
     float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
     uint32_t c = c0;
     for (; c + 4 <= c1; c += 4, src += 4 * plane) {
-        m0 = fmaxf(m0, fabsf(src[0]));
-        m1 = fmaxf(m1, fabsf(src[plane]));
-        m2 = fmaxf(m2, fabsf(src[2 * plane]));
-        m3 = fmaxf(m3, fabsf(src[3 * plane]));
+        m0 = fmaxf(m0, mag(src[0]));
+        m1 = fmaxf(m1, mag(src[plane]));
+        m2 = fmaxf(m2, mag(src[2 * plane]));
+        m3 = fmaxf(m3, mag(src[3 * plane]));
     }
-    for (; c < c1; ++c, src += plane) m0 = fmaxf(m0, fabsf(src[0]));
+    for (; c < c1; ++c, src += plane) m0 = fmaxf(m0, mag(src[0]));
     partial[blockIdx.y * plane + p] = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+}
+
+// Row scales of any im2col geometry from the channel-group maxima: the
+// maximum over the k x k input positions of output pixel r (positions in the
+// zero padding contribute nothing) is the absmax of im2col row r.
+__global__ __launch_bounds__(256) void window_scale_kernel(const float* __restrict__ partial, uint32_t groups,
+                                                           uint64_t plane, uint32_t iw, uint32_t ih, uint32_t ow,
+                                                           uint32_t rows, uint32_t k, uint32_t stride, int32_t pad,
+                                                           float* __restrict__ scales) {
+    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
+    if (r >= rows) return;
+    const uint32_t oy = r / ow, ox = r - oy * ow;
+    float m = 0.0f;
+    for (uint32_t ky = 0; ky < k; ++ky) {
+        const int32_t iy = static_cast<int32_t>(oy * stride + ky) - pad;
+        if (iy < 0 || iy >= static_cast<int32_t>(ih)) continue;
+        for (uint32_t kx = 0; kx < k; ++kx) {
+            const int32_t ix = static_cast<int32_t>(ox * stride + kx) - pad;
+            if (ix < 0 || ix >= static_cast<int32_t>(iw)) continue;
+            const float* src = partial + static_cast<uint64_t>(iy) * iw + static_cast<uint32_t>(ix);
+            for (uint32_t g = 0; g < groups; ++g) m = fmaxf(m, src[g * plane]);
+        }
+    }
+    scales[r] = row_scale(m);
 }
 
 __global__ __launch_bounds__(256) void im2col3x3_kernel(const float* __restrict__ x, const float* __restrict__ partial,
@@ -355,6 +383,11 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
             wv[j] = weight[min(lane + 64u * j, last)];
             bv[j] = bias[min(lane + 64u * j, last)];
         }
+        // Tie the row values to the weight and bias loads so the compiler
+        // cannot sink those loads below the reductions (a second memory
+        // round trip): the sums below then start after all three arrived.
+#pragma unroll
+        for (int j = 0; j < kKept; ++j) asm volatile("" : "+v"(v[j]) : "v"(wv[j]), "v"(bv[j]));
 #pragma unroll
         for (int j = 0; j < kKept; ++j) {
             const bool in = lane + 64u * j < columns;
@@ -441,9 +474,10 @@ hipError_t launch_layer_norm(const float* in, const float* w, const float* b, ui
 }  // namespace
 
 hipError_t dav2k::launch_channel_group_absmax(const float* x, uint32_t channels, uint64_t plane, float* partial,
-                                              hipStream_t stream) {
-    hipLaunchKernelGGL(channel_group_absmax_kernel, dim3(ceil_div(plane, 256), channel_groups(channels)), dim3(256), 0,
-                       stream, x, channels, plane, partial);
+                                              bool relu, hipStream_t stream) {
+    const dim3 grid(ceil_div(plane, 256), channel_groups(channels));
+    if (relu) hipLaunchKernelGGL(channel_group_absmax_kernel<true>, grid, dim3(256), 0, stream, x, channels, plane, partial);
+    else hipLaunchKernelGGL(channel_group_absmax_kernel<false>, grid, dim3(256), 0, stream, x, channels, plane, partial);
     return hipGetLastError();
 }
 
@@ -514,9 +548,10 @@ int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32
                        output_width == input_width && output_height == input_height;
     const bool fast1 = kernel == 1 && stride == 1 && padding == 0 && output_width == input_width &&
                        output_height == input_height;
-    if ((fast3 || fast1) && scratch && scratch_floats >= plane * groups && input_height <= 65535u) {
-        hipLaunchKernelGGL(channel_group_absmax_kernel, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s, input,
-                           input_channels, plane, scratch);
+    const bool have_partial = scratch && scratch_floats >= plane * groups;
+    if ((fast3 || fast1) && have_partial && input_height <= 65535u) {
+        hipLaunchKernelGGL(channel_group_absmax_kernel<false>, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s,
+                           input, input_channels, plane, scratch);
         // Enough workgroups to fill the chip: split the channel chunks of
         // small maps over blockIdx.z (each split recomputes the 64 scales).
         if (fast3) {
@@ -537,8 +572,16 @@ int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32
         }
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(im2col_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
-                       s, g, rows, scales);
+    if (have_partial) {
+        // Scales from the channel-group maxima (same values, one thread per row).
+        hipLaunchKernelGGL(channel_group_absmax_kernel<false>, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s,
+                           input, input_channels, plane, scratch);
+        hipLaunchKernelGGL(window_scale_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, scratch, groups, plane,
+                           input_width, input_height, output_width, rows, kernel, stride, padding, scales);
+    } else {
+        hipLaunchKernelGGL(im2col_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
+                           s, g, rows, scales);
+    }
     const uint32_t ldq_words = ldq / 4u;
     const uint64_t total = rows64 * ldq_words;
     hipLaunchKernelGGL(im2col_quantize_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, g, rows,

@@ -319,7 +319,8 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
                                const DeviceBuffer& weight_scales, const DeviceBuffer& bias,
                                std::uint32_t input_width, std::uint32_t input_height, std::uint32_t input_channels,
                                std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
-                               std::uint32_t padding, bool has_bias, const DeviceBuffer* tapmajor_weight) {
+                               std::uint32_t padding, bool has_bias, const DeviceBuffer* tapmajor_weight,
+                               const ConvFusion& fusion) {
     if (input_width == 0 || input_height == 0 || input_channels == 0 || output_channels == 0 || kernel == 0 ||
         stride == 0 || input_width + 2u * padding < kernel || input_height + 2u * padding < kernel)
         throw std::invalid_argument("invalid INT8 convolution dimensions");
@@ -333,6 +334,7 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     require_bytes(weight_scales, output_channels, "convolution weight scale");
     require_bytes(bias, has_bias ? output_channels : 1u, "convolution bias");
     require_bytes(output, std::uint64_t(rows) * output_channels, "output");
+    if (fusion.residual) require_bytes(*fusion.residual, std::uint64_t(rows) * output_channels, "residual");
     const hipStream_t s = context_.active_stream();
     const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
     // Implicit GEMM: same bits as im2col + GEMM, no im2col matrix. Maps
@@ -366,8 +368,18 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
         a.out = output.as<float>();
         a.scratch = im2col_scratch_.as<float>();
         a.scratch_floats = scratch_floats;
+        a.flags = (fusion.relu_input ? DAV2_CONV_RELU_INPUT : 0u) | (fusion.relu_output ? DAV2_CONV_RELU_OUTPUT : 0u);
+        a.residual = fusion.residual ? fusion.residual->as<float>() : nullptr;
         hip_check(dav2_hip_conv2d_i8(&a, s), "implicit-GEMM convolution");
         return;
+    }
+    // im2col + GEMM, with the fused steps as separate passes.
+    const DeviceBuffer* src = &input;
+    if (fusion.relu_input) {
+        const std::uint32_t count = input_width * input_height * input_channels;
+        grow(conv_act_, std::uint64_t(count) * sizeof(float));
+        relu(conv_act_, input, count);
+        src = &conv_act_;
     }
     const std::uint32_t ld = ld64(inner);
     DeviceBuffer& packed = workspace_.packed(std::uint64_t(rows) * ld);
@@ -375,13 +387,44 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     ProfileScope prof(context_.profiler(), "im2col_quantize_i8",
                       4.0 * input_width * input_height * input_channels + 1.0 * rows * inner + 4.0 * rows, "B", s);
     grow(im2col_scratch_, scratch_floats * sizeof(float));
-    hip_check(dav2_hip_im2col_quantize_i8(input.as<float>(), input_width, input_height, input_channels, ow, oh,
+    hip_check(dav2_hip_im2col_quantize_i8(src->as<float>(), input_width, input_height, input_channels, ow, oh,
                                           kernel, stride, static_cast<std::int32_t>(padding), packed.as<int8_t>(),
                                           ld, scales.as<float>(), im2col_scratch_.as<float>(), scratch_floats, s),
               "im2col quantize");
     workspace_ld_ = ld;
     linear_int8_packed(output, packed, ld, int8_weight, scales, weight_scales, bias, rows, inner, output_channels, 0u,
                        rows, true, has_bias);
+    const std::uint32_t out_count = rows * output_channels;
+    if (fusion.residual) add(output, output, *fusion.residual, out_count);
+    if (fusion.relu_output) relu(output, output, out_count);
+}
+
+void HipOperators::conv1x1_narrow_int8(DeviceBuffer& output, const DeviceBuffer& input,
+                                       const DeviceBuffer& int8_weight, std::uint32_t weight_ld,
+                                       const DeviceBuffer& weight_scales, const DeviceBuffer& bias,
+                                       std::uint32_t width, std::uint32_t height, std::uint32_t channels,
+                                       std::uint32_t output_channels, bool has_bias, const ConvFusion& fusion,
+                                       DeviceBuffer* pre_relu) {
+    if (width == 0 || height == 0 || channels == 0 || channels > 64 || output_channels == 0 || output_channels > 4 ||
+        weight_ld < channels || fusion.residual)
+        throw std::invalid_argument("invalid narrow 1x1 INT8 convolution");
+    const std::uint64_t plane = std::uint64_t(width) * height;
+    require_bytes(input, plane * channels, "convolution input");
+    if (int8_weight.size() < std::uint64_t(output_channels) * weight_ld)
+        throw std::invalid_argument("INT8 convolution weight is too small");
+    require_bytes(weight_scales, output_channels, "convolution weight scale");
+    if (has_bias) require_bytes(bias, output_channels, "convolution bias");
+    require_bytes(output, plane * output_channels, "output");
+    if (pre_relu) require_bytes(*pre_relu, plane * output_channels, "pre-ReLU output");
+    const hipStream_t s = context_.active_stream();
+    ProfileScope prof(context_.profiler(), "conv1x1_narrow_i8", 4.0 * plane * (channels + output_channels), "B", s);
+    const std::uint32_t flags =
+        (fusion.relu_input ? DAV2_CONV_RELU_INPUT : 0u) | (fusion.relu_output ? DAV2_CONV_RELU_OUTPUT : 0u);
+    hip_check(dav2_hip_conv1x1_narrow_i8(input.as<float>(), width, height, channels, int8_weight.as<int8_t>(), weight_ld,
+                                         weight_scales.as<float>(), has_bias ? bias.as<float>() : nullptr,
+                                         output_channels, output.as<float>(), pre_relu ? pre_relu->as<float>() : nullptr,
+                                         flags, s),
+              "narrow 1x1 convolution");
 }
 
 // src/operators.cpp:1908-1976

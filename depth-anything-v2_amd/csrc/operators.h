@@ -21,6 +21,15 @@ namespace dav2 {
 // Mirrors the InferBridge native Precision enum used by the reference.
 enum class Precision { fp32, fp16, int8 };
 
+// Work folded into a convolution: a ReLU on its input, a residual added to its
+// output, then a ReLU on the result (relu.glsl / add.glsl semantics, the
+// order the DPT residual units apply them in).
+struct ConvFusion {
+    bool relu_input = false;
+    bool relu_output = false;
+    const DeviceBuffer* residual = nullptr;
+};
+
 // Reusable int8 activation workspace (role of the reference's
 // Int8ActivationWorkspace): packed rows + per-row scales, grown on demand.
 class Int8Workspace {
@@ -66,7 +75,16 @@ public:
                      const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t input_width,
                      std::uint32_t input_height, std::uint32_t input_channels, std::uint32_t output_channels,
                      std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding, bool has_bias,
-                     const DeviceBuffer* tapmajor_weight = nullptr);
+                     const DeviceBuffer* tapmajor_weight = nullptr, const ConvFusion& fusion = ConvFusion{});
+
+    // 1x1 convolution to at most 4 output channels from at most 64 (the DPT
+    // head's last layer); pre_relu, when given, receives the output before
+    // fusion.relu_output. No residual.
+    void conv1x1_narrow_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+                             std::uint32_t weight_ld, const DeviceBuffer& weight_scales, const DeviceBuffer& bias,
+                             std::uint32_t width, std::uint32_t height, std::uint32_t channels,
+                             std::uint32_t output_channels, bool has_bias, const ConvFusion& fusion,
+                             DeviceBuffer* pre_relu);
 
     void conv_transpose_nonoverlap_int8(DeviceBuffer& output, const DeviceBuffer& input,
                                         const DeviceBuffer& int8_weight, const DeviceBuffer& weight_scales,
@@ -129,6 +147,7 @@ private:
     DeviceBuffer interpolated_;
     DeviceBuffer im2col_scratch_;  // per-channel-group maxima for the tiled im2col kernels
     DeviceBuffer conv_weights_;    // tap-major weights of a conv2d_int8 call that brought none
+    DeviceBuffer conv_act_;        // ReLU of a conv2d_int8 input on the im2col path
     std::uint32_t workspace_ld_ = 0;  // row stride of the int8 rows currently in the workspace
 };
 

@@ -37,8 +37,9 @@ DAV2_API int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset
 /* Replaces im2col_quantize_int8.glsl:26-83 (src/operators.cpp:1284-1298,
  * :1787-1801, :1946-1960). CHW input; rows = output_width*output_height.
  * scratch (optional, dav2_hip_im2col_scratch_floats() floats) enables the
- * tiled 3x3-stride-1 and 1x1 kernels; without it the generic gather runs.
- * Both produce the same bytes. */
+ * tiled 3x3-stride-1 and 1x1 kernels and, for other geometries, row scales
+ * from per-pixel channel-group maxima; without it the generic gather runs.
+ * All produce the same bytes. */
 DAV2_API uint64_t dav2_hip_im2col_scratch_floats(uint32_t input_width, uint32_t input_height,
                                                  uint32_t input_channels);
 DAV2_API int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width,
@@ -105,6 +106,11 @@ DAV2_API int dav2_hip_gemm_i8(const dav2_gemm_i8_args* args, void* stream);
  * DAV2_GEMM_EPI_TRANSPOSED; the im2col matrix is never stored. The weights are
  * the GpuModel int8 rows permuted tap-major by dav2_hip_conv_weights_tapmajor:
  * dst[n][(ky*k + kx)*channels + c] = src[n][c*k*k + ky*k + kx]. */
+enum {
+    DAV2_CONV_RELU_INPUT = 1,   /* convolve max(input, 0) (relu.glsl before the conv)  */
+    DAV2_CONV_RELU_OUTPUT = 2   /* out = max(out, 0) after the residual (relu.glsl)     */
+};
+
 typedef struct dav2_conv_i8_args {
     const float* input;          /* CHW [channels][height][width]                  */
     uint32_t width, height, channels;
@@ -116,6 +122,8 @@ typedef struct dav2_conv_i8_args {
     float* out;                  /* CHW [out_channels][height][width]              */
     float* scratch;              /* dav2_hip_im2col_scratch_floats() floats        */
     uint64_t scratch_floats;
+    uint32_t flags;              /* DAV2_CONV_*                                    */
+    const float* residual;       /* NULL, or CHW like out: out = conv + residual   */
 } dav2_conv_i8_args;
 
 DAV2_API int dav2_hip_conv2d_i8_supported(uint32_t width, uint32_t height, uint32_t channels,
@@ -125,6 +133,18 @@ DAV2_API int dav2_hip_conv_weights_tapmajor(int8_t* dst, const int8_t* src, uint
                                             uint32_t channels, uint32_t kernel, uint64_t ldb,
                                             void* stream);
 DAV2_API int dav2_hip_conv2d_i8(const dav2_conv_i8_args* args, void* stream);
+
+/* 1x1 convolution to a few output channels (out_channels <= 4, channels <=
+ * 64), the DPT head's last layer (dpt.cpp:838-855 routed through the int8
+ * convolution): same bits as dav2_hip_im2col_quantize_i8 + dav2_hip_gemm_i8
+ * (DAV2_GEMM_EPI_TRANSPOSED), one thread per pixel. weight is the GpuModel
+ * int8 layout [out_channels][ldw]. flags as above (no residual); pre_relu
+ * (optional) receives the output before DAV2_CONV_RELU_OUTPUT. */
+DAV2_API int dav2_hip_conv1x1_narrow_i8(const float* input, uint32_t width, uint32_t height,
+                                        uint32_t channels, const int8_t* weight, uint32_t ldw,
+                                        const float* weight_scales, const float* bias,
+                                        uint32_t out_channels, float* out, float* pre_relu,
+                                        uint32_t flags, void* stream);
 
 /* Elementwise kernels. Reference: gelu.glsl, add_scaled.glsl, add.glsl, relu.glsl. */
 DAV2_API int dav2_hip_gelu(float* out, const float* input, uint64_t count, void* stream);

@@ -165,6 +165,82 @@ def test_conv2d_i8_matches_oracle(gpu, pkg, lib, oracle):
     assert np.array_equal(host(torch, out).view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("flags,with_residual", [(1, False), (2, False), (3, False), (0, True), (2, True)])
+def test_conv2d_i8_fusions(gpu, pkg, lib, oracle, flags, with_residual):
+    # relu(input) -> conv -> + residual -> relu, each step as its own kernel
+    # (relu.glsl, add.glsl), against the flags of the fused kernel.
+    torch = gpu
+    _announce("conv2d_i8 fusions", flags, with_residual)
+    c, h, w, n = 128, 20, 90, 128
+    rng = np.random.default_rng(flags * 7 + with_residual)
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    res = rng.standard_normal((n, h * w)).astype(np.float32)
+    wq, ws = oracle.quantize_weight_rows(rng.standard_normal((n, c * 9)).astype(np.float32) * 0.05)
+    wt = wq.reshape(n, c, 9).transpose(0, 2, 1).reshape(n, c * 9)
+    bias = rng.standard_normal(n).astype(np.float32)
+    xd, wtd, wsd, bd, rd = dev(torch, x), dev(torch, wt), dev(torch, ws), dev(torch, bias), dev(torch, res)
+    s = stream(torch)
+    n_scratch = lib.dav2_hip_im2col_scratch_floats(w, h, c)
+    scratch = empty(torch, (n_scratch,), torch.float32)
+
+    def conv(inp, out, fl, resid):
+        a = pkg.ConvArgs(input=ptr(inp), width=w, height=h, channels=c, kernel=3, weight=ptr(wtd), weight_scales=ptr(wsd),
+                         bias=ptr(bd), out_channels=n, out=ptr(out), scratch=ptr(scratch), scratch_floats=n_scratch,
+                         flags=fl, residual=ptr(resid) if resid is not None else None)
+        ok(lib, lib.dav2_hip_conv2d_i8(C.byref(a), s))
+
+    src = xd
+    if flags & 1:
+        src = empty(torch, xd.shape, torch.float32)
+        ok(lib, lib.dav2_hip_relu(ptr(src), ptr(xd), xd.numel(), s))
+    want = empty(torch, (n, h * w), torch.float32)
+    conv(src, want, 0, None)
+    if with_residual:
+        ok(lib, lib.dav2_hip_add(ptr(want), ptr(want), ptr(rd), want.numel(), s))
+    if flags & 2:
+        ok(lib, lib.dav2_hip_relu(ptr(want), ptr(want), want.numel(), s))
+    got = empty(torch, (n, h * w), torch.float32)
+    conv(xd, got, flags, rd if with_residual else None)
+    assert np.array_equal(host(torch, got).view(np.uint32), host(torch, want).view(np.uint32))
+
+
+@pytest.mark.parametrize("c,h,w,n,flags", [(32, 518, 518, 1, 2), (32, 20, 33, 1, 0), (64, 7, 9, 3, 1), (12, 5, 5, 4, 3)])
+def test_conv1x1_narrow_matches_im2col_gemm(gpu, pkg, lib, oracle, c, h, w, n, flags):
+    torch = gpu
+    _announce("conv1x1 narrow", c, h, w, n, flags)
+    rng = np.random.default_rng(c + h + n)
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    ld = (c + 63) // 64 * 64
+    wq, ws = oracle.quantize_weight_rows(rng.standard_normal((n, c)).astype(np.float32) * 0.2)
+    bias = rng.standard_normal(n).astype(np.float32)
+    xd, wqd, wsd, bd = dev(torch, x), dev(torch, pad_rows(wq, ld)), dev(torch, ws), dev(torch, bias)
+    s = stream(torch)
+    rows = h * w
+    src = xd
+    if flags & 1:
+        src = empty(torch, xd.shape, torch.float32)
+        ok(lib, lib.dav2_hip_relu(ptr(src), ptr(xd), xd.numel(), s))
+    qd = empty(torch, (rows, ld), torch.int8)
+    sd = empty(torch, (rows,), torch.float32)
+    n_scratch = lib.dav2_hip_im2col_scratch_floats(w, h, c)
+    scratch = empty(torch, (n_scratch,), torch.float32)
+    ok(lib, lib.dav2_hip_im2col_quantize_i8(ptr(src), w, h, c, w, h, 1, 1, 0, ptr(qd), ld, ptr(sd), ptr(scratch),
+                                            n_scratch, s))
+    want = empty(torch, (n, rows), torch.float32)
+    args = _gemm_args(pkg, a=ptr(qd), lda=ld, b=ptr(wqd), ldb=ld, m=rows, n=n, k=ld, epilogue=pkg.GEMM_EPI["transposed"],
+                      a_scales=ptr(sd), b_scales=ptr(wsd), bias=ptr(bd), out=ptr(want), out_row_stride=rows)
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(args), s))
+    pre = host(torch, want).copy()
+    if flags & 2:
+        ok(lib, lib.dav2_hip_relu(ptr(want), ptr(want), want.numel(), s))
+    got = empty(torch, (n, rows), torch.float32)
+    got_pre = empty(torch, (n, rows), torch.float32)
+    ok(lib, lib.dav2_hip_conv1x1_narrow_i8(ptr(xd), w, h, c, ptr(wqd), ld, ptr(wsd), ptr(bd), n, ptr(got), ptr(got_pre),
+                                           flags, s))
+    assert np.array_equal(host(torch, got).view(np.uint32), host(torch, want).view(np.uint32))
+    assert np.array_equal(host(torch, got_pre).view(np.uint32), pre.view(np.uint32))
+
+
 def test_conv2d_i8_rejects_unsupported(gpu, pkg, lib):
     torch = gpu
     for args in [(10, 10, 48, 32, 3, 1, 1), (10, 10, 64, 48, 3, 1, 1), (10, 10, 64, 32, 3, 2, 1), (10, 10, 64, 32, 5, 1, 2),
