@@ -23,9 +23,24 @@ HipExecutor::HipExecutor(const std::string& model_path, dav2_encoder encoder, in
       attention_precision_(attention_precision_for(flags)),
       weights_(model_, context_),
       operators_(context_),
+      side_operators_(context_),
       dino_(encoder, weights_, operators_, attention_precision_),
       dpt_(encoder, weights_, operators_) {
+    context_.make_current();
+    hip_check(hipStreamCreateWithFlags(&side_stream_, hipStreamNonBlocking), "side stream");
+    for (hipEvent_t& e : captured_) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "capture event");
+    hip_check(hipEventCreateWithFlags(&side_done_, hipEventDisableTiming), "side event");
+    side_operators_.set_stream(side_stream_);
     context_.synchronize();
+}
+
+HipExecutor::~HipExecutor() {
+    context_.make_current();
+    if (side_stream_) (void)hipStreamSynchronize(side_stream_);
+    for (hipEvent_t e : captured_)
+        if (e) (void)hipEventDestroy(e);
+    if (side_done_) (void)hipEventDestroy(side_done_);
+    if (side_stream_) (void)hipStreamDestroy(side_stream_);
 }
 
 void HipExecutor::prepare(int image_width, int image_height, int input_size) {
@@ -38,10 +53,30 @@ void HipExecutor::prepare(int image_width, int image_height, int input_size) {
 
 void HipExecutor::run(const float* input, int batch, int width, int height, float* output, float* pre_relu) {
     DeviceBuffer* features[4] = {nullptr, nullptr, nullptr, nullptr};
-    dino_.forward(input, static_cast<std::uint32_t>(width), static_cast<std::uint32_t>(height),
-                  static_cast<std::uint32_t>(batch), arena_, features);
-    dpt_.forward(features, static_cast<std::uint32_t>(width / 14), static_cast<std::uint32_t>(height / 14),
-                 static_cast<std::uint32_t>(batch), arena_, output, pre_relu);
+    const std::uint32_t w = static_cast<std::uint32_t>(width), h = static_cast<std::uint32_t>(height);
+    const std::uint32_t pw = w / 14, ph = h / 14;
+    if (batch != 1) {
+        dino_.forward(input, w, h, static_cast<std::uint32_t>(batch), arena_, features);
+        dpt_.forward(features, pw, ph, static_cast<std::uint32_t>(batch), arena_, output, pre_relu);
+        return;
+    }
+    // Levels 0-2 of the DPT head only need their own captured feature: each
+    // runs on the side stream as soon as the encoder has produced it, beside
+    // the remaining encoder blocks. Level 3 (the last block's feature) runs
+    // on the main stream, which then waits for the side stream before the
+    // refinenets read all four levels.
+    const hipStream_t main = operators_.stream();
+    FeatureMap refined[4];
+    dino_.forward(input, w, h, 1u, arena_, features, [&](std::uint32_t level) {
+        if (level >= 3) return;
+        hip_check(hipEventRecord(captured_[level], main), "capture event");
+        hip_check(hipStreamWaitEvent(side_stream_, captured_[level], 0), "side wait");
+        refined[level] = dpt_.prepare_level(level, *features[level], 0, pw, ph, arena_, side_operators_);
+    });
+    refined[3] = dpt_.prepare_level(3, *features[3], 0, pw, ph, arena_, operators_);
+    hip_check(hipEventRecord(side_done_, side_stream_), "side event");
+    hip_check(hipStreamWaitEvent(main, side_done_, 0), "main wait");
+    dpt_.refine_and_head(refined, 0, pw, ph, arena_, output, pre_relu);
 }
 
 void HipExecutor::infer(const float* input, int width, int height, float* output) {

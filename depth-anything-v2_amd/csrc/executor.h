@@ -36,12 +36,26 @@ public:
 private:
     void run(const float* input, int batch, int width, int height, float* output, float* pre_relu);
 
+public:
+    ~HipExecutor();
+    HipExecutor(const HipExecutor&) = delete;
+    HipExecutor& operator=(const HipExecutor&) = delete;
+
+private:
+
     dav2_encoder encoder_;
     ModelFile model_;  // validated before any HIP call, as the reference's member order does
     HipContext context_;
     Precision attention_precision_;
     GpuModel weights_;
     HipOperators operators_;
+    // Second operator set with its own workspaces on side_stream_: the DPT
+    // levels whose encoder features are ready run there while the encoder
+    // continues (batch 1).
+    HipOperators side_operators_;
+    hipStream_t side_stream_ = nullptr;
+    hipEvent_t captured_[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipEvent_t side_done_ = nullptr;
     DinoEncoder dino_;
     DptHead dpt_;
     Arena arena_;

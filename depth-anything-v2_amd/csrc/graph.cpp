@@ -59,7 +59,8 @@ DinoEncoder::DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& 
 const DeviceBuffer& DinoEncoder::fp32(const std::string& name) const { return weights_.tensor(name).buffer; }
 
 void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t height, std::uint32_t batch,
-                          Arena& arena, DeviceBuffer* features[4]) {
+                          Arena& arena, DeviceBuffer* features[4],
+                          const std::function<void(std::uint32_t)>& on_capture) {
     if (width == 0 || height == 0 || width % 14 != 0 || height % 14 != 0 || batch == 0)
         throw std::invalid_argument("encoder dimensions must be positive multiples of 14");
     const std::uint32_t D = config_.embedding, H = config_.heads;
@@ -88,7 +89,8 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
                                               std::uint64_t(T) * D * sizeof(float));
         ops_.prepare_tokens(out, img, DeviceBuffer(), DeviceBuffer(), patch.int8_buffer, patch.int8_scales,
                             fp32("pretrained.patch_embed.proj.bias"), fp32("pretrained.cls_token"),
-                            fp32("pretrained.pos_embed"), width, height, D, Precision::int8);
+                            fp32("pretrained.pos_embed"), width, height, D, Precision::int8,
+                            /*position_is_constant=*/true);
     }
 
     std::uint32_t capture = 0;
@@ -125,6 +127,7 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
         if (capture < 4 && blk == config_.capture[capture]) {
             ops_.layer_norm(*features[capture], current, fp32("pretrained.norm.weight"), fp32("pretrained.norm.bias"),
                             rows, D, 1.0e-6f);
+            if (on_capture) on_capture(capture);
             ++capture;
         }
     }
@@ -137,7 +140,7 @@ DptHead::DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operator
     hip_check(hipMemsetAsync(zero_bias_.data(), 0, sizeof(float), ops_.context().active_stream()), "zero bias");
 }
 
-FeatureMap DptHead::conv(const FeatureMap& in, const std::string& weight, const std::string& bias,
+FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::string& weight, const std::string& bias,
                          std::uint32_t oc, std::uint32_t k, std::uint32_t stride, std::uint32_t pad, bool has_bias,
                          Arena& arena, const std::string& slot, const ConvFusion& fusion) {
     // dpt.cpp:479-535, every convolution through conv2d_int8
@@ -149,8 +152,8 @@ FeatureMap DptHead::conv(const FeatureMap& in, const std::string& weight, const 
     const GpuTensor& w = weights_.tensor(weight);
     if (!w.int8_buffer) throw std::runtime_error("convolution weight is not int8: " + weight);
     const DeviceBuffer& b = has_bias ? weights_.tensor(bias).buffer : zero_bias_;
-    ops_.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc, k,
-                     stride, pad, has_bias, &w.int8_tapmajor, fusion);
+    ops.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc, k,
+                    stride, pad, has_bias, &w.int8_tapmajor, fusion);
     return out;
 }
 
@@ -161,11 +164,11 @@ FeatureMap DptHead::residual_unit(const FeatureMap& in, const std::string& prefi
     ConvFusion first_fusion;
     first_fusion.relu_input = true;
     first_fusion.relu_output = true;
-    FeatureMap first = conv(in, prefix + ".conv1.weight", prefix + ".conv1.bias", in.channels, 3, 1, 1, true, arena,
+    FeatureMap first = conv(ops_, in, prefix + ".conv1.weight", prefix + ".conv1.bias", in.channels, 3, 1, 1, true, arena,
                             "dpt.ru.first", first_fusion);
     ConvFusion second_fusion;
     second_fusion.residual = in.buffer;
-    return conv(first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.channels, 3, 1, 1, true, arena, slot,
+    return conv(ops_, first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.channels, 3, 1, 1, true, arena, slot,
                 second_fusion);
 }
 
@@ -180,82 +183,85 @@ FeatureMap DptHead::fusion(const FeatureMap& path, const FeatureMap* skip, const
     FeatureMap resized{&arena.get("dpt.fu.resized", std::uint64_t(ow) * oh * config_.features * sizeof(float)), ow,
                        oh, config_.features};
     ops_.bilinear_align_true(*resized.buffer, *unit.buffer, unit.width, unit.height, ow, oh, config_.features);
-    return conv(resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", config_.features, 1, 1, 0, true,
+    return conv(ops_, resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", config_.features, 1, 1, 0, true,
                 arena, slot);
+}
+
+FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, std::uint32_t b, std::uint32_t pw,
+                                  std::uint32_t ph, Arena& arena, HipOperators& ops) {
+    const std::uint32_t D = config_.embedding, T = pw * ph + 1;
+    // Projection and resize layer (dpt.cpp:635-736).
+    const std::string prefix = "depth_head.projects." + std::to_string(i);
+    const GpuTensor& w = weights_.tensor(prefix + ".weight");
+    FeatureMap proj{&arena.get("dpt.proj" + std::to_string(i), std::uint64_t(pw) * ph * config_.project[i] * sizeof(float)),
+                    pw, ph, config_.project[i]};
+    DeviceBuffer tokens = DeviceBuffer::view(feature.as<float>() + std::uint64_t(b) * T * D,
+                                             std::uint64_t(T) * D * sizeof(float));
+    ops.project_tokens_int8(*proj.buffer, tokens, w.int8_buffer, w.int8_scales, weights_.tensor(prefix + ".bias").buffer,
+                            pw, ph, D, config_.project[i]);
+    FeatureMap layer;
+    if (i < 2) {
+        const std::uint32_t k = i == 0 ? 4 : 2;
+        const std::string r = "depth_head.resize_layers." + std::to_string(i);
+        const GpuTensor& rw = weights_.tensor(r + ".weight");
+        layer = FeatureMap{&arena.get("dpt.layer" + std::to_string(i),
+                                      std::uint64_t(pw) * k * ph * k * proj.channels * sizeof(float)),
+                           pw * k, ph * k, proj.channels};
+        ops.conv_transpose_nonoverlap_int8(*layer.buffer, *proj.buffer, rw.int8_buffer, rw.int8_scales,
+                                           weights_.tensor(r + ".bias").buffer, pw, ph, proj.channels, proj.channels, k);
+    } else if (i == 2) {
+        layer = proj;
+    } else {
+        layer = conv(ops, proj, "depth_head.resize_layers.3.weight", "depth_head.resize_layers.3.bias",
+                     config_.project[3], 3, 2, 1, true, arena, "dpt.layer3");
+    }
+    // layer*_rn (dpt.cpp:743-756)
+    return conv(ops, layer, "depth_head.scratch.layer" + std::to_string(i + 1) + "_rn.weight", "", config_.features, 3,
+                1, 1, false, arena, "dpt.rn" + std::to_string(i));
+}
+
+void DptHead::refine_and_head(const FeatureMap refined[4], std::uint32_t b, std::uint32_t pw, std::uint32_t ph,
+                              Arena& arena, float* depth, float* pre_relu) {
+    const std::uint32_t F = config_.features;
+    // refinenets (dpt.cpp:759-790); outputs alternate between two slots.
+    FeatureMap path = fusion(refined[3], nullptr, "depth_head.scratch.refinenet4", refined[2].width, refined[2].height,
+                             arena, "dpt.pathA");
+    path = fusion(path, &refined[2], "depth_head.scratch.refinenet3", refined[1].width, refined[1].height, arena,
+                  "dpt.pathB");
+    path = fusion(path, &refined[1], "depth_head.scratch.refinenet2", refined[0].width, refined[0].height, arena,
+                  "dpt.pathA");
+    path = fusion(path, &refined[0], "depth_head.scratch.refinenet1", refined[0].width * 2, refined[0].height * 2,
+                  arena, "dpt.pathB");
+    // output head (dpt.cpp:792-855)
+    path = conv(ops_, path, "depth_head.scratch.output_conv1.weight", "depth_head.scratch.output_conv1.bias", F / 2, 3,
+                1, 1, true, arena, "dpt.out1");
+    FeatureMap full{&arena.get("dpt.full", std::uint64_t(pw) * 14 * ph * 14 * (F / 2) * sizeof(float)), pw * 14,
+                    ph * 14, F / 2};
+    ops_.bilinear_align_true(*full.buffer, *path.buffer, path.width, path.height, full.width, full.height,
+                             full.channels);
+    ConvFusion relu_after;
+    relu_after.relu_output = true;
+    FeatureMap head = conv(ops_, full, "depth_head.scratch.output_conv2.0.weight", "depth_head.scratch.output_conv2.0.bias",
+                           32, 3, 1, 1, true, arena, "dpt.out2", relu_after);
+    // output_conv2.2 (1x1, 32 -> 1) and the final ReLU in one pass; the
+    // pre-ReLU logits go to pre_relu when asked.
+    const std::uint64_t pixels = std::uint64_t(pw) * 14 * ph * 14;
+    DeviceBuffer out = DeviceBuffer::view(depth + b * pixels, pixels * sizeof(float));
+    DeviceBuffer logits;
+    if (pre_relu) logits = DeviceBuffer::view(pre_relu, pixels * sizeof(float));
+    const GpuTensor& w3 = weights_.tensor("depth_head.scratch.output_conv2.2.weight");
+    if (!w3.int8_buffer) throw std::runtime_error("output_conv2.2 weight is not int8");
+    ops_.conv1x1_narrow_int8(out, *head.buffer, w3.int8_buffer, w3.int8_ld, w3.int8_scales,
+                             weights_.tensor("depth_head.scratch.output_conv2.2.bias").buffer, head.width, head.height,
+                             head.channels, 1, true, relu_after, logits ? &logits : nullptr);
 }
 
 void DptHead::forward(DeviceBuffer* features[4], std::uint32_t pw, std::uint32_t ph, std::uint32_t batch,
                       Arena& arena, float* depth, float* pre_relu) {
-    const std::uint32_t D = config_.embedding, T = pw * ph + 1;
-    const std::uint32_t F = config_.features;
     for (std::uint32_t b = 0; b < batch; ++b) {
-        // Projections and resize layers (dpt.cpp:635-736).
-        FeatureMap layers[4];
-        for (std::uint32_t i = 0; i < 4; ++i) {
-            const std::string prefix = "depth_head.projects." + std::to_string(i);
-            const GpuTensor& w = weights_.tensor(prefix + ".weight");
-            FeatureMap proj{&arena.get("dpt.proj" + std::to_string(i),
-                                       std::uint64_t(pw) * ph * config_.project[i] * sizeof(float)),
-                            pw, ph, config_.project[i]};
-            DeviceBuffer tokens = DeviceBuffer::view(features[i]->as<float>() + std::uint64_t(b) * T * D,
-                                                     std::uint64_t(T) * D * sizeof(float));
-            ops_.project_tokens_int8(*proj.buffer, tokens, w.int8_buffer, w.int8_scales,
-                                     weights_.tensor(prefix + ".bias").buffer, pw, ph, D, config_.project[i]);
-            if (i < 2) {
-                const std::uint32_t k = i == 0 ? 4 : 2;
-                const std::string r = "depth_head.resize_layers." + std::to_string(i);
-                const GpuTensor& rw = weights_.tensor(r + ".weight");
-                FeatureMap res{&arena.get("dpt.layer" + std::to_string(i),
-                                          std::uint64_t(pw) * k * ph * k * proj.channels * sizeof(float)),
-                               pw * k, ph * k, proj.channels};
-                ops_.conv_transpose_nonoverlap_int8(*res.buffer, *proj.buffer, rw.int8_buffer, rw.int8_scales,
-                                                    weights_.tensor(r + ".bias").buffer, pw, ph, proj.channels,
-                                                    proj.channels, k);
-                layers[i] = res;
-            } else if (i == 2) {
-                layers[i] = proj;
-            } else {
-                layers[i] = conv(proj, "depth_head.resize_layers.3.weight", "depth_head.resize_layers.3.bias",
-                                 config_.project[3], 3, 2, 1, true, arena, "dpt.layer3");
-            }
-        }
-        // layer*_rn (dpt.cpp:743-756)
         FeatureMap refined[4];
-        for (std::uint32_t i = 0; i < 4; ++i)
-            refined[i] = conv(layers[i], "depth_head.scratch.layer" + std::to_string(i + 1) + "_rn.weight", "", F, 3, 1,
-                              1, false, arena, "dpt.rn" + std::to_string(i));
-        // refinenets (dpt.cpp:759-790); outputs alternate between two slots.
-        FeatureMap path = fusion(refined[3], nullptr, "depth_head.scratch.refinenet4", refined[2].width,
-                                 refined[2].height, arena, "dpt.pathA");
-        path = fusion(path, &refined[2], "depth_head.scratch.refinenet3", refined[1].width, refined[1].height, arena,
-                      "dpt.pathB");
-        path = fusion(path, &refined[1], "depth_head.scratch.refinenet2", refined[0].width, refined[0].height, arena,
-                      "dpt.pathA");
-        path = fusion(path, &refined[0], "depth_head.scratch.refinenet1", refined[0].width * 2,
-                      refined[0].height * 2, arena, "dpt.pathB");
-        // output head (dpt.cpp:792-855)
-        path = conv(path, "depth_head.scratch.output_conv1.weight", "depth_head.scratch.output_conv1.bias", F / 2, 3, 1,
-                    1, true, arena, "dpt.out1");
-        FeatureMap full{&arena.get("dpt.full", std::uint64_t(pw) * 14 * ph * 14 * (F / 2) * sizeof(float)), pw * 14,
-                        ph * 14, F / 2};
-        ops_.bilinear_align_true(*full.buffer, *path.buffer, path.width, path.height, full.width, full.height,
-                                 full.channels);
-        ConvFusion relu_after;
-        relu_after.relu_output = true;
-        FeatureMap head = conv(full, "depth_head.scratch.output_conv2.0.weight",
-                               "depth_head.scratch.output_conv2.0.bias", 32, 3, 1, 1, true, arena, "dpt.out2",
-                               relu_after);
-        // output_conv2.2 (1x1, 32 -> 1) and the final ReLU in one pass; the
-        // pre-ReLU logits of the last image go to pre_relu when asked.
-        const std::uint64_t pixels = std::uint64_t(pw) * 14 * ph * 14;
-        DeviceBuffer out = DeviceBuffer::view(depth + b * pixels, pixels * sizeof(float));
-        DeviceBuffer logits;
-        if (pre_relu && b + 1 == batch) logits = DeviceBuffer::view(pre_relu, pixels * sizeof(float));
-        const GpuTensor& w3 = weights_.tensor("depth_head.scratch.output_conv2.2.weight");
-        if (!w3.int8_buffer) throw std::runtime_error("output_conv2.2 weight is not int8");
-        ops_.conv1x1_narrow_int8(out, *head.buffer, w3.int8_buffer, w3.int8_ld, w3.int8_scales,
-                                 weights_.tensor("depth_head.scratch.output_conv2.2.bias").buffer, head.width,
-                                 head.height, head.channels, 1, true, relu_after, logits ? &logits : nullptr);
+        for (std::uint32_t i = 0; i < 4; ++i) refined[i] = prepare_level(i, *features[i], b, pw, ph, arena, ops_);
+        refine_and_head(refined, b, pw, ph, arena, depth, b + 1 == batch ? pre_relu : nullptr);
     }
 }
 

@@ -16,6 +16,7 @@
 #include "gpu_model.h"
 #include "operators.h"
 
+#include <functional>
 #include <map>
 #include <string>
 
@@ -46,8 +47,10 @@ public:
     DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, Precision attention_precision);
     // image: device [batch][3][height][width]. On return features[i] holds the
     // final-norm token matrix [batch*tokens][D] of capture layer i.
+    // on_capture(i), when given, runs right after the work producing
+    // features[i] has been enqueued.
     void forward(const float* image, std::uint32_t width, std::uint32_t height, std::uint32_t batch, Arena& arena,
-                 DeviceBuffer* features[4]);
+                 DeviceBuffer* features[4], const std::function<void(std::uint32_t)>& on_capture = {});
     const EncoderConfig& config() const { return config_; }
 
 private:
@@ -73,8 +76,17 @@ public:
     void forward(DeviceBuffer* features[4], std::uint32_t patch_width, std::uint32_t patch_height,
                  std::uint32_t batch, Arena& arena, float* depth, float* pre_relu = nullptr);
 
+    // The two phases of forward for image b. prepare_level runs projection,
+    // resize layer and layer*_rn of level i (its own arena slots, so the four
+    // levels may run on different operator sets / streams); refine_and_head
+    // runs the refinenets and the output head on the main operator set.
+    FeatureMap prepare_level(std::uint32_t level, const DeviceBuffer& feature, std::uint32_t b,
+                             std::uint32_t patch_width, std::uint32_t patch_height, Arena& arena, HipOperators& ops);
+    void refine_and_head(const FeatureMap refined[4], std::uint32_t b, std::uint32_t patch_width,
+                         std::uint32_t patch_height, Arena& arena, float* depth, float* pre_relu);
+
 private:
-    FeatureMap conv(const FeatureMap& input, const std::string& weight, const std::string& bias,
+    FeatureMap conv(HipOperators& ops, const FeatureMap& input, const std::string& weight, const std::string& bias,
                     std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding,
                     bool has_bias, Arena& arena, const std::string& slot, const ConvFusion& fusion = ConvFusion{});
     FeatureMap residual_unit(const FeatureMap& input, const std::string& prefix, Arena& arena,

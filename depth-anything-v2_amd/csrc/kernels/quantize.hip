@@ -200,26 +200,26 @@ __global__ __launch_bounds__(256) void channel_group_absmax_kernel(const float* 
 
 // Row scales of any im2col geometry from the channel-group maxima: the
 // maximum over the k x k input positions of output pixel r (positions in the
-// zero padding contribute nothing) is the absmax of im2col row r.
-__global__ __launch_bounds__(256) void window_scale_kernel(const float* __restrict__ partial, uint32_t groups,
-                                                           uint64_t plane, uint32_t iw, uint32_t ih, uint32_t ow,
-                                                           uint32_t rows, uint32_t k, uint32_t stride, int32_t pad,
-                                                           float* __restrict__ scales) {
-    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
+// zero padding contribute nothing) is the absmax of im2col row r. One wave per
+// row; lanes stride over the (position, group) pairs, then a wave maximum.
+__global__ __launch_bounds__(64 * kRowsPerBlock) void window_scale_kernel(
+    const float* __restrict__ partial, uint32_t groups, uint64_t plane, uint32_t iw, uint32_t ih, uint32_t ow,
+    uint32_t rows, uint32_t k, uint32_t stride, int32_t pad, float* __restrict__ scales) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (r >= rows) return;
     const uint32_t oy = r / ow, ox = r - oy * ow;
+    const uint32_t taps = k * k, total = taps * groups;
     float m = 0.0f;
-    for (uint32_t ky = 0; ky < k; ++ky) {
+    for (uint32_t e = lane; e < total; e += 64u) {
+        const uint32_t g = e / taps, t = e - g * taps, ky = t / k, kx = t - ky * k;
         const int32_t iy = static_cast<int32_t>(oy * stride + ky) - pad;
-        if (iy < 0 || iy >= static_cast<int32_t>(ih)) continue;
-        for (uint32_t kx = 0; kx < k; ++kx) {
-            const int32_t ix = static_cast<int32_t>(ox * stride + kx) - pad;
-            if (ix < 0 || ix >= static_cast<int32_t>(iw)) continue;
-            const float* src = partial + static_cast<uint64_t>(iy) * iw + static_cast<uint32_t>(ix);
-            for (uint32_t g = 0; g < groups; ++g) m = fmaxf(m, src[g * plane]);
-        }
+        const int32_t ix = static_cast<int32_t>(ox * stride + kx) - pad;
+        if (iy >= 0 && iy < static_cast<int32_t>(ih) && ix >= 0 && ix < static_cast<int32_t>(iw))
+            m = fmaxf(m, partial[g * plane + static_cast<uint64_t>(iy) * iw + static_cast<uint32_t>(ix)]);
     }
-    scales[r] = row_scale(m);
+    m = wave_max(m);
+    if (lane == 0) scales[r] = row_scale(m);
 }
 
 __global__ __launch_bounds__(256) void im2col3x3_kernel(const float* __restrict__ x, const float* __restrict__ partial,
@@ -576,8 +576,9 @@ int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32
         // Scales from the channel-group maxima (same values, one thread per row).
         hipLaunchKernelGGL(channel_group_absmax_kernel<false>, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s,
                            input, input_channels, plane, scratch);
-        hipLaunchKernelGGL(window_scale_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, scratch, groups, plane,
-                           input_width, input_height, output_width, rows, kernel, stride, padding, scales);
+        hipLaunchKernelGGL(window_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0, s,
+                           scratch, groups, plane, input_width, input_height, output_width, rows, kernel, stride,
+                           padding, scales);
     } else {
         hipLaunchKernelGGL(im2col_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
                            s, g, rows, scales);

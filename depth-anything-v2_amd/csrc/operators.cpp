@@ -64,9 +64,9 @@ void HipOperators::quantize_rows(const DeviceBuffer& input, std::uint64_t input_
     DeviceBuffer& packed = workspace_.packed(std::uint64_t(rows) * ld);
     DeviceBuffer& scales = workspace_.scales(std::uint64_t(rows) * sizeof(float));
     ProfileScope prof(context_.profiler(), "quantize_rows_i8", 5.0 * rows * columns + 4.0 * rows, "B",
-                      context_.active_stream());
+                      stream());
     hip_check(dav2_hip_quantize_rows_i8(input.as<float>(), input_offset, rows, columns, packed.as<int8_t>(), ld,
-                                        scales.as<float>(), context_.active_stream()),
+                                        scales.as<float>(), stream()),
               "quantize_rows_int8");
     workspace_ld_ = ld;
 }
@@ -85,11 +85,11 @@ void HipOperators::layer_norm_quantize(const DeviceBuffer& input, const DeviceBu
     DeviceBuffer& scales = workspace_.scales(std::uint64_t(rows) * sizeof(float));
     ProfileScope prof(context_.profiler(), "layer_norm_quantize_i8",
                       5.0 * rows * columns + 8.0 * columns + 4.0 * rows + (fp32_out ? 4.0 * rows * columns : 0.0),
-                      "B", context_.active_stream());
+                      "B", stream());
     hip_check(dav2_hip_layer_norm_quantize_i8(packed.as<int8_t>(), ld, scales.as<float>(),
                                               fp32_out ? fp32_out->as<float>() : nullptr, input.as<float>(),
                                               weight.as<float>(), bias.as<float>(), rows, columns, epsilon,
-                                              context_.active_stream()),
+                                              stream()),
               "layer_norm_quantize");
     workspace_ld_ = ld;
 }
@@ -122,8 +122,8 @@ void HipOperators::linear_int8_prequantized(DeviceBuffer& output, const DeviceBu
     a.residual = output.as<float>();
     a.gamma = gamma ? gamma->as<float>() : nullptr;
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
-                      context_.active_stream());
-    hip_check(dav2_hip_gemm_i8(&a, context_.active_stream()), "int8 GEMM");
+                      stream());
+    hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
 }
 
 // src/operators.cpp:847-880
@@ -149,8 +149,8 @@ void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& 
     a.out_row_offset = output_row_offset;
     a.out_row_stride = output_row_stride;
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
-                      context_.active_stream());
-    hip_check(dav2_hip_gemm_i8(&a, context_.active_stream()), "int8 GEMM");
+                      stream());
+    hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
 }
 
 // src/operators.cpp:1016-1042
@@ -162,9 +162,9 @@ void HipOperators::layer_norm(DeviceBuffer& output, const DeviceBuffer& input, c
     require_bytes(weight, columns, "weight");
     require_bytes(bias, columns, "bias");
     ProfileScope prof(context_.profiler(), "layer_norm", 8.0 * rows * columns + 8.0 * columns, "B",
-                      context_.active_stream());
+                      stream());
     hip_check(dav2_hip_layer_norm(output.as<float>(), input.as<float>(), weight.as<float>(), bias.as<float>(), rows,
-                                  columns, epsilon, context_.active_stream()),
+                                  columns, epsilon, stream()),
               "layer_norm");
 }
 
@@ -176,9 +176,9 @@ void HipOperators::add_scaled(DeviceBuffer& output, const DeviceBuffer& residual
     require_bytes(residual, count, "residual");
     require_bytes(addend, count, "addend");
     require_bytes(scale, columns, "scale");
-    ProfileScope prof(context_.profiler(), "add_scaled", 12.0 * count, "B", context_.active_stream());
+    ProfileScope prof(context_.profiler(), "add_scaled", 12.0 * count, "B", stream());
     hip_check(dav2_hip_add_scaled(output.as<float>(), residual.as<float>(), addend.as<float>(), scale.as<float>(),
-                                  count, columns, context_.active_stream()),
+                                  count, columns, stream()),
               "add_scaled");
 }
 
@@ -210,7 +210,7 @@ void HipOperators::attention_batched(DeviceBuffer& output, const DeviceBuffer& q
                                      std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scores,
                                      Precision precision) {
     const int fp16 = precision == Precision::fp16 ? 1 : 0;
-    const hipStream_t s = context_.active_stream();
+    const hipStream_t s = stream();
     const std::uint32_t stride = fp16 ? ((tokens + 7u) & ~7u) : tokens;
     const double flops = 2.0 * batch * heads * double(tokens) * tokens * 64.0;
     const double score_bytes = double(batch) * heads * tokens * tokens * (fp16 ? 2.0 : 4.0);
@@ -246,7 +246,7 @@ void HipOperators::attention_fused(DeviceBuffer& output, const DeviceBuffer& qkv
     require_bytes(qkv, elements * 3, "QKV");
     const std::uint64_t need = attention_fused_scratch_bytes(tokens, heads, batch);
     if (scratch.size() < need) throw std::invalid_argument("attention scratch device buffer is too small");
-    const hipStream_t s = context_.active_stream();
+    const hipStream_t s = stream();
     // QK^T and PV: 4*T*T*64 flops per head.
     const double flops = 4.0 * batch * heads * double(tokens) * tokens * 64.0;
     ProfileScope p(context_.profiler(), "attention_fused", flops, "FLOP", s);
@@ -261,7 +261,7 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
                                   const DeviceBuffer& patch_int8_scales, const DeviceBuffer& patch_bias,
                                   const DeviceBuffer& class_token, const DeviceBuffer& position,
                                   std::uint32_t input_width, std::uint32_t input_height, std::uint32_t embedding,
-                                  Precision precision) {
+                                  Precision precision, bool position_is_constant) {
     if (input_width == 0 || input_height == 0 || input_width % 14 != 0 || input_height % 14 != 0 || embedding == 0)
         throw std::invalid_argument("invalid patch embedding dimensions");
     if (precision != Precision::int8) throw std::runtime_error("only the INT8 patch embedding is built");
@@ -275,7 +275,7 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
     require_bytes(class_token, embedding, "class token");
     require_bytes(position, std::uint64_t(1370) * embedding, "position");
     require_bytes(output, tokens * embedding, "token output");
-    const hipStream_t s = context_.active_stream();
+    const hipStream_t s = stream();
     const std::uint32_t ld = ld64(patch_columns);
     DeviceBuffer& packed = workspace_.packed(std::uint64_t(spatial) * ld);
     DeviceBuffer& scales = workspace_.scales(std::uint64_t(spatial) * sizeof(float));
@@ -288,9 +288,18 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
     linear_int8_packed(output, packed, ld, patch_int8_weight, scales, patch_int8_scales, patch_bias, spatial,
                        patch_columns, embedding, 1u, static_cast<std::uint32_t>(tokens), false, true);
     workspace_ld_ = ld;
+    const void* before = interpolated_.data();
     grow(interpolated_, std::uint64_t(spatial) * embedding * sizeof(float));
-    hip_check(dav2_hip_position_bicubic(interpolated_.as<float>(), position.as<float>(), pw, ph, embedding, s),
-              "position bicubic");
+    if (!position_is_constant || interpolated_.data() != before || interpolated_position_ != position.data() ||
+        interpolated_pw_ != pw || interpolated_ph_ != ph || interpolated_dim_ != embedding) {
+        hip_check(dav2_hip_position_bicubic(interpolated_.as<float>(), position.as<float>(), pw, ph, embedding, s),
+                  "position bicubic");
+        interpolated_position_ = position.data();
+        interpolated_pw_ = pw;
+        interpolated_ph_ = ph;
+        interpolated_dim_ = embedding;
+        if (!position_is_constant) interpolated_position_ = nullptr;
+    }
     hip_check(dav2_hip_finish_tokens(output.as<float>(), interpolated_.as<float>(), position.as<float>(),
                                      class_token.as<float>(), pw, ph, embedding, 1, s),
               "class/position tokens");
@@ -335,7 +344,7 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     require_bytes(bias, has_bias ? output_channels : 1u, "convolution bias");
     require_bytes(output, std::uint64_t(rows) * output_channels, "output");
     if (fusion.residual) require_bytes(*fusion.residual, std::uint64_t(rows) * output_channels, "residual");
-    const hipStream_t s = context_.active_stream();
+    const hipStream_t s = stream();
     const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
     // Implicit GEMM: same bits as im2col + GEMM, no im2col matrix. Maps
     // narrower than its 64-pixel row tiles (37x37, 19x19 in the DPT head) run
@@ -416,7 +425,7 @@ void HipOperators::conv1x1_narrow_int8(DeviceBuffer& output, const DeviceBuffer&
     if (has_bias) require_bytes(bias, output_channels, "convolution bias");
     require_bytes(output, plane * output_channels, "output");
     if (pre_relu) require_bytes(*pre_relu, plane * output_channels, "pre-ReLU output");
-    const hipStream_t s = context_.active_stream();
+    const hipStream_t s = stream();
     ProfileScope prof(context_.profiler(), "conv1x1_narrow_i8", 4.0 * plane * (channels + output_channels), "B", s);
     const std::uint32_t flags =
         (fusion.relu_input ? DAV2_CONV_RELU_INPUT : 0u) | (fusion.relu_output ? DAV2_CONV_RELU_OUTPUT : 0u);
@@ -447,7 +456,7 @@ void HipOperators::conv_transpose_nonoverlap_int8(DeviceBuffer& output, const De
     const std::uint32_t ld = ld64(input_channels);
     DeviceBuffer& packed = workspace_.packed(std::uint64_t(input_rows) * ld);
     DeviceBuffer& scales = workspace_.scales(std::uint64_t(input_rows) * sizeof(float));
-    const hipStream_t s = context_.active_stream();
+    const hipStream_t s = stream();
     ProfileScope prof_q(context_.profiler(), "im2col_quantize_i8",
                         4.0 * input_rows * input_channels + 1.0 * input_rows * input_channels + 4.0 * input_rows, "B", s);
     const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
@@ -488,9 +497,9 @@ void HipOperators::bilinear_align_true(DeviceBuffer& output, const DeviceBuffer&
     require_bytes(output, std::uint64_t(output_width) * output_height * channels, "bilinear output");
     ProfileScope prof(context_.profiler(), "bilinear",
                       4.0 * channels * (double(input_width) * input_height + double(output_width) * output_height), "B",
-                      context_.active_stream());
+                      stream());
     hip_check(dav2_hip_bilinear_align_true(output.as<float>(), input.as<float>(), input_width, input_height,
-                                           output_width, output_height, channels, context_.active_stream()),
+                                           output_width, output_height, channels, stream()),
               "bilinear");
 }
 
@@ -500,9 +509,9 @@ void HipOperators::reduce_minmax(const DeviceBuffer& input, DeviceBuffer& range,
     require_bytes(input, count, "depth reduction input");
     require_bytes(range, 2, "depth reduction range");
     grow(minmax_partials_, std::uint64_t(dav2_hip_minmax_partials(count)) * 2 * sizeof(float));
-    ProfileScope prof(context_.profiler(), "reduce_minmax", 4.0 * count, "B", context_.active_stream());
+    ProfileScope prof(context_.profiler(), "reduce_minmax", 4.0 * count, "B", stream());
     hip_check(dav2_hip_reduce_minmax(input.as<float>(), count, range.as<float>(), minmax_partials_.as<float>(),
-                                     context_.active_stream()),
+                                     stream()),
               "reduce_minmax");
 }
 
@@ -510,8 +519,8 @@ void HipOperators::normalize_relative(DeviceBuffer& depth, const DeviceBuffer& r
     if (count == 0) throw std::invalid_argument("empty relative depth");
     require_bytes(depth, count, "relative depth");
     require_bytes(range, 2, "relative depth range");
-    ProfileScope prof(context_.profiler(), "normalize_relative", 8.0 * count, "B", context_.active_stream());
-    hip_check(dav2_hip_normalize_relative(depth.as<float>(), range.as<float>(), count, context_.active_stream()),
+    ProfileScope prof(context_.profiler(), "normalize_relative", 8.0 * count, "B", stream());
+    hip_check(dav2_hip_normalize_relative(depth.as<float>(), range.as<float>(), count, stream()),
               "normalize_relative");
 }
 
@@ -519,8 +528,8 @@ void HipOperators::normalize_relative(DeviceBuffer& depth, const DeviceBuffer& r
 void HipOperators::relu(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t count) {
     require_bytes(output, count, "ReLU output");
     require_bytes(input, count, "ReLU input");
-    ProfileScope prof(context_.profiler(), "relu", 8.0 * count, "B", context_.active_stream());
-    hip_check(dav2_hip_relu(output.as<float>(), input.as<float>(), count, context_.active_stream()), "relu");
+    ProfileScope prof(context_.profiler(), "relu", 8.0 * count, "B", stream());
+    hip_check(dav2_hip_relu(output.as<float>(), input.as<float>(), count, stream()), "relu");
 }
 
 void HipOperators::add(DeviceBuffer& output, const DeviceBuffer& left, const DeviceBuffer& right,
@@ -528,15 +537,15 @@ void HipOperators::add(DeviceBuffer& output, const DeviceBuffer& left, const Dev
     require_bytes(output, count, "add output");
     require_bytes(left, count, "add left");
     require_bytes(right, count, "add right");
-    ProfileScope prof(context_.profiler(), "add", 12.0 * count, "B", context_.active_stream());
-    hip_check(dav2_hip_add(output.as<float>(), left.as<float>(), right.as<float>(), count, context_.active_stream()),
+    ProfileScope prof(context_.profiler(), "add", 12.0 * count, "B", stream());
+    hip_check(dav2_hip_add(output.as<float>(), left.as<float>(), right.as<float>(), count, stream()),
               "add");
 }
 
 void HipOperators::gelu(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t count) {
     require_bytes(output, count, "GELU output");
     require_bytes(input, count, "GELU input");
-    hip_check(dav2_hip_gelu(output.as<float>(), input.as<float>(), count, context_.active_stream()), "gelu");
+    hip_check(dav2_hip_gelu(output.as<float>(), input.as<float>(), count, stream()), "gelu");
 }
 
 }  // namespace dav2

@@ -46,6 +46,12 @@ class HipOperators {
 public:
     explicit HipOperators(HipContext& context);
 
+    // Stream the operators enqueue on: the context's active stream, unless a
+    // fixed one is set (a second operator set working beside the first on its
+    // own stream, with its own workspaces).
+    void set_stream(hipStream_t stream) { stream_ = stream; }
+    hipStream_t stream() const { return stream_ ? stream_ : context_.active_stream(); }
+
     void linear_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
                      const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
                      std::uint32_t input_columns, std::uint32_t output_columns, bool gelu,
@@ -65,7 +71,8 @@ public:
                         const DeviceBuffer& patch_half_weight, const DeviceBuffer& patch_int8_weight,
                         const DeviceBuffer& patch_int8_scales, const DeviceBuffer& patch_bias,
                         const DeviceBuffer& class_token, const DeviceBuffer& position, std::uint32_t input_width,
-                        std::uint32_t input_height, std::uint32_t embedding, Precision precision);
+                        std::uint32_t input_height, std::uint32_t embedding, Precision precision,
+                        bool position_is_constant = false);
 
     void project_tokens_int8(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& int8_weight,
                              const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t width,
@@ -142,9 +149,16 @@ private:
                             bool has_bias);
 
     HipContext& context_;
+    hipStream_t stream_ = nullptr;
     Int8Workspace workspace_;
     DeviceBuffer minmax_partials_;
     DeviceBuffer interpolated_;
+    // Inputs of the position interpolation held in interpolated_. It depends
+    // only on pos_embed and the patch grid; callers whose pos_embed never
+    // changes (the model graph) pass position_is_constant and a fixed
+    // resolution computes it once.
+    const void* interpolated_position_ = nullptr;
+    std::uint32_t interpolated_pw_ = 0, interpolated_ph_ = 0, interpolated_dim_ = 0;
     DeviceBuffer im2col_scratch_;  // per-channel-group maxima for the tiled im2col kernels
     DeviceBuffer conv_weights_;    // tap-major weights of a conv2d_int8 call that brought none
     DeviceBuffer conv_act_;        // ReLU of a conv2d_int8 input on the im2col path
