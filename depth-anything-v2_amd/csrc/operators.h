@@ -130,8 +130,9 @@ public:
                            Precision precision);
     static std::uint64_t attention_score_bytes(std::uint32_t tokens, std::uint32_t heads, std::uint32_t batch,
                                                Precision precision);
-    // Fused attention (binary16 operands, fp32 scores in registers): the
-    // int8-mode default in place of the materialised binary16 scores.
+    // Fused integer-exact attention (int8 digit planes, exact int32 MFMA
+    // sums): the int8-mode default in place of the materialised binary16
+    // scores.
     void attention_fused(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens, std::uint32_t heads,
                          std::uint32_t batch, DeviceBuffer& scratch);
     static std::uint64_t attention_fused_scratch_bytes(std::uint32_t tokens, std::uint32_t heads,

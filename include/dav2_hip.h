@@ -176,10 +176,12 @@ DAV2_API int dav2_hip_attention_values(float* out, const void* probabilities,
 
 /* Fused attention (int8-mode default): replaces the materialised binary16
  * path of src/operators.cpp:1132-1167 (bmm_score_fp16.glsl,
- * softmax_lastdim_half.glsl, bmm_value_fp16.glsl) with one pass that keeps
- * scores and probabilities in fp32 registers. Operands are binary16
- * fp16(q*0.125), fp16(k), fp16(v); products are exact and accumulate in fp32.
- * qkv and out as above; scratch holds the packed binary16 operands,
+ * softmax_lastdim_half.glsl, bmm_value_fp16.glsl) with an integer-exact
+ * kernel: q*0.125, k and v in 15-bit block floating point split into int8
+ * digit planes, every dot product an exact int32 MFMA sum, 21-bit softmax
+ * numerators, one rounding of the exact quotient per output. The result does
+ * not depend on summation order. qkv and out as above; scratch holds the
+ * digit planes, exponents and block maxima,
  * dav2_hip_attention_fused_scratch_bytes() bytes, 16-byte aligned. */
 DAV2_API uint64_t dav2_hip_attention_fused_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch);
 DAV2_API int dav2_hip_attention_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
