@@ -41,6 +41,7 @@ struct GemmParams {
     const float* residual;
     const float* gamma;
     uint32_t convt_k, convt_w, convt_h, convt_c;
+    uint32_t coalesced_out;  // row-major output rows 16-byte aligned (n % 4 == 0, out aligned)
 };
 
 DAV2_DEV float dequant(int32_t acc, float s_in, float s_w, float b) {
@@ -60,15 +61,86 @@ struct Orientation {
     static constexpr bool swapped = EPI == DAV2_GEMM_EPI_TRANSPOSED || EPI == DAV2_GEMM_EPI_CONVT;
 };
 
-template <int EPI>
-DAV2_DEV void store_one(const GemmParams& g, uint32_t prow, uint32_t qcol, int32_t acc) {
-    const bool sw = Orientation<EPI>::swapped;
+// Epilogue operands of one lane, loaded before the K loop so that no global
+// load latency falls between the last MFMA and the stores. "p" values follow
+// the lane's output rows of operand P (16i + 4(l/16) + r), "q" values its
+// columns (16j + l%16); rows and columns past the matrix load a valid element
+// whose result is never stored.
+template <int EPI, int TM, int TN>
+struct EpilogueOperands {
+    static constexpr bool kSwapped = Orientation<EPI>::swapped;
+    static constexpr bool kScales = EPI != DAV2_GEMM_EPI_RAW_I32;
+    static constexpr bool kLayerScale = EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE;
+    float ps[TM][4];  // scale of the P row: a_scales[m] (row-major) or b_scales[n] (swapped)
+    float pb[TM][4];  // bias of the P row (swapped)
+    float qs[TN];     // scale of the Q column: b_scales[n] (row-major) or a_scales[m] (swapped)
+    float qb[TN];     // bias of the Q column (row-major)
+    float qg[TN];     // LayerScale gamma
+    float res[kLayerScale ? TM : 1][kLayerScale ? TN : 1][4];
+
+    DAV2_DEV void load(const GemmParams& g, uint32_t prow0, uint32_t qcol0, int lane) {
+        if (!kScales) return;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t qc = min(qcol0 + j * 16 + (lane & 15), g.rows_q - 1);
+            qs[j] = kSwapped ? g.a_scales[qc] : g.b_scales[qc];
+            if (!kSwapped) {
+                qb[j] = g.bias ? g.bias[qc] : 0.0f;
+                if (kLayerScale) qg[j] = g.gamma[qc];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t pr = min(prow0 + i * 16 + 4 * (lane >> 4) + r, g.rows_p - 1);
+                ps[i][r] = kSwapped ? g.b_scales[pr] : g.a_scales[pr];
+                if (EPI == DAV2_GEMM_EPI_CONVT) {
+                    const uint32_t kidx = pr / g.convt_c;
+                    pb[i][r] = g.bias[pr - kidx * g.convt_c];
+                } else if (kSwapped) {
+                    pb[i][r] = g.bias ? g.bias[pr] : 0.0f;
+                }
+                if (kLayerScale) {
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const uint32_t qc = min(qcol0 + j * 16 + (lane & 15), g.rows_q - 1);
+                        res[i][j][r] = g.residual[(static_cast<uint64_t>(pr) + g.out_row_offset) * g.n + qc];
+                    }
+                }
+            }
+    }
+};
+
+// Final value of a row-major epilogue from the dequantized v.
+template <int EPI, int TM, int TN>
+DAV2_DEV float row_value(const EpilogueOperands<EPI, TM, TN>& e, int i, int j, int r, float v) {
+    if (EPI == DAV2_GEMM_EPI_ROW_GELU) return gelu_erf(v);
+    if (EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE) {
+        // add_scaled.glsl:26-30: residual + (addend * gamma), no contraction.
+        constexpr bool ls = EpilogueOperands<EPI, TM, TN>::kLayerScale;
+        const float scaled = v * e.qg[j];
+        return e.res[ls ? i : 0][ls ? j : 0][r] + scaled;
+    }
+    return v;
+}
+
+// One output element (row prow of P, column qcol of Q) of block (i, j),
+// accumulator r: dequant ((acc * s_in) * s_w) + bias, then the epilogue.
+template <int EPI, int TM, int TN>
+DAV2_DEV void store_one(const GemmParams& g, const EpilogueOperands<EPI, TM, TN>& e, int i, int j, int r,
+                        uint32_t prow, uint32_t qcol, int32_t acc) {
+    constexpr bool sw = Orientation<EPI>::swapped;
     const uint32_t m = sw ? qcol : prow;
     const uint32_t n = sw ? prow : qcol;
     if (EPI == DAV2_GEMM_EPI_RAW_I32) {
         g.out_i32[static_cast<uint64_t>(m) * g.n + n] = acc;
         return;
     }
+    const float s_in = sw ? e.qs[j] : e.ps[i][r];
+    const float s_w = sw ? e.ps[i][r] : e.qs[j];
+    const float b = sw ? e.pb[i][r] : e.qb[j];
+    const float v = dequant(acc, s_in, s_w, b);
     if (EPI == DAV2_GEMM_EPI_CONVT) {
         const uint32_t k = g.convt_k;
         const uint32_t iy = m / g.convt_w, ix = m - iy * g.convt_w;
@@ -76,24 +148,15 @@ DAV2_DEV void store_one(const GemmParams& g, uint32_t prow, uint32_t qcol, int32
         const uint32_t ky = kidx / k, kx = kidx - ky * k;
         const uint32_t ow = g.convt_w * k, oh = g.convt_h * k;
         const uint64_t idx = (static_cast<uint64_t>(oc) * oh + iy * k + ky) * ow + ix * k + kx;
-        g.out[idx] = dequant(acc, g.a_scales[m], g.b_scales[n], g.bias[oc]);
+        g.out[idx] = v;
         return;
     }
-    const float v = dequant(acc, g.a_scales[m], g.b_scales[n], g.bias ? g.bias[n] : 0.0f);
     if (EPI == DAV2_GEMM_EPI_TRANSPOSED) {
         g.out[static_cast<uint64_t>(n) * g.out_row_stride + m + g.out_row_offset] = v;
         return;
     }
     const uint64_t idx = (static_cast<uint64_t>(m) + g.out_row_offset) * g.n + n;
-    if (EPI == DAV2_GEMM_EPI_ROW) {
-        g.out[idx] = v;
-    } else if (EPI == DAV2_GEMM_EPI_ROW_GELU) {
-        g.out[idx] = gelu_erf(v);
-    } else if (EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE) {
-        // add_scaled.glsl:26-30: residual + (addend * gamma), no contraction.
-        const float scaled = v * g.gamma[n];
-        g.out[idx] = g.residual[idx] + scaled;
-    }
+    g.out[idx] = row_value<EPI, TM, TN>(e, i, j, r, v);
 }
 
 // Tile index of this workgroup. Workgroups are dealt to the 8 XCDs round
@@ -203,6 +266,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
         if (s < ksteps) issue(s);
+    // Epilogue operands: issued after the first stages' copies, waited for
+    // only at the stores.
+    EpilogueOperands<EPI, TM, TN> epi;
+    epi.load(g, row0 + wm * WM, col0 + wn * WN, lane);
 
     const int frag_row = lane & 15;
     const int frag_c = lane >> 4;  // logical chunk within a 64-byte k step
@@ -251,6 +318,45 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
         }
     }
 
+    // Row-major epilogues: the final values go through LDS so that each
+    // store writes whole 256-byte row segments (16 lanes x float4) instead
+    // of 64-byte pieces of four rows.
+    constexpr bool kRowMajor = EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_GELU ||
+                               EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE;
+    constexpr int kOutStride = BN + 4;  // floats; rows 4 apart start 16 banks apart (launch_cfg sizes LDS for it)
+    if (kRowMajor && g.coalesced_out) {
+        float* tile = reinterpret_cast<float*>(smem);
+        __syncthreads();  // every wave is done with the last stage's operands
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int lr = wm * WM + i * 16 + 4 * (lane >> 4) + r, lc = wn * WN + j * 16 + (lane & 15);
+                    const float v = dequant(acc[i][j][r], epi.ps[i][r], epi.qs[j], epi.qb[j]);
+                    tile[lr * kOutStride + lc] = row_value<EPI, TM, TN>(epi, i, j, r, v);
+                }
+        __syncthreads();
+        constexpr int kLanesPerRow = BN / 4, kRowsPerPass = 64 * NW / kLanesPerRow;
+        const int c4 = (tid % kLanesPerRow) * 4;
+        const uint32_t col = col0 + c4;
+#pragma unroll
+        for (int rr = tid / kLanesPerRow; rr < BM; rr += kRowsPerPass) {
+            const uint32_t row = row0 + rr;
+            if (row >= g.rows_p) break;
+            const float4 v = *reinterpret_cast<const float4*>(tile + rr * kOutStride + c4);
+            float* dst = g.out + (static_cast<uint64_t>(row) + g.out_row_offset) * g.n + col;
+            if (col + 3 < g.rows_q) {
+                *reinterpret_cast<float4*>(dst) = v;
+            } else {
+                if (col < g.rows_q) dst[0] = v.x;
+                if (col + 1 < g.rows_q) dst[1] = v.y;
+                if (col + 2 < g.rows_q) dst[2] = v.z;
+            }
+        }
+        return;
+    }
     // 16x16 MFMA result layout: lane l holds rows 4*(l/16)+r (r = 0..3) of
     // column l%16.
 #pragma unroll
@@ -262,7 +368,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t prow = row0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
-                if (prow < g.rows_p) store_one<EPI>(g, prow, qcol, acc[i][j][r]);
+                if (prow < g.rows_p) store_one<EPI, TM, TN>(g, epi, i, j, r, prow, qcol, acc[i][j][r]);
             }
         }
     }
@@ -270,7 +376,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
 
 template <int BM, int BN, int WMW, int WNW, int BK, int STAGES, int EPI>
 void launch_cfg(const GemmParams& g, hipStream_t s) {
-    constexpr size_t lds = static_cast<size_t>(STAGES) * (BM + BN) * BK;
+    // LDS: the stage ring, or the row-major output tile if that is larger.
+    constexpr size_t ring = static_cast<size_t>(STAGES) * (BM + BN) * BK;
+    constexpr size_t out_tile = static_cast<size_t>(BM) * (BN + 4) * 4;
+    constexpr bool row_major = EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_GELU ||
+                               EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE;
+    constexpr size_t lds = row_major && out_tile > ring ? out_tile : ring;
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
@@ -282,11 +393,15 @@ void launch_cfg(const GemmParams& g, hipStream_t s) {
 template <int EPI>
 void launch_epi(const GemmParams& g, hipStream_t s) {
     // Measured on MI355X for the ViT-L encoder shapes (M = 1370, K = 1024 /
-    // 4096): 64x64 tiles with four waves, 128-byte stages and a three-stage
-    // ring beat every larger tile (more workgroups in flight hide the load
-    // latency better) and match the vendor int8 GEMM. Channel-major GEMMs
-    // with few output channels use 32-row tiles.
+    // 4096, 128-byte stages): for N = 1024 64x64 tiles with a three-stage
+    // ring are fastest; for N >= 2048 96x64 tiles with a two-stage ring are
+    // (720 workgroups for N = 3072, one round at three per CU, against 1056
+    // 64x64 ones). Channel-major GEMMs with few output channels use 32-row
+    // tiles.
+    constexpr bool row_major = EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_GELU ||
+                               EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE;
     if (g.rows_p <= 32) launch_cfg<32, 64, 1, 2, 128, 3, EPI>(g, s);
+    else if (row_major && g.rows_q >= 2048 && g.rows_p >= 512) launch_cfg<96, 64, 2, 2, 128, 2, EPI>(g, s);
     else launch_cfg<64, 64, 2, 2, 128, 3, EPI>(g, s);
 }
 
@@ -333,6 +448,7 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     g.convt_w = a->convt_width;
     g.convt_h = a->convt_height;
     g.convt_c = a->convt_channels;
+    g.coalesced_out = !swapped && a->n % 4 == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (e) {
         case DAV2_GEMM_EPI_RAW_I32: launch_epi<DAV2_GEMM_EPI_RAW_I32>(g, s); break;
