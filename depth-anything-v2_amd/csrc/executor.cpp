@@ -2,7 +2,9 @@
 
 #include "dav2_hip.h"
 
+#include <cstdlib>
 #include <stdexcept>
+#include <string>
 
 namespace dav2 {
 
@@ -31,12 +33,18 @@ HipExecutor::HipExecutor(const std::string& model_path, dav2_encoder encoder, in
     for (hipEvent_t& e : captured_) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "capture event");
     hip_check(hipEventCreateWithFlags(&side_done_, hipEventDisableTiming), "side event");
     side_operators_.set_stream(side_stream_);
+    // Graph replay is opt-in: on MI355X the eager launches of the ViT-L 518
+    // inference measured 2-3% faster than replaying its captured graph.
+    const char* env = std::getenv("DAV2_HIP_GRAPHS");
+    graphs_enabled_ = env && std::string(env) == "1";
     context_.synchronize();
 }
 
 HipExecutor::~HipExecutor() {
     context_.make_current();
     if (side_stream_) (void)hipStreamSynchronize(side_stream_);
+    (void)hipStreamSynchronize(context_.stream());
+    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
     for (hipEvent_t e : captured_)
         if (e) (void)hipEventDestroy(e);
     if (side_done_) (void)hipEventDestroy(side_done_);
@@ -79,6 +87,54 @@ void HipExecutor::run(const float* input, int batch, int width, int height, floa
     dpt_.refine_and_head(refined, 0, pw, ph, arena_, output, pre_relu);
 }
 
+void HipExecutor::run_graph(const float* input, int batch, int width, int height, float* output, float* pre_relu) {
+    const hipStream_t main = operators_.stream();
+    if (!graphs_enabled_ || batch != 1 || context_.profiler().enabled()) {
+        run(input, batch, width, height, output, pre_relu);
+        return;
+    }
+    GraphKey key;
+    key.input = input;
+    key.output = output;
+    key.pre_relu = pre_relu;
+    key.width = width;
+    key.height = height;
+    key.stream = main;
+    if (graph_exec_ && key == graph_key_) {
+        hip_check(hipGraphLaunch(graph_exec_, main), "graph launch");
+        return;
+    }
+    if (!warm_valid_ || !(key == warm_key_)) {
+        // First run at this key: eager, so every arena slot and workspace is
+        // allocated (nothing may allocate or synchronise during a capture).
+        run(input, batch, width, height, output, pre_relu);
+        warm_key_ = key;
+        warm_valid_ = true;
+        return;
+    }
+    hipGraph_t graph = nullptr;
+    hip_check(hipStreamBeginCapture(main, hipStreamCaptureModeThreadLocal), "begin capture");
+    try {
+        run(input, batch, width, height, output, pre_relu);
+    } catch (...) {
+        (void)hipStreamEndCapture(main, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+    }
+    hip_check(hipStreamEndCapture(main, &graph), "end capture");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    hip_check(inst, "graph instantiate");
+    if (graph_exec_) {
+        hip_check(hipStreamSynchronize(main), "graph replace");
+        (void)hipGraphExecDestroy(graph_exec_);
+    }
+    graph_exec_ = exec;
+    graph_key_ = key;
+    hip_check(hipGraphLaunch(graph_exec_, main), "graph launch");
+}
+
 void HipExecutor::infer(const float* input, int width, int height, float* output) {
     std::lock_guard<std::mutex> lock(mutex_);
     context_.make_current();
@@ -88,7 +144,7 @@ void HipExecutor::infer(const float* input, int width, int height, float* output
     DeviceBuffer& in = arena_.get("io.input", in_elems * sizeof(float));
     DeviceBuffer& out = arena_.get("io.output", out_elems * sizeof(float));
     context_.upload(in, input, in_elems * sizeof(float));
-    run(in.as<float>(), 1, width, height, out.as<float>(), nullptr);
+    run_graph(in.as<float>(), 1, width, height, out.as<float>(), nullptr);
     context_.download(out, output, out_elems * sizeof(float));
 }
 
@@ -97,7 +153,7 @@ void HipExecutor::infer_device(const float* input, int batch, int width, int hei
     std::lock_guard<std::mutex> lock(mutex_);
     context_.make_current();
     ScopedStream scoped(context_, stream);
-    run(input, batch, width, height, output, pre_relu);
+    run_graph(input, batch, width, height, output, pre_relu);
 }
 
 void HipExecutor::normalize_relative_device(float* depth, std::uint64_t count, hipStream_t stream) {

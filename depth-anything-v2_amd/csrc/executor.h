@@ -35,6 +35,12 @@ public:
 
 private:
     void run(const float* input, int batch, int width, int height, float* output, float* pre_relu);
+    // run() through a HIP graph: the first call with a given (input, output,
+    // pre_relu, size, stream) runs eagerly and sizes every buffer, the next
+    // one captures the enqueued work (both streams) into a graph, later ones
+    // replay it, when DAV2_HIP_GRAPHS=1 is set at creation. Batch > 1 and
+    // profiling always run eagerly.
+    void run_graph(const float* input, int batch, int width, int height, float* output, float* pre_relu);
 
 public:
     ~HipExecutor();
@@ -56,6 +62,22 @@ private:
     hipStream_t side_stream_ = nullptr;
     hipEvent_t captured_[4] = {nullptr, nullptr, nullptr, nullptr};
     hipEvent_t side_done_ = nullptr;
+    struct GraphKey {
+        const float* input = nullptr;
+        float* output = nullptr;
+        float* pre_relu = nullptr;
+        int width = 0, height = 0;
+        hipStream_t stream = nullptr;
+        bool operator==(const GraphKey& o) const {
+            return input == o.input && output == o.output && pre_relu == o.pre_relu && width == o.width &&
+                   height == o.height && stream == o.stream;
+        }
+    };
+    bool graphs_enabled_ = true;
+    bool warm_valid_ = false;
+    GraphKey warm_key_;   // last eager run (buffers sized for it)
+    GraphKey graph_key_;  // what graph_exec_ replays
+    hipGraphExec_t graph_exec_ = nullptr;
     DinoEncoder dino_;
     DptHead dpt_;
     Arena arena_;

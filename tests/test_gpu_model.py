@@ -89,6 +89,37 @@ def test_batched_device_entry_matches_single(gpu, pkg, lib, models):
         assert np.array_equal(got[b], singles[b])
 
 
+def test_graph_replays_match_eager(gpu, pkg, lib, models, monkeypatch):
+    # The first inference at a given (input, output, size, stream) runs
+    # eagerly, the second captures a HIP graph, later ones replay it. Every
+    # replay must equal the eager result bit for bit, also with other eager
+    # inferences (other buffers, the host entry) and synchronisations between
+    # the replays.
+    torch = gpu
+    width = height = 518
+    x = pkg.dav2_format.imagenet_input(width, height, seed=SEED + 7)[0]
+    xd = dev(torch, x)
+    out = empty(torch, (height, width), torch.float32)
+    other = empty(torch, (height, width), torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    monkeypatch.setenv("DAV2_HIP_GRAPHS", "1")  # read when the context is created
+    with pkg.Context(str(models["vits"]), "vits") as ctx:
+        ctx.infer_device(xd.data_ptr(), 1, width, height, out.data_ptr(), out.numel(), stream)
+        ref = host(torch, out).copy()
+        assert np.isfinite(ref).all()
+        for i in range(4):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            ctx.infer_device(xd.data_ptr(), 1, width, height, out.data_ptr(), out.numel(), stream)
+            got = host(torch, out)
+            print(f"case: graph replay {i}", flush=True)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+            # eager work in between: another output buffer, then the host entry
+            ctx.infer_device(xd.data_ptr(), 1, width, height, other.data_ptr(), other.numel(), stream)
+            assert np.array_equal(host(torch, other).view(np.uint32), ref.view(np.uint32))
+            assert np.array_equal(ctx.infer(x, width, height).view(np.uint32), ref.view(np.uint32))
+
+
 def test_normalize_relative_device(gpu, pkg, lib, oracle, models):
     torch = gpu
     rng = np.random.default_rng(4)
