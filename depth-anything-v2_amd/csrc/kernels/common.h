@@ -56,6 +56,18 @@ DAV2_DEV float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
 inline unsigned ceil_div(uint64_t a, uint64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane l's bytes land at lds_base + 16*l; the
+// base must be the same for the whole wave. The copies count in vmcnt.
+DAV2_DEV void copy16_to_lds(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)lds_base, 16, 0, 0);
+}
+
+// s_waitcnt with vmcnt = n (expcnt, lgkmcnt not waited on), n < 64.
+#define DAV2_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
 // Scale rule shared by every activation quantizer:
 // quantize_rows_int8_fused.glsl:37 and im2col_quantize_int8.glsl:63.
 DAV2_DEV float row_scale(float absmax) { return fmaxf(absmax / 127.0f, 1.0e-8f); }

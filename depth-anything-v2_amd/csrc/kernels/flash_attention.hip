@@ -305,32 +305,43 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     // log2(e) * 2^(eq + ek): turns u - max u into the exponent of 2
     const float row_scale = ldexpf(1.44269504f, qe[static_cast<uint64_t>(bh) * tp + q0 + col] + ke[bh]);
 
-    // Staging of one key half: K planes (2 x 64 rows x 64 B) and V planes in
-    // 16-byte chunks c < 512: plane c >> 8, row (c >> 2) & 63, column c & 3.
-    v4i stage[8];
-    auto fetch = [&](uint32_t kb, bool values) {
+    // Staging of one key half, global memory straight into LDS
+    // (global_load_lds_dwordx4, no registers). A block of 64 keys is the K
+    // planes (LDS planes 0 = high digit, 1 = low digit: 2 x 64 rows x 64 B)
+    // and, in pass 2, the V planes (2, 3). Each 1 KB piece (16 rows of one
+    // plane) is one wave instruction: lane l lands at piece + 16 l, i.e. row
+    // 16 q + l / 4, physical chunk l % 4, and fetches the logical chunk that
+    // lds_chunk() stores there. The two waves of a key half issue 4 pieces
+    // each per plane pair. Pass 1 keeps kRing1 K-only blocks in flight,
+    // pass 2 two K+V blocks.
+    const int wave_in_half = group;
+    auto issue_planes = [&](uint32_t kb, int8_t* tile, bool values) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t c = static_cast<uint32_t>(htid) + 128u * i;
-            const uint32_t plane = c >> 8, row = (c >> 2) & 63u, c16 = (c & 3u) * 16u;
-            stage[i] = *reinterpret_cast<const v4i*>(kbase + plane * plane_qk +
-                                                     (static_cast<uint64_t>(kb) * kBlock + row) * 64u + c16);
+            const uint32_t piece = static_cast<uint32_t>(wave_in_half) * 4u + i;  // 0..7
+            const uint32_t lplane = piece >> 2;                                   // 0: high, 1: low digit
+            const uint32_t row = (piece & 3u) * 16u + (static_cast<uint32_t>(lane) >> 2);
+            const uint32_t c = ((static_cast<uint32_t>(lane) & 3u) ^ (row >> 2)) & 3u;  // logical chunk
+            const uint32_t gplane = 1u - lplane;                                   // global plane 1 = high digit
+            copy16_to_lds(kbase + gplane * plane_qk + (static_cast<uint64_t>(kb) * kBlock + row) * 64u + c * 16u,
+                          tile + lplane * kPlane + (piece & 3u) * 1024u);
             if (values)
-                stage[4 + i] = *reinterpret_cast<const v4i*>(
-                    vbase + (plane * 64u + row) * static_cast<uint64_t>(tp) + kb * kBlock + c16);
+                copy16_to_lds(vbase + (gplane * 64u + row) * static_cast<uint64_t>(tp) + kb * kBlock + c * 16u,
+                              tile + (2u + lplane) * kPlane + (piece & 3u) * 1024u);
         }
     };
-    auto store = [&](int buf, bool values) {
-        int8_t* t = tiles + buf * kTile;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t c = static_cast<uint32_t>(htid) + 128u * i;
-            const uint32_t plane = c >> 8, row = (c >> 2) & 63u;
-            // LDS planes: K1 = 0, K0 = 1, V1 = 2, V0 = 3 (global plane 1 is the high digit)
-            const uint32_t at = lds_chunk(row, c & 3u);
-            *reinterpret_cast<v4i*>(t + (1u - plane) * kPlane + at) = stage[i];
-            if (values) *reinterpret_cast<v4i*>(t + (3u - plane) * kPlane + at) = stage[4 + i];
-        }
+    // Waits until the copies of the current block have landed in every wave:
+    // copies retire in issue order, so it is enough that at most `later`
+    // blocks' copies of this wave are outstanding, then a plain barrier
+    // (__syncthreads would also drain the later blocks).
+    auto wait_block = [&](int later, int per_block) {
+        const int n = later * per_block;
+        if (n >= 12) DAV2_WAIT_VMCNT(12);
+        else if (n >= 8) DAV2_WAIT_VMCNT(8);
+        else if (n >= 4) DAV2_WAIT_VMCNT(4);
+        else DAV2_WAIT_VMCNT(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
     };
     // Unscaled scores of the block for this lane: u[j][r] = key 16j + 4g + r,
     // query col; TAIL masks keys >= tokens. All MFMAs are issued first.
@@ -360,20 +371,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     };
 
     const bool ragged = tokens != tp;
-    // Pass 1: row maxima of u over this key half.
+    // Pass 1: row maxima of u over this key half (K only, kRing1 blocks of
+    // 8 KB in flight in the half's 32 KB).
+    constexpr int kRing1 = 4;
     float m = -INFINITY;
-    if (nkb > 0) {
-        fetch(kb0, false);
-        store(0, false);
-    }
-    __syncthreads();
+#pragma unroll
+    for (int d = 0; d < kRing1 - 1; ++d)
+        if (static_cast<uint32_t>(d) < nkb) issue_planes(kb0 + d, tiles + d * (kTile / 2), false);
     for (uint32_t it = 0; it < first_half; ++it) {
-        const int buf = static_cast<int>(it & 1u);
         const uint32_t kb = kb0 + it;
         const bool have = it < nkb;
-        if (it + 1 < nkb) fetch(kb + 1, false);
+        // this wave has issued blocks up to min(it + kRing1 - 2, nkb - 1)
+        const int later = have ? min(kRing1 - 2, static_cast<int>(nkb) - 1 - static_cast<int>(it)) : 0;
+        wait_block(later, 4);
+        if (it + kRing1 - 1 < nkb)
+            issue_planes(kb + kRing1 - 1, tiles + ((it + kRing1 - 1) % kRing1) * (kTile / 2), false);
         if (have) {
-            const int8_t* t = tiles + buf * kTile;
+            const int8_t* t = tiles + (it % kRing1) * (kTile / 2);
             float s[4][4];
             if (ragged && kb + 1 == blocks)
                 block_scores(t, kb, std::true_type{}, s);
@@ -382,33 +396,30 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
 #pragma unroll
             for (int j = 0; j < 4; ++j) m = fmaxf(fmaxf(m, fmaxf(s[j][0], s[j][1])), fmaxf(s[j][2], s[j][3]));
         }
-        if (it + 1 < nkb) store(buf ^ 1, false);
-        __syncthreads();
     }
+    __syncthreads();  // every wave is done with the pass-1 ring before it is reused
     m = fmaxf(m, __shfl_xor(m, 16, kWave));
     m = fmaxf(m, __shfl_xor(m, 32, kWave));
-    // [half][group][query] maxima in the buffer-1 tile of key half 1, which
-    // pass 2 first writes after its opening barrier
+    // [half][group][query] maxima in the second pass-2 slot of key half 1;
+    // every wave has read them (full barrier) before pass 2 copies anything.
     float* half_max = reinterpret_cast<float*>(lds + 3 * kTile);
     if (g == 0) half_max[(half * 2 + group) * 16 + col] = m;
     __syncthreads();
     m = fmaxf(half_max[group * 16 + col], half_max[(2 + group) * 16 + col]);
+    __syncthreads();
 
     // Pass 2: E = 21-bit softmax numerators, sum_j E, sum_j E V over this half.
     v4i c0[4], c7[4], c14[4], c21[4];
 #pragma unroll
     for (int fb = 0; fb < 4; ++fb) c0[fb] = c7[fb] = c14[fb] = c21[fb] = v4i{0, 0, 0, 0};
     uint64_t lsum = 0;
-    if (nkb > 0) {
-        fetch(kb0, true);
-        store(0, true);
-    }
-    __syncthreads();
+    if (nkb > 0) issue_planes(kb0, tiles, true);
     for (uint32_t it = 0; it < first_half; ++it) {
         const int buf = static_cast<int>(it & 1u);
         const uint32_t kb = kb0 + it;
         const bool have = it < nkb;
-        if (it + 1 < nkb) fetch(kb + 1, true);
+        wait_block(0, 8);
+        if (it + 1 < nkb) issue_planes(kb + 1, tiles + (buf ^ 1) * kTile, true);
         if (have) {
             const int8_t* t = tiles + buf * kTile;
             float s[4][4];
@@ -443,9 +454,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
                 c21[fb] = mfma8(v1, e2, c21[fb]);
             }
         }
-        if (it + 1 < nkb) store(buf ^ 1, true);
-        __syncthreads();
     }
+    __syncthreads();  // every wave is done with the ring before the sums reuse it
 
     // Half 1 hands its integer sums to half 0 (exact adds): [group][lane][66].
     int* red = reinterpret_cast<int*>(lds);

@@ -173,14 +173,6 @@ DAV2_DEV void tile_of(uint32_t& tm, uint32_t& tn) {
     tn = lin / mt;
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// 16 bytes per lane from global memory straight into LDS
-// (global_load_lds_dwordx4): lane l's bytes land at lds_base + 16*l; the
-// base must be the same for the whole wave.
-DAV2_DEV void copy16_to_lds(const int8_t* src, int8_t* lds_base) {
-    __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)lds_base, 16, 0, 0);
-}
 
 // LDS byte offset of logical 16-byte chunk c of row r in a stage of BK-byte
 // rows: chunks are XOR-swizzled with the row's 256-byte period index, so the
@@ -192,8 +184,6 @@ DAV2_DEV uint32_t swz(uint32_t r, uint32_t c) {
     return r * BK + ((c ^ ((r / rows_per_period) & (cpr - 1))) << 4);
 }
 
-// s_waitcnt with vmcnt = n (expcnt, lgkmcnt not waited on), n < 64.
-#define DAV2_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, int EPI>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmParams g) {
