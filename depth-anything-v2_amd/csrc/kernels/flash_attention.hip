@@ -279,7 +279,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     const int* __restrict__ qe, const int* __restrict__ ke, const int* __restrict__ ve, float* __restrict__ out,
     uint32_t tokens, uint32_t heads, uint32_t tp) {
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];  // [half][buffer][kTile]
-    const uint32_t h = blockIdx.y, b = blockIdx.z, bh = b * heads + h;
+    // Workgroups are dealt to the 8 XCDs round robin; give each XCD one
+    // contiguous run of (head, query tile) pairs, so that the key and value
+    // planes of a head are read by one XCD and stay in its L2.
+    const uint32_t qtiles = gridDim.x, total = gridDim.x * gridDim.y * gridDim.z;
+    const uint32_t id = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    const uint32_t xcd = id & 7u, slot = id >> 3, per = total >> 3, extra = total & 7u;
+    const uint32_t lin = xcd * per + min(xcd, extra) + slot;
+    const uint32_t qtile = lin % qtiles, bh = lin / qtiles, b = bh / heads, h = bh - b * heads;
     const uint32_t D = heads * 64u;
     const int tid = threadIdx.x, lane = tid & 63;
     // wave-uniform values kept in scalar registers (uniform branches)
@@ -287,7 +294,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     const int group = wave & 1, half = wave >> 1;
     const int htid = tid & 127;  // thread index within the key half
     const int col = lane & 15, g = lane >> 4;
-    const uint32_t q0 = blockIdx.x * 32u + group * 16u;
+    const uint32_t q0 = qtile * 32u + group * 16u;
     const uint64_t plane_qk = static_cast<uint64_t>(tp) * 64u;
     const uint32_t blocks = tp / kBlock;
     const uint32_t first_half = (blocks + 1u) / 2u;  // blocks of half 0; half 1 has the rest
