@@ -26,8 +26,9 @@
 // key-permuted as below), attention.
 //
 // Attention: one workgroup = 4 waves = 2 query groups of 16 x 2 key halves.
-// The two waves of a key half share its key blocks of 64, staged through LDS
-// (double buffered, one barrier per block). Pass 1 computes the row maxima,
+// The two waves of a key half share its key blocks of 64, staged through a
+// ring of three 8 KB LDS slots per half (48 KB per workgroup, three
+// workgroups per CU). Pass 1 computes the row maxima,
 // pass 2 recomputes the same scores and accumulates E and E V; the halves
 // combine their maxima and their (exact integer) sums through LDS.
 //
@@ -50,10 +51,12 @@ namespace {
 
 constexpr uint32_t kBlock = 64;    // keys per LDS block, tokens per pack workgroup
 constexpr int kPlane = 64 * 64;   // one digit plane of a block in LDS (64 rows x 64 B)
-constexpr int kTile = 4 * kPlane;  // K1 | K0 | V1 | V0
+constexpr int kSlot = 2 * kPlane;  // one block's K1 | K0 or V1 | V0 planes
+constexpr int kSlots = 3;          // ring slots per key half
 constexpr int kEMax = 2097151;     // 2^21 - 1
 constexpr int kAttnThreads = 256;  // 2 query groups x 2 key halves
-constexpr size_t kAttnLds = 2 * 2 * kTile;  // [key half][buffer] tiles
+constexpr size_t kAttnLds = 2 * kSlots * kSlot;  // [key half][slot]
+static_assert(2 * 64 * 66 * 4 <= kAttnLds, "the sums hand-over fits in the slots");
 
 inline uint32_t padded_tokens(uint32_t tokens) { return (tokens + kBlock - 1u) / kBlock * kBlock; }
 
@@ -278,7 +281,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     const int8_t* __restrict__ qd, const int8_t* __restrict__ kd, const int8_t* __restrict__ vd,
     const int* __restrict__ qe, const int* __restrict__ ke, const int* __restrict__ ve, float* __restrict__ out,
     uint32_t tokens, uint32_t heads, uint32_t tp) {
-    extern __shared__ __attribute__((aligned(16))) int8_t lds[];  // [half][buffer][kTile]
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];  // [half][slot][kSlot]
     // Workgroups are dealt to the 8 XCDs round robin; give each XCD one
     // contiguous run of (head, query tile) pairs, so that the key and value
     // planes of a head are read by one XCD and stay in its L2.
@@ -300,7 +303,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     const uint32_t first_half = (blocks + 1u) / 2u;  // blocks of half 0; half 1 has the rest
     const uint32_t kb0 = half ? first_half : 0u;
     const uint32_t nkb = half ? blocks - first_half : first_half;
-    int8_t* tiles = lds + half * 2 * kTile;
+    int8_t* slots = lds + half * kSlots * kSlot;
 
     const int8_t* kbase = kd + static_cast<uint64_t>(bh) * 2u * plane_qk;
     const int8_t* vbase = vd + static_cast<uint64_t>(bh) * 2u * plane_qk;
@@ -313,16 +316,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     const float row_scale = ldexpf(1.44269504f, qe[static_cast<uint64_t>(bh) * tp + q0 + col] + ke[bh]);
 
     // Staging of one key half, global memory straight into LDS
-    // (global_load_lds_dwordx4, no registers). A block of 64 keys is the K
-    // planes (LDS planes 0 = high digit, 1 = low digit: 2 x 64 rows x 64 B)
-    // and, in pass 2, the V planes (2, 3). Each 1 KB piece (16 rows of one
-    // plane) is one wave instruction: lane l lands at piece + 16 l, i.e. row
-    // 16 q + l / 4, physical chunk l % 4, and fetches the logical chunk that
-    // lds_chunk() stores there. The two waves of a key half issue 4 pieces
-    // each per plane pair. Pass 1 keeps kRing1 K-only blocks in flight,
-    // pass 2 two K+V blocks.
+    // (global_load_lds_dwordx4, no registers). A slot holds the two digit
+    // planes (0 = high, 1 = low: 2 x 64 rows x 64 B) of a block's keys or of
+    // its values. Each 1 KB piece (16 rows of one plane) is one wave
+    // instruction: lane l lands at piece + 16 l, i.e. row 16 q + l / 4,
+    // physical chunk l % 4, and fetches the logical chunk that lds_chunk()
+    // stores there. The two waves of a key half issue 4 pieces each per slot.
     const int wave_in_half = group;
-    auto issue_planes = [&](uint32_t kb, int8_t* tile, bool values) {
+    auto issue_planes = [&](uint32_t kb, int8_t* slot, bool values) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t piece = static_cast<uint32_t>(wave_in_half) * 4u + i;  // 0..7
@@ -330,22 +331,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
             const uint32_t row = (piece & 3u) * 16u + (static_cast<uint32_t>(lane) >> 2);
             const uint32_t c = ((static_cast<uint32_t>(lane) & 3u) ^ (row >> 2)) & 3u;  // logical chunk
             const uint32_t gplane = 1u - lplane;                                   // global plane 1 = high digit
-            copy16_to_lds(kbase + gplane * plane_qk + (static_cast<uint64_t>(kb) * kBlock + row) * 64u + c * 16u,
-                          tile + lplane * kPlane + (piece & 3u) * 1024u);
-            if (values)
-                copy16_to_lds(vbase + (gplane * 64u + row) * static_cast<uint64_t>(tp) + kb * kBlock + c * 16u,
-                              tile + (2u + lplane) * kPlane + (piece & 3u) * 1024u);
+            const int8_t* src = values ? vbase + (gplane * 64u + row) * static_cast<uint64_t>(tp) + kb * kBlock + c * 16u
+                                       : kbase + gplane * plane_qk + (static_cast<uint64_t>(kb) * kBlock + row) * 64u + c * 16u;
+            copy16_to_lds(src, slot + lplane * kPlane + (piece & 3u) * 1024u);
         }
     };
-    // Waits until the copies of the current block have landed in every wave:
-    // copies retire in issue order, so it is enough that at most `later`
-    // blocks' copies of this wave are outstanding, then a plain barrier
-    // (__syncthreads would also drain the later blocks).
-    auto wait_block = [&](int later, int per_block) {
-        const int n = later * per_block;
-        if (n >= 12) DAV2_WAIT_VMCNT(12);
-        else if (n >= 8) DAV2_WAIT_VMCNT(8);
-        else if (n >= 4) DAV2_WAIT_VMCNT(4);
+    // Waits until this wave has at most `later` slots' copies outstanding
+    // (copies retire in issue order, 4 per slot and wave), then a plain
+    // barrier: the slot issued before those has landed in every wave
+    // (__syncthreads would also drain the later slots).
+    auto wait_slots = [&](int later) {
+        if (later >= 2) DAV2_WAIT_VMCNT(8);
+        else if (later == 1) DAV2_WAIT_VMCNT(4);
         else DAV2_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
@@ -378,23 +375,19 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     };
 
     const bool ragged = tokens != tp;
-    // Pass 1: row maxima of u over this key half (K only, kRing1 blocks of
-    // 8 KB in flight in the half's 32 KB).
-    constexpr int kRing1 = 4;
+    // Pass 1: row maxima of u over this key half, K only, blocks it and
+    // it + 1 in flight while it is scored (slot it % 3).
     float m = -INFINITY;
-#pragma unroll
-    for (int d = 0; d < kRing1 - 1; ++d)
-        if (static_cast<uint32_t>(d) < nkb) issue_planes(kb0 + d, tiles + d * (kTile / 2), false);
+    if (nkb > 0) issue_planes(kb0, slots, false);
+    if (nkb > 1) issue_planes(kb0 + 1, slots + kSlot, false);
     for (uint32_t it = 0; it < first_half; ++it) {
         const uint32_t kb = kb0 + it;
         const bool have = it < nkb;
-        // this wave has issued blocks up to min(it + kRing1 - 2, nkb - 1)
-        const int later = have ? min(kRing1 - 2, static_cast<int>(nkb) - 1 - static_cast<int>(it)) : 0;
-        wait_block(later, 4);
-        if (it + kRing1 - 1 < nkb)
-            issue_planes(kb + kRing1 - 1, tiles + ((it + kRing1 - 1) % kRing1) * (kTile / 2), false);
+        // this wave has issued blocks up to min(it + 1, nkb - 1)
+        wait_slots(have ? min(1, static_cast<int>(nkb) - 1 - static_cast<int>(it)) : 0);
+        if (it + 2 < nkb) issue_planes(kb + 2, slots + ((it + 2) % kSlots) * kSlot, false);
         if (have) {
-            const int8_t* t = tiles + (it % kRing1) * (kTile / 2);
+            const int8_t* t = slots + (it % kSlots) * kSlot;
             float s[4][4];
             if (ragged && kb + 1 == blocks)
                 block_scores(t, kb, std::true_type{}, s);
@@ -407,33 +400,46 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     __syncthreads();  // every wave is done with the pass-1 ring before it is reused
     m = fmaxf(m, __shfl_xor(m, 16, kWave));
     m = fmaxf(m, __shfl_xor(m, 32, kWave));
-    // [half][group][query] maxima in the second pass-2 slot of key half 1;
-    // every wave has read them (full barrier) before pass 2 copies anything.
-    float* half_max = reinterpret_cast<float*>(lds + 3 * kTile);
+    // [half][group][query] maxima; every wave has read them (full barrier)
+    // before pass 2 copies anything.
+    float* half_max = reinterpret_cast<float*>(lds);
     if (g == 0) half_max[(half * 2 + group) * 16 + col] = m;
     __syncthreads();
     m = fmaxf(half_max[group * 16 + col], half_max[(2 + group) * 16 + col]);
     __syncthreads();
 
     // Pass 2: E = 21-bit softmax numerators, sum_j E, sum_j E V over this half.
+    // Slots rotate: block it has K in slot ks and V in slot vs; K(it + 1) is
+    // copied into the free slot once block it - 1 is done everywhere (top
+    // barrier), V(it + 1) into ks once every wave has scored block it (middle
+    // barrier).
     v4i c0[4], c7[4], c14[4], c21[4];
 #pragma unroll
     for (int fb = 0; fb < 4; ++fb) c0[fb] = c7[fb] = c14[fb] = c21[fb] = v4i{0, 0, 0, 0};
     uint64_t lsum = 0;
-    if (nkb > 0) issue_planes(kb0, tiles, true);
+    int ks = 0, vs = 1, fs = 2;
+    if (nkb > 0) {
+        issue_planes(kb0, slots, false);
+        issue_planes(kb0, slots + kSlot, true);
+    }
     for (uint32_t it = 0; it < first_half; ++it) {
-        const int buf = static_cast<int>(it & 1u);
         const uint32_t kb = kb0 + it;
         const bool have = it < nkb;
-        wait_block(0, 8);
-        if (it + 1 < nkb) issue_planes(kb + 1, tiles + (buf ^ 1) * kTile, true);
+        const bool next = it + 1 < nkb;
+        wait_slots(have ? 1 : 0);  // K(it); V(it) may still be in flight
+        if (next) issue_planes(kb + 1, slots + fs * kSlot, false);
+        float s[4][4];
         if (have) {
-            const int8_t* t = tiles + buf * kTile;
-            float s[4][4];
+            const int8_t* t = slots + ks * kSlot;
             if (ragged && kb + 1 == blocks)
                 block_scores(t, kb, std::true_type{}, s);
             else
                 block_scores(t, kb, std::false_type{}, s);
+        }
+        wait_slots(next ? 1 : 0);  // V(it); K(it + 1) may still be in flight
+        if (next) issue_planes(kb + 1, slots + ks * kSlot, true);
+        if (have) {
+            const int8_t* t = slots + vs * kSlot;
             v4i e0, e1, e2;
             uint32_t lblock = 0;  // <= 16 * 2^21
 #pragma unroll
@@ -453,14 +459,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
 #pragma unroll
             for (int fb = 0; fb < 4; ++fb) {
                 const uint32_t at = lds_chunk(fb * 16 + col, g);
-                const v4i v1 = *reinterpret_cast<const v4i*>(t + 2 * kPlane + at);
-                const v4i v0 = *reinterpret_cast<const v4i*>(t + 3 * kPlane + at);
+                const v4i v1 = *reinterpret_cast<const v4i*>(t + 0 * kPlane + at);
+                const v4i v0 = *reinterpret_cast<const v4i*>(t + 1 * kPlane + at);
                 c0[fb] = mfma8(v0, e0, c0[fb]);
                 c7[fb] = mfma8(v1, e0, mfma8(v0, e1, c7[fb]));
                 c14[fb] = mfma8(v1, e1, mfma8(v0, e2, c14[fb]));
                 c21[fb] = mfma8(v1, e2, c21[fb]);
             }
         }
+        const int k2 = fs;
+        fs = vs;
+        vs = ks;
+        ks = k2;
     }
     __syncthreads();  // every wave is done with the ring before the sums reuse it
 
