@@ -89,7 +89,7 @@ class GemmArgs(C.Structure):
                 ("out_i32", C.c_void_p), ("out", C.c_void_p), ("out_row_offset", C.c_uint64),
                 ("out_row_stride", C.c_uint64), ("residual", C.c_void_p), ("gamma", C.c_void_p),
                 ("convt_kernel", C.c_uint32), ("convt_width", C.c_uint32), ("convt_height", C.c_uint32),
-                ("convt_channels", C.c_uint32)]
+                ("convt_channels", C.c_uint32), ("col_absmax", C.c_void_p), ("col_absmax_begin", C.c_uint32)]
 
 
 class ConvArgs(C.Structure):
@@ -149,6 +149,7 @@ PROTOTYPES = {
     "dav2_hip_layer_norm": (C.c_int, [vp, vp, vp, vp, u32, u32, f32, vp]),
     "dav2_hip_layer_norm_quantize_i8": (C.c_int, [vp, u32, vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "dav2_hip_gemm_i8": (C.c_int, [C.POINTER(GemmArgs), vp]),
+    "dav2_hip_gemm_i8_row_tiles": (u32, [u32, u32, u32]),
     "dav2_hip_gelu": (C.c_int, [vp, vp, u64, vp]),
     "dav2_hip_add_scaled": (C.c_int, [vp, vp, vp, vp, u64, u32, vp]),
     "dav2_hip_add": (C.c_int, [vp, vp, vp, u64, vp]),
@@ -159,6 +160,7 @@ PROTOTYPES = {
     "dav2_hip_attention_scratch_bytes": (u64, [u32, u32, u32, C.c_int]),
     "dav2_hip_attention_fused_scratch_bytes": (u64, [u32, u32, u32]),
     "dav2_hip_attention_fused": (C.c_int, [vp, vp, u32, u32, u32, vp, u64, vp]),
+    "dav2_hip_attention_fused_colmax": (C.c_int, [vp, vp, u32, u32, vp, u32, vp, u64, vp]),
     "dav2_hip_bilinear_align_true": (C.c_int, [vp, vp, u32, u32, u32, u32, u32, vp]),
     "dav2_hip_minmax_partials": (u32, [u64]),
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),

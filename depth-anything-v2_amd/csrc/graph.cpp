@@ -78,6 +78,12 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
         arena.get("enc.scores", fused ? HipOperators::attention_fused_scratch_bytes(T, H, batch)
                                       : HipOperators::attention_score_bytes(T, H, batch, attention_precision_));
     for (int i = 0; i < 4; ++i) features[i] = &arena.get("enc.feature" + std::to_string(i), tok_bytes);
+    // One image: the qkv GEMM also leaves the |k| and |v| column maxima per
+    // row tile, so the attention's digit packing reads qkv once.
+    const bool colmax = fused && batch == 1;
+    const std::uint32_t qkv_tiles = colmax ? HipOperators::gemm_row_tiles(rows, 3 * D) : 0;
+    DeviceBuffer* col_absmax =
+        colmax ? &arena.get("enc.qkv_colmax", std::uint64_t(qkv_tiles) * 2 * D * sizeof(float)) : nullptr;
 
     // Patch embedding + class token + position (operators.cpp:1211-1406), one
     // image at a time into rows [b*T, (b+1)*T).
@@ -101,11 +107,12 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
         ops_.layer_norm_quantize(current, F(".norm1.weight"), F(".norm1.bias"), rows, D, 1.0e-6f, nullptr);
         const GpuTensor& wqkv = W(".attn.qkv.weight");
         ops_.linear_int8_prequantized(qkv, wqkv.int8_buffer, wqkv.int8_scales, &F(".attn.qkv.bias"), rows, D, 3 * D,
-                                      HipOperators::Epilogue::row);
+                                      colmax ? HipOperators::Epilogue::row_colmax : HipOperators::Epilogue::row,
+                                      nullptr, 0, col_absmax, D);
         // attention (encoder.cpp:454-460): fused binary16-operand kernel in
         // int8 mode, materialised fp32 scores under FORCE_FP32(_ATTENTION)
         if (fused)
-            ops_.attention_fused(attn, qkv, T, H, batch, scores);
+            ops_.attention_fused(attn, qkv, T, H, batch, scores, col_absmax, qkv_tiles);
         else
             ops_.attention_batched(attn, qkv, T, H, batch, scores, attention_precision_);
         // proj + LayerScale residual (encoder.cpp:478-491), in place

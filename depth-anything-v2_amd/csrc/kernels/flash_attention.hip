@@ -254,6 +254,118 @@ __global__ __launch_bounds__(256) void pack_kv_kernel(const float* __restrict__ 
     }
 }
 
+// One image: q, k and v of 64 tokens of head h into digit planes in one
+// pass (pack_q_kernel + pack_kv_kernel for batch 1), the maxima of |k| and
+// |v| per column coming from the qkv GEMM's row-tile partials
+// col_absmax[t][c] (c < D: k column c, c >= D: v column c - D). Thread t
+// owns token row t/4, features 16*(t%4)..+15 of q and k, and feature t/4,
+// block positions 16*(t%4)..+15 of v.
+__global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__ qkv,
+                                                       const float* __restrict__ col_absmax, uint32_t partial_rows,
+                                                       int8_t* __restrict__ qd, int8_t* __restrict__ kd,
+                                                       int8_t* __restrict__ vd, int* __restrict__ qe,
+                                                       int* __restrict__ ke, int* __restrict__ ve, uint32_t tokens,
+                                                       uint32_t heads, uint32_t tp) {
+    __shared__ float tile[64][65];  // v [token][feature]
+    __shared__ float kred[4];
+    __shared__ float vred[4][64];
+    const uint32_t h = blockIdx.y;
+    const uint32_t D = heads * 64u;
+    const uint32_t j0 = blockIdx.x * kBlock;
+    const int tid = threadIdx.x, hi4 = tid >> 2, c16 = (tid & 3) * 16;
+    const uint32_t t = j0 + hi4;
+
+    float q[16], k[16];
+    {
+        const float* src = qkv + static_cast<uint64_t>(t) * 3u * D + h * 64u + c16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4 vq = make_float4(0.f, 0.f, 0.f, 0.f), vk = vq, vv = vq;
+            if (t < tokens) {
+                vq = *reinterpret_cast<const float4*>(src + 4 * i);
+                vk = *reinterpret_cast<const float4*>(src + D + 4 * i);
+                vv = *reinterpret_cast<const float4*>(src + 2u * D + 4 * i);
+            }
+            q[4 * i + 0] = vq.x * 0.125f;
+            q[4 * i + 1] = vq.y * 0.125f;
+            q[4 * i + 2] = vq.z * 0.125f;
+            q[4 * i + 3] = vq.w * 0.125f;
+            k[4 * i + 0] = vk.x;
+            k[4 * i + 1] = vk.y;
+            k[4 * i + 2] = vk.z;
+            k[4 * i + 3] = vk.w;
+            tile[hi4][c16 + 4 * i + 0] = vv.x;
+            tile[hi4][c16 + 4 * i + 1] = vv.y;
+            tile[hi4][c16 + 4 * i + 2] = vv.z;
+            tile[hi4][c16 + 4 * i + 3] = vv.w;
+        }
+    }
+    // Head maximum of |k| and column maxima of |v| from the partials (wave w
+    // folds row tiles w, w + 4, ...; lane = feature).
+    {
+        const uint32_t f = static_cast<uint32_t>(tid & 63);
+        float mk = 0.0f, mv = 0.0f;
+        for (uint32_t r = static_cast<uint32_t>(tid >> 6); r < partial_rows; r += 4u) {
+            const float* row = col_absmax + static_cast<uint64_t>(r) * 2u * D + h * 64u + f;
+            mk = fmaxf(mk, row[0]);
+            mv = fmaxf(mv, row[D]);
+        }
+        mk = wave_max(mk);
+        if ((tid & 63) == 0) kred[tid >> 6] = mk;
+        vred[tid >> 6][f] = mv;
+    }
+
+    // q: exponent of the row maximum over the four lanes of the row
+    int8_t d1[16], d0[16];
+    {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a = fmaxf(a, fabsf(q[i]));
+        a = fmaxf(a, __shfl_xor(a, 1, kWave));
+        a = fmaxf(a, __shfl_xor(a, 2, kWave));
+        int e = 0;
+        if (a != 0.0f) frexpf(a, &e);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            d1[i] = 0;
+            d0[i] = 0;
+            if (a != 0.0f) digits15(q[i], 14 - e, d1[i], d0[i]);
+        }
+        int8_t* p0 = qd + (static_cast<uint64_t>(h) * 2u * tp + t) * 64u + c16;
+        store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
+        if ((tid & 3) == 0) qe[static_cast<uint64_t>(h) * tp + t] = a != 0.0f ? e - 14 : 0;
+    }
+    __syncthreads();
+    {  // k: one exponent per head
+        const float a = fmaxf(fmaxf(kred[0], kred[1]), fmaxf(kred[2], kred[3]));
+        int e = 0;
+        if (a != 0.0f) frexpf(a, &e);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            d1[i] = 0;
+            d0[i] = 0;
+            if (a != 0.0f) digits15(k[i], 14 - e, d1[i], d0[i]);
+        }
+        int8_t* p0 = kd + (static_cast<uint64_t>(h) * 2u * tp + t) * 64u + c16;
+        store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
+        if (blockIdx.x == 0 && tid == 0) ke[h] = a != 0.0f ? e - 14 : 0;
+    }
+    {  // v: feature hi4, block positions c16..c16+15
+        const float mv = fmaxf(fmaxf(vred[0][hi4], vred[1][hi4]), fmaxf(vred[2][hi4], vred[3][hi4]));
+        int e = 0;
+        if (mv != 0.0f) frexpf(mv, &e);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            d1[i] = 0;
+            d0[i] = 0;
+            if (mv != 0.0f) digits15(tile[perm64(c16 + i)][hi4], 14 - e, d1[i], d0[i]);
+        }
+        int8_t* p0 = vd + (static_cast<uint64_t>(h) * 2u * 64u + hi4) * tp + j0 + c16;
+        store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
+        if (blockIdx.x == 0 && (tid & 3) == 0) ve[static_cast<uint64_t>(h) * 64u + hi4] = mv != 0.0f ? e - 14 : 0;
+    }
+}
+
 DAV2_DEV v4i mfma8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 
 // E = min(rint(pow2(x) * 2^21), 2^21 - 1) for x <= 0 (or -inf / NaN: 0).
@@ -295,7 +407,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     // wave-uniform values kept in scalar registers (uniform branches)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int group = wave & 1, half = wave >> 1;
-    const int htid = tid & 127;  // thread index within the key half
     const int col = lane & 15, g = lane >> 4;
     const uint32_t q0 = qtile * 32u + group * 16u;
     const uint64_t plane_qk = static_cast<uint64_t>(tp) * 64u;
@@ -529,16 +640,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     }
 }
 
-}  // namespace
-
-extern "C" {
-
-DAV2_API uint64_t dav2_hip_attention_fused_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch) {
-    return layout_for(tokens, heads, batch).bytes;
-}
-
-DAV2_API int dav2_hip_attention_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
-                                      uint32_t batch, void* scratch, uint64_t scratch_bytes, void* stream) {
+// Digit packing (two passes, or one from the GEMM's column maxima when
+// col_absmax is given, batch 1), then the attention kernel.
+int run_attention(float* out, const float* qkv, uint32_t tokens, uint32_t heads, uint32_t batch,
+                  const float* col_absmax, uint32_t partial_rows, void* scratch, uint64_t scratch_bytes,
+                  void* stream) {
     if (!out || !qkv || !scratch || tokens == 0 || heads == 0 || batch == 0) return hipErrorInvalidValue;
     if (heads > 65535u || batch > 65535u || tokens > 65536u) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(qkv) |
@@ -562,11 +668,36 @@ DAV2_API int dav2_hip_attention_fused(float* out, const float* qkv, uint32_t tok
     float* vmax = reinterpret_cast<float*>(base + l.vmax);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(tp / kBlock, heads, batch);
-    hipLaunchKernelGGL(pack_q_kernel, grid, dim3(256), 0, s, qkv, qd, qe, kmax, vmax, tokens, heads, tp);
-    hipLaunchKernelGGL(pack_kv_kernel, grid, dim3(256), 0, s, qkv, kmax, vmax, kd, vd, ke, ve, tokens, heads, tp);
+    if (col_absmax) {
+        hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(256), 0, s, qkv, col_absmax, partial_rows, qd, kd, vd, qe, ke,
+                           ve, tokens, heads, tp);
+    } else {
+        hipLaunchKernelGGL(pack_q_kernel, grid, dim3(256), 0, s, qkv, qd, qe, kmax, vmax, tokens, heads, tp);
+        hipLaunchKernelGGL(pack_kv_kernel, grid, dim3(256), 0, s, qkv, kmax, vmax, kd, vd, ke, ve, tokens, heads, tp);
+    }
     hipLaunchKernelGGL(attention_exact_kernel, dim3(tp / 32u, heads, batch), dim3(kAttnThreads), kAttnLds, s, qd,
                        kd, vd, qe, ke, ve, out, tokens, heads, tp);
     return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+DAV2_API uint64_t dav2_hip_attention_fused_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch) {
+    return layout_for(tokens, heads, batch).bytes;
+}
+
+DAV2_API int dav2_hip_attention_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
+                                      uint32_t batch, void* scratch, uint64_t scratch_bytes, void* stream) {
+    return run_attention(out, qkv, tokens, heads, batch, nullptr, 0, scratch, scratch_bytes, stream);
+}
+
+DAV2_API int dav2_hip_attention_fused_colmax(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
+                                             const float* col_absmax, uint32_t partial_rows, void* scratch,
+                                             uint64_t scratch_bytes, void* stream) {
+    if (!col_absmax || partial_rows == 0 || (reinterpret_cast<uintptr_t>(col_absmax) & 3u)) return hipErrorInvalidValue;
+    return run_attention(out, qkv, tokens, heads, 1, col_absmax, partial_rows, scratch, scratch_bytes, stream);
 }
 
 }  // extern "C"

@@ -42,7 +42,15 @@ struct GemmParams {
     const float* gamma;
     uint32_t convt_k, convt_w, convt_h, convt_c;
     uint32_t coalesced_out;  // row-major output rows 16-byte aligned (n % 4 == 0, out aligned)
+    float* col_absmax;       // ROW_COLMAX partial maxima [row tile][n - col_absmax_begin]
+    uint32_t col_absmax_begin;
 };
+
+template <int EPI>
+constexpr bool row_major_epi() {
+    return EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_GELU || EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE ||
+           EPI == DAV2_GEMM_EPI_ROW_COLMAX;
+}
 
 DAV2_DEV float dequant(int32_t acc, float s_in, float s_w, float b) {
     float v = static_cast<float>(acc);
@@ -311,10 +319,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
     // Row-major epilogues: the final values go through LDS so that each
     // store writes whole 256-byte row segments (16 lanes x float4) instead
     // of 64-byte pieces of four rows.
-    constexpr bool kRowMajor = EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_GELU ||
-                               EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE;
+    constexpr bool kRowMajor = row_major_epi<EPI>();
+    constexpr bool kColMax = EPI == DAV2_GEMM_EPI_ROW_COLMAX;
     constexpr int kOutStride = BN + 4;  // floats; rows 4 apart start 16 banks apart (launch_cfg sizes LDS for it)
-    if (kRowMajor && g.coalesced_out) {
+    if (kRowMajor && (kColMax || g.coalesced_out)) {
         float* tile = reinterpret_cast<float*>(smem);
         __syncthreads();  // every wave is done with the last stage's operands
 #pragma unroll
@@ -331,11 +339,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
         constexpr int kLanesPerRow = BN / 4, kRowsPerPass = 64 * NW / kLanesPerRow;
         const int c4 = (tid % kLanesPerRow) * 4;
         const uint32_t col = col0 + c4;
+        float4 cmax = make_float4(0.f, 0.f, 0.f, 0.f);  // column maxima over this thread's rows
 #pragma unroll
         for (int rr = tid / kLanesPerRow; rr < BM; rr += kRowsPerPass) {
             const uint32_t row = row0 + rr;
             if (row >= g.rows_p) break;
             const float4 v = *reinterpret_cast<const float4*>(tile + rr * kOutStride + c4);
+            if (kColMax) {
+                cmax.x = fmaxf(cmax.x, fabsf(v.x));
+                cmax.y = fmaxf(cmax.y, fabsf(v.y));
+                cmax.z = fmaxf(cmax.z, fabsf(v.z));
+                cmax.w = fmaxf(cmax.w, fabsf(v.w));
+            }
             float* dst = g.out + (static_cast<uint64_t>(row) + g.out_row_offset) * g.n + col;
             if (col + 3 < g.rows_q) {
                 *reinterpret_cast<float4*>(dst) = v;
@@ -343,6 +358,29 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
                 if (col < g.rows_q) dst[0] = v.x;
                 if (col + 1 < g.rows_q) dst[1] = v.y;
                 if (col + 2 < g.rows_q) dst[2] = v.z;
+            }
+        }
+        if (kColMax && col0 >= g.col_absmax_begin) {
+            // lanes l, l ^ 16, l ^ 32, l ^ 48 of a wave hold the same columns
+            static_assert(kLanesPerRow == 16 && BM * kOutStride * 4 + NW * BN * 4 <=
+                          (BM * kOutStride * 4 > STAGES * (BM + BN) * BK ? BM * kOutStride * 4 : STAGES * (BM + BN) * BK),
+                          "column maxima: 16 lanes per row, partials fit behind the output tile");
+#pragma unroll
+            for (int o = 16; o < 64; o <<= 1) {
+                cmax.x = fmaxf(cmax.x, __shfl_xor(cmax.x, o, kWave));
+                cmax.y = fmaxf(cmax.y, __shfl_xor(cmax.y, o, kWave));
+                cmax.z = fmaxf(cmax.z, __shfl_xor(cmax.z, o, kWave));
+                cmax.w = fmaxf(cmax.w, __shfl_xor(cmax.w, o, kWave));
+            }
+            float* part = tile + BM * kOutStride;  // [wave][BN]
+            if (lane < 16) *reinterpret_cast<float4*>(part + wave * BN + c4) = cmax;
+            __syncthreads();
+            if (tid < BN && col0 + tid < g.rows_q) {
+                float m = part[tid];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) m = fmaxf(m, part[w * BN + tid]);
+                const uint64_t ld = g.rows_q - g.col_absmax_begin;
+                g.col_absmax[static_cast<uint64_t>(tm) * ld + (col0 - g.col_absmax_begin) + tid] = m;
             }
         }
         return;
@@ -369,15 +407,20 @@ void launch_cfg(const GemmParams& g, hipStream_t s) {
     // LDS: the stage ring, or the row-major output tile if that is larger.
     constexpr size_t ring = static_cast<size_t>(STAGES) * (BM + BN) * BK;
     constexpr size_t out_tile = static_cast<size_t>(BM) * (BN + 4) * 4;
-    constexpr bool row_major = EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_GELU ||
-                               EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE;
-    constexpr size_t lds = row_major && out_tile > ring ? out_tile : ring;
+    constexpr size_t lds = row_major_epi<EPI>() && out_tile > ring ? out_tile : ring;
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     (void)attr;
     const dim3 grid(ceil_div(g.rows_p, BM), ceil_div(g.rows_q, BN));
     hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>), grid, dim3(64 * WMW * WNW), lds, s, g);
+}
+
+// Rows of P per tile of the configuration launch_epi picks.
+inline uint32_t tile_rows(uint32_t rows_p, uint32_t rows_q, bool row_major) {
+    if (rows_p <= 32) return 32;
+    if (row_major && rows_q >= 2048 && rows_p >= 512) return 96;
+    return 64;
 }
 
 template <int EPI>
@@ -388,11 +431,11 @@ void launch_epi(const GemmParams& g, hipStream_t s) {
     // (720 workgroups for N = 3072, one round at three per CU, against 1056
     // 64x64 ones). Channel-major GEMMs with few output channels use 32-row
     // tiles.
-    constexpr bool row_major = EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_GELU ||
-                               EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE;
-    if (g.rows_p <= 32) launch_cfg<32, 64, 1, 2, 128, 3, EPI>(g, s);
-    else if (row_major && g.rows_q >= 2048 && g.rows_p >= 512) launch_cfg<96, 64, 2, 2, 128, 2, EPI>(g, s);
-    else launch_cfg<64, 64, 2, 2, 128, 3, EPI>(g, s);
+    switch (tile_rows(g.rows_p, g.rows_q, row_major_epi<EPI>())) {
+        case 32: launch_cfg<32, 64, 1, 2, 128, 3, EPI>(g, s); break;
+        case 96: launch_cfg<96, 64, 2, 2, 128, 2, EPI>(g, s); break;
+        default: launch_cfg<64, 64, 2, 2, 128, 3, EPI>(g, s); break;
+    }
 }
 
 }  // namespace
@@ -413,7 +456,11 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
          static_cast<uint64_t>(a->convt_width) * a->convt_height != a->m ||
          static_cast<uint64_t>(a->convt_kernel) * a->convt_kernel * a->convt_channels != a->n))
         return hipErrorInvalidValue;
-    if (e > DAV2_GEMM_EPI_CONVT) return hipErrorInvalidValue;
+    if (e == DAV2_GEMM_EPI_ROW_COLMAX &&
+        (!a->col_absmax || a->col_absmax_begin % 64 || a->col_absmax_begin >= a->n || a->n % 4 ||
+         (reinterpret_cast<uintptr_t>(a->out) & 15)))
+        return hipErrorInvalidValue;
+    if (e > DAV2_GEMM_EPI_ROW_COLMAX) return hipErrorInvalidValue;
 
     GemmParams g{};
     const bool swapped = e == DAV2_GEMM_EPI_TRANSPOSED || e == DAV2_GEMM_EPI_CONVT;
@@ -439,6 +486,8 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     g.convt_h = a->convt_height;
     g.convt_c = a->convt_channels;
     g.coalesced_out = !swapped && a->n % 4 == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0;
+    g.col_absmax = a->col_absmax;
+    g.col_absmax_begin = a->col_absmax_begin;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (e) {
         case DAV2_GEMM_EPI_RAW_I32: launch_epi<DAV2_GEMM_EPI_RAW_I32>(g, s); break;
@@ -447,6 +496,15 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
         case DAV2_GEMM_EPI_ROW_LAYERSCALE: launch_epi<DAV2_GEMM_EPI_ROW_LAYERSCALE>(g, s); break;
         case DAV2_GEMM_EPI_TRANSPOSED: launch_epi<DAV2_GEMM_EPI_TRANSPOSED>(g, s); break;
         case DAV2_GEMM_EPI_CONVT: launch_epi<DAV2_GEMM_EPI_CONVT>(g, s); break;
+        case DAV2_GEMM_EPI_ROW_COLMAX: launch_epi<DAV2_GEMM_EPI_ROW_COLMAX>(g, s); break;
     }
     return hipGetLastError();
+}
+
+extern "C" uint32_t dav2_hip_gemm_i8_row_tiles(uint32_t m, uint32_t n, uint32_t epilogue) {
+    const bool swapped = epilogue == DAV2_GEMM_EPI_TRANSPOSED || epilogue == DAV2_GEMM_EPI_CONVT;
+    const bool row_major = epilogue == DAV2_GEMM_EPI_ROW || epilogue == DAV2_GEMM_EPI_ROW_GELU ||
+                           epilogue == DAV2_GEMM_EPI_ROW_LAYERSCALE || epilogue == DAV2_GEMM_EPI_ROW_COLMAX;
+    const uint32_t rows_p = swapped ? n : m, rows_q = swapped ? m : n;
+    return ceil_div(rows_p, tile_rows(rows_p, rows_q, row_major));
 }

@@ -98,11 +98,19 @@ void HipOperators::linear_int8_prequantized(DeviceBuffer& output, const DeviceBu
                                             const DeviceBuffer& weight_scales, const DeviceBuffer* bias,
                                             std::uint32_t rows, std::uint32_t input_columns,
                                             std::uint32_t output_columns, Epilogue epilogue,
-                                            const DeviceBuffer* gamma, std::uint64_t output_row_offset) {
+                                            const DeviceBuffer* gamma, std::uint64_t output_row_offset,
+                                            DeviceBuffer* col_absmax, std::uint32_t col_absmax_begin) {
     if (workspace_ld_ != ld64(input_columns)) throw std::logic_error("int8 workspace holds rows of another width");
     require_bytes(output, (std::uint64_t(rows) + output_row_offset) * output_columns, "output");
     if (epilogue == Epilogue::row_layerscale && (!gamma || gamma->size() < output_columns * sizeof(float)))
         throw std::invalid_argument("layer scale buffer is too small");
+    if (epilogue == Epilogue::row_colmax) {
+        if (!col_absmax || col_absmax_begin % 64 || col_absmax_begin >= output_columns || output_row_offset != 0)
+            throw std::invalid_argument("invalid column maxima request");
+        require_bytes(*col_absmax,
+                      std::uint64_t(gemm_row_tiles(rows, output_columns)) * (output_columns - col_absmax_begin),
+                      "column maxima");
+    }
     dav2_gemm_i8_args a{};
     a.a = workspace_.packed(0).as<int8_t>();
     a.lda = workspace_ld_;
@@ -113,7 +121,12 @@ void HipOperators::linear_int8_prequantized(DeviceBuffer& output, const DeviceBu
     a.k = ld64(input_columns);
     a.epilogue = epilogue == Epilogue::row ? DAV2_GEMM_EPI_ROW
                  : epilogue == Epilogue::row_gelu ? DAV2_GEMM_EPI_ROW_GELU
-                                                  : DAV2_GEMM_EPI_ROW_LAYERSCALE;
+                 : epilogue == Epilogue::row_colmax ? DAV2_GEMM_EPI_ROW_COLMAX
+                                                    : DAV2_GEMM_EPI_ROW_LAYERSCALE;
+    if (epilogue == Epilogue::row_colmax) {
+        a.col_absmax = col_absmax->as<float>();
+        a.col_absmax_begin = col_absmax_begin;
+    }
     a.a_scales = workspace_.scales(0).as<float>();
     a.b_scales = weight_scales.as<float>();
     a.bias = bias ? bias->as<float>() : nullptr;
@@ -238,8 +251,13 @@ std::uint64_t HipOperators::attention_fused_scratch_bytes(std::uint32_t tokens, 
     return dav2_hip_attention_fused_scratch_bytes(tokens, heads, batch);
 }
 
+std::uint32_t HipOperators::gemm_row_tiles(std::uint32_t rows, std::uint32_t output_columns) {
+    return dav2_hip_gemm_i8_row_tiles(rows, output_columns, DAV2_GEMM_EPI_ROW_COLMAX);
+}
+
 void HipOperators::attention_fused(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
-                                   std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scratch) {
+                                   std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scratch,
+                                   const DeviceBuffer* col_absmax, std::uint32_t partial_rows) {
     if (tokens == 0 || heads == 0 || batch == 0) throw std::invalid_argument("invalid attention dimensions");
     const std::uint64_t elements = std::uint64_t(batch) * tokens * heads * 64;
     require_bytes(output, elements, "attention output");
@@ -250,6 +268,15 @@ void HipOperators::attention_fused(DeviceBuffer& output, const DeviceBuffer& qkv
     // QK^T and PV: 4*T*T*64 flops per head.
     const double flops = 4.0 * batch * heads * double(tokens) * tokens * 64.0;
     ProfileScope p(context_.profiler(), "attention_fused", flops, "FLOP", s);
+    if (col_absmax) {
+        if (batch != 1 || partial_rows == 0) throw std::invalid_argument("column maxima serve one image");
+        require_bytes(*col_absmax, std::uint64_t(partial_rows) * 2 * heads * 64, "column maxima");
+        hip_check(dav2_hip_attention_fused_colmax(output.as<float>(), qkv.as<float>(), tokens, heads,
+                                                  col_absmax->as<float>(), partial_rows, scratch.data(),
+                                                  scratch.size(), s),
+                  "fused attention");
+        return;
+    }
     hip_check(dav2_hip_attention_fused(output.as<float>(), qkv.as<float>(), tokens, heads, batch, scratch.data(),
                                        scratch.size(), s),
               "fused attention");

@@ -119,11 +119,16 @@ public:
     void quantize_rows(const DeviceBuffer& input, std::uint64_t input_offset, std::uint32_t rows,
                        std::uint32_t columns);
     // GEMM on the rows currently held by the workspace.
-    enum class Epilogue { row, row_gelu, row_layerscale };
+    // row_colmax: row, and per GEMM row tile the maxima of |out| of the
+    // columns from col_absmax_begin on into col_absmax
+    // (gemm_row_tiles() x (output_columns - col_absmax_begin) floats).
+    enum class Epilogue { row, row_gelu, row_layerscale, row_colmax };
     void linear_int8_prequantized(DeviceBuffer& output, const DeviceBuffer& int8_weight,
                                   const DeviceBuffer& weight_scales, const DeviceBuffer* bias, std::uint32_t rows,
                                   std::uint32_t input_columns, std::uint32_t output_columns, Epilogue epilogue,
-                                  const DeviceBuffer* gamma = nullptr, std::uint64_t output_row_offset = 0);
+                                  const DeviceBuffer* gamma = nullptr, std::uint64_t output_row_offset = 0,
+                                  DeviceBuffer* col_absmax = nullptr, std::uint32_t col_absmax_begin = 0);
+    static std::uint32_t gemm_row_tiles(std::uint32_t rows, std::uint32_t output_columns);
     // Batched attention over `batch` token matrices of `tokens` rows each.
     void attention_batched(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
                            std::uint32_t heads, std::uint32_t batch, DeviceBuffer& score_scratch,
@@ -133,8 +138,12 @@ public:
     // Fused integer-exact attention (int8 digit planes, exact int32 MFMA
     // sums): the int8-mode default in place of the materialised binary16
     // scores.
+    // With col_absmax (batch 1): the |k| and |v| column maxima of a
+    // row_colmax qkv GEMM from column heads*64 on, partial_rows row tiles;
+    // the digit packing then reads qkv once.
     void attention_fused(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens, std::uint32_t heads,
-                         std::uint32_t batch, DeviceBuffer& scratch);
+                         std::uint32_t batch, DeviceBuffer& scratch, const DeviceBuffer* col_absmax = nullptr,
+                         std::uint32_t partial_rows = 0);
     static std::uint64_t attention_fused_scratch_bytes(std::uint32_t tokens, std::uint32_t heads,
                                                        std::uint32_t batch);
 

@@ -71,7 +71,9 @@ enum {
     DAV2_GEMM_EPI_ROW_GELU = 2,       /* ... then exact-erf GELU                        */
     DAV2_GEMM_EPI_ROW_LAYERSCALE = 3, /* out = residual + (acc*sa*sb + bias)*gamma[n'] */
     DAV2_GEMM_EPI_TRANSPOSED = 4,     /* out[n'*stride + m + off] (channel-major)       */
-    DAV2_GEMM_EPI_CONVT = 5           /* stride==kernel ConvTranspose scatter           */
+    DAV2_GEMM_EPI_CONVT = 5,          /* stride==kernel ConvTranspose scatter           */
+    DAV2_GEMM_EPI_ROW_COLMAX = 6      /* ROW, and per tile of rows the max |out| of each
+                                         column n' >= col_absmax_begin                  */
 };
 
 typedef struct dav2_gemm_i8_args {
@@ -91,11 +93,20 @@ typedef struct dav2_gemm_i8_args {
     const float* residual;  /* LAYERSCALE: may alias out                      */
     const float* gamma;
     uint32_t convt_kernel, convt_width, convt_height, convt_channels;
+    /* ROW_COLMAX: col_absmax[t][n' - col_absmax_begin] = max |out[m][n']| over
+     * the rows m of row tile t (dav2_hip_gemm_i8_row_tiles() tiles); the
+     * begin is a multiple of 64, n % 4 == 0 and out 16-byte aligned. */
+    float* col_absmax;
+    uint32_t col_absmax_begin;
 } dav2_gemm_i8_args;
 
 /* Replaces linear_int8_tiled.glsl:40-117 (src/operators.cpp:847-880) and
  * conv_transpose_int8.glsl:31-58 (:1969-1975). */
 DAV2_API int dav2_hip_gemm_i8(const dav2_gemm_i8_args* args, void* stream);
+/* Row tiles (rows of col_absmax) of a dav2_hip_gemm_i8 call with m rows and
+ * n output columns. No reference counterpart: the attention's digit packing
+ * reads these maxima instead of a pass over k and v. */
+DAV2_API uint32_t dav2_hip_gemm_i8_row_tiles(uint32_t m, uint32_t n, uint32_t epilogue);
 
 /* Implicit-GEMM int8 convolution: replaces the im2col_quantize_int8.glsl +
  * linear_int8_tiled.glsl pair of VulkanOperators::conv2d_int8
@@ -186,6 +197,14 @@ DAV2_API int dav2_hip_attention_values(float* out, const void* probabilities,
 DAV2_API uint64_t dav2_hip_attention_fused_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch);
 DAV2_API int dav2_hip_attention_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
                                       uint32_t batch, void* scratch, uint64_t scratch_bytes, void* stream);
+/* The same attention for one image (batch 1) when the qkv GEMM ran with
+ * DAV2_GEMM_EPI_ROW_COLMAX from column heads*64 on: col_absmax holds
+ * [partial_rows][2*heads*64] maxima of |k| and |v| per column and row tile,
+ * so the digit packing reads qkv once. Same output bits as
+ * dav2_hip_attention_fused. No reference counterpart (a fusion). */
+DAV2_API int dav2_hip_attention_fused_colmax(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
+                                             const float* col_absmax, uint32_t partial_rows, void* scratch,
+                                             uint64_t scratch_bytes, void* stream);
 
 /* bilinear_align_true.glsl:27-63, CHW. */
 DAV2_API int dav2_hip_bilinear_align_true(float* out, const float* input,

@@ -342,6 +342,37 @@ def test_gemm_row_epilogues(gpu, pkg, lib, oracle, m, n, k):
     assert np.array_equal(host(torch, outr).view(np.uint32), refr.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,n,k,begin", [(1370, 3072, 1024, 1024), (1369, 2304, 384, 768), (300, 1024, 256, 512),
+                                         (20, 192, 64, 64), (1, 128, 64, 0)])
+def test_gemm_colmax_epilogue(gpu, pkg, lib, oracle, m, n, k, begin):
+    # ROW output, plus per row tile the max |out| of each column >= begin
+    # (max is exact, so the partials equal numpy's over the same rows).
+    torch = gpu
+    _announce("gemm colmax", m, n, k, begin)
+    rng = np.random.default_rng(m + n + begin)
+    a, b, sa, sb, bias = _random_gemm_case(rng, m, n, k)
+    acc = oracle.gemm_i8(a, b)
+    ld = (k + 63) // 64 * 64
+    ad, bd = dev(torch, pad_rows(a, ld)), dev(torch, pad_rows(b, ld))
+    sad, sbd, biasd = dev(torch, sa), dev(torch, sb), dev(torch, bias)
+    tiles = lib.dav2_hip_gemm_i8_row_tiles(m, n, 6)
+    bm = 32 if m <= 32 else (96 if n >= 2048 and m >= 512 else 64)
+    assert tiles == -(-m // bm)
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    cmax = torch.full((tiles, n - begin), -1.0, dtype=torch.float32, device="cuda")
+    base = dict(a=ptr(ad), lda=ld, b=ptr(bd), ldb=ld, m=m, n=n, k=ld, a_scales=ptr(sad), b_scales=ptr(sbd),
+                bias=ptr(biasd), out=ptr(out), epilogue=6)
+    ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, col_absmax=ptr(cmax), col_absmax_begin=begin)),
+                                 stream(torch)))
+    ref = oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m).reshape(m, n)
+    assert np.array_equal(host(torch, out).view(np.uint32), ref.view(np.uint32))
+    want = np.stack([np.abs(ref[t * bm:(t + 1) * bm, begin:]).max(axis=0) for t in range(tiles)])
+    assert np.array_equal(host(torch, cmax), want)
+    for bad in (dict(col_absmax=ptr(cmax), col_absmax_begin=begin + 32), dict(col_absmax=ptr(cmax), col_absmax_begin=n),
+                dict(col_absmax=None, col_absmax_begin=begin)):
+        assert lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, **bad)), stream(torch)) != 0
+
+
 def test_gemm_rejects_bad_arguments(gpu, pkg, lib):
     torch = gpu
     a = torch.zeros((4, 64), dtype=torch.int8, device="cuda")
@@ -485,7 +516,46 @@ def test_attention_fused(gpu, lib, oracle, tokens, heads, batch):
         assert np.abs(out[rows] - exact).max() <= 2e-4
 
 
-def test_attention_fused_peaked_and_zero_rows(gpu, lib, oracle):
+def _attention_colmax_gpu(torch, lib, qkv, tokens, heads, partial_rows):
+    # column maxima of |k| | |v| over `partial_rows` row chunks, as the qkv
+    # GEMM's ROW_COLMAX epilogue leaves them
+    D = heads * 64
+    bounds = np.linspace(0, tokens, partial_rows + 1).astype(int)
+    cm = np.zeros((partial_rows, 2 * D), np.float32)
+    for p in range(partial_rows):
+        if bounds[p + 1] > bounds[p]:
+            cm[p] = np.abs(qkv[bounds[p]:bounds[p + 1], D:]).max(axis=0)
+    qd, cmd = dev(torch, qkv), dev(torch, cm)
+    nbytes = lib.dav2_hip_attention_fused_scratch_bytes(tokens, heads, 1)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    out = empty(torch, (tokens, D), torch.float32)
+    ok(lib, lib.dav2_hip_attention_fused_colmax(ptr(out), ptr(qd), tokens, heads, ptr(cmd), partial_rows, ptr(buf),
+                                                nbytes, stream(torch)))
+    assert lib.dav2_hip_attention_fused_colmax(ptr(out), ptr(qd), tokens, heads, None, partial_rows, ptr(buf),
+                                               nbytes, stream(torch)) != 0
+    assert lib.dav2_hip_attention_fused_colmax(ptr(out), ptr(qd), tokens, heads, ptr(cmd), 0, ptr(buf),
+                                               nbytes, stream(torch)) != 0
+    return host(torch, out)
+
+
+@pytest.mark.parametrize("tokens,heads,partial_rows", [(1, 1, 1), (5, 2, 3), (64, 3, 1), (77, 4, 2), (1370, 16, 15),
+                                                       (1370, 6, 22), (2000, 2, 7)])
+def test_attention_fused_colmax(gpu, lib, oracle, tokens, heads, partial_rows):
+    # One-pass digit packing from column maxima: the same bits as the
+    # two-pass packing and the oracle.
+    torch = gpu
+    _announce("attention fused colmax", tokens, heads, partial_rows)
+    rng = np.random.default_rng(tokens * 5 + heads)
+    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * 0.5).astype(np.float32)
+    got = _attention_colmax_gpu(torch, lib, qkv, tokens, heads, partial_rows)
+    two_pass = _attention_fused_gpu(torch, lib, qkv, tokens, heads, 1)
+    assert np.array_equal(got.view(np.uint32), two_pass.view(np.uint32))
+    ref = oracle.attention(qkv, tokens, heads, fused=True)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("colmax", [False, True])
+def test_attention_fused_peaked_and_zero_rows(gpu, lib, oracle, colmax):
     # Peaked rows (|s| up to ~60, most numerators underflow to 0), an all-zero
     # query row, an all-zero key row and an all-zero value column.
     torch = gpu
@@ -495,7 +565,8 @@ def test_attention_fused_peaked_and_zero_rows(gpu, lib, oracle):
     qkv[7, :64] = 0.0
     qkv[9, heads * 64:heads * 64 + 64] = 0.0
     qkv[:, 2 * heads * 64 + 5] = 0.0
-    out = _attention_fused_gpu(torch, lib, qkv, tokens, heads, 1)
+    out = (_attention_colmax_gpu(torch, lib, qkv, tokens, heads, 4) if colmax
+           else _attention_fused_gpu(torch, lib, qkv, tokens, heads, 1))
     ref = oracle.attention(qkv, tokens, heads, fused=True)
     assert np.isfinite(out).all()
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
