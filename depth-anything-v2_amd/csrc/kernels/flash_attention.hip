@@ -56,7 +56,7 @@ constexpr int kSlots = 3;          // ring slots per key half
 constexpr int kEMax = 2097151;     // 2^21 - 1
 constexpr int kAttnThreads = 256;  // 2 query groups x 2 key halves
 constexpr size_t kAttnLds = 2 * kSlots * kSlot;  // [key half][slot]
-static_assert(2 * 64 * 66 * 4 <= kAttnLds, "the sums hand-over fits in the slots");
+static_assert(2 * 64 * 67 * 4 <= kAttnLds, "the sums hand-over fits in the slots");
 
 inline uint32_t padded_tokens(uint32_t tokens) { return (tokens + kBlock - 1u) / kBlock * kBlock; }
 
@@ -303,12 +303,22 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
     // Head maximum of |k| and column maxima of |v| from the partials (wave w
     // folds row tiles w, w + 4, ...; lane = feature).
     {
+        // The first 16 row tiles are loaded at once (indices clamped: a
+        // repeated row leaves a maximum unchanged), further ones in a loop.
         const uint32_t f = static_cast<uint32_t>(tid & 63);
-        float mk = 0.0f, mv = 0.0f;
-        for (uint32_t r = static_cast<uint32_t>(tid >> 6); r < partial_rows; r += 4u) {
-            const float* row = col_absmax + static_cast<uint64_t>(r) * 2u * D + h * 64u + f;
-            mk = fmaxf(mk, row[0]);
-            mv = fmaxf(mv, row[D]);
+        const float* cols = col_absmax + h * 64u + f;
+        float pk[4], pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = min(static_cast<uint32_t>(tid >> 6) + 4u * i, partial_rows - 1u);
+            pk[i] = cols[static_cast<uint64_t>(r) * 2u * D];
+            pv[i] = cols[static_cast<uint64_t>(r) * 2u * D + D];
+        }
+        float mk = fmaxf(fmaxf(pk[0], pk[1]), fmaxf(pk[2], pk[3]));
+        float mv = fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3]));
+        for (uint32_t r = static_cast<uint32_t>(tid >> 6) + 16u; r < partial_rows; r += 4u) {
+            mk = fmaxf(mk, cols[static_cast<uint64_t>(r) * 2u * D]);
+            mv = fmaxf(mv, cols[static_cast<uint64_t>(r) * 2u * D + D]);
         }
         mk = wave_max(mk);
         if ((tid & 63) == 0) kred[tid >> 6] = mk;
@@ -368,28 +378,52 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
 
 DAV2_DEV v4i mfma8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 
-// E = min(rint(pow2(x) * 2^21), 2^21 - 1) for x <= 0 (or -inf / NaN: 0).
-// pow2(x) = 2^n * p(x - n), n = rint(x), p the degree-6 Taylor polynomial of
-// 2^f (coefficients ln2^k / k!); x below -100 gives E = 0. The final
-// rounding adds 2^23 (ties to even) and reads the integer from the bits.
-DAV2_DEV int numerator21(float x) {
+// E = rint(min(pow2(x) * 2^21, 2^21 - 1)) for x <= 0 (or -inf: 0), returned
+// as the bits of E + 2^23, i.e. 0x4B000000 + E. pow2(x) = 2^n p(x - n),
+// n = rint(x), p the degree-6 Taylor polynomial of 2^f (coefficients
+// ln2^k / k!, here times 2^21, which scales every Horner step exactly);
+// x below -100 gives E = 0. Adding 2^23 rounds ties to even.
+DAV2_DEV uint32_t numerator21_bits(float x) {
+    constexpr float k21 = 2097152.0f;
     const float xc = fmaxf(x, -100.0f);
     const float n = __builtin_rintf(xc);
     const float f = xc - n;
-    float p = 1.54035304e-4f;
-    p = fmaf(p, f, 1.33335581e-3f);
-    p = fmaf(p, f, 9.61812911e-3f);
-    p = fmaf(p, f, 5.55041087e-2f);
-    p = fmaf(p, f, 2.40226507e-1f);
-    p = fmaf(p, f, 6.93147181e-1f);
-    p = fmaf(p, f, 1.0f);
-    const float v = ldexpf(p, static_cast<int>(n) + 21);  // < 2^21 + 1, normal
-    const float r = v + 8388608.0f;
-    return min(static_cast<int>(__float_as_uint(r) - 0x4B000000u), kEMax);
+    float p = 1.54035304e-4f * k21;
+    p = fmaf(p, f, 1.33335581e-3f * k21);
+    p = fmaf(p, f, 9.61812911e-3f * k21);
+    p = fmaf(p, f, 5.55041087e-2f * k21);
+    p = fmaf(p, f, 2.40226507e-1f * k21);
+    p = fmaf(p, f, 6.93147181e-1f * k21);
+    p = fmaf(p, f, k21);
+    const float v = fminf(ldexpf(p, static_cast<int>(n)), static_cast<float>(kEMax));  // normal
+    return __float_as_uint(v + 8388608.0f);
+}
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+DAV2_DEV uint32_t shr16x2(uint32_t v, int s) {  // each 16-bit half shifted right
+    u16x2 h = __builtin_bit_cast(u16x2, v);
+    h = h >> static_cast<unsigned short>(s);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// 7-bit digits of E_k = R_k - 0x4B000000 (k = 0..3, E_k < 2^21) as the bytes
+// of three words: w0 = E_k & 127, w1 = (E_k >> 7) & 127, w2 = E_k >> 14.
+DAV2_DEV void digits21(const uint32_t R[4], int& w0, int& w1, int& w2) {
+    const uint32_t lo01 = __builtin_amdgcn_perm(R[1], R[0], 0x05040100u);  // R0 bits 0..15 | R1 bits 0..15
+    const uint32_t lo23 = __builtin_amdgcn_perm(R[3], R[2], 0x05040100u);
+    const uint32_t hi01 = __builtin_amdgcn_perm(R[1], R[0], 0x06050201u);  // R0 bits 8..23 | R1 bits 8..23
+    const uint32_t hi23 = __builtin_amdgcn_perm(R[3], R[2], 0x06050201u);
+    // byte 0 of each 16-bit half, gathered: [x01.b0, x01.b2, x23.b0, x23.b2]
+    w0 = static_cast<int>(__builtin_amdgcn_perm(lo23, lo01, 0x06040200u) & 0x7f7f7f7fu);
+    w1 = static_cast<int>(__builtin_amdgcn_perm(shr16x2(lo23, 7), shr16x2(lo01, 7), 0x06040200u) & 0x7f7f7f7fu);
+    // bits 14..21 of R: bit 21 is 0 (E < 2^21)
+    w2 = static_cast<int>(__builtin_amdgcn_perm(shr16x2(hi23, 6), shr16x2(hi01, 6), 0x06040200u));
 }
 
 // Wave w: query group w & 1 (16 queries), key half w >> 1.
-__global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
+// Three workgroups per CU need at most 168 VGPRs (3 waves per SIMD).
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3))) void attention_exact_kernel(
     const int8_t* __restrict__ qd, const int8_t* __restrict__ kd, const int8_t* __restrict__ vd,
     const int* __restrict__ qe, const int* __restrict__ ke, const int* __restrict__ ve, float* __restrict__ out,
     uint32_t tokens, uint32_t heads, uint32_t tp) {
@@ -459,30 +493,36 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
         __builtin_amdgcn_sched_barrier(0);
     };
     // Unscaled scores of the block for this lane: u[j][r] = key 16j + 4g + r,
-    // query col; TAIL masks keys >= tokens. All MFMAs are issued first.
+    // query col; TAIL masks keys >= tokens. The MFMAs of two key groups are
+    // issued before their results are converted (fewer live registers than
+    // all four).
     auto block_scores = [&](const int8_t* t, uint32_t kb, auto TAIL, float s[4][4]) {
-        v4i hi[4], mid[4], lo[4];
         const v4i zero = {0, 0, 0, 0};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t at = lds_chunk(j * 16 + col, g);
-            const v4i a1 = *reinterpret_cast<const v4i*>(t + 0 * kPlane + at);
-            const v4i a0 = *reinterpret_cast<const v4i*>(t + 1 * kPlane + at);
-            hi[j] = mfma8(a1, q1, zero);
-            mid[j] = mfma8(a1, q0v, zero);
-            lo[j] = mfma8(a0, q0v, zero);
-            mid[j] = mfma8(a0, q1, mid[j]);
-        }
+        for (int jp = 0; jp < 4; jp += 2) {
+            v4i hi[2], mid[2], lo[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                // |128 mid + lo| < 2^29 (exact in int32); hi * 2^14 is exact in fp32
-                const int rest = mid[j][r] * 128 + lo[j][r];
-                float v = fmaf(static_cast<float>(hi[j][r]), 16384.0f, static_cast<float>(rest));
-                if (decltype(TAIL)::value && kb * kBlock + j * 16 + 4 * g + r >= tokens) v = -INFINITY;
-                s[j][r] = v;
+            for (int jj = 0; jj < 2; ++jj) {
+                const uint32_t at = lds_chunk((jp + jj) * 16 + col, g);
+                const v4i a1 = *reinterpret_cast<const v4i*>(t + 0 * kPlane + at);
+                const v4i a0 = *reinterpret_cast<const v4i*>(t + 1 * kPlane + at);
+                hi[jj] = mfma8(a1, q1, zero);
+                mid[jj] = mfma8(a1, q0v, zero);
+                lo[jj] = mfma8(a0, q0v, zero);
+                mid[jj] = mfma8(a0, q1, mid[jj]);
             }
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int j = jp + jj;
+                    // |128 mid + lo| < 2^29 (exact in int32); hi * 2^14 is exact in fp32
+                    const int rest = mid[jj][r] * 128 + lo[jj][r];
+                    float v = fmaf(static_cast<float>(hi[jj][r]), 16384.0f, static_cast<float>(rest));
+                    if (decltype(TAIL)::value && kb * kBlock + j * 16 + 4 * g + r >= tokens) v = -INFINITY;
+                    s[j][r] = v;
+                }
+        }
     };
 
     const bool ragged = tokens != tp;
@@ -527,7 +567,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     v4i c0[4], c7[4], c14[4], c21[4];
 #pragma unroll
     for (int fb = 0; fb < 4; ++fb) c0[fb] = c7[fb] = c14[fb] = c21[fb] = v4i{0, 0, 0, 0};
-    uint64_t lsum = 0;
+    // sum_j E as the three digit sums, on the MFMA (A = all ones)
+    v4i l0 = {0, 0, 0, 0}, l7 = l0, l14 = l0;
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    // x = (u - max) log2(e) 2^(eq + ek) as fma(u, scale, -(max * scale))
+    const float neg_ms = -(m * row_scale);
     int ks = 0, vs = 1, fs = 2;
     if (nkb > 0) {
         issue_planes(kb0, slots, false);
@@ -552,21 +596,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
         if (have) {
             const int8_t* t = slots + vs * kSlot;
             v4i e0, e1, e2;
-            uint32_t lblock = 0;  // <= 16 * 2^21
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                int E[4];
+                uint32_t R[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    E[r] = numerator21((s[j][r] - m) * row_scale);
-                    lblock += static_cast<uint32_t>(E[r]);
-                }
-                e0[j] = (E[0] & 127) | ((E[1] & 127) << 8) | ((E[2] & 127) << 16) | ((E[3] & 127) << 24);
-                e1[j] = ((E[0] >> 7) & 127) | (((E[1] >> 7) & 127) << 8) | (((E[2] >> 7) & 127) << 16) |
-                        (((E[3] >> 7) & 127) << 24);
-                e2[j] = (E[0] >> 14) | ((E[1] >> 14) << 8) | ((E[2] >> 14) << 16) | ((E[3] >> 14) << 24);
+                for (int r = 0; r < 4; ++r) R[r] = numerator21_bits(fmaf(s[j][r], row_scale, neg_ms));
+                int w0, w1, w2;
+                digits21(R, w0, w1, w2);
+                e0[j] = w0;
+                e1[j] = w1;
+                e2[j] = w2;
             }
-            lsum += lblock;
+            l0 = mfma8(ones, e0, l0);
+            l7 = mfma8(ones, e1, l7);
+            l14 = mfma8(ones, e2, l14);
 #pragma unroll
             for (int fb = 0; fb < 4; ++fb) {
                 const uint32_t at = lds_chunk(fb * 16 + col, g);
@@ -585,10 +628,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
     }
     __syncthreads();  // every wave is done with the ring before the sums reuse it
 
-    // Half 1 hands its integer sums to half 0 (exact adds): [group][lane][66].
+    // Half 1 hands its integer sums to half 0 (exact adds): [group][lane][67].
     int* red = reinterpret_cast<int*>(lds);
     if (half == 1) {
-        int* mine = red + (group * 64 + lane) * 66;
+        int* mine = red + (group * 64 + lane) * 67;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
@@ -598,13 +641,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
                 mine[fb * 16 + 8 + r] = c14[fb][r];
                 mine[fb * 16 + 12 + r] = c21[fb][r];
             }
-        mine[64] = static_cast<int>(static_cast<uint32_t>(lsum));
-        mine[65] = static_cast<int>(static_cast<uint32_t>(lsum >> 32));
+        mine[64] = l0[0];
+        mine[65] = l7[0];
+        mine[66] = l14[0];
     }
     __syncthreads();
     if (half == 1) return;
     {
-        const int* other = red + (group * 64 + lane) * 66;
+        const int* other = red + (group * 64 + lane) * 67;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
@@ -614,12 +658,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_exact_kernel(
                 c14[fb][r] += other[fb * 16 + 8 + r];
                 c21[fb][r] += other[fb * 16 + 12 + r];
             }
-        lsum += static_cast<uint64_t>(static_cast<uint32_t>(other[64])) |
-                (static_cast<uint64_t>(static_cast<uint32_t>(other[65])) << 32);
+        l0[0] += other[64];
+        l7[0] += other[65];
+        l14[0] += other[66];
     }
-    double l = static_cast<double>(lsum);
-    l = l + __shfl_xor(l, 16, kWave);
-    l = l + __shfl_xor(l, 32, kWave);
+    // digit sums < 2^31 each (< 2^17 keys x 127); the total is exact in double
+    const double l = static_cast<double>(l14[0]) * 16384.0 + (static_cast<double>(l7[0]) * 128.0 + static_cast<double>(l0[0]));
     const float lf = static_cast<float>(l);
     const uint32_t q = q0 + col;
     if (q < tokens) {

@@ -472,22 +472,25 @@ void block_fixed15(const float* x, size_t n, size_t stride, int32_t* X, int* exp
     *exponent = e - 14;
 }
 
-// 2^x scaled to 21 bits: E = min(rint(2^n p(x - n) * 2^21), 2^21 - 1) with
-// n = rint(max(x, -100)), p the degree-6 Taylor polynomial of 2^f
-// (coefficients ln2^k / k!) evaluated by Horner with fused multiply-adds.
+// 2^x scaled to 21 bits: E = rint(min(2^n P(x - n), 2^21 - 1)) with
+// n = rint(max(x, -100)) and P = 2^21 p, p the degree-6 Taylor polynomial of
+// 2^f (coefficients ln2^k / k!, each times 2^21, an exact scaling) evaluated
+// by Horner with fused multiply-adds. (Equal to min(rint(2^(n+21) p),
+// 2^21 - 1): rint is monotone and 2^21 - 1 is an integer.)
 float numerator21(float x) {
+    constexpr float k21 = 2097152.0f;
     const float xc = std::fmax(x, -100.0f);
     const float n = std::nearbyint(xc);
     const float f = xc - n;
-    float p = 1.54035304e-4f;
-    p = std::fmaf(p, f, 1.33335581e-3f);
-    p = std::fmaf(p, f, 9.61812911e-3f);
-    p = std::fmaf(p, f, 5.55041087e-2f);
-    p = std::fmaf(p, f, 2.40226507e-1f);
-    p = std::fmaf(p, f, 6.93147181e-1f);
-    p = std::fmaf(p, f, 1.0f);
-    const float v = std::ldexp(p, static_cast<int>(n) + 21);
-    return std::min(std::nearbyint(v), 2097151.0f);
+    float p = 1.54035304e-4f * k21;
+    p = std::fmaf(p, f, 1.33335581e-3f * k21);
+    p = std::fmaf(p, f, 9.61812911e-3f * k21);
+    p = std::fmaf(p, f, 5.55041087e-2f * k21);
+    p = std::fmaf(p, f, 2.40226507e-1f * k21);
+    p = std::fmaf(p, f, 6.93147181e-1f * k21);
+    p = std::fmaf(p, f, k21);
+    const float v = std::fmin(std::ldexp(p, static_cast<int>(n)), 2097151.0f);
+    return std::nearbyint(v);
 }
 
 // Integer-exact attention (the int8-mode kernel): q*0.125 in 15-bit block
@@ -496,7 +499,7 @@ float numerator21(float x) {
 // d0 in [0, 127]).
 //   H_ij = sum_f d1(Q_if) d1(K_jf),  R_ij = Q_i . K_j - 2^14 H_ij  (exact)
 //   u_ij = fmaf(fp32(H), 2^14, fp32(R))      (score = u_ij * 2^(eq_i + ek))
-//   x_ij = (u_ij - max_j u_ij) * ldexp(log2(e), eq_i + ek)
+//   c_i = ldexp(log2(e), eq_i + ek),  x_ij = fmaf(u_ij, c_i, -(max_j u_ij * c_i))
 //   E_ij = numerator21(x_ij)
 //   o_if = ldexp(fp32(sum_j E_ij V_jf) / fp32(sum_j E_ij), ev_f)
 // Every sum is an exact integer, so no result depends on summation order.
@@ -555,9 +558,10 @@ void attention_exact(const float* qkv, uint32_t tokens, uint32_t heads, float* o
                 maximum = std::max(maximum, u[j]);
             }
             const float row_scale = std::ldexp(1.44269504f, qe[i] + ke);
+            const float neg_ms = -(maximum * row_scale);
             double L = 0.0;
             for (size_t j = 0; j < T; ++j) {
-                E[j] = numerator21((u[j] - maximum) * row_scale);
+                E[j] = numerator21(std::fmaf(u[j], row_scale, neg_ms));
                 L += E[j];
             }
             // E < 2^21, |V| < 2^14, T < 2^17: sums stay below 2^52 (exact)
