@@ -380,22 +380,24 @@ DAV2_DEV v4i mfma8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16
 
 // E = rint(min(pow2(x) * 2^21, 2^21 - 1)) for x <= 0 (or -inf: 0), returned
 // as the bits of E + 2^23, i.e. 0x4B000000 + E. pow2(x) = 2^n p(x - n),
-// n = rint(x), p the degree-6 Taylor polynomial of 2^f (coefficients
-// ln2^k / k!, here times 2^21, which scales every Horner step exactly);
-// x below -100 gives E = 0. Adding 2^23 rounds ties to even.
+// n = rint(max(x, -100)), p the degree-5 minimax polynomial of 2^f on
+// [-1/2, 1/2] (relative error 7.5e-8 before rounding), its coefficients times
+// 2^21, which scales every Horner step exactly. Adding 2^23 rounds ties to
+// even. The clamp to -100 matters only for x = -inf (masked keys, CLAMP):
+// every finite x below -100 gives E = 0 with or without it.
+template <bool CLAMP>
 DAV2_DEV uint32_t numerator21_bits(float x) {
     constexpr float k21 = 2097152.0f;
-    const float xc = fmaxf(x, -100.0f);
+    const float xc = CLAMP ? fmaxf(x, -100.0f) : x;
     const float n = __builtin_rintf(xc);
     const float f = xc - n;
-    float p = 1.54035304e-4f * k21;
-    p = fmaf(p, f, 1.33335581e-3f * k21);
-    p = fmaf(p, f, 9.61812911e-3f * k21);
-    p = fmaf(p, f, 5.55041087e-2f * k21);
-    p = fmaf(p, f, 2.40226507e-1f * k21);
-    p = fmaf(p, f, 6.93147181e-1f * k21);
-    p = fmaf(p, f, k21);
-    const float v = fminf(ldexpf(p, static_cast<int>(n)), static_cast<float>(kEMax));  // normal
+    float p = 1.327647245e-3f * k21;
+    p = fmaf(p, f, 9.675540961e-3f * k21);
+    p = fmaf(p, f, 5.550713092e-2f * k21);
+    p = fmaf(p, f, 2.402212024e-1f * k21);
+    p = fmaf(p, f, 6.931469440e-1f * k21);
+    p = fmaf(p, f, 1.000000119e+0f * k21);
+    const float v = fminf(ldexpf(p, static_cast<int>(n)), static_cast<float>(kEMax));
     return __float_as_uint(v + 8388608.0f);
 }
 
@@ -596,17 +598,24 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)
         if (have) {
             const int8_t* t = slots + vs * kSlot;
             v4i e0, e1, e2;
+            auto numerators = [&](auto CLAMP) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t R[4];
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t R[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) R[r] = numerator21_bits(fmaf(s[j][r], row_scale, neg_ms));
-                int w0, w1, w2;
-                digits21(R, w0, w1, w2);
-                e0[j] = w0;
-                e1[j] = w1;
-                e2[j] = w2;
-            }
+                    for (int r = 0; r < 4; ++r)
+                        R[r] = numerator21_bits<decltype(CLAMP)::value>(fmaf(s[j][r], row_scale, neg_ms));
+                    int w0, w1, w2;
+                    digits21(R, w0, w1, w2);
+                    e0[j] = w0;
+                    e1[j] = w1;
+                    e2[j] = w2;
+                }
+            };
+            if (ragged && kb + 1 == blocks)  // masked keys carry u = -inf
+                numerators(std::true_type{});
+            else
+                numerators(std::false_type{});
             l0 = mfma8(ones, e0, l0);
             l7 = mfma8(ones, e1, l7);
             l14 = mfma8(ones, e2, l14);

@@ -473,22 +473,22 @@ void block_fixed15(const float* x, size_t n, size_t stride, int32_t* X, int* exp
 }
 
 // 2^x scaled to 21 bits: E = rint(min(2^n P(x - n), 2^21 - 1)) with
-// n = rint(max(x, -100)) and P = 2^21 p, p the degree-6 Taylor polynomial of
-// 2^f (coefficients ln2^k / k!, each times 2^21, an exact scaling) evaluated
-// by Horner with fused multiply-adds. (Equal to min(rint(2^(n+21) p),
-// 2^21 - 1): rint is monotone and 2^21 - 1 is an integer.)
+// n = rint(max(x, -100)) and P = 2^21 p, p the degree-5 minimax polynomial
+// of 2^f on [-1/2, 1/2] (relative error 7.5e-8; coefficients computed for
+// this build by the Remez exchange on the relative error, rounded to float,
+// each times 2^21, an exact scaling) evaluated by Horner with fused
+// multiply-adds.
 float numerator21(float x) {
     constexpr float k21 = 2097152.0f;
     const float xc = std::fmax(x, -100.0f);
     const float n = std::nearbyint(xc);
     const float f = xc - n;
-    float p = 1.54035304e-4f * k21;
-    p = std::fmaf(p, f, 1.33335581e-3f * k21);
-    p = std::fmaf(p, f, 9.61812911e-3f * k21);
-    p = std::fmaf(p, f, 5.55041087e-2f * k21);
-    p = std::fmaf(p, f, 2.40226507e-1f * k21);
-    p = std::fmaf(p, f, 6.93147181e-1f * k21);
-    p = std::fmaf(p, f, k21);
+    float p = 1.327647245e-3f * k21;
+    p = std::fmaf(p, f, 9.675540961e-3f * k21);
+    p = std::fmaf(p, f, 5.550713092e-2f * k21);
+    p = std::fmaf(p, f, 2.402212024e-1f * k21);
+    p = std::fmaf(p, f, 6.931469440e-1f * k21);
+    p = std::fmaf(p, f, 1.000000119e+0f * k21);
     const float v = std::fmin(std::ldexp(p, static_cast<int>(n)), 2097151.0f);
     return std::nearbyint(v);
 }
@@ -585,6 +585,10 @@ void attention_exact(const float* qkv, uint32_t tokens, uint32_t heads, float* o
 }
 
 }  // namespace
+
+void orc_numerator21(const float* x, uint64_t count, float* out) {
+    for (uint64_t i = 0; i < count; ++i) out[i] = numerator21(x[i]);
+}
 
 void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int mode,
                           float* out, float* probabilities) {

@@ -84,6 +84,8 @@ void orc_softmax_rows(const float* input, uint64_t rows, uint32_t columns,
  * probabilities (optional) receives [H][T][T]. */
 void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads,
                           int mode, float* out, float* probabilities);
+/* The 21-bit softmax numerator of mode 2 for each x (as a float integer). */
+void orc_numerator21(const float* x, uint64_t count, float* out);
 void orc_bilinear_align_true(const float* input, uint32_t input_width,
                              uint32_t input_height, uint32_t output_width,
                              uint32_t output_height, uint32_t channels,

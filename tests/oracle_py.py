@@ -23,6 +23,7 @@ _PROTO = {
     "orc_linear_epilogue": (None, [vp, vp, vp, vp, u32, u32, u32, u32, C.c_int, vp]),
     "orc_linear_int8": (None, [vp, vp, vp, vp, u32, u32, u32, C.c_int, vp]),
     "orc_gelu": (None, [vp, u64, vp]),
+    "orc_numerator21": (None, [vp, u64, vp]),
     "orc_exp": (None, [vp, u64, vp]),
     "orc_layer_norm": (None, [vp, vp, vp, u32, u32, f32, vp]),
     "orc_add_scaled": (None, [vp, vp, vp, u64, u32, vp]),
@@ -140,6 +141,12 @@ class Oracle:
         x = _f32(x)
         out = np.empty_like(x)
         self.lib.orc_gelu(x.ctypes.data, x.size, out.ctypes.data)
+        return out
+
+    def numerator21(self, x):
+        x = _f32(x)
+        out = np.empty_like(x)
+        self.lib.orc_numerator21(x.ctypes.data, x.size, out.ctypes.data)
         return out
 
     def exp(self, x):

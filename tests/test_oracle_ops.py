@@ -148,6 +148,22 @@ def test_attention_exact_mode_is_order_free(oracle):
                           base.view(np.uint32))
 
 
+def test_numerator21_vs_float64(oracle):
+    # E(x) = rint(min(2^x 2^21, 2^21 - 1)) up to the polynomial's rounding:
+    # within 0.5 + 2.5e-7 * 2^(x+21) of the float64 value, exact integers,
+    # 0 below -100 and for -inf, 2^21 - 1 at the top
+    x = np.concatenate([np.linspace(-40.0, 0.0, 400001), -np.logspace(-9, 0, 2001),
+                        np.linspace(-0.5, 0.5, 1001)]).astype(np.float32)
+    e = oracle.numerator21(x)
+    want = np.minimum(np.exp2(x.astype(np.float64) + 21.0), 2097151.0)
+    assert np.all(e == np.rint(e))
+    assert np.all(np.abs(e - want) <= 0.5 + 2.5e-7 * want)
+    assert np.abs(e - want).max() >= 0.4  # the test sees real roundings
+    far = np.array([-100.5, -1e4, -3e38, -np.inf], np.float32)
+    assert np.all(oracle.numerator21(far) == 0.0)
+    assert np.all(oracle.numerator21(np.array([0.0, 1e-6, 0.03], np.float32)) == 2097151.0)
+
+
 def test_attention_exact_mode_uniform_keys(oracle):
     # identical keys: every probability is 1/T, the output is the mean of the
     # (15-bit block floating point) values
