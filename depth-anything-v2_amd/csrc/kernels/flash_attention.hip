@@ -541,13 +541,17 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)
         if (it + 2 < nkb) issue_planes(kb + 2, slots + ((it + 2) % kSlots) * kSlot, false);
         if (have) {
             const int8_t* t = slots + (it % kSlots) * kSlot;
-            float s[4][4];
-            if (ragged && kb + 1 == blocks)
-                block_scores(t, kb, std::true_type{}, s);
-            else
-                block_scores(t, kb, std::false_type{}, s);
+            // block maximum inside each variant: the scores are then fma
+            // results, which max needs no canonicalization for
+            auto block_max = [&](auto TAIL) {
+                float s[4][4];
+                block_scores(t, kb, TAIL, s);
+                float bm = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) m = fmaxf(fmaxf(m, fmaxf(s[j][0], s[j][1])), fmaxf(s[j][2], s[j][3]));
+                for (int i = 3; i < 15; i += 2) bm = fmaxf(fmaxf(bm, s[i >> 2][i & 3]), s[(i + 1) >> 2][(i + 1) & 3]);
+                return fmaxf(bm, s[3][3]);
+            };
+            m = fmaxf(m, ragged && kb + 1 == blocks ? block_max(std::true_type{}) : block_max(std::false_type{}));
         }
     }
     __syncthreads();  // every wave is done with the pass-1 ring before it is reused
