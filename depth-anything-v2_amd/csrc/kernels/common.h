@@ -65,6 +65,12 @@ DAV2_DEV void copy16_to_lds(const void* src, void* lds_base) {
     __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)lds_base, 16, 0, 0);
 }
 
+// 4 bytes per lane (global_load_lds_dword): lane l's bytes land at
+// lds_base + 4*l.
+DAV2_DEV void copy4_to_lds(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)lds_base, 4, 0, 0);
+}
+
 // s_waitcnt with vmcnt = n (expcnt, lgkmcnt not waited on), n < 64.
 #define DAV2_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 

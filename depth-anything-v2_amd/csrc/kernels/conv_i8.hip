@@ -25,10 +25,14 @@
 // (XOR-swizzled rows, conflict-free for the MFMA operand reads), and the
 // waves multiply it against weight fragments read straight from global
 // memory (v_mfma_i32_16x16x64_i8, weights as the row operand so each lane's
-// accumulators run along pixels and the CHW stores coalesce). The next
-// channel block's window is loaded into registers while the nine taps of the
-// current one run, and weight fragments three steps ahead, so global latency
-// hides behind the quantize and MFMA work. One LDS-only barrier per tap.
+// accumulators run along pixels and the CHW stores coalesce). Each wave
+// stages the window of the 16 channels it quantizes itself. For 3x3 the next
+// channel block's window rows are copied global->LDS without registers
+// (global_load_lds_dword) as soon as the current block's taps are done with
+// each row (row 0 after tap 2, row 1 after tap 5, row 2 after tap 8), seven
+// steps before they are read; 1x1 loads the next block into registers.
+// Weight fragments come three steps ahead, so global latency hides behind
+// the quantize and MFMA work. One LDS-only barrier per tap.
 
 #include <algorithm>
 #include <type_traits>
@@ -57,6 +61,10 @@ struct ConvParams {
     const float* residual; // nullable, CHW [N][plane]
     uint32_t flags;        // DAV2_CONV_*
 };
+
+// Source of the 3x3 window positions outside the image (zero padding): the
+// copies of those positions read it instead of the input.
+__device__ float g_conv_zero_row[64];
 
 // Workgroup barrier that orders LDS only: waits for this wave's LDS
 // operations (lgkmcnt) but leaves global loads in flight.
@@ -176,7 +184,7 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
     const uint32_t col4 = min(x0 + lane, rowlen - 1u) * 4u;
     const uint32_t plane32 = static_cast<uint32_t>(g.plane);
     const char* xbase = reinterpret_cast<const char*>(g.x);
-    float xs[kLoads];
+    float xs[KS == 3 ? 1 : kLoads];  // 3x3 windows bypass registers
     float xh[2] = {0.0f, 0.0f};
     constexpr bool relu_in = RELU_IN;
     // Byte offsets of the window rows within a channel plane (clamped).
@@ -190,6 +198,7 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
     // j % kRowsT. The channel offset advances through an opaque register so
     // the compiler does not precompute (and keep live) all kLoads offsets.
     auto issue_rows = [&](uint32_t cb, int j0, int j1) {
+        if constexpr (KS == 3) return;
         uint32_t chan = ((cb * kCB + wave * (kCB / 4) + j0 / kRowsT) * plane32) * 4u;
         asm volatile("" : "+s"(chan));
 #pragma unroll
@@ -202,22 +211,60 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
             xs[j] = *reinterpret_cast<const float*>(xbase + (chan + row4[j % kRowsT] + col4));
         }
     };
+    // 3x3 halo columns x0 - 1 and x0 + 64 of the wave's 16 channels: value
+    // h = 6 c + 2 r + side (96 per wave) is lane h % 64's register h / 64.
     auto issue_halo = [&](uint32_t cb) {
         if constexpr (KS == 3) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t idx = min(tid + 256u * h, 2u * kCB * 3u - 1u);  // 2 * 192 halo values
-                const uint32_t R = idx >> 1, c = R / 3u, r = R - 3u * c;
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t h = min(lane + 64u * i, 95u);
+                const uint32_t c = wave * 16u + h / 6u, r = (h >> 1) % 3u;
                 const int gy = static_cast<int>(y) + static_cast<int>(r) - 1;
-                const int gx = (idx & 1u) ? static_cast<int>(x0) + kPix : static_cast<int>(x0) - 1;
+                const int gx = (h & 1u) ? static_cast<int>(x0) + kPix : static_cast<int>(x0) - 1;
                 const uint32_t gyc = static_cast<uint32_t>(min(max(gy, 0), static_cast<int>(g.height) - 1));
                 const uint32_t gxc = static_cast<uint32_t>(min(max(gx, 0), static_cast<int>(g.width) - 1));
                 const uint32_t off = ((cb * kCB + c) * plane32 + gyc * g.width + gxc) * 4u;
-                xh[h] = *reinterpret_cast<const float*>(xbase + off);
+                xh[i] = *reinterpret_cast<const float*>(xbase + off);
             }
         }
     };
+    auto write_halo = [&]() {
+        if constexpr (KS == 3) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t h = lane + 64u * i;
+                if (h < 96u) {
+                    const uint32_t c = wave * 16u + h / 6u, r = (h >> 1) % 3u;
+                    const int gy = static_cast<int>(y) + static_cast<int>(r) - 1;
+                    const int gx = (h & 1u) ? static_cast<int>(x0) + kPix : static_cast<int>(x0) - 1;
+                    const bool ok =
+                        gy >= 0 && gy < static_cast<int>(g.height) && gx >= 0 && gx < static_cast<int>(g.width);
+                    xt[c * kPlaneT + r * kColsT + ((h & 1u) ? kColsT - 1u : 0u)] = ok ? xh[i] : 0.0f;
+                }
+            }
+        }
+    };
+    // 3x3: window row r (image row y + r - 1) of the wave's 16 channels of
+    // block cb, columns x0 .. x0 + 63, straight into LDS: one copy per
+    // channel, lane = column; positions outside the image read zeros.
+    const char* zero_lane = reinterpret_cast<const char*>(g_conv_zero_row + lane);
+    auto copy_rows = [&](uint32_t cb, int r) {
+        if constexpr (KS == 3) {
+            const int gy = static_cast<int>(y) + r - 1;
+            const bool ok = col_ok && gy >= 0 && gy < static_cast<int>(nrows);
+            uint32_t chan = ((cb * kCB + wave * 16u) * plane32) * 4u + row4[r] + col4;
+            asm volatile("" : "+v"(chan));
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const char* src = ok ? xbase + (chan + static_cast<uint32_t>(e) * plane32 * 4u) : zero_lane;
+                copy4_to_lds(src, xt + (wave * 16u + e) * kPlaneT + r * kColsT + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     auto write_window = [&]() {
+        if constexpr (KS == 3) return;
 #pragma unroll
         for (int j = 0; j < kLoads; ++j) {
             const uint32_t R = wave * kLoads + j;
@@ -271,10 +318,13 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
     const uint32_t nblocks = g.channels / kCB, nsteps = nblocks * kTaps;
     v4i ring[kRing][NB];
     issue_rows(0, 0, kLoads);
+#pragma unroll
+    for (int r = 0; r < kRowsT; ++r) copy_rows(0, r);
     issue_halo(0);
 #pragma unroll
     for (int d = 0; d < kRing; ++d) load_w(ring[d], min(static_cast<uint32_t>(d), nsteps - 1));
     write_window();
+    write_halo();  // its loads follow the row copies, so those have landed too
     lds_barrier();
 
     // Operand reads of this wave's pixel blocks: lane l reads pixel
@@ -307,13 +357,25 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
             {
                 uint32_t w4[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    w4[q] = quant4(f[4 * q + 0], f[4 * q + 1], f[4 * q + 2], f[4 * q + 3], inv);
+                for (int q = 0; q < 4; ++q) {
+                    // 3x3 windows arrive unmodified: the input ReLU is taken here
+                    const bool r = KS == 3 && relu_in;
+                    w4[q] = quant4(r ? fmaxf(f[4 * q + 0], 0.0f) : f[4 * q + 0], r ? fmaxf(f[4 * q + 1], 0.0f) : f[4 * q + 1],
+                                   r ? fmaxf(f[4 * q + 2], 0.0f) : f[4 * q + 2], r ? fmaxf(f[4 * q + 3], 0.0f) : f[4 * q + 3],
+                                   inv);
+                }
                 *reinterpret_cast<v4i*>(abuf + qdst) =
                     v4i{static_cast<int>(w4[0]), static_cast<int>(w4[1]), static_cast<int>(w4[2]),
                         static_cast<int>(w4[3])};
             }
-            if (tap + 1 < kTaps) read_tap(tap + 1);
+            if (tap + 1 < kTaps) {
+                // 3x3: window rows 1 and 2 of this block were copied during
+                // the previous one; 32 copies (the next two rows) follow
+                // each row's, so at most 32 outstanding operations mean it
+                // has landed (copies retire in issue order)
+                if (KS == 3 && (tap + 1 == 3 || tap + 1 == 6)) DAV2_WAIT_VMCNT(32);
+                read_tap(tap + 1);
+            }
             lds_barrier();
             v4i (&bw)[NB] = ring[tap % kRing];
 #pragma unroll
@@ -331,12 +393,25 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
                 issue_rows(next_cb, 0, kLoads);
                 issue_halo(next_cb);
             }
+            // 3x3: a row of the window is free once every tap reading it has
+            // read (the read runs a step ahead, before the step's barrier);
+            // past the last block the copies repeat the current rows
+            if (tap == 1) copy_rows(next_cb, 0);
+            if (tap == 4) copy_rows(next_cb, 1);
+            if (tap == 7) copy_rows(next_cb, 2);
         }
         if (more) {
-            // Every wave is past the last tap's barrier, so no quantizer still
-            // reads the window: replace it with the next block's.
-            write_window();
-            lds_barrier();
+            if constexpr (KS == 3) {
+                // the window is wave-local: halo values, then row 0 of the
+                // next block (rows 1 and 2, 32 copies, were issued after it)
+                write_halo();
+                DAV2_WAIT_VMCNT(32);
+            } else {
+                // Every wave is past the last tap's barrier, so no quantizer
+                // still reads the window: replace it with the next block's.
+                write_window();
+                lds_barrier();
+            }
             read_tap(0);
         }
     }
