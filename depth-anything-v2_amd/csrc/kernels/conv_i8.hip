@@ -334,9 +334,11 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
     const float* qsrc = xt + (wave * 16u) * kPlaneT + lane;
     const uint32_t qdst = a_offset(lane, wave);
 
-    // The 16 window values a thread quantizes for a tap are read one step
-    // ahead, before the barrier, so their LDS latency overlaps the barrier
-    // wait instead of following it.
+    // Pipeline per step (tap t): barrier; the step's operand reads are issued;
+    // the next tap is quantized into the other operand buffer and the window
+    // values of the tap after that are read (both overlap the operand read
+    // latency); then the MFMAs. Tap 0 of a block is quantized before the
+    // block's first barrier.
     float f[16];
     auto read_tap = [&](int tap) {
         uint32_t qoff = (tap / KS) * kColsT + (tap % KS);
@@ -345,7 +347,27 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) f[e] = src[e * kPlaneT];
     };
-    read_tap(0);
+    auto quantize_into = [&](int8_t* abuf) {
+        uint32_t w4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            // 3x3 windows arrive unmodified: the input ReLU is taken here
+            const bool r = KS == 3 && relu_in;
+            w4[q] = quant4(r ? fmaxf(f[4 * q + 0], 0.0f) : f[4 * q + 0], r ? fmaxf(f[4 * q + 1], 0.0f) : f[4 * q + 1],
+                           r ? fmaxf(f[4 * q + 2], 0.0f) : f[4 * q + 2], r ? fmaxf(f[4 * q + 3], 0.0f) : f[4 * q + 3],
+                           inv);
+        }
+        *reinterpret_cast<v4i*>(abuf + qdst) =
+            v4i{static_cast<int>(w4[0]), static_cast<int>(w4[1]), static_cast<int>(w4[2]), static_cast<int>(w4[3])};
+    };
+    // Tap 0 of the block starting at step s0 into its operand buffer, and
+    // the window values of tap 1.
+    auto block_start = [&](uint32_t s0) {
+        read_tap(0);
+        quantize_into(at[s0 & 1u]);
+        if (kTaps > 1) read_tap(1);
+    };
+    block_start(0);
 
     for (uint32_t cb = 0; cb < nblocks; ++cb) {
         const bool more = cb + 1 < nblocks;
@@ -353,38 +375,30 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
 #pragma unroll
         for (int tap = 0; tap < kTaps; ++tap) {
             const uint32_t step = cb * kTaps + tap;
-            int8_t* abuf = at[step & 1u];
-            {
-                uint32_t w4[4];
+            lds_barrier();  // operand tile `step` is complete
+            const int8_t* abuf = at[step & 1u];
+            v4i bp[PB];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    // 3x3 windows arrive unmodified: the input ReLU is taken here
-                    const bool r = KS == 3 && relu_in;
-                    w4[q] = quant4(r ? fmaxf(f[4 * q + 0], 0.0f) : f[4 * q + 0], r ? fmaxf(f[4 * q + 1], 0.0f) : f[4 * q + 1],
-                                   r ? fmaxf(f[4 * q + 2], 0.0f) : f[4 * q + 2], r ? fmaxf(f[4 * q + 3], 0.0f) : f[4 * q + 3],
-                                   inv);
-                }
-                *reinterpret_cast<v4i*>(abuf + qdst) =
-                    v4i{static_cast<int>(w4[0]), static_cast<int>(w4[1]), static_cast<int>(w4[2]),
-                        static_cast<int>(w4[3])};
-            }
+            for (int j = 0; j < PB; ++j) bp[j] = *reinterpret_cast<const v4i*>(abuf + a_offset(prow + 16u * j, pchunk));
             if (tap + 1 < kTaps) {
-                // 3x3: window rows 1 and 2 of this block were copied during
-                // the previous one; 32 copies (the next two rows) follow
-                // each row's, so at most 32 outstanding operations mean it
-                // has landed (copies retire in issue order)
-                if (KS == 3 && (tap + 1 == 3 || tap + 1 == 6)) DAV2_WAIT_VMCNT(32);
-                read_tap(tap + 1);
+                // the other buffer was last read by step - 1, which every
+                // wave finished before this step's barrier
+                quantize_into(at[(step + 1u) & 1u]);
+                if (tap + 2 < kTaps) {
+                    // 3x3: rows 1 and 2 of this block were copied during the
+                    // previous one and 16 copies (the next row's) follow
+                    // each, so at most 16 outstanding operations mean the
+                    // row has landed (copies retire in issue order)
+                    if (KS == 3 && (tap + 2 == 3 || tap + 2 == 6)) DAV2_WAIT_VMCNT(16);
+                    read_tap(tap + 2);
+                }
             }
-            lds_barrier();
             v4i (&bw)[NB] = ring[tap % kRing];
 #pragma unroll
-            for (int j = 0; j < PB; ++j) {
-                const v4i bp = *reinterpret_cast<const v4i*>(abuf + a_offset(prow + 16u * j, pchunk));
+            for (int j = 0; j < PB; ++j)
 #pragma unroll
                 for (int i = 0; i < NB; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[i], bp, acc[i][j], 0, 0, 0);
-            }
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[i], bp[j], acc[i][j], 0, 0, 0);
             // Prefetches are unconditional (a branch around a load makes the
             // compiler wait for it at the merge); past the end they re-read
             // the last step / block, which is harmless.
@@ -394,8 +408,8 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
                 issue_halo(next_cb);
             }
             // 3x3: a row of the window is free once every tap reading it has
-            // read (the read runs a step ahead, before the step's barrier);
-            // past the last block the copies repeat the current rows
+            // read (reads run two taps ahead, before the next barrier); past
+            // the last block the copies repeat the current rows
             if (tap == 1) copy_rows(next_cb, 0);
             if (tap == 4) copy_rows(next_cb, 1);
             if (tap == 7) copy_rows(next_cb, 2);
@@ -412,7 +426,8 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
                 write_window();
                 lds_barrier();
             }
-            read_tap(0);
+            // the buffer of step (cb + 1) * kTaps was last read two steps ago
+            block_start((cb + 1) * kTaps);
         }
     }
 
