@@ -89,7 +89,8 @@ class GemmArgs(C.Structure):
                 ("out_i32", C.c_void_p), ("out", C.c_void_p), ("out_row_offset", C.c_uint64),
                 ("out_row_stride", C.c_uint64), ("residual", C.c_void_p), ("gamma", C.c_void_p),
                 ("convt_kernel", C.c_uint32), ("convt_width", C.c_uint32), ("convt_height", C.c_uint32),
-                ("convt_channels", C.c_uint32), ("col_absmax", C.c_void_p), ("col_absmax_begin", C.c_uint32)]
+                ("convt_channels", C.c_uint32), ("col_absmax", C.c_void_p), ("col_absmax_begin", C.c_uint32),
+                ("relu_output", C.c_uint32)]
 
 
 class ConvArgs(C.Structure):
@@ -142,6 +143,7 @@ PROTOTYPES = {
     "dav2_hip_quantize_rows_i8": (C.c_int, [vp, u64, u32, u32, vp, u32, vp, vp]),
     "dav2_hip_im2col_scratch_floats": (u64, [u32, u32, u32]),
     "dav2_hip_im2col_quantize_i8": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, vp, u32, vp, vp, u64, vp]),
+    "dav2_hip_im2col_quantize_relu_i8": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, vp, u32, vp, vp, u64, vp]),
     "dav2_hip_conv2d_i8_supported": (C.c_int, [u32, u32, u32, u32, u32, u32, u32]),
     "dav2_hip_conv_weights_tapmajor": (C.c_int, [vp, vp, u32, u32, u32, u64, vp]),
     "dav2_hip_conv2d_i8": (C.c_int, [C.POINTER(ConvArgs), vp]),

@@ -18,6 +18,8 @@
 // workgroup barrier per stage. Workgroups are remapped so that each XCD
 // works on one contiguous band of tiles.
 
+#include <type_traits>
+
 #include "common.h"
 #include "dav2_hip.h"
 
@@ -44,6 +46,7 @@ struct GemmParams {
     uint32_t coalesced_out;  // row-major output rows 16-byte aligned (n % 4 == 0, out aligned)
     float* col_absmax;       // ROW_COLMAX partial maxima [row tile][n - col_absmax_begin]
     uint32_t col_absmax_begin;
+    uint32_t relu_output;    // TRANSPOSED: max(out, 0) after the residual
 };
 
 template <int EPI>
@@ -134,8 +137,10 @@ DAV2_DEV float row_value(const EpilogueOperands<EPI, TM, TN>& e, int i, int j, i
 }
 
 // One output element (row prow of P, column qcol of Q) of block (i, j),
-// accumulator r: dequant ((acc * s_in) * s_w) + bias, then the epilogue.
-template <int EPI, int TM, int TN>
+// accumulator r: dequant ((acc * s_in) * s_w) + bias, then the epilogue;
+// TRANSPOSED adds the residual at the same index (RES, add.glsl) and then
+// takes max(., 0) (RELU, relu.glsl).
+template <int EPI, int TM, int TN, bool RES = false, bool RELU = false>
 DAV2_DEV void store_one(const GemmParams& g, const EpilogueOperands<EPI, TM, TN>& e, int i, int j, int r,
                         uint32_t prow, uint32_t qcol, int32_t acc) {
     constexpr bool sw = Orientation<EPI>::swapped;
@@ -160,7 +165,11 @@ DAV2_DEV void store_one(const GemmParams& g, const EpilogueOperands<EPI, TM, TN>
         return;
     }
     if (EPI == DAV2_GEMM_EPI_TRANSPOSED) {
-        g.out[static_cast<uint64_t>(n) * g.out_row_stride + m + g.out_row_offset] = v;
+        const uint64_t idx = static_cast<uint64_t>(n) * g.out_row_stride + m + g.out_row_offset;
+        float o = v;
+        if (RES) o = o + g.residual[idx];
+        if (RELU) o = fmaxf(o, 0.0f);
+        g.out[idx] = o;
         return;
     }
     const uint64_t idx = (static_cast<uint64_t>(m) + g.out_row_offset) * g.n + n;
@@ -386,19 +395,35 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
         return;
     }
     // 16x16 MFMA result layout: lane l holds rows 4*(l/16)+r (r = 0..3) of
-    // column l%16.
+    // column l%16. The TRANSPOSED residual / ReLU choice is made once, outside
+    // the unrolled stores.
+    auto store_all = [&](auto res_tag, auto relu_tag) {
+        constexpr bool kRes = decltype(res_tag)::value, kRelu = decltype(relu_tag)::value;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+        for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const uint32_t qcol = col0 + wn * WN + j * 16 + (lane & 15);
-            if (qcol >= g.rows_q) continue;
+            for (int j = 0; j < TN; ++j) {
+                const uint32_t qcol = col0 + wn * WN + j * 16 + (lane & 15);
+                if (qcol >= g.rows_q) continue;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t prow = row0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
-                if (prow < g.rows_p) store_one<EPI, TM, TN>(g, epi, i, j, r, prow, qcol, acc[i][j][r]);
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t prow = row0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
+                    if (prow < g.rows_p)
+                        store_one<EPI, TM, TN, kRes, kRelu>(g, epi, i, j, r, prow, qcol, acc[i][j][r]);
+                }
             }
         }
+    };
+    if constexpr (EPI == DAV2_GEMM_EPI_TRANSPOSED) {
+        if (g.residual) {
+            if (g.relu_output) store_all(std::true_type{}, std::true_type{});
+            else store_all(std::true_type{}, std::false_type{});
+        } else {
+            if (g.relu_output) store_all(std::false_type{}, std::true_type{});
+            else store_all(std::false_type{}, std::false_type{});
+        }
+    } else {
+        store_all(std::false_type{}, std::false_type{});
     }
 }
 
@@ -461,6 +486,7 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
          (reinterpret_cast<uintptr_t>(a->out) & 15)))
         return hipErrorInvalidValue;
     if (e > DAV2_GEMM_EPI_ROW_COLMAX) return hipErrorInvalidValue;
+    if (a->relu_output && e != DAV2_GEMM_EPI_TRANSPOSED) return hipErrorInvalidValue;
 
     GemmParams g{};
     const bool swapped = e == DAV2_GEMM_EPI_TRANSPOSED || e == DAV2_GEMM_EPI_CONVT;
@@ -488,6 +514,7 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     g.coalesced_out = !swapped && a->n % 4 == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0;
     g.col_absmax = a->col_absmax;
     g.col_absmax_begin = a->col_absmax_begin;
+    g.relu_output = a->relu_output;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (e) {
         case DAV2_GEMM_EPI_RAW_I32: launch_epi<DAV2_GEMM_EPI_RAW_I32>(g, s); break;

@@ -222,6 +222,8 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void window_scale_kernel(
     if (lane == 0) scales[r] = row_scale(m);
 }
 
+// RELU: the rows are those of max(x, 0) (a ReLU ahead of the convolution).
+template <bool RELU>
 __global__ __launch_bounds__(256) void im2col3x3_kernel(const float* __restrict__ x, const float* __restrict__ partial,
                                                         uint32_t groups, uint32_t C, uint32_t H, uint32_t W,
                                                         uint32_t chunks_per_block, int8_t* __restrict__ q,
@@ -272,7 +274,7 @@ __global__ __launch_bounds__(256) void im2col3x3_kernel(const float* __restrict_
             float v = 0.0f;
             if (gy >= 0 && gy < static_cast<int>(H) && gx >= 0 && gx < static_cast<int>(W))
                 v = x[(c0 + ch) * plane + static_cast<uint64_t>(gy) * W + gx];
-            tile[idx] = v;
+            tile[idx] = RELU ? fmaxf(v, 0.0f) : v;
         }
         __syncthreads();
         // 36 words (144 bytes) per pixel; word w of pixel p covers chunk
@@ -308,6 +310,7 @@ __global__ __launch_bounds__(256) void im2col3x3_kernel(const float* __restrict_
 // 64-byte segment per output row. Columns beyond C (the row padding) are zero.
 constexpr int kChunk1 = 64;
 
+template <bool RELU>
 __global__ __launch_bounds__(256) void im2col1x1_kernel(const float* __restrict__ x, const float* __restrict__ partial,
                                                         uint32_t groups, uint32_t C, uint64_t plane,
                                                         uint32_t chunks_per_block, int8_t* __restrict__ q,
@@ -334,7 +337,8 @@ __global__ __launch_bounds__(256) void im2col1x1_kernel(const float* __restrict_
         const uint32_t c0 = chunk * kChunk1;
         for (uint32_t idx = tid; idx < kChunk1 * kTile; idx += 256) {
             const uint32_t ch = idx / kTile, p = idx - ch * kTile;
-            tile[ch * (kTile + 1) + p] = (c0 + ch < C && p < valid) ? x[(c0 + ch) * plane + p0 + p] : 0.0f;
+            const float v = (c0 + ch < C && p < valid) ? x[(c0 + ch) * plane + p0 + p] : 0.0f;
+            tile[ch * (kTile + 1) + p] = RELU ? fmaxf(v, 0.0f) : v;
         }
         __syncthreads();
         for (uint32_t idx = tid; idx < valid * 16u; idx += 256) {
@@ -512,11 +516,14 @@ uint64_t dav2_hip_im2col_scratch_floats(uint32_t input_width, uint32_t input_hei
     return static_cast<uint64_t>(input_width) * input_height * ((input_channels + kGroupChannels - 1) / kGroupChannels);
 }
 
-int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32_t input_height,
-                                uint32_t input_channels, uint32_t output_width,
-                                uint32_t output_height, uint32_t kernel, uint32_t stride,
-                                int32_t padding, int8_t* q, uint32_t ldq, float* scales,
-                                float* scratch, uint64_t scratch_floats, void* stream) {
+namespace {
+
+// relu: quantize the rows of max(input, 0); only the tiled 3x3 / 1x1 paths
+// (with scratch) take it, other geometries return hipErrorInvalidValue.
+int im2col_quantize(const float* input, uint32_t input_width, uint32_t input_height, uint32_t input_channels,
+                    uint32_t output_width, uint32_t output_height, uint32_t kernel, uint32_t stride, int32_t padding,
+                    int8_t* q, uint32_t ldq, float* scales, float* scratch, uint64_t scratch_floats, bool relu,
+                    void* stream) {
     const uint64_t rows64 = static_cast<uint64_t>(output_width) * output_height;
     const uint64_t cols64 = static_cast<uint64_t>(input_channels) * kernel * kernel;
     if (rows64 == 0) return hipSuccess;
@@ -550,8 +557,8 @@ int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32
                        output_height == input_height;
     const bool have_partial = scratch && scratch_floats >= plane * groups;
     if ((fast3 || fast1) && have_partial && input_height <= 65535u) {
-        hipLaunchKernelGGL(channel_group_absmax_kernel<false>, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s,
-                           input, input_channels, plane, scratch);
+        const hipError_t e = launch_channel_group_absmax(input, input_channels, plane, scratch, relu, s);
+        if (e != hipSuccess) return e;
         // Enough workgroups to fill the chip: split the channel chunks of
         // small maps over blockIdx.z (each split recomputes the 64 scales).
         if (fast3) {
@@ -559,19 +566,29 @@ int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32
             const uint32_t chunks = input_channels / kChunk;
             const uint32_t splits = std::max(1u, std::min(chunks, static_cast<uint32_t>(2048u / tiles)));
             const uint32_t per = (chunks + splits - 1) / splits;
-            hipLaunchKernelGGL(im2col3x3_kernel, dim3(ceil_div(input_width, kTile), input_height, ceil_div(chunks, per)),
-                               dim3(256), 0, s, input, scratch, groups, input_channels, input_height, input_width, per,
-                               q, ldq, scales);
+            const dim3 grid(ceil_div(input_width, kTile), input_height, ceil_div(chunks, per));
+            if (relu)
+                hipLaunchKernelGGL(im2col3x3_kernel<true>, grid, dim3(256), 0, s, input, scratch, groups,
+                                   input_channels, input_height, input_width, per, q, ldq, scales);
+            else
+                hipLaunchKernelGGL(im2col3x3_kernel<false>, grid, dim3(256), 0, s, input, scratch, groups,
+                                   input_channels, input_height, input_width, per, q, ldq, scales);
         } else {
             const unsigned tiles = ceil_div(plane, kTile);
             const uint32_t chunks = ldq / kChunk1;
             const uint32_t splits = std::max(1u, std::min(chunks, static_cast<uint32_t>(2048u / tiles)));
             const uint32_t per = (chunks + splits - 1) / splits;
-            hipLaunchKernelGGL(im2col1x1_kernel, dim3(tiles, ceil_div(chunks, per)), dim3(256), 0, s, input, scratch,
-                               groups, input_channels, plane, per, q, ldq, scales);
+            const dim3 grid(tiles, ceil_div(chunks, per));
+            if (relu)
+                hipLaunchKernelGGL(im2col1x1_kernel<true>, grid, dim3(256), 0, s, input, scratch, groups,
+                                   input_channels, plane, per, q, ldq, scales);
+            else
+                hipLaunchKernelGGL(im2col1x1_kernel<false>, grid, dim3(256), 0, s, input, scratch, groups,
+                                   input_channels, plane, per, q, ldq, scales);
         }
         return hipGetLastError();
     }
+    if (relu) return hipErrorInvalidValue;
     if (have_partial) {
         // Scales from the channel-group maxima (same values, one thread per row).
         hipLaunchKernelGGL(channel_group_absmax_kernel<false>, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s,
@@ -588,6 +605,25 @@ int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32
     hipLaunchKernelGGL(im2col_quantize_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, g, rows,
                        ldq_words, scales, q);
     return hipGetLastError();
+}
+
+}  // namespace
+
+int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_width, uint32_t input_height,
+                                uint32_t input_channels, uint32_t output_width,
+                                uint32_t output_height, uint32_t kernel, uint32_t stride,
+                                int32_t padding, int8_t* q, uint32_t ldq, float* scales,
+                                float* scratch, uint64_t scratch_floats, void* stream) {
+    return im2col_quantize(input, input_width, input_height, input_channels, output_width, output_height, kernel,
+                           stride, padding, q, ldq, scales, scratch, scratch_floats, false, stream);
+}
+
+int dav2_hip_im2col_quantize_relu_i8(const float* input, uint32_t input_width, uint32_t input_height,
+                                     uint32_t input_channels, uint32_t output_width, uint32_t output_height,
+                                     uint32_t kernel, uint32_t stride, int32_t padding, int8_t* q, uint32_t ldq,
+                                     float* scales, float* scratch, uint64_t scratch_floats, void* stream) {
+    return im2col_quantize(input, input_width, input_height, input_channels, output_width, output_height, kernel,
+                           stride, padding, q, ldq, scales, scratch, scratch_floats, true, stream);
 }
 
 int dav2_hip_layer_norm(float* out, const float* input, const float* weight, const float* bias,

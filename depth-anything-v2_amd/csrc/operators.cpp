@@ -145,7 +145,8 @@ void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& 
                                       const DeviceBuffer& input_scales, const DeviceBuffer& weight_scales,
                                       const DeviceBuffer& bias, std::uint32_t rows, std::uint32_t input_columns,
                                       std::uint32_t output_columns, std::uint32_t output_row_offset,
-                                      std::uint32_t output_row_stride, bool output_transposed, bool has_bias) {
+                                      std::uint32_t output_row_stride, bool output_transposed, bool has_bias,
+                                      const DeviceBuffer* residual, bool relu_output) {
     dav2_gemm_i8_args a{};
     a.a = packed_input.as<int8_t>();
     a.lda = packed_ld;
@@ -161,6 +162,8 @@ void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& 
     a.out = output.as<float>();
     a.out_row_offset = output_row_offset;
     a.out_row_stride = output_row_stride;
+    a.residual = residual ? residual->as<float>() : nullptr;  // TRANSPOSED only
+    a.relu_output = relu_output ? 1u : 0u;
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
                       stream());
     hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
@@ -409,9 +412,13 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
         hip_check(dav2_hip_conv2d_i8(&a, s), "implicit-GEMM convolution");
         return;
     }
-    // im2col + GEMM, with the fused steps as separate passes.
+    // im2col + GEMM: the input ReLU is taken by the tiled im2col kernels
+    // (other geometries get a separate pass), the residual and the output
+    // ReLU by the GEMM's channel-major epilogue.
+    const bool tiled = stride == 1 && ((kernel == 3 && padding == 1 && input_channels % 16 == 0) ||
+                                       (kernel == 1 && padding == 0));
     const DeviceBuffer* src = &input;
-    if (fusion.relu_input) {
+    if (fusion.relu_input && !tiled) {
         const std::uint32_t count = input_width * input_height * input_channels;
         grow(conv_act_, std::uint64_t(count) * sizeof(float));
         relu(conv_act_, input, count);
@@ -423,16 +430,14 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     ProfileScope prof(context_.profiler(), "im2col_quantize_i8",
                       4.0 * input_width * input_height * input_channels + 1.0 * rows * inner + 4.0 * rows, "B", s);
     grow(im2col_scratch_, scratch_floats * sizeof(float));
-    hip_check(dav2_hip_im2col_quantize_i8(src->as<float>(), input_width, input_height, input_channels, ow, oh,
-                                          kernel, stride, static_cast<std::int32_t>(padding), packed.as<int8_t>(),
-                                          ld, scales.as<float>(), im2col_scratch_.as<float>(), scratch_floats, s),
+    const auto im2col = fusion.relu_input && tiled ? dav2_hip_im2col_quantize_relu_i8 : dav2_hip_im2col_quantize_i8;
+    hip_check(im2col(src->as<float>(), input_width, input_height, input_channels, ow, oh, kernel, stride,
+                     static_cast<std::int32_t>(padding), packed.as<int8_t>(), ld, scales.as<float>(),
+                     im2col_scratch_.as<float>(), scratch_floats, s),
               "im2col quantize");
     workspace_ld_ = ld;
     linear_int8_packed(output, packed, ld, int8_weight, scales, weight_scales, bias, rows, inner, output_channels, 0u,
-                       rows, true, has_bias);
-    const std::uint32_t out_count = rows * output_channels;
-    if (fusion.residual) add(output, output, *fusion.residual, out_count);
-    if (fusion.relu_output) relu(output, output, out_count);
+                       rows, true, has_bias, fusion.residual, fusion.relu_output);
 }
 
 void HipOperators::conv1x1_narrow_int8(DeviceBuffer& output, const DeviceBuffer& input,

@@ -156,7 +156,7 @@ private:
                             const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
                             std::uint32_t input_columns, std::uint32_t output_columns,
                             std::uint32_t output_row_offset, std::uint32_t output_row_stride, bool output_transposed,
-                            bool has_bias);
+                            bool has_bias, const DeviceBuffer* residual = nullptr, bool relu_output = false);
 
     HipContext& context_;
     hipStream_t stream_ = nullptr;

@@ -48,6 +48,17 @@ DAV2_API int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_widt
                                          uint32_t kernel, uint32_t stride, int32_t padding,
                                          int8_t* q, uint32_t ldq, float* scales,
                                          float* scratch, uint64_t scratch_floats, void* stream);
+/* The same for max(input, 0) (relu.glsl ahead of the convolution, as the DPT
+ * residual units apply it), without materialising the ReLU; kernel 3 / stride
+ * 1 / padding 1 (channels % 16 == 0) or kernel 1 / stride 1 / padding 0 with
+ * scratch only, else hipErrorInvalidValue. No reference counterpart (a
+ * fusion of two reference passes). */
+DAV2_API int dav2_hip_im2col_quantize_relu_i8(const float* input, uint32_t input_width,
+                                              uint32_t input_height, uint32_t input_channels,
+                                              uint32_t output_width, uint32_t output_height,
+                                              uint32_t kernel, uint32_t stride, int32_t padding,
+                                              int8_t* q, uint32_t ldq, float* scales,
+                                              float* scratch, uint64_t scratch_floats, void* stream);
 
 /* Replaces layer_norm.glsl:27-68 (src/operators.cpp:1016-1042). */
 DAV2_API int dav2_hip_layer_norm(float* out, const float* input, const float* weight,
@@ -70,7 +81,9 @@ enum {
     DAV2_GEMM_EPI_ROW = 1,            /* out[(m+off)*n + n'] = acc*sa*sb + bias        */
     DAV2_GEMM_EPI_ROW_GELU = 2,       /* ... then exact-erf GELU                        */
     DAV2_GEMM_EPI_ROW_LAYERSCALE = 3, /* out = residual + (acc*sa*sb + bias)*gamma[n'] */
-    DAV2_GEMM_EPI_TRANSPOSED = 4,     /* out[n'*stride + m + off] (channel-major)       */
+    DAV2_GEMM_EPI_TRANSPOSED = 4,     /* out[n'*stride + m + off] (channel-major), plus
+                                         residual at the same index when given, then
+                                         max(., 0) when relu_output                     */
     DAV2_GEMM_EPI_CONVT = 5,          /* stride==kernel ConvTranspose scatter           */
     DAV2_GEMM_EPI_ROW_COLMAX = 6      /* ROW, and per tile of rows the max |out| of each
                                          column n' >= col_absmax_begin                  */
@@ -90,7 +103,7 @@ typedef struct dav2_gemm_i8_args {
     float* out;
     uint64_t out_row_offset;
     uint64_t out_row_stride;
-    const float* residual;  /* LAYERSCALE: may alias out                      */
+    const float* residual;  /* LAYERSCALE (may alias out) or TRANSPOSED        */
     const float* gamma;
     uint32_t convt_kernel, convt_width, convt_height, convt_channels;
     /* ROW_COLMAX: col_absmax[t][n' - col_absmax_begin] = max |out[m][n']| over
@@ -98,6 +111,7 @@ typedef struct dav2_gemm_i8_args {
      * begin is a multiple of 64, n % 4 == 0 and out 16-byte aligned. */
     float* col_absmax;
     uint32_t col_absmax_begin;
+    uint32_t relu_output;   /* TRANSPOSED only: max(out, 0) after the residual */
 } dav2_gemm_i8_args;
 
 /* Replaces linear_int8_tiled.glsl:40-117 (src/operators.cpp:847-880) and

@@ -90,6 +90,35 @@ def test_im2col_quantize_bit_exact(gpu, lib, oracle, c, h, w, k, s, p):
         assert np.all(q[:, kk:] == 0)
 
 
+@pytest.mark.parametrize("c,h,w,k", [(256, 37, 37, 3), (1024, 19, 19, 3), (16, 3, 70, 3), (256, 37, 37, 1),
+                                     (48, 5, 7, 1)])
+def test_im2col_quantize_relu_bit_exact(gpu, lib, oracle, c, h, w, k):
+    # the fused ReLU quantizes exactly the rows of max(x, 0)
+    torch = gpu
+    _announce("im2col relu", c, h, w, k)
+    rng = np.random.default_rng(c + h + 3 * k)
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    p = (k - 1) // 2
+    q_ref, s_ref = oracle.im2col_quantize(np.maximum(x, 0.0), k, 1, p)
+    kk = c * k * k
+    ld = (kk + 63) // 64 * 64
+    xd = dev(torch, x)
+    n_scratch = lib.dav2_hip_im2col_scratch_floats(w, h, c)
+    scratch = empty(torch, (n_scratch,), torch.float32)
+    qd = torch.full((w * h, ld), 0x55, dtype=torch.int8, device="cuda")
+    sd = empty(torch, (w * h,), torch.float32)
+    ok(lib, lib.dav2_hip_im2col_quantize_relu_i8(ptr(xd), w, h, c, w, h, k, 1, p, ptr(qd), ld, ptr(sd), ptr(scratch),
+                                                 n_scratch, stream(torch)))
+    q = host(torch, qd)
+    assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q[:, :kk], q_ref)
+    assert np.all(q[:, kk:] == 0)
+    # x itself is unchanged, and the geometries without a tiled kernel refuse
+    assert np.array_equal(host(torch, xd), x)
+    assert lib.dav2_hip_im2col_quantize_relu_i8(ptr(xd), w, h, c, w, h, k, 1, p, ptr(qd), ld, ptr(sd), None, 0,
+                                                stream(torch)) != 0
+
+
 # ---------------------------------------------------------------------------
 # implicit-GEMM convolution == im2col_quantize_int8.glsl + linear_int8_tiled.glsl
 # (CHW store), bit for bit. Shapes cover every channel-tile configuration the
@@ -371,6 +400,36 @@ def test_gemm_colmax_epilogue(gpu, pkg, lib, oracle, m, n, k, begin):
     for bad in (dict(col_absmax=ptr(cmax), col_absmax_begin=begin + 32), dict(col_absmax=ptr(cmax), col_absmax_begin=n),
                 dict(col_absmax=None, col_absmax_begin=begin)):
         assert lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, **bad)), stream(torch)) != 0
+
+
+@pytest.mark.parametrize("m,n,k", [(1369, 256, 2304), (361, 256, 9216), (37, 96, 576)])
+def test_gemm_transposed_residual_relu(gpu, pkg, lib, oracle, m, n, k):
+    # channel-major output + residual (add.glsl) then max(., 0) (relu.glsl)
+    torch = gpu
+    _announce("gemm transposed residual relu", m, n, k)
+    rng = np.random.default_rng(m + n)
+    a, b, sa, sb, bias = _random_gemm_case(rng, m, n, k)
+    acc = oracle.gemm_i8(a, b)
+    ld = (k + 63) // 64 * 64
+    ad, bd = dev(torch, pad_rows(a, ld)), dev(torch, pad_rows(b, ld))
+    sad, sbd, biasd = dev(torch, sa), dev(torch, sb), dev(torch, bias)
+    conv = oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m, row_stride=m, transposed=True).reshape(n, m)
+    resid = (rng.standard_normal((n, m)) * np.abs(conv).mean()).astype(np.float32)
+    rd = dev(torch, resid)
+    base = dict(a=ptr(ad), lda=ld, b=ptr(bd), ldb=ld, m=m, n=n, k=ld, a_scales=ptr(sad), b_scales=ptr(sbd),
+                bias=ptr(biasd), epilogue=4, out_row_stride=m)
+    for res, relu in ((True, False), (False, True), (True, True)):
+        out = torch.full((n, m), float("nan"), dtype=torch.float32, device="cuda")
+        ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, out=ptr(out), residual=ptr(rd) if res else None,
+                                                        relu_output=int(relu))), stream(torch)))
+        want = oracle.add(conv, resid) if res else conv.copy()
+        if relu:
+            want = oracle.relu(want)
+        assert np.array_equal(host(torch, out).view(np.uint32), want.view(np.uint32)), (res, relu)
+    # relu_output belongs to the channel-major epilogue only
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    bad = dict(base, epilogue=1)
+    assert lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **bad, out=ptr(out), relu_output=1)), stream(torch)) != 0
 
 
 def test_gemm_rejects_bad_arguments(gpu, pkg, lib):
