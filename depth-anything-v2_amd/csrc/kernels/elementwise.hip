@@ -72,14 +72,19 @@ __global__ __launch_bounds__(kBlock) void relu_kernel(float* out, const float* i
     for (; i < n; i += stride) out[i] = fmaxf(in[i], 0.0f);
 }
 
-// bilinear_align_true.glsl:27-63. One thread per output pixel of one channel.
+// bilinear_align_true.glsl:27-63. One thread per output pixel and
+// kBilinearChannels channels: the source coordinates and weights are formed
+// once (the shader's operation order) and reused for every channel, and all
+// the channels' gathers are issued before the first blend.
+constexpr uint32_t kBilinearChannels = 8;
+
 __global__ __launch_bounds__(kBlock) void bilinear_kernel(float* __restrict__ out, const float* __restrict__ in,
                                                           uint32_t iw, uint32_t ih, uint32_t ow, uint32_t oh,
                                                           uint32_t channels) {
     const uint32_t ox = blockIdx.x * 64u + (threadIdx.x & 63u);
     const uint32_t oy = blockIdx.y * 4u + (threadIdx.x >> 6);
-    const uint32_t c = blockIdx.z;
-    if (ox >= ow || oy >= oh || c >= channels) return;
+    const uint32_t c0 = blockIdx.z * kBilinearChannels;
+    if (ox >= ow || oy >= oh) return;
     const float sx = ow > 1 ? static_cast<float>(ox) * static_cast<float>(iw - 1) / static_cast<float>(ow - 1) : 0.0f;
     const float sy = oh > 1 ? static_cast<float>(oy) * static_cast<float>(ih - 1) / static_cast<float>(oh - 1) : 0.0f;
     const uint32_t x0 = static_cast<uint32_t>(floorf(sx));
@@ -88,10 +93,25 @@ __global__ __launch_bounds__(kBlock) void bilinear_kernel(float* __restrict__ ou
     const uint32_t y1 = min(y0 + 1u, ih - 1u);
     const float fx = sx - static_cast<float>(x0);
     const float fy = sy - static_cast<float>(y0);
-    const float* src = in + static_cast<uint64_t>(c) * ih * iw;
-    const float top = src[y0 * iw + x0] * (1.0f - fx) + src[y0 * iw + x1] * fx;
-    const float bottom = src[y1 * iw + x0] * (1.0f - fx) + src[y1 * iw + x1] * fx;
-    out[(static_cast<uint64_t>(c) * oh + oy) * ow + ox] = top * (1.0f - fy) + bottom * fy;
+    const uint64_t iplane = static_cast<uint64_t>(ih) * iw, oplane = static_cast<uint64_t>(oh) * ow;
+    const uint32_t n = min(kBilinearChannels, channels - c0);
+    const float* src = in + static_cast<uint64_t>(c0) * iplane;
+    float a[kBilinearChannels], b[kBilinearChannels], c[kBilinearChannels], d[kBilinearChannels];
+#pragma unroll
+    for (uint32_t k = 0; k < kBilinearChannels; ++k) {
+        const float* p = src + static_cast<uint64_t>(min(k, n - 1u)) * iplane;  // clamped: every load valid
+        a[k] = p[y0 * iw + x0];
+        b[k] = p[y0 * iw + x1];
+        c[k] = p[y1 * iw + x0];
+        d[k] = p[y1 * iw + x1];
+    }
+    float* dst = out + static_cast<uint64_t>(c0) * oplane + static_cast<uint64_t>(oy) * ow + ox;
+#pragma unroll
+    for (uint32_t k = 0; k < kBilinearChannels; ++k) {
+        const float top = a[k] * (1.0f - fx) + b[k] * fx;
+        const float bottom = c[k] * (1.0f - fx) + d[k] * fx;
+        if (k < n) dst[static_cast<uint64_t>(k) * oplane] = top * (1.0f - fy) + bottom * fy;
+    }
 }
 
 // reduce_minmax.glsl as a grid reduction. Stage 1: each workgroup folds a
@@ -262,7 +282,7 @@ int dav2_hip_bilinear_align_true(float* out, const float* input, uint32_t iw, ui
                                  uint32_t oh, uint32_t channels, void* stream) {
     if (ow == 0 || oh == 0 || channels == 0) return hipSuccess;
     if (!out || !input || iw == 0 || ih == 0 || channels > 65535u) return hipErrorInvalidValue;
-    const dim3 grid(ceil_div(ow, 64), ceil_div(oh, 4), channels);
+    const dim3 grid(ceil_div(ow, 64), ceil_div(oh, 4), ceil_div(channels, kBilinearChannels));
     hipLaunchKernelGGL(bilinear_kernel, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), out, input, iw, ih,
                        ow, oh, channels);
     return hipGetLastError();

@@ -677,7 +677,7 @@ def test_elementwise_exact(gpu, lib, oracle):
 
 
 @pytest.mark.parametrize("c,ih,iw,oh,ow", [(256, 19, 19, 37, 37), (256, 148, 148, 296, 296), (128, 296, 296, 518, 518),
-                                           (3, 5, 7, 1, 1), (2, 1, 1, 4, 3), (64, 25, 19, 50, 38)])
+                                           (3, 5, 7, 1, 1), (2, 1, 1, 4, 3), (64, 25, 19, 50, 38), (13, 9, 11, 20, 21)])
 def test_bilinear_bit_exact(gpu, lib, oracle, c, ih, iw, oh, ow):
     torch = gpu
     _announce("bilinear", c, ih, iw, oh, ow)
