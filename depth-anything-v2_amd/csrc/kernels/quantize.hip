@@ -186,6 +186,18 @@ __global__ __launch_bounds__(256) void channel_group_absmax_kernel(const float* 
     const uint32_t c1 = min(C, c0 + kGroupChannels);
     const float* src = x + c0 * plane + p;
     auto mag = [](float v) { return RELU ? fmaxf(v, 0.0f) : fabsf(v); };
+    if (c1 - c0 == kGroupChannels) {
+        // a full group: all 32 loads in flight at once
+        float v[kGroupChannels];
+#pragma unroll
+        for (uint32_t k = 0; k < kGroupChannels; ++k) v[k] = mag(src[k * plane]);
+#pragma unroll
+        for (uint32_t w = kGroupChannels / 2; w > 0; w >>= 1)
+#pragma unroll
+            for (uint32_t k = 0; k < w; ++k) v[k] = fmaxf(v[k], v[k + w]);
+        partial[blockIdx.y * plane + p] = fmaxf(v[0], 0.0f);  // max is exact: same value as the loop below
+        return;
+    }
     float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
     uint32_t c = c0;
     for (; c + 4 <= c1; c += 4, src += 4 * plane) {
