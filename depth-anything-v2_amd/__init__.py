@@ -90,7 +90,7 @@ class GemmArgs(C.Structure):
                 ("out_row_stride", C.c_uint64), ("residual", C.c_void_p), ("gamma", C.c_void_p),
                 ("convt_kernel", C.c_uint32), ("convt_width", C.c_uint32), ("convt_height", C.c_uint32),
                 ("convt_channels", C.c_uint32), ("col_absmax", C.c_void_p), ("col_absmax_begin", C.c_uint32),
-                ("relu_output", C.c_uint32)]
+                ("relu_output", C.c_uint32), ("split_k", C.c_uint32), ("split_scratch", C.c_void_p)]
 
 
 class ConvArgs(C.Structure):
@@ -152,6 +152,7 @@ PROTOTYPES = {
     "dav2_hip_layer_norm_quantize_i8": (C.c_int, [vp, u32, vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "dav2_hip_gemm_i8": (C.c_int, [C.POINTER(GemmArgs), vp]),
     "dav2_hip_gemm_i8_row_tiles": (u32, [u32, u32, u32]),
+    "dav2_hip_gemm_i8_split_scratch_bytes": (u64, [u32, u32, u32]),
     "dav2_hip_gelu": (C.c_int, [vp, vp, u64, vp]),
     "dav2_hip_add_scaled": (C.c_int, [vp, vp, vp, vp, u64, u32, vp]),
     "dav2_hip_add": (C.c_int, [vp, vp, vp, u64, vp]),

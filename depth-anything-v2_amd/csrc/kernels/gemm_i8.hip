@@ -47,7 +47,13 @@ struct GemmParams {
     float* col_absmax;       // ROW_COLMAX partial maxima [row tile][n - col_absmax_begin]
     uint32_t col_absmax_begin;
     uint32_t relu_output;    // TRANSPOSED: max(out, 0) after the residual
+    uint32_t k_split;        // K bytes per blockIdx.z slice (multiple of 128; == k without split-K)
 };
+
+// Split-K slices of a channel-major GEMM store their int32 sums here:
+// out_i32[(slice * rows_p + prow) * rows_q + qcol]; a second kernel adds the
+// slices (exact) and applies the TRANSPOSED epilogue.
+constexpr int kEpiSplitPartial = 100;
 
 template <int EPI>
 constexpr bool row_major_epi() {
@@ -69,7 +75,8 @@ DAV2_DEV float gelu_erf(float v) {
 template <int EPI>
 struct Orientation {
     // Channel-major epilogues swap operands (see file comment).
-    static constexpr bool swapped = EPI == DAV2_GEMM_EPI_TRANSPOSED || EPI == DAV2_GEMM_EPI_CONVT;
+    static constexpr bool swapped =
+        EPI == DAV2_GEMM_EPI_TRANSPOSED || EPI == DAV2_GEMM_EPI_CONVT || EPI == kEpiSplitPartial;
 };
 
 // Epilogue operands of one lane, loaded before the K loop so that no global
@@ -80,7 +87,7 @@ struct Orientation {
 template <int EPI, int TM, int TN>
 struct EpilogueOperands {
     static constexpr bool kSwapped = Orientation<EPI>::swapped;
-    static constexpr bool kScales = EPI != DAV2_GEMM_EPI_RAW_I32;
+    static constexpr bool kScales = EPI != DAV2_GEMM_EPI_RAW_I32 && EPI != kEpiSplitPartial;
     static constexpr bool kLayerScale = EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE;
     float ps[TM][4];  // scale of the P row: a_scales[m] (row-major) or b_scales[n] (swapped)
     float pb[TM][4];  // bias of the P row (swapped)
@@ -148,6 +155,10 @@ DAV2_DEV void store_one(const GemmParams& g, const EpilogueOperands<EPI, TM, TN>
     const uint32_t n = sw ? prow : qcol;
     if (EPI == DAV2_GEMM_EPI_RAW_I32) {
         g.out_i32[static_cast<uint64_t>(m) * g.n + n] = acc;
+        return;
+    }
+    if (EPI == kEpiSplitPartial) {
+        g.out_i32[(static_cast<uint64_t>(blockIdx.z) * g.rows_p + prow) * g.rows_q + qcol] = acc;
         return;
     }
     const float s_in = sw ? e.qs[j] : e.ps[i][r];
@@ -229,8 +240,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
     tile_of(tm, tn);
     const uint32_t row0 = tm * BM;
     const uint32_t col0 = tn * BN;
-    // K is a multiple of 64: full stages, then possibly a partial one
-    const int ksteps = static_cast<int>((g.k + kBK - 1) / kBK);
+    // This workgroup's K slice (all of K without split-K): kbase is a
+    // multiple of 128, klen a multiple of 64 -- full stages, then possibly a
+    // partial one.
+    const uint32_t kbase = blockIdx.z * g.k_split;
+    const uint32_t klen = min(g.k_split, g.k - kbase);
+    const int ksteps = static_cast<int>((klen + kBK - 1) / kBK);
 
     // Loads of this wave: instruction i covers stage rows RPL*(wave*LPW + i)
     // .. +RPL-1; lane l brings row +l/CPR, physical chunk l%CPR, i.e. the
@@ -245,10 +260,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
         chunk_bytes[i] = ((lane % CPR) ^ ((srow / (256 / BK)) & (CPR - 1))) * 16u;
         if (srow < static_cast<uint32_t>(BM)) {  // uniform per instruction (BM % RPL == 0)
             const uint32_t r = min(row0 + srow, g.rows_p - 1);
-            src[i] = g.p + r * g.ldp + chunk_bytes[i];
+            src[i] = g.p + r * g.ldp + kbase + chunk_bytes[i];
         } else {
             const uint32_t r = min(col0 + srow - BM, g.rows_q - 1);
-            src[i] = g.q + r * g.ldq + chunk_bytes[i];
+            src[i] = g.q + r * g.ldq + kbase + chunk_bytes[i];
         }
     }
     auto issue = [&](int ks) {
@@ -259,7 +274,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
             // In a partial stage chunks past K re-read bytes of the same row
             // inside K (never multiplied).
             int64_t off = static_cast<int64_t>(kofs);
-            while (off + chunk_bytes[i] >= g.k) off -= 64;
+            while (off + chunk_bytes[i] >= klen) off -= 64;
             copy16_to_lds(src[i] + off, smem + slot * STAGE_BYTES + (wave * LOADS_PER_WAVE + i) * 1024);
         }
     };
@@ -301,7 +316,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
         __builtin_amdgcn_sched_barrier(0);
         if (ks + STAGES - 1 < ksteps) issue(ks + STAGES - 1);
         const int8_t* st = smem + (ks % STAGES) * STAGE_BYTES;
-        const int ksub = min(static_cast<int>((g.k - static_cast<uint32_t>(ks) * kBK) / 64), BK / 64);
+        const int ksub = min(static_cast<int>((klen - static_cast<uint32_t>(ks) * kBK) / 64), BK / 64);
 #pragma unroll
         for (int kk = 0; kk < BK / 64; ++kk) {
             if (kk < ksub) {
@@ -437,7 +452,7 @@ void launch_cfg(const GemmParams& g, hipStream_t s) {
         reinterpret_cast<const void*>(gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     (void)attr;
-    const dim3 grid(ceil_div(g.rows_p, BM), ceil_div(g.rows_q, BN));
+    const dim3 grid(ceil_div(g.rows_p, BM), ceil_div(g.rows_q, BN), ceil_div(g.k, g.k_split));
     hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>), grid, dim3(64 * WMW * WNW), lds, s, g);
 }
 
@@ -463,7 +478,32 @@ void launch_epi(const GemmParams& g, hipStream_t s) {
     }
 }
 
+// Adds the split-K slices (exact int32 sums) and applies the TRANSPOSED
+// epilogue: out[n * stride + m + off] = ((acc * a_scale[m]) * b_scale[n]) +
+// bias[n], + residual (add.glsl), max(., 0) (relu.glsl). One thread per
+// output, m fastest.
+__global__ __launch_bounds__(256) void split_reduce_transposed_kernel(
+    const int32_t* __restrict__ partial, uint32_t slices, uint32_t n, uint32_t m, const float* __restrict__ a_scales,
+    const float* __restrict__ b_scales, const float* __restrict__ bias, const float* __restrict__ residual,
+    uint32_t relu, float* __restrict__ out, uint64_t out_row_stride, uint64_t out_row_offset) {
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    const uint64_t total = static_cast<uint64_t>(n) * m;
+    if (idx >= total) return;
+    const uint32_t nn = static_cast<uint32_t>(idx / m), mm = static_cast<uint32_t>(idx - static_cast<uint64_t>(nn) * m);
+    int32_t acc = 0;
+    for (uint32_t z = 0; z < slices; ++z) acc += partial[static_cast<uint64_t>(z) * total + idx];
+    float v = dequant(acc, a_scales[mm], b_scales[nn], bias ? bias[nn] : 0.0f);
+    const uint64_t o = static_cast<uint64_t>(nn) * out_row_stride + mm + out_row_offset;
+    if (residual) v = v + residual[o];
+    if (relu) v = fmaxf(v, 0.0f);
+    out[o] = v;
+}
+
 }  // namespace
+
+extern "C" uint64_t dav2_hip_gemm_i8_split_scratch_bytes(uint32_t m, uint32_t n, uint32_t split_k) {
+    return static_cast<uint64_t>(split_k) * m * n * sizeof(int32_t);
+}
 
 extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     if (!a) return hipErrorInvalidValue;
@@ -487,6 +527,10 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
         return hipErrorInvalidValue;
     if (e > DAV2_GEMM_EPI_ROW_COLMAX) return hipErrorInvalidValue;
     if (a->relu_output && e != DAV2_GEMM_EPI_TRANSPOSED) return hipErrorInvalidValue;
+    const bool split = a->split_k > 1;
+    if (split && (e != DAV2_GEMM_EPI_TRANSPOSED || a->split_k > 64 || !a->split_scratch ||
+                  (reinterpret_cast<uintptr_t>(a->split_scratch) & 3u)))
+        return hipErrorInvalidValue;
 
     GemmParams g{};
     const bool swapped = e == DAV2_GEMM_EPI_TRANSPOSED || e == DAV2_GEMM_EPI_CONVT;
@@ -515,7 +559,24 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     g.col_absmax = a->col_absmax;
     g.col_absmax_begin = a->col_absmax_begin;
     g.relu_output = a->relu_output;
+    g.k_split = a->k;
+    uint32_t slices = 1;
+    if (split) {
+        // slices of whole 128-byte stages; the last one may be shorter
+        g.k_split = ceil_div(ceil_div(a->k, a->split_k), 128) * 128u;
+        slices = ceil_div(a->k, g.k_split);
+        g.out_i32 = a->split_scratch;
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (split && slices > 1) {
+        launch_epi<kEpiSplitPartial>(g, s);
+        const uint64_t total = static_cast<uint64_t>(a->m) * a->n;
+        hipLaunchKernelGGL(split_reduce_transposed_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s,
+                           a->split_scratch, slices, a->n, a->m, a->a_scales, a->b_scales, a->bias, a->residual,
+                           a->relu_output, a->out, a->out_row_stride, a->out_row_offset);
+        return hipGetLastError();
+    }
+    if (split) g.out_i32 = a->out_i32;
     switch (e) {
         case DAV2_GEMM_EPI_RAW_I32: launch_epi<DAV2_GEMM_EPI_RAW_I32>(g, s); break;
         case DAV2_GEMM_EPI_ROW: launch_epi<DAV2_GEMM_EPI_ROW>(g, s); break;

@@ -1,5 +1,7 @@
 #include "operators.h"
 
+#include <algorithm>
+
 #include "dav2_hip.h"
 
 #include <limits>
@@ -164,6 +166,18 @@ void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& 
     a.out_row_stride = output_row_stride;
     a.residual = residual ? residual->as<float>() : nullptr;  // TRANSPOSED only
     a.relu_output = relu_output ? 1u : 0u;
+    if (output_transposed) {
+        // Few output tiles (the DPT's 37x37 / 19x19 maps): split K so that
+        // about 256 workgroups run, each slice at least two 128-byte stages.
+        const std::uint32_t tiles = ((output_columns + 63) / 64) * ((rows + 63) / 64);
+        const std::uint32_t ksteps = (a.k + 127) / 128;
+        const std::uint32_t split = std::min({8u, (256u + tiles - 1) / tiles, ksteps / 2});
+        if (split > 1) {
+            grow(gemm_split_, dav2_hip_gemm_i8_split_scratch_bytes(rows, output_columns, split));
+            a.split_k = split;
+            a.split_scratch = gemm_split_.as<std::int32_t>();
+        }
+    }
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
                       stream());
     hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");

@@ -172,6 +172,7 @@ private:
     DeviceBuffer im2col_scratch_;  // per-channel-group maxima for the tiled im2col kernels
     DeviceBuffer conv_weights_;    // tap-major weights of a conv2d_int8 call that brought none
     DeviceBuffer conv_act_;        // ReLU of a conv2d_int8 input on the im2col path
+    DeviceBuffer gemm_split_;      // int32 slices of split-K channel-major GEMMs
     std::uint32_t workspace_ld_ = 0;  // row stride of the int8 rows currently in the workspace
 };
 

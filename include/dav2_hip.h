@@ -112,6 +112,12 @@ typedef struct dav2_gemm_i8_args {
     float* col_absmax;
     uint32_t col_absmax_begin;
     uint32_t relu_output;   /* TRANSPOSED only: max(out, 0) after the residual */
+    /* TRANSPOSED only: split_k > 1 runs K in that many slices on more
+     * workgroups (for GEMMs with few output tiles), their int32 sums in
+     * split_scratch (dav2_hip_gemm_i8_split_scratch_bytes), then one pass
+     * adds them (exact) and applies the epilogue. Same output bits. */
+    uint32_t split_k;
+    int32_t* split_scratch;
 } dav2_gemm_i8_args;
 
 /* Replaces linear_int8_tiled.glsl:40-117 (src/operators.cpp:847-880) and
@@ -121,6 +127,8 @@ DAV2_API int dav2_hip_gemm_i8(const dav2_gemm_i8_args* args, void* stream);
  * n output columns. No reference counterpart: the attention's digit packing
  * reads these maxima instead of a pass over k and v. */
 DAV2_API uint32_t dav2_hip_gemm_i8_row_tiles(uint32_t m, uint32_t n, uint32_t epilogue);
+/* Scratch bytes of a split-K dav2_hip_gemm_i8 call. No reference counterpart. */
+DAV2_API uint64_t dav2_hip_gemm_i8_split_scratch_bytes(uint32_t m, uint32_t n, uint32_t split_k);
 
 /* Implicit-GEMM int8 convolution: replaces the im2col_quantize_int8.glsl +
  * linear_int8_tiled.glsl pair of VulkanOperators::conv2d_int8

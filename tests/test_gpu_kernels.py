@@ -432,6 +432,42 @@ def test_gemm_transposed_residual_relu(gpu, pkg, lib, oracle, m, n, k):
     assert lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **bad, out=ptr(out), relu_output=1)), stream(torch)) != 0
 
 
+@pytest.mark.parametrize("m,n,k,split", [(361, 256, 2304, 8), (1369, 256, 9216, 3), (361, 1024, 9216, 3),
+                                         (37, 96, 576, 2), (361, 256, 2304, 5), (100, 64, 192, 4)])
+def test_gemm_split_k_matches_single_pass(gpu, pkg, lib, oracle, m, n, k, split):
+    # K in slices on more workgroups, slices added as int32 (exact): the same
+    # bits as one pass, with and without residual / ReLU
+    torch = gpu
+    _announce("gemm split-k", m, n, k, split)
+    rng = np.random.default_rng(m + n + split)
+    a, b, sa, sb, bias = _random_gemm_case(rng, m, n, k)
+    acc = oracle.gemm_i8(a, b)
+    ld = (k + 63) // 64 * 64
+    ad, bd = dev(torch, pad_rows(a, ld)), dev(torch, pad_rows(b, ld))
+    sad, sbd, biasd = dev(torch, sa), dev(torch, sb), dev(torch, bias)
+    conv = oracle.linear_epilogue(acc, sa, sb, bias, out_rows=m, row_stride=m, transposed=True).reshape(n, m)
+    resid = (rng.standard_normal((n, m)) * np.abs(conv).mean()).astype(np.float32)
+    rd = dev(torch, resid)
+    nbytes = lib.dav2_hip_gemm_i8_split_scratch_bytes(m, n, split)
+    assert nbytes == split * m * n * 4
+    scratch = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda")
+    base = dict(a=ptr(ad), lda=ld, b=ptr(bd), ldb=ld, m=m, n=n, k=ld, a_scales=ptr(sad), b_scales=ptr(sbd),
+                bias=ptr(biasd), epilogue=4, out_row_stride=m, split_k=split, split_scratch=ptr(scratch))
+    for res, relu in ((False, False), (True, True)):
+        out = torch.full((n, m), float("nan"), dtype=torch.float32, device="cuda")
+        ok(lib, lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **base, out=ptr(out), residual=ptr(rd) if res else None,
+                                                        relu_output=int(relu))), stream(torch)))
+        want = oracle.add(conv, resid) if res else conv.copy()
+        if relu:
+            want = oracle.relu(want)
+        assert np.array_equal(host(torch, out).view(np.uint32), want.view(np.uint32)), (res, relu)
+    # split-K belongs to the channel-major epilogue and needs its scratch
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    assert lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **dict(base, epilogue=1), out=ptr(out))), stream(torch)) != 0
+    assert lib.dav2_hip_gemm_i8(C.byref(_gemm_args(pkg, **dict(base, split_scratch=None), out=ptr(out))),
+                                stream(torch)) != 0
+
+
 def test_gemm_rejects_bad_arguments(gpu, pkg, lib):
     torch = gpu
     a = torch.zeros((4, 64), dtype=torch.int8, device="cuda")
