@@ -164,34 +164,34 @@ FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::str
     return out;
 }
 
-FeatureMap DptHead::residual_unit(const FeatureMap& in, const std::string& prefix, Arena& arena,
-                                  const std::string& slot) {
+FeatureMap DptHead::residual_unit(HipOperators& ops, const FeatureMap& in, const std::string& prefix, Arena& arena,
+                                  const std::string& temp_slot, const std::string& slot) {
     // dpt.cpp:537-572: relu -> conv3x3 -> relu -> conv3x3 -> + input, the
     // ReLUs and the residual add folded into the two convolutions.
     ConvFusion first_fusion;
     first_fusion.relu_input = true;
     first_fusion.relu_output = true;
-    FeatureMap first = conv(ops_, in, prefix + ".conv1.weight", prefix + ".conv1.bias", in.channels, 3, 1, 1, true, arena,
-                            "dpt.ru.first", first_fusion);
+    FeatureMap first = conv(ops, in, prefix + ".conv1.weight", prefix + ".conv1.bias", in.channels, 3, 1, 1, true, arena,
+                            temp_slot, first_fusion);
     ConvFusion second_fusion;
     second_fusion.residual = in.buffer;
-    return conv(ops_, first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.channels, 3, 1, 1, true, arena, slot,
+    return conv(ops, first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.channels, 3, 1, 1, true, arena, slot,
                 second_fusion);
 }
 
-FeatureMap DptHead::fusion(const FeatureMap& path, const FeatureMap* skip, const std::string& prefix,
-                           std::uint32_t ow, std::uint32_t oh, Arena& arena, const std::string& slot) {
-    // dpt.cpp:574-615
-    if (skip) {
-        FeatureMap processed = residual_unit(*skip, prefix + ".resConfUnit1", arena, "dpt.fu.skip");
-        ops_.add(*path.buffer, *path.buffer, *processed.buffer, static_cast<std::uint32_t>(path.elements()));
-    }
-    FeatureMap unit = residual_unit(path, prefix + ".resConfUnit2", arena, "dpt.fu.unit");
+FeatureMap DptHead::fusion(const FeatureMap& path, const std::string& prefix, std::uint32_t ow, std::uint32_t oh,
+                           const FeatureMap* next_skip, Arena& arena, const std::string& slot) {
+    // dpt.cpp:574-615 from resConfUnit2 on: the path arrives with this
+    // refinenet's processed skip already added (by the previous out_conv).
+    FeatureMap unit = residual_unit(ops_, path, prefix + ".resConfUnit2", arena, "dpt.ru.first", "dpt.fu.unit");
     FeatureMap resized{&arena.get("dpt.fu.resized", std::uint64_t(ow) * oh * config_.features * sizeof(float)), ow,
                        oh, config_.features};
     ops_.bilinear_align_true(*resized.buffer, *unit.buffer, unit.width, unit.height, ow, oh, config_.features);
+    // path + processed skip of the next refinenet (add.glsl; a + b == b + a)
+    ConvFusion add_skip;
+    add_skip.residual = next_skip ? next_skip->buffer : nullptr;
     return conv(ops_, resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", config_.features, 1, 1, 0, true,
-                arena, slot);
+                arena, slot, add_skip);
 }
 
 FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, std::uint32_t b, std::uint32_t pw,
@@ -223,22 +223,30 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
                      config_.project[3], 3, 2, 1, true, arena, "dpt.layer3");
     }
     // layer*_rn (dpt.cpp:743-756)
-    return conv(ops, layer, "depth_head.scratch.layer" + std::to_string(i + 1) + "_rn.weight", "", config_.features, 3,
-                1, 1, false, arena, "dpt.rn" + std::to_string(i));
+    const std::string level = std::to_string(i);
+    FeatureMap rn = conv(ops, layer, "depth_head.scratch.layer" + std::to_string(i + 1) + "_rn.weight", "",
+                         config_.features, 3, 1, 1, false, arena, "dpt.rn" + level);
+    if (i == 3) return rn;
+    // refinenet(i+1).resConfUnit1 on this level (dpt.cpp:574-590): its own
+    // arena slots, so it may run beside the other levels
+    return residual_unit(ops, rn, "depth_head.scratch.refinenet" + std::to_string(i + 1) + ".resConfUnit1", arena,
+                         "dpt.ru.first" + level, "dpt.skip" + level);
 }
 
 void DptHead::refine_and_head(const FeatureMap refined[4], std::uint32_t b, std::uint32_t pw, std::uint32_t ph,
                               Arena& arena, float* depth, float* pre_relu) {
     const std::uint32_t F = config_.features;
-    // refinenets (dpt.cpp:759-790); outputs alternate between two slots.
-    FeatureMap path = fusion(refined[3], nullptr, "depth_head.scratch.refinenet4", refined[2].width, refined[2].height,
-                             arena, "dpt.pathA");
-    path = fusion(path, &refined[2], "depth_head.scratch.refinenet3", refined[1].width, refined[1].height, arena,
+    // refinenets (dpt.cpp:759-790); refined[0..2] are the processed skip
+    // inputs of refinenet1..3, refined[3] the deepest level. Outputs
+    // alternate between two slots.
+    FeatureMap path = fusion(refined[3], "depth_head.scratch.refinenet4", refined[2].width, refined[2].height,
+                             &refined[2], arena, "dpt.pathA");
+    path = fusion(path, "depth_head.scratch.refinenet3", refined[1].width, refined[1].height, &refined[1], arena,
                   "dpt.pathB");
-    path = fusion(path, &refined[1], "depth_head.scratch.refinenet2", refined[0].width, refined[0].height, arena,
+    path = fusion(path, "depth_head.scratch.refinenet2", refined[0].width, refined[0].height, &refined[0], arena,
                   "dpt.pathA");
-    path = fusion(path, &refined[0], "depth_head.scratch.refinenet1", refined[0].width * 2, refined[0].height * 2,
-                  arena, "dpt.pathB");
+    path = fusion(path, "depth_head.scratch.refinenet1", refined[0].width * 2, refined[0].height * 2, nullptr, arena,
+                  "dpt.pathB");
     // output head (dpt.cpp:792-855)
     path = conv(ops_, path, "depth_head.scratch.output_conv1.weight", "depth_head.scratch.output_conv1.bias", F / 2, 3,
                 1, 1, true, arena, "dpt.out1");

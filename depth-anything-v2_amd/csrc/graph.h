@@ -78,8 +78,11 @@ public:
 
     // The two phases of forward for image b. prepare_level runs projection,
     // resize layer and layer*_rn of level i (its own arena slots, so the four
-    // levels may run on different operator sets / streams); refine_and_head
-    // runs the refinenets and the output head on the main operator set.
+    // levels may run on different operator sets / streams) and, for levels
+    // 0-2, the first residual unit of the refinenet that takes the level as
+    // its skip input (it does not depend on the deeper levels), returning
+    // that unit's output; refine_and_head runs the rest of the refinenets and
+    // the output head on the main operator set.
     FeatureMap prepare_level(std::uint32_t level, const DeviceBuffer& feature, std::uint32_t b,
                              std::uint32_t patch_width, std::uint32_t patch_height, Arena& arena, HipOperators& ops);
     void refine_and_head(const FeatureMap refined[4], std::uint32_t b, std::uint32_t patch_width,
@@ -89,10 +92,13 @@ private:
     FeatureMap conv(HipOperators& ops, const FeatureMap& input, const std::string& weight, const std::string& bias,
                     std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding,
                     bool has_bias, Arena& arena, const std::string& slot, const ConvFusion& fusion = ConvFusion{});
-    FeatureMap residual_unit(const FeatureMap& input, const std::string& prefix, Arena& arena,
-                             const std::string& slot);
-    FeatureMap fusion(const FeatureMap& path, const FeatureMap* skip, const std::string& prefix,
-                      std::uint32_t output_width, std::uint32_t output_height, Arena& arena, const std::string& slot);
+    FeatureMap residual_unit(HipOperators& ops, const FeatureMap& input, const std::string& prefix, Arena& arena,
+                             const std::string& temp_slot, const std::string& slot);
+    // Second residual unit, resize and out_conv of a refinenet; out_conv adds
+    // next_skip (the next refinenet's processed skip input, the add of
+    // dpt.cpp:574-615) when given.
+    FeatureMap fusion(const FeatureMap& path, const std::string& prefix, std::uint32_t output_width,
+                      std::uint32_t output_height, const FeatureMap* next_skip, Arena& arena, const std::string& slot);
 
     DptConfig config_;
     GpuModel& weights_;
