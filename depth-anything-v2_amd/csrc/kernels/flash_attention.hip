@@ -254,12 +254,12 @@ __global__ __launch_bounds__(256) void pack_kv_kernel(const float* __restrict__ 
     }
 }
 
-// One image: q, k and v of 64 tokens of head h into digit planes in one
-// pass (pack_q_kernel + pack_kv_kernel for batch 1), the maxima of |k| and
-// |v| per column coming from the qkv GEMM's row-tile partials
-// col_absmax[t][c] (c < D: k column c, c >= D: v column c - D). Thread t
-// owns token row t/4, features 16*(t%4)..+15 of q and k, and feature t/4,
-// block positions 16*(t%4)..+15 of v.
+// One image: q, k or v (blockIdx.z = 0, 1, 2) of 64 tokens of head h into
+// digit planes in one pass (pack_q_kernel + pack_kv_kernel for batch 1),
+// the maxima of |k| and |v| per column coming from the qkv GEMM's row-tile
+// partials col_absmax[t][c] (c < D: k column c, c >= D: v column c - D).
+// Thread t owns token row t/4, features 16*(t%4)..+15 of q or k, and
+// feature t/4, block positions 16*(t%4)..+15 of v.
 __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__ qkv,
                                                        const float* __restrict__ col_absmax, uint32_t partial_rows,
                                                        int8_t* __restrict__ qd, int8_t* __restrict__ kd,
@@ -267,70 +267,34 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
                                                        int* __restrict__ ke, int* __restrict__ ve, uint32_t tokens,
                                                        uint32_t heads, uint32_t tp) {
     __shared__ float tile[64][65];  // v [token][feature]
-    __shared__ float kred[4];
-    __shared__ float vred[4][64];
-    const uint32_t h = blockIdx.y;
+    __shared__ float red[4][64];    // k: per-wave maxima; v: per-wave column maxima
+    const uint32_t h = blockIdx.y, part = blockIdx.z;
     const uint32_t D = heads * 64u;
     const uint32_t j0 = blockIdx.x * kBlock;
     const int tid = threadIdx.x, hi4 = tid >> 2, c16 = (tid & 3) * 16;
     const uint32_t t = j0 + hi4;
 
-    float q[16], k[16];
+    float x[16];
     {
-        const float* src = qkv + static_cast<uint64_t>(t) * 3u * D + h * 64u + c16;
+        const float* src = qkv + static_cast<uint64_t>(t) * 3u * D + part * D + h * 64u + c16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float4 vq = make_float4(0.f, 0.f, 0.f, 0.f), vk = vq, vv = vq;
-            if (t < tokens) {
-                vq = *reinterpret_cast<const float4*>(src + 4 * i);
-                vk = *reinterpret_cast<const float4*>(src + D + 4 * i);
-                vv = *reinterpret_cast<const float4*>(src + 2u * D + 4 * i);
-            }
-            q[4 * i + 0] = vq.x * 0.125f;
-            q[4 * i + 1] = vq.y * 0.125f;
-            q[4 * i + 2] = vq.z * 0.125f;
-            q[4 * i + 3] = vq.w * 0.125f;
-            k[4 * i + 0] = vk.x;
-            k[4 * i + 1] = vk.y;
-            k[4 * i + 2] = vk.z;
-            k[4 * i + 3] = vk.w;
-            tile[hi4][c16 + 4 * i + 0] = vv.x;
-            tile[hi4][c16 + 4 * i + 1] = vv.y;
-            tile[hi4][c16 + 4 * i + 2] = vv.z;
-            tile[hi4][c16 + 4 * i + 3] = vv.w;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t < tokens) v = *reinterpret_cast<const float4*>(src + 4 * i);
+            x[4 * i + 0] = v.x;
+            x[4 * i + 1] = v.y;
+            x[4 * i + 2] = v.z;
+            x[4 * i + 3] = v.w;
         }
     }
-    // Head maximum of |k| and column maxima of |v| from the partials (wave w
-    // folds row tiles w, w + 4, ...; lane = feature).
-    {
-        // The first 16 row tiles are loaded at once (indices clamped: a
-        // repeated row leaves a maximum unchanged), further ones in a loop.
-        const uint32_t f = static_cast<uint32_t>(tid & 63);
-        const float* cols = col_absmax + h * 64u + f;
-        float pk[4], pv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = min(static_cast<uint32_t>(tid >> 6) + 4u * i, partial_rows - 1u);
-            pk[i] = cols[static_cast<uint64_t>(r) * 2u * D];
-            pv[i] = cols[static_cast<uint64_t>(r) * 2u * D + D];
-        }
-        float mk = fmaxf(fmaxf(pk[0], pk[1]), fmaxf(pk[2], pk[3]));
-        float mv = fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3]));
-        for (uint32_t r = static_cast<uint32_t>(tid >> 6) + 16u; r < partial_rows; r += 4u) {
-            mk = fmaxf(mk, cols[static_cast<uint64_t>(r) * 2u * D]);
-            mv = fmaxf(mv, cols[static_cast<uint64_t>(r) * 2u * D + D]);
-        }
-        mk = wave_max(mk);
-        if ((tid & 63) == 0) kred[tid >> 6] = mk;
-        vred[tid >> 6][f] = mv;
-    }
-
-    // q: exponent of the row maximum over the four lanes of the row
     int8_t d1[16], d0[16];
-    {
+    if (part == 0) {  // q * 0.125: exponent of the row maximum over the four lanes of the row
         float a = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) a = fmaxf(a, fabsf(q[i]));
+        for (int i = 0; i < 16; ++i) {
+            x[i] = x[i] * 0.125f;
+            a = fmaxf(a, fabsf(x[i]));
+        }
         a = fmaxf(a, __shfl_xor(a, 1, kWave));
         a = fmaxf(a, __shfl_xor(a, 2, kWave));
         int e = 0;
@@ -339,29 +303,54 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
         for (int i = 0; i < 16; ++i) {
             d1[i] = 0;
             d0[i] = 0;
-            if (a != 0.0f) digits15(q[i], 14 - e, d1[i], d0[i]);
+            if (a != 0.0f) digits15(x[i], 14 - e, d1[i], d0[i]);
         }
         int8_t* p0 = qd + (static_cast<uint64_t>(h) * 2u * tp + t) * 64u + c16;
         store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
         if ((tid & 3) == 0) qe[static_cast<uint64_t>(h) * tp + t] = a != 0.0f ? e - 14 : 0;
+        return;
+    }
+    if (part == 2) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tile[hi4][c16 + i] = x[i];
+    }
+    // Head maximum of |k| (part 1) or column maxima of |v| (part 2) from the
+    // partials: wave w folds row tiles w, w + 4, ...; lane = feature. The
+    // first 16 row tiles are loaded at once (indices clamped: a repeated row
+    // leaves a maximum unchanged), further ones in a loop.
+    {
+        const uint32_t f = static_cast<uint32_t>(tid & 63);
+        const float* cols = col_absmax + (part - 1u) * D + h * 64u + f;
+        float pm[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = min(static_cast<uint32_t>(tid >> 6) + 4u * i, partial_rows - 1u);
+            pm[i] = cols[static_cast<uint64_t>(r) * 2u * D];
+        }
+        float m = fmaxf(fmaxf(pm[0], pm[1]), fmaxf(pm[2], pm[3]));
+        for (uint32_t r = static_cast<uint32_t>(tid >> 6) + 16u; r < partial_rows; r += 4u)
+            m = fmaxf(m, cols[static_cast<uint64_t>(r) * 2u * D]);
+        if (part == 1) m = wave_max(m);
+        red[tid >> 6][f] = m;
     }
     __syncthreads();
-    {  // k: one exponent per head
-        const float a = fmaxf(fmaxf(kred[0], kred[1]), fmaxf(kred[2], kred[3]));
+    if (part == 1) {  // k: one exponent per head
+        const float a = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
         int e = 0;
         if (a != 0.0f) frexpf(a, &e);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             d1[i] = 0;
             d0[i] = 0;
-            if (a != 0.0f) digits15(k[i], 14 - e, d1[i], d0[i]);
+            if (a != 0.0f) digits15(x[i], 14 - e, d1[i], d0[i]);
         }
         int8_t* p0 = kd + (static_cast<uint64_t>(h) * 2u * tp + t) * 64u + c16;
         store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
         if (blockIdx.x == 0 && tid == 0) ke[h] = a != 0.0f ? e - 14 : 0;
+        return;
     }
     {  // v: feature hi4, block positions c16..c16+15
-        const float mv = fmaxf(fmaxf(vred[0][hi4], vred[1][hi4]), fmaxf(vred[2][hi4], vred[3][hi4]));
+        const float mv = fmaxf(fmaxf(red[0][hi4], red[1][hi4]), fmaxf(red[2][hi4], red[3][hi4]));
         int e = 0;
         if (mv != 0.0f) frexpf(mv, &e);
 #pragma unroll
@@ -726,8 +715,8 @@ int run_attention(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(tp / kBlock, heads, batch);
     if (col_absmax) {
-        hipLaunchKernelGGL(pack_qkv_kernel, grid, dim3(256), 0, s, qkv, col_absmax, partial_rows, qd, kd, vd, qe, ke,
-                           ve, tokens, heads, tp);
+        hipLaunchKernelGGL(pack_qkv_kernel, dim3(tp / kBlock, heads, 3), dim3(256), 0, s, qkv, col_absmax,
+                           partial_rows, qd, kd, vd, qe, ke, ve, tokens, heads, tp);
     } else {
         hipLaunchKernelGGL(pack_q_kernel, grid, dim3(256), 0, s, qkv, qd, qe, kmax, vmax, tokens, heads, tp);
         hipLaunchKernelGGL(pack_kv_kernel, grid, dim3(256), 0, s, qkv, kmax, vmax, kd, vd, ke, ve, tokens, heads, tp);
