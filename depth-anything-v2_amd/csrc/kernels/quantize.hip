@@ -20,37 +20,50 @@ constexpr int kRowsPerBlock = 4;
 
 // ---------------------------------------------------------------------------
 // Per-row quantization, quantize_rows_int8_fused.glsl:20-55. q = rne(clamp(x / s)).
-// Lane l owns float4 chunks at columns 4l + 256j; CH = chunks kept in VGPRs.
-template <int CH>
+// WPR waves share a row (kRowsPerBlock / WPR rows per workgroup): wave part
+// p owns float4 chunks p*64*CH + lane + 64j (j < CH) kept in VGPRs; the row
+// maximum is the maximum of the parts' maxima (exact, order-free).
+template <int CH, int WPR>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_kernel(
     const float* __restrict__ input, uint64_t input_offset, uint32_t rows,
     uint32_t columns, int8_t* __restrict__ q, uint32_t ldq,
     float* __restrict__ scales) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const float* x = input + input_offset + static_cast<uint64_t>(row) * columns;
-    const uint32_t words = columns >> 2;
+    static_assert(kRowsPerBlock % WPR == 0, "waves per row");
+    __shared__ float part_max[kRowsPerBlock];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t row = blockIdx.x * (kRowsPerBlock / WPR) + wave / WPR, part = wave % WPR;
+    const bool live = row < rows;
+    const float* x = input + input_offset + static_cast<uint64_t>(live ? row : 0u) * columns;
+    const uint32_t words = columns >> 2, w0 = part * 64u * CH;
     float4 v[CH];
     float absmax = 0.0f;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-        const uint32_t w = lane + 64u * j;
-        v[j] = w < words ? *reinterpret_cast<const float4*>(x + 4u * w) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const uint32_t w = w0 + lane + 64u * j;
+        v[j] = live && w < words ? *reinterpret_cast<const float4*>(x + 4u * w) : make_float4(0.f, 0.f, 0.f, 0.f);
         absmax = fmaxf(absmax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
     }
     absmax = wave_max(absmax);
+    if (WPR > 1) {
+        if (lane == 0) part_max[wave] = absmax;
+        __syncthreads();
+        const uint32_t first = wave - part;
+#pragma unroll
+        for (int i = 0; i < WPR; ++i) absmax = fmaxf(absmax, part_max[first + i]);
+    }
+    if (!live) return;
     const float s = row_scale(absmax);
-    if (lane == 0) scales[row] = s;
+    if (lane == 0 && part == 0) scales[row] = s;
     uint32_t* out = reinterpret_cast<uint32_t*>(q + static_cast<uint64_t>(row) * ldq);
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-        const uint32_t w = lane + 64u * j;
+        const uint32_t w = w0 + lane + 64u * j;
         if (w < words)
             out[w] = pack4(quantize_rne(v[j].x / s), quantize_rne(v[j].y / s),
                            quantize_rne(v[j].z / s), quantize_rne(v[j].w / s));
     }
-    for (uint32_t w = words + lane; w < (ldq >> 2); w += 64u) out[w] = 0u;
+    if (part == 0)
+        for (uint32_t w = words + lane; w < (ldq >> 2); w += 64u) out[w] = 0u;
 }
 
 // Rows too long to hold in registers: read twice.
@@ -509,14 +522,15 @@ int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset, uint32_
     hipStream_t s = static_cast<hipStream_t>(stream);
     const unsigned grid = ceil_div(rows, kRowsPerBlock);
     const uint32_t ch = (columns / 4u + 63u) / 64u;
-#define DAV2_QR_CASE(N)                                                                         \
-    hipLaunchKernelGGL(quantize_rows_kernel<N>, dim3(grid), dim3(64 * kRowsPerBlock), 0, s, input, \
-                       input_offset, rows, columns, q, ldq, scales)
-    if (ch <= 1) DAV2_QR_CASE(1);
-    else if (ch <= 2) DAV2_QR_CASE(2);
-    else if (ch <= 4) DAV2_QR_CASE(4);
-    else if (ch <= 8) DAV2_QR_CASE(8);
-    else if (ch <= 16) DAV2_QR_CASE(16);
+    // Long rows are split over several waves (more loads in flight per row).
+#define DAV2_QR_CASE(N, W)                                                                                         \
+    hipLaunchKernelGGL((quantize_rows_kernel<N, W>), dim3(ceil_div(rows, kRowsPerBlock / W)), dim3(64 * kRowsPerBlock), \
+                       0, s, input, input_offset, rows, columns, q, ldq, scales)
+    if (ch <= 1) DAV2_QR_CASE(1, 1);
+    else if (ch <= 2) DAV2_QR_CASE(2, 1);
+    else if (ch <= 4) DAV2_QR_CASE(4, 1);
+    else if (ch <= 8) DAV2_QR_CASE(4, 2);
+    else if (ch <= 16) DAV2_QR_CASE(4, 4);
     else
         hipLaunchKernelGGL(quantize_rows_long_kernel, dim3(grid), dim3(64 * kRowsPerBlock), 0, s,
                            input, input_offset, rows, columns, q, ldq, scales);
