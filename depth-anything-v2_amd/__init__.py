@@ -168,6 +168,9 @@ PROTOTYPES = {
     "dav2_hip_minmax_partials": (u32, [u64]),
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),
     "dav2_hip_normalize_relative": (C.c_int, [vp, vp, u64, vp]),
+    "dav2_hip_preprocess_bgr8": (C.c_int, [vp, u32, u32, u64, u32, u32, vp, vp]),
+    "dav2_hip_preprocess_bgra8_nearest": (C.c_int, [vp, u32, u32, u64, u32, u32, vp, vp]),
+    "dav2_hip_normalize_span": (C.c_int, [vp, vp, u64, vp, vp]),
     "dav2_hip_position_bicubic": (C.c_int, [vp, vp, u32, u32, u32, vp]),
     "dav2_hip_finish_tokens": (C.c_int, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
     "dav2_hip_error_string": (C.c_char_p, [C.c_int]),
@@ -257,6 +260,35 @@ class Context:
         check(self.lib.dav2_infer_tensor_f32(self.handle, x.ctypes.data, width, height, out.ctypes.data, out.size),
               self.lib)
         return out.reshape(height, width)
+
+    def infer_bgr8(self, image, input_size: int = 518):
+        """image: uint8 [H][W][3] BGR (cv2.imread order); returns float32 [H][W] depth."""
+        import numpy as np
+        img = np.ascontiguousarray(image, dtype=np.uint8)
+        height, width = img.shape[0], img.shape[1]
+        return self.infer_bgr8_rows(img, width, height, width * 3, input_size)
+
+    def infer_bgr8_rows(self, buf, width: int, height: int, stride: int, input_size: int = 518):
+        """buf: uint8 buffer of `height` rows, `stride` bytes apart, 3 bytes per pixel."""
+        import numpy as np
+        buf = np.ascontiguousarray(buf, dtype=np.uint8)
+        out = np.empty(max(width, 0) * max(height, 0), dtype=np.float32)
+        check(self.lib.dav2_infer_bgr8(self.handle, buf.ctypes.data, width, height, stride, input_size,
+                                       out.ctypes.data, out.size), self.lib)
+        return out.reshape(height, width)
+
+    def inferbridge_bgra8(self, image, input_size: int = 518):
+        """image: uint8 [H][W][4] BGRA; returns float32 min/max-normalised depth
+        at the transposed network shape (dav2_get_inferbridge_shape)."""
+        import numpy as np
+        img = np.ascontiguousarray(image, dtype=np.uint8)
+        height, width = img.shape[0], img.shape[1]
+        shape = ImageShape()
+        check(self.lib.dav2_get_inferbridge_shape(width, height, input_size, C.byref(shape)), self.lib)
+        out = np.empty(shape.width * shape.height, dtype=np.float32)
+        check(self.lib.dav2_inferbridge_bgra8_f32(self.handle, img.ctypes.data, width, height, width * 4, input_size,
+                                                  out.ctypes.data, out.size), self.lib)
+        return out.reshape(shape.height, shape.width)
 
     def profile(self, enable: bool) -> None:
         check(self.lib.dav2_profile_enable(self.handle, int(enable)), self.lib)

@@ -287,23 +287,48 @@ dav2_status DAV2_CALL dav2_gpu_texture_output_acquire(dav2_gpu_job* job, uint32_
 
 void DAV2_CALL dav2_gpu_output_release(dav2_gpu_output_lease*) {}
 
-// ---- host-image paths: not part of this build (next after the hot path) ----
+// ---- host-image paths -------------------------------------------------------
+// src/dav2.cpp:630-665: network_shape, BGR8 cubic preprocessing, inference,
+// bilinear resize of the raw depth back to the image; here the
+// preprocessing and the resize run on the device.
 dav2_status DAV2_CALL dav2_infer_bgr8(dav2_context* context, const uint8_t* bgr, int32_t image_width,
-                                     int32_t image_height, ptrdiff_t, int32_t, float* output_depth,
-                                     size_t output_count) {
+                                     int32_t image_height, ptrdiff_t row_stride_bytes, int32_t input_size,
+                                     float* output_depth, size_t output_count) {
     if (context == nullptr || bgr == nullptr || output_depth == nullptr)
         return fail(DAV2_STATUS_INVALID_ARGUMENT, "null inference argument");
     const size_t required =
         image_width > 0 && image_height > 0 ? static_cast<size_t>(image_width) * static_cast<size_t>(image_height) : 0;
     if (output_count < required) return fail(DAV2_STATUS_BUFFER_TOO_SMALL, "output buffer is too small");
-    return fail(DAV2_STATUS_UNSUPPORTED, "BGR8 image preprocessing is not part of this build");
+    return protect([&] {
+        const dav2_image_shape shape = network_shape(image_width, image_height, input_size);
+        // image.cpp:171-175
+        if (row_stride_bytes < static_cast<ptrdiff_t>(image_width) * 3)
+            throw std::invalid_argument("invalid source image");
+        context->executor->infer_bgr8(bgr, image_width, image_height, static_cast<size_t>(row_stride_bytes),
+                                      shape.width, shape.height, output_depth);
+    });
 }
 
-dav2_status DAV2_CALL dav2_inferbridge_bgra8_f32(dav2_context* context, const uint8_t* bgra, int32_t, int32_t,
-                                                ptrdiff_t, int32_t, float* output_depth, size_t) {
+// src/dav2.cpp:754-802: the InferBridge contract -- BGRA bytes kept in BGR
+// order as model channels, nearest resize to the transposed network shape,
+// depth min/max normalised at that size. (Metric models, which take a fixed
+// 25 m span there, are refused at dav2_create by this build.)
+dav2_status DAV2_CALL dav2_inferbridge_bgra8_f32(dav2_context* context, const uint8_t* bgra, int32_t image_width,
+                                                int32_t image_height, ptrdiff_t row_stride_bytes, int32_t input_size,
+                                                float* output_depth, size_t output_count) {
     if (context == nullptr || bgra == nullptr || output_depth == nullptr)
         return fail(DAV2_STATUS_INVALID_ARGUMENT, "null inference argument");
-    return fail(DAV2_STATUS_UNSUPPORTED, "the InferBridge BGRA path is not part of this build");
+    return protect([&] {
+        const dav2_image_shape upstream = network_shape(image_width, image_height, input_size);
+        const int out_w = upstream.height, out_h = upstream.width;
+        const size_t required = static_cast<size_t>(out_w) * out_h;
+        if (output_count < required) throw ApiError(DAV2_STATUS_BUFFER_TOO_SMALL, "output buffer is too small");
+        // image.cpp:296-300
+        if (row_stride_bytes < static_cast<ptrdiff_t>(image_width) * 4)
+            throw std::invalid_argument("invalid InferBridge source image");
+        context->executor->infer_bgra8_normalized(bgra, image_width, image_height,
+                                                  static_cast<size_t>(row_stride_bytes), out_w, out_h, output_depth);
+    });
 }
 
 // ---- the hot path ------------------------------------------------------------

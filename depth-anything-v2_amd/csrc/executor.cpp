@@ -167,4 +167,63 @@ void HipExecutor::normalize_relative_device(float* depth, std::uint64_t count, h
     operators_.normalize_relative(d, range, static_cast<std::uint32_t>(count));
 }
 
+void HipExecutor::infer_bgr8(const std::uint8_t* bgr, int width, int height, std::size_t stride, int network_width,
+                             int network_height, float* output) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    context_.make_current();
+    ScopedStream scoped(context_, nullptr);
+    const std::uint64_t row_bytes = std::uint64_t(width) * 3;
+    const std::uint64_t net = std::uint64_t(network_width) * network_height;
+    const std::uint64_t pixels = std::uint64_t(width) * height;
+    DeviceBuffer& image = arena_.get("io.bgr8", row_bytes * height);
+    DeviceBuffer& in = arena_.get("io.input", net * 3 * sizeof(float));
+    DeviceBuffer& depth = arena_.get("io.output", net * sizeof(float));
+    context_.upload_rows(image, bgr, stride, row_bytes, static_cast<std::size_t>(height));
+    hip_check(dav2_hip_preprocess_bgr8(image.as<std::uint8_t>(), static_cast<std::uint32_t>(width),
+                                       static_cast<std::uint32_t>(height), row_bytes,
+                                       static_cast<std::uint32_t>(network_width),
+                                       static_cast<std::uint32_t>(network_height), in.as<float>(),
+                                       context_.active_stream()),
+              "preprocess_bgr8");
+    run_graph(in.as<float>(), 1, network_width, network_height, depth.as<float>(), nullptr);
+    if (network_width == width && network_height == height) {
+        context_.download(depth, output, pixels * sizeof(float));
+        return;
+    }
+    // vulkan_executor.cpp:586-598: bilinear (align corners) back to the image
+    DeviceBuffer& resized = arena_.get("io.resized", pixels * sizeof(float));
+    operators_.bilinear_align_true(resized, depth, static_cast<std::uint32_t>(network_width),
+                                   static_cast<std::uint32_t>(network_height), static_cast<std::uint32_t>(width),
+                                   static_cast<std::uint32_t>(height), 1);
+    context_.download(resized, output, pixels * sizeof(float));
+}
+
+void HipExecutor::infer_bgra8_normalized(const std::uint8_t* bgra, int width, int height, std::size_t stride,
+                                         int network_width, int network_height, float* output) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    context_.make_current();
+    ScopedStream scoped(context_, nullptr);
+    const std::uint64_t row_bytes = std::uint64_t(width) * 4;
+    const std::uint64_t net = std::uint64_t(network_width) * network_height;
+    if (net > 0xffffffffull) throw std::invalid_argument("network size too large");
+    DeviceBuffer& image = arena_.get("io.bgra8", row_bytes * height);
+    DeviceBuffer& in = arena_.get("io.input", net * 3 * sizeof(float));
+    DeviceBuffer& depth = arena_.get("io.output", net * sizeof(float));
+    DeviceBuffer& normalized = arena_.get("io.normalized", net * sizeof(float));
+    DeviceBuffer& range = arena_.get("io.range", 2 * sizeof(float));
+    context_.upload_rows(image, bgra, stride, row_bytes, static_cast<std::size_t>(height));
+    hip_check(dav2_hip_preprocess_bgra8_nearest(image.as<std::uint8_t>(), static_cast<std::uint32_t>(width),
+                                                static_cast<std::uint32_t>(height), row_bytes,
+                                                static_cast<std::uint32_t>(network_width),
+                                                static_cast<std::uint32_t>(network_height), in.as<float>(),
+                                                context_.active_stream()),
+              "preprocess_bgra8_nearest");
+    run_graph(in.as<float>(), 1, network_width, network_height, depth.as<float>(), nullptr);
+    operators_.reduce_minmax(depth, range, static_cast<std::uint32_t>(net));
+    hip_check(dav2_hip_normalize_span(depth.as<float>(), range.as<float>(), net, normalized.as<float>(),
+                                      context_.active_stream()),
+              "normalize_span");
+    context_.download(normalized, output, net * sizeof(float));
+}
+
 }  // namespace dav2

@@ -22,6 +22,16 @@ public:
     void infer_device(const float* input, int batch, int width, int height, float* output, hipStream_t stream,
                       float* pre_relu = nullptr);
     void normalize_relative_device(float* depth, std::uint64_t count, hipStream_t stream);
+    // Host image paths (src/dav2.cpp:630-665, :754-802), preprocessing and
+    // post-processing on the device. bgr8: interleaved BGR rows, inference at
+    // network_width x network_height, raw depth resized back to the image
+    // (bilinear, align corners) into output [height][width]. bgra8: BGRA rows,
+    // nearest resize to network_width x network_height, output min/max
+    // normalised at the network size.
+    void infer_bgr8(const std::uint8_t* bgr, int width, int height, std::size_t stride, int network_width,
+                    int network_height, float* output);
+    void infer_bgra8_normalized(const std::uint8_t* bgra, int width, int height, std::size_t stride,
+                                int network_width, int network_height, float* output);
 
     dav2_encoder encoder() const { return encoder_; }
     float metric_max_depth() const { return model_.derivation().metric_max_depth; }

@@ -243,6 +243,25 @@ DAV2_API int dav2_hip_reduce_minmax(const float* input, uint64_t count, float* r
 DAV2_API int dav2_hip_normalize_relative(float* depth, const float* range, uint64_t count,
                                          void* stream);
 
+/* Host-image paths (the reference runs them on the CPU around the tensor
+ * inference; here they run on the device buffers of the image).
+ * preprocess_bgr8: src/image.cpp:163-270 (dav2::preprocess_bgr8) -- bgr is
+ *   height rows of `stride` bytes, 3 bytes (B, G, R) per pixel; out is the
+ *   normalised RGB CHW float32 [3][dst_height][dst_width] of the cubic resize.
+ * preprocess_bgra8_nearest: src/image.cpp:289-339
+ *   (dav2::preprocess_inferbridge_bgra8) -- 4 bytes per pixel, stride and base
+ *   4-byte aligned; model channel c is byte c of the pixel.
+ * normalize_span: src/dav2.cpp:787-800 -- out = (depth - range[0]) /
+ *   (range[1] - range[0]), or 0 everywhere when that span is not positive;
+ *   range from dav2_hip_reduce_minmax. */
+DAV2_API int dav2_hip_preprocess_bgr8(const uint8_t* bgr, uint32_t width, uint32_t height, uint64_t stride,
+                                      uint32_t dst_width, uint32_t dst_height, float* out, void* stream);
+DAV2_API int dav2_hip_preprocess_bgra8_nearest(const uint8_t* bgra, uint32_t width, uint32_t height,
+                                               uint64_t stride, uint32_t dst_width, uint32_t dst_height,
+                                               float* out, void* stream);
+DAV2_API int dav2_hip_normalize_span(const float* depth, const float* range, uint64_t count, float* out,
+                                     void* stream);
+
 /* position_bicubic.glsl:76-105 with the set-up of src/operators.cpp:1323-1376:
  * position is the [1370][D] pos_embed, out is CHW [D][ph][pw]. */
 DAV2_API int dav2_hip_position_bicubic(float* out, const float* position,

@@ -753,6 +753,118 @@ void orc_normalize_relative(float* depth, const float* range, uint64_t count) {
         depth[i] = span > 1.0e-12f ? std::min(std::max((depth[i] - minimum) / span, 0.0f), 1.0f) : 0.0f;
 }
 
+int orc_network_shape(int width, int height, int input_size, int* out_width, int* out_height) {
+    // image.cpp:138-161: scale the shorter side up to input_size, round each
+    // side to a multiple of 14 with ties to even (numpy.round), keep at least
+    // input_size, then round up to a multiple of 14.
+    if (width <= 0 || height <= 0 || input_size <= 0) return 1;
+    const double scale = std::max(static_cast<double>(input_size) / height, static_cast<double>(input_size) / width);
+    auto to14 = [](double v) { return static_cast<int>(std::nearbyint(v / 14)) * 14; };
+    int h = std::max(to14(scale * height), input_size);
+    int w = std::max(to14(scale * width), input_size);
+    h = (h + 13) / 14 * 14;
+    w = (w + 13) / 14 * 14;
+    *out_width = w;
+    *out_height = h;
+    return 0;
+}
+
+namespace {
+// image.cpp:20-39: OpenCV's interpolateCubic (A = -0.75) in float32, in the
+// shader-independent order written there; c[3] closes the partition of unity.
+void opencv_cubic(float x, float c[4]) {
+    const float a = -0.75f;
+    const float x1 = x + 1.0f, o = 1.0f - x;
+    c[0] = ((a * x1 - 5.0f * a) * x1 + 8.0f * a) * x1 - 4.0f * a;
+    c[1] = ((a + 2.0f) * x - (a + 3.0f)) * x * x + 1.0f;
+    c[2] = ((a + 2.0f) * o - (a + 3.0f)) * o * o + 1.0f;
+    c[3] = 1.0f - c[0] - c[1] - c[2];
+}
+
+// Source sample position of destination index d (half-pixel centres,
+// image.cpp:187-196 / :238-241): float32 coordinate, floor index, weights.
+void cubic_tap(int d, double scale, int* base, float c[4]) {
+    const float coord = static_cast<float>((d + 0.5) * scale - 0.5);
+    *base = static_cast<int>(std::floor(coord));
+    opencv_cubic(coord - static_cast<float>(*base), c);
+}
+}  // namespace
+
+void orc_preprocess_bgr8(const uint8_t* bgr, int width, int height, int64_t stride, int dst_width, int dst_height,
+                         float* out) {
+    // image.cpp:163-270. Horizontal pass per source row into float64
+    // [height][dst_width][3] (RGB order; tap sum from 0.0 in tap order), then
+    // the vertical pass ((h0 b0 + h1 b1) + h2 b2) + h3 b3 and
+    // float((v - mean) / std) in float64. Taps clamp to the image edge.
+    const double sx = static_cast<double>(width) / dst_width, sy = static_cast<double>(height) / dst_height;
+    std::vector<double> rows(static_cast<size_t>(height) * dst_width * 3);
+    const double mean[3] = {0.485, 0.456, 0.406}, stddev[3] = {0.229, 0.224, 0.225};
+#pragma omp parallel for schedule(static)
+    for (int64_t y = 0; y < height; ++y) {
+        const uint8_t* src = bgr + y * stride;
+        for (int dx = 0; dx < dst_width; ++dx) {
+            int base;
+            float c[4];
+            cubic_tap(dx, sx, &base, c);
+            for (int ch = 0; ch < 3; ++ch) {
+                double acc = 0.0;
+                for (int t = 0; t < 4; ++t) {
+                    const int x = std::min(std::max(base - 1 + t, 0), width - 1);
+                    acc += static_cast<double>(src[3 * x + (2 - ch)]) / 255.0 * c[t];
+                }
+                rows[(static_cast<size_t>(y) * dst_width + dx) * 3 + ch] = acc;
+            }
+        }
+    }
+    const size_t plane = static_cast<size_t>(dst_width) * dst_height;
+#pragma omp parallel for schedule(static)
+    for (int64_t dy = 0; dy < dst_height; ++dy) {
+        int base;
+        float c[4];
+        cubic_tap(static_cast<int>(dy), sy, &base, c);
+        int ys[4];
+        for (int t = 0; t < 4; ++t) ys[t] = std::min(std::max(base - 1 + t, 0), height - 1);
+        for (int dx = 0; dx < dst_width; ++dx)
+            for (int ch = 0; ch < 3; ++ch) {
+                auto h = [&](int t) { return rows[(static_cast<size_t>(ys[t]) * dst_width + dx) * 3 + ch]; };
+                const double v = h(0) * c[0] + h(1) * c[1] + h(2) * c[2] + h(3) * c[3];
+                out[ch * plane + static_cast<size_t>(dy) * dst_width + dx] =
+                    static_cast<float>((v - mean[ch]) / stddev[ch]);
+            }
+    }
+}
+
+void orc_preprocess_bgra8_nearest(const uint8_t* bgra, int width, int height, int64_t stride, int dst_width,
+                                  int dst_height, float* out) {
+    // image.cpp:289-339: float32 scale, floor(d * scale) clamped to the
+    // last pixel, byte c of the pixel is model channel c (B, G, R).
+    const float sx = static_cast<float>(width) / dst_width, sy = static_cast<float>(height) / dst_height;
+    const float mean[3] = {0.485f, 0.456f, 0.406f}, stddev[3] = {0.229f, 0.224f, 0.225f};
+    const size_t plane = static_cast<size_t>(dst_width) * dst_height;
+    for (int dy = 0; dy < dst_height; ++dy) {
+        const int y = std::min(static_cast<int>(std::floor(dy * sy)), height - 1);
+        for (int dx = 0; dx < dst_width; ++dx) {
+            const int x = std::min(static_cast<int>(std::floor(dx * sx)), width - 1);
+            const uint8_t* px = bgra + y * stride + 4 * static_cast<int64_t>(x);
+            for (int ch = 0; ch < 3; ++ch)
+                out[ch * plane + static_cast<size_t>(dy) * dst_width + dx] =
+                    (static_cast<float>(px[ch]) / 255.0f - mean[ch]) / stddev[ch];
+        }
+    }
+}
+
+void orc_normalize_span(const float* depth, uint64_t count, float* out) {
+    // dav2.cpp:787-800 (relative models): min and max over the map.
+    if (count == 0) return;
+    float mn = depth[0], mx = depth[0];
+    for (uint64_t i = 1; i < count; ++i) {
+        mn = std::min(mn, depth[i]);
+        mx = std::max(mx, depth[i]);
+    }
+    const float span = mx - mn;
+    for (uint64_t i = 0; i < count; ++i) out[i] = span > 0.0f ? (depth[i] - mn) / span : 0.0f;
+}
+
 static inline void cubic_coeffs(float t, float c[4]) {
     // position_bicubic.glsl:39-56 (A = -0.75)
     const float a = -0.75f;

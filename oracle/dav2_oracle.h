@@ -134,6 +134,25 @@ int orc_model_infer(orc_model* model, const float* chw, uint32_t width,
 int orc_model_encoder_blocks(orc_model* model, float* tokens, uint32_t tokens_count,
                              uint32_t first, uint32_t last, int fp16_attention);
 
+/* Host image paths (src/image.cpp, src/dav2.cpp:630-665, :754-802).
+ * network_shape: image.cpp:138-161; returns 0, or 1 for a non-positive size.
+ * preprocess_bgr8: image.cpp:163-270 -- interleaved BGR bytes (row stride in
+ *   bytes) -> normalised RGB CHW float32 [3][dh][dw], separable cubic resize
+ *   with float32 coefficients and float64 intermediates.
+ * preprocess_bgra8_nearest: image.cpp:289-339 -- BGRA bytes kept in BGR
+ *   channel order, floor-nearest resize, float32 normalisation.
+ * normalize_span: dav2.cpp:787-800 -- (x - min) / (max - min), all zero when
+ *   the span is not positive. */
+int orc_network_shape(int width, int height, int input_size, int* out_width,
+                      int* out_height);
+void orc_preprocess_bgr8(const uint8_t* bgr, int width, int height,
+                         int64_t stride, int dst_width, int dst_height,
+                         float* out);
+void orc_preprocess_bgra8_nearest(const uint8_t* bgra, int width, int height,
+                                  int64_t stride, int dst_width,
+                                  int dst_height, float* out);
+void orc_normalize_span(const float* depth, uint64_t count, float* out);
+
 /* IEEE binary16 round-to-nearest-even helpers used by the fp16 attention path. */
 uint16_t orc_float_to_half(float value);
 float orc_half_to_float(uint16_t value);

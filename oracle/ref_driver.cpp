@@ -1,5 +1,6 @@
 // Test-only C shim over reference sources that compile on their own
-// (src/model.cpp: .dav2 loader and validation; src/image.cpp: network_shape).
+// (src/model.cpp: .dav2 loader and validation; src/image.cpp: network_shape
+// and the two host image preprocessors).
 // Built by `make -C oracle ref` straight from the reference tree into
 // oracle/_ref/; used by tests to check this build's .dav2 writer, loader
 // verdicts and network-shape rule against the reference implementation.
@@ -10,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <vector>
 
 extern "C" {
 
@@ -55,6 +57,36 @@ long long ref_model_tensor(const char* path, int encoder, const char* name, floa
         return static_cast<long long>(n);
     } catch (const std::exception&) {
         return -1;
+    }
+}
+
+// src/image.cpp:163-270 (reference's own BGR8 preprocessing). Returns 0 and
+// fills out [3][dst_height][dst_width], or 1 with the exception text.
+int ref_preprocess_bgr8(const unsigned char* bgr, int width, int height, long long stride, int dst_width,
+                        int dst_height, float* out, char* error, size_t error_bytes) {
+    try {
+        std::vector<float> chw;
+        dav2::preprocess_bgr8(bgr, width, height, static_cast<std::ptrdiff_t>(stride), {dst_width, dst_height}, chw);
+        std::memcpy(out, chw.data(), chw.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(error, error_bytes, "%s", e.what());
+        return 1;
+    }
+}
+
+// src/image.cpp:289-339 (InferBridge BGRA nearest preprocessing).
+int ref_preprocess_inferbridge_bgra8(const unsigned char* bgra, int width, int height, long long stride,
+                                     int dst_width, int dst_height, float* out, char* error, size_t error_bytes) {
+    try {
+        std::vector<float> chw;
+        dav2::preprocess_inferbridge_bgra8(bgra, width, height, static_cast<std::ptrdiff_t>(stride),
+                                           {dst_width, dst_height}, chw);
+        std::memcpy(out, chw.data(), chw.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(error, error_bytes, "%s", e.what());
+        return 1;
     }
 }
 

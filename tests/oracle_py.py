@@ -43,6 +43,10 @@ _PROTO = {
     "orc_model_free": (None, [vp]),
     "orc_model_infer": (C.c_int, [vp, vp, u32, u32, C.c_int, vp, vp, vp]),
     "orc_model_encoder_blocks": (C.c_int, [vp, vp, u32, u32, u32, C.c_int]),
+    "orc_network_shape": (C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "orc_preprocess_bgr8": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, vp]),
+    "orc_preprocess_bgra8_nearest": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, vp]),
+    "orc_normalize_span": (None, [vp, u64, vp]),
     "orc_float_to_half": (C.c_uint16, [f32]),
     "orc_half_to_float": (f32, [C.c_uint16]),
     "orc_crc32": (C.c_uint32, [vp, sz]),
@@ -216,6 +220,33 @@ class Oracle:
         r = _f32(r)
         self.lib.orc_normalize_relative(d.ctypes.data, r.ctypes.data, d.size)
         return d
+
+    def network_shape(self, width: int, height: int, input_size: int):
+        w, h = C.c_int(), C.c_int()
+        if self.lib.orc_network_shape(width, height, input_size, C.byref(w), C.byref(h)) != 0:
+            raise ValueError("image dimensions and input_size must be positive")
+        return w.value, h.value
+
+    def preprocess_bgr8(self, buf, width: int, height: int, stride: int, dst_width: int, dst_height: int):
+        buf = np.ascontiguousarray(buf, dtype=np.uint8)
+        assert buf.size >= (height - 1) * stride + 3 * width
+        out = np.empty((3, dst_height, dst_width), np.float32)
+        self.lib.orc_preprocess_bgr8(buf.ctypes.data, width, height, stride, dst_width, dst_height, out.ctypes.data)
+        return out
+
+    def preprocess_bgra8_nearest(self, buf, width: int, height: int, stride: int, dst_width: int, dst_height: int):
+        buf = np.ascontiguousarray(buf, dtype=np.uint8)
+        assert buf.size >= (height - 1) * stride + 4 * width
+        out = np.empty((3, dst_height, dst_width), np.float32)
+        self.lib.orc_preprocess_bgra8_nearest(buf.ctypes.data, width, height, stride, dst_width, dst_height,
+                                              out.ctypes.data)
+        return out
+
+    def normalize_span(self, d):
+        d = _f32(d)
+        out = np.empty_like(d)
+        self.lib.orc_normalize_span(d.ctypes.data, d.size, out.ctypes.data)
+        return out
 
     def position_bicubic(self, position, pw: int, ph: int, dim: int):
         position = _f32(position)

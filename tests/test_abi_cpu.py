@@ -112,6 +112,9 @@ def test_null_context_entry_points(pkg, lib):
     assert lib.dav2_infer_tensor_f32(None, x, 14, 14, x, 196) == 1
     assert lib.dav2_infer_tensor_f32_device(None, x, 1, 14, 14, x, 196, None) == 1
     assert lib.dav2_prepare(None, 1, 1, 1) == 1
+    img = (C.c_uint8 * 48)()
+    assert lib.dav2_infer_bgr8(None, img, 4, 4, 12, 518, x, 16) == 1
+    assert lib.dav2_inferbridge_bgra8_f32(None, img, 4, 4, 16, 518, x, 16) == 1
     assert lib.dav2_profile_enable(None, 1) == 1
     lib.dav2_destroy(None)  # safe (src/dav2.cpp:227-229)
     assert lib.dav2_gpu_job_cancel(None) == 1
