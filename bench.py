@@ -64,6 +64,25 @@ def cpu_baseline(model_path: Path, encoder: str, size: int, budget_s: float) -> 
         oracle.free_model(h)
 
 
+def cpu_preprocess_ms(width: int, height: int, input_size: int) -> float:
+    """The oracle's restatement of the reference's CPU BGR8 preprocessing
+    (src/image.cpp:163-270) on one frame, OpenMP over the host cores; the best
+    of three runs."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_py import Oracle
+
+    oracle = Oracle()
+    dw, dh = oracle.network_shape(width, height, input_size)
+    buf = np.random.default_rng(SEED + 5).integers(0, 256, size=width * height * 3, dtype=np.uint8)
+    best = float("inf")
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.preprocess_bgr8(buf, width, height, width * 3, dw, dh)
+        best = min(best, time.perf_counter() - t0)
+    return 1e3 * best
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,14 +152,59 @@ def main() -> int:
 
         # The host-buffer entry (dav2_infer_tensor_f32): PCIe copies included.
         host_rate = None
+        host_steps = min(args.steps, 10)
         if args.batch == 1:
             x_host = fmt.imagenet_input(args.size, args.size, SEED + 3)[0]
             ctx.infer(x_host, args.size, args.size)
             h0 = time.perf_counter()
-            host_steps = min(args.steps, 10)
             for _ in range(host_steps):
                 ctx.infer(x_host, args.size, args.size)
             host_rate = host_steps / (time.perf_counter() - h0)
+
+        # Host-image entries (dav2_infer_bgr8): a 518x518 BGR8 frame through
+        # the GPU preprocessing and the same inference, PCIe copies included;
+        # then the cubic preprocessing kernel alone on a 1920x1080 frame
+        # (resized to the 518 network shape, 924x518), timed with HIP events
+        # on the stream it runs on.
+        image_paths = None
+        if args.batch == 1:
+            import ctypes as C
+            lib = pkg.load()
+            rng = np.random.default_rng(SEED + 5)
+            bgr = rng.integers(0, 256, size=(args.size, args.size, 3), dtype=np.uint8)
+            ctx.infer_bgr8(bgr, args.size)
+            b0 = time.perf_counter()
+            for _ in range(host_steps):
+                ctx.infer_bgr8(bgr, args.size)
+            bgr_rate = host_steps / (time.perf_counter() - b0)
+            fw, fh = 1920, 1080
+            shape = pkg.ImageShape()
+            pkg.check(lib.dav2_get_network_shape(fw, fh, 518, C.byref(shape)), lib)
+            frame = torch.from_numpy(rng.integers(0, 256, size=fh * fw * 3, dtype=np.uint8)).cuda()
+            pre = torch.empty(3 * shape.width * shape.height, dtype=torch.float32, device="cuda")
+
+            def preprocess():
+                pkg.check(lib.dav2_hip_preprocess_bgr8(frame.data_ptr(), fw, fh, fw * 3, shape.width, shape.height,
+                                                       pre.data_ptr(), stream), lib)
+
+            for _ in range(3):
+                preprocess()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 50
+            e0.record()
+            for _ in range(reps):
+                preprocess()
+            e1.record()
+            torch.cuda.synchronize()
+            pre_us = 1e3 * e0.elapsed_time(e1) / reps
+            pre_bytes = fw * fh * 3 + 3 * shape.width * shape.height * 4
+            image_paths = {
+                "bgr8_entry_images_per_s": bgr_rate,
+                "bgr8_entry": f"dav2_infer_bgr8, {args.size}x{args.size} BGR8 host frame, input_size {args.size}",
+                "preprocess_bgr8": {"frame": f"{fw}x{fh} BGR8 -> {shape.width}x{shape.height} RGB CHW",
+                                    "avg_us": pre_us, "bytes": pre_bytes,
+                                    "GB/s": pre_bytes / (pre_us * 1e-6) / 1e9,
+                                    "frac_hbm": pre_bytes / (pre_us * 1e-6) / 1e9 / PEAK_HBM_GBS}}
 
         # Second pass with per-launch HIP events for the kernel rooflines.
         ctx.profile(True)
@@ -184,6 +248,8 @@ def main() -> int:
         cpu = None
         if not args.no_cpu_baseline:
             cpu = cpu_baseline(model, args.encoder, args.size, args.cpu_budget)
+            if image_paths is not None:
+                cpu["preprocess_bgr8_1080p_ms"] = cpu_preprocess_ms(1920, 1080, 518)
 
     ms = 1e3 * elapsed / args.steps
     result = {
@@ -212,6 +278,7 @@ def main() -> int:
         "kernels": {k: kernels[k] for k in list(kernels)[:8]},
         "profiled_ms_per_step": 1e3 * profiled_elapsed / args.steps,
         "host_entry_images_per_s": host_rate,
+        "image_paths": image_paths,
         "depth_finite": bool(np.isfinite(depth).all()),
         "cpu_baseline": cpu,
     }

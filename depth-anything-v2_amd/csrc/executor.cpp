@@ -3,6 +3,7 @@
 #include "dav2_hip.h"
 
 #include <cstdlib>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 
@@ -167,6 +168,29 @@ void HipExecutor::normalize_relative_device(float* depth, std::uint64_t count, h
     operators_.normalize_relative(d, range, static_cast<std::uint32_t>(count));
 }
 
+std::size_t HipExecutor::upload_image(const char* slot, const std::uint8_t* image, std::size_t row_bytes,
+                                      int height, std::size_t stride, bool keep_stride, DeviceBuffer*& device) {
+    // One host-to-device copy either way (a pitched copy from pageable memory
+    // goes row by row): the rows with their padding when it is small, else
+    // the rows packed on the host first.
+    const std::size_t rows = static_cast<std::size_t>(height);
+    const std::size_t span = (rows - 1) * stride + row_bytes, packed = rows * row_bytes;
+    if (keep_stride && span <= packed + packed / 4) {
+        device = &arena_.get(slot, span);
+        context_.upload(*device, image, span);
+        return stride;
+    }
+    image_stage_.resize(packed);
+    for (std::size_t r = 0; r < rows; ++r)
+        std::memcpy(image_stage_.data() + r * row_bytes, image + r * stride, row_bytes);
+    device = &arena_.get(slot, packed);
+    context_.upload(*device, image_stage_.data(), packed);
+    // the copy reads the staging rows asynchronously: wait before they can
+    // be reused by the next call
+    context_.synchronize();
+    return row_bytes;
+}
+
 void HipExecutor::infer_bgr8(const std::uint8_t* bgr, int width, int height, std::size_t stride, int network_width,
                              int network_height, float* output) {
     std::lock_guard<std::mutex> lock(mutex_);
@@ -175,12 +199,12 @@ void HipExecutor::infer_bgr8(const std::uint8_t* bgr, int width, int height, std
     const std::uint64_t row_bytes = std::uint64_t(width) * 3;
     const std::uint64_t net = std::uint64_t(network_width) * network_height;
     const std::uint64_t pixels = std::uint64_t(width) * height;
-    DeviceBuffer& image = arena_.get("io.bgr8", row_bytes * height);
+    DeviceBuffer* image = nullptr;
+    const std::size_t device_stride = upload_image("io.bgr8", bgr, row_bytes, height, stride, true, image);
     DeviceBuffer& in = arena_.get("io.input", net * 3 * sizeof(float));
     DeviceBuffer& depth = arena_.get("io.output", net * sizeof(float));
-    context_.upload_rows(image, bgr, stride, row_bytes, static_cast<std::size_t>(height));
-    hip_check(dav2_hip_preprocess_bgr8(image.as<std::uint8_t>(), static_cast<std::uint32_t>(width),
-                                       static_cast<std::uint32_t>(height), row_bytes,
+    hip_check(dav2_hip_preprocess_bgr8(image->as<std::uint8_t>(), static_cast<std::uint32_t>(width),
+                                       static_cast<std::uint32_t>(height), device_stride,
                                        static_cast<std::uint32_t>(network_width),
                                        static_cast<std::uint32_t>(network_height), in.as<float>(),
                                        context_.active_stream()),
@@ -206,14 +230,15 @@ void HipExecutor::infer_bgra8_normalized(const std::uint8_t* bgra, int width, in
     const std::uint64_t row_bytes = std::uint64_t(width) * 4;
     const std::uint64_t net = std::uint64_t(network_width) * network_height;
     if (net > 0xffffffffull) throw std::invalid_argument("network size too large");
-    DeviceBuffer& image = arena_.get("io.bgra8", row_bytes * height);
+    // the kernel reads whole pixels: a stride that is not a multiple of 4 is packed
+    DeviceBuffer* image = nullptr;
+    const std::size_t device_stride = upload_image("io.bgra8", bgra, row_bytes, height, stride, stride % 4 == 0, image);
     DeviceBuffer& in = arena_.get("io.input", net * 3 * sizeof(float));
     DeviceBuffer& depth = arena_.get("io.output", net * sizeof(float));
     DeviceBuffer& normalized = arena_.get("io.normalized", net * sizeof(float));
     DeviceBuffer& range = arena_.get("io.range", 2 * sizeof(float));
-    context_.upload_rows(image, bgra, stride, row_bytes, static_cast<std::size_t>(height));
-    hip_check(dav2_hip_preprocess_bgra8_nearest(image.as<std::uint8_t>(), static_cast<std::uint32_t>(width),
-                                                static_cast<std::uint32_t>(height), row_bytes,
+    hip_check(dav2_hip_preprocess_bgra8_nearest(image->as<std::uint8_t>(), static_cast<std::uint32_t>(width),
+                                                static_cast<std::uint32_t>(height), device_stride,
                                                 static_cast<std::uint32_t>(network_width),
                                                 static_cast<std::uint32_t>(network_height), in.as<float>(),
                                                 context_.active_stream()),

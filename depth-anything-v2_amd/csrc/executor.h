@@ -8,6 +8,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <vector>
 
 namespace dav2 {
 
@@ -32,6 +33,15 @@ public:
                     int network_height, float* output);
     void infer_bgra8_normalized(const std::uint8_t* bgra, int width, int height, std::size_t stride,
                                 int network_width, int network_height, float* output);
+
+private:
+    // Uploads `height` rows of `row_bytes` (`stride` bytes apart) into the
+    // arena slot `slot` with one copy; returns the device row stride, which
+    // is `stride` only if keep_stride allows it.
+    std::size_t upload_image(const char* slot, const std::uint8_t* image, std::size_t row_bytes, int height,
+                             std::size_t stride, bool keep_stride, DeviceBuffer*& device);
+
+public:
 
     dav2_encoder encoder() const { return encoder_; }
     float metric_max_depth() const { return model_.derivation().metric_max_depth; }
@@ -88,6 +98,7 @@ private:
     GraphKey warm_key_;   // last eager run (buffers sized for it)
     GraphKey graph_key_;  // what graph_exec_ replays
     hipGraphExec_t graph_exec_ = nullptr;
+    std::vector<std::uint8_t> image_stage_;  // host rows of a strided image, packed before the upload
     DinoEncoder dino_;
     DptHead dpt_;
     Arena arena_;

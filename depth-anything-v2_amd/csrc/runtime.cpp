@@ -144,17 +144,6 @@ void HipContext::upload(DeviceBuffer& destination, const void* source, std::size
     upload_bytes_ += bytes;
 }
 
-void HipContext::upload_rows(DeviceBuffer& destination, const void* source, std::size_t source_stride,
-                             std::size_t row_bytes, std::size_t rows) {
-    if (row_bytes * rows > destination.size()) throw std::invalid_argument("upload exceeds device buffer");
-    if (row_bytes == 0 || rows == 0) return;
-    if (source_stride < row_bytes) throw std::invalid_argument("row stride shorter than a row");
-    hip_check(hipMemcpy2DAsync(destination.data(), row_bytes, source, source_stride, row_bytes, rows,
-                               hipMemcpyHostToDevice, active_),
-              "upload rows");
-    upload_bytes_ += row_bytes * rows;
-}
-
 void HipContext::download(const DeviceBuffer& source, void* destination, std::size_t bytes) {
     if (bytes > source.size()) throw std::invalid_argument("download exceeds device buffer");
     if (bytes == 0) return;

@@ -109,10 +109,6 @@ public:
 
     DeviceBuffer create_device_buffer(std::size_t bytes) { return DeviceBuffer(bytes); }
     void upload(DeviceBuffer& destination, const void* source, std::size_t bytes);
-    // `rows` host rows of `row_bytes`, `source_stride` bytes apart, packed
-    // into destination (row_bytes apart).
-    void upload_rows(DeviceBuffer& destination, const void* source, std::size_t source_stride,
-                     std::size_t row_bytes, std::size_t rows);
     void download(const DeviceBuffer& source, void* destination, std::size_t bytes);
     void synchronize();
     void make_current() const;

@@ -101,7 +101,10 @@ def _oracle_depth(oracle, model, chw, width, height):
     return depth
 
 
-@pytest.mark.parametrize("width,height,input_size,pad", [(300, 200, 140, 0), (97, 131, 112, 7), (140, 140, 140, 0)])
+# pad 7: rows uploaded with their padding; pad 360 (stride twice the row):
+# rows packed on the host before the upload
+@pytest.mark.parametrize("width,height,input_size,pad",
+                         [(300, 200, 140, 0), (97, 131, 112, 7), (140, 140, 140, 0), (120, 90, 70, 360)])
 def test_infer_bgr8_end_to_end(gpu, pkg, lib, oracle, vits_model, width, height, input_size, pad):
     # dav2.cpp:630-665: network_shape -> preprocess -> inference -> bilinear
     # (align corners) back to the image size; int8 mode is bit-exact.
@@ -135,6 +138,30 @@ def test_inferbridge_bgra8_end_to_end(gpu, pkg, lib, oracle, vits_model):
     want = oracle.normalize_span(_oracle_depth(oracle, vits_model, chw, nw, nh)).reshape(nh, nw)
     assert got.shape == (nh, nw)
     assert np.array_equal(got, want)
+
+
+def test_inferbridge_bgra8_strides(gpu, pkg, lib, vits_model):
+    # The same pixels with row padding kept (stride % 4 == 0) and packed on
+    # the host (odd stride; large padding) give the same output.
+    width, height, input_size = 70, 56, 56
+    rng = np.random.default_rng(11)
+    img = rng.integers(0, 256, size=(height, width * 4), dtype=np.uint8)
+    shape = pkg.ImageShape()
+    import ctypes as C
+    assert lib.dav2_get_inferbridge_shape(width, height, input_size, C.byref(shape)) == 0
+    outs = []
+    with pkg.Context(str(vits_model), "vits") as ctx:
+        for pad in (0, 8, 3, width * 4):
+            stride = width * 4 + pad
+            buf = np.zeros((height, stride), np.uint8)
+            buf[:, : width * 4] = img
+            out = np.empty(shape.width * shape.height, np.float32)
+            _announce("inferbridge stride", stride)
+            assert lib.dav2_inferbridge_bgra8_f32(ctx.handle, buf.ctypes.data, width, height, stride, input_size,
+                                                  out.ctypes.data, out.size) == 0
+            outs.append(out)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
 
 
 def test_image_entry_argument_checks(gpu, pkg, lib, vits_model):
