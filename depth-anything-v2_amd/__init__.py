@@ -93,6 +93,15 @@ class GemmArgs(C.Structure):
                 ("relu_output", C.c_uint32), ("split_k", C.c_uint32), ("split_scratch", C.c_void_p)]
 
 
+class GemmF32Args(C.Structure):
+    _fields_ = [("a", C.c_void_p), ("lda", C.c_uint64), ("b", C.c_void_p), ("ldb", C.c_uint64),
+                ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("epilogue", C.c_uint32),
+                ("bias", C.c_void_p), ("out", C.c_void_p), ("out_row_offset", C.c_uint64),
+                ("out_row_stride", C.c_uint64), ("residual", C.c_void_p), ("gamma", C.c_void_p),
+                ("convt_kernel", C.c_uint32), ("convt_width", C.c_uint32), ("convt_height", C.c_uint32),
+                ("convt_channels", C.c_uint32), ("relu_output", C.c_uint32)]
+
+
 class ConvArgs(C.Structure):
     _fields_ = [("input", C.c_void_p), ("width", C.c_uint32), ("height", C.c_uint32), ("channels", C.c_uint32),
                 ("kernel", C.c_uint32), ("weight", C.c_void_p), ("weight_scales", C.c_void_p), ("bias", C.c_void_p),
@@ -168,6 +177,8 @@ PROTOTYPES = {
     "dav2_hip_minmax_partials": (u32, [u64]),
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),
     "dav2_hip_normalize_relative": (C.c_int, [vp, vp, u64, vp]),
+    "dav2_hip_gemm_f32": (C.c_int, [C.c_void_p, vp]),
+    "dav2_hip_im2col_f32": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, u32, vp, u32, vp]),
     "dav2_hip_preprocess_bgr8": (C.c_int, [vp, u32, u32, u64, u32, u32, vp, vp]),
     "dav2_hip_preprocess_bgra8_nearest": (C.c_int, [vp, u32, u32, u64, u32, u32, vp, vp]),
     "dav2_hip_normalize_span": (C.c_int, [vp, vp, u64, vp, vp]),
@@ -188,6 +199,11 @@ PROTOTYPES = {
     "dav2_ops_project_tokens_int8": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, u32]),
     "dav2_ops_conv2d_int8": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, u32, u32, u32, u32, i32]),
     "dav2_ops_conv_transpose_nonoverlap_int8": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, u32, u32]),
+    "dav2_ops_linear": (C.c_int, [vp, DB, DB, DB, DB, u32, u32, u32, i32]),
+    "dav2_ops_project_tokens": (C.c_int, [vp, DB, DB, DB, DB, u32, u32, u32, u32]),
+    "dav2_ops_conv2d": (C.c_int, [vp, DB, DB, DB, DB, u32, u32, u32, u32, u32, u32, u32, i32]),
+    "dav2_ops_conv_transpose_nonoverlap": (C.c_int, [vp, DB, DB, DB, DB, u32, u32, u32, u32, u32]),
+    "dav2_ops_prepare_tokens_f32": (C.c_int, [vp, DB, DB, DB, DB, DB, DB, u32, u32, u32]),
     "dav2_ops_bilinear_align_true": (C.c_int, [vp, DB, DB, u32, u32, u32, u32, u32]),
     "dav2_ops_reduce_minmax": (C.c_int, [vp, DB, DB, u32]),
     "dav2_ops_normalize_relative": (C.c_int, [vp, DB, DB, u32]),

@@ -136,9 +136,11 @@ dav2_status DAV2_CALL dav2_create(const char* model_path_utf8, const dav2_create
     if (precision != 0 && (precision & (precision - 1u)) != 0)
         return fail(DAV2_STATUS_INVALID_ARGUMENT, "multiple DAV2 execution precisions were requested");
     if (options->vulkan_device_index < 0) return fail(DAV2_STATUS_INVALID_ARGUMENT, "invalid device index");
-    // This build executes the int8 operator path only.
-    if (options->flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP16 | DAV2_CREATE_FORCE_FP32_WEIGHTS))
-        return fail(DAV2_STATUS_UNSUPPORTED, "only the INT8 execution precision is built for MI355X");
+    // This build executes the int8 operator path (the default) and the fp32
+    // precision mode (FORCE_FP32). FORCE_FP32_WEIGHTS is accepted and has no
+    // further effect, as in the reference (dav2.cpp:182 is its only use).
+    if (options->flags & DAV2_CREATE_FORCE_FP16)
+        return fail(DAV2_STATUS_UNSUPPORTED, "the FP16 execution precision is not built for MI355X");
     if (options->flags & DAV2_CREATE_FORCE_METAL)
         return fail(DAV2_STATUS_UNSUPPORTED, "the Metal executor is not available on this platform");
     return protect([&] {

@@ -23,12 +23,13 @@ HipExecutor::HipExecutor(const std::string& model_path, dav2_encoder encoder, in
     : encoder_(encoder),
       model_(model_path, encoder),
       context_(device_index),
+      precision_((flags & DAV2_CREATE_FORCE_FP32) != 0 ? Precision::fp32 : Precision::int8),
       attention_precision_(attention_precision_for(flags)),
-      weights_(model_, context_),
+      weights_(model_, context_, precision_ == Precision::fp32),
       operators_(context_),
       side_operators_(context_),
-      dino_(encoder, weights_, operators_, attention_precision_),
-      dpt_(encoder, weights_, operators_) {
+      dino_(encoder, weights_, operators_, attention_precision_, precision_),
+      dpt_(encoder, weights_, operators_, precision_) {
     context_.make_current();
     hip_check(hipStreamCreateWithFlags(&side_stream_, hipStreamNonBlocking), "side stream");
     for (hipEvent_t& e : captured_) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "capture event");

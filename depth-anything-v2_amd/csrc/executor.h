@@ -50,6 +50,7 @@ public:
         download = context_.download_bytes();
     }
     Precision attention_precision() const { return attention_precision_; }
+    Precision precision() const { return precision_; }
     HipContext& context() { return context_; }
     std::uint64_t arena_bytes() const { return arena_.bytes(); }
 
@@ -72,6 +73,7 @@ private:
     dav2_encoder encoder_;
     ModelFile model_;  // validated before any HIP call, as the reference's member order does
     HipContext context_;
+    Precision precision_;  // int8, or fp32 under FORCE_FP32
     Precision attention_precision_;
     GpuModel weights_;
     HipOperators operators_;

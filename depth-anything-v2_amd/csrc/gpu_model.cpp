@@ -54,7 +54,7 @@ bool use_int8_weight(std::string_view name, const TensorView& t) {
     return (t.elements / t.dimensions[0]) % 4 == 0;
 }
 
-GpuModel::GpuModel(const ModelFile& model, HipContext& context) {
+GpuModel::GpuModel(const ModelFile& model, HipContext& context, bool fp32_weights) {
     tensors_.reserve(model.tensor_count());
     DeviceBuffer staging;
     std::vector<std::unique_ptr<std::vector<float>>> host_keepalive;
@@ -94,6 +94,16 @@ GpuModel::GpuModel(const ModelFile& model, HipContext& context) {
                 columns = src.elements / rows;
             }
             if (rows > 0xffffffffull || columns > 0xffffffffull) throw std::runtime_error("weight too large");
+            if (fp32_weights) {
+                dst.f32_rows = static_cast<std::uint32_t>(rows);
+                dst.f32_columns = static_cast<std::uint32_t>(columns);
+                dst.buffer = context.create_device_buffer(bytes);
+                context.upload(dst.buffer, rows_source, bytes);  // host copies live until the final sync
+                device_bytes_ += bytes;
+                if (!tensors_.emplace(std::string(name), std::move(dst)).second)
+                    throw std::runtime_error("duplicate GPU tensor name: " + std::string(name));
+                continue;
+            }
             dst.int8_rows = static_cast<std::uint32_t>(rows);
             dst.int8_columns = static_cast<std::uint32_t>(columns);
             dst.int8_ld = padded_k(columns);

@@ -2,7 +2,7 @@
 // (reference src/gpu_model.cpp:127-146). Tensors the reference quantizes for
 // its int8 mode (selection rule: src/gpu_model.cpp:16-44) are stored only as
 // per-output-row int8 + fp32 scales (quantizer: src/gpu_model.cpp:241-264),
-// everything else as fp32.
+// everything else as fp32. The fp32 precision mode keeps every tensor fp32.
 //
 // int8 layout: [rows][ld] bytes, ld = columns rounded up to 64, zero padding.
 // Conv weights [OC][IC][k][k] flatten to rows = OC, column ic*k*k + ky*k + kx
@@ -22,7 +22,11 @@
 namespace dav2 {
 
 struct GpuTensor {
-    DeviceBuffer buffer;       // fp32 copy (only for tensors not stored as int8)
+    // fp32 copy: tensors not stored as int8; in the fp32 precision mode every
+    // tensor, weights in the GEMM layout [f32_rows][f32_columns] (the int8
+    // row layout unpadded: ConvTranspose reordered, everything else as stored)
+    DeviceBuffer buffer;
+    std::uint32_t f32_rows = 0, f32_columns = 0;
     DeviceBuffer int8_buffer;  // [int8_rows][int8_ld]
     DeviceBuffer int8_scales;  // [int8_rows]
     // Conv weights the implicit-GEMM convolution takes (kernel 1 or 3,
@@ -43,7 +47,8 @@ inline std::uint32_t padded_k(std::uint64_t columns) { return static_cast<std::u
 
 class GpuModel {
 public:
-    GpuModel(const ModelFile& model, HipContext& context);
+    // fp32_weights: the fp32 precision mode (no int8 copies).
+    GpuModel(const ModelFile& model, HipContext& context, bool fp32_weights = false);
     const GpuTensor& tensor(std::string_view name) const;
     bool contains(std::string_view name) const { return tensors_.count(std::string(name)) != 0; }
     std::size_t tensor_count() const { return tensors_.size(); }

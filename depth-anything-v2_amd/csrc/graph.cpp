@@ -48,9 +48,10 @@ std::string block_name(std::uint32_t block, const char* suffix) {
 
 // ---------------------------------------------------------------------------
 DinoEncoder::DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators,
-                         Precision attention_precision)
+                         Precision attention_precision, Precision precision)
     : config_(encoder_config(encoder)), weights_(weights), ops_(operators),
-      attention_precision_(attention_precision) {
+      attention_precision_(attention_precision), precision_(precision) {
+    if (precision_ == Precision::fp16) throw std::invalid_argument("the fp16 encoder is not part of this build");
     if (weights_.tensor("pretrained.cls_token").elements != config_.embedding ||
         weights_.tensor("pretrained.pos_embed").elements != std::uint64_t(1370) * config_.embedding)
         throw std::runtime_error("encoder tensor dimensions do not match");
@@ -73,7 +74,8 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
     DeviceBuffer& qkv = arena.get("enc.qkv", tok_bytes * 3);
     DeviceBuffer& attn = arena.get("enc.attention", tok_bytes);
     DeviceBuffer& hidden = arena.get("enc.hidden", tok_bytes * 4);
-    const bool fused = attention_precision_ == Precision::fp16;
+    const bool f32 = precision_ == Precision::fp32;
+    const bool fused = !f32 && attention_precision_ == Precision::fp16;
     DeviceBuffer& scores =
         arena.get("enc.scores", fused ? HipOperators::attention_fused_scratch_bytes(T, H, batch)
                                       : HipOperators::attention_score_bytes(T, H, batch, attention_precision_));
@@ -93,10 +95,14 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
         DeviceBuffer img = DeviceBuffer::view(const_cast<float*>(image) + b * image_elems, image_elems * sizeof(float));
         DeviceBuffer out = DeviceBuffer::view(current.as<float>() + std::uint64_t(b) * T * D,
                                               std::uint64_t(T) * D * sizeof(float));
-        ops_.prepare_tokens(out, img, DeviceBuffer(), DeviceBuffer(), patch.int8_buffer, patch.int8_scales,
+        ops_.prepare_tokens(out, img, patch.buffer, DeviceBuffer(), patch.int8_buffer, patch.int8_scales,
                             fp32("pretrained.patch_embed.proj.bias"), fp32("pretrained.cls_token"),
-                            fp32("pretrained.pos_embed"), width, height, D, Precision::int8,
+                            fp32("pretrained.pos_embed"), width, height, D, f32 ? Precision::fp32 : Precision::int8,
                             /*position_is_constant=*/true);
+    }
+    if (f32) {
+        forward_fp32(rows, T, batch, arena, current, qkv, attn, hidden, scores, features, on_capture);
+        return;
     }
 
     std::uint32_t capture = 0;
@@ -141,9 +147,44 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
     if (capture != 4) throw std::runtime_error("encoder did not produce four features");
 }
 
+void DinoEncoder::forward_fp32(std::uint32_t rows, std::uint32_t T, std::uint32_t batch, Arena& arena,
+                               DeviceBuffer& current, DeviceBuffer& qkv, DeviceBuffer& attn, DeviceBuffer& hidden,
+                               DeviceBuffer& scores, DeviceBuffer* features[4],
+                               const std::function<void(std::uint32_t)>& on_capture) {
+    // encoder.cpp:407-597 in the fp32 precision mode: LayerNorm rows in fp32,
+    // fp32 GEMMs (GELU and the LayerScale residual in their epilogues, the
+    // arithmetic of the reference's separate gelu / add_scaled passes),
+    // materialised fp32 attention.
+    const std::uint32_t D = config_.embedding, H = config_.heads;
+    DeviceBuffer& normed = arena.get("enc.normed", std::uint64_t(rows) * D * sizeof(float));
+    using E = HipOperators::Epilogue;
+    std::uint32_t capture = 0;
+    for (std::uint32_t blk = 0; blk < config_.blocks; ++blk) {
+        const auto W = [&](const char* s) -> const DeviceBuffer& { return weights_.tensor(block_name(blk, s)).buffer; };
+        ops_.layer_norm(normed, current, W(".norm1.weight"), W(".norm1.bias"), rows, D, 1.0e-6f);
+        ops_.linear_f32(qkv, normed, W(".attn.qkv.weight"), &W(".attn.qkv.bias"), rows, D, 3 * D, E::row);
+        ops_.attention_batched(attn, qkv, T, H, batch, scores, Precision::fp32);
+        ops_.linear_f32(current, attn, W(".attn.proj.weight"), &W(".attn.proj.bias"), rows, D, D, E::row_layerscale,
+                        &W(".ls1.gamma"));
+        ops_.layer_norm(normed, current, W(".norm2.weight"), W(".norm2.bias"), rows, D, 1.0e-6f);
+        ops_.linear_f32(hidden, normed, W(".mlp.fc1.weight"), &W(".mlp.fc1.bias"), rows, D, 4 * D, E::row_gelu);
+        ops_.linear_f32(current, hidden, W(".mlp.fc2.weight"), &W(".mlp.fc2.bias"), rows, 4 * D, D, E::row_layerscale,
+                        &W(".ls2.gamma"));
+        if (capture < 4 && blk == config_.capture[capture]) {
+            ops_.layer_norm(*features[capture], current, fp32("pretrained.norm.weight"), fp32("pretrained.norm.bias"),
+                            rows, D, 1.0e-6f);
+            if (on_capture) on_capture(capture);
+            ++capture;
+        }
+    }
+    if (capture != 4) throw std::runtime_error("encoder did not produce four features");
+}
+
 // ---------------------------------------------------------------------------
-DptHead::DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operators)
-    : config_(dpt_config(encoder)), weights_(weights), ops_(operators), zero_bias_(sizeof(float)) {
+DptHead::DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, Precision precision)
+    : config_(dpt_config(encoder)), weights_(weights), ops_(operators), zero_bias_(sizeof(float)),
+      precision_(precision) {
+    if (precision_ == Precision::fp16) throw std::invalid_argument("the fp16 DPT head is not part of this build");
     hip_check(hipMemsetAsync(zero_bias_.data(), 0, sizeof(float), ops_.context().active_stream()), "zero bias");
 }
 
@@ -157,8 +198,13 @@ FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::str
     out.channels = oc;
     out.buffer = &arena.get(slot, out.elements() * sizeof(float));
     const GpuTensor& w = weights_.tensor(weight);
-    if (!w.int8_buffer) throw std::runtime_error("convolution weight is not int8: " + weight);
     const DeviceBuffer& b = has_bias ? weights_.tensor(bias).buffer : zero_bias_;
+    if (precision_ == Precision::fp32) {
+        ops.conv2d(*out.buffer, *in.buffer, w.buffer, b, in.width, in.height, in.channels, oc, k, stride, pad, has_bias,
+                   fusion);
+        return out;
+    }
+    if (!w.int8_buffer) throw std::runtime_error("convolution weight is not int8: " + weight);
     ops.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc, k,
                     stride, pad, has_bias, &w.int8_tapmajor, fusion);
     return out;
@@ -204,8 +250,12 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
                     pw, ph, config_.project[i]};
     DeviceBuffer tokens = DeviceBuffer::view(feature.as<float>() + std::uint64_t(b) * T * D,
                                              std::uint64_t(T) * D * sizeof(float));
-    ops.project_tokens_int8(*proj.buffer, tokens, w.int8_buffer, w.int8_scales, weights_.tensor(prefix + ".bias").buffer,
-                            pw, ph, D, config_.project[i]);
+    if (precision_ == Precision::fp32)
+        ops.project_tokens(*proj.buffer, tokens, w.buffer, weights_.tensor(prefix + ".bias").buffer, pw, ph, D,
+                           config_.project[i]);
+    else
+        ops.project_tokens_int8(*proj.buffer, tokens, w.int8_buffer, w.int8_scales,
+                                weights_.tensor(prefix + ".bias").buffer, pw, ph, D, config_.project[i]);
     FeatureMap layer;
     if (i < 2) {
         const std::uint32_t k = i == 0 ? 4 : 2;
@@ -214,8 +264,13 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
         layer = FeatureMap{&arena.get("dpt.layer" + std::to_string(i),
                                       std::uint64_t(pw) * k * ph * k * proj.channels * sizeof(float)),
                            pw * k, ph * k, proj.channels};
-        ops.conv_transpose_nonoverlap_int8(*layer.buffer, *proj.buffer, rw.int8_buffer, rw.int8_scales,
-                                           weights_.tensor(r + ".bias").buffer, pw, ph, proj.channels, proj.channels, k);
+        if (precision_ == Precision::fp32)
+            ops.conv_transpose_nonoverlap(*layer.buffer, *proj.buffer, rw.buffer, weights_.tensor(r + ".bias").buffer,
+                                          pw, ph, proj.channels, proj.channels, k);
+        else
+            ops.conv_transpose_nonoverlap_int8(*layer.buffer, *proj.buffer, rw.int8_buffer, rw.int8_scales,
+                                               weights_.tensor(r + ".bias").buffer, pw, ph, proj.channels,
+                                               proj.channels, k);
     } else if (i == 2) {
         layer = proj;
     } else {
@@ -265,6 +320,17 @@ void DptHead::refine_and_head(const FeatureMap refined[4], std::uint32_t b, std:
     DeviceBuffer logits;
     if (pre_relu) logits = DeviceBuffer::view(pre_relu, pixels * sizeof(float));
     const GpuTensor& w3 = weights_.tensor("depth_head.scratch.output_conv2.2.weight");
+    if (precision_ == Precision::fp32) {
+        const DeviceBuffer& b3 = weights_.tensor("depth_head.scratch.output_conv2.2.bias").buffer;
+        if (logits) {
+            ops_.conv2d(logits, *head.buffer, w3.buffer, b3, head.width, head.height, head.channels, 1, 1, 1, 0, true);
+            ops_.relu(out, logits, static_cast<std::uint32_t>(pixels));
+        } else {
+            ops_.conv2d(out, *head.buffer, w3.buffer, b3, head.width, head.height, head.channels, 1, 1, 1, 0, true,
+                        relu_after);
+        }
+        return;
+    }
     if (!w3.int8_buffer) throw std::runtime_error("output_conv2.2 weight is not int8");
     ops_.conv1x1_narrow_int8(out, *head.buffer, w3.int8_buffer, w3.int8_ld, w3.int8_scales,
                              weights_.tensor("depth_head.scratch.output_conv2.2.bias").buffer, head.width, head.height,

@@ -8,7 +8,8 @@
 //    proj/fc2 epilogues;
 //  - every DPT convolution, 3x3 and 1x1, runs as im2col + int8 GEMM (the
 //    reference's int8 mode sends only resize_layers.* through conv2d_int8 and
-//    the refinement convolutions through fp16);
+//    the refinement convolutions through fp16); in the fp32 precision mode
+//    everything runs in fp32, as in the reference's;
 //  - buffers come from a grow-only arena, so a fixed resolution allocates only
 //    on its first run.
 #pragma once
@@ -44,7 +45,10 @@ private:
 
 class DinoEncoder {
 public:
-    DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, Precision attention_precision);
+    // precision: int8 (the product path) or fp32 (the fp32 precision mode:
+    // fp32 weights and GEMMs, no quantization).
+    DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, Precision attention_precision,
+                Precision precision = Precision::int8);
     // image: device [batch][3][height][width]. On return features[i] holds the
     // final-norm token matrix [batch*tokens][D] of capture layer i.
     // on_capture(i), when given, runs right after the work producing
@@ -55,10 +59,15 @@ public:
 
 private:
     const DeviceBuffer& fp32(const std::string& name) const;
+    void forward_fp32(std::uint32_t rows, std::uint32_t tokens, std::uint32_t batch, Arena& arena,
+                      DeviceBuffer& current, DeviceBuffer& qkv, DeviceBuffer& attn, DeviceBuffer& hidden,
+                      DeviceBuffer& scores, DeviceBuffer* features[4],
+                      const std::function<void(std::uint32_t)>& on_capture);
     EncoderConfig config_;
     GpuModel& weights_;
     HipOperators& ops_;
     Precision attention_precision_;
+    Precision precision_;
 };
 
 struct FeatureMap {
@@ -69,7 +78,7 @@ struct FeatureMap {
 
 class DptHead {
 public:
-    DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operators);
+    DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, Precision precision = Precision::int8);
     // features[i]: [batch*tokens][D]; writes batch raw depth maps
     // [batch][ph*14][pw*14] to depth. pre_relu (optional) receives the last
     // image's depth before the final ReLU.
@@ -104,6 +113,7 @@ private:
     GpuModel& weights_;
     HipOperators& ops_;
     DeviceBuffer zero_bias_;
+    Precision precision_;
 };
 
 }  // namespace dav2

@@ -300,7 +300,7 @@ void HipOperators::attention_fused(DeviceBuffer& output, const DeviceBuffer& qkv
 }
 
 // src/operators.cpp:1211-1406 (int8 branch)
-void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& image, const DeviceBuffer&,
+void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& image, const DeviceBuffer& patch_weight,
                                   const DeviceBuffer&, const DeviceBuffer& patch_int8_weight,
                                   const DeviceBuffer& patch_int8_scales, const DeviceBuffer& patch_bias,
                                   const DeviceBuffer& class_token, const DeviceBuffer& position,
@@ -308,30 +308,44 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
                                   Precision precision, bool position_is_constant) {
     if (input_width == 0 || input_height == 0 || input_width % 14 != 0 || input_height % 14 != 0 || embedding == 0)
         throw std::invalid_argument("invalid patch embedding dimensions");
-    if (precision != Precision::int8) throw std::runtime_error("only the INT8 patch embedding is built");
+    if (precision == Precision::fp16) throw std::runtime_error("the fp16 patch embedding is not part of this build");
     const std::uint32_t pw = input_width / 14, ph = input_height / 14, spatial = pw * ph;
     const std::uint64_t tokens = std::uint64_t(spatial) + 1;
     constexpr std::uint32_t patch_columns = 3u * 14u * 14u;
     require_bytes(image, std::uint64_t(input_width) * input_height * 3, "image");
-    require_int8_weight(patch_int8_weight, embedding, patch_columns, "INT8 patch weight buffer");
-    require_bytes(patch_int8_scales, embedding, "patch weight scale");
+    if (precision == Precision::int8) {
+        require_int8_weight(patch_int8_weight, embedding, patch_columns, "INT8 patch weight buffer");
+        require_bytes(patch_int8_scales, embedding, "patch weight scale");
+    } else {
+        require_bytes(patch_weight, std::uint64_t(embedding) * patch_columns, "patch weight");
+    }
     require_bytes(patch_bias, embedding, "patch bias");
     require_bytes(class_token, embedding, "class token");
     require_bytes(position, std::uint64_t(1370) * embedding, "position");
     require_bytes(output, tokens * embedding, "token output");
     const hipStream_t s = stream();
-    const std::uint32_t ld = ld64(patch_columns);
-    DeviceBuffer& packed = workspace_.packed(std::uint64_t(spatial) * ld);
-    DeviceBuffer& scales = workspace_.scales(std::uint64_t(spatial) * sizeof(float));
-    ProfileScope prof_patch(context_.profiler(), "im2col_quantize_i8",
-                            12.0 * input_width * input_height + 1.0 * spatial * patch_columns + 4.0 * spatial,
-                            "B", s);
-    hip_check(dav2_hip_im2col_quantize_i8(image.as<float>(), input_width, input_height, 3, pw, ph, 14, 14, 0,
-                                          packed.as<int8_t>(), ld, scales.as<float>(), nullptr, 0, s),
-              "patch im2col");
-    linear_int8_packed(output, packed, ld, patch_int8_weight, scales, patch_int8_scales, patch_bias, spatial,
-                       patch_columns, embedding, 1u, static_cast<std::uint32_t>(tokens), false, true);
-    workspace_ld_ = ld;
+    if (precision == Precision::int8) {
+        const std::uint32_t ld = ld64(patch_columns);
+        DeviceBuffer& packed = workspace_.packed(std::uint64_t(spatial) * ld);
+        DeviceBuffer& scales = workspace_.scales(std::uint64_t(spatial) * sizeof(float));
+        ProfileScope prof_patch(context_.profiler(), "im2col_quantize_i8",
+                                12.0 * input_width * input_height + 1.0 * spatial * patch_columns + 4.0 * spatial,
+                                "B", s);
+        hip_check(dav2_hip_im2col_quantize_i8(image.as<float>(), input_width, input_height, 3, pw, ph, 14, 14, 0,
+                                              packed.as<int8_t>(), ld, scales.as<float>(), nullptr, 0, s),
+                  "patch im2col");
+        linear_int8_packed(output, packed, ld, patch_int8_weight, scales, patch_int8_scales, patch_bias, spatial,
+                           patch_columns, embedding, 1u, static_cast<std::uint32_t>(tokens), false, true);
+        workspace_ld_ = ld;
+    } else {
+        // fp32: im2col rows of the 14x14 patches, GEMM into token rows 1..
+        DeviceBuffer& cols = grow(f32_cols_, std::uint64_t(spatial) * patch_columns * sizeof(float));
+        hip_check(dav2_hip_im2col_f32(image.as<float>(), input_width, input_height, 3, pw, ph, 14, 14, 0, 0,
+                                      cols.as<float>(), patch_columns, s),
+                  "patch im2col");
+        linear_f32(output, cols, patch_weight, &patch_bias, spatial, patch_columns, embedding, Epilogue::row, nullptr,
+                   1);
+    }
     const void* before = interpolated_.data();
     grow(interpolated_, std::uint64_t(spatial) * embedding * sizeof(float));
     if (!position_is_constant || interpolated_.data() != before || interpolated_position_ != position.data() ||
@@ -347,6 +361,164 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
     hip_check(dav2_hip_finish_tokens(output.as<float>(), interpolated_.as<float>(), position.as<float>(),
                                      class_token.as<float>(), pw, ph, embedding, 1, s),
               "class/position tokens");
+}
+
+// ---- fp32 precision mode ------------------------------------------------------
+void HipOperators::linear_f32(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                              const DeviceBuffer* bias, std::uint32_t rows, std::uint32_t input_columns,
+                              std::uint32_t output_columns, Epilogue epilogue, const DeviceBuffer* gamma,
+                              std::uint64_t output_row_offset) {
+    if (rows == 0 || input_columns == 0 || output_columns == 0)
+        throw std::invalid_argument("linear dimensions cannot be zero");
+    if (input_columns % 4u) throw std::invalid_argument("fp32 linear input columns must be a multiple of four");
+    if (epilogue == Epilogue::row_colmax) throw std::invalid_argument("no column maxima on the fp32 GEMM");
+    require_bytes(input, std::uint64_t(rows) * input_columns, "input");
+    require_bytes(weight, std::uint64_t(output_columns) * input_columns, "weight");
+    if (bias) require_bytes(*bias, output_columns, "bias");
+    require_bytes(output, (std::uint64_t(rows) + output_row_offset) * output_columns, "output");
+    dav2_gemm_f32_args a{};
+    a.a = input.as<float>();
+    a.lda = input_columns;
+    a.b = weight.as<float>();
+    a.ldb = input_columns;
+    a.m = rows;
+    a.n = output_columns;
+    a.k = input_columns;
+    a.bias = bias ? bias->as<float>() : nullptr;
+    a.out = output.as<float>();
+    a.out_row_offset = output_row_offset;
+    switch (epilogue) {
+        case Epilogue::row_gelu: a.epilogue = DAV2_GEMM_EPI_ROW_GELU; break;
+        case Epilogue::row_layerscale:
+            if (!gamma) throw std::invalid_argument("LayerScale epilogue needs gamma");
+            require_bytes(*gamma, output_columns, "LayerScale gamma");
+            a.epilogue = DAV2_GEMM_EPI_ROW_LAYERSCALE;
+            a.residual = output.as<float>();
+            a.gamma = gamma->as<float>();
+            break;
+        default: a.epilogue = DAV2_GEMM_EPI_ROW; break;
+    }
+    ProfileScope prof(context_.profiler(), "gemm_f32", 2.0 * rows * output_columns * input_columns, "OP", stream());
+    hip_check(dav2_hip_gemm_f32(&a, stream()), "fp32 linear");
+}
+
+// src/operators.cpp:882-955
+void HipOperators::linear(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                          const DeviceBuffer& bias, std::uint32_t rows, std::uint32_t input_columns,
+                          std::uint32_t output_columns, bool gelu) {
+    linear_f32(output, input, weight, &bias, rows, input_columns, output_columns,
+               gelu ? Epilogue::row_gelu : Epilogue::row);
+}
+
+// src/operators.cpp:1408-1452: CLS skipped, channel-major output
+void HipOperators::project_tokens(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& weight,
+                                  const DeviceBuffer& bias, std::uint32_t width, std::uint32_t height,
+                                  std::uint32_t embedding, std::uint32_t output_channels) {
+    const std::uint32_t spatial = width * height;
+    if (width == 0 || height == 0 || embedding == 0 || output_channels == 0)
+        throw std::invalid_argument("invalid token projection dimensions");
+    if (embedding % 4u) throw std::invalid_argument("fp32 token embedding must be a multiple of four");
+    require_bytes(tokens, std::uint64_t(spatial + 1u) * embedding, "tokens");
+    require_bytes(weight, std::uint64_t(output_channels) * embedding, "weight");
+    require_bytes(bias, output_channels, "bias");
+    require_bytes(output, std::uint64_t(spatial) * output_channels, "output");
+    dav2_gemm_f32_args a{};
+    a.a = tokens.as<float>() + embedding;
+    a.lda = embedding;
+    a.b = weight.as<float>();
+    a.ldb = embedding;
+    a.m = spatial;
+    a.n = output_channels;
+    a.k = embedding;
+    a.epilogue = DAV2_GEMM_EPI_TRANSPOSED;
+    a.bias = bias.as<float>();
+    a.out = output.as<float>();
+    a.out_row_stride = spatial;
+    ProfileScope prof(context_.profiler(), "gemm_f32", 2.0 * spatial * output_channels * embedding, "OP", stream());
+    hip_check(dav2_hip_gemm_f32(&a, stream()), "fp32 token projection");
+}
+
+// src/operators.cpp:1528-1676: im2col + GEMM, CHW output; fusion as conv2d_int8
+void HipOperators::conv2d(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                          const DeviceBuffer& bias, std::uint32_t input_width, std::uint32_t input_height,
+                          std::uint32_t input_channels, std::uint32_t output_channels, std::uint32_t kernel,
+                          std::uint32_t stride, std::uint32_t padding, bool has_bias, const ConvFusion& fusion) {
+    if (input_width == 0 || input_height == 0 || input_channels == 0 || output_channels == 0 || kernel == 0 ||
+        stride == 0 || input_width + 2u * padding < kernel || input_height + 2u * padding < kernel)
+        throw std::invalid_argument("invalid convolution dimensions");
+    const std::uint32_t inner = input_channels * kernel * kernel;
+    if (inner % 4u) throw std::invalid_argument("fp32 convolution inner size must be a multiple of four");
+    const std::uint32_t ow = (input_width + 2u * padding - kernel) / stride + 1u;
+    const std::uint32_t oh = (input_height + 2u * padding - kernel) / stride + 1u;
+    const std::uint64_t pixels = std::uint64_t(ow) * oh;
+    if (pixels > 0xffffffffull) throw std::invalid_argument("convolution output too large");
+    require_bytes(input, std::uint64_t(input_width) * input_height * input_channels, "convolution input");
+    require_bytes(weight, std::uint64_t(output_channels) * inner, "convolution weight");
+    if (has_bias) require_bytes(bias, output_channels, "convolution bias");
+    require_bytes(output, pixels * output_channels, "convolution output");
+    if (fusion.residual) require_bytes(*fusion.residual, pixels * output_channels, "convolution residual");
+    const hipStream_t s = stream();
+    DeviceBuffer& cols = grow(f32_cols_, pixels * inner * sizeof(float));
+    ProfileScope prof_cols(context_.profiler(), "im2col_f32", 4.0 * pixels * inner, "B", s);
+    hip_check(dav2_hip_im2col_f32(input.as<float>(), input_width, input_height, input_channels, ow, oh, kernel, stride,
+                                  static_cast<std::int32_t>(padding), fusion.relu_input ? 1u : 0u, cols.as<float>(),
+                                  inner, s),
+              "fp32 im2col");
+    dav2_gemm_f32_args a{};
+    a.a = cols.as<float>();
+    a.lda = inner;
+    a.b = weight.as<float>();
+    a.ldb = inner;
+    a.m = static_cast<std::uint32_t>(pixels);
+    a.n = output_channels;
+    a.k = inner;
+    a.epilogue = DAV2_GEMM_EPI_TRANSPOSED;
+    a.bias = has_bias ? bias.as<float>() : nullptr;
+    a.out = output.as<float>();
+    a.out_row_stride = pixels;
+    a.residual = fusion.residual ? fusion.residual->as<float>() : nullptr;
+    a.relu_output = fusion.relu_output ? 1u : 0u;
+    ProfileScope prof(context_.profiler(), "gemm_f32", 2.0 * pixels * output_channels * inner, "OP", s);
+    hip_check(dav2_hip_gemm_f32(&a, s), "fp32 convolution");
+}
+
+// src/operators.cpp:1807-1861, stride == kernel
+void HipOperators::conv_transpose_nonoverlap(DeviceBuffer& output, const DeviceBuffer& input,
+                                             const DeviceBuffer& weight, const DeviceBuffer& bias,
+                                             std::uint32_t input_width, std::uint32_t input_height,
+                                             std::uint32_t input_channels, std::uint32_t output_channels,
+                                             std::uint32_t kernel) {
+    if (input_width == 0 || input_height == 0 || input_channels == 0 || output_channels == 0 || kernel == 0)
+        throw std::invalid_argument("invalid transposed convolution dimensions");
+    if (input_channels % 4u) throw std::invalid_argument("fp32 transposed convolution channels must be a multiple of four");
+    const std::uint64_t pixels = std::uint64_t(input_width) * input_height;
+    const std::uint32_t wrows = kernel * kernel * output_channels;
+    require_bytes(input, pixels * input_channels, "transposed convolution input");
+    require_bytes(weight, std::uint64_t(wrows) * input_channels, "transposed convolution weight");
+    require_bytes(bias, output_channels, "transposed convolution bias");
+    require_bytes(output, pixels * kernel * kernel * output_channels, "transposed convolution output");
+    const hipStream_t s = stream();
+    DeviceBuffer& cols = grow(f32_cols_, pixels * input_channels * sizeof(float));
+    hip_check(dav2_hip_im2col_f32(input.as<float>(), input_width, input_height, input_channels, input_width,
+                                  input_height, 1, 1, 0, 0, cols.as<float>(), input_channels, s),
+              "fp32 pixel rows");
+    dav2_gemm_f32_args a{};
+    a.a = cols.as<float>();
+    a.lda = input_channels;
+    a.b = weight.as<float>();
+    a.ldb = input_channels;
+    a.m = static_cast<std::uint32_t>(pixels);
+    a.n = wrows;
+    a.k = input_channels;
+    a.epilogue = DAV2_GEMM_EPI_CONVT;
+    a.bias = bias.as<float>();
+    a.out = output.as<float>();
+    a.convt_kernel = kernel;
+    a.convt_width = input_width;
+    a.convt_height = input_height;
+    a.convt_channels = output_channels;
+    ProfileScope prof(context_.profiler(), "gemm_f32", 2.0 * pixels * wrows * input_channels, "OP", s);
+    hip_check(dav2_hip_gemm_f32(&a, s), "fp32 transposed convolution");
 }
 
 // src/operators.cpp:1483-1526

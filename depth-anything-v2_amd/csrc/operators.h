@@ -6,7 +6,9 @@
 // src/operators.cpp:93-102) and work is enqueued asynchronously on the
 // context's active stream. DeviceBuffer replaces VulkanBuffer; the int8 weight
 // buffers are the GpuModel layout ([rows][ld] bytes, ld = K rounded up to 64).
-// fp32/fp16 operator variants are not part of this build.
+// The fp32 variants (linear, project_tokens, conv2d, conv_transpose_nonoverlap,
+// prepare_tokens with Precision::fp32) serve the fp32 precision mode; fp16
+// variants are not part of this build.
 //
 // Fused variants (no reference counterpart) serve the encoder/DPT drivers:
 // they compute the same arithmetic as the reference's separate passes.
@@ -99,6 +101,23 @@ public:
                                         std::uint32_t input_height, std::uint32_t input_channels,
                                         std::uint32_t output_channels, std::uint32_t kernel);
 
+    // ---- fp32 precision mode ---------------------------------------------
+    // fp32 weights: linear/projection [N][K], conv [OC][C*k*k] (the model
+    // layout), conv-transpose rows (ky*k + kx)*OC + oc of IC columns (the
+    // GpuModel reorder); K, C*k*k and IC multiples of 4.
+    void linear(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight, const DeviceBuffer& bias,
+                std::uint32_t rows, std::uint32_t input_columns, std::uint32_t output_columns, bool gelu);
+    void project_tokens(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& weight,
+                        const DeviceBuffer& bias, std::uint32_t width, std::uint32_t height, std::uint32_t embedding,
+                        std::uint32_t output_channels);
+    void conv2d(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight, const DeviceBuffer& bias,
+                std::uint32_t input_width, std::uint32_t input_height, std::uint32_t input_channels,
+                std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding,
+                bool has_bias, const ConvFusion& fusion = ConvFusion{});
+    void conv_transpose_nonoverlap(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                                   const DeviceBuffer& bias, std::uint32_t input_width, std::uint32_t input_height,
+                                   std::uint32_t input_channels, std::uint32_t output_channels, std::uint32_t kernel);
+
     void bilinear_align_true(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t input_width,
                              std::uint32_t input_height, std::uint32_t output_width, std::uint32_t output_height,
                              std::uint32_t channels);
@@ -129,6 +148,12 @@ public:
                                   const DeviceBuffer* gamma = nullptr, std::uint64_t output_row_offset = 0,
                                   DeviceBuffer* col_absmax = nullptr, std::uint32_t col_absmax_begin = 0);
     static std::uint32_t gemm_row_tiles(std::uint32_t rows, std::uint32_t output_columns);
+    // fp32 GEMM with the row epilogues (row_colmax excluded), for the fp32
+    // precision mode's encoder.
+    void linear_f32(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                    const DeviceBuffer* bias, std::uint32_t rows, std::uint32_t input_columns,
+                    std::uint32_t output_columns, Epilogue epilogue, const DeviceBuffer* gamma = nullptr,
+                    std::uint64_t output_row_offset = 0);
     // Batched attention over `batch` token matrices of `tokens` rows each.
     void attention_batched(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
                            std::uint32_t heads, std::uint32_t batch, DeviceBuffer& score_scratch,
@@ -173,6 +198,7 @@ private:
     DeviceBuffer conv_weights_;    // tap-major weights of a conv2d_int8 call that brought none
     DeviceBuffer conv_act_;        // ReLU of a conv2d_int8 input on the im2col path
     DeviceBuffer gemm_split_;      // int32 slices of split-K channel-major GEMMs
+    DeviceBuffer f32_cols_;        // fp32 im2col rows of the fp32 convolutions
     std::uint32_t workspace_ld_ = 0;  // row stride of the int8 rows currently in the workspace
 };
 

@@ -151,6 +151,55 @@ dav2_status DAV2_CALL dav2_ops_conv_transpose_nonoverlap_int8(dav2_ops* ops, dav
     });
 }
 
+dav2_status DAV2_CALL dav2_ops_linear(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                      dav2_device_buffer weight, dav2_device_buffer bias, uint32_t rows,
+                                      uint32_t input_columns, uint32_t output_columns, int32_t gelu) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.linear(out, v(input), v(weight), v(bias), rows, input_columns, output_columns, gelu != 0);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_project_tokens(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer tokens,
+                                              dav2_device_buffer weight, dav2_device_buffer bias, uint32_t width,
+                                              uint32_t height, uint32_t embedding, uint32_t channels) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.project_tokens(out, v(tokens), v(weight), v(bias), width, height, embedding, channels);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_conv2d(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                      dav2_device_buffer weight, dav2_device_buffer bias, uint32_t iw, uint32_t ih,
+                                      uint32_t ic, uint32_t oc, uint32_t kernel, uint32_t stride, uint32_t padding,
+                                      int32_t has_bias) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.conv2d(out, v(input), v(weight), v(bias), iw, ih, ic, oc, kernel, stride, padding, has_bias != 0);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_conv_transpose_nonoverlap(dav2_ops* ops, dav2_device_buffer output,
+                                                         dav2_device_buffer input, dav2_device_buffer weight,
+                                                         dav2_device_buffer bias, uint32_t iw, uint32_t ih,
+                                                         uint32_t ic, uint32_t oc, uint32_t kernel) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.conv_transpose_nonoverlap(out, v(input), v(weight), v(bias), iw, ih, ic, oc, kernel);
+    });
+}
+
+dav2_status DAV2_CALL dav2_ops_prepare_tokens_f32(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer image,
+                                                  dav2_device_buffer weight, dav2_device_buffer bias,
+                                                  dav2_device_buffer cls, dav2_device_buffer position,
+                                                  uint32_t width, uint32_t height, uint32_t embedding) {
+    return guard(ops, [&](dav2::HipOperators& o) {
+        auto out = v(output);
+        o.prepare_tokens(out, v(image), v(weight), dav2::DeviceBuffer(), dav2::DeviceBuffer(), dav2::DeviceBuffer(),
+                         v(bias), v(cls), v(position), width, height, embedding, dav2::Precision::fp32);
+    });
+}
+
 dav2_status DAV2_CALL dav2_ops_bilinear_align_true(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
                                                   uint32_t iw, uint32_t ih, uint32_t ow, uint32_t oh,
                                                   uint32_t channels) {

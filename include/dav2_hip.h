@@ -123,6 +123,39 @@ typedef struct dav2_gemm_i8_args {
 /* Replaces linear_int8_tiled.glsl:40-117 (src/operators.cpp:847-880) and
  * conv_transpose_int8.glsl:31-58 (:1969-1975). */
 DAV2_API int dav2_hip_gemm_i8(const dav2_gemm_i8_args* args, void* stream);
+
+/* fp32 GEMM of the fp32 precision mode: out = a . b^T + bias with the
+ * epilogues ROW, ROW_GELU, ROW_LAYERSCALE, TRANSPOSED (residual, relu_output)
+ * and CONVT of the int8 GEMM. a [m][lda], b [n][ldb] float32, 16-byte
+ * aligned, k, lda, ldb multiples of 4 (pad columns with zeros).
+ * Replaces linear_tiled.glsl / linear_vec*.glsl (src/operators.cpp:882-955),
+ * the GEMM of conv2d (:1528-1676), conv_transpose_nonoverlap (:1807-1861) and
+ * project_tokens (:1408-1452). */
+typedef struct dav2_gemm_f32_args {
+    const float* a;
+    uint64_t lda;
+    const float* b;
+    uint64_t ldb;
+    uint32_t m, n, k;
+    uint32_t epilogue;      /* DAV2_GEMM_EPI_* (not RAW_I32 / ROW_COLMAX)      */
+    const float* bias;      /* [n] (CONVT: [convt_channels]) or NULL = 0      */
+    float* out;
+    uint64_t out_row_offset;
+    uint64_t out_row_stride;
+    const float* residual;  /* LAYERSCALE (may alias out) or TRANSPOSED        */
+    const float* gamma;
+    uint32_t convt_kernel, convt_width, convt_height, convt_channels;
+    uint32_t relu_output;   /* TRANSPOSED only                                 */
+} dav2_gemm_f32_args;
+DAV2_API int dav2_hip_gemm_f32(const dav2_gemm_f32_args* args, void* stream);
+
+/* fp32 im2col of conv2d (src/operators.cpp:1528-1676): out[p][c], p = oy*OW
+ * + ox, c = ic*k*k + ky*k + kx, zero padding, columns C*k*k .. ld-1 zero;
+ * relu != 0 takes max(input, 0) (the DPT residual units' ReLU). */
+DAV2_API int dav2_hip_im2col_f32(const float* input, uint32_t input_width, uint32_t input_height,
+                                 uint32_t input_channels, uint32_t output_width, uint32_t output_height,
+                                 uint32_t kernel, uint32_t stride, int32_t padding, uint32_t relu, float* out,
+                                 uint32_t ld, void* stream);
 /* Row tiles (rows of col_absmax) of a dav2_hip_gemm_i8 call with m rows and
  * n output columns. No reference counterpart: the attention's digit packing
  * reads these maxima instead of a pass over k and v. */

@@ -86,6 +86,33 @@ DAV2_API dav2_status DAV2_CALL dav2_ops_conv_transpose_nonoverlap_int8(
     dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input, dav2_device_buffer int8_weight,
     dav2_device_buffer weight_scales, dav2_device_buffer bias, uint32_t input_width, uint32_t input_height,
     uint32_t input_channels, uint32_t output_channels, uint32_t kernel);
+/* fp32 precision mode (src/operators.h: linear :62-80, project_tokens
+ * :143-152, conv2d :173-187, conv_transpose_nonoverlap :218-227). fp32
+ * weights: linear/projection [N][K], conv [OC][C*k*k], transposed conv rows
+ * (ky*k + kx)*OC + oc of IC columns; K, C*k*k and IC multiples of 4.
+ * prepare_tokens_f32: the fp32 patch embedding, weight [D][3*14*14]. */
+DAV2_API dav2_status DAV2_CALL dav2_ops_linear(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                               dav2_device_buffer weight, dav2_device_buffer bias, uint32_t rows,
+                                               uint32_t input_columns, uint32_t output_columns, int32_t gelu);
+DAV2_API dav2_status DAV2_CALL dav2_ops_project_tokens(dav2_ops* ops, dav2_device_buffer output,
+                                                       dav2_device_buffer tokens, dav2_device_buffer weight,
+                                                       dav2_device_buffer bias, uint32_t width, uint32_t height,
+                                                       uint32_t embedding, uint32_t output_channels);
+DAV2_API dav2_status DAV2_CALL dav2_ops_conv2d(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
+                                               dav2_device_buffer weight, dav2_device_buffer bias,
+                                               uint32_t input_width, uint32_t input_height, uint32_t input_channels,
+                                               uint32_t output_channels, uint32_t kernel, uint32_t stride,
+                                               uint32_t padding, int32_t has_bias);
+DAV2_API dav2_status DAV2_CALL dav2_ops_conv_transpose_nonoverlap(
+    dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input, dav2_device_buffer weight,
+    dav2_device_buffer bias, uint32_t input_width, uint32_t input_height, uint32_t input_channels,
+    uint32_t output_channels, uint32_t kernel);
+DAV2_API dav2_status DAV2_CALL dav2_ops_prepare_tokens_f32(dav2_ops* ops, dav2_device_buffer output,
+                                                           dav2_device_buffer image, dav2_device_buffer patch_weight,
+                                                           dav2_device_buffer patch_bias,
+                                                           dav2_device_buffer class_token,
+                                                           dav2_device_buffer position, uint32_t input_width,
+                                                           uint32_t input_height, uint32_t embedding);
 /* src/operators.h:251-258 */
 DAV2_API dav2_status DAV2_CALL dav2_ops_bilinear_align_true(dav2_ops* ops, dav2_device_buffer output,
                                                             dav2_device_buffer input, uint32_t input_width,

@@ -229,6 +229,7 @@ struct orc_model {
     uint32_t capture[4] = {0, 0, 0, 0};
     uint32_t project[4] = {0, 0, 0, 0};
     std::unordered_map<std::string, Tensor> tensors;
+    bool fp32 = false;  // graph precision of the current inference (fp32 mode vs int8)
 
     const Tensor& t(const std::string& name) const {
         auto it = tensors.find(name);
@@ -1001,6 +1002,117 @@ void orc_conv_transpose_int8(const float* input, const int8_t* w8, const float* 
 }
 
 // ---------------------------------------------------------------------------
+// fp32 precision mode (DAV2_CREATE_FORCE_FP32): the same operators with fp32
+// weights and no quantization. Each dot product is a float32 sum in k order.
+
+namespace {
+// acc[i][j] = sum_k a[i][k] * w[j][k], float32, k ascending.
+void gemm_f32(const float* a, uint64_t lda, const float* w, uint32_t m, uint32_t n, uint32_t k, float* acc) {
+    std::vector<float> wt(static_cast<size_t>(k) * n);
+    for (uint32_t j = 0; j < n; ++j)
+        for (uint32_t kk = 0; kk < k; ++kk) wt[static_cast<size_t>(kk) * n + j] = w[static_cast<size_t>(j) * k + kk];
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(m); ++i) {
+        float* o = acc + static_cast<size_t>(i) * n;
+        std::fill(o, o + n, 0.0f);
+        const float* ai = a + static_cast<size_t>(i) * lda;
+        for (uint32_t kk = 0; kk < k; ++kk) {
+            const float av = ai[kk];
+            const float* wr = wt.data() + static_cast<size_t>(kk) * n;
+            for (uint32_t j = 0; j < n; ++j) o[j] = o[j] + av * wr[j];
+        }
+    }
+}
+}  // namespace
+
+void orc_linear_f32(const float* input, const float* weight, const float* bias, uint32_t rows, uint32_t in_cols,
+                    uint32_t out_cols, int gelu, float* out) {
+    // operators.cpp:882-955: out = x W^T + b, then gelu.glsl when asked
+    gemm_f32(input, in_cols, weight, rows, out_cols, in_cols, out);
+    const size_t count = static_cast<size_t>(rows) * out_cols;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) {
+        const float v = out[i] + (bias ? bias[static_cast<size_t>(i) % out_cols] : 0.0f);
+        out[i] = gelu ? gelu_value(v) : v;
+    }
+}
+
+void orc_conv2d_f32(const float* input, const float* weight, const float* bias, uint32_t width, uint32_t height,
+                    uint32_t ic, uint32_t oc, uint32_t kernel, uint32_t stride, uint32_t padding, int has_bias,
+                    float* out) {
+    // operators.cpp:1528-1676: weight [OC][IC][k][k], CHW in and out
+    const uint32_t ow = (width + 2 * padding - kernel) / stride + 1;
+    const uint32_t oh = (height + 2 * padding - kernel) / stride + 1;
+    const uint32_t rows = ow * oh, K = ic * kernel * kernel;
+    std::vector<float> cols(static_cast<size_t>(rows) * K);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < static_cast<int64_t>(rows); ++r)
+        for (uint32_t c = 0; c < K; ++c)
+            cols[static_cast<size_t>(r) * K + c] = im2col_read(input, width, height, ow, kernel, stride,
+                                                               static_cast<int32_t>(padding),
+                                                               static_cast<uint32_t>(r), c);
+    std::vector<float> acc(static_cast<size_t>(rows) * oc);
+    gemm_f32(cols.data(), K, weight, rows, oc, K, acc.data());
+#pragma omp parallel for schedule(static)
+    for (int64_t o = 0; o < static_cast<int64_t>(oc); ++o)
+        for (uint32_t p = 0; p < rows; ++p)
+            out[static_cast<size_t>(o) * rows + p] =
+                acc[static_cast<size_t>(p) * oc + o] + (has_bias ? bias[o] : 0.0f);
+}
+
+void orc_conv_transpose_f32(const float* input, const float* weight, const float* bias, uint32_t width,
+                            uint32_t height, uint32_t ic, uint32_t oc, uint32_t kernel, float* out) {
+    // operators.cpp:1807-1861, stride == kernel: every output pixel has one
+    // source pixel; weight [IC][OC][k][k]
+    const uint32_t ow = width * kernel, oh = height * kernel;
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t o = 0; o < oc; ++o)
+        for (int64_t oy = 0; oy < oh; ++oy)
+            for (uint32_t ox = 0; ox < ow; ++ox) {
+                const uint32_t iy = static_cast<uint32_t>(oy) / kernel, ky = static_cast<uint32_t>(oy) % kernel;
+                const uint32_t ix = ox / kernel, kx = ox % kernel;
+                float sum = 0.0f;
+                for (uint32_t c = 0; c < ic; ++c)
+                    sum = sum + input[(static_cast<size_t>(c) * height + iy) * width + ix] *
+                                    weight[((static_cast<size_t>(c) * oc + o) * kernel + ky) * kernel + kx];
+                out[(static_cast<size_t>(o) * oh + oy) * ow + ox] = sum + bias[o];
+            }
+}
+
+void orc_project_tokens_f32(const float* tokens, const float* weight, const float* bias, uint32_t width,
+                            uint32_t height, uint32_t D, uint32_t C, float* out) {
+    // operators.cpp:1408-1452: skip CLS, channel-major output
+    const uint32_t spatial = width * height;
+    std::vector<float> acc(static_cast<size_t>(spatial) * C);
+    gemm_f32(tokens + D, D, weight, spatial, C, D, acc.data());
+#pragma omp parallel for schedule(static)
+    for (int64_t c = 0; c < static_cast<int64_t>(C); ++c)
+        for (uint32_t p = 0; p < spatial; ++p)
+            out[static_cast<size_t>(c) * spatial + p] = acc[static_cast<size_t>(p) * C + c] + bias[c];
+}
+
+void orc_prepare_tokens_f32(const float* image, const float* weight, const float* bias, const float* class_token,
+                            const float* position, uint32_t width, uint32_t height, uint32_t D, float* tokens) {
+    // operators.cpp:1211-1406 (fp32 branch): patch conv (k = s = 14) into
+    // rows 1.., the class token in row 0, then the position embedding
+    const uint32_t pw = width / 14, ph = height / 14, spatial = pw * ph;
+    std::vector<float> patches(static_cast<size_t>(D) * spatial);
+    orc_conv2d_f32(image, weight, bias, width, height, 3, D, 14, 14, 0, 1, patches.data());
+    std::memcpy(tokens, class_token, D * sizeof(float));
+    for (uint32_t p = 0; p < spatial; ++p)
+        for (uint32_t d = 0; d < D; ++d)
+            tokens[static_cast<size_t>(p + 1) * D + d] = patches[static_cast<size_t>(d) * spatial + p];
+    std::vector<float> interp(static_cast<size_t>(spatial) * D);
+    orc_position_bicubic(position, pw, ph, D, interp.data());
+    const size_t count = static_cast<size_t>(spatial + 1) * D;
+    for (size_t i = 0; i < count; ++i) {
+        const size_t token = i / D, feature = i % D;
+        const float p = token == 0 ? position[feature] : interp[feature * spatial + (token - 1)];
+        tokens[i] = tokens[i] + p;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Model
 
 static bool use_int8_weight(const std::string& name, const Tensor& t) {
@@ -1101,7 +1213,11 @@ void encoder_block(const orc_model& m, std::vector<float>& cur, uint32_t T, uint
     auto lin = [&](const std::vector<float>& in, const std::string& w, const std::string& bias,
                    uint32_t ic, uint32_t oc, bool gelu, std::vector<float>& out) {
         const Tensor& wt = m.t(w);
-        orc_linear_int8(in.data(), wt.q.data(), wt.qscale.data(), m.t(bias).data.data(), T, ic, oc, gelu, out.data());
+        if (m.fp32)
+            orc_linear_f32(in.data(), wt.data.data(), m.t(bias).data.data(), T, ic, oc, gelu, out.data());
+        else
+            orc_linear_int8(in.data(), wt.q.data(), wt.qscale.data(), m.t(bias).data.data(), T, ic, oc, gelu,
+                            out.data());
     };
     orc_layer_norm(cur.data(), m.t(blk(b, ".norm1.weight")).data.data(), m.t(blk(b, ".norm1.bias")).data.data(),
                    T, D, 1.0e-6f, norm.data());
@@ -1128,6 +1244,11 @@ Map conv(const orc_model& m, const Map& in, const std::string& w, const std::str
     out.c = oc;
     out.v.resize(static_cast<size_t>(out.w) * out.h * oc);
     const Tensor& wt = m.t(w);
+    if (m.fp32) {
+        orc_conv2d_f32(in.v.data(), wt.data.data(), has_bias ? m.t(b).data.data() : nullptr, in.w, in.h, in.c, oc, k,
+                       stride, pad, has_bias ? 1 : 0, out.v.data());
+        return out;
+    }
     if (wt.q.empty()) throw std::runtime_error("oracle: conv weight not int8: " + w);
     orc_conv2d_int8(in.v.data(), wt.q.data(), wt.qscale.data(), has_bias ? m.t(b).data.data() : nullptr,
                     in.w, in.h, in.c, oc, k, stride, pad, has_bias ? 1 : 0, out.v.data());
@@ -1174,6 +1295,15 @@ int orc_model_encoder_blocks(orc_model* model, float* tokens, uint32_t T, uint32
     }
 }
 
+int orc_model_infer_fp32(orc_model* model, const float* chw, uint32_t width, uint32_t height, float* depth,
+                         float* pre_relu, float* features) {
+    // FORCE_FP32: fp32 weights everywhere, fp32 attention (encoder.cpp:389-396)
+    model->fp32 = true;
+    const int rc = orc_model_infer(model, chw, width, height, 0, depth, pre_relu, features);
+    model->fp32 = false;
+    return rc;
+}
+
 int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t height,
                     int fp16, float* depth, float* pre_relu, float* features) {
     try {
@@ -1182,9 +1312,15 @@ int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t
         const size_t n = static_cast<size_t>(T) * D;
         std::vector<float> cur(n);
         const Tensor& pe = m.t("pretrained.patch_embed.proj.weight");
-        orc_prepare_tokens_int8(chw, pe.q.data(), pe.qscale.data(), m.t("pretrained.patch_embed.proj.bias").data.data(),
-                                m.t("pretrained.cls_token").data.data(), m.t("pretrained.pos_embed").data.data(),
-                                width, height, D, cur.data());
+        if (m.fp32)
+            orc_prepare_tokens_f32(chw, pe.data.data(), m.t("pretrained.patch_embed.proj.bias").data.data(),
+                                   m.t("pretrained.cls_token").data.data(), m.t("pretrained.pos_embed").data.data(),
+                                   width, height, D, cur.data());
+        else
+            orc_prepare_tokens_int8(chw, pe.q.data(), pe.qscale.data(),
+                                    m.t("pretrained.patch_embed.proj.bias").data.data(),
+                                    m.t("pretrained.cls_token").data.data(), m.t("pretrained.pos_embed").data.data(),
+                                    width, height, D, cur.data());
         std::vector<std::vector<float>> feats;
         uint32_t ci = 0;
         for (uint32_t b = 0; b < m.blocks; ++b) {
@@ -1206,8 +1342,12 @@ int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t
             proj.w = pw; proj.h = ph; proj.c = m.project[i];
             proj.v.resize(static_cast<size_t>(pw) * ph * proj.c);
             const Tensor& wt = m.t(prefix + ".weight");
-            orc_project_tokens_int8(feats[i].data(), wt.q.data(), wt.qscale.data(), m.t(prefix + ".bias").data.data(),
-                                    pw, ph, D, proj.c, proj.v.data());
+            if (m.fp32)
+                orc_project_tokens_f32(feats[i].data(), wt.data.data(), m.t(prefix + ".bias").data.data(), pw, ph, D,
+                                       proj.c, proj.v.data());
+            else
+                orc_project_tokens_int8(feats[i].data(), wt.q.data(), wt.qscale.data(),
+                                        m.t(prefix + ".bias").data.data(), pw, ph, D, proj.c, proj.v.data());
             if (i < 2) {
                 const uint32_t k = i == 0 ? 4 : 2;
                 const std::string r = "depth_head.resize_layers." + std::to_string(i);
@@ -1215,8 +1355,12 @@ int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t
                 res.w = pw * k; res.h = ph * k; res.c = proj.c;
                 res.v.resize(static_cast<size_t>(res.w) * res.h * res.c);
                 const Tensor& rw = m.t(r + ".weight");
-                orc_conv_transpose_int8(proj.v.data(), rw.q.data(), rw.qscale.data(), m.t(r + ".bias").data.data(),
-                                        pw, ph, proj.c, proj.c, k, res.v.data());
+                if (m.fp32)
+                    orc_conv_transpose_f32(proj.v.data(), rw.data.data(), m.t(r + ".bias").data.data(), pw, ph,
+                                           proj.c, proj.c, k, res.v.data());
+                else
+                    orc_conv_transpose_int8(proj.v.data(), rw.q.data(), rw.qscale.data(),
+                                            m.t(r + ".bias").data.data(), pw, ph, proj.c, proj.c, k, res.v.data());
                 layers[i] = std::move(res);
             } else if (i == 2) {
                 layers[i] = std::move(proj);

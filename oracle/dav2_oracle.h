@@ -130,6 +130,31 @@ void orc_model_free(orc_model* model);
 int orc_model_infer(orc_model* model, const float* chw, uint32_t width,
                     uint32_t height, int fp16_attention, float* depth,
                     float* pre_relu, float* features);
+/* The same graph in the fp32 precision mode (DAV2_CREATE_FORCE_FP32): fp32
+ * weights and activations, fp32 attention. */
+int orc_model_infer_fp32(orc_model* model, const float* chw, uint32_t width,
+                         uint32_t height, float* depth, float* pre_relu,
+                         float* features);
+/* fp32 operators (operators.cpp:882-955, :1211-1452, :1528-1676,
+ * :1807-1861): float32 sums in k order. Weights in the model file layout. */
+void orc_linear_f32(const float* input, const float* weight, const float* bias,
+                    uint32_t rows, uint32_t in_cols, uint32_t out_cols, int gelu,
+                    float* out);
+void orc_conv2d_f32(const float* input, const float* weight, const float* bias,
+                    uint32_t width, uint32_t height, uint32_t in_channels,
+                    uint32_t out_channels, uint32_t kernel, uint32_t stride,
+                    uint32_t padding, int has_bias, float* out);
+void orc_conv_transpose_f32(const float* input, const float* weight,
+                            const float* bias, uint32_t width, uint32_t height,
+                            uint32_t in_channels, uint32_t out_channels,
+                            uint32_t kernel, float* out);
+void orc_project_tokens_f32(const float* tokens, const float* weight,
+                            const float* bias, uint32_t width, uint32_t height,
+                            uint32_t D, uint32_t C, float* out);
+void orc_prepare_tokens_f32(const float* image, const float* weight,
+                            const float* bias, const float* class_token,
+                            const float* position, uint32_t width,
+                            uint32_t height, uint32_t D, float* tokens);
 /* Encoder blocks [first, last) only, on tokens [T][D] in place (timing sample). */
 int orc_model_encoder_blocks(orc_model* model, float* tokens, uint32_t tokens_count,
                              uint32_t first, uint32_t last, int fp16_attention);

@@ -7,7 +7,11 @@ import numpy as np
 
 
 def dev(torch, a: np.ndarray):
-    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    # complete before any other stream (a context's or operator set's own)
+    # reads it
+    t = torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    torch.cuda.current_stream().synchronize()
+    return t
 
 
 def empty(torch, shape, dtype):

@@ -43,6 +43,12 @@ _PROTO = {
     "orc_model_free": (None, [vp]),
     "orc_model_infer": (C.c_int, [vp, vp, u32, u32, C.c_int, vp, vp, vp]),
     "orc_model_encoder_blocks": (C.c_int, [vp, vp, u32, u32, u32, C.c_int]),
+    "orc_model_infer_fp32": (C.c_int, [vp, vp, u32, u32, vp, vp, vp]),
+    "orc_linear_f32": (None, [vp, vp, vp, u32, u32, u32, C.c_int, vp]),
+    "orc_conv2d_f32": (None, [vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, C.c_int, vp]),
+    "orc_conv_transpose_f32": (None, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
+    "orc_project_tokens_f32": (None, [vp, vp, vp, u32, u32, u32, u32, vp]),
+    "orc_prepare_tokens_f32": (None, [vp, vp, vp, vp, vp, u32, u32, u32, vp]),
     "orc_network_shape": (C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "orc_preprocess_bgr8": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, vp]),
     "orc_preprocess_bgra8_nearest": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, vp]),
@@ -303,6 +309,62 @@ class Oracle:
 
     def free_model(self, h) -> None:
         self.lib.orc_model_free(h)
+
+    def infer_fp32(self, h, chw, width: int, height: int):
+        """The graph in the fp32 precision mode; returns (depth, pre-ReLU logits)."""
+        chw = _f32(chw)
+        depth = np.empty((height, width), np.float32)
+        logits = np.empty((height, width), np.float32)
+        if self.lib.orc_model_infer_fp32(h, chw.ctypes.data, width, height, depth.ctypes.data, logits.ctypes.data,
+                                         None) != 0:
+            raise RuntimeError("oracle inference failed")
+        return depth, logits
+
+    def linear_f32(self, x, w, b, gelu: bool = False):
+        x, w = _f32(x), _f32(w)
+        rows, k = x.shape
+        n = w.shape[0]
+        out = np.empty((rows, n), np.float32)
+        self.lib.orc_linear_f32(x.ctypes.data, w.ctypes.data, _p(None if b is None else _f32(b)), rows, k, n,
+                                int(gelu), out.ctypes.data)
+        return out
+
+    def conv2d_f32(self, x, w, b, stride: int, padding: int):
+        x, w = _f32(x), _f32(w)
+        ic, ih, iw = x.shape
+        oc, _, k, _ = w.shape
+        ow, oh = (iw + 2 * padding - k) // stride + 1, (ih + 2 * padding - k) // stride + 1
+        out = np.empty((oc, oh, ow), np.float32)
+        bb = None if b is None else _f32(b)
+        self.lib.orc_conv2d_f32(x.ctypes.data, w.ctypes.data, _p(bb), iw, ih, ic, oc, k, stride, padding,
+                                int(b is not None), out.ctypes.data)
+        return out
+
+    def conv_transpose_f32(self, x, w, b):
+        x, w, b = _f32(x), _f32(w), _f32(b)
+        ic, ih, iw = x.shape
+        _, oc, k, _ = w.shape
+        out = np.empty((oc, ih * k, iw * k), np.float32)
+        self.lib.orc_conv_transpose_f32(x.ctypes.data, w.ctypes.data, b.ctypes.data, iw, ih, ic, oc, k,
+                                        out.ctypes.data)
+        return out
+
+    def project_tokens_f32(self, tokens, w, b, pw: int, ph: int):
+        tokens, w, b = _f32(tokens), _f32(w), _f32(b)
+        c, d = w.shape
+        out = np.empty((c, ph, pw), np.float32)
+        self.lib.orc_project_tokens_f32(tokens.ctypes.data, w.ctypes.data, b.ctypes.data, pw, ph, d, c,
+                                        out.ctypes.data)
+        return out
+
+    def prepare_tokens_f32(self, image, w, b, cls, pos, width: int, height: int):
+        image, w, b, cls, pos = _f32(image), _f32(w), _f32(b), _f32(cls), _f32(pos)
+        d = w.shape[0]
+        t = (width // 14) * (height // 14) + 1
+        out = np.empty((t, d), np.float32)
+        self.lib.orc_prepare_tokens_f32(image.ctypes.data, w.ctypes.data, b.ctypes.data, cls.ctypes.data,
+                                        pos.ctypes.data, width, height, d, out.ctypes.data)
+        return out
 
     def infer(self, h, chw, width: int, height: int, fp16_attention: bool = True, dim: int | None = None):
         chw = _f32(chw)
