@@ -95,6 +95,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=30.0)
     ap.add_argument("--profile-json", default="")
+    ap.add_argument("--no-fp32-mode", action="store_true", help="skip the FORCE_FP32 comparison run")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run one device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -219,6 +220,24 @@ def main() -> int:
         depth = out.cpu().numpy()
         ctx.close()
 
+        # The fp32 precision mode (FORCE_FP32) on the same model and input:
+        # a short run, reported beside the int8 headline.
+        fp32_rate = None
+        if args.batch == 1 and not args.no_fp32_mode:
+            with pkg.Context(str(model), args.encoder, pkg.FORCE_FP32) as ctx32:
+                def step32():
+                    ctx32.infer_device(x.data_ptr(), 1, args.size, args.size, out.data_ptr(), n_out, stream)
+
+                for _ in range(2):
+                    step32()
+                torch.cuda.synchronize()
+                f0 = time.perf_counter()
+                fp32_steps = 5
+                for _ in range(fp32_steps):
+                    step32()
+                torch.cuda.synchronize()
+                fp32_rate = fp32_steps / (time.perf_counter() - f0)
+
         gemm = prof.get("gemm_i8", {})
         g_ms = gemm.get("ms", 0.0)
         g_launches = max(1, gemm.get("launches", 1))
@@ -279,6 +298,7 @@ def main() -> int:
         "profiled_ms_per_step": 1e3 * profiled_elapsed / args.steps,
         "host_entry_images_per_s": host_rate,
         "image_paths": image_paths,
+        "fp32_mode_images_per_s": fp32_rate,
         "depth_finite": bool(np.isfinite(depth).all()),
         "cpu_baseline": cpu,
     }
