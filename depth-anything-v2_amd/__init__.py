@@ -93,6 +93,26 @@ class GemmArgs(C.Structure):
                 ("relu_output", C.c_uint32), ("split_k", C.c_uint32), ("split_scratch", C.c_void_p)]
 
 
+class HipSubmitRequest(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_version", C.c_uint32), ("input", C.c_void_p),
+                ("input_byte_size", C.c_uint64), ("width", C.c_uint32), ("height", C.c_uint32),
+                ("row_stride_bytes", C.c_uint32), ("pixel_format", C.c_uint32), ("input_size", C.c_int32),
+                ("flags", C.c_uint32), ("wait_event", C.c_void_p), ("output", C.c_void_p),
+                ("output_byte_size", C.c_uint64), ("input_offset", C.c_uint64), ("output_offset", C.c_uint64),
+                ("input_ipc", C.c_uint8 * 64), ("output_ipc", C.c_uint8 * 64), ("wait_event_ipc", C.c_uint8 * 64),
+                ("source_frame_id", C.c_uint64), ("timestamp_ns", C.c_uint64)]
+
+
+class GpuJobStatus(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("state", C.c_uint32), ("output_count", C.c_uint32),
+                ("reserved", C.c_uint32), ("source_frame_id", C.c_uint64)]
+
+
+GPU_PIXEL_BGRA8, GPU_PIXEL_RGBA8 = 1, 2
+GPU_JOB_QUEUED, GPU_JOB_RUNNING, GPU_JOB_COMPLETE, GPU_JOB_FAILED, GPU_JOB_CANCELLED = 0, 1, 2, 3, 4
+HIP_SUBMIT_WAIT_EVENT_IPC = 1
+
+
 class GemmF32Args(C.Structure):
     _fields_ = [("a", C.c_void_p), ("lda", C.c_uint64), ("b", C.c_void_p), ("ldb", C.c_uint64),
                 ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("epilogue", C.c_uint32),
@@ -136,6 +156,7 @@ PROTOTYPES = {
     "dav2_submit_d3d12_texture_binding": (C.c_int, [vp, vp, C.POINTER(vp)]),
     "dav2_submit_metal_texture_binding": (C.c_int, [vp, vp, C.POINTER(vp)]),
     "dav2_gpu_job_poll": (C.c_int, [vp, vp]),
+    "dav2_submit_hip": (C.c_int, [vp, vp, C.POINTER(C.c_void_p)]),
     "dav2_gpu_job_cancel": (C.c_int, [vp]),
     "dav2_gpu_job_release": (None, [vp]),
     "dav2_gpu_output_acquire": (C.c_int, [vp, u32, vp, C.POINTER(vp)]),
@@ -182,6 +203,7 @@ PROTOTYPES = {
     "dav2_hip_preprocess_bgr8": (C.c_int, [vp, u32, u32, u64, u32, u32, vp, vp]),
     "dav2_hip_preprocess_bgra8_nearest": (C.c_int, [vp, u32, u32, u64, u32, u32, vp, vp]),
     "dav2_hip_normalize_span": (C.c_int, [vp, vp, u64, vp, vp]),
+    "dav2_hip_preprocess_rgba8": (C.c_int, [vp, u32, u32, u64, u32, u32, u32, vp, vp]),
     "dav2_hip_position_bicubic": (C.c_int, [vp, vp, u32, u32, u32, vp]),
     "dav2_hip_finish_tokens": (C.c_int, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
     "dav2_hip_error_string": (C.c_char_p, [C.c_int]),

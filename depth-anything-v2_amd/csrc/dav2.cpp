@@ -7,6 +7,7 @@
 #include "executor.h"
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstddef>
 #include <cstring>
@@ -258,17 +259,61 @@ dav2_status DAV2_CALL dav2_submit_metal_texture_binding(dav2_context* context,
     return fail(DAV2_STATUS_UNSUPPORTED, "Metal texture bindings are only available on Apple platforms");
 }
 
+// GPU jobs come from dav2_submit_hip (src/dav2.cpp:429-473 semantics).
 dav2_status DAV2_CALL dav2_gpu_job_poll(const dav2_gpu_job* job, dav2_gpu_job_status* status) {
     if (job == nullptr || status == nullptr) return fail(DAV2_STATUS_INVALID_ARGUMENT, "null GPU job poll argument");
-    return fail(DAV2_STATUS_UNSUPPORTED, "GPU jobs are not available on this platform");
+    if (status->struct_size < sizeof(*status))
+        return fail(DAV2_STATUS_INVALID_ARGUMENT, "GPU job status struct is too small");
+    return protect([&] {
+        const dav2_gpu_job_state state = job->implementation->state();
+        *status = {};
+        status->struct_size = sizeof(*status);
+        status->state = state;
+        status->output_count = state == DAV2_GPU_JOB_CANCELLED ? 0u : 1u;
+        status->source_frame_id = job->source_frame_id;
+    });
 }
 
 dav2_status DAV2_CALL dav2_gpu_job_cancel(dav2_gpu_job* job) {
     if (job == nullptr) return fail(DAV2_STATUS_INVALID_ARGUMENT, "GPU job is null");
-    return fail(DAV2_STATUS_UNSUPPORTED, "GPU jobs are not available on this platform");
+    return protect([&] {
+        if (job->implementation->state() == DAV2_GPU_JOB_COMPLETE)
+            throw ApiError(DAV2_STATUS_INVALID_STATE, "completed GPU job cannot be cancelled");
+        job->implementation->cancel();
+    });
 }
 
-void DAV2_CALL dav2_gpu_job_release(dav2_gpu_job*) {}
+void DAV2_CALL dav2_gpu_job_release(dav2_gpu_job* job) { delete job; }
+
+dav2_status DAV2_CALL dav2_submit_hip(dav2_context* context, const dav2_hip_submit_request* request,
+                                     dav2_gpu_job** job) {
+    if (!context || !request || !job) return fail(DAV2_STATUS_INVALID_ARGUMENT, "null HIP submit argument");
+    *job = nullptr;
+    if (request->struct_size < sizeof(*request) || request->abi_version != DAV2_ABI_VERSION)
+        return fail(DAV2_STATUS_INVALID_ARGUMENT, "invalid HIP submit request");
+    return protect([&] {
+        // vulkan_executor.cpp:669-690
+        const dav2_hip_submit_request& r = *request;
+        if (r.width == 0 || r.height == 0 || r.row_stride_bytes < r.width * 4ull || r.row_stride_bytes % 4u ||
+            (r.pixel_format != DAV2_GPU_PIXEL_BGRA8 && r.pixel_format != DAV2_GPU_PIXEL_RGBA8) ||
+            (r.flags & ~static_cast<uint32_t>(DAV2_HIP_SUBMIT_WAIT_EVENT_IPC)) != 0)
+            throw std::invalid_argument("invalid HIP GPU inference request");
+        if (static_cast<uint64_t>(r.row_stride_bytes) * r.height > r.input_byte_size ||
+            r.width > static_cast<uint32_t>(INT32_MAX) || r.height > static_cast<uint32_t>(INT32_MAX))
+            throw std::invalid_argument("HIP GPU input dimensions exceed the buffer");
+        if (r.output_byte_size < static_cast<uint64_t>(r.width) * r.height * sizeof(float))
+            throw ApiError(DAV2_STATUS_BUFFER_TOO_SMALL, "output buffer is too small");
+        if ((r.input && (reinterpret_cast<uintptr_t>(r.input) & 3u)) || (r.input == nullptr && (r.input_offset & 3u)) ||
+            (r.output && (reinterpret_cast<uintptr_t>(r.output) & 3u)) || (r.output == nullptr && (r.output_offset & 3u)))
+            throw std::invalid_argument("HIP GPU buffers must be 4-byte aligned");
+        const dav2_image_shape shape =
+            network_shape(static_cast<int>(r.width), static_cast<int>(r.height), r.input_size);
+        auto result = std::make_unique<dav2_gpu_job>();
+        result->source_frame_id = r.source_frame_id;
+        result->implementation = context->executor->submit_hip(r, shape.width, shape.height);
+        *job = result.release();
+    });
+}
 
 dav2_status DAV2_CALL dav2_gpu_output_acquire(dav2_gpu_job* job, uint32_t, dav2_d3d12_output_descriptor* descriptor,
                                              dav2_gpu_output_lease** lease) {

@@ -192,6 +192,83 @@ std::size_t HipExecutor::upload_image(const char* slot, const std::uint8_t* imag
     return row_bytes;
 }
 
+HipJob::~HipJob() {
+    (void)hipSetDevice(device_);
+    if (done_) {
+        (void)hipEventSynchronize(done_);
+        (void)hipEventDestroy(done_);
+    }
+    if (ipc_wait_) (void)hipEventDestroy(ipc_wait_);
+    if (mapped_input_) (void)hipIpcCloseMemHandle(mapped_input_);
+    if (mapped_output_) (void)hipIpcCloseMemHandle(mapped_output_);
+}
+
+dav2_gpu_job_state HipJob::state() const {
+    if (cancelled_) return DAV2_GPU_JOB_CANCELLED;
+    const hipError_t e = hipEventQuery(done_);
+    if (e == hipSuccess) return DAV2_GPU_JOB_COMPLETE;
+    if (e == hipErrorNotReady) return DAV2_GPU_JOB_QUEUED;
+    return DAV2_GPU_JOB_FAILED;
+}
+
+void HipJob::wait() const { hip_check(hipEventSynchronize(done_), "GPU job wait"); }
+
+std::unique_ptr<HipJob> HipExecutor::submit_hip(const dav2_hip_submit_request& r, int network_width,
+                                                int network_height) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    context_.make_current();
+    ScopedStream scoped(context_, nullptr);
+    const hipStream_t main = context_.active_stream();
+    auto job = std::make_unique<HipJob>();
+    job->device_ = context_.device();
+    hip_check(hipEventCreateWithFlags(&job->done_, hipEventDisableTiming), "job event");
+    // Buffers: this process's pointers, or the other process's allocations
+    // mapped through their IPC handles (held by the job until release).
+    const std::uint8_t* input = static_cast<const std::uint8_t*>(r.input);
+    if (!input) {
+        hipIpcMemHandle_t h;
+        std::memcpy(&h, r.input_ipc, sizeof(h));
+        hip_check(hipIpcOpenMemHandle(&job->mapped_input_, h, hipIpcMemLazyEnablePeerAccess), "open input IPC handle");
+        input = static_cast<const std::uint8_t*>(job->mapped_input_) + r.input_offset;
+    }
+    float* output = r.output;
+    if (!output) {
+        hipIpcMemHandle_t h;
+        std::memcpy(&h, r.output_ipc, sizeof(h));
+        hip_check(hipIpcOpenMemHandle(&job->mapped_output_, h, hipIpcMemLazyEnablePeerAccess),
+                  "open output IPC handle");
+        output = reinterpret_cast<float*>(static_cast<std::uint8_t*>(job->mapped_output_) + r.output_offset);
+    }
+    if (r.flags & DAV2_HIP_SUBMIT_WAIT_EVENT_IPC) {
+        hipIpcEventHandle_t h;
+        std::memcpy(&h, r.wait_event_ipc, sizeof(h));
+        hip_check(hipIpcOpenEventHandle(&job->ipc_wait_, h), "open wait event IPC handle");
+        hip_check(hipStreamWaitEvent(main, job->ipc_wait_, 0), "wait for the producer");
+    } else if (r.wait_event) {
+        hip_check(hipStreamWaitEvent(main, static_cast<hipEvent_t>(r.wait_event), 0), "wait for the producer");
+    }
+    // vulkan_executor.cpp:694-787: GPU preprocessing, inference, min/max
+    // normalisation at the network size, bilinear resize into the output
+    const std::uint64_t net = std::uint64_t(network_width) * network_height;
+    const std::uint64_t pixels = std::uint64_t(r.width) * r.height;
+    DeviceBuffer& in = arena_.get("io.input", net * 3 * sizeof(float));
+    DeviceBuffer& depth = arena_.get("io.output", net * sizeof(float));
+    DeviceBuffer& range = arena_.get("io.range", 2 * sizeof(float));
+    hip_check(dav2_hip_preprocess_rgba8(reinterpret_cast<const std::uint32_t*>(input), r.width, r.height,
+                                        r.row_stride_bytes, static_cast<std::uint32_t>(network_width),
+                                        static_cast<std::uint32_t>(network_height),
+                                        r.pixel_format == DAV2_GPU_PIXEL_RGBA8 ? 1u : 0u, in.as<float>(), main),
+              "preprocess_rgba8");
+    run_graph(in.as<float>(), 1, network_width, network_height, depth.as<float>(), nullptr);
+    operators_.reduce_minmax(depth, range, static_cast<std::uint32_t>(net));
+    operators_.normalize_relative(depth, range, static_cast<std::uint32_t>(net));
+    DeviceBuffer out = DeviceBuffer::view(output, pixels * sizeof(float));
+    operators_.bilinear_align_true(out, depth, static_cast<std::uint32_t>(network_width),
+                                   static_cast<std::uint32_t>(network_height), r.width, r.height, 1);
+    hip_check(hipEventRecord(job->done_, main), "job event");
+    return job;
+}
+
 void HipExecutor::infer_bgr8(const std::uint8_t* bgr, int width, int height, std::size_t stride, int network_width,
                              int network_height, float* output) {
     std::lock_guard<std::mutex> lock(mutex_);

@@ -12,6 +12,26 @@
 
 namespace dav2 {
 
+// A submitted GPU inference (dav2_submit_hip): its completion event, the IPC
+// mappings and event it holds until release, and the cancel flag.
+class HipJob {
+public:
+    ~HipJob();
+    // DAV2_GPU_JOB_* state: QUEUED until the GPU work has finished.
+    dav2_gpu_job_state state() const;
+    void cancel() { cancelled_ = true; }
+    void wait() const;
+
+private:
+    friend class HipExecutor;
+    int device_ = 0;
+    hipEvent_t done_ = nullptr;
+    hipEvent_t ipc_wait_ = nullptr;
+    void* mapped_input_ = nullptr;
+    void* mapped_output_ = nullptr;
+    bool cancelled_ = false;
+};
+
 class HipExecutor {
 public:
     HipExecutor(const std::string& model_path, dav2_encoder encoder, int device_index, std::uint32_t flags);
@@ -33,6 +53,10 @@ public:
                     int network_height, float* output);
     void infer_bgra8_normalized(const std::uint8_t* bgra, int width, int height, std::size_t stride,
                                 int network_width, int network_height, float* output);
+    // dav2_submit_hip: enqueue the zero-copy GPU path; the request has been
+    // validated by the caller.
+    std::unique_ptr<HipJob> submit_hip(const dav2_hip_submit_request& request, int network_width,
+                                       int network_height);
 
 private:
     // Uploads `height` rows of `row_bytes` (`stride` bytes apart) into the
@@ -109,7 +133,11 @@ private:
 
 }  // namespace dav2
 
-// Opaque handle of the public ABI.
+// Opaque handles of the public ABI.
 struct dav2_context {
     std::unique_ptr<dav2::HipExecutor> executor;
+};
+struct dav2_gpu_job {
+    std::unique_ptr<dav2::HipJob> implementation;
+    std::uint64_t source_frame_id = 0;
 };

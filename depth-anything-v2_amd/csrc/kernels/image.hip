@@ -4,6 +4,8 @@
 //    the network size, OpenCV-style separable cubic resize (image.cpp:163-270);
 //  - preprocess_bgra8_nearest_kernel: BGRA bytes -> channels in byte order,
 //    floor-nearest resize (image.cpp:289-339);
+//  - preprocess_rgba8_kernel: the GPU submit path's float32 cubic resize of
+//    BGRA / RGBA words (preprocess_rgba.glsl);
 //  - normalize_span_kernel: (x - min) / (max - min) (dav2.cpp:787-800).
 // One thread per destination pixel. Every float32 / float64 step is the same
 // IEEE operation, in the same order, as the reference's C++ (the build turns
@@ -97,6 +99,67 @@ __global__ __launch_bounds__(kTileX* kTileY) void preprocess_bgra8_nearest_kerne
         out[ch * plane + o] = div_rn(div_rn(static_cast<float>(bytes[ch]), 255.0f) - mean[ch], stddev[ch]);
 }
 
+// preprocess_rgba.glsl (src/gpu_preprocess.cpp:41-104): the GPU submit
+// path's resize, all in float32 -- coordinate ((d + 0.5) * src) / dst - 0.5,
+// weights cubic2(f + 1), cubic1(f), cubic1(1 - f), cubic2(2 - f), row and
+// column sums from 0 in tap order, byte / 255 and (v - mean) / std divided.
+DAV2_DEV float rgba_cubic1(float v) { return ((1.25f * v - 2.25f) * v) * v + 1.0f; }
+DAV2_DEV float rgba_cubic2(float v) {
+    const float a = -0.75f;
+    return ((a * v - 5.0f * a) * v + 8.0f * a) * v - 4.0f * a;
+}
+
+DAV2_DEV void rgba_taps(uint32_t d, uint32_t src, uint32_t dst, int idx[4], float c[4]) {
+    const float coord = div_rn((static_cast<float>(d) + 0.5f) * static_cast<float>(src), static_cast<float>(dst)) - 0.5f;
+    const int base = static_cast<int>(floorf(coord));
+    const float f = coord - static_cast<float>(base);
+    c[0] = rgba_cubic2(f + 1.0f);
+    c[1] = rgba_cubic1(f);
+    c[2] = rgba_cubic1(1.0f - f);
+    c[3] = rgba_cubic2(2.0f - f);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) idx[t] = min(max(base - 1 + t, 0), static_cast<int>(src) - 1);
+}
+
+__global__ __launch_bounds__(kTileX* kTileY) void preprocess_rgba8_kernel(const uint32_t* __restrict__ pixels,
+                                                                           uint32_t width, uint32_t height,
+                                                                           uint32_t stride_pixels, uint32_t dst_width,
+                                                                           uint32_t dst_height, uint32_t rgba_order,
+                                                                           float* __restrict__ out) {
+    const uint32_t dx = blockIdx.x * kTileX + threadIdx.x % kTileX;
+    const uint32_t dy = blockIdx.y * kTileY + threadIdx.x / kTileX;
+    if (dx >= dst_width || dy >= dst_height) return;
+    int xs[4], ys[4];
+    float cx[4], cy[4];
+    rgba_taps(dx, width, dst_width, xs, cx);
+    rgba_taps(dy, height, dst_height, ys, cy);
+    uint32_t px[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) px[t][k] = pixels[static_cast<uint64_t>(ys[t]) * stride_pixels + xs[k]];
+    const float mean[3] = {0.485f, 0.456f, 0.406f}, stddev[3] = {0.229f, 0.224f, 0.225f};
+    // channel 0 is red: byte 0 of an RGBA pixel, byte 2 of a BGRA one
+    const uint32_t shifts[3] = {rgba_order ? 0u : 16u, 8u, rgba_order ? 16u : 0u};
+    const uint64_t plane = static_cast<uint64_t>(dst_width) * dst_height;
+    const uint64_t o = static_cast<uint64_t>(dy) * dst_width + dx;
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) {
+        float resized = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float row = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float v = div_rn(static_cast<float>((px[t][k] >> shifts[ch]) & 255u), 255.0f);
+                row = row + v * cx[k];
+            }
+            resized = resized + row * cy[t];
+        }
+        out[ch * plane + o] = div_rn(resized - mean[ch], stddev[ch]);
+    }
+}
+
 __global__ __launch_bounds__(256) void normalize_span_kernel(const float* __restrict__ depth,
                                                              const float* __restrict__ range, uint64_t count,
                                                              float* __restrict__ out) {
@@ -136,6 +199,20 @@ int dav2_hip_preprocess_bgra8_nearest(const uint8_t* bgra, uint32_t width, uint3
                        static_cast<hipStream_t>(stream), bgra, width, height, stride, dst_width, dst_height,
                        static_cast<float>(width) / static_cast<float>(dst_width),
                        static_cast<float>(height) / static_cast<float>(dst_height), out);
+    return hipGetLastError();
+}
+
+int dav2_hip_preprocess_rgba8(const uint32_t* pixels, uint32_t width, uint32_t height, uint64_t stride_bytes,
+                              uint32_t dst_width, uint32_t dst_height, uint32_t rgba_order, float* out, void* stream) {
+    // gpu_preprocess.cpp:50-88
+    if (!pixels || !out || width == 0 || height == 0 || dst_width == 0 || dst_height == 0 || stride_bytes % 4u ||
+        stride_bytes < 4ull * width || stride_bytes / 4u > 0xffffffffull || width > (1u << 24) ||
+        height > (1u << 24) || dst_width > (1u << 24) || dst_height > kTileY * 65535u)
+        return hipErrorInvalidValue;
+    const dim3 grid(ceil_div(dst_width, kTileX), ceil_div(dst_height, kTileY));
+    hipLaunchKernelGGL(preprocess_rgba8_kernel, grid, dim3(kTileX * kTileY), 0, static_cast<hipStream_t>(stream),
+                       pixels, width, height, static_cast<uint32_t>(stride_bytes / 4u), dst_width, dst_height,
+                       rgba_order, out);
     return hipGetLastError();
 }
 

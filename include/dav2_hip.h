@@ -294,6 +294,13 @@ DAV2_API int dav2_hip_preprocess_bgra8_nearest(const uint8_t* bgra, uint32_t wid
                                                float* out, void* stream);
 DAV2_API int dav2_hip_normalize_span(const float* depth, const float* range, uint64_t count, float* out,
                                      void* stream);
+/* preprocess_rgba.glsl (src/gpu_preprocess.cpp:41-104, the resize of the
+ * GPU submit path): 32-bit pixels, rgba_order 1 = R in byte 0 (RGBA8), 0 =
+ * R in byte 2 (BGRA8); stride a multiple of 4 bytes; float32 cubic resize to
+ * the normalised RGB CHW [3][dst_height][dst_width]. */
+DAV2_API int dav2_hip_preprocess_rgba8(const uint32_t* pixels, uint32_t width, uint32_t height,
+                                       uint64_t stride_bytes, uint32_t dst_width, uint32_t dst_height,
+                                       uint32_t rgba_order, float* out, void* stream);
 
 /* position_bicubic.glsl:76-105 with the set-up of src/operators.cpp:1323-1376:
  * position is the [1370][D] pos_embed, out is CHW [D][ph][pw]. */

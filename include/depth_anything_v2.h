@@ -352,6 +352,51 @@ DAV2_API dav2_status DAV2_CALL dav2_infer_tensor_f32_device(
     size_t output_count, void* hip_stream);
 
 /*
+ * HIP counterpart of dav2_submit_d3d12 (the reference's zero-copy GPU
+ * submission, src/vulkan_executor.cpp:656-800; request layout after
+ * dav2_d3d12_submit_request). The input is a device buffer of BGRA8 or RGBA8
+ * pixels and the output a device buffer of width*height float32, each given
+ * as a pointer in this process or, when the pointer is NULL, as a HIP IPC
+ * memory handle exported by another process (plus a byte offset into that
+ * allocation). The work waits for an optional HIP event (wait_event, or the
+ * IPC event handle when DAV2_HIP_SUBMIT_WAIT_EVENT_IPC is set), then runs the
+ * GPU preprocessing (float32 cubic resize to network_shape(width, height,
+ * input_size)), the inference, min/max normalisation and the bilinear resize
+ * back to width x height, on the device and without host copies. The returned
+ * job works with dav2_gpu_job_poll (QUEUED until the GPU work has finished,
+ * then COMPLETE), dav2_gpu_job_cancel (CANCELLED: the GPU work still runs,
+ * its output is not to be used) and dav2_gpu_job_release (waits for the GPU
+ * work, closes IPC mappings, frees the job).
+ */
+typedef struct dav2_hip_submit_request {
+    uint32_t struct_size;
+    uint32_t abi_version;
+    const void* input;          /* device pointer, or NULL: input_ipc */
+    uint64_t input_byte_size;   /* readable bytes from input (or from the mapping + input_offset) */
+    uint32_t width;
+    uint32_t height;
+    uint32_t row_stride_bytes;  /* multiple of 4, >= 4 * width */
+    uint32_t pixel_format;      /* DAV2_GPU_PIXEL_BGRA8 or DAV2_GPU_PIXEL_RGBA8 */
+    int32_t input_size;
+    uint32_t flags;             /* DAV2_HIP_SUBMIT_* */
+    void* wait_event;           /* hipEvent_t, or NULL */
+    float* output;              /* device pointer, or NULL: output_ipc */
+    uint64_t output_byte_size;  /* >= 4 * width * height */
+    uint64_t input_offset;
+    uint64_t output_offset;
+    uint8_t input_ipc[64];      /* hipIpcMemHandle_t */
+    uint8_t output_ipc[64];     /* hipIpcMemHandle_t */
+    uint8_t wait_event_ipc[64]; /* hipIpcEventHandle_t */
+    uint64_t source_frame_id;
+    uint64_t timestamp_ns;
+} dav2_hip_submit_request;
+
+enum { DAV2_HIP_SUBMIT_WAIT_EVENT_IPC = 1u };
+
+DAV2_API dav2_status DAV2_CALL dav2_submit_hip(
+    dav2_context* context, const dav2_hip_submit_request* request, dav2_gpu_job** job);
+
+/*
  * Relative-depth normalisation on device: reduce_minmax + normalize_relative
  * over count floats in place (reference semantics: src/operators.cpp:2050-2071,
  * used by src/vulkan_executor.cpp:759-787).

@@ -854,6 +854,55 @@ void orc_preprocess_bgra8_nearest(const uint8_t* bgra, int width, int height, in
     }
 }
 
+namespace {
+// preprocess_rgba.glsl:19-35 in float32
+float rgba_cubic1(float v) { return ((1.25f * v - 2.25f) * v) * v + 1.0f; }
+float rgba_cubic2(float v) {
+    const float a = -0.75f;
+    return ((a * v - 5.0f * a) * v + 8.0f * a) * v - 4.0f * a;
+}
+}  // namespace
+
+void orc_preprocess_rgba8(const uint32_t* pixels, int width, int height, int64_t stride_pixels, int dst_width,
+                          int dst_height, int rgba_order, float* out) {
+    // preprocess_rgba.glsl:50-101 (src/gpu_preprocess.cpp:41-104)
+    const float mean[3] = {0.485f, 0.456f, 0.406f}, dev[3] = {0.229f, 0.224f, 0.225f};
+    const size_t plane = static_cast<size_t>(dst_width) * dst_height;
+    auto taps = [](int d, int src, int dst, int idx[4], float c[4]) {
+        const float coord = (static_cast<float>(d) + 0.5f) * static_cast<float>(src) / static_cast<float>(dst) - 0.5f;
+        const int base = static_cast<int>(std::floor(coord));
+        const float f = coord - static_cast<float>(base);
+        c[0] = rgba_cubic2(f + 1.0f);
+        c[1] = rgba_cubic1(f);
+        c[2] = rgba_cubic1(1.0f - f);
+        c[3] = rgba_cubic2(2.0f - f);
+        for (int t = 0; t < 4; ++t) idx[t] = std::min(std::max(base - 1 + t, 0), src - 1);
+    };
+    for (int dy = 0; dy < dst_height; ++dy) {
+        int ys[4];
+        float cy[4];
+        taps(dy, height, dst_height, ys, cy);
+        for (int dx = 0; dx < dst_width; ++dx) {
+            int xs[4];
+            float cx[4];
+            taps(dx, width, dst_width, xs, cx);
+            for (int ch = 0; ch < 3; ++ch) {
+                const int shift = ch == 1 ? 8 : ((ch == 0) == (rgba_order != 0) ? 0 : 16);
+                float resized = 0.0f;
+                for (int t = 0; t < 4; ++t) {
+                    float row = 0.0f;
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t p = pixels[ys[t] * stride_pixels + xs[k]];
+                        row = row + static_cast<float>((p >> shift) & 255u) / 255.0f * cx[k];
+                    }
+                    resized = resized + row * cy[t];
+                }
+                out[ch * plane + static_cast<size_t>(dy) * dst_width + dx] = (resized - mean[ch]) / dev[ch];
+            }
+        }
+    }
+}
+
 void orc_normalize_span(const float* depth, uint64_t count, float* out) {
     // dav2.cpp:787-800 (relative models): min and max over the map.
     if (count == 0) return;

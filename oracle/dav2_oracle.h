@@ -177,6 +177,11 @@ void orc_preprocess_bgra8_nearest(const uint8_t* bgra, int width, int height,
                                   int64_t stride, int dst_width,
                                   int dst_height, float* out);
 void orc_normalize_span(const float* depth, uint64_t count, float* out);
+/* preprocess_rgba.glsl (src/gpu_preprocess.cpp:41-104): float32 cubic
+ * resize of 32-bit pixels (rgba_order 1: R in byte 0; 0: BGRA, R in byte 2). */
+void orc_preprocess_rgba8(const uint32_t* pixels, int width, int height,
+                          int64_t stride_pixels, int dst_width, int dst_height,
+                          int rgba_order, float* out);
 
 /* IEEE binary16 round-to-nearest-even helpers used by the fp16 attention path. */
 uint16_t orc_float_to_half(float value);

@@ -53,6 +53,7 @@ _PROTO = {
     "orc_preprocess_bgr8": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, vp]),
     "orc_preprocess_bgra8_nearest": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, vp]),
     "orc_normalize_span": (None, [vp, u64, vp]),
+    "orc_preprocess_rgba8": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, C.c_int, vp]),
     "orc_float_to_half": (C.c_uint16, [f32]),
     "orc_half_to_float": (f32, [C.c_uint16]),
     "orc_crc32": (C.c_uint32, [vp, sz]),
@@ -246,6 +247,16 @@ class Oracle:
         out = np.empty((3, dst_height, dst_width), np.float32)
         self.lib.orc_preprocess_bgra8_nearest(buf.ctypes.data, width, height, stride, dst_width, dst_height,
                                               out.ctypes.data)
+        return out
+
+    def preprocess_rgba8(self, words, width: int, height: int, stride_pixels: int, dst_width: int, dst_height: int,
+                         rgba: bool):
+        """words: uint32 pixels, `height` rows of `stride_pixels`."""
+        words = np.ascontiguousarray(words, dtype=np.uint32)
+        assert words.size >= (height - 1) * stride_pixels + width
+        out = np.empty((3, dst_height, dst_width), np.float32)
+        self.lib.orc_preprocess_rgba8(words.ctypes.data, width, height, stride_pixels, dst_width, dst_height, int(rgba),
+                                      out.ctypes.data)
         return out
 
     def normalize_span(self, d):

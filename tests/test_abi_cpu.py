@@ -118,6 +118,10 @@ def test_null_context_entry_points(pkg, lib):
     img = (C.c_uint8 * 48)()
     assert lib.dav2_infer_bgr8(None, img, 4, 4, 12, 518, x, 16) == 1
     assert lib.dav2_inferbridge_bgra8_f32(None, img, 4, 4, 16, 518, x, 16) == 1
+    job = C.c_void_p()
+    assert lib.dav2_submit_hip(None, None, C.byref(job)) == 1
+    assert lib.dav2_gpu_job_cancel(None) == 1
+    lib.dav2_gpu_job_release(None)  # safe
     assert lib.dav2_profile_enable(None, 1) == 1
     lib.dav2_destroy(None)  # safe (src/dav2.cpp:227-229)
     assert lib.dav2_gpu_job_cancel(None) == 1

@@ -140,3 +140,40 @@ def test_normalize_span(oracle):
     span = np.float32(d.max() - d.min())
     assert np.array_equal(got, (d - d.min()) / span)
     assert np.array_equal(oracle.normalize_span(np.full(10, 2.5, np.float32)), np.zeros(10, np.float32))
+
+
+def _words(img):
+    """uint8 [H][W][4] -> uint32 little-endian pixel words."""
+    return np.ascontiguousarray(img).view(np.uint32).reshape(img.shape[0], img.shape[1])
+
+
+def test_preprocess_rgba8_identity_is_normalisation(oracle):
+    # preprocess_rgba.glsl at scale 1: every fraction is 0 and the weights are
+    # exactly (0, 1, 0, 0); R is byte 0 of an RGBA word and byte 2 of BGRA.
+    rng = np.random.default_rng(4)
+    w, h = 30, 17
+    img = rng.integers(0, 256, size=(h, w, 4), dtype=np.uint8)
+    mean = np.array([0.485, 0.456, 0.406], np.float32)[:, None, None]
+    std = np.array([0.229, 0.224, 0.225], np.float32)[:, None, None]
+    for rgba, order in ((True, [0, 1, 2]), (False, [2, 1, 0])):
+        got = oracle.preprocess_rgba8(_words(img), w, h, w, w, h, rgba)
+        rgb = img[:, :, order].transpose(2, 0, 1).astype(np.float32)
+        assert np.array_equal(got, (rgb / np.float32(255.0) - mean) / std)
+
+
+def test_preprocess_rgba8_close_to_reference_cpu_resize(oracle, ref_lib):
+    # The float32 GPU resize and the reference's float64 CPU resize
+    # (image.cpp, built from its sources) are the same cubic filter up to
+    # rounding; the GPU path rounds the sample coordinate to float32 first
+    # (an ulp of 600 is 6e-5 of a pixel), so they agree to 1e-4.
+    _ref_setup(ref_lib)
+    rng = np.random.default_rng(5)
+    for (w, h, s) in ((97, 61, 140), (640, 480, 518), (300, 17, 56)):
+        img = rng.integers(0, 256, size=(h, w, 4), dtype=np.uint8)
+        dw, dh = oracle.network_shape(w, h, s)
+        got = oracle.preprocess_rgba8(_words(img), w, h, w, dw, dh, False)  # BGRA
+        bgr = np.ascontiguousarray(img[:, :, :3])
+        want = np.empty_like(got)
+        err = C.create_string_buffer(256)
+        assert ref_lib.ref_preprocess_bgr8(bgr.ctypes.data, w, h, 3 * w, dw, dh, want.ctypes.data, err, 256) == 0
+        assert np.abs(got - want).max() < 1e-4
