@@ -10,6 +10,23 @@
 namespace dav2 {
 
 namespace {
+// Orders a call's work after the previous call's (which may have been
+// enqueued on another stream: the context's own or a caller's) and marks the
+// call's end for the next one.
+class CallOrder {
+public:
+    CallOrder(hipEvent_t done, hipStream_t stream) : done_(done), stream_(stream) {
+        hip_check(hipStreamWaitEvent(stream_, done_, 0), "order after the previous call");
+    }
+    ~CallOrder() { (void)hipEventRecord(done_, stream_); }
+    CallOrder(const CallOrder&) = delete;
+    CallOrder& operator=(const CallOrder&) = delete;
+
+private:
+    hipEvent_t done_;
+    hipStream_t stream_;
+};
+
 Precision attention_precision_for(std::uint32_t flags) {
     // src/encoder.cpp:389-396: int8 mode uses binary16 attention operands
     // (the fused kernel) unless FORCE_FP32(_ATTENTION) asks for fp32 scores.
@@ -34,6 +51,7 @@ HipExecutor::HipExecutor(const std::string& model_path, dav2_encoder encoder, in
     hip_check(hipStreamCreateWithFlags(&side_stream_, hipStreamNonBlocking), "side stream");
     for (hipEvent_t& e : captured_) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "capture event");
     hip_check(hipEventCreateWithFlags(&side_done_, hipEventDisableTiming), "side event");
+    hip_check(hipEventCreateWithFlags(&call_done_, hipEventDisableTiming), "call event");
     side_operators_.set_stream(side_stream_);
     // Graph replay is opt-in: on MI355X the eager launches of the ViT-L 518
     // inference measured 2-3% faster than replaying its captured graph.
@@ -50,6 +68,7 @@ HipExecutor::~HipExecutor() {
     for (hipEvent_t e : captured_)
         if (e) (void)hipEventDestroy(e);
     if (side_done_) (void)hipEventDestroy(side_done_);
+    if (call_done_) (void)hipEventDestroy(call_done_);
     if (side_stream_) (void)hipStreamDestroy(side_stream_);
 }
 
@@ -141,6 +160,7 @@ void HipExecutor::infer(const float* input, int width, int height, float* output
     std::lock_guard<std::mutex> lock(mutex_);
     context_.make_current();
     ScopedStream scoped(context_, nullptr);
+    CallOrder order(call_done_, context_.active_stream());
     const std::uint64_t in_elems = std::uint64_t(width) * height * 3;
     const std::uint64_t out_elems = std::uint64_t(width) * height;
     DeviceBuffer& in = arena_.get("io.input", in_elems * sizeof(float));
@@ -155,6 +175,7 @@ void HipExecutor::infer_device(const float* input, int batch, int width, int hei
     std::lock_guard<std::mutex> lock(mutex_);
     context_.make_current();
     ScopedStream scoped(context_, stream);
+    CallOrder order(call_done_, context_.active_stream());
     run_graph(input, batch, width, height, output, pre_relu);
 }
 
@@ -162,6 +183,7 @@ void HipExecutor::normalize_relative_device(float* depth, std::uint64_t count, h
     std::lock_guard<std::mutex> lock(mutex_);
     context_.make_current();
     ScopedStream scoped(context_, stream);
+    CallOrder order(call_done_, context_.active_stream());
     if (count == 0 || count > 0xffffffffull) throw std::invalid_argument("invalid relative depth count");
     DeviceBuffer d = DeviceBuffer::view(depth, count * sizeof(float));
     DeviceBuffer& range = arena_.get("io.range", 2 * sizeof(float));
@@ -218,6 +240,7 @@ std::unique_ptr<HipJob> HipExecutor::submit_hip(const dav2_hip_submit_request& r
     std::lock_guard<std::mutex> lock(mutex_);
     context_.make_current();
     ScopedStream scoped(context_, nullptr);
+    CallOrder order(call_done_, context_.active_stream());
     const hipStream_t main = context_.active_stream();
     auto job = std::make_unique<HipJob>();
     job->device_ = context_.device();
@@ -274,6 +297,7 @@ void HipExecutor::infer_bgr8(const std::uint8_t* bgr, int width, int height, std
     std::lock_guard<std::mutex> lock(mutex_);
     context_.make_current();
     ScopedStream scoped(context_, nullptr);
+    CallOrder order(call_done_, context_.active_stream());
     const std::uint64_t row_bytes = std::uint64_t(width) * 3;
     const std::uint64_t net = std::uint64_t(network_width) * network_height;
     const std::uint64_t pixels = std::uint64_t(width) * height;
@@ -305,6 +329,7 @@ void HipExecutor::infer_bgra8_normalized(const std::uint8_t* bgra, int width, in
     std::lock_guard<std::mutex> lock(mutex_);
     context_.make_current();
     ScopedStream scoped(context_, nullptr);
+    CallOrder order(call_done_, context_.active_stream());
     const std::uint64_t row_bytes = std::uint64_t(width) * 4;
     const std::uint64_t net = std::uint64_t(network_width) * network_height;
     if (net > 0xffffffffull) throw std::invalid_argument("network size too large");

@@ -108,6 +108,9 @@ private:
     hipStream_t side_stream_ = nullptr;
     hipEvent_t captured_[4] = {nullptr, nullptr, nullptr, nullptr};
     hipEvent_t side_done_ = nullptr;
+    // End of the previous call's work on whichever stream it ran: every call
+    // waits for it first, since all calls share the arena buffers.
+    hipEvent_t call_done_ = nullptr;
     struct GraphKey {
         const float* input = nullptr;
         float* output = nullptr;
