@@ -89,6 +89,49 @@ def test_batched_device_entry_matches_single(gpu, pkg, lib, models):
         assert np.array_equal(got[b], singles[b])
 
 
+def test_depth_parity_1036_tokens(gpu, pkg, lib, oracle, models):
+    # The 1036x1036 configuration's token count (74 x 74 patches + CLS =
+    # 5477) on the ViT-S model, bit-exact against the oracle in int8 mode.
+    torch = gpu
+    width = height = 1036
+    print("case: vits 1036x1036 int8", flush=True)
+    x = pkg.dav2_format.imagenet_input(width, height, seed=SEED + 11)[0]
+    xd = dev(torch, x)
+    d = empty(torch, (height, width), torch.float32)
+    logits = empty(torch, (height, width), torch.float32)
+    with pkg.Context(str(models["vits"]), "vits") as ctx:
+        assert lib.dav2_infer_tensor_f32_device_logits(ctx.handle, xd.data_ptr(), width, height, d.data_ptr(),
+                                                       logits.data_ptr(), torch.cuda.current_stream().cuda_stream) == 0
+        d, logits = host(torch, d), host(torch, logits)
+    h = oracle.load_model(models["vits"], ENC["vits"])
+    try:
+        ref_depth, ref_logits, _ = oracle.infer(h, x, width, height, fp16_attention=True)
+    finally:
+        oracle.free_model(h)
+    assert np.array_equal(logits.view(np.uint32), ref_logits.view(np.uint32))
+    assert np.array_equal(d.view(np.uint32), ref_depth.view(np.uint32))
+
+
+def test_vitl_1036_batch4_equals_singles(gpu, pkg, lib, models):
+    # ViT-L + DPT at 1036x1036, batch 4 (the large-input configuration): the
+    # batched device entry gives each image exactly its single-image result.
+    torch = gpu
+    width = height = 1036
+    print("case: vitl 1036x1036 batch 4", flush=True)
+    xs = pkg.dav2_format.imagenet_input(width, height, seed=SEED + 12, batch=4)
+    xd = dev(torch, xs)
+    out = empty(torch, (4, height, width), torch.float32)
+    single = empty(torch, (height, width), torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    with pkg.Context(str(models["vitl"]), "vitl") as ctx:
+        ctx.infer_device(xd.data_ptr(), 4, width, height, out.data_ptr(), out.numel(), stream)
+        got = host(torch, out)
+        assert np.isfinite(got).all()
+        for b in range(4):
+            ctx.infer_device(xd[b].data_ptr(), 1, width, height, single.data_ptr(), single.numel(), stream)
+            assert np.array_equal(host(torch, single).view(np.uint32), got[b].view(np.uint32))
+
+
 def test_graph_replays_match_eager(gpu, pkg, lib, models, monkeypatch):
     # The first inference at a given (input, output, size, stream) runs
     # eagerly, the second captures a HIP graph, later ones replay it. Every
