@@ -126,10 +126,11 @@ class ConvArgs(C.Structure):
     _fields_ = [("input", C.c_void_p), ("width", C.c_uint32), ("height", C.c_uint32), ("channels", C.c_uint32),
                 ("kernel", C.c_uint32), ("weight", C.c_void_p), ("weight_scales", C.c_void_p), ("bias", C.c_void_p),
                 ("out_channels", C.c_uint32), ("out", C.c_void_p), ("scratch", C.c_void_p),
-                ("scratch_floats", C.c_uint64), ("flags", C.c_uint32), ("residual", C.c_void_p)]
+                ("scratch_floats", C.c_uint64), ("flags", C.c_uint32), ("residual", C.c_void_p),
+                ("partial_in", C.c_void_p), ("partial_out", C.c_void_p)]
 
 
-CONV_RELU_INPUT, CONV_RELU_OUTPUT = 1, 2
+CONV_RELU_INPUT, CONV_RELU_OUTPUT, CONV_EMIT_ABSMAX, CONV_EMIT_RELU_MAX = 1, 2, 4, 8
 
 
 vp, u32, i32, u64, f32, sz = C.c_void_p, C.c_uint32, C.c_int32, C.c_uint64, C.c_float, C.c_size_t
@@ -195,6 +196,8 @@ PROTOTYPES = {
     "dav2_hip_attention_fused": (C.c_int, [vp, vp, u32, u32, u32, vp, u64, vp]),
     "dav2_hip_attention_fused_colmax": (C.c_int, [vp, vp, u32, u32, vp, u32, vp, u64, vp]),
     "dav2_hip_bilinear_align_true": (C.c_int, [vp, vp, u32, u32, u32, u32, u32, vp]),
+    "dav2_hip_bilinear_align_true_maxima": (C.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
+    "dav2_hip_conv2d_i8_emits": (C.c_int, [u32, u32]),
     "dav2_hip_minmax_partials": (u32, [u64]),
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),
     "dav2_hip_normalize_relative": (C.c_int, [vp, vp, u64, vp]),

@@ -190,7 +190,7 @@ DptHead::DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operator
 
 FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::string& weight, const std::string& bias,
                          std::uint32_t oc, std::uint32_t k, std::uint32_t stride, std::uint32_t pad, bool has_bias,
-                         Arena& arena, const std::string& slot, const ConvFusion& fusion) {
+                         Arena& arena, const std::string& slot, const ConvFusion& fusion, Emit emit) {
     // dpt.cpp:479-535, every convolution through conv2d_int8
     FeatureMap out;
     out.width = (in.width + 2 * pad - k) / stride + 1;
@@ -205,8 +205,37 @@ FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::str
         return out;
     }
     if (!w.int8_buffer) throw std::runtime_error("convolution weight is not int8: " + weight);
-    ops.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc, k,
-                    stride, pad, has_bias, &w.int8_tapmajor, fusion);
+    // Group maxima: the input's when its producer wrote them in the mode this
+    // convolution reads (max(x, 0) under an input ReLU); the output's when
+    // the consumer asked (same values as computing them afterwards: max is
+    // exact and order-free).
+    ConvFusion f = fusion;
+    if (in.maxima && in.maxima_relu == f.relu_input) f.input_maxima = in.maxima;
+    DeviceBuffer* maxima = nullptr;
+    if (emit != Emit::none && oc % 32 == 0) {
+        maxima = &arena.get(slot + ".max", std::uint64_t(oc / 32) * out.width * out.height * sizeof(float));
+        f.emit_maxima = maxima;
+        f.emit_relu = emit == Emit::relu;
+    }
+    if (ops.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc,
+                        k, stride, pad, has_bias, &w.int8_tapmajor, f)) {
+        out.maxima = maxima;
+        out.maxima_relu = emit == Emit::relu;
+    }
+    return out;
+}
+
+FeatureMap DptHead::resize(HipOperators& ops, const FeatureMap& in, std::uint32_t ow, std::uint32_t oh, Arena& arena,
+                           const std::string& slot, std::uint32_t consumer_channels, std::uint32_t consumer_kernel) {
+    FeatureMap out{&arena.get(slot, std::uint64_t(ow) * oh * in.channels * sizeof(float)), ow, oh, in.channels};
+    const std::uint32_t pad = (consumer_kernel - 1) / 2;
+    if (precision_ != Precision::fp32 && in.channels % 32 == 0 &&
+        HipOperators::implicit_conv(ow, oh, in.channels, consumer_channels, consumer_kernel, 1, pad)) {
+        out.maxima = &arena.get(slot + ".max", std::uint64_t(in.channels / 32) * ow * oh * sizeof(float));
+        ops.bilinear_align_true_maxima(*out.buffer, *out.maxima, *in.buffer, in.width, in.height, ow, oh, in.channels);
+        return out;
+    }
+    ops.bilinear_align_true(*out.buffer, *in.buffer, in.width, in.height, ow, oh, in.channels);
     return out;
 }
 
@@ -217,8 +246,10 @@ FeatureMap DptHead::residual_unit(HipOperators& ops, const FeatureMap& in, const
     ConvFusion first_fusion;
     first_fusion.relu_input = true;
     first_fusion.relu_output = true;
+    const bool second_implicit =
+        HipOperators::implicit_conv(in.width, in.height, in.channels, in.channels, 3, 1, 1);
     FeatureMap first = conv(ops, in, prefix + ".conv1.weight", prefix + ".conv1.bias", in.channels, 3, 1, 1, true, arena,
-                            temp_slot, first_fusion);
+                            temp_slot, first_fusion, second_implicit ? Emit::absolute : Emit::none);
     ConvFusion second_fusion;
     second_fusion.residual = in.buffer;
     return conv(ops, first, prefix + ".conv2.weight", prefix + ".conv2.bias", in.channels, 3, 1, 1, true, arena, slot,
@@ -226,18 +257,23 @@ FeatureMap DptHead::residual_unit(HipOperators& ops, const FeatureMap& in, const
 }
 
 FeatureMap DptHead::fusion(const FeatureMap& path, const std::string& prefix, std::uint32_t ow, std::uint32_t oh,
-                           const FeatureMap* next_skip, Arena& arena, const std::string& slot) {
+                           const FeatureMap* next_skip, Arena& arena, const std::string& slot, bool next_is_head) {
     // dpt.cpp:574-615 from resConfUnit2 on: the path arrives with this
     // refinenet's processed skip already added (by the previous out_conv).
+    const std::uint32_t F = config_.features;
     FeatureMap unit = residual_unit(ops_, path, prefix + ".resConfUnit2", arena, "dpt.ru.first", "dpt.fu.unit");
-    FeatureMap resized{&arena.get("dpt.fu.resized", std::uint64_t(ow) * oh * config_.features * sizeof(float)), ow,
-                       oh, config_.features};
-    ops_.bilinear_align_true(*resized.buffer, *unit.buffer, unit.width, unit.height, ow, oh, config_.features);
-    // path + processed skip of the next refinenet (add.glsl; a + b == b + a)
+    FeatureMap resized = resize(ops_, unit, ow, oh, arena, "dpt.fu.resized", F, 1);
+    // path + processed skip of the next refinenet (add.glsl; a + b == b + a).
+    // The output feeds the next refinenet's residual unit (input ReLU) or
+    // the head's output_conv1.
     ConvFusion add_skip;
     add_skip.residual = next_skip ? next_skip->buffer : nullptr;
-    return conv(ops_, resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", config_.features, 1, 1, 0, true,
-                arena, slot, add_skip);
+    const std::uint32_t next_oc = next_is_head ? F / 2 : F;
+    const Emit emit = !HipOperators::implicit_conv(ow, oh, F, next_oc, 3, 1, 1) ? Emit::none
+                      : next_is_head                                         ? Emit::absolute
+                                                                             : Emit::relu;
+    return conv(ops_, resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", F, 1, 1, 0, true, arena, slot,
+                add_skip, emit);
 }
 
 FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, std::uint32_t b, std::uint32_t pw,
@@ -279,8 +315,12 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
     }
     // layer*_rn (dpt.cpp:743-756)
     const std::string level = std::to_string(i);
+    // levels 0-2 feed the first residual unit of a refinenet (input ReLU)
+    const bool unit_implicit = i < 3 && HipOperators::implicit_conv(layer.width, layer.height, config_.features,
+                                                                    config_.features, 3, 1, 1);
     FeatureMap rn = conv(ops, layer, "depth_head.scratch.layer" + std::to_string(i + 1) + "_rn.weight", "",
-                         config_.features, 3, 1, 1, false, arena, "dpt.rn" + level);
+                         config_.features, 3, 1, 1, false, arena, "dpt.rn" + level, ConvFusion{},
+                         unit_implicit ? Emit::relu : Emit::none);
     if (i == 3) return rn;
     // refinenet(i+1).resConfUnit1 on this level (dpt.cpp:574-590): its own
     // arena slots, so it may run beside the other levels
@@ -301,14 +341,11 @@ void DptHead::refine_and_head(const FeatureMap refined[4], std::uint32_t b, std:
     path = fusion(path, "depth_head.scratch.refinenet2", refined[0].width, refined[0].height, &refined[0], arena,
                   "dpt.pathA");
     path = fusion(path, "depth_head.scratch.refinenet1", refined[0].width * 2, refined[0].height * 2, nullptr, arena,
-                  "dpt.pathB");
+                  "dpt.pathB", /*next_is_head=*/true);
     // output head (dpt.cpp:792-855)
     path = conv(ops_, path, "depth_head.scratch.output_conv1.weight", "depth_head.scratch.output_conv1.bias", F / 2, 3,
                 1, 1, true, arena, "dpt.out1");
-    FeatureMap full{&arena.get("dpt.full", std::uint64_t(pw) * 14 * ph * 14 * (F / 2) * sizeof(float)), pw * 14,
-                    ph * 14, F / 2};
-    ops_.bilinear_align_true(*full.buffer, *path.buffer, path.width, path.height, full.width, full.height,
-                             full.channels);
+    FeatureMap full = resize(ops_, path, pw * 14, ph * 14, arena, "dpt.full", 32, 3);
     ConvFusion relu_after;
     relu_after.relu_output = true;
     FeatureMap head = conv(ops_, full, "depth_head.scratch.output_conv2.0.weight", "depth_head.scratch.output_conv2.0.bias",

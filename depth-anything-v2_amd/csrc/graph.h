@@ -73,8 +73,15 @@ private:
 struct FeatureMap {
     DeviceBuffer* buffer = nullptr;
     std::uint32_t width = 0, height = 0, channels = 0;
+    // Per-pixel 32-channel group maxima written by the producer for the next
+    // convolution (of max(x, 0) when maxima_relu), or null.
+    DeviceBuffer* maxima = nullptr;
+    bool maxima_relu = false;
     std::uint64_t elements() const { return std::uint64_t(width) * height * channels; }
 };
+
+// Group maxima a convolution writes for its consumer.
+enum class Emit { none, absolute, relu };
 
 class DptHead {
 public:
@@ -100,14 +107,23 @@ public:
 private:
     FeatureMap conv(HipOperators& ops, const FeatureMap& input, const std::string& weight, const std::string& bias,
                     std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding,
-                    bool has_bias, Arena& arena, const std::string& slot, const ConvFusion& fusion = ConvFusion{});
+                    bool has_bias, Arena& arena, const std::string& slot, const ConvFusion& fusion = ConvFusion{},
+                    Emit emit = Emit::none);
+    // Bilinear resize; with maxima for a following implicit convolution of
+    // `consumer_channels` outputs and kernel `consumer_kernel`.
+    FeatureMap resize(HipOperators& ops, const FeatureMap& input, std::uint32_t width, std::uint32_t height,
+                      Arena& arena, const std::string& slot, std::uint32_t consumer_channels,
+                      std::uint32_t consumer_kernel);
     FeatureMap residual_unit(HipOperators& ops, const FeatureMap& input, const std::string& prefix, Arena& arena,
                              const std::string& temp_slot, const std::string& slot);
     // Second residual unit, resize and out_conv of a refinenet; out_conv adds
     // next_skip (the next refinenet's processed skip input, the add of
     // dpt.cpp:574-615) when given.
+    // next_is_head: the output feeds the head's output_conv1 (no input ReLU)
+    // rather than the next refinenet's residual unit.
     FeatureMap fusion(const FeatureMap& path, const std::string& prefix, std::uint32_t output_width,
-                      std::uint32_t output_height, const FeatureMap* next_skip, Arena& arena, const std::string& slot);
+                      std::uint32_t output_height, const FeatureMap* next_skip, Arena& arena, const std::string& slot,
+                      bool next_is_head = false);
 
     DptConfig config_;
     GpuModel& weights_;

@@ -60,6 +60,7 @@ struct ConvParams {
     float* out;            // CHW [N][plane]
     const float* residual; // nullable, CHW [N][plane]
     uint32_t flags;        // DAV2_CONV_*
+    float* emit;           // channel-group maxima of the output (EMIT flags), [N/32][plane]
 };
 
 // Source of the 3x3 window positions outside the image (zero padding): the
@@ -436,6 +437,15 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
     // flag tests sit outside the unrolled store loops.
     // Accumulator r of lane l in block (i, j): channel 16i + 4(l/16) + r,
     // pixel 16j + l%16 of the wave's sub-tile.
+    // Channels of a group: 16-channel blocks i of this lane (rows
+    // 4(l/16) + r) and of lanes l^16, l^32, l^48.
+    constexpr int kEmitGroups = (NW % 32 == 0) ? NW / 32 : 0;
+    const bool emit_relu = (g.flags & DAV2_CONV_EMIT_RELU_MAX) != 0;
+    float gmax[PB][kEmitGroups > 0 ? kEmitGroups : 1];
+#pragma unroll
+    for (int j = 0; j < PB; ++j)
+#pragma unroll
+        for (int q = 0; q < (kEmitGroups > 0 ? kEmitGroups : 1); ++q) gmax[j][q] = 0.0f;
     auto epilogue = [&](auto residual_tag, auto relu_tag) {
         constexpr bool kResidual = decltype(residual_tag)::value, kRelu = decltype(relu_tag)::value;
 #pragma unroll
@@ -456,7 +466,29 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
                     if (kResidual) v = v + g.residual[idx];
                     if (kRelu) v = fmaxf(v, 0.0f);
                     g.out[idx] = v;
+                    // group maxima for the next convolution: group gi of the
+                    // wave's channels holds blocks i of 32 channels
+                    if constexpr (kEmitGroups > 0) {
+                        const float m = emit_relu ? fmaxf(v, 0.0f) : fabsf(v);
+                        gmax[j][(16 * i) / 32] = fmaxf(gmax[j][(16 * i) / 32], m);
+                    }
                 }
+        }
+    };
+    auto emit_groups = [&]() {
+        if constexpr (kEmitGroups > 0) {
+#pragma unroll
+            for (int j = 0; j < PB; ++j) {
+                const uint32_t p = wm * PW + 16u * j + (lane & 15u);
+#pragma unroll
+                for (int q = 0; q < kEmitGroups; ++q) {
+                    float m = gmax[j][q];
+                    m = fmaxf(m, __shfl_xor(m, 16, kWave));
+                    m = fmaxf(m, __shfl_xor(m, 32, kWave));
+                    const uint32_t group = (nb * BN + wn * NW) / 32u + q;
+                    if (lane < 16u && p < valid) g.emit[static_cast<uint64_t>(group) * g.plane + mbase + p] = m;
+                }
+            }
         }
     };
     const bool relu_out = (g.flags & DAV2_CONV_RELU_OUTPUT) != 0;
@@ -467,6 +499,7 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
         if (relu_out) epilogue(std::false_type{}, std::true_type{});
         else epilogue(std::false_type{}, std::false_type{});
     }
+    if (g.emit) emit_groups();
 }
 
 // 1x1 convolution to at most kNarrowN output channels: one thread per pixel
@@ -567,27 +600,42 @@ int dav2_hip_conv2d_i8_supported(uint32_t width, uint32_t height, uint32_t chann
            out_channels % 32 == 0 && static_cast<uint64_t>(width) * height < (1ull << 31);
 }
 
+int dav2_hip_conv2d_i8_emits(uint32_t out_channels, uint32_t kernel) {
+    // launch_ks: 256- and 128-channel tiles give each wave 64 or 32 channels,
+    // whole groups; the narrower tiles split a group over waves.
+    return (kernel == 1 || kernel == 3) && out_channels > 0 && out_channels % 128 == 0;
+}
+
 int dav2_hip_conv2d_i8(const dav2_conv_i8_args* a, void* stream) {
     if (!a) return hipErrorInvalidValue;
     if (!dav2_hip_conv2d_i8_supported(a->width, a->height, a->channels, a->out_channels, a->kernel, 1,
                                       (a->kernel - 1) / 2))
         return hipErrorInvalidValue;
-    if (!a->input || !a->weight || !a->weight_scales || !a->out || !a->scratch) return hipErrorInvalidValue;
+    if (!a->input || !a->weight || !a->weight_scales || !a->out || (!a->scratch && !a->partial_in))
+        return hipErrorInvalidValue;
     const uint64_t plane = static_cast<uint64_t>(a->width) * a->height;
     const uint32_t groups = channel_groups(a->channels);
-    if (a->scratch_floats < plane * groups) return hipErrorInvalidValue;
+    if (!a->partial_in && a->scratch_floats < plane * groups) return hipErrorInvalidValue;
+    const uint32_t emit = a->flags & (DAV2_CONV_EMIT_ABSMAX | DAV2_CONV_EMIT_RELU_MAX);
+    if (emit == (DAV2_CONV_EMIT_ABSMAX | DAV2_CONV_EMIT_RELU_MAX) ||
+        (emit && (!a->partial_out || !dav2_hip_conv2d_i8_emits(a->out_channels, a->kernel))))
+        return hipErrorInvalidValue;
     // The kernel addresses input and weights with 32-bit byte offsets.
     if (plane * a->channels * sizeof(float) >= (1ull << 32) ||
         static_cast<uint64_t>(a->out_channels) * a->kernel * a->kernel * a->channels >= (1ull << 32))
         return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (a->flags & ~static_cast<uint32_t>(DAV2_CONV_RELU_INPUT | DAV2_CONV_RELU_OUTPUT)) return hipErrorInvalidValue;
-    hipError_t e = launch_channel_group_absmax(a->input, a->channels, plane, a->scratch,
-                                               (a->flags & DAV2_CONV_RELU_INPUT) != 0, s);
-    if (e != hipSuccess) return e;
+    if (a->flags & ~static_cast<uint32_t>(DAV2_CONV_RELU_INPUT | DAV2_CONV_RELU_OUTPUT | DAV2_CONV_EMIT_ABSMAX |
+                                          DAV2_CONV_EMIT_RELU_MAX))
+        return hipErrorInvalidValue;
+    if (!a->partial_in) {
+        const hipError_t e = launch_channel_group_absmax(a->input, a->channels, plane, a->scratch,
+                                                         (a->flags & DAV2_CONV_RELU_INPUT) != 0, s);
+        if (e != hipSuccess) return e;
+    }
     ConvParams g;
     g.x = a->input;
-    g.partial = a->scratch;
+    g.partial = a->partial_in ? a->partial_in : a->scratch;
     g.groups = groups;
     g.channels = a->channels;
     g.height = a->height;
@@ -600,6 +648,7 @@ int dav2_hip_conv2d_i8(const dav2_conv_i8_args* a, void* stream) {
     g.out = a->out;
     g.residual = a->residual;
     g.flags = a->flags;
+    g.emit = emit ? a->partial_out : nullptr;
     if (a->kernel == 3) launch_ks<3>(g, g.tiles_x * a->height, a->out_channels, s);
     else launch_ks<1>(g, ceil_div(plane, kPix), a->out_channels, s);
     return hipGetLastError();

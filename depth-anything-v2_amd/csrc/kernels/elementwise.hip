@@ -78,9 +78,13 @@ __global__ __launch_bounds__(kBlock) void relu_kernel(float* out, const float* i
 // the channels' gathers are issued before the first blend.
 constexpr uint32_t kBilinearChannels = 8;
 
+// CPT channels per thread; with a maxima buffer (CPT = 32, channels % 32 ==
+// 0) the thread also writes max |out| of its 32-channel group.
+template <uint32_t CPT>
 __global__ __launch_bounds__(kBlock) void bilinear_kernel(float* __restrict__ out, const float* __restrict__ in,
                                                           uint32_t iw, uint32_t ih, uint32_t ow, uint32_t oh,
-                                                          uint32_t channels) {
+                                                          uint32_t channels, float* __restrict__ maxima) {
+    constexpr uint32_t kBilinearChannels = CPT;
     const uint32_t ox = blockIdx.x * 64u + (threadIdx.x & 63u);
     const uint32_t oy = blockIdx.y * 4u + (threadIdx.x >> 6);
     const uint32_t c0 = blockIdx.z * kBilinearChannels;
@@ -106,12 +110,16 @@ __global__ __launch_bounds__(kBlock) void bilinear_kernel(float* __restrict__ ou
         d[k] = p[y1 * iw + x1];
     }
     float* dst = out + static_cast<uint64_t>(c0) * oplane + static_cast<uint64_t>(oy) * ow + ox;
+    float m = 0.0f;
 #pragma unroll
     for (uint32_t k = 0; k < kBilinearChannels; ++k) {
         const float top = a[k] * (1.0f - fx) + b[k] * fx;
         const float bottom = c[k] * (1.0f - fx) + d[k] * fx;
-        if (k < n) dst[static_cast<uint64_t>(k) * oplane] = top * (1.0f - fy) + bottom * fy;
+        const float v = top * (1.0f - fy) + bottom * fy;
+        if (k < n) dst[static_cast<uint64_t>(k) * oplane] = v;
+        m = fmaxf(m, fabsf(v));
     }
+    if (CPT == 32 && maxima) maxima[static_cast<uint64_t>(blockIdx.z) * oplane + static_cast<uint64_t>(oy) * ow + ox] = m;
 }
 
 // reduce_minmax.glsl as a grid reduction. Stage 1: each workgroup folds a
@@ -283,8 +291,19 @@ int dav2_hip_bilinear_align_true(float* out, const float* input, uint32_t iw, ui
     if (ow == 0 || oh == 0 || channels == 0) return hipSuccess;
     if (!out || !input || iw == 0 || ih == 0 || channels > 65535u) return hipErrorInvalidValue;
     const dim3 grid(ceil_div(ow, 64), ceil_div(oh, 4), ceil_div(channels, kBilinearChannels));
-    hipLaunchKernelGGL(bilinear_kernel, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), out, input, iw, ih,
-                       ow, oh, channels);
+    hipLaunchKernelGGL(bilinear_kernel<kBilinearChannels>, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                       out, input, iw, ih, ow, oh, channels, nullptr);
+    return hipGetLastError();
+}
+
+int dav2_hip_bilinear_align_true_maxima(float* out, float* partial, const float* input, uint32_t iw, uint32_t ih,
+                                        uint32_t ow, uint32_t oh, uint32_t channels, void* stream) {
+    if (ow == 0 || oh == 0 || channels == 0) return hipSuccess;
+    if (!out || !partial || !input || iw == 0 || ih == 0 || channels % 32u || channels > 65535u)
+        return hipErrorInvalidValue;
+    const dim3 grid(ceil_div(ow, 64), ceil_div(oh, 4), channels / 32u);
+    hipLaunchKernelGGL(bilinear_kernel<32>, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), out, input, iw,
+                       ih, ow, oh, channels, partial);
     return hipGetLastError();
 }
 

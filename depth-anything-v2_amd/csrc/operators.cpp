@@ -25,6 +25,9 @@ void require_int8_weight(const DeviceBuffer& weight, std::uint64_t rows, std::ui
 
 std::uint32_t ld64(std::uint64_t columns) { return static_cast<std::uint32_t>((columns + 63) & ~63ull); }
 
+// 32-channel groups of the per-pixel maxima the convolutions' scales use.
+std::uint32_t channel_group_count(std::uint32_t channels) { return (channels + 31u) / 32u; }
+
 DeviceBuffer& grow(DeviceBuffer& buffer, std::uint64_t bytes) {
     if (buffer.size() < bytes) {
         // Work already queued may still read the old allocation.
@@ -540,7 +543,23 @@ void HipOperators::project_tokens_int8(DeviceBuffer& output, const DeviceBuffer&
 }
 
 // src/operators.cpp:1735-1805
-void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+bool HipOperators::implicit_conv(std::uint32_t width, std::uint32_t height, std::uint32_t channels,
+                                 std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
+                                 std::uint32_t padding) {
+    // Maps narrower than the implicit GEMM's 64-pixel row tiles (37x37, 19x19
+    // in the DPT head) run faster as im2col + GEMM.
+    return width >= 64 &&
+           dav2_hip_conv2d_i8_supported(width, height, channels, output_channels, kernel, stride, padding) != 0;
+}
+
+bool HipOperators::implicit_conv_emits(std::uint32_t width, std::uint32_t height, std::uint32_t channels,
+                                       std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
+                                       std::uint32_t padding) {
+    return implicit_conv(width, height, channels, output_channels, kernel, stride, padding) &&
+           dav2_hip_conv2d_i8_emits(output_channels, kernel) != 0;
+}
+
+bool HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
                                const DeviceBuffer& weight_scales, const DeviceBuffer& bias,
                                std::uint32_t input_width, std::uint32_t input_height, std::uint32_t input_channels,
                                std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
@@ -562,11 +581,8 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     if (fusion.residual) require_bytes(*fusion.residual, std::uint64_t(rows) * output_channels, "residual");
     const hipStream_t s = stream();
     const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
-    // Implicit GEMM: same bits as im2col + GEMM, no im2col matrix. Maps
-    // narrower than its 64-pixel row tiles (37x37, 19x19 in the DPT head) run
-    // faster as im2col + GEMM.
-    if (input_width >= 64 && dav2_hip_conv2d_i8_supported(input_width, input_height, input_channels,
-                                                          output_channels, kernel, stride, padding)) {
+    // Implicit GEMM: same bits as im2col + GEMM, no im2col matrix.
+    if (implicit_conv(input_width, input_height, input_channels, output_channels, kernel, stride, padding)) {
         const DeviceBuffer* tapmajor = tapmajor_weight;
         if (!tapmajor || !*tapmajor) {
             grow(conv_weights_, std::uint64_t(output_channels) * inner);
@@ -595,8 +611,19 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
         a.scratch_floats = scratch_floats;
         a.flags = (fusion.relu_input ? DAV2_CONV_RELU_INPUT : 0u) | (fusion.relu_output ? DAV2_CONV_RELU_OUTPUT : 0u);
         a.residual = fusion.residual ? fusion.residual->as<float>() : nullptr;
+        const std::uint64_t group_floats = std::uint64_t(channel_group_count(input_channels)) * rows;
+        if (fusion.input_maxima) {
+            require_bytes(*fusion.input_maxima, group_floats, "convolution input maxima");
+            a.partial_in = fusion.input_maxima->as<float>();
+        }
+        const bool emit = fusion.emit_maxima && dav2_hip_conv2d_i8_emits(output_channels, kernel);
+        if (emit) {
+            require_bytes(*fusion.emit_maxima, std::uint64_t(output_channels / 32u) * rows, "convolution output maxima");
+            a.partial_out = fusion.emit_maxima->as<float>();
+            a.flags |= fusion.emit_relu ? DAV2_CONV_EMIT_RELU_MAX : DAV2_CONV_EMIT_ABSMAX;
+        }
         hip_check(dav2_hip_conv2d_i8(&a, s), "implicit-GEMM convolution");
-        return;
+        return emit;
     }
     // im2col + GEMM: the input ReLU is taken by the tiled im2col kernels
     // (other geometries get a separate pass), the residual and the output
@@ -624,6 +651,7 @@ void HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     workspace_ld_ = ld;
     linear_int8_packed(output, packed, ld, int8_weight, scales, weight_scales, bias, rows, inner, output_channels, 0u,
                        rows, true, has_bias, fusion.residual, fusion.relu_output);
+    return false;
 }
 
 void HipOperators::conv1x1_narrow_int8(DeviceBuffer& output, const DeviceBuffer& input,
@@ -722,6 +750,25 @@ void HipOperators::bilinear_align_true(DeviceBuffer& output, const DeviceBuffer&
 }
 
 // src/operators.cpp:2050-2071
+void HipOperators::bilinear_align_true_maxima(DeviceBuffer& output, DeviceBuffer& maxima, const DeviceBuffer& input,
+                                              std::uint32_t input_width, std::uint32_t input_height,
+                                              std::uint32_t output_width, std::uint32_t output_height,
+                                              std::uint32_t channels) {
+    if (input_width == 0 || input_height == 0 || output_width == 0 || output_height == 0 || channels == 0 ||
+        channels % 32u)
+        throw std::invalid_argument("invalid bilinear dimensions");
+    require_bytes(input, std::uint64_t(input_width) * input_height * channels, "bilinear input");
+    require_bytes(output, std::uint64_t(output_width) * output_height * channels, "bilinear output");
+    require_bytes(maxima, std::uint64_t(output_width) * output_height * (channels / 32u), "bilinear maxima");
+    ProfileScope prof(context_.profiler(), "bilinear",
+                      4.0 * channels * (double(input_width) * input_height + double(output_width) * output_height), "B",
+                      stream());
+    hip_check(dav2_hip_bilinear_align_true_maxima(output.as<float>(), maxima.as<float>(), input.as<float>(),
+                                                  input_width, input_height, output_width, output_height, channels,
+                                                  stream()),
+              "bilinear");
+}
+
 void HipOperators::reduce_minmax(const DeviceBuffer& input, DeviceBuffer& range, std::uint32_t count) {
     if (count == 0) throw std::invalid_argument("empty depth reduction");
     require_bytes(input, count, "depth reduction input");

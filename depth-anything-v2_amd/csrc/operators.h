@@ -30,6 +30,15 @@ struct ConvFusion {
     bool relu_input = false;
     bool relu_output = false;
     const DeviceBuffer* residual = nullptr;
+    // Per-pixel maxima over 32-channel groups of the input, already written
+    // by its producer (|x|, or max(x, 0) when relu_input): the implicit-GEMM
+    // path then skips computing them.
+    const DeviceBuffer* input_maxima = nullptr;
+    // Ask the implicit-GEMM path to write the output's group maxima (of
+    // max(out, 0) with emit_relu, for a consumer with relu_input) here;
+    // conv2d_int8 returns whether it did.
+    DeviceBuffer* emit_maxima = nullptr;
+    bool emit_relu = false;
 };
 
 // Reusable int8 activation workspace (role of the reference's
@@ -80,7 +89,8 @@ public:
                              const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t width,
                              std::uint32_t height, std::uint32_t embedding, std::uint32_t output_channels);
 
-    void conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+    // Returns true when fusion.emit_maxima was written.
+    bool conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
                      const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t input_width,
                      std::uint32_t input_height, std::uint32_t input_channels, std::uint32_t output_channels,
                      std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding, bool has_bias,
@@ -121,6 +131,19 @@ public:
     void bilinear_align_true(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t input_width,
                              std::uint32_t input_height, std::uint32_t output_width, std::uint32_t output_height,
                              std::uint32_t channels);
+    // The same, also writing the output's 32-channel group maxima (|out|)
+    // into maxima (channels % 32 == 0).
+    void bilinear_align_true_maxima(DeviceBuffer& output, DeviceBuffer& maxima, const DeviceBuffer& input,
+                                    std::uint32_t input_width, std::uint32_t input_height,
+                                    std::uint32_t output_width, std::uint32_t output_height, std::uint32_t channels);
+    // Whether conv2d_int8 takes the implicit-GEMM path for this geometry (the
+    // path that reads input_maxima), and whether that path can emit maxima.
+    static bool implicit_conv(std::uint32_t width, std::uint32_t height, std::uint32_t channels,
+                              std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
+                              std::uint32_t padding);
+    static bool implicit_conv_emits(std::uint32_t width, std::uint32_t height, std::uint32_t channels,
+                                    std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
+                                    std::uint32_t padding);
 
     void reduce_minmax(const DeviceBuffer& input, DeviceBuffer& range, std::uint32_t count);
     void normalize_relative(DeviceBuffer& depth, const DeviceBuffer& range, std::uint32_t count);

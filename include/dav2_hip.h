@@ -174,7 +174,14 @@ DAV2_API uint64_t dav2_hip_gemm_i8_split_scratch_bytes(uint32_t m, uint32_t n, u
  * dst[n][(ky*k + kx)*channels + c] = src[n][c*k*k + ky*k + kx]. */
 enum {
     DAV2_CONV_RELU_INPUT = 1,   /* convolve max(input, 0) (relu.glsl before the conv)  */
-    DAV2_CONV_RELU_OUTPUT = 2   /* out = max(out, 0) after the residual (relu.glsl)     */
+    DAV2_CONV_RELU_OUTPUT = 2,  /* out = max(out, 0) after the residual (relu.glsl)     */
+    /* Also write the next convolution's per-pixel channel-group maxima of the
+     * output into partial_out ([out_channels/32][height*width], the layout of
+     * the scratch): |out| (EMIT_ABSMAX) or max(out, 0) (EMIT_RELU_MAX, for a
+     * consumer that applies DAV2_CONV_RELU_INPUT). Needs out_channels / 32
+     * groups that each lie in one wave's channels (dav2_hip_conv2d_i8_emits). */
+    DAV2_CONV_EMIT_ABSMAX = 4,
+    DAV2_CONV_EMIT_RELU_MAX = 8
 };
 
 typedef struct dav2_conv_i8_args {
@@ -190,11 +197,20 @@ typedef struct dav2_conv_i8_args {
     uint64_t scratch_floats;
     uint32_t flags;              /* DAV2_CONV_*                                    */
     const float* residual;       /* NULL, or CHW like out: out = conv + residual   */
+    /* The input's channel-group maxima (|x|, or max(x, 0) with RELU_INPUT)
+     * when a producer has already written them (an EMIT flag or
+     * dav2_hip_bilinear_align_true_maxima); NULL: computed into scratch. */
+    const float* partial_in;
+    float* partial_out;          /* with an EMIT flag                              */
 } dav2_conv_i8_args;
 
 DAV2_API int dav2_hip_conv2d_i8_supported(uint32_t width, uint32_t height, uint32_t channels,
                                           uint32_t out_channels, uint32_t kernel, uint32_t stride,
                                           uint32_t padding);
+/* Nonzero if a supported convolution to out_channels can also emit its
+ * output's channel-group maxima (DAV2_CONV_EMIT_*). No reference
+ * counterpart (a fusion of channel_group maxima into the producer). */
+DAV2_API int dav2_hip_conv2d_i8_emits(uint32_t out_channels, uint32_t kernel);
 DAV2_API int dav2_hip_conv_weights_tapmajor(int8_t* dst, const int8_t* src, uint32_t out_channels,
                                             uint32_t channels, uint32_t kernel, uint64_t ldb,
                                             void* stream);
@@ -266,6 +282,14 @@ DAV2_API int dav2_hip_bilinear_align_true(float* out, const float* input,
                                           uint32_t input_width, uint32_t input_height,
                                           uint32_t output_width, uint32_t output_height,
                                           uint32_t channels, void* stream);
+/* The same output bits, plus the per-pixel maxima of |out| over each group of
+ * 32 channels into partial ([channels/32][output plane], channels % 32 == 0):
+ * the input maxima of a following dav2_hip_conv2d_i8 (partial_in). No
+ * reference counterpart (a fusion). */
+DAV2_API int dav2_hip_bilinear_align_true_maxima(float* out, float* partial, const float* input,
+                                                 uint32_t input_width, uint32_t input_height,
+                                                 uint32_t output_width, uint32_t output_height,
+                                                 uint32_t channels, void* stream);
 
 /* reduce_minmax.glsl as a two-stage grid reduction; partials must hold
  * 2*dav2_hip_minmax_partials(count) floats. range[0] = min, range[1] = max. */

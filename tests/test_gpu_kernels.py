@@ -233,6 +233,76 @@ def test_conv2d_i8_fusions(gpu, pkg, lib, oracle, flags, with_residual):
     assert np.array_equal(host(torch, got).view(np.uint32), host(torch, want).view(np.uint32))
 
 
+def _group_max(x, relu):
+    """Per-pixel maxima over 32-channel groups of a [C][P] map."""
+    m = np.maximum(x, 0) if relu else np.abs(x)
+    return m.reshape(x.shape[0] // 32, 32, -1).max(axis=1)
+
+
+@pytest.mark.parametrize("k,n,relu_in,emit", [(3, 256, True, 4), (3, 128, False, 8), (1, 256, False, 8),
+                                              (1, 128, True, 4)])
+def test_conv2d_i8_group_maxima(gpu, pkg, lib, oracle, k, n, relu_in, emit):
+    # EMIT_*: the output's 32-channel group maxima written by the epilogue
+    # equal those of the output; partial_in: the same output as maxima
+    # computed by the kernel itself.
+    torch = gpu
+    _announce("conv2d_i8 group maxima", k, n, relu_in, emit)
+    c, h, w = 128, 9, 77
+    rng = np.random.default_rng(k * n + emit)
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    wq, ws = oracle.quantize_weight_rows(rng.standard_normal((n, c * k * k)).astype(np.float32) * 0.05)
+    wt = wq.reshape(n, c, k * k).transpose(0, 2, 1).reshape(n, c * k * k)
+    bias = rng.standard_normal(n).astype(np.float32)
+    xd, wtd, wsd, bd = dev(torch, x), dev(torch, wt), dev(torch, ws), dev(torch, bias)
+    s = stream(torch)
+    n_scratch = lib.dav2_hip_im2col_scratch_floats(w, h, c)
+    scratch = empty(torch, (n_scratch,), torch.float32)
+    assert lib.dav2_hip_conv2d_i8_emits(n, k) == 1 and lib.dav2_hip_conv2d_i8_emits(64, k) == 0
+    fl = 1 if relu_in else 0
+
+    def conv(out, flags, partial_in=None, partial_out=None):
+        a = pkg.ConvArgs(input=ptr(xd), width=w, height=h, channels=c, kernel=k, weight=ptr(wtd),
+                         weight_scales=ptr(wsd), bias=ptr(bd), out_channels=n, out=ptr(out), scratch=ptr(scratch),
+                         scratch_floats=n_scratch, flags=flags, residual=None,
+                         partial_in=ptr(partial_in) if partial_in is not None else None,
+                         partial_out=ptr(partial_out) if partial_out is not None else None)
+        return lib.dav2_hip_conv2d_i8(C.byref(a), s)
+
+    want = empty(torch, (n, h * w), torch.float32)
+    ok(lib, conv(want, fl))
+    got = empty(torch, (n, h * w), torch.float32)
+    maxima = empty(torch, (n // 32, h * w), torch.float32)
+    ok(lib, conv(got, fl | emit, partial_out=maxima))
+    ref = host(torch, want)
+    assert np.array_equal(host(torch, got).view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(host(torch, maxima), _group_max(ref, relu=(emit == 8)))
+    # the input's maxima given by a producer instead of computed here
+    pin = dev(torch, _group_max(x.reshape(c, -1), relu=relu_in))
+    again = empty(torch, (n, h * w), torch.float32)
+    ok(lib, conv(again, fl, partial_in=pin))
+    assert np.array_equal(host(torch, again).view(np.uint32), ref.view(np.uint32))
+    # both emit modes at once, or an emit without a buffer, are rejected
+    assert conv(got, fl | 12, partial_out=maxima) != 0
+    assert conv(got, fl | 4) != 0
+
+
+@pytest.mark.parametrize("c,ih,iw,oh,ow", [(128, 296, 296, 518, 518), (256, 37, 37, 74, 74), (32, 5, 7, 9, 13)])
+def test_bilinear_maxima(gpu, lib, c, ih, iw, oh, ow):
+    torch = gpu
+    _announce("bilinear maxima", c, ih, iw, oh, ow)
+    x = np.random.default_rng(c + oh).standard_normal((c, ih, iw)).astype(np.float32)
+    xd = dev(torch, x)
+    plain = empty(torch, (c, oh * ow), torch.float32)
+    fused = empty(torch, (c, oh * ow), torch.float32)
+    maxima = empty(torch, (c // 32, oh * ow), torch.float32)
+    s = stream(torch)
+    ok(lib, lib.dav2_hip_bilinear_align_true(ptr(plain), ptr(xd), iw, ih, ow, oh, c, s))
+    ok(lib, lib.dav2_hip_bilinear_align_true_maxima(ptr(fused), ptr(maxima), ptr(xd), iw, ih, ow, oh, c, s))
+    ref = host(torch, plain)
+    assert np.array_equal(host(torch, fused).view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(host(torch, maxima), _group_max(ref, relu=False))
+
+
 @pytest.mark.parametrize("c,h,w,n,flags", [(32, 518, 518, 1, 2), (32, 20, 33, 1, 0), (64, 7, 9, 3, 1), (12, 5, 5, 4, 3)])
 def test_conv1x1_narrow_matches_im2col_gemm(gpu, pkg, lib, oracle, c, h, w, n, flags):
     torch = gpu
