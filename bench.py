@@ -10,8 +10,9 @@ the batch. Prints one JSON line.
 
 Roofline: the dominant kernel is the int8 MFMA GEMM. Its algorithmic work is
 2*M*N*K int8 ops per launch (unpadded K); achieved = total ops / total
-launch time, measured with HIP events around every GEMM launch on the stream
-it runs on, during a second timed pass of the same K steps.
+launch time, measured with a start and a stop HIP event per GEMM launch that
+its kernel dispatches record (hipExtLaunchKernelGGL) on the stream it runs on,
+during a second timed pass of the same K steps.
 """
 
 from __future__ import annotations

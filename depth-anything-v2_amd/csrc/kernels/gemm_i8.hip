@@ -21,6 +21,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include <hip/hip_ext.h>
 #include "dav2_hip.h"
 
 using namespace dav2k;
@@ -442,8 +443,25 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
     }
 }
 
+// Events for the calling thread's next GEMM launch (dav2_hip_gemm_i8_events):
+// the kernel dispatch itself records them (hipExtLaunchKernelGGL), so they
+// time the kernel and nothing else; consumed by that launch.
+thread_local hipEvent_t t_start_event = nullptr, t_stop_event = nullptr;
+
+template <typename Kernel, typename... Args>
+void launch_timed(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, bool first, bool last,
+                  Args... args) {
+    hipEvent_t start = first ? t_start_event : nullptr, stop = last ? t_stop_event : nullptr;
+    if (first) t_start_event = nullptr;
+    if (last) t_stop_event = nullptr;
+    if (start || stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, s, start, stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+}
+
 template <int BM, int BN, int WMW, int WNW, int BK, int STAGES, int EPI>
-void launch_cfg(const GemmParams& g, hipStream_t s) {
+void launch_cfg(const GemmParams& g, hipStream_t s, bool last = true) {
     // LDS: the stage ring, or the row-major output tile if that is larger.
     constexpr size_t ring = static_cast<size_t>(STAGES) * (BM + BN) * BK;
     constexpr size_t out_tile = static_cast<size_t>(BM) * (BN + 4) * 4;
@@ -453,7 +471,7 @@ void launch_cfg(const GemmParams& g, hipStream_t s) {
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     (void)attr;
     const dim3 grid(ceil_div(g.rows_p, BM), ceil_div(g.rows_q, BN), ceil_div(g.k, g.k_split));
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>), grid, dim3(64 * WMW * WNW), lds, s, g);
+    launch_timed(gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>, grid, dim3(64 * WMW * WNW), lds, s, true, last, g);
 }
 
 // Rows of P per tile of the configuration launch_epi picks.
@@ -464,7 +482,7 @@ inline uint32_t tile_rows(uint32_t rows_p, uint32_t rows_q, bool row_major) {
 }
 
 template <int EPI>
-void launch_epi(const GemmParams& g, hipStream_t s) {
+void launch_epi(const GemmParams& g, hipStream_t s, bool last = true) {
     // Measured on MI355X for the ViT-L encoder shapes (M = 1370, K = 1024 /
     // 4096, 128-byte stages): for N = 1024 64x64 tiles with a three-stage
     // ring are fastest; for N >= 2048 96x64 tiles with a two-stage ring are
@@ -472,9 +490,9 @@ void launch_epi(const GemmParams& g, hipStream_t s) {
     // 64x64 ones). Channel-major GEMMs with few output channels use 32-row
     // tiles.
     switch (tile_rows(g.rows_p, g.rows_q, row_major_epi<EPI>())) {
-        case 32: launch_cfg<32, 64, 1, 2, 128, 3, EPI>(g, s); break;
-        case 96: launch_cfg<96, 64, 2, 2, 128, 2, EPI>(g, s); break;
-        default: launch_cfg<64, 64, 2, 2, 128, 3, EPI>(g, s); break;
+        case 32: launch_cfg<32, 64, 1, 2, 128, 3, EPI>(g, s, last); break;
+        case 96: launch_cfg<96, 64, 2, 2, 128, 2, EPI>(g, s, last); break;
+        default: launch_cfg<64, 64, 2, 2, 128, 3, EPI>(g, s, last); break;
     }
 }
 
@@ -569,11 +587,11 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (split && slices > 1) {
-        launch_epi<kEpiSplitPartial>(g, s);
+        launch_epi<kEpiSplitPartial>(g, s, false);
         const uint64_t total = static_cast<uint64_t>(a->m) * a->n;
-        hipLaunchKernelGGL(split_reduce_transposed_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s,
-                           a->split_scratch, slices, a->n, a->m, a->a_scales, a->b_scales, a->bias, a->residual,
-                           a->relu_output, a->out, a->out_row_stride, a->out_row_offset);
+        launch_timed(split_reduce_transposed_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, false, true,
+                     a->split_scratch, slices, a->n, a->m, a->a_scales, a->b_scales, a->bias, a->residual,
+                     a->relu_output, a->out, a->out_row_stride, a->out_row_offset);
         return hipGetLastError();
     }
     if (split) g.out_i32 = a->out_i32;
@@ -587,6 +605,11 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
         case DAV2_GEMM_EPI_ROW_COLMAX: launch_epi<DAV2_GEMM_EPI_ROW_COLMAX>(g, s); break;
     }
     return hipGetLastError();
+}
+
+extern "C" void dav2_hip_gemm_i8_events(void* start, void* stop) {
+    t_start_event = static_cast<hipEvent_t>(start);
+    t_stop_event = static_cast<hipEvent_t>(stop);
 }
 
 extern "C" uint32_t dav2_hip_gemm_i8_row_tiles(uint32_t m, uint32_t n, uint32_t epilogue) {

@@ -140,7 +140,7 @@ void HipOperators::linear_int8_prequantized(DeviceBuffer& output, const DeviceBu
     a.residual = output.as<float>();
     a.gamma = gamma ? gamma->as<float>() : nullptr;
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
-                      stream());
+                      stream(), /*dispatch_events=*/true);
     hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
 }
 
@@ -182,7 +182,7 @@ void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& 
         }
     }
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
-                      stream());
+                      stream(), /*dispatch_events=*/true);
     hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
 }
 
@@ -729,7 +729,8 @@ void HipOperators::conv_transpose_nonoverlap_int8(DeviceBuffer& output, const De
     a.convt_width = input_width;
     a.convt_height = input_height;
     a.convt_channels = output_channels;
-    ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * input_rows * weight_rows * input_channels, "OP", s);
+    ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * input_rows * weight_rows * input_channels, "OP", s,
+                      /*dispatch_events=*/true);
     hip_check(dav2_hip_gemm_i8(&a, s), "transposed convolution GEMM");
 }
 

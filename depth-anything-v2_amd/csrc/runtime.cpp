@@ -1,5 +1,7 @@
 #include "runtime.h"
 
+#include "dav2_hip.h"
+
 #include <cstdio>
 #include <new>
 #include <utility>
@@ -68,24 +70,36 @@ hipEvent_t Profiler::take_event() {
     return e;
 }
 
-int Profiler::begin(const char* name, double work, const char* unit, hipStream_t stream) {
+int Profiler::begin(const char* name, double work, const char* unit, hipStream_t stream, bool dispatch_events) {
     if (!enabled_) return -1;
-    Record r{name, unit, work, take_event(), take_event()};
-    hip_check(hipEventRecord(r.start, stream), "hipEventRecord");
+    Record r{name, unit, work, take_event(), take_event(), dispatch_events};
+    if (dispatch_events)
+        dav2_hip_gemm_i8_events(r.start, r.stop);
+    else
+        hip_check(hipEventRecord(r.start, stream), "hipEventRecord");
     pending_.push_back(r);
     return static_cast<int>(pending_.size() - 1);
 }
 
 void Profiler::end(int id, hipStream_t stream) {
     if (id < 0 || static_cast<std::size_t>(id) >= pending_.size()) return;
-    (void)hipEventRecord(pending_[id].stop, stream);
+    if (pending_[id].dispatch)
+        dav2_hip_gemm_i8_events(nullptr, nullptr);  // a launch that did not happen leaves none behind
+    else
+        (void)hipEventRecord(pending_[id].stop, stream);
 }
 
 std::string Profiler::report() {
+    hip_check(hipDeviceSynchronize(), "profile synchronize");
     for (auto& r : pending_) {
-        hip_check(hipEventSynchronize(r.stop), "hipEventSynchronize");
         float ms = 0.0f;
-        hip_check(hipEventElapsedTime(&ms, r.start, r.stop), "hipEventElapsedTime");
+        // an event pair a launch never recorded (it failed) has no time
+        if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) {
+            (void)hipGetLastError();
+            free_.push_back(r.start);
+            free_.push_back(r.stop);
+            continue;
+        }
         Total& t = totals_[r.name];
         t.launches += 1;
         t.ms += ms;

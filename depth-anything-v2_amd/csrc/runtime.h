@@ -56,8 +56,11 @@ public:
     ~Profiler();
     void set_enabled(bool on) { enabled_ = on; }
     bool enabled() const { return enabled_; }
-    // Returns a record id, or -1 when disabled.
-    int begin(const char* name, double work, const char* unit, hipStream_t stream);
+    // Returns a record id, or -1 when disabled. With dispatch_events the
+    // events go to the next GEMM launch (dav2_hip_gemm_i8_events), which
+    // records them at the kernel's start and end; otherwise they are
+    // recorded on the stream around the enqueued work.
+    int begin(const char* name, double work, const char* unit, hipStream_t stream, bool dispatch_events = false);
     void end(int id, hipStream_t stream);
     // Synchronises, folds pending records into the totals and returns them as
     // a JSON object {name: {"launches", "ms", "work", "unit"}}; then clears.
@@ -69,6 +72,7 @@ private:
         const char* unit;
         double work;
         hipEvent_t start, stop;
+        bool dispatch;
     };
     struct Total {
         std::uint64_t launches = 0;
@@ -84,8 +88,9 @@ private:
 
 class ProfileScope {
 public:
-    ProfileScope(Profiler& p, const char* name, double work, const char* unit, hipStream_t s)
-        : p_(p), s_(s), id_(p.begin(name, work, unit, s)) {}
+    ProfileScope(Profiler& p, const char* name, double work, const char* unit, hipStream_t s,
+                 bool dispatch_events = false)
+        : p_(p), s_(s), id_(p.begin(name, work, unit, s, dispatch_events)) {}
     ~ProfileScope() { p_.end(id_, s_); }
 
 private:

@@ -123,6 +123,10 @@ typedef struct dav2_gemm_i8_args {
 /* Replaces linear_int8_tiled.glsl:40-117 (src/operators.cpp:847-880) and
  * conv_transpose_int8.glsl:31-58 (:1969-1975). */
 DAV2_API int dav2_hip_gemm_i8(const dav2_gemm_i8_args* args, void* stream);
+/* Timing hook, no reference counterpart: hipEvent_t start / stop for the
+ * calling thread's next dav2_hip_gemm_i8, recorded by its kernel dispatches
+ * (the GEMM's start, the last kernel's end); NULL, NULL clears. */
+DAV2_API void dav2_hip_gemm_i8_events(void* start, void* stop);
 
 /* fp32 GEMM of the fp32 precision mode: out = a . b^T + bias with the
  * epilogues ROW, ROW_GELU, ROW_LAYERSCALE, TRANSPOSED (residual, relu_output)
