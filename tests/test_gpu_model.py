@@ -132,6 +132,35 @@ def test_vitl_1036_batch4_equals_singles(gpu, pkg, lib, models):
             assert np.array_equal(host(torch, single).view(np.uint32), got[b].view(np.uint32))
 
 
+def test_contexts_on_two_threads(gpu, pkg, lib, models):
+    # One context per thread (docs/architecture.md:254-256): two contexts
+    # inferring at the same time, each on its own host thread and stream,
+    # give the single-context result.
+    import threading
+    width, height = 350, 266
+    x = pkg.dav2_format.imagenet_input(width, height, seed=SEED + 21)[0]
+    with pkg.Context(str(models["vits"]), "vits") as ctx:
+        ref = ctx.infer(x, width, height)
+    results, errors = {}, []
+
+    def worker(i):
+        try:
+            with pkg.Context(str(models["vits"]), "vits") as ctx:
+                results[i] = [ctx.infer(x, width, height) for _ in range(3)]
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    for i in range(2):
+        for d in results[i]:
+            assert np.array_equal(d.view(np.uint32), ref.view(np.uint32))
+
+
 def test_graph_replays_match_eager(gpu, pkg, lib, models, monkeypatch):
     # The first inference at a given (input, output, size, stream) runs
     # eagerly, the second captures a HIP graph, later ones replay it. Every
