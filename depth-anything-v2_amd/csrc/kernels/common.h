@@ -114,7 +114,18 @@ DAV2_DEV float exp_cw(float a) {
 DAV2_DEV float gelu_erfcc(float value) {
     const float x = value * 0.70710678118654752440f;
     const float magnitude = fabsf(x);
-    const float t = 1.0f / (1.0f + 0.5f * magnitude);
+    // t = 1 / (1 + m/2) correctly rounded: the hardware reciprocal refined by
+    // one Newton step with fma (Markstein's reciprocal iteration), which
+    // returns the correctly rounded quotient for every float d in [1, 16)
+    // (checked exhaustively on gfx950). For d >= 16 (m >= 30) or NaN,
+    // exp_cw(-m*m + poly) below is 0 or NaN whatever finite t is, so t = 0
+    // gives the same result as the IEEE quotient.
+    const float d = 1.0f + 0.5f * magnitude;
+    float t = 0.0f;
+    if (d < 16.0f) {
+        const float r = __builtin_amdgcn_rcpf(d);
+        t = fmaf(fmaf(-d, r, 1.0f), r, r);
+    }
     float poly = t * 0.17087277f;
     poly = t * (-0.82215223f + poly);
     poly = t * (1.48851587f + poly);

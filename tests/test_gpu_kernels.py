@@ -776,10 +776,41 @@ def test_elementwise_exact(gpu, lib, oracle):
     # wide sweep through every branch of the exp and erfc evaluation
     w = np.concatenate([np.linspace(-40, 40, 200001, dtype=np.float32),
                         (rng.standard_normal(100000) * 10).astype(np.float32),
-                        np.array([0.0, -0.0, 1e-30, -1e-30, 13.5, -13.5, 1e4, -1e4], np.float32)])
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 13.5, -13.5, 1e4, -1e4, np.inf, 3e38, -3e38, 42.42, -42.42,
+                                  42.43, -42.43, 42.44, -42.44, 100.0, -100.0], np.float32),
+                        # around 1 + |x|/(2 sqrt 2) = 16, where the reciprocal switches form
+                        (42.426407 + np.arange(-64, 64) * 1e-5).astype(np.float32)]).astype(np.float32)
     wd, wo = dev(torch, w), empty(torch, w.shape, torch.float32)
     ok(lib, lib.dav2_hip_gelu(ptr(wo), ptr(wd), w.size, s))
     assert np.array_equal(host(torch, wo).view(np.uint32), oracle.gelu(w).view(np.uint32))
+    # -inf: both give NaN (-inf * 0); NaN bit patterns are not compared
+    ninf = dev(torch, np.array([-np.inf, np.nan], np.float32))
+    no = empty(torch, (2,), torch.float32)
+    ok(lib, lib.dav2_hip_gelu(ptr(no), ptr(ninf), 2, s))
+    assert np.isnan(host(torch, no)).all() and np.isnan(oracle.gelu(np.array([-np.inf, np.nan], np.float32))).all()
+
+
+def test_gelu_every_float_below_42(gpu, lib, oracle):
+    # Every float x with |x| < 42.5 (2.2e9 values): the range in which the
+    # GELU's 1 / (1 + |x|/(2 sqrt 2)) takes the refined hardware reciprocal;
+    # bit-exact against the oracle's IEEE division.
+    torch = gpu
+    s = stream(torch)
+    limit, chunk = 0x422A0000, 1 << 26
+    for sign in (0, -(2**31)):
+        for start in range(0, limit, chunk):
+            n = min(chunk, limit - start)
+            bits = torch.arange(start, start + n, dtype=torch.int32, device="cuda")
+            if sign:
+                bits = bits | sign
+            x = bits.view(torch.float32)
+            out = torch.empty_like(x)
+            ok(lib, lib.dav2_hip_gelu(ptr(out), ptr(x), n, s))
+            xh = (np.arange(start, start + n, dtype=np.uint32) | np.uint32(sign & 0xFFFFFFFF)).view(np.float32)
+            got = host(torch, out)
+            if not np.array_equal(got.view(np.uint32), oracle.gelu(xh).view(np.uint32)):
+                bad = np.nonzero(got.view(np.uint32) != oracle.gelu(xh).view(np.uint32))[0][:4]
+                pytest.fail(f"GELU differs at x = {xh[bad]}")
 
 
 @pytest.mark.parametrize("c,ih,iw,oh,ow", [(256, 19, 19, 37, 37), (256, 148, 148, 296, 296), (128, 296, 296, 518, 518),
