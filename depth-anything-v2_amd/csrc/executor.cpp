@@ -215,6 +215,9 @@ std::size_t HipExecutor::upload_image(const char* slot, const std::uint8_t* imag
 }
 
 HipJob::~HipJob() {
+    // the job's device current for the calls below, the caller's afterwards
+    int previous = -1;
+    (void)hipGetDevice(&previous);
     (void)hipSetDevice(device_);
     if (done_) {
         (void)hipEventSynchronize(done_);
@@ -223,6 +226,7 @@ HipJob::~HipJob() {
     if (ipc_wait_) (void)hipEventDestroy(ipc_wait_);
     if (mapped_input_) (void)hipIpcCloseMemHandle(mapped_input_);
     if (mapped_output_) (void)hipIpcCloseMemHandle(mapped_output_);
+    if (previous >= 0) (void)hipSetDevice(previous);
 }
 
 dav2_gpu_job_state HipJob::state() const {
