@@ -84,9 +84,26 @@ void HipExecutor::run(const float* input, int batch, int width, int height, floa
     DeviceBuffer* features[4] = {nullptr, nullptr, nullptr, nullptr};
     const std::uint32_t w = static_cast<std::uint32_t>(width), h = static_cast<std::uint32_t>(height);
     const std::uint32_t pw = w / 14, ph = h / 14;
+    const hipStream_t main = operators_.stream();
     if (batch != 1) {
+        // The encoder runs the batch at once; then the images' DPT heads
+        // alternate between the main and the side stream (own operator set,
+        // workspaces and arena slots each), two in flight at a time.
         dino_.forward(input, w, h, static_cast<std::uint32_t>(batch), arena_, features);
-        dpt_.forward(features, pw, ph, static_cast<std::uint32_t>(batch), arena_, output, pre_relu);
+        hip_check(hipEventRecord(captured_[0], main), "encoder event");
+        hip_check(hipStreamWaitEvent(side_stream_, captured_[0], 0), "side wait");
+        for (std::uint32_t b = 0; b < static_cast<std::uint32_t>(batch); ++b) {
+            const bool side = (b & 1u) != 0;
+            HipOperators& ops = side ? side_operators_ : operators_;
+            dpt_.set_slot_suffix(side ? "@side" : "");
+            FeatureMap refined[4];
+            for (std::uint32_t i = 0; i < 4; ++i) refined[i] = dpt_.prepare_level(i, *features[i], b, pw, ph, arena_, ops);
+            dpt_.refine_and_head(refined, b, pw, ph, arena_, output,
+                                 b + 1 == static_cast<std::uint32_t>(batch) ? pre_relu : nullptr, &ops);
+        }
+        dpt_.set_slot_suffix("");
+        hip_check(hipEventRecord(side_done_, side_stream_), "side event");
+        hip_check(hipStreamWaitEvent(main, side_done_, 0), "main wait");
         return;
     }
     // Levels 0-2 of the DPT head only need their own captured feature: each
@@ -94,7 +111,6 @@ void HipExecutor::run(const float* input, int batch, int width, int height, floa
     // the remaining encoder blocks. Level 3 (the last block's feature) runs
     // on the main stream, which then waits for the side stream before the
     // refinenets read all four levels.
-    const hipStream_t main = operators_.stream();
     FeatureMap refined[4];
     dino_.forward(input, w, h, 1u, arena_, features, [&](std::uint32_t level) {
         if (level >= 3) return;

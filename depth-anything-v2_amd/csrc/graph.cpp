@@ -196,7 +196,7 @@ FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::str
     out.width = (in.width + 2 * pad - k) / stride + 1;
     out.height = (in.height + 2 * pad - k) / stride + 1;
     out.channels = oc;
-    out.buffer = &arena.get(slot, out.elements() * sizeof(float));
+    out.buffer = &arena.get(slot + suffix_, out.elements() * sizeof(float));
     const GpuTensor& w = weights_.tensor(weight);
     const DeviceBuffer& b = has_bias ? weights_.tensor(bias).buffer : zero_bias_;
     if (precision_ == Precision::fp32) {
@@ -213,7 +213,7 @@ FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::str
     if (in.maxima && in.maxima_relu == f.relu_input) f.input_maxima = in.maxima;
     DeviceBuffer* maxima = nullptr;
     if (emit != Emit::none && oc % 32 == 0) {
-        maxima = &arena.get(slot + ".max", std::uint64_t(oc / 32) * out.width * out.height * sizeof(float));
+        maxima = &arena.get(slot + suffix_ + ".max", std::uint64_t(oc / 32) * out.width * out.height * sizeof(float));
         f.emit_maxima = maxima;
         f.emit_relu = emit == Emit::relu;
     }
@@ -227,11 +227,12 @@ FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::str
 
 FeatureMap DptHead::resize(HipOperators& ops, const FeatureMap& in, std::uint32_t ow, std::uint32_t oh, Arena& arena,
                            const std::string& slot, std::uint32_t consumer_channels, std::uint32_t consumer_kernel) {
-    FeatureMap out{&arena.get(slot, std::uint64_t(ow) * oh * in.channels * sizeof(float)), ow, oh, in.channels};
+    FeatureMap out{&arena.get(slot + suffix_, std::uint64_t(ow) * oh * in.channels * sizeof(float)), ow, oh,
+                   in.channels};
     const std::uint32_t pad = (consumer_kernel - 1) / 2;
     if (precision_ != Precision::fp32 && in.channels % 32 == 0 &&
         HipOperators::implicit_conv(ow, oh, in.channels, consumer_channels, consumer_kernel, 1, pad)) {
-        out.maxima = &arena.get(slot + ".max", std::uint64_t(in.channels / 32) * ow * oh * sizeof(float));
+        out.maxima = &arena.get(slot + suffix_ + ".max", std::uint64_t(in.channels / 32) * ow * oh * sizeof(float));
         ops.bilinear_align_true_maxima(*out.buffer, *out.maxima, *in.buffer, in.width, in.height, ow, oh, in.channels);
         return out;
     }
@@ -256,13 +257,14 @@ FeatureMap DptHead::residual_unit(HipOperators& ops, const FeatureMap& in, const
                 second_fusion);
 }
 
-FeatureMap DptHead::fusion(const FeatureMap& path, const std::string& prefix, std::uint32_t ow, std::uint32_t oh,
-                           const FeatureMap* next_skip, Arena& arena, const std::string& slot, bool next_is_head) {
+FeatureMap DptHead::fusion(HipOperators& ops, const FeatureMap& path, const std::string& prefix, std::uint32_t ow,
+                           std::uint32_t oh, const FeatureMap* next_skip, Arena& arena, const std::string& slot,
+                           bool next_is_head) {
     // dpt.cpp:574-615 from resConfUnit2 on: the path arrives with this
     // refinenet's processed skip already added (by the previous out_conv).
     const std::uint32_t F = config_.features;
-    FeatureMap unit = residual_unit(ops_, path, prefix + ".resConfUnit2", arena, "dpt.ru.first", "dpt.fu.unit");
-    FeatureMap resized = resize(ops_, unit, ow, oh, arena, "dpt.fu.resized", F, 1);
+    FeatureMap unit = residual_unit(ops, path, prefix + ".resConfUnit2", arena, "dpt.ru.first", "dpt.fu.unit");
+    FeatureMap resized = resize(ops, unit, ow, oh, arena, "dpt.fu.resized", F, 1);
     // path + processed skip of the next refinenet (add.glsl; a + b == b + a).
     // The output feeds the next refinenet's residual unit (input ReLU) or
     // the head's output_conv1.
@@ -272,7 +274,7 @@ FeatureMap DptHead::fusion(const FeatureMap& path, const std::string& prefix, st
     const Emit emit = !HipOperators::implicit_conv(ow, oh, F, next_oc, 3, 1, 1) ? Emit::none
                       : next_is_head                                         ? Emit::absolute
                                                                              : Emit::relu;
-    return conv(ops_, resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", F, 1, 1, 0, true, arena, slot,
+    return conv(ops, resized, prefix + ".out_conv.weight", prefix + ".out_conv.bias", F, 1, 1, 0, true, arena, slot,
                 add_skip, emit);
 }
 
@@ -282,7 +284,8 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
     // Projection and resize layer (dpt.cpp:635-736).
     const std::string prefix = "depth_head.projects." + std::to_string(i);
     const GpuTensor& w = weights_.tensor(prefix + ".weight");
-    FeatureMap proj{&arena.get("dpt.proj" + std::to_string(i), std::uint64_t(pw) * ph * config_.project[i] * sizeof(float)),
+    FeatureMap proj{&arena.get("dpt.proj" + std::to_string(i) + suffix_,
+                               std::uint64_t(pw) * ph * config_.project[i] * sizeof(float)),
                     pw, ph, config_.project[i]};
     DeviceBuffer tokens = DeviceBuffer::view(feature.as<float>() + std::uint64_t(b) * T * D,
                                              std::uint64_t(T) * D * sizeof(float));
@@ -297,7 +300,7 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
         const std::uint32_t k = i == 0 ? 4 : 2;
         const std::string r = "depth_head.resize_layers." + std::to_string(i);
         const GpuTensor& rw = weights_.tensor(r + ".weight");
-        layer = FeatureMap{&arena.get("dpt.layer" + std::to_string(i),
+        layer = FeatureMap{&arena.get("dpt.layer" + std::to_string(i) + suffix_,
                                       std::uint64_t(pw) * k * ph * k * proj.channels * sizeof(float)),
                            pw * k, ph * k, proj.channels};
         if (precision_ == Precision::fp32)
@@ -329,26 +332,27 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
 }
 
 void DptHead::refine_and_head(const FeatureMap refined[4], std::uint32_t b, std::uint32_t pw, std::uint32_t ph,
-                              Arena& arena, float* depth, float* pre_relu) {
+                              Arena& arena, float* depth, float* pre_relu, HipOperators* ops_in) {
+    HipOperators& ops = ops_in ? *ops_in : ops_;
     const std::uint32_t F = config_.features;
     // refinenets (dpt.cpp:759-790); refined[0..2] are the processed skip
     // inputs of refinenet1..3, refined[3] the deepest level. Outputs
     // alternate between two slots.
-    FeatureMap path = fusion(refined[3], "depth_head.scratch.refinenet4", refined[2].width, refined[2].height,
+    FeatureMap path = fusion(ops, refined[3], "depth_head.scratch.refinenet4", refined[2].width, refined[2].height,
                              &refined[2], arena, "dpt.pathA");
-    path = fusion(path, "depth_head.scratch.refinenet3", refined[1].width, refined[1].height, &refined[1], arena,
+    path = fusion(ops, path, "depth_head.scratch.refinenet3", refined[1].width, refined[1].height, &refined[1], arena,
                   "dpt.pathB");
-    path = fusion(path, "depth_head.scratch.refinenet2", refined[0].width, refined[0].height, &refined[0], arena,
+    path = fusion(ops, path, "depth_head.scratch.refinenet2", refined[0].width, refined[0].height, &refined[0], arena,
                   "dpt.pathA");
-    path = fusion(path, "depth_head.scratch.refinenet1", refined[0].width * 2, refined[0].height * 2, nullptr, arena,
+    path = fusion(ops, path, "depth_head.scratch.refinenet1", refined[0].width * 2, refined[0].height * 2, nullptr, arena,
                   "dpt.pathB", /*next_is_head=*/true);
     // output head (dpt.cpp:792-855)
-    path = conv(ops_, path, "depth_head.scratch.output_conv1.weight", "depth_head.scratch.output_conv1.bias", F / 2, 3,
+    path = conv(ops, path, "depth_head.scratch.output_conv1.weight", "depth_head.scratch.output_conv1.bias", F / 2, 3,
                 1, 1, true, arena, "dpt.out1");
-    FeatureMap full = resize(ops_, path, pw * 14, ph * 14, arena, "dpt.full", 32, 3);
+    FeatureMap full = resize(ops, path, pw * 14, ph * 14, arena, "dpt.full", 32, 3);
     ConvFusion relu_after;
     relu_after.relu_output = true;
-    FeatureMap head = conv(ops_, full, "depth_head.scratch.output_conv2.0.weight", "depth_head.scratch.output_conv2.0.bias",
+    FeatureMap head = conv(ops, full, "depth_head.scratch.output_conv2.0.weight", "depth_head.scratch.output_conv2.0.bias",
                            32, 3, 1, 1, true, arena, "dpt.out2", relu_after);
     // output_conv2.2 (1x1, 32 -> 1) and the final ReLU in one pass; the
     // pre-ReLU logits go to pre_relu when asked.
@@ -360,16 +364,16 @@ void DptHead::refine_and_head(const FeatureMap refined[4], std::uint32_t b, std:
     if (precision_ == Precision::fp32) {
         const DeviceBuffer& b3 = weights_.tensor("depth_head.scratch.output_conv2.2.bias").buffer;
         if (logits) {
-            ops_.conv2d(logits, *head.buffer, w3.buffer, b3, head.width, head.height, head.channels, 1, 1, 1, 0, true);
-            ops_.relu(out, logits, static_cast<std::uint32_t>(pixels));
+            ops.conv2d(logits, *head.buffer, w3.buffer, b3, head.width, head.height, head.channels, 1, 1, 1, 0, true);
+            ops.relu(out, logits, static_cast<std::uint32_t>(pixels));
         } else {
-            ops_.conv2d(out, *head.buffer, w3.buffer, b3, head.width, head.height, head.channels, 1, 1, 1, 0, true,
+            ops.conv2d(out, *head.buffer, w3.buffer, b3, head.width, head.height, head.channels, 1, 1, 1, 0, true,
                         relu_after);
         }
         return;
     }
     if (!w3.int8_buffer) throw std::runtime_error("output_conv2.2 weight is not int8");
-    ops_.conv1x1_narrow_int8(out, *head.buffer, w3.int8_buffer, w3.int8_ld, w3.int8_scales,
+    ops.conv1x1_narrow_int8(out, *head.buffer, w3.int8_buffer, w3.int8_ld, w3.int8_scales,
                              weights_.tensor("depth_head.scratch.output_conv2.2.bias").buffer, head.width, head.height,
                              head.channels, 1, true, relu_after, logits ? &logits : nullptr);
 }

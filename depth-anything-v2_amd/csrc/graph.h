@@ -102,7 +102,11 @@ public:
     FeatureMap prepare_level(std::uint32_t level, const DeviceBuffer& feature, std::uint32_t b,
                              std::uint32_t patch_width, std::uint32_t patch_height, Arena& arena, HipOperators& ops);
     void refine_and_head(const FeatureMap refined[4], std::uint32_t b, std::uint32_t patch_width,
-                         std::uint32_t patch_height, Arena& arena, float* depth, float* pre_relu);
+                         std::uint32_t patch_height, Arena& arena, float* depth, float* pre_relu,
+                         HipOperators* ops = nullptr);
+    // Appended to every arena slot name of the calls that follow, so that
+    // two images' heads can be in flight on two streams at once.
+    void set_slot_suffix(const std::string& suffix) { suffix_ = suffix; }
 
 private:
     FeatureMap conv(HipOperators& ops, const FeatureMap& input, const std::string& weight, const std::string& bias,
@@ -121,15 +125,16 @@ private:
     // dpt.cpp:574-615) when given.
     // next_is_head: the output feeds the head's output_conv1 (no input ReLU)
     // rather than the next refinenet's residual unit.
-    FeatureMap fusion(const FeatureMap& path, const std::string& prefix, std::uint32_t output_width,
-                      std::uint32_t output_height, const FeatureMap* next_skip, Arena& arena, const std::string& slot,
-                      bool next_is_head = false);
+    FeatureMap fusion(HipOperators& ops, const FeatureMap& path, const std::string& prefix,
+                      std::uint32_t output_width, std::uint32_t output_height, const FeatureMap* next_skip,
+                      Arena& arena, const std::string& slot, bool next_is_head = false);
 
     DptConfig config_;
     GpuModel& weights_;
     HipOperators& ops_;
     DeviceBuffer zero_bias_;
     Precision precision_;
+    std::string suffix_;
 };
 
 }  // namespace dav2
