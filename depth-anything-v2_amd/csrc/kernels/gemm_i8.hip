@@ -385,7 +385,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
                 if (col + 2 < g.rows_q) dst[2] = v.z;
             }
         }
-        if (kColMax && col0 >= g.col_absmax_begin) {
+        if constexpr (kColMax) if (col0 >= g.col_absmax_begin) {
             // lanes l, l ^ 16, l ^ 32, l ^ 48 of a wave hold the same columns
             static_assert(kLanesPerRow == 16 && BM * kOutStride * 4 + NW * BN * 4 <=
                           (BM * kOutStride * 4 > STAGES * (BM + BN) * BK ? BM * kOutStride * 4 : STAGES * (BM + BN) * BK),
@@ -474,7 +474,12 @@ void launch_cfg(const GemmParams& g, hipStream_t s, bool last = true) {
     launch_timed(gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>, grid, dim3(64 * WMW * WNW), lds, s, true, last, g);
 }
 
-// Rows of P per tile of the configuration launch_epi picks.
+// Rows of P from which launch_epi picks 64x128 tiles for the row-major
+// epilogues other than the column-maxima one.
+constexpr uint32_t kWideTileRows = 4096;
+
+// Rows of P per tile of the configuration launch_epi picks (the 64x128 tiles
+// have 64 rows as well).
 inline uint32_t tile_rows(uint32_t rows_p, uint32_t rows_q, bool row_major) {
     if (rows_p <= 32) return 32;
     if (row_major && rows_q >= 2048 && rows_p >= 512) return 96;
@@ -489,6 +494,17 @@ void launch_epi(const GemmParams& g, hipStream_t s, bool last = true) {
     // (720 workgroups for N = 3072, one round at three per CU, against 1056
     // 64x64 ones). Channel-major GEMMs with few output channels use 32-row
     // tiles.
+    // From M = 4096 rows on (ViT-L 518 batch 8: M = 10960) 64x128 tiles
+    // with a two-stage ring are fastest for the row-major GEMMs without
+    // column maxima (proj / fc1 / fc2: 35 / 126 / 106 us with the tiles
+    // below, 29 / 97 / 73 us with these); the column-maxima epilogue needs
+    // 64-column tiles.
+    if constexpr (row_major_epi<EPI>() && EPI != DAV2_GEMM_EPI_ROW_COLMAX) {
+        if (g.rows_p >= kWideTileRows) {
+            launch_cfg<64, 128, 2, 2, 128, 2, EPI>(g, s, last);
+            return;
+        }
+    }
     switch (tile_rows(g.rows_p, g.rows_q, row_major_epi<EPI>())) {
         case 32: launch_cfg<32, 64, 1, 2, 128, 3, EPI>(g, s, last); break;
         case 96: launch_cfg<96, 64, 2, 2, 128, 2, EPI>(g, s, last); break;
