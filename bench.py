@@ -50,7 +50,9 @@ def cpu_baseline(model_path: Path, encoder: str, size: int, budget_s: float) -> 
 
     fmt = load_package().dav2_format
     oracle = Oracle()
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    # Every core this process may run on; OMP_NUM_THREADS, where the host
+    # sets it (the GPU host caps a one-GPU job's CPU share this way), wins.
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or host_cpus()["usable"]
     oracle.lib.orc_set_threads(threads)
     enc_id = {"vits": 0, "vitb": 1, "vitl": 2}[encoder]
     h = oracle.load_model(model_path, enc_id)
@@ -60,9 +62,28 @@ def cpu_baseline(model_path: Path, encoder: str, size: int, budget_s: float) -> 
         oracle.infer(h, x, size, size, fp16_attention=True)
         dt = time.perf_counter() - t0
         return {"value": 1.0 / dt, "unit": "images/s", "cores": oracle.lib.orc_get_threads(), "kind": "port",
-                "sample": f"1 full {encoder} {size}x{size} image through the oracle's int8 graph ({dt:.2f} s)"}
+                "sample": f"1 full {encoder} {size}x{size} image through the oracle's int8 graph ({dt:.2f} s)",
+                **{f"host_{k}": v for k, v in host_cpus().items()}}
     finally:
         oracle.free_model(h)
+
+
+def host_cpus() -> dict:
+    """CPU facts of this host: logical CPUs (nproc of the machine), the CPUs
+    this process may run on, and the CPU model name."""
+    model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"nproc": os.cpu_count() or 1, "usable": usable, "cpu_model": model}
 
 
 def cpu_preprocess_ms(width: int, height: int, input_size: int) -> float:
@@ -84,6 +105,44 @@ def cpu_preprocess_ms(width: int, height: int, input_size: int) -> float:
     return 1e3 * best
 
 
+BANDWIDTH_KERNELS = ("layer_norm_quantize_i8", "layer_norm", "softmax_f32", "quantize_rows_i8")
+
+
+def profile_config(pkg, fmt, torch, model: Path, size: int, batch: int, fp32_attention: bool, steps: int) -> dict:
+    """A few profiled steps of one configuration: per-launch HIP events give
+    each kernel's time; reported are the GEMM's int8 rate and the HBM rate of
+    the bandwidth-bound kernels, with the images/s of the profiled pass."""
+    flags = pkg.FORCE_INT8 | (pkg.FORCE_FP32_ATTENTION if fp32_attention else 0)
+    x = torch.from_numpy(fmt.imagenet_input(size, size, SEED + 3, batch)).cuda()
+    n_out = batch * size * size
+    out = torch.empty(n_out, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    with pkg.Context(str(model), "vitl", flags) as ctx:
+        ctx.infer_device(x.data_ptr(), batch, size, size, out.data_ptr(), n_out, stream)
+        torch.cuda.synchronize()
+        ctx.profile(True)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ctx.infer_device(x.data_ptr(), batch, size, size, out.data_ptr(), n_out, stream)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        prof = ctx.profile_report()
+        ctx.profile(False)
+    res = {"profiled_images_per_s": batch * steps / dt}
+    g = prof.get("gemm_i8")
+    if g and g["ms"]:
+        rate = g["work"] / (g["ms"] * 1e-3) / 1e12
+        res["gemm_i8"] = {"T/s": rate, "frac": rate / PEAK_INT8_TOPS, "avg_us": 1e3 * g["ms"] / g["launches"]}
+    for name in BANDWIDTH_KERNELS:
+        v = prof.get(name)
+        if v and v["ms"]:
+            rate = v["work"] / (v["ms"] * 1e-3) / 1e9
+            res[name] = {"GB/s": rate, "frac_hbm": rate / PEAK_HBM_GBS, "avg_us": 1e3 * v["ms"] / v["launches"]}
+    del x, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,6 +156,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=30.0)
     ap.add_argument("--profile-json", default="")
     ap.add_argument("--no-fp32-mode", action="store_true", help="skip the FORCE_FP32 comparison run")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the batch-8 / 1036x1036 kernel measurements")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run one device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -152,16 +213,33 @@ def main() -> int:
         elapsed = time.perf_counter() - t0
         print(f"bench: {args.steps} steps in {elapsed:.3f} s", file=sys.stderr, flush=True)
 
-        # The host-buffer entry (dav2_infer_tensor_f32): PCIe copies included.
+        # Per-step device-resident times (each step synchronised), for the
+        # median beside the K-step throughput.
+        step_s = []
+        for _ in range(max(20, args.steps)):
+            s0 = time.perf_counter()
+            step()
+            torch.cuda.synchronize()
+            step_s.append(time.perf_counter() - s0)
+        device_median = args.batch / float(np.median(step_s))
+
+        # The host-buffer entry (dav2_infer_tensor_f32): H2D and D2H copies
+        # included; the median over >= 20 calls after one warm-up call.
         host_rate = None
+        host_entry = None
         host_steps = min(args.steps, 10)
         if args.batch == 1:
             x_host = fmt.imagenet_input(args.size, args.size, SEED + 3)[0]
             ctx.infer(x_host, args.size, args.size)
-            h0 = time.perf_counter()
-            for _ in range(host_steps):
+            calls = []
+            for _ in range(max(20, args.steps)):
+                h0 = time.perf_counter()
                 ctx.infer(x_host, args.size, args.size)
-            host_rate = host_steps / (time.perf_counter() - h0)
+                calls.append(time.perf_counter() - h0)
+            host_rate = 1.0 / float(np.median(calls))
+            host_entry = {"entry": "dav2_infer_tensor_f32 (host buffers, PCIe copies included)",
+                          "calls": len(calls), "median_ms": 1e3 * float(np.median(calls)),
+                          "mean_ms": 1e3 * float(np.mean(calls)), "images_per_s_median": host_rate}
 
         # Host-image entries (dav2_infer_bgr8): a 518x518 BGR8 frame through
         # the GPU preprocessing and the same inference, PCIe copies included;
@@ -265,6 +343,18 @@ def main() -> int:
             Path(args.profile_json).write_text(json.dumps({"raw": prof, "kernels": kernels}, indent=1))
         print("bench: per-kernel " + json.dumps(kernels), file=sys.stderr, flush=True)
 
+        # Further configurations of the same model family, a few profiled
+        # steps each: the bandwidth-bound kernels (LayerNorm + quantize,
+        # materialised softmax of the fp32-attention path) and the GEMM at
+        # batch 8 and at 1036x1036 batch 4.
+        extra = None
+        if not args.no_extra and args.encoder == "vitl" and args.size == 518 and args.batch == 1:
+            extra = {}
+            for size, batch, fp32_att in ((518, 8, False), (1036, 4, False), (518, 8, True), (1036, 4, True)):
+                key = f"vitl_{size}_b{batch}" + ("_fp32_attention" if fp32_att else "")
+                extra[key] = profile_config(pkg, fmt, torch, model, size, batch, fp32_att, steps=3)
+                print(f"bench: extra {key} " + json.dumps(extra[key]), file=sys.stderr, flush=True)
+
         cpu = None
         if not args.no_cpu_baseline:
             cpu = cpu_baseline(model, args.encoder, args.size, args.cpu_budget)
@@ -297,7 +387,10 @@ def main() -> int:
                      "traffic": traffic},
         "kernels": {k: kernels[k] for k in list(kernels)[:8]},
         "profiled_ms_per_step": 1e3 * profiled_elapsed / args.steps,
+        "device_median_images_per_s": device_median,
         "host_entry_images_per_s": host_rate,
+        "host_entry": host_entry,
+        "extra_configs": extra,
         "image_paths": image_paths,
         "fp32_mode_images_per_s": fp32_rate,
         "depth_finite": bool(np.isfinite(depth).all()),

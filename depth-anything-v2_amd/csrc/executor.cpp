@@ -246,10 +246,12 @@ HipJob::~HipJob() {
 }
 
 dav2_gpu_job_state HipJob::state() const {
-    if (cancelled_) return DAV2_GPU_JOB_CANCELLED;
+    // vulkan_executor.cpp:450-457: CANCELLED, else COMPLETE once the
+    // submission has finished, else RUNNING.
+    if (cancelled_.load(std::memory_order_acquire)) return DAV2_GPU_JOB_CANCELLED;
     const hipError_t e = hipEventQuery(done_);
     if (e == hipSuccess) return DAV2_GPU_JOB_COMPLETE;
-    if (e == hipErrorNotReady) return DAV2_GPU_JOB_QUEUED;
+    if (e == hipErrorNotReady) return DAV2_GPU_JOB_RUNNING;
     return DAV2_GPU_JOB_FAILED;
 }
 

@@ -5,6 +5,7 @@
 #include "graph.h"
 #include "model.h"
 
+#include <atomic>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -17,9 +18,10 @@ namespace dav2 {
 class HipJob {
 public:
     ~HipJob();
-    // DAV2_GPU_JOB_* state: QUEUED until the GPU work has finished.
+    // DAV2_GPU_JOB_* state: RUNNING while the GPU work is in flight, then
+    // COMPLETE (or CANCELLED once cancel() has been called).
     dav2_gpu_job_state state() const;
-    void cancel() { cancelled_ = true; }
+    void cancel() { cancelled_.store(true, std::memory_order_release); }
     void wait() const;
 
 private:
@@ -29,7 +31,7 @@ private:
     hipEvent_t ipc_wait_ = nullptr;
     void* mapped_input_ = nullptr;
     void* mapped_output_ = nullptr;
-    bool cancelled_ = false;
+    std::atomic<bool> cancelled_{false};
 };
 
 class HipExecutor {
@@ -68,7 +70,7 @@ private:
 public:
 
     dav2_encoder encoder() const { return encoder_; }
-    float metric_max_depth() const { return model_.derivation().metric_max_depth; }
+    float metric_max_depth() const { return model_.provenance().metric_max_depth; }
     void transfer_counters(std::uint64_t& upload, std::uint64_t& download) const {
         upload = context_.upload_bytes();
         download = context_.download_bytes();
@@ -95,7 +97,7 @@ public:
 private:
 
     dav2_encoder encoder_;
-    ModelFile model_;  // validated before any HIP call, as the reference's member order does
+    MappedModel model_;  // validated before any HIP call, as the reference's member order does
     HipContext context_;
     Precision precision_;  // int8, or fp32 under FORCE_FP32
     Precision attention_precision_;

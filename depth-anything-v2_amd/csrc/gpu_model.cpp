@@ -26,7 +26,7 @@ bool quantizable_family(std::string_view name) {
 }
 
 std::uint32_t fast_crc32(const void* data, std::uint64_t bytes) {
-    // zlib's CRC-32 is the same polynomial/reflection as crc32() in model.cpp
+    // zlib's CRC-32 is the IEEE 802.3 polynomial/reflection the .dav2 format stores
     // (IEEE 802.3), just faster; fed in <4 GiB pieces.
     uLong c = ::crc32(0L, Z_NULL, 0);
     const auto* p = static_cast<const Bytef*>(data);
@@ -45,53 +45,53 @@ bool transposed_convolution_weight(std::string_view name) {
     return name == "depth_head.resize_layers.0.weight" || name == "depth_head.resize_layers.1.weight";
 }
 
-bool use_int8_weight(std::string_view name, const TensorView& t) {
+bool use_int8_weight(std::string_view name, const WeightRecord& t) {
     // src/gpu_model.cpp:35-44
-    if (!quantizable_family(name) || t.dimensions[0] == 0) return false;
-    if (t.rank == 2) return t.dimensions[1] % 4 == 0;
+    if (!quantizable_family(name) || t.shape[0] == 0) return false;
+    if (t.rank == 2) return t.shape[1] % 4 == 0;
     if (t.rank != 4) return false;
-    if (transposed_convolution_weight(name)) return t.dimensions[0] % 4 == 0;
-    return (t.elements / t.dimensions[0]) % 4 == 0;
+    if (transposed_convolution_weight(name)) return t.shape[0] % 4 == 0;
+    return (t.count / t.shape[0]) % 4 == 0;
 }
 
-GpuModel::GpuModel(const ModelFile& model, HipContext& context, bool fp32_weights) {
-    tensors_.reserve(model.tensor_count());
+GpuModel::GpuModel(const MappedModel& model, HipContext& context, bool fp32_weights) {
+    tensors_.reserve(model.records().size());
     DeviceBuffer staging;
     std::vector<std::unique_ptr<std::vector<float>>> host_keepalive;
     const hipStream_t stream = context.active_stream();
-    for (std::string_view name : model.tensor_names()) {
-        const TensorView& src = model.tensor(name);
-        const std::uint64_t bytes = src.elements * sizeof(float);
-        if (fast_crc32(src.data, bytes) != src.crc32)
+    for (const WeightRecord& src : model.records()) {
+        const std::string_view name = src.name;
+        const std::uint64_t bytes = src.count * sizeof(float);
+        if (fast_crc32(src.values, bytes) != src.checksum)
             throw std::runtime_error("model tensor checksum mismatch: " + std::string(name));
         GpuTensor dst;
-        dst.dimensions = src.dimensions;
+        for (int d = 0; d < 4; ++d) dst.dimensions[d] = src.shape[d];
         dst.rank = src.rank;
-        dst.elements = src.elements;
+        dst.elements = src.count;
         if (!use_int8_weight(name, src)) {
             dst.buffer = context.create_device_buffer(bytes);
-            context.upload(dst.buffer, src.data, bytes);
+            context.upload(dst.buffer, src.values, bytes);
             device_bytes_ += bytes;
         } else {
             const bool convT = transposed_convolution_weight(name);
-            const float* rows_source = src.data;
+            const float* rows_source = src.values;
             std::uint64_t rows = 0, columns = 0;
             if (convT) {
-                const std::uint64_t ic = src.dimensions[0], oc = src.dimensions[1], k = src.dimensions[2];
-                if (src.rank != 4 || src.dimensions[3] != k) throw std::runtime_error("invalid ConvTranspose weight");
+                const std::uint64_t ic = src.shape[0], oc = src.shape[1], k = src.shape[2];
+                if (src.rank != 4 || src.shape[3] != k) throw std::runtime_error("invalid ConvTranspose weight");
                 rows = k * k * oc;
                 columns = ic;
                 auto reordered = std::make_unique<std::vector<float>>(rows * columns);
                 for (std::uint64_t r = 0; r < rows; ++r) {
                     const std::uint64_t kidx = r / oc, o = r % oc, ky = kidx / k, kx = kidx % k;
                     for (std::uint64_t c = 0; c < ic; ++c)
-                        (*reordered)[r * columns + c] = src.data[((c * oc + o) * k + ky) * k + kx];
+                        (*reordered)[r * columns + c] = src.values[((c * oc + o) * k + ky) * k + kx];
                 }
                 rows_source = reordered->data();
                 host_keepalive.push_back(std::move(reordered));
             } else {
-                rows = src.dimensions[0];
-                columns = src.elements / rows;
+                rows = src.shape[0];
+                columns = src.count / rows;
             }
             if (rows > 0xffffffffull || columns > 0xffffffffull) throw std::runtime_error("weight too large");
             if (fp32_weights) {
@@ -122,14 +122,14 @@ GpuModel::GpuModel(const ModelFile& model, HipContext& context, bool fp32_weight
                                                 dst.int8_scales.as<float>(), stream),
                       "weight quantization");
             device_bytes_ += rows * dst.int8_ld + rows * sizeof(float);
-            const std::uint64_t k = src.dimensions[2];
-            if (!convT && src.rank == 4 && src.dimensions[3] == k &&
-                dav2_hip_conv2d_i8_supported(1, 1, static_cast<std::uint32_t>(src.dimensions[1]),
+            const std::uint64_t k = src.shape[2];
+            if (!convT && src.rank == 4 && src.shape[3] == k &&
+                dav2_hip_conv2d_i8_supported(1, 1, static_cast<std::uint32_t>(src.shape[1]),
                                              dst.int8_rows, static_cast<std::uint32_t>(k), 1,
                                              static_cast<std::uint32_t>((k - 1) / 2))) {
                 dst.int8_tapmajor = context.create_device_buffer(rows * columns);
                 hip_check(dav2_hip_conv_weights_tapmajor(dst.int8_tapmajor.as<int8_t>(), dst.int8_buffer.as<int8_t>(),
-                                                         dst.int8_rows, static_cast<std::uint32_t>(src.dimensions[1]),
+                                                         dst.int8_rows, static_cast<std::uint32_t>(src.shape[1]),
                                                          static_cast<std::uint32_t>(k), dst.int8_ld, stream),
                           "tap-major conv weights");
                 device_bytes_ += rows * columns;

@@ -41,14 +41,14 @@ struct GpuTensor {
     std::uint64_t elements = 0;
 };
 
-bool use_int8_weight(std::string_view name, const TensorView& tensor);
+bool use_int8_weight(std::string_view name, const WeightRecord& tensor);
 bool transposed_convolution_weight(std::string_view name);
 inline std::uint32_t padded_k(std::uint64_t columns) { return static_cast<std::uint32_t>((columns + 63) & ~63ull); }
 
 class GpuModel {
 public:
     // fp32_weights: the fp32 precision mode (no int8 copies).
-    GpuModel(const ModelFile& model, HipContext& context, bool fp32_weights = false);
+    GpuModel(const MappedModel& model, HipContext& context, bool fp32_weights = false);
     const GpuTensor& tensor(std::string_view name) const;
     bool contains(std::string_view name) const { return tensors_.count(std::string(name)) != 0; }
     std::size_t tensor_count() const { return tensors_.size(); }

@@ -478,9 +478,11 @@ void launch_cfg(const GemmParams& g, hipStream_t s, bool last = true) {
 // epilogues other than the column-maxima one.
 constexpr uint32_t kWideTileRows = 4096;
 
-// Rows of P per tile of the configuration launch_epi picks (the 64x128 tiles
-// have 64 rows as well).
-inline uint32_t tile_rows(uint32_t rows_p, uint32_t rows_q, bool row_major) {
+// Rows of P per tile of the configuration launch_epi picks: 64 for the
+// 64x128 tiles of the large row-major GEMMs without column maxima
+// (rows_p >= kWideTileRows), else 32, 96 or 64 as in the switch below.
+inline uint32_t tile_rows(uint32_t rows_p, uint32_t rows_q, bool row_major, bool col_max) {
+    if (row_major && !col_max && rows_p >= kWideTileRows) return 64;
     if (rows_p <= 32) return 32;
     if (row_major && rows_q >= 2048 && rows_p >= 512) return 96;
     return 64;
@@ -505,7 +507,7 @@ void launch_epi(const GemmParams& g, hipStream_t s, bool last = true) {
             return;
         }
     }
-    switch (tile_rows(g.rows_p, g.rows_q, row_major_epi<EPI>())) {
+    switch (tile_rows(g.rows_p, g.rows_q, row_major_epi<EPI>(), EPI == DAV2_GEMM_EPI_ROW_COLMAX)) {
         case 32: launch_cfg<32, 64, 1, 2, 128, 3, EPI>(g, s, last); break;
         case 96: launch_cfg<96, 64, 2, 2, 128, 2, EPI>(g, s, last); break;
         default: launch_cfg<64, 64, 2, 2, 128, 3, EPI>(g, s, last); break;
@@ -633,5 +635,5 @@ extern "C" uint32_t dav2_hip_gemm_i8_row_tiles(uint32_t m, uint32_t n, uint32_t 
     const bool row_major = epilogue == DAV2_GEMM_EPI_ROW || epilogue == DAV2_GEMM_EPI_ROW_GELU ||
                            epilogue == DAV2_GEMM_EPI_ROW_LAYERSCALE || epilogue == DAV2_GEMM_EPI_ROW_COLMAX;
     const uint32_t rows_p = swapped ? n : m, rows_q = swapped ? m : n;
-    return ceil_div(rows_p, tile_rows(rows_p, rows_q, row_major));
+    return ceil_div(rows_p, tile_rows(rows_p, rows_q, row_major, epilogue == DAV2_GEMM_EPI_ROW_COLMAX));
 }

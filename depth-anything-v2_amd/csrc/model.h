@@ -1,63 +1,70 @@
-// .dav2 model file: read-only mmap with bounded validation.
-// Format and checks: reference src/model.{h,cpp} (header :27-69, checks
-// :165-315) and tools/export_model.py:21-38.
+// .dav2 weight file, memory-mapped read-only and validated before use.
+//
+// The on-disk format (64-byte header, 192-byte tensor records, optional
+// 128-byte provenance record, 64-byte aligned little-endian float32 payloads)
+// and its acceptance rules are those of the reference loader,
+// src/model.cpp:27-320, written by tools/export_model.py:21-38. The class
+// below is this build's own: it keeps the mapping alive, exposes the tensors
+// as a name-sorted table of WeightRecord entries for the GPU upload, and
+// records the provenance fields the C ABI reports (dav2_get_model_info).
 #pragma once
 
 #include "depth_anything_v2.h"
 
-#include <array>
 #include <cstddef>
 #include <cstdint>
 #include <string>
 #include <string_view>
-#include <unordered_map>
 #include <vector>
 
 namespace dav2 {
 
-struct TensorView {
-    const float* data = nullptr;
-    std::array<std::uint64_t, 4> dimensions{};
-    std::uint32_t rank = 0;
-    std::uint64_t elements = 0;
-    std::uint32_t crc32 = 0;
+// One float32 tensor inside the mapping.
+struct WeightRecord {
+    std::string_view name;     // points into the mapping (NUL-terminated there)
+    const float* values = nullptr;
+    std::uint32_t rank = 0;    // 1..4
+    std::uint64_t shape[4] = {0, 0, 0, 0};  // unused dimensions are 0
+    std::uint64_t count = 0;   // product of the used dimensions
+    std::uint32_t checksum = 0;  // CRC-32 (IEEE 802.3) the file stores for the payload
+
+    std::uint64_t dim(std::uint32_t i) const { return i < 4 ? shape[i] : 0; }
 };
 
-struct ModelDerivation {
-    bool present = false;
-    std::array<std::uint8_t, 32> canonical_sha256{};
+// The optional provenance record ("DAV2META").
+struct ModelProvenance {
+    bool recorded = false;
+    bool metric = false;
+    float metric_max_depth = 0.0f;  // 20 or 80 for metric heads, else 0
     std::string converter;
-    std::uint32_t format_version = 0;
-    dav2_encoder encoder = DAV2_ENCODER_VITS;
-    float metric_max_depth = 0.0f;
 };
 
-// Thrown for every malformed-file condition; the C ABI reports it as
-// DAV2_STATUS_INTERNAL_ERROR like the reference (src/dav2.cpp:85-86).
-class ModelFile {
+// Malformed files throw std::runtime_error with the reference's message; the
+// C ABI reports them as DAV2_STATUS_INTERNAL_ERROR (src/dav2.cpp:85-86).
+class MappedModel {
 public:
-    ModelFile(const std::string& path_utf8, dav2_encoder expected_encoder);
-    ~ModelFile();
-    ModelFile(const ModelFile&) = delete;
-    ModelFile& operator=(const ModelFile&) = delete;
+    MappedModel(const std::string& path_utf8, dav2_encoder expected_encoder);
+    ~MappedModel();
+    MappedModel(const MappedModel&) = delete;
+    MappedModel& operator=(const MappedModel&) = delete;
 
-    const TensorView& tensor(std::string_view name) const;
-    bool contains(std::string_view name) const;
-    std::size_t tensor_count() const { return tensors_.size(); }
-    const std::vector<std::string_view>& tensor_names() const { return names_; }
-    const ModelDerivation& derivation() const { return derivation_; }
+    // Tensors in file order.
+    const std::vector<WeightRecord>& records() const { return records_; }
+    // Lookup by name (binary search over a name-sorted index); find() returns
+    // nullptr for a missing name, at() throws.
+    const WeightRecord* find(std::string_view name) const;
+    const WeightRecord& at(std::string_view name) const;
+    const ModelProvenance& provenance() const { return provenance_; }
 
 private:
-    void close() noexcept;
+    void unmap() noexcept;
 
     int fd_ = -1;
-    const std::byte* view_ = nullptr;
-    std::uint64_t size_ = 0;
-    std::unordered_map<std::string_view, TensorView> tensors_;
-    std::vector<std::string_view> names_;
-    ModelDerivation derivation_;
+    const std::byte* base_ = nullptr;
+    std::uint64_t bytes_ = 0;
+    std::vector<WeightRecord> records_;
+    std::vector<std::uint32_t> by_name_;  // indices into records_, sorted by name
+    ModelProvenance provenance_;
 };
-
-std::uint32_t crc32(const void* data, std::size_t bytes);
 
 }  // namespace dav2

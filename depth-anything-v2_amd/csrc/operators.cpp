@@ -331,12 +331,14 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
         const std::uint32_t ld = ld64(patch_columns);
         DeviceBuffer& packed = workspace_.packed(std::uint64_t(spatial) * ld);
         DeviceBuffer& scales = workspace_.scales(std::uint64_t(spatial) * sizeof(float));
-        ProfileScope prof_patch(context_.profiler(), "im2col_quantize_i8",
-                                12.0 * input_width * input_height + 1.0 * spatial * patch_columns + 4.0 * spatial,
-                                "B", s);
-        hip_check(dav2_hip_im2col_quantize_i8(image.as<float>(), input_width, input_height, 3, pw, ph, 14, 14, 0,
-                                              packed.as<int8_t>(), ld, scales.as<float>(), nullptr, 0, s),
-                  "patch im2col");
+        {  // the scope ends before the GEMM launch: it times the im2col kernel alone
+            ProfileScope prof_patch(context_.profiler(), "im2col_quantize_i8",
+                                    12.0 * input_width * input_height + 1.0 * spatial * patch_columns + 4.0 * spatial,
+                                    "B", s);
+            hip_check(dav2_hip_im2col_quantize_i8(image.as<float>(), input_width, input_height, 3, pw, ph, 14, 14, 0,
+                                                  packed.as<int8_t>(), ld, scales.as<float>(), nullptr, 0, s),
+                      "patch im2col");
+        }
         linear_int8_packed(output, packed, ld, patch_int8_weight, scales, patch_int8_scales, patch_bias, spatial,
                            patch_columns, embedding, 1u, static_cast<std::uint32_t>(tokens), false, true);
         workspace_ld_ = ld;
@@ -640,14 +642,17 @@ bool HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     const std::uint32_t ld = ld64(inner);
     DeviceBuffer& packed = workspace_.packed(std::uint64_t(rows) * ld);
     DeviceBuffer& scales = workspace_.scales(std::uint64_t(rows) * sizeof(float));
-    ProfileScope prof(context_.profiler(), "im2col_quantize_i8",
-                      4.0 * input_width * input_height * input_channels + 1.0 * rows * inner + 4.0 * rows, "B", s);
     grow(im2col_scratch_, scratch_floats * sizeof(float));
-    const auto im2col = fusion.relu_input && tiled ? dav2_hip_im2col_quantize_relu_i8 : dav2_hip_im2col_quantize_i8;
-    hip_check(im2col(src->as<float>(), input_width, input_height, input_channels, ow, oh, kernel, stride,
-                     static_cast<std::int32_t>(padding), packed.as<int8_t>(), ld, scales.as<float>(),
-                     im2col_scratch_.as<float>(), scratch_floats, s),
-              "im2col quantize");
+    {  // the scope ends before the GEMM launch: it times the im2col kernels alone
+        ProfileScope prof(context_.profiler(), "im2col_quantize_i8",
+                          4.0 * input_width * input_height * input_channels + 1.0 * rows * inner + 4.0 * rows, "B", s);
+        const auto im2col =
+            fusion.relu_input && tiled ? dav2_hip_im2col_quantize_relu_i8 : dav2_hip_im2col_quantize_i8;
+        hip_check(im2col(src->as<float>(), input_width, input_height, input_channels, ow, oh, kernel, stride,
+                         static_cast<std::int32_t>(padding), packed.as<int8_t>(), ld, scales.as<float>(),
+                         im2col_scratch_.as<float>(), scratch_floats, s),
+                  "im2col quantize");
+    }
     workspace_ld_ = ld;
     linear_int8_packed(output, packed, ld, int8_weight, scales, weight_scales, bias, rows, inner, output_channels, 0u,
                        rows, true, has_bias, fusion.residual, fusion.relu_output);
@@ -703,14 +708,17 @@ void HipOperators::conv_transpose_nonoverlap_int8(DeviceBuffer& output, const De
     DeviceBuffer& packed = workspace_.packed(std::uint64_t(input_rows) * ld);
     DeviceBuffer& scales = workspace_.scales(std::uint64_t(input_rows) * sizeof(float));
     const hipStream_t s = stream();
-    ProfileScope prof_q(context_.profiler(), "im2col_quantize_i8",
-                        4.0 * input_rows * input_channels + 1.0 * input_rows * input_channels + 4.0 * input_rows, "B", s);
     const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
     grow(im2col_scratch_, scratch_floats * sizeof(float));
-    hip_check(dav2_hip_im2col_quantize_i8(input.as<float>(), input_width, input_height, input_channels, input_width,
-                                          input_height, 1, 1, 0, packed.as<int8_t>(), ld, scales.as<float>(),
-                                          im2col_scratch_.as<float>(), scratch_floats, s),
-              "im2col quantize");
+    {  // the scope ends before the GEMM launch: it times the im2col kernels alone
+        ProfileScope prof_q(context_.profiler(), "im2col_quantize_i8",
+                            4.0 * input_rows * input_channels + 1.0 * input_rows * input_channels + 4.0 * input_rows,
+                            "B", s);
+        hip_check(dav2_hip_im2col_quantize_i8(input.as<float>(), input_width, input_height, input_channels,
+                                              input_width, input_height, 1, 1, 0, packed.as<int8_t>(), ld,
+                                              scales.as<float>(), im2col_scratch_.as<float>(), scratch_floats, s),
+                  "im2col quantize");
+    }
     workspace_ld_ = ld;
     dav2_gemm_i8_args a{};
     a.a = packed.as<int8_t>();

@@ -363,7 +363,7 @@ DAV2_API dav2_status DAV2_CALL dav2_infer_tensor_f32_device(
  * GPU preprocessing (float32 cubic resize to network_shape(width, height,
  * input_size)), the inference, min/max normalisation and the bilinear resize
  * back to width x height, on the device and without host copies. The returned
- * job works with dav2_gpu_job_poll (QUEUED until the GPU work has finished,
+ * job works with dav2_gpu_job_poll (RUNNING until the GPU work has finished,
  * then COMPLETE), dav2_gpu_job_cancel (CANCELLED: the GPU work still runs,
  * its output is not to be used) and dav2_gpu_job_release (waits for the GPU
  * work, closes IPC mappings, frees the job).

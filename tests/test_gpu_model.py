@@ -37,7 +37,8 @@ def rel_err(got, ref):
 
 @pytest.mark.parametrize("enc,width,height,flags", [
     ("vits", 518, 518, "fp32att"), ("vits", 518, 518, "int8"), ("vits", 350, 266, "int8"),
-    ("vitb", 518, 518, "int8"), ("vitl", 518, 518, "int8"), ("vitl", 294, 196, "fp32att")])
+    ("vitb", 518, 518, "int8"), ("vitl", 518, 518, "int8"), ("vitl", 294, 196, "fp32att"),
+    ("vitl", 518, 518, "fp32att")])
 def test_depth_parity(gpu, pkg, lib, oracle, models, enc, width, height, flags):
     torch = gpu
     print("case: model", enc, width, height, flags, flush=True)
@@ -87,6 +88,33 @@ def test_batched_device_entry_matches_single(gpu, pkg, lib, models):
                                                 out.numel() - 1, None) == 7
     for b in range(3):
         assert np.array_equal(got[b], singles[b])
+
+
+def test_vitl_518_batch8_matches_singles_and_oracle(gpu, pkg, lib, oracle, models):
+    # ViT-L + DPT at 518x518, batch 8 (the throughput configuration) through
+    # the batched device entry: each image equals its single-image result bit
+    # for bit, and image 0 equals the oracle's int8 graph bit for bit.
+    torch = gpu
+    width = height = 518
+    print("case: vitl 518x518 batch 8", flush=True)
+    xs = pkg.dav2_format.imagenet_input(width, height, seed=SEED + 13, batch=8)
+    xd = dev(torch, xs)
+    out = empty(torch, (8, height, width), torch.float32)
+    single = empty(torch, (height, width), torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    with pkg.Context(str(models["vitl"]), "vitl") as ctx:
+        ctx.infer_device(xd.data_ptr(), 8, width, height, out.data_ptr(), out.numel(), stream)
+        got = host(torch, out)
+        assert np.isfinite(got).all()
+        for b in range(8):
+            ctx.infer_device(xd[b].data_ptr(), 1, width, height, single.data_ptr(), single.numel(), stream)
+            assert np.array_equal(host(torch, single).view(np.uint32), got[b].view(np.uint32)), b
+    h = oracle.load_model(models["vitl"], ENC["vitl"])
+    try:
+        ref_depth, _, _ = oracle.infer(h, xs[0], width, height, fp16_attention=True)
+    finally:
+        oracle.free_model(h)
+    assert np.array_equal(got[0].view(np.uint32), ref_depth.view(np.uint32))
 
 
 def test_depth_parity_1036_tokens(gpu, pkg, lib, oracle, models):

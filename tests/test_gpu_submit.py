@@ -85,7 +85,7 @@ def _wait(pkg, lib, job, limit_s=60.0):
     t0 = time.time()
     while True:
         assert lib.dav2_gpu_job_poll(job, C.byref(st)) == 0
-        if st.state != pkg.GPU_JOB_QUEUED or time.time() - t0 > limit_s:
+        if st.state not in (pkg.GPU_JOB_QUEUED, pkg.GPU_JOB_RUNNING) or time.time() - t0 > limit_s:
             return st
         time.sleep(0.002)
 
@@ -116,6 +116,42 @@ def test_submit_hip_matches_oracle(gpu, pkg, lib, oracle, hip, vits_model, width
         hip.hipEventDestroy(ev)
         got = host(torch, out)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_submit_hip_in_flight_polls_running(gpu, pkg, lib, hip, vits_model):
+    """vulkan_executor.cpp:450-457: a job whose GPU work has not finished
+    polls as RUNNING. The job waits for an event recorded behind a bounded
+    spin kernel (torch.cuda._sleep) on torch's stream."""
+    torch = gpu
+    width, height = 64, 48
+    _announce("submit_hip running", width, height)
+    src = torch.zeros(width * height, dtype=torch.int32, device="cuda")
+    out = torch.zeros(width * height, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    with pkg.Context(str(vits_model), "vits") as ctx:
+        r = _request(pkg, width, height, width, 56, False, frame=9)
+        r.input, r.input_byte_size, r.output, r.output_byte_size = ptr(src), 4 * src.numel(), ptr(out), \
+            4 * out.numel()
+        job = C.c_void_p()
+        # a first submission sizes the context's workspaces
+        assert lib.dav2_submit_hip(ctx.handle, C.byref(r), C.byref(job)) == 0, lib.dav2_last_error()
+        assert _wait(pkg, lib, job).state == pkg.GPU_JOB_COMPLETE
+        lib.dav2_gpu_job_release(job)
+        ev = C.c_void_p()
+        assert hip.hipEventCreate(C.byref(ev)) == 0
+        torch.cuda._sleep(200_000_000)  # bounded spin: 0.1-2 s depending on the counter's clock
+        assert hip.hipEventRecord(ev, C.c_void_p(stream(torch))) == 0
+        r.wait_event = ev
+        assert lib.dav2_submit_hip(ctx.handle, C.byref(r), C.byref(job)) == 0, lib.dav2_last_error()
+        st = pkg.GpuJobStatus()
+        st.struct_size = C.sizeof(st)
+        assert lib.dav2_gpu_job_poll(job, C.byref(st)) == 0
+        assert st.state == pkg.GPU_JOB_RUNNING
+        done = _wait(pkg, lib, job)
+        assert done.state == pkg.GPU_JOB_COMPLETE
+        lib.dav2_gpu_job_release(job)
+        hip.hipEventDestroy(ev)
+        torch.cuda.synchronize()
 
 
 def test_submit_hip_cancel_and_checks(gpu, pkg, lib, vits_model):
