@@ -27,11 +27,14 @@ private:
     hipStream_t stream_;
 };
 
-Precision attention_precision_for(std::uint32_t flags) {
-    // src/encoder.cpp:389-396: int8 mode uses binary16 attention operands
-    // (the fused kernel) unless FORCE_FP32(_ATTENTION) asks for fp32 scores.
-    return (flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP32_ATTENTION)) != 0 ? Precision::fp32
-                                                                                       : Precision::fp16;
+AttentionMode attention_mode_for(std::uint32_t flags) {
+    // src/encoder.cpp:389-396: int8 mode runs the reference's binary16
+    // attention unless FORCE_FP32(_ATTENTION) asks for fp32 scores. Here the
+    // int8-mode default is the integer-exact fused attention; the reference's
+    // binary16 arithmetic is DAV2_CREATE_REFERENCE_FP16_ATTENTION.
+    if (flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP32_ATTENTION)) return AttentionMode::fp32;
+    if (flags & DAV2_CREATE_REFERENCE_FP16_ATTENTION) return AttentionMode::binary16;
+    return AttentionMode::exact;
 }
 }  // namespace
 
@@ -41,11 +44,11 @@ HipExecutor::HipExecutor(const std::string& model_path, dav2_encoder encoder, in
       model_(model_path, encoder),
       context_(device_index),
       precision_((flags & DAV2_CREATE_FORCE_FP32) != 0 ? Precision::fp32 : Precision::int8),
-      attention_precision_(attention_precision_for(flags)),
+      attention_mode_(attention_mode_for(flags)),
       weights_(model_, context_, precision_ == Precision::fp32),
       operators_(context_),
       side_operators_(context_),
-      dino_(encoder, weights_, operators_, attention_precision_, precision_),
+      dino_(encoder, weights_, operators_, attention_mode_, precision_),
       dpt_(encoder, weights_, operators_, precision_) {
     context_.make_current();
     hip_check(hipStreamCreateWithFlags(&side_stream_, hipStreamNonBlocking), "side stream");

@@ -75,7 +75,7 @@ public:
         upload = context_.upload_bytes();
         download = context_.download_bytes();
     }
-    Precision attention_precision() const { return attention_precision_; }
+    AttentionMode attention_mode() const { return attention_mode_; }
     Precision precision() const { return precision_; }
     HipContext& context() { return context_; }
     std::uint64_t arena_bytes() const { return arena_.bytes(); }
@@ -100,7 +100,7 @@ private:
     MappedModel model_;  // validated before any HIP call, as the reference's member order does
     HipContext context_;
     Precision precision_;  // int8, or fp32 under FORCE_FP32
-    Precision attention_precision_;
+    AttentionMode attention_mode_;
     GpuModel weights_;
     HipOperators operators_;
     // Second operator set with its own workspaces on side_stream_: the DPT

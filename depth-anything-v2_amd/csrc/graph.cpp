@@ -48,9 +48,9 @@ std::string block_name(std::uint32_t block, const char* suffix) {
 
 // ---------------------------------------------------------------------------
 DinoEncoder::DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators,
-                         Precision attention_precision, Precision precision)
+                         AttentionMode attention, Precision precision)
     : config_(encoder_config(encoder)), weights_(weights), ops_(operators),
-      attention_precision_(attention_precision), precision_(precision) {
+      attention_(attention), precision_(precision) {
     if (precision_ == Precision::fp16) throw std::invalid_argument("the fp16 encoder is not part of this build");
     if (weights_.tensor("pretrained.cls_token").elements != config_.embedding ||
         weights_.tensor("pretrained.pos_embed").elements != std::uint64_t(1370) * config_.embedding)
@@ -75,10 +75,11 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
     DeviceBuffer& attn = arena.get("enc.attention", tok_bytes);
     DeviceBuffer& hidden = arena.get("enc.hidden", tok_bytes * 4);
     const bool f32 = precision_ == Precision::fp32;
-    const bool fused = !f32 && attention_precision_ == Precision::fp16;
+    const bool fused = !f32 && attention_ == AttentionMode::exact;
+    const Precision materialised = attention_ == AttentionMode::binary16 ? Precision::fp16 : Precision::fp32;
     DeviceBuffer& scores =
         arena.get("enc.scores", fused ? HipOperators::attention_fused_scratch_bytes(T, H, batch)
-                                      : HipOperators::attention_score_bytes(T, H, batch, attention_precision_));
+                                      : HipOperators::attention_score_bytes(T, H, batch, materialised));
     for (int i = 0; i < 4; ++i) features[i] = &arena.get("enc.feature" + std::to_string(i), tok_bytes);
     // One image: the qkv GEMM also leaves the |k| and |v| column maxima per
     // row tile, so the attention's digit packing reads qkv once.
@@ -115,12 +116,13 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
         ops_.linear_int8_prequantized(qkv, wqkv.int8_buffer, wqkv.int8_scales, &F(".attn.qkv.bias"), rows, D, 3 * D,
                                       colmax ? HipOperators::Epilogue::row_colmax : HipOperators::Epilogue::row,
                                       nullptr, 0, col_absmax, D);
-        // attention (encoder.cpp:454-460): fused binary16-operand kernel in
-        // int8 mode, materialised fp32 scores under FORCE_FP32(_ATTENTION)
+        // attention (encoder.cpp:454-460): the integer-exact fused kernel, or
+        // the reference's materialised binary16 / fp32 pipeline in its own
+        // arithmetic order
         if (fused)
             ops_.attention_fused(attn, qkv, T, H, batch, scores, col_absmax, qkv_tiles);
         else
-            ops_.attention_batched(attn, qkv, T, H, batch, scores, attention_precision_);
+            ops_.attention_batched(attn, qkv, T, H, batch, scores, materialised);
         // proj + LayerScale residual (encoder.cpp:478-491), in place
         ops_.quantize_rows(attn, 0, rows, D);
         const GpuTensor& wproj = W(".attn.proj.weight");
@@ -163,7 +165,7 @@ void DinoEncoder::forward_fp32(std::uint32_t rows, std::uint32_t T, std::uint32_
         const auto W = [&](const char* s) -> const DeviceBuffer& { return weights_.tensor(block_name(blk, s)).buffer; };
         ops_.layer_norm(normed, current, W(".norm1.weight"), W(".norm1.bias"), rows, D, 1.0e-6f);
         ops_.linear_f32(qkv, normed, W(".attn.qkv.weight"), &W(".attn.qkv.bias"), rows, D, 3 * D, E::row);
-        ops_.attention_batched(attn, qkv, T, H, batch, scores, Precision::fp32);
+        ops_.attention_mfma_f32(attn, qkv, T, H, batch, scores);
         ops_.linear_f32(current, attn, W(".attn.proj.weight"), &W(".attn.proj.bias"), rows, D, D, E::row_layerscale,
                         &W(".ls1.gamma"));
         ops_.layer_norm(normed, current, W(".norm2.weight"), W(".norm2.bias"), rows, D, 1.0e-6f);

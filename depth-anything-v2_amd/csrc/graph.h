@@ -43,11 +43,16 @@ private:
     std::map<std::string, DeviceBuffer> buffers_;
 };
 
+// Attention of the int8 graph: the integer-exact fused kernel (default), the
+// reference's binary16 pipeline, or fp32 scores (FORCE_FP32_ATTENTION; also
+// the fp32 precision mode, which uses the matrix-core fp32 kernels).
+enum class AttentionMode { exact, binary16, fp32 };
+
 class DinoEncoder {
 public:
     // precision: int8 (the product path) or fp32 (the fp32 precision mode:
     // fp32 weights and GEMMs, no quantization).
-    DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, Precision attention_precision,
+    DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, AttentionMode attention,
                 Precision precision = Precision::int8);
     // image: device [batch][3][height][width]. On return features[i] holds the
     // final-norm token matrix [batch*tokens][D] of capture layer i.
@@ -66,7 +71,7 @@ private:
     EncoderConfig config_;
     GpuModel& weights_;
     HipOperators& ops_;
-    Precision attention_precision_;
+    AttentionMode attention_;
     Precision precision_;
 };
 

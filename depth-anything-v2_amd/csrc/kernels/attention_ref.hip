@@ -1,0 +1,453 @@
+// Head-64 attention in the reference's own arithmetic order, for gfx950.
+//
+// Reference: src/operators.cpp:1098-1209 (attention_head64) with
+//   fp32:     bmm.glsl:31-154 (scores and values), softmax_lastdim.glsl:19-69;
+//   binary16: bmm_score_fp16.glsl:13-70, softmax_lastdim_half.glsl:16-65,
+//             bmm_value_fp16.glsl:22-80 (the reference's int8-mode default,
+//             encoder.cpp:389-396, on devices without the cooperative-matrix
+//             score shader).
+// Every output element is the same sequence of IEEE operations the shaders
+// state: a score is a sum over the 64 features in order 0..63, an output
+// element a sum over the source tokens in order 0..T-1, each product
+// rounded to binary16 first in the binary16 pipeline; the softmax partitions
+// a row over 128 lanes (lane = column % 128, or packed word % 128) and adds
+// the lane partials by the halving tree. No multiply-add is contracted
+// (-ffp-contract=off), exp is exp_cw and the division is IEEE, the same
+// choices as the CPU oracle, so both produce the same bits. These sums are
+// sequential per output, so they run on the VALU (a matrix core's
+// accumulation order is its own).
+//
+// Layouts: qkv [batch*T][3*H*64] token-major (q | k | v, head h at h*64);
+// fp32 scores [batch][H][T][T] floats; binary16 scores [batch][H][T][words]
+// packed half2 words, words = ceil(T/2) (the reference's layout and size);
+// out [batch*T][H*64].
+
+#include "common.h"
+#include "dav2_hip.h"
+
+using namespace dav2k;
+
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+constexpr int kQueryTile = 128;  // score tile: 128 queries x 64 keys
+constexpr int kKeyTile = 64;
+constexpr int kValueRows = 64;   // value tile: 64 queries x 64 features
+constexpr int kSourceChunk = 32; // source tokens staged per step
+
+DAV2_DEV uint32_t pack_half2(float lo, float hi) {
+    const _Float16 a = static_cast<_Float16>(lo), b = static_cast<_Float16>(hi);
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+DAV2_DEV float half_lo(uint32_t w) { return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w))); }
+DAV2_DEV float half_hi(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
+// s + float(fp16(a * b)) for two pairs: one binary16 multiplication of
+// each pair (v_pk_mul_f16), each product widened and added in fp32.
+DAV2_DEV void add_half_products(float& s0, float& s1, h2 a, h2 b) {
+    const h2 p = a * b;
+    s0 = s0 + static_cast<float>(p.x);
+    s1 = s1 + static_cast<float>(p.y);
+}
+
+// ---------------------------------------------------------------------------
+// Scores. Thread (tx, ty) of 16 x 16 owns queries ty*8 .. +7 and keys
+// tx*4 .. +3 of the tile, 32 sums. LDS holds the tile's q*0.125 and k
+// feature-major so that a thread's 8 query and 4 key values of one feature
+// are two and one 16-byte reads. Binary16: the values are rounded to binary16
+// when staged (stored as floats: exact).
+template <bool HALF>
+__global__ __launch_bounds__(256) void ref_scores_kernel(const float* __restrict__ qkv, void* __restrict__ scores,
+                                                         uint32_t tokens, uint32_t heads) {
+    __shared__ __attribute__((aligned(16))) float qs[64][kQueryTile + 4];
+    __shared__ __attribute__((aligned(16))) float ks[64][kKeyTile + 4];
+    const uint32_t bh = blockIdx.z;
+    const uint32_t b = bh / heads, h = bh - b * heads;
+    const uint32_t D = heads * 64u;
+    const uint32_t i0 = blockIdx.y * kQueryTile, j0 = blockIdx.x * kKeyTile;
+    const float* base = qkv + static_cast<uint64_t>(b) * tokens * 3u * D + h * 64u;
+    const int tid = threadIdx.x;
+
+    // 128 query rows x 64 features: 2048 float4, 8 per thread; 64 key rows: 4.
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+        const int c = tid + it * 256;
+        const int r = c >> 4, f4 = (c & 15) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i0 + r < tokens) v = *reinterpret_cast<const float4*>(base + static_cast<uint64_t>(i0 + r) * 3u * D + f4);
+        // bmm.glsl:57-63 / bmm_score_fp16.glsl:32-33: q * 0.125 (exact), then binary16
+        float q[4] = {v.x * 0.125f, v.y * 0.125f, v.z * 0.125f, v.w * 0.125f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qs[f4 + e][r] = HALF ? static_cast<float>(static_cast<_Float16>(q[e])) : q[e];
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int c = tid + it * 256;
+        const int r = c >> 4, f4 = (c & 15) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j0 + r < tokens)
+            v = *reinterpret_cast<const float4*>(base + static_cast<uint64_t>(j0 + r) * 3u * D + D + f4);
+        float k[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ks[f4 + e][r] = HALF ? static_cast<float>(static_cast<_Float16>(k[e])) : k[e];
+    }
+    __syncthreads();
+
+    const int tx = tid & 15, ty = tid >> 4;
+    float s[8][4];
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[r][c] = 0.0f;
+#pragma unroll 4
+    for (int f = 0; f < 64; ++f) {
+        const float4 qa = *reinterpret_cast<const float4*>(&qs[f][ty * 8]);
+        const float4 qb = *reinterpret_cast<const float4*>(&qs[f][ty * 8 + 4]);
+        const float4 kv = *reinterpret_cast<const float4*>(&ks[f][tx * 4]);
+        const float q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const float k[4] = {kv.x, kv.y, kv.z, kv.w};
+        if (HALF) {
+            const h2 k01 = {static_cast<_Float16>(k[0]), static_cast<_Float16>(k[1])};
+            const h2 k23 = {static_cast<_Float16>(k[2]), static_cast<_Float16>(k[3])};
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const _Float16 qh = static_cast<_Float16>(q[r]);
+                const h2 qq = {qh, qh};
+                add_half_products(s[r][0], s[r][1], qq, k01);
+                add_half_products(s[r][2], s[r][3], qq, k23);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) s[r][c] = s[r][c] + q[r] * k[c];
+        }
+    }
+
+    const uint64_t plane = static_cast<uint64_t>(bh) * tokens;
+    const uint32_t j = j0 + tx * 4;
+    if (HALF) {
+        // packHalf2x16 of (column, column + 1); a column past the row is 0
+        const uint32_t words = (tokens + 1u) >> 1;
+        uint32_t* out = static_cast<uint32_t*>(scores);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const uint32_t i = i0 + ty * 8 + r;
+            if (i >= tokens) continue;
+#pragma unroll
+            for (int c = 0; c < 4; c += 2) {
+                if (j + c >= tokens) continue;
+                const float hi = j + c + 1 < tokens ? s[r][c + 1] : 0.0f;
+                out[(plane + i) * words + (j + c) / 2] = pack_half2(s[r][c], hi);
+            }
+        }
+    } else {
+        float* out = static_cast<float*>(scores);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const uint32_t i = i0 + ty * 8 + r;
+            if (i >= tokens) continue;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (j + c < tokens) out[(plane + i) * tokens + j + c] = s[r][c];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax, in place, one wave per row. The shader's 128 lanes become two
+// virtual lanes per thread (t and t + 64). Lane l visits items l, l + 128,
+// ... (columns, or packed words in binary16); a thread keeps up to CH items
+// per virtual lane in registers (CH = 0: the row is read again per pass).
+template <int CH, bool HALF>
+__global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t rows, uint32_t columns) {
+    const uint32_t t = threadIdx.x & 63u;
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 4u + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint32_t items = HALF ? (columns + 1u) >> 1 : columns;
+    float* fr = HALF ? nullptr : static_cast<float*>(data) + row * items;
+    uint32_t* wr = HALF ? static_cast<uint32_t*>(data) + row * items : nullptr;
+    constexpr int R = CH > 0 ? CH : 1;
+    float lo[2][R], hi[2][R];  // hi: the word's upper half (binary16)
+
+    auto load = [&](uint32_t item, float& a, float& b) {
+        if (HALF) {
+            const uint32_t w = wr[item];
+            a = half_lo(w);
+            b = half_hi(w);
+        } else {
+            a = fr[item];
+            b = 0.0f;
+        }
+    };
+    // item's value(s) into the running maximum (softmax_lastdim_half.glsl:27-33)
+    auto fold_max = [&](float m, uint32_t item, float a, float b) {
+        m = fmaxf(m, a);
+        if (HALF && item * 2u + 1u < columns) m = fmaxf(m, b);
+        return m;
+    };
+
+    float maximum = -3.402823466e+38f;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+        const uint32_t lane = t + 64u * v;
+        if (CH > 0) {
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                const uint32_t item = lane + 128u * k;
+                if (item < items) {
+                    load(item, lo[v][k], hi[v][k]);
+                    maximum = fold_max(maximum, item, lo[v][k], hi[v][k]);
+                }
+            }
+        } else {
+            for (uint32_t item = lane; item < items; item += 128u) {
+                float a, b;
+                load(item, a, b);
+                maximum = fold_max(maximum, item, a, b);
+            }
+        }
+    }
+    maximum = wave_max(maximum);  // order-free
+
+    // exponentials, stored as they are produced; per-lane fp32 partials
+    float partial[2] = {0.0f, 0.0f};
+    auto exponentials = [&](uint32_t item, float a, float b, float& ea, float& eb) {
+        ea = exp_cw(a - maximum);
+        if (HALF) {
+            eb = item * 2u + 1u < columns ? exp_cw(b - maximum) : 0.0f;
+            wr[item] = pack_half2(ea, eb);
+            return ea + eb;
+        }
+        fr[item] = ea;
+        return ea;
+    };
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+        const uint32_t lane = t + 64u * v;
+        float d = 0.0f;
+        if (CH > 0) {
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                const uint32_t item = lane + 128u * k;
+                if (item < items) {
+                    float ea, eb;
+                    d = d + exponentials(item, lo[v][k], hi[v][k], ea, eb);
+                    lo[v][k] = ea;
+                    hi[v][k] = eb;
+                }
+            }
+        } else {
+            for (uint32_t item = lane; item < items; item += 128u) {
+                float a, b, ea, eb;
+                load(item, a, b);
+                d = d + exponentials(item, a, b, ea, eb);
+            }
+        }
+        partial[v] = d;
+    }
+    // halving tree over the 128 partials: stride 64 inside the thread, then
+    // 32 .. 1 across lanes (lane t adds lane t + stride)
+    float sum = partial[0] + partial[1];
+#pragma unroll
+    for (int stride = 32; stride > 0; stride >>= 1) sum = sum + __shfl_down(sum, stride, kWave);
+    sum = __shfl(sum, 0, kWave);
+    const float inverse = div_rn(1.0f, fmaxf(sum, 1.0e-20f));
+
+    auto normalize = [&](uint32_t item, float ea, float eb) {
+        if (HALF) {
+            // p = fp16(float(fp16(e)) * inverse); the stored exponentials are fp16(e)
+            const float pa = static_cast<float>(static_cast<_Float16>(ea)) * inverse;
+            const float pb = static_cast<float>(static_cast<_Float16>(eb)) * inverse;
+            wr[item] = pack_half2(pa, pb);
+        } else {
+            fr[item] = ea * inverse;
+        }
+    };
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+        const uint32_t lane = t + 64u * v;
+        if (CH > 0) {
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                const uint32_t item = lane + 128u * k;
+                if (item < items) normalize(item, lo[v][k], hi[v][k]);
+            }
+        } else {
+            for (uint32_t item = lane; item < items; item += 128u) {
+                float a, b;
+                load(item, a, b);  // the stored exponentials
+                normalize(item, a, b);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Values. Thread (tx, ty) of 16 x 16 owns queries ty*4 .. +3 and features
+// tx*4 .. +3 of a 64 x 64 tile; the source tokens advance in chunks of 32,
+// probabilities staged source-major and values (binary16-rounded in that
+// pipeline) source-major in LDS.
+template <bool HALF>
+__global__ __launch_bounds__(256) void ref_values_kernel(float* __restrict__ out, const void* __restrict__ probs,
+                                                         const float* __restrict__ qkv, uint32_t tokens,
+                                                         uint32_t heads) {
+    __shared__ __attribute__((aligned(16))) float ps[kSourceChunk][kValueRows + 4];
+    __shared__ __attribute__((aligned(16))) float vs[kSourceChunk][64 + 4];
+    const uint32_t bh = blockIdx.z;
+    const uint32_t b = bh / heads, h = bh - b * heads;
+    const uint32_t D = heads * 64u;
+    const uint32_t i0 = blockIdx.x * kValueRows;
+    const float* vbase = qkv + static_cast<uint64_t>(b) * tokens * 3u * D + 2u * D + h * 64u;
+    const uint64_t plane = static_cast<uint64_t>(bh) * tokens;
+    const uint32_t words = (tokens + 1u) >> 1;
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+
+    float o[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[r][c] = 0.0f;
+
+    for (uint32_t jb = 0; jb < tokens; jb += kSourceChunk) {
+        // probabilities: 64 rows x 32 sources (8 per thread), transposed into LDS
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int c = tid + it * 256;
+            const int r = c >> 5, jj = c & 31;
+            const uint32_t i = i0 + r, j = jb + jj;
+            float p = 0.0f;
+            if (i < tokens && j < tokens) {
+                if (HALF) {
+                    const uint32_t w = static_cast<const uint32_t*>(probs)[(plane + i) * words + j / 2];
+                    p = (j & 1u) ? half_hi(w) : half_lo(w);
+                } else {
+                    p = static_cast<const float*>(probs)[(plane + i) * tokens + j];
+                }
+            }
+            ps[jj][r] = p;
+        }
+        // values: 32 sources x 64 features, 2 float4 per thread
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int c = tid + it * 256;
+            const int jj = c >> 4, f4 = (c & 15) * 4;
+            const uint32_t j = jb + jj;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (j < tokens) v = *reinterpret_cast<const float4*>(vbase + static_cast<uint64_t>(j) * 3u * D + f4);
+            if (HALF) {
+                v.x = static_cast<float>(static_cast<_Float16>(v.x));
+                v.y = static_cast<float>(static_cast<_Float16>(v.y));
+                v.z = static_cast<float>(static_cast<_Float16>(v.z));
+                v.w = static_cast<float>(static_cast<_Float16>(v.w));
+            }
+            *reinterpret_cast<float4*>(&vs[jj][f4]) = v;
+        }
+        __syncthreads();
+        const int count = static_cast<int>(min(static_cast<uint32_t>(kSourceChunk), tokens - jb));
+        for (int jj = 0; jj < count; ++jj) {
+            const float4 pv = *reinterpret_cast<const float4*>(&ps[jj][ty * 4]);
+            const float4 vv = *reinterpret_cast<const float4*>(&vs[jj][tx * 4]);
+            const float p[4] = {pv.x, pv.y, pv.z, pv.w};
+            const float v[4] = {vv.x, vv.y, vv.z, vv.w};
+            if (HALF) {
+                const h2 v01 = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
+                const h2 v23 = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const _Float16 ph = static_cast<_Float16>(p[r]);
+                    const h2 pp = {ph, ph};
+                    add_half_products(o[r][0], o[r][1], pp, v01);
+                    add_half_products(o[r][2], o[r][3], pp, v23);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) o[r][c] = o[r][c] + p[r] * v[c];
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t i = i0 + ty * 4 + r;
+        if (i >= tokens) continue;
+        *reinterpret_cast<float4*>(out + (static_cast<uint64_t>(b) * tokens + i) * D + h * 64u + tx * 4) =
+            make_float4(o[r][0], o[r][1], o[r][2], o[r][3]);
+    }
+}
+
+template <bool HALF>
+hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream_t s) {
+    const uint32_t items = HALF ? (columns + 1u) >> 1 : columns;
+    const uint32_t per_lane = (items + 127u) / 128u;
+    const dim3 grid(static_cast<uint32_t>((rows + 3u) / 4u)), block(256);
+#define DAV2_SOFTMAX_CASE(N)                                                              \
+    if (per_lane <= N) {                                                                  \
+        hipLaunchKernelGGL((ref_softmax_kernel<N, HALF>), grid, block, 0, s, data, rows, columns); \
+        return hipGetLastError();                                                         \
+    }
+    DAV2_SOFTMAX_CASE(4)
+    DAV2_SOFTMAX_CASE(8)
+    DAV2_SOFTMAX_CASE(12)
+    DAV2_SOFTMAX_CASE(24)
+    DAV2_SOFTMAX_CASE(48)
+#undef DAV2_SOFTMAX_CASE
+    hipLaunchKernelGGL((ref_softmax_kernel<0, HALF>), grid, block, 0, s, data, rows, columns);
+    return hipGetLastError();
+}
+
+bool valid(uint32_t tokens, uint32_t heads, uint32_t batch) {
+    return tokens > 0 && heads > 0 && batch > 0 && uint64_t(batch) * heads <= 65535u;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t dav2_hip_attention_ref_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch, int fp16) {
+    const uint64_t planes = static_cast<uint64_t>(batch) * heads * tokens;
+    return fp16 ? planes * ((tokens + 1u) / 2u) * 4u : planes * tokens * 4u;
+}
+
+int dav2_hip_attention_ref_scores(void* scores, const float* qkv, uint32_t tokens, uint32_t heads, uint32_t batch,
+                                  int fp16, void* stream) {
+    if (!scores || !qkv || !valid(tokens, heads, batch)) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(qkv) & 15) return hipErrorInvalidValue;
+    const dim3 grid(ceil_div(tokens, kKeyTile), ceil_div(tokens, kQueryTile), batch * heads);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (fp16)
+        hipLaunchKernelGGL(ref_scores_kernel<true>, grid, dim3(256), 0, s, qkv, scores, tokens, heads);
+    else
+        hipLaunchKernelGGL(ref_scores_kernel<false>, grid, dim3(256), 0, s, qkv, scores, tokens, heads);
+    return hipGetLastError();
+}
+
+int dav2_hip_attention_ref_softmax(void* scores, uint64_t rows, uint32_t columns, int fp16, void* stream) {
+    if (!scores || columns == 0) return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return fp16 ? launch_softmax<true>(scores, rows, columns, s) : launch_softmax<false>(scores, rows, columns, s);
+}
+
+int dav2_hip_attention_ref_values(float* out, const void* probabilities, const float* qkv, uint32_t tokens,
+                                  uint32_t heads, uint32_t batch, int fp16, void* stream) {
+    if (!out || !probabilities || !qkv || !valid(tokens, heads, batch)) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(out)) & 15) return hipErrorInvalidValue;
+    const dim3 grid(ceil_div(tokens, kValueRows), 1, batch * heads);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (fp16)
+        hipLaunchKernelGGL(ref_values_kernel<true>, grid, dim3(256), 0, s, out, probabilities, qkv, tokens, heads);
+    else
+        hipLaunchKernelGGL(ref_values_kernel<false>, grid, dim3(256), 0, s, out, probabilities, qkv, tokens, heads);
+    return hipGetLastError();
+}
+
+}  // extern "C"

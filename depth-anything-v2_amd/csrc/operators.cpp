@@ -217,7 +217,9 @@ void HipOperators::add_scaled(DeviceBuffer& output, const DeviceBuffer& residual
 
 std::uint64_t HipOperators::attention_score_bytes(std::uint32_t tokens, std::uint32_t heads, std::uint32_t batch,
                                                   Precision precision) {
-    return dav2_hip_attention_scratch_bytes(tokens, heads, batch, precision == Precision::fp16 ? 1 : 0);
+    // fp32: H*T*T floats; fp16: H*T*ceil(T/2) packed half2 words (the
+    // reference's sizes, operators.cpp:1112-1119)
+    return dav2_hip_attention_ref_scratch_bytes(tokens, heads, batch, precision == Precision::fp16 ? 1 : 0);
 }
 
 // src/operators.cpp:1098-1209
@@ -242,26 +244,55 @@ void HipOperators::attention_head64(DeviceBuffer& output, const DeviceBuffer& qk
 void HipOperators::attention_batched(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
                                      std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scores,
                                      Precision precision) {
+    if (tokens == 0 || heads == 0 || batch == 0) throw std::invalid_argument("invalid attention dimensions");
     const int fp16 = precision == Precision::fp16 ? 1 : 0;
+    if (scores.size() < attention_score_bytes(tokens, heads, batch, precision))
+        throw std::invalid_argument("attention score scratch device buffer is too small");
     const hipStream_t s = stream();
-    const std::uint32_t stride = fp16 ? ((tokens + 7u) & ~7u) : tokens;
     const double flops = 2.0 * batch * heads * double(tokens) * tokens * 64.0;
-    const double score_bytes = double(batch) * heads * tokens * tokens * (fp16 ? 2.0 : 4.0);
+    const double score_bytes = double(dav2_hip_attention_ref_scratch_bytes(tokens, heads, batch, fp16));
     Profiler& prof = context_.profiler();
     {
-        ProfileScope p(prof, "attention_scores", flops, "FLOP", s);
-        hip_check(dav2_hip_attention_scores(scores.data(), qkv.as<float>(), tokens, heads, batch, fp16, s),
+        ProfileScope p(prof, fp16 ? "attention_scores_ref_f16" : "attention_scores_ref_f32", flops, "FLOP", s);
+        hip_check(dav2_hip_attention_ref_scores(scores.data(), qkv.as<float>(), tokens, heads, batch, fp16, s),
                   "attention scores");
     }
     {
+        // bytes: the row read once and written once
         ProfileScope p(prof, fp16 ? "softmax_f16" : "softmax_f32", 2.0 * score_bytes, "B", s);
-        hip_check(dav2_hip_softmax_rows(scores.data(), std::uint64_t(batch) * heads * tokens, tokens, stride, fp16, s),
+        hip_check(dav2_hip_attention_ref_softmax(scores.data(), std::uint64_t(batch) * heads * tokens, tokens, fp16, s),
+                  "attention softmax");
+    }
+    {
+        ProfileScope p(prof, fp16 ? "attention_values_ref_f16" : "attention_values_ref_f32", flops, "FLOP", s);
+        hip_check(dav2_hip_attention_ref_values(output.as<float>(), scores.data(), qkv.as<float>(), tokens, heads,
+                                                batch, fp16, s),
+                  "attention values");
+    }
+}
+
+void HipOperators::attention_mfma_f32(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
+                                      std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scores) {
+    if (scores.size() < dav2_hip_attention_scratch_bytes(tokens, heads, batch, 0))
+        throw std::invalid_argument("attention score scratch device buffer is too small");
+    const hipStream_t s = stream();
+    const double flops = 2.0 * batch * heads * double(tokens) * tokens * 64.0;
+    const double score_bytes = double(batch) * heads * tokens * tokens * 4.0;
+    Profiler& prof = context_.profiler();
+    {
+        ProfileScope p(prof, "attention_scores", flops, "FLOP", s);
+        hip_check(dav2_hip_attention_scores(scores.data(), qkv.as<float>(), tokens, heads, batch, 0, s),
+                  "attention scores");
+    }
+    {
+        ProfileScope p(prof, "softmax_f32_mfma_path", 2.0 * score_bytes, "B", s);
+        hip_check(dav2_hip_softmax_rows(scores.data(), std::uint64_t(batch) * heads * tokens, tokens, tokens, 0, s),
                   "attention softmax");
     }
     {
         ProfileScope p(prof, "attention_values", flops, "FLOP", s);
         hip_check(dav2_hip_attention_values(output.as<float>(), scores.data(), qkv.as<float>(), tokens, heads, batch,
-                                            fp16, s),
+                                            0, s),
                   "attention values");
     }
 }

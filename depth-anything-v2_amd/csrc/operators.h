@@ -177,12 +177,18 @@ public:
                     const DeviceBuffer* bias, std::uint32_t rows, std::uint32_t input_columns,
                     std::uint32_t output_columns, Epilogue epilogue, const DeviceBuffer* gamma = nullptr,
                     std::uint64_t output_row_offset = 0);
-    // Batched attention over `batch` token matrices of `tokens` rows each.
+    // Batched attention over `batch` token matrices of `tokens` rows each, in
+    // the reference shaders' arithmetic order (fp32: bmm.glsl /
+    // softmax_lastdim.glsl; fp16: the binary16 shaders), VALU kernels.
     void attention_batched(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
                            std::uint32_t heads, std::uint32_t batch, DeviceBuffer& score_scratch,
                            Precision precision);
     static std::uint64_t attention_score_bytes(std::uint32_t tokens, std::uint32_t heads, std::uint32_t batch,
                                                Precision precision);
+    // fp32 attention on the matrix cores (fp32 precision mode): the same
+    // scratch as attention_batched(fp32), sums in the MFMA's own order.
+    void attention_mfma_f32(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
+                            std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scores);
     // Fused integer-exact attention (int8 digit planes, exact int32 MFMA
     // sums): the int8-mode default in place of the materialised binary16
     // scores.

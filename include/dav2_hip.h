@@ -260,6 +260,25 @@ DAV2_API int dav2_hip_attention_values(float* out, const void* probabilities,
                                        const float* qkv, uint32_t tokens, uint32_t heads,
                                        uint32_t batch, int fp16, void* stream);
 
+/* Attention in the reference shaders' own arithmetic order (VALU): fp16 = 0
+ * follows bmm.glsl + softmax_lastdim.glsl (fp32 scores [batch][H][T][T]),
+ * fp16 = 1 follows bmm_score_fp16.glsl + softmax_lastdim_half.glsl +
+ * bmm_value_fp16.glsl (binary16 scores packed as half2 words
+ * [batch][H][T][ceil(T/2)], every product rounded to binary16). Scores and
+ * values sum in feature / source-token order, the softmax over 128 lanes and
+ * the halving tree, exp is exp_cw, the division IEEE: the CPU oracle's
+ * orc_attention_head64 modes 0 and 1 give the same bits. Reference:
+ * src/operators.cpp:1098-1209. Scratch: dav2_hip_attention_ref_scratch_bytes()
+ * (the reference's score buffer size). The softmax works in place on rows of
+ * `columns` scores. */
+DAV2_API uint64_t dav2_hip_attention_ref_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch, int fp16);
+DAV2_API int dav2_hip_attention_ref_scores(void* scores, const float* qkv, uint32_t tokens, uint32_t heads,
+                                           uint32_t batch, int fp16, void* stream);
+DAV2_API int dav2_hip_attention_ref_softmax(void* scores, uint64_t rows, uint32_t columns, int fp16, void* stream);
+DAV2_API int dav2_hip_attention_ref_values(float* out, const void* probabilities, const float* qkv,
+                                           uint32_t tokens, uint32_t heads, uint32_t batch, int fp16,
+                                           void* stream);
+
 /* Fused attention (int8-mode default): replaces the materialised binary16
  * path of src/operators.cpp:1132-1167 (bmm_score_fp16.glsl,
  * softmax_lastdim_half.glsl, bmm_value_fp16.glsl) with an integer-exact

@@ -55,8 +55,10 @@ DAV2_API dav2_status DAV2_CALL dav2_ops_add_scaled(dav2_ops* ops, dav2_device_bu
                                                    dav2_device_buffer residual, dav2_device_buffer addend,
                                                    dav2_device_buffer scale, uint32_t count, uint32_t columns);
 /* src/operators.h:119-126. score_scratch.data may be NULL (allocated internally).
- * fp32 scratch: H*T*T floats; fp16 scratch: dav2_hip_attention_scratch_bytes(T, H, 1, 1)
- * bytes (binary16 scores H*T*ldt, ldt = T rounded up to 8, then a packed copy of v). */
+ * Scratch sizes are the reference's (src/operators.cpp:1112-1119): fp32 H*T*T
+ * floats, fp16 H*T*ceil(T/2) packed half2 words. Both precisions compute in
+ * the reference shaders' arithmetic order (bmm.glsl / softmax_lastdim.glsl,
+ * and the binary16 shaders with every product rounded to binary16). */
 DAV2_API dav2_status DAV2_CALL dav2_ops_attention_head64(dav2_ops* ops, dav2_device_buffer output,
                                                          dav2_device_buffer qkv, uint32_t tokens, uint32_t heads,
                                                          dav2_device_buffer score_scratch, int32_t precision);

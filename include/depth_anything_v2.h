@@ -338,6 +338,18 @@ DAV2_API dav2_status DAV2_CALL dav2_infer_tensor_f32(
  * ------------------------------------------------------------------------ */
 
 /*
+ * Create flag (int8 mode): run the attention with the reference's binary16
+ * arithmetic -- bmm_score_fp16.glsl, softmax_lastdim_half.glsl and
+ * bmm_value_fp16.glsl, every product rounded to binary16 and every sum in
+ * the shaders' order (the reference's int8-mode default on devices without
+ * its cooperative-matrix score shader, src/encoder.cpp:389-396) -- instead of
+ * this build's default integer-exact fused attention. Slower; for callers
+ * that need the reference's int8-mode depth maps bit for bit. Not combinable
+ * with FORCE_FP32 / FORCE_FP32_ATTENTION.
+ */
+enum { DAV2_CREATE_REFERENCE_FP16_ATTENTION = 1u << 16u };
+
+/*
  * Device-resident, batched variant of dav2_infer_tensor_f32 for callers whose
  * images already live in HBM (serving loops, benchmarks). device_input holds
  * batch images, each 3*H*W float32 CHW, back to back; device_output receives

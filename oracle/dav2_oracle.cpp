@@ -431,7 +431,7 @@ static void softmax_row_fp32(const float* x, uint32_t columns, float* y) {
     for (uint32_t lane = 0; lane < 128; ++lane) {
         float d = 0.0f;
         for (uint32_t c = lane; c < columns; c += 128) {
-            const float e = std::exp(x[c] - maximum);
+            const float e = exp_cw(x[c] - maximum);
             y[c] = e;
             d = d + e;
         }
@@ -591,6 +591,139 @@ void orc_numerator21(const float* x, uint64_t count, float* out) {
     for (uint64_t i = 0; i < count; ++i) out[i] = numerator21(x[i]);
 }
 
+// Binary16 attention, the reference's int8-mode default (encoder.cpp:389-396
+// -> operators.cpp:1132-1167 without the cooperative-matrix shader), as the
+// three shaders state it:
+//  * bmm_score_fp16.glsl:24-70: operands q16 = fp16(q * 0.125) and
+//    k16 = fp16(k); each product q16 * k16 is a binary16 multiplication
+//    (rounded to binary16), converted to float and added to an fp32 sum in
+//    feature order 0..63; the sum is stored as binary16 (packHalf2x16).
+//  * softmax_lastdim_half.glsl:19-65: the row maximum; per word w = (2w, 2w+1)
+//    e = exp(score - max) in fp32, stored as binary16, while lane w % 128
+//    adds (e.x + e.y) of its words in order to an fp32 partial; the 128
+//    partials are added by the halving tree (stride 64, 32, ..., 1);
+//    p = fp16(float(fp16(e)) * (1 / max(sum, 1e-20))).
+//  * bmm_value_fp16.glsl:23-79: v16 = fp16(v); out = sum over source tokens
+//    0..T-1 in order of float(fp16(p16 * v16)) in fp32.
+// Pinned build choices where GLSL leaves latitude: binary16 rounding is to
+// nearest even with subnormals, no multiply-add contraction, exp is exp_cw,
+// the division is IEEE.
+namespace {
+
+// fp16(a * b) for binary16 values a, b held in floats: the fp32 product is
+// exact (11 x 11 significant bits), so one rounding to binary16 is the
+// binary16 multiplication. Eight lanes: F16C round-to-nearest-even.
+inline __m256 mul_round_half8(__m256 a, __m256 b) {
+    return _mm256_cvtph_ps(_mm256_cvtps_ph(_mm256_mul_ps(a, b), _MM_FROUND_TO_NEAREST_INT));
+}
+
+// Keys of head h feature-major [64][T8] (T8 = T rounded up to 8, zero
+// padding), rounded to binary16.
+std::vector<float> binary16_keys(const float* qkv, size_t T, size_t D, size_t h) {
+    const size_t T8 = (T + 7) & ~size_t(7);
+    std::vector<float> kt(64 * T8, 0.0f);
+    for (size_t j = 0; j < T; ++j)
+        for (int f = 0; f < 64; ++f) kt[f * T8 + j] = round_half(qkv[j * D * 3 + D + h * 64 + f]);
+    return kt;
+}
+
+// One row of bmm_score_fp16.glsl: for every key j, features 0..63 in order,
+// s = s + float(fp16(q16[f] * k16[j][f])); stored as binary16. Eight keys per
+// vector.
+void binary16_score_row(const float* q16, const std::vector<float>& kt, size_t T, uint16_t* hrow) {
+    const size_t T8 = (T + 7) & ~size_t(7);
+    for (size_t j = 0; j < T; j += 8) {
+        __m256 s = _mm256_setzero_ps();
+        for (int f = 0; f < 64; ++f)
+            s = _mm256_add_ps(s, mul_round_half8(_mm256_set1_ps(q16[f]), _mm256_loadu_ps(&kt[f * T8 + j])));
+        alignas(32) float lanes[8];
+        _mm256_store_ps(lanes, s);
+        for (size_t l = 0; l < 8 && j + l < T; ++l) hrow[j + l] = f2h(lanes[l]);
+    }
+}
+
+void attention_binary16(const float* qkv, uint32_t tokens, uint32_t heads, float* out, float* probabilities) {
+    const size_t D = static_cast<size_t>(heads) * 64;
+    const size_t T = tokens;
+    // Per head: keys feature-major and values token-major [T][64], rounded to
+    // binary16 once.
+    std::vector<std::vector<float>> keys_t(heads), values(heads);
+#pragma omp parallel for schedule(static)
+    for (int64_t h = 0; h < heads; ++h) {
+        keys_t[h] = binary16_keys(qkv, T, D, h);
+        values[h].resize(T * 64);
+        for (size_t j = 0; j < T; ++j)
+            for (int f = 0; f < 64; ++f) values[h][j * 64 + f] = round_half(qkv[j * D * 3 + 2 * D + h * 64 + f]);
+    }
+#pragma omp parallel
+    {
+        std::vector<uint16_t> hrow(T + 1);
+        std::vector<float> p(T);
+#pragma omp for schedule(dynamic, 4) collapse(2)
+        for (int64_t h = 0; h < heads; ++h) {
+            for (int64_t i = 0; i < static_cast<int64_t>(T); ++i) {
+                const float* q = qkv + static_cast<size_t>(i) * D * 3 + h * 64;
+                float q16[64];
+                for (int f = 0; f < 64; ++f) q16[f] = round_half(q[f] * 0.125f);
+                binary16_score_row(q16, keys_t[h], T, hrow.data());
+                // softmax over the packed row
+                float maximum = -3.402823466e+38f;
+                for (size_t j = 0; j < T; ++j) maximum = std::max(maximum, h2f(hrow[j]));
+                const size_t words = (T + 1) / 2;
+                float partial[128];
+                for (uint32_t lane = 0; lane < 128; ++lane) {
+                    float d = 0.0f;
+                    for (size_t w = lane; w < words; w += 128) {
+                        const size_t j0 = 2 * w, j1 = 2 * w + 1;
+                        const float ex = exp_cw(h2f(hrow[j0]) - maximum);
+                        const float ey = j1 < T ? exp_cw(h2f(hrow[j1]) - maximum) : 0.0f;
+                        hrow[j0] = f2h(ex);
+                        if (j1 < T) hrow[j1] = f2h(ey);
+                        d = d + (ex + ey);
+                    }
+                    partial[lane] = d;
+                }
+                for (uint32_t stride = 64; stride > 0; stride >>= 1)
+                    for (uint32_t lane = 0; lane < stride; ++lane) partial[lane] = partial[lane] + partial[lane + stride];
+                const float inverse = 1.0f / std::max(partial[0], 1.0e-20f);
+                for (size_t j = 0; j < T; ++j) p[j] = round_half(h2f(hrow[j]) * inverse);
+                // values: eight features per vector, source tokens in order
+                const std::vector<float>& vr = values[h];
+                float* o = out + static_cast<size_t>(i) * D + h * 64;
+                for (int f0 = 0; f0 < 64; f0 += 8) {
+                    __m256 s = _mm256_setzero_ps();
+                    for (size_t j = 0; j < T; ++j)
+                        s = _mm256_add_ps(s, mul_round_half8(_mm256_set1_ps(p[j]), _mm256_loadu_ps(&vr[j * 64 + f0])));
+                    _mm256_storeu_ps(o + f0, s);
+                }
+                if (probabilities) std::memcpy(probabilities + (h * T + i) * T, p.data(), T * sizeof(float));
+            }
+        }
+    }
+}
+
+}  // namespace
+
+void orc_attention_scores_binary16(const float* qkv, uint32_t tokens, uint32_t heads, uint16_t* scores) {
+    const size_t D = static_cast<size_t>(heads) * 64, T = tokens;
+    for (size_t h = 0; h < heads; ++h) {
+        const std::vector<float> kt = binary16_keys(qkv, T, D, h);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < static_cast<int64_t>(T); ++i) {
+            float q16[64];
+            for (int f = 0; f < 64; ++f) q16[f] = round_half(qkv[i * D * 3 + h * 64 + f] * 0.125f);
+            binary16_score_row(q16, kt, T, scores + (h * T + i) * T);
+        }
+    }
+}
+
+void orc_round_half_product(const float* a, const float* b, uint64_t count, float* out) {
+    uint64_t i = 0;
+    for (; i + 8 <= count; i += 8)
+        _mm256_storeu_ps(out + i, mul_round_half8(_mm256_loadu_ps(a + i), _mm256_loadu_ps(b + i)));
+    for (; i < count; ++i) out[i] = round_half(a[i] * b[i]);
+}
+
 void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int mode,
                           float* out, float* probabilities) {
     if (mode == 2) {
@@ -599,112 +732,35 @@ void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int
     }
     const size_t D = static_cast<size_t>(heads) * 64;
     const size_t T = tokens;
-    const int fp16 = mode != 0;
-    // fp16 path: binary16-rounded keys (feature-major, 64 x T) and values
-    // (T x 64) per head, converted once.
-    std::vector<std::vector<float>> half_keys_t(fp16 ? heads : 0), half_values(fp16 ? heads : 0);
-    if (fp16) {
-#pragma omp parallel for schedule(static)
-        for (int64_t h = 0; h < heads; ++h) {
-            half_keys_t[h].resize(64 * T);
-            half_values[h].resize(T * 64);
-            for (size_t j = 0; j < T; ++j)
-                for (int f = 0; f < 64; ++f) {
-                    half_keys_t[h][f * T + j] = round_half(qkv[j * D * 3 + D + h * 64 + f]);
-                    half_values[h][j * 64 + f] = round_half(qkv[j * D * 3 + 2 * D + h * 64 + f]);
-                }
-        }
+    if (mode == 1) {
+        attention_binary16(qkv, tokens, heads, out, probabilities);
+        return;
     }
 #pragma omp parallel
     {
         std::vector<float> row(T), p(T);
-        std::vector<uint16_t> hrow(T);
 #pragma omp for schedule(dynamic, 4) collapse(2)
         for (int64_t h = 0; h < heads; ++h) {
             for (int64_t i = 0; i < static_cast<int64_t>(T); ++i) {
                 const float* q = qkv + static_cast<size_t>(i) * D * 3 + h * 64;
-                if (!fp16) {
-                    // bmm.glsl with input_qkv_query=1, weight_qkv_kind=1: sequential
-                    // accumulation over the 64 features of (q*0.125)*k.
-                    for (size_t j = 0; j < T; ++j) {
-                        const float* k = qkv + j * D * 3 + D + h * 64;
-                        float s = 0.0f;
-                        for (int f = 0; f < 64; ++f) {
-                            const float sq = q[f] * 0.125f;
-                            s = s + sq * k[f];
-                        }
-                        row[j] = s;
-                    }
-                    softmax_row_fp32(row.data(), tokens, p.data());
-                    // bmm.glsl value pass: sequential over source tokens j.
-                    float* o = out + static_cast<size_t>(i) * D + h * 64;
+                // bmm.glsl with input_qkv_query=1, weight_qkv_kind=1: sequential
+                // accumulation over the 64 features of (q*0.125)*k.
+                for (size_t j = 0; j < T; ++j) {
+                    const float* k = qkv + j * D * 3 + D + h * 64;
+                    float s = 0.0f;
                     for (int f = 0; f < 64; ++f) {
-                        float s = 0.0f;
-                        for (size_t j = 0; j < T; ++j) s = s + p[j] * qkv[j * D * 3 + 2 * D + h * 64 + f];
-                        o[f] = s;
+                        const float sq = q[f] * 0.125f;
+                        s = s + sq * k[f];
                     }
-                } else {
-                    // bmm_score_fp16.glsl:29-70 operands: fp16(q*0.125), fp16(k),
-                    // score stored as fp16. Products of two binary16 values are
-                    // exact in fp32 and are accumulated in fp32 without the
-                    // shader's per-product fp16 rounding (the matrix-core
-                    // semantics of the HIP path). Eight keys per AVX lane set.
-                    const std::vector<float>& kt = half_keys_t[h];
-                    float qr[64];
-                    for (int f = 0; f < 64; ++f) qr[f] = round_half(q[f] * 0.125f);
-                    size_t j = 0;
-                    for (; j + 8 <= T; j += 8) {
-                        __m256 s = _mm256_setzero_ps();
-                        for (int f = 0; f < 64; ++f) {
-                            const __m256 prod = _mm256_mul_ps(_mm256_set1_ps(qr[f]), _mm256_loadu_ps(&kt[f * T + j]));
-                            s = _mm256_add_ps(s, prod);
-                        }
-                        alignas(32) float tmp[8];
-                        _mm256_store_ps(tmp, s);
-                        for (int l = 0; l < 8; ++l) hrow[j + l] = f2h(tmp[l]);
-                    }
-                    for (; j < T; ++j) {
-                        float s = 0.0f;
-                        for (int f = 0; f < 64; ++f) s = s + qr[f] * kt[f * T + j];
-                        hrow[j] = f2h(s);
-                    }
-                    // softmax_lastdim_half.glsl: word w = (2w, 2w+1) handled by
-                    // lane w % 128; exp stored as fp16, fp32 denominator.
-                    float maximum = -3.402823466e+38f;
-                    for (size_t j = 0; j < T; ++j) maximum = std::max(maximum, h2f(hrow[j]));
-                    const size_t words = (T + 1) / 2;
-                    float partial[128];
-                    for (uint32_t lane = 0; lane < 128; ++lane) {
-                        float d = 0.0f;
-                        for (size_t w = lane; w < words; w += 128) {
-                            const size_t j0 = 2 * w, j1 = 2 * w + 1;
-                            const float ex = std::exp(h2f(hrow[j0]) - maximum);
-                            float ey = 0.0f;
-                            if (j1 < T) ey = std::exp(h2f(hrow[j1]) - maximum);
-                            hrow[j0] = f2h(ex);
-                            if (j1 < T) hrow[j1] = f2h(ey);
-                            d = d + (ex + ey);
-                        }
-                        partial[lane] = d;
-                    }
-                    for (uint32_t stride = 64; stride > 0; stride >>= 1)
-                        for (uint32_t lane = 0; lane < stride; ++lane)
-                            partial[lane] = partial[lane] + partial[lane + stride];
-                    const float inverse = 1.0f / std::max(partial[0], 1.0e-20f);
-                    for (size_t j = 0; j < T; ++j) p[j] = round_half(h2f(hrow[j]) * inverse);
-                    // bmm_value_fp16.glsl operands fp16(p), fp16(v); exact
-                    // products, fp32 accumulation over the source tokens;
-                    // 8 features per lane set.
-                    const std::vector<float>& vr = half_values[h];
-                    float* o = out + static_cast<size_t>(i) * D + h * 64;
-                    for (int f0 = 0; f0 < 64; f0 += 8) {
-                        __m256 s = _mm256_setzero_ps();
-                        for (size_t jj = 0; jj < T; ++jj) {
-                            const __m256 prod = _mm256_mul_ps(_mm256_set1_ps(p[jj]), _mm256_loadu_ps(&vr[jj * 64 + f0]));
-                            s = _mm256_add_ps(s, prod);
-                        }
-                        _mm256_storeu_ps(o + f0, s);
-                    }
+                    row[j] = s;
+                }
+                softmax_row_fp32(row.data(), tokens, p.data());
+                // bmm.glsl value pass: sequential over source tokens j.
+                float* o = out + static_cast<size_t>(i) * D + h * 64;
+                for (int f = 0; f < 64; ++f) {
+                    float s = 0.0f;
+                    for (size_t j = 0; j < T; ++j) s = s + p[j] * qkv[j * D * 3 + 2 * D + h * 64 + f];
+                    o[f] = s;
                 }
                 if (probabilities) std::memcpy(probabilities + (h * T + i) * T, p.data(), T * sizeof(float));
             }
@@ -1255,7 +1311,7 @@ struct Map {
 
 std::string blk(uint32_t b, const char* s) { return "pretrained.blocks." + std::to_string(b) + s; }
 
-void encoder_block(const orc_model& m, std::vector<float>& cur, uint32_t T, uint32_t b, int fp16) {
+void encoder_block(const orc_model& m, std::vector<float>& cur, uint32_t T, uint32_t b, int attention_mode) {
     const uint32_t D = m.dim;
     const size_t n = static_cast<size_t>(T) * D;
     std::vector<float> norm(n), qkv(n * 3), attn(n), tmp(n), next(n), hidden(n * 4);
@@ -1271,8 +1327,9 @@ void encoder_block(const orc_model& m, std::vector<float>& cur, uint32_t T, uint
     orc_layer_norm(cur.data(), m.t(blk(b, ".norm1.weight")).data.data(), m.t(blk(b, ".norm1.bias")).data.data(),
                    T, D, 1.0e-6f, norm.data());
     lin(norm, blk(b, ".attn.qkv.weight"), blk(b, ".attn.qkv.bias"), D, 3 * D, false, qkv);
-    // int8 default: fused attention (binary16 operands, fp32 scores)
-    orc_attention_head64(qkv.data(), T, m.heads, fp16 ? 2 : 0, attn.data(), nullptr);
+    // attention_mode as orc_attention_head64: 0 fp32 scores, 1 the reference's
+    // binary16 pipeline, 2 integer-exact (this build's int8-mode default)
+    orc_attention_head64(qkv.data(), T, m.heads, attention_mode, attn.data(), nullptr);
     lin(attn, blk(b, ".attn.proj.weight"), blk(b, ".attn.proj.bias"), D, D, false, tmp);
     orc_add_scaled(cur.data(), tmp.data(), m.t(blk(b, ".ls1.gamma")).data.data(), n, D, next.data());
     cur.swap(next);
@@ -1332,10 +1389,10 @@ Map fusion(const orc_model& m, Map path, const Map* skip, const std::string& pre
 }  // namespace
 
 int orc_model_encoder_blocks(orc_model* model, float* tokens, uint32_t T, uint32_t first,
-                             uint32_t last, int fp16) {
+                             uint32_t last, int attention_mode) {
     try {
         std::vector<float> cur(tokens, tokens + static_cast<size_t>(T) * model->dim);
-        for (uint32_t b = first; b < last && b < model->blocks; ++b) encoder_block(*model, cur, T, b, fp16);
+        for (uint32_t b = first; b < last && b < model->blocks; ++b) encoder_block(*model, cur, T, b, attention_mode);
         std::memcpy(tokens, cur.data(), cur.size() * sizeof(float));
         return 0;
     } catch (const std::exception& e) {
@@ -1354,7 +1411,7 @@ int orc_model_infer_fp32(orc_model* model, const float* chw, uint32_t width, uin
 }
 
 int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t height,
-                    int fp16, float* depth, float* pre_relu, float* features) {
+                    int attention_mode, float* depth, float* pre_relu, float* features) {
     try {
         const orc_model& m = *model;
         const uint32_t D = m.dim, pw = width / 14, ph = height / 14, T = pw * ph + 1;
@@ -1373,7 +1430,7 @@ int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t
         std::vector<std::vector<float>> feats;
         uint32_t ci = 0;
         for (uint32_t b = 0; b < m.blocks; ++b) {
-            encoder_block(m, cur, T, b, fp16);
+            encoder_block(m, cur, T, b, attention_mode);
             if (ci < 4 && b == m.capture[ci]) {
                 std::vector<float> f(n);
                 orc_layer_norm(cur.data(), m.t("pretrained.norm.weight").data.data(),

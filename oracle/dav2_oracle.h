@@ -75,15 +75,21 @@ void orc_relu(const float* input, uint64_t count, float* out);
 void orc_softmax_rows(const float* input, uint64_t rows, uint32_t columns,
                       float* out);
 /* mode 0: fp32 bmm/softmax (bmm.glsl, softmax_lastdim.glsl).
- * mode 1: materialised binary16 scores and probabilities
- *         (bmm_score_fp16.glsl, softmax_lastdim_half.glsl, bmm_value_fp16.glsl)
- *         with exact products accumulated in fp32.
+ * mode 1: materialised binary16 scores and probabilities, the arithmetic of
+ *         bmm_score_fp16.glsl, softmax_lastdim_half.glsl, bmm_value_fp16.glsl:
+ *         every product rounded to binary16, fp32 sums in the shaders' order.
  * mode 2: integer-exact (the int8-mode kernel): 15-bit block floating point
  *         q*0.125 (per token), k (per head) and v (per feature), exact
  *         integer dot products, 21-bit softmax numerators.
  * probabilities (optional) receives [H][T][T]. */
 void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads,
                           int mode, float* out, float* probabilities);
+/* The binary16 scores of mode 1 before the softmax (bmm_score_fp16.glsl):
+ * scores [H][T][T] binary16 bit patterns. */
+void orc_attention_scores_binary16(const float* qkv, uint32_t tokens, uint32_t heads, uint16_t* scores);
+/* out[i] = fp16(a[i] * b[i]) for binary16 values a, b (the vector path the
+ * mode-1 attention uses; the tail uses the scalar conversion). */
+void orc_round_half_product(const float* a, const float* b, uint64_t count, float* out);
 /* The 21-bit softmax numerator of mode 2 for each x (as a float integer). */
 void orc_numerator21(const float* x, uint64_t count, float* out);
 void orc_bilinear_align_true(const float* input, uint32_t input_width,
@@ -123,12 +129,15 @@ typedef struct orc_model orc_model;
 orc_model* orc_model_load(const char* path, int encoder, char* error,
                           size_t error_bytes);
 void orc_model_free(orc_model* model);
-/* fp16_attention != 0 runs attention in mode 2 (the int8 default), else mode 0.
+/* attention_mode selects orc_attention_head64's mode for every block: 2 (the
+ * integer-exact attention, this build's int8-mode default), 1 (the
+ * reference's binary16 pipeline, DAV2_CREATE_REFERENCE_FP16_ATTENTION) or 0
+ * (fp32 scores, FORCE_FP32_ATTENTION).
  * depth: W*H raw ReLU depth. pre_relu (nullable): W*H before the final ReLU.
  * features (nullable): 4*T*D captured encoder features.
  * Returns 0 on success. */
 int orc_model_infer(orc_model* model, const float* chw, uint32_t width,
-                    uint32_t height, int fp16_attention, float* depth,
+                    uint32_t height, int attention_mode, float* depth,
                     float* pre_relu, float* features);
 /* The same graph in the fp32 precision mode (DAV2_CREATE_FORCE_FP32): fp32
  * weights and activations, fp32 attention. */
@@ -157,7 +166,7 @@ void orc_prepare_tokens_f32(const float* image, const float* weight,
                             uint32_t height, uint32_t D, float* tokens);
 /* Encoder blocks [first, last) only, on tokens [T][D] in place (timing sample). */
 int orc_model_encoder_blocks(orc_model* model, float* tokens, uint32_t tokens_count,
-                             uint32_t first, uint32_t last, int fp16_attention);
+                             uint32_t first, uint32_t last, int attention_mode);
 
 /* Host image paths (src/image.cpp, src/dav2.cpp:630-665, :754-802).
  * network_shape: image.cpp:138-161; returns 0, or 1 for a non-positive size.

@@ -25,6 +25,8 @@ _PROTO = {
     "orc_gelu": (None, [vp, u64, vp]),
     "orc_numerator21": (None, [vp, u64, vp]),
     "orc_exp": (None, [vp, u64, vp]),
+    "orc_round_half_product": (None, [vp, vp, u64, vp]),
+    "orc_attention_scores_binary16": (None, [vp, u32, u32, vp]),
     "orc_layer_norm": (None, [vp, vp, vp, u32, u32, f32, vp]),
     "orc_add_scaled": (None, [vp, vp, vp, u64, u32, vp]),
     "orc_add": (None, [vp, vp, u64, vp]),
@@ -196,6 +198,19 @@ class Oracle:
         x = _f32(x)
         out = np.empty_like(x)
         self.lib.orc_softmax_rows(x.ctypes.data, x.shape[0], x.shape[1], out.ctypes.data)
+        return out
+
+    def round_half_product(self, a, b):
+        a, b = _f32(a), _f32(b)
+        out = np.empty_like(a)
+        self.lib.orc_round_half_product(a.ctypes.data, b.ctypes.data, a.size, out.ctypes.data)
+        return out
+
+    def scores_binary16(self, qkv, tokens: int, heads: int):
+        """Binary16 scores [H][T][T] as float16 (bmm_score_fp16.glsl)."""
+        qkv = _f32(qkv)
+        out = np.empty((heads, tokens, tokens), np.float16)
+        self.lib.orc_attention_scores_binary16(qkv.ctypes.data, tokens, heads, out.ctypes.data)
         return out
 
     def attention(self, qkv, tokens: int, heads: int, fp16: bool = False, probabilities: bool = False,
@@ -377,7 +392,14 @@ class Oracle:
                                         pos.ctypes.data, width, height, d, out.ctypes.data)
         return out
 
-    def infer(self, h, chw, width: int, height: int, fp16_attention: bool = True, dim: int | None = None):
+    ATTENTION_MODES = {"fp32": 0, "binary16": 1, "exact": 2}
+
+    def infer(self, h, chw, width: int, height: int, fp16_attention: bool = True, dim: int | None = None,
+              attention: str | None = None):
+        """The int8 graph. attention: "exact" (the int8-mode default, also
+        fp16_attention=True), "binary16" (the reference's binary16 pipeline)
+        or "fp32" (FORCE_FP32_ATTENTION, also fp16_attention=False)."""
+        mode = self.ATTENTION_MODES[attention or ("exact" if fp16_attention else "fp32")]
         chw = _f32(chw)
         depth = np.empty((height, width), np.float32)
         logits = np.empty((height, width), np.float32)
@@ -385,7 +407,7 @@ class Oracle:
         if dim is not None:
             t = (width // 14) * (height // 14) + 1
             feats = np.empty((4, t, dim), np.float32)
-        rc = self.lib.orc_model_infer(h, chw.ctypes.data, width, height, int(fp16_attention), depth.ctypes.data,
+        rc = self.lib.orc_model_infer(h, chw.ctypes.data, width, height, mode, depth.ctypes.data,
                                       logits.ctypes.data, _p(feats))
         if rc != 0:
             raise RuntimeError("oracle inference failed")

@@ -582,32 +582,117 @@ def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
 
 # ---------------------------------------------------------------------------
 # attention: scores -> softmax -> values
-def _attention_gpu(torch, lib, qkv, tokens, heads, fp16):
+def _attention_mfma_gpu(torch, lib, qkv, tokens, heads):
+    """fp32 attention on the matrix cores (the fp32 precision mode's path)."""
     qd = dev(torch, qkv)
-    ldt = (tokens + 7) // 8 * 8 if fp16 else tokens
-    nbytes = lib.dav2_hip_attention_scratch_bytes(tokens, heads, 1, int(fp16))
+    nbytes = lib.dav2_hip_attention_scratch_bytes(tokens, heads, 1, 0)
     buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     out = empty(torch, (tokens, heads * 64), torch.float32)
     s = stream(torch)
-    ok(lib, lib.dav2_hip_attention_scores(ptr(buf), ptr(qd), tokens, heads, 1, int(fp16), s))
-    ok(lib, lib.dav2_hip_softmax_rows(ptr(buf), heads * tokens, tokens, ldt, int(fp16), s))
-    ok(lib, lib.dav2_hip_attention_values(ptr(out), ptr(buf), ptr(qd), tokens, heads, 1, int(fp16), s))
-    n = heads * tokens * ldt
-    scores = buf[: n * (2 if fp16 else 4)].view(torch.float16 if fp16 else torch.float32).reshape(heads, tokens, ldt)
-    probs = host(torch, scores)
-    if fp16:
-        assert np.all(probs[:, :, tokens:] == 0)  # padding columns are zero after the softmax
-    return host(torch, out), probs[:, :, :tokens].astype(np.float32)
+    ok(lib, lib.dav2_hip_attention_scores(ptr(buf), ptr(qd), tokens, heads, 1, 0, s))
+    ok(lib, lib.dav2_hip_softmax_rows(ptr(buf), heads * tokens, tokens, tokens, 0, s))
+    ok(lib, lib.dav2_hip_attention_values(ptr(out), ptr(buf), ptr(qd), tokens, heads, 1, 0, s))
+    probs = host(torch, buf[: heads * tokens * tokens * 4].view(torch.float32).reshape(heads, tokens, tokens))
+    return host(torch, out), probs
+
+
+def _attention_ref_gpu(torch, lib, qkv, tokens, heads, fp16, batch=1):
+    """The reference-order kernels; returns the output, the probabilities
+    ([batch*H][T][T] as float32) and the scores before the softmax."""
+    qd = dev(torch, qkv)
+    nbytes = lib.dav2_hip_attention_ref_scratch_bytes(tokens, heads, batch, int(fp16))
+    words = (tokens + 1) // 2
+    assert nbytes == batch * heads * tokens * (words * 4 if fp16 else tokens * 4)  # the reference's size
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    out = empty(torch, (batch * tokens, heads * 64), torch.float32)
+    s = stream(torch)
+    ok(lib, lib.dav2_hip_attention_ref_scores(ptr(buf), ptr(qd), tokens, heads, batch, int(fp16), s))
+
+    def unpack():
+        if fp16:
+            w = host(torch, buf.view(torch.float16)).reshape(batch * heads, tokens, 2 * words)
+            return w[:, :, :tokens].astype(np.float32), w[:, :, tokens:]
+        return host(torch, buf.view(torch.float32)).reshape(batch * heads, tokens, tokens), None
+
+    scores, pad = unpack()
+    if fp16 and tokens % 2:
+        assert np.all(pad == 0)  # the high half of a row's last word is 0
+    ok(lib, lib.dav2_hip_attention_ref_softmax(ptr(buf), batch * heads * tokens, tokens, int(fp16), s))
+    probs, pad = unpack()
+    if fp16 and tokens % 2:
+        assert np.all(pad == 0)
+    ok(lib, lib.dav2_hip_attention_ref_values(ptr(out), ptr(buf), ptr(qd), tokens, heads, batch, int(fp16), s))
+    return host(torch, out), probs, scores
+
+
+@pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (5, 2, 1), (65, 3, 1), (258, 2, 2), (1370, 6, 1),
+                                                (1370, 16, 1)])
+def test_attention_ref_fp32_bit_exact(gpu, lib, oracle, tokens, heads, batch):
+    # bmm.glsl + softmax_lastdim.glsl order (mode 0 of the oracle), bit for bit
+    torch = gpu
+    _announce("attention ref fp32", tokens, heads, batch)
+    rng = np.random.default_rng(tokens + heads)
+    qkv = rng.standard_normal((batch * tokens, 3 * heads * 64)).astype(np.float32)
+    out, p, _ = _attention_ref_gpu(torch, lib, qkv, tokens, heads, False, batch)
+    for b in range(batch):
+        rows = slice(b * tokens, (b + 1) * tokens)
+        ref, p_ref = oracle.attention(qkv[rows], tokens, heads, fp16=False, probabilities=True)
+        assert np.array_equal(p[b * heads:(b + 1) * heads].view(np.uint32), p_ref.view(np.uint32))
+        assert np.array_equal(out[rows].view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (2, 1, 1), (5, 2, 1), (77, 4, 1), (258, 2, 2),
+                                                (1369, 3, 1), (1370, 16, 1)])
+def test_attention_ref_fp16_bit_exact(gpu, lib, oracle, tokens, heads, batch):
+    # bmm_score_fp16 + softmax_lastdim_half + bmm_value_fp16 (mode 1 of the
+    # oracle: every product rounded to binary16), bit for bit: the binary16
+    # scores, the probabilities and the output
+    torch = gpu
+    _announce("attention ref fp16", tokens, heads, batch)
+    rng = np.random.default_rng(tokens * 3 + heads)
+    qkv = (rng.standard_normal((batch * tokens, 3 * heads * 64)) * 1.5).astype(np.float32)
+    out, p, scores = _attention_ref_gpu(torch, lib, qkv, tokens, heads, True, batch)
+    for b in range(batch):
+        rows = slice(b * tokens, (b + 1) * tokens)
+        hs = slice(b * heads, (b + 1) * heads)
+        s_ref = oracle.scores_binary16(qkv[rows], tokens, heads).astype(np.float32)
+        assert np.array_equal(scores[hs].view(np.uint32), s_ref.view(np.uint32))
+        ref, p_ref = oracle.attention(qkv[rows], tokens, heads, fp16=True, probabilities=True)
+        assert np.array_equal(p[hs].view(np.uint32), p_ref.view(np.uint32))
+        assert np.array_equal(out[rows].view(np.uint32), ref.view(np.uint32))
+
+
+def test_attention_ref_hand_vectors(gpu, lib):
+    # Scores that only the shader's arithmetic gives (see the oracle tests):
+    # binary16 products cancel exactly; 1, 2^-24, -1 in feature order sum to
+    # 0 while -1, 2^-24, 1 keep 2^-24.
+    torch = gpu
+    qkv = np.zeros((3, 192), np.float32)
+    qkv[0, 0:2] = 8.0 * np.float32([1 + 2.0 ** -10, -1.0])
+    qkv[1, 64:66] = [1 + 2.0 ** -10, 1 + 2.0 ** -9]
+    qkv[2, 64:67] = [-1.0, 2.0 ** -12, 1.0]
+    _, _, scores = _attention_ref_gpu(torch, lib, qkv, 3, 1, True)
+    assert scores[0, 0, 1] == 0.0
+    qkv[0, 0:3] = 8.0 * np.float32([1.0, 2.0 ** -12, -1.0])
+    qkv[1, 64:67] = [1.0, 2.0 ** -12, 1.0]
+    qkv[2, 64:67] = [1.0, 2.0 ** -12, 1.0]
+    _, _, scores = _attention_ref_gpu(torch, lib, qkv, 3, 1, True)
+    assert scores[0, 0, 1] == 0.0
+    qkv[0, 0:3] = 8.0 * np.float32([-1.0, 2.0 ** -12, 1.0])
+    _, _, scores = _attention_ref_gpu(torch, lib, qkv, 3, 1, True)
+    assert scores[0, 0, 1] == np.float32(2.0 ** -24)
 
 
 @pytest.mark.parametrize("tokens,heads", [(5, 2), (65, 3), (1370, 6), (1370, 16)])
-def test_attention_fp32(gpu, lib, oracle, tokens, heads):
+def test_attention_mfma_fp32(gpu, lib, oracle, tokens, heads):
+    # the matrix-core fp32 path of the fp32 precision mode: its own sum order,
+    # within tolerance of the reference order
     torch = gpu
-    _announce("attention fp32", tokens, heads)
+    _announce("attention mfma fp32", tokens, heads)
     rng = np.random.default_rng(tokens + heads)
     qkv = rng.standard_normal((tokens, 3 * heads * 64)).astype(np.float32)
     ref, p_ref = oracle.attention(qkv, tokens, heads, fp16=False, probabilities=True)
-    out, p = _attention_gpu(torch, lib, qkv, tokens, heads, False)
+    out, p = _attention_mfma_gpu(torch, lib, qkv, tokens, heads)
     np.testing.assert_allclose(p, p_ref, rtol=2e-5, atol=2e-7)
     np.testing.assert_allclose(out, ref, rtol=1e-4, atol=2e-6)
 
@@ -626,25 +711,12 @@ def test_attention_reference_kat(gpu, lib):
     p = np.exp(sc - sc.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
     expect = np.einsum("hij,jhf->ihf", p, v).reshape(tokens, d)
-    out32, _ = _attention_gpu(torch, lib, qkv, tokens, heads, False)
+    out32, _, _ = _attention_ref_gpu(torch, lib, qkv, tokens, heads, False)
     assert np.abs(out32 - expect).max() <= 2e-6
-    out16, _ = _attention_gpu(torch, lib, qkv, tokens, heads, True)
+    out16, _, _ = _attention_ref_gpu(torch, lib, qkv, tokens, heads, True)
     assert np.abs(out16 - out32).max() <= 3e-4
-
-
-@pytest.mark.parametrize("tokens,heads", [(5, 2), (77, 4), (1370, 6), (1370, 16)])
-def test_attention_fp16(gpu, lib, oracle, tokens, heads):
-    torch = gpu
-    _announce("attention fp16", tokens, heads)
-    rng = np.random.default_rng(tokens * 3 + heads)
-    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * 0.5).astype(np.float32)
-    ref16, p16 = oracle.attention(qkv, tokens, heads, fp16=True, probabilities=True)
-    ref32 = oracle.attention(qkv, tokens, heads, fp16=False)
-    out, p = _attention_gpu(torch, lib, qkv, tokens, heads, True)
-    # binary16 scores/probabilities: one fp16 ulp of the largest probability
-    np.testing.assert_allclose(p, p16, rtol=0, atol=2e-3 * max(1.0, float(p16.max())))
-    assert np.abs(out - ref16).max() <= 2e-3
-    assert np.abs(out - ref32).max() <= 3e-3
+    outm, _ = _attention_mfma_gpu(torch, lib, qkv, tokens, heads)
+    assert np.abs(outm - expect).max() <= 2e-6
 
 
 def _attention_fused_gpu(torch, lib, qkv, tokens, heads, batch):
@@ -741,13 +813,18 @@ def test_attention_fused_peaked_and_zero_rows(gpu, lib, oracle, colmax):
     assert np.all(out[:, 5] == 0.0)
 
 
-@pytest.mark.parametrize("rows,cols", [(16 * 1370, 1370), (7, 5477), (3, 64), (5, 9000)])
+@pytest.mark.parametrize("rows,cols", [(16 * 1370, 1370), (7, 5477), (3, 64), (5, 9000), (4, 6144), (2, 1)])
 def test_softmax_fp32(gpu, lib, oracle, rows, cols):
+    # softmax_lastdim.glsl in its lane/tree order: bit for bit (register and
+    # streaming forms); the matrix-core path's row softmax within tolerance
     torch = gpu
     _announce("softmax", rows, cols)
     rng = np.random.default_rng(rows)
     x = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
     ref = oracle.softmax_rows(x)
+    xd = dev(torch, x)
+    ok(lib, lib.dav2_hip_attention_ref_softmax(ptr(xd), rows, cols, 0, stream(torch)))
+    assert np.array_equal(host(torch, xd).view(np.uint32), ref.view(np.uint32))
     xd = dev(torch, x)
     ok(lib, lib.dav2_hip_softmax_rows(ptr(xd), rows, cols, cols, 0, stream(torch)))
     np.testing.assert_allclose(host(torch, xd), ref, rtol=5e-6, atol=1e-9)

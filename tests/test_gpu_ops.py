@@ -274,7 +274,17 @@ def test_attention_head64_surface(gpu, pkg, lib, oracle, ops, tokens, heads, pre
                                            precision))
     sync(lib, ops)
     ref = oracle.attention(qkv, tokens, heads, fp16=bool(precision))
-    np.testing.assert_allclose(host(torch, out), ref, atol=2e-3 if precision else 2e-6, rtol=1e-4)
+    # the reference shaders' arithmetic order: bit for bit
+    assert np.array_equal(host(torch, out).view(np.uint32), ref.view(np.uint32))
+    # a caller-provided scratch of exactly the reference's size
+    # (operators.cpp:1112-1119: H*T*T floats, or H*T*ceil(T/2) half2 words)
+    nbytes = heads * tokens * ((tokens + 1) // 2 * 4 if precision else tokens * 4)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    out2 = empty(torch, (tokens, heads * 64), torch.float32)
+    run(lib, lib.dav2_ops_attention_head64(ops, db(pkg, out2), db(pkg, qkv_d), tokens, heads, db(pkg, scratch),
+                                           precision))
+    sync(lib, ops)
+    assert np.array_equal(host(torch, out2).view(np.uint32), ref.view(np.uint32))
     small = empty(torch, (16,), torch.float32)
     assert lib.dav2_ops_attention_head64(ops, db(pkg, out), db(pkg, qkv_d), tokens, heads, db(pkg, small),
                                          precision) == 1

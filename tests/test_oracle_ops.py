@@ -148,6 +148,131 @@ def test_attention_exact_mode_is_order_free(oracle):
                           base.view(np.uint32))
 
 
+# --- binary16 attention (mode 1): the reference's int8-mode default ----------------
+F16, F32 = np.float16, np.float32
+
+
+def _binary16_attention_numpy(oracle, qkv, tokens, heads):
+    """bmm_score_fp16.glsl, softmax_lastdim_half.glsl and bmm_value_fp16.glsl
+    written loop for loop with numpy's IEEE float16 / float32 types (one
+    query row at a time, every sum in the shaders' order). exp is the
+    oracle's exp_cw (GLSL leaves exp's precision open; exp_cw is pinned
+    against float64 in test_exp_cw_*)."""
+    d = heads * 64
+    out = np.zeros((tokens, d), F32)
+    for h in range(heads):
+        q16 = (qkv[:, h * 64:h * 64 + 64].astype(F32) * F32(0.125)).astype(F16)
+        k16 = qkv[:, d + h * 64:d + h * 64 + 64].astype(F16)
+        v16 = qkv[:, 2 * d + h * 64:2 * d + h * 64 + 64].astype(F16)
+        for i in range(tokens):
+            # scores: s[j] += float(q16 * k16) for features 0..63 in order
+            s = np.zeros(tokens, F32)
+            for f in range(64):
+                s = (s + (q16[i, f].astype(F32) * k16[:, f].astype(F32)).astype(F16).astype(F32)).astype(F32)
+            row = s.astype(F16).astype(F32)
+            # softmax: 128 lanes over words (2w, 2w+1), then the halving tree
+            m = row.max()
+            e = oracle.exp((row - m).astype(F32))
+            words = (tokens + 1) // 2
+            part = np.zeros(128, F32)
+            for lane in range(128):
+                acc = F32(0)
+                for w in range(lane, words, 128):
+                    ex = e[2 * w]
+                    ey = e[2 * w + 1] if 2 * w + 1 < tokens else F32(0)
+                    acc = F32(acc + F32(ex + ey))
+                part[lane] = acc
+            stride = 64
+            while stride:
+                part[:stride] = (part[:stride] + part[stride:2 * stride]).astype(F32)
+                stride //= 2
+            inv = F32(F32(1) / max(part[0], F32(1e-20)))
+            p16 = (e.astype(F16).astype(F32) * inv).astype(F16)
+            # values: o[f] += float(p16[j] * v16[j][f]) for tokens j in order
+            o = np.zeros(64, F32)
+            for j in range(tokens):
+                o = (o + (p16[j].astype(F32) * v16[j].astype(F32)).astype(F16).astype(F32)).astype(F32)
+            out[i, h * 64:h * 64 + 64] = o
+    return out
+
+
+def test_round_half_product_matches_numpy(oracle):
+    rng = np.random.default_rng(31)
+    a = rng.standard_normal(1 << 20).astype(F16)
+    b = (rng.standard_normal(1 << 20) * np.exp2(rng.integers(-14, 6, 1 << 20))).astype(F16)
+    a[:8] = [F16(2.0 ** -12), F16(-1.0), F16(65504), F16(2.0 ** -14), 0, F16(1 + 2.0 ** -10), F16(3), F16(-0.0)]
+    b[:8] = [F16(2.0 ** -12), F16(1 + 2.0 ** -9), F16(2), F16(2.0 ** -11), F16(-5), F16(1 + 2.0 ** -10), F16(1e-7), 1]
+    want = (a.astype(F32) * b.astype(F32)).astype(F16).astype(F32)
+    got = oracle.round_half_product(a.astype(F32), b.astype(F32))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _qkv_with(features_q, features_k, tokens=2, heads=1):
+    """qkv rows for a score between query 0 and key 1 with the given q*0.125
+    and k feature values (everything else zero)."""
+    qkv = np.zeros((tokens, 3 * heads * 64), F32)
+    for f, (q, k) in enumerate(zip(features_q, features_k)):
+        qkv[0, f] = 8.0 * q
+        qkv[1, heads * 64 + f] = k
+    return qkv
+
+
+def test_binary16_scores_round_each_product(oracle):
+    # q*0.125 = 1 + 2^-10 times k = 1 + 2^-10 is 1 + 2^-9 + 2^-20 exactly, which
+    # binary16 rounds to 1 + 2^-9; the second feature adds -(1 + 2^-9). Binary16
+    # products give the score 0 exactly; exact products would give 2^-20 (a
+    # binary16 subnormal, so the stored score would keep it).
+    qkv = _qkv_with([1 + 2.0 ** -10, -1.0], [1 + 2.0 ** -10, 1 + 2.0 ** -9])
+    s = oracle.scores_binary16(qkv, 2, 1)
+    assert s[0, 0, 1] == 0.0
+    assert F16(2.0 ** -20) != 0.0  # the exact-product score would survive storage
+    # Feature order of the fp32 sum: 1, 2^-24, -1 in order gives 1 + 2^-24 = 1
+    # (tie to even), then 0; the reversed order would give 2^-24 (the smallest
+    # binary16 subnormal).
+    qkv = _qkv_with([1.0, 2.0 ** -12, -1.0], [1.0, 2.0 ** -12, 1.0])
+    assert oracle.scores_binary16(qkv, 2, 1)[0, 0, 1] == 0.0
+    qkv = _qkv_with([-1.0, 2.0 ** -12, 1.0], [1.0, 2.0 ** -12, 1.0])  # -1 first: -1 + 2^-24 is exact
+    assert oracle.scores_binary16(qkv, 2, 1)[0, 0, 1] == F16(2.0 ** -24)
+    # the score is rounded to binary16 when stored: 1 + 2^-11 + 2^-12 -> 1 + 2^-10
+    qkv = _qkv_with([1.0, 2.0 ** -11, 2.0 ** -12], [1.0, 1.0, 1.0])
+    assert oracle.scores_binary16(qkv, 2, 1)[0, 0, 1] == F16(1 + 2.0 ** -10)
+
+
+@pytest.mark.parametrize("tokens,heads", [(2, 1), (37, 2), (258, 1)])
+def test_binary16_attention_matches_shader_restatement(oracle, tokens, heads):
+    # T = 258: 129 packed words, so lane 0 of the softmax sums two words
+    rng = np.random.default_rng(tokens + 100 * heads)
+    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * 1.5).astype(F32)
+    want = _binary16_attention_numpy(oracle, qkv, tokens, heads)
+    got = oracle.attention(qkv, tokens, heads, fp16=True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_binary16_attention_differs_from_exact_products(oracle):
+    # the binary16 rounding of every product is visible at this size: the
+    # outputs are not those of exact products accumulated in fp32 (a
+    # restatement that drops the product rounding fails here)
+    tokens, heads = 64, 1
+    rng = np.random.default_rng(77)
+    qkv = (rng.standard_normal((tokens, 192)) * 2.0).astype(F32)
+    got = oracle.attention(qkv, tokens, heads, fp16=True)
+    d = 64
+    q16 = (qkv[:, :64] * F32(0.125)).astype(F16).astype(np.float64)
+    k16 = qkv[:, 64:128].astype(F16).astype(np.float64)
+    exact_scores = (q16 @ k16.T).astype(F32).astype(F16).astype(F32)
+    # scores alone already differ somewhere in binary16
+    binary16_scores = np.zeros_like(exact_scores)
+    for i in range(tokens):
+        s = np.zeros(tokens, F32)
+        for f in range(d):
+            s = (s + (F32(q16[i, f]) * k16[:, f].astype(F32)).astype(F16).astype(F32)).astype(F32)
+        binary16_scores[i] = s.astype(F16).astype(F32)
+    assert (binary16_scores != exact_scores).any()
+    # binary16 scores of magnitude up to ~30 carry 2^-6 steps: a loose sanity
+    # bound against float64 attention
+    assert np.abs(got - _attention_f64(qkv, tokens, heads)).max() <= 2e-2
+
+
 def test_numerator21_vs_float64(oracle):
     # E(x) = rint(min(2^x 2^21, 2^21 - 1)) up to the polynomial's rounding:
     # within 0.5 + 2.5e-7 * 2^(x+21) of the float64 value, exact integers,
