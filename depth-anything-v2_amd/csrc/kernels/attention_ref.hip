@@ -36,8 +36,11 @@ constexpr int kKeyTile = 64;
 constexpr int kValueRows = 64;   // value tile: 64 queries x 64 features
 constexpr int kSourceChunk = 32; // source tokens staged per step
 
+// packHalf2x16: each fp32 value rounded to binary16 (round to nearest even).
+// The values are pinned as fp32 first so that the conversion rounds the fp32
+// result, never a fused wider intermediate.
 DAV2_DEV uint32_t pack_half2(float lo, float hi) {
-    const _Float16 a = static_cast<_Float16>(lo), b = static_cast<_Float16>(hi);
+    const _Float16 a = static_cast<_Float16>(keep_fp32(lo)), b = static_cast<_Float16>(keep_fp32(hi));
     return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
 }
@@ -83,7 +86,8 @@ __global__ __launch_bounds__(256) void ref_scores_kernel(const float* __restrict
         // bmm.glsl:57-63 / bmm_score_fp16.glsl:32-33: q * 0.125 (exact), then binary16
         float q[4] = {v.x * 0.125f, v.y * 0.125f, v.z * 0.125f, v.w * 0.125f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) qs[f4 + e][r] = HALF ? static_cast<float>(static_cast<_Float16>(q[e])) : q[e];
+        for (int e = 0; e < 4; ++e)
+            qs[f4 + e][r] = HALF ? static_cast<float>(static_cast<_Float16>(keep_fp32(q[e]))) : q[e];
     }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -263,7 +267,7 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
         if (HALF) {
             // p = fp16(float(fp16(e)) * inverse); the stored exponentials are fp16(e)
             const float pa = static_cast<float>(static_cast<_Float16>(ea)) * inverse;
-            const float pb = static_cast<float>(static_cast<_Float16>(eb)) * inverse;
+            const float pb = static_cast<float>(static_cast<_Float16>(eb)) * inverse;  // pack_half2 keeps them fp32
             wr[item] = pack_half2(pa, pb);
         } else {
             fr[item] = ea * inverse;

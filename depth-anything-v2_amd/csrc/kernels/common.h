@@ -54,6 +54,17 @@ DAV2_DEV uint32_t pack4(int a, int b, int c, int d) {
 // CPU oracle bit for bit).
 DAV2_DEV float div_rn(float a, float b) { return __fdiv_rn(a, b); }
 
+// v exactly as computed: a rounded fp32 value the compiler may not fuse
+// into the operation that consumes it. Needed where an fp32 result is then
+// rounded to binary16: fp16(a * b) would otherwise become one
+// v_fma_mixlo_f16, which rounds the exact product once instead of rounding
+// it to fp32 first (the two differ when the fp32 rounding lands on a
+// binary16 tie).
+DAV2_DEV float keep_fp32(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 inline unsigned ceil_div(uint64_t a, uint64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;

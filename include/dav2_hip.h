@@ -241,14 +241,13 @@ DAV2_API int dav2_hip_add(float* out, const float* left, const float* right, uin
                           void* stream);
 DAV2_API int dav2_hip_relu(float* out, const float* input, uint64_t count, void* stream);
 
-/* Attention, head_dim 64 (src/operators.cpp:1098-1209). qkv is [batch*T][3*H*64]
- * token-major (q | k | v, head h at h*64). fp16 = 0: fp32 scores [batch][H][T][T]
- * (bmm.glsl, softmax_lastdim.glsl); fp16 = 1: binary16 scores
- * [batch][H][T][ldt], ldt = T rounded up to a multiple of 8 (bmm_score_fp16.glsl,
- * softmax_lastdim_half.glsl, bmm_value_fp16.glsl), followed (at the next
- * 256-byte boundary) by a packed binary16 copy of v that attention_values
- * writes and reads. Softmax is in place. The whole score buffer holds
- * dav2_hip_attention_scratch_bytes() bytes. */
+/* fp32 attention, head_dim 64, on the matrix cores (the fp32 precision
+ * mode's path; src/operators.cpp:1169-1208 with bmm.glsl and
+ * softmax_lastdim.glsl, sums in the MFMA's order: within tolerance of the
+ * reference, not bit for bit). qkv is [batch*T][3*H*64] token-major (q | k |
+ * v, head h at h*64); scores [batch][H][T][T] fp32, softmax in place,
+ * dav2_hip_attention_scratch_bytes() bytes. fp16 must be 0 (binary16 is
+ * dav2_hip_attention_ref_*). */
 DAV2_API uint64_t dav2_hip_attention_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch,
                                                    int fp16);
 DAV2_API int dav2_hip_attention_scores(void* scores, const float* qkv, uint32_t tokens,
