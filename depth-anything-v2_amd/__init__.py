@@ -194,6 +194,7 @@ PROTOTYPES = {
     "dav2_hip_attention_values": (C.c_int, [vp, vp, vp, u32, u32, u32, C.c_int, vp]),
     "dav2_hip_attention_scratch_bytes": (u64, [u32, u32, u32, C.c_int]),
     "dav2_hip_attention_ref_scratch_bytes": (u64, [u32, u32, u32, C.c_int]),
+    "dav2_hip_pad_rows_i8": (C.c_int, [vp, u32, u32, vp, u32, vp]),
     "dav2_hip_attention_ref_scores": (C.c_int, [vp, vp, u32, u32, u32, C.c_int, vp]),
     "dav2_hip_attention_ref_softmax": (C.c_int, [vp, u64, u32, C.c_int, vp]),
     "dav2_hip_attention_ref_values": (C.c_int, [vp, vp, vp, u32, u32, u32, C.c_int, vp]),

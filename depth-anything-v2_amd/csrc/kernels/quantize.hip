@@ -510,7 +510,41 @@ hipError_t dav2k::launch_channel_group_absmax(const float* x, uint32_t channels,
     return hipGetLastError();
 }
 
+// int8 rows of `columns` bytes (the reference GpuModel layout) to rows of
+// ld bytes, zero beyond columns: 16 bytes per thread, one row per y block.
+__global__ __launch_bounds__(256) void pad_rows_kernel(const int8_t* __restrict__ src, uint32_t columns,
+                                                       int8_t* __restrict__ dst, uint32_t ld) {
+    const uint64_t row = blockIdx.y;
+    const uint32_t c0 = (blockIdx.x * 256u + threadIdx.x) * 16u;
+    if (c0 >= ld) return;
+    const int8_t* s = src + row * columns;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t c = c0 + q * 4 + b;
+            const uint32_t byte = c < columns ? static_cast<uint8_t>(s[c]) : 0u;
+            word |= byte << (8 * b);
+        }
+        w[q] = word;
+    }
+    *reinterpret_cast<uint4*>(dst + row * ld + c0) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 extern "C" {
+
+int dav2_hip_pad_rows_i8(const int8_t* src, uint32_t rows, uint32_t columns, int8_t* dst, uint32_t ld,
+                         void* stream) {
+    if (rows == 0) return hipSuccess;
+    if (!src || !dst || columns == 0 || ld < columns || ld % 16u || (reinterpret_cast<uintptr_t>(dst) & 15) ||
+        rows > 65535u)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pad_rows_kernel, dim3(ceil_div(ld, 256u * 16u), rows), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), src, columns, dst, ld);
+    return hipGetLastError();
+}
 
 int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset, uint32_t rows,
                               uint32_t columns, int8_t* q, uint32_t ldq, float* scales,

@@ -63,6 +63,39 @@ void HipOperators::linear_int8(DeviceBuffer& output, const DeviceBuffer& input, 
                              gelu ? Epilogue::row_gelu : Epilogue::row);
 }
 
+void HipOperators::linear_int8_in(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+                                  const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
+                                  std::uint32_t input_columns, std::uint32_t output_columns, bool gelu,
+                                  const DeviceBuffer& packed, const DeviceBuffer& scales) {
+    if (rows == 0 || input_columns == 0 || output_columns == 0 || input_columns % 4 != 0)
+        throw std::invalid_argument("invalid INT8 linear dimensions");
+    require_bytes(input, std::uint64_t(rows) * input_columns, "input");
+    require_int8_weight(int8_weight, output_columns, input_columns, "packed INT8 weight buffer");
+    require_bytes(weight_scales, output_columns, "weight scale");
+    require_bytes(bias, output_columns, "bias");
+    require_bytes(output, std::uint64_t(rows) * output_columns, "output");
+    const std::uint32_t ld = ld64(input_columns);
+    if (packed.size() < std::uint64_t(rows) * ld || scales.size() < std::uint64_t(rows) * sizeof(float))
+        throw std::invalid_argument("INT8 linear workspace is too small");
+    hip_check(dav2_hip_quantize_rows_i8(input.as<float>(), 0, rows, input_columns, packed.as<int8_t>(), ld,
+                                        scales.as<float>(), stream()),
+              "quantize_rows_int8");
+    dav2_gemm_i8_args a{};
+    a.a = packed.as<int8_t>();
+    a.lda = ld;
+    a.b = int8_weight.as<int8_t>();
+    a.ldb = ld;
+    a.m = rows;
+    a.n = output_columns;
+    a.k = ld;
+    a.epilogue = gelu ? DAV2_GEMM_EPI_ROW_GELU : DAV2_GEMM_EPI_ROW;
+    a.a_scales = scales.as<float>();
+    a.b_scales = weight_scales.as<float>();
+    a.bias = bias.as<float>();
+    a.out = output.as<float>();
+    hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
+}
+
 void HipOperators::quantize_rows(const DeviceBuffer& input, std::uint64_t input_offset, std::uint32_t rows,
                                  std::uint32_t columns) {
     const std::uint32_t ld = ld64(columns);

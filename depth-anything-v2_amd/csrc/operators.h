@@ -67,6 +67,14 @@ public:
                      const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
                      std::uint32_t input_columns, std::uint32_t output_columns, bool gelu,
                      bool weight_transposed = false);
+    // linear_int8 with the quantized rows in caller memory: packed holds
+    // rows x roundup(input_columns, 64) bytes, scales rows floats. The same
+    // kernels and bits as linear_int8; allocates nothing (no workspace
+    // growth, no profiling events).
+    void linear_int8_in(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
+                        const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
+                        std::uint32_t input_columns, std::uint32_t output_columns, bool gelu,
+                        const DeviceBuffer& packed, const DeviceBuffer& scales);
 
     void layer_norm(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
                     const DeviceBuffer& bias, std::uint32_t rows, std::uint32_t columns, float epsilon);

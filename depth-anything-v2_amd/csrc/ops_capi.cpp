@@ -1,10 +1,12 @@
 // C ABI over dav2::HipOperators (include/dav2_ops.h).
 
+#include "dav2_hip.h"
 #include "dav2_ops.h"
 
 #include "executor.h"
 #include "operators.h"
 
+#include <algorithm>
 #include <memory>
 #include <new>
 #include <stdexcept>
@@ -13,6 +15,9 @@
 struct dav2_ops {
     std::unique_ptr<dav2::HipContext> context;
     std::unique_ptr<dav2::HipOperators> ops;
+    // int8 weights of the reference layout repacked to the GEMM layout when
+    // their row length is not a multiple of 64 (grown on demand)
+    dav2::DeviceBuffer padded_weight;
 };
 
 namespace {
@@ -42,6 +47,37 @@ dav2_status guard(dav2_ops* ops, Function&& f) {
 }
 
 dav2::DeviceBuffer v(const dav2_device_buffer& b) { return dav2::DeviceBuffer::view(b.data, b.data ? b.bytes : 0); }
+
+std::uint32_t ld64(std::uint64_t columns) { return static_cast<std::uint32_t>((columns + 63) & ~63ull); }
+
+// int8 weights as the reference's GpuModel hands them to its operators:
+// [rows][columns] bytes, i.e. [rows][columns/4] little-endian words of four
+// int8 (src/gpu_model.cpp:241-284, quantize_rows_int8_fused.glsl:51). The
+// operators take rows of roundup(columns, 64) bytes with zero padding; for
+// columns % 64 == 0 that is the same memory, otherwise the rows are copied
+// into the instance's padded buffer (enqueued on its stream).
+dav2::DeviceBuffer reference_int8_weight(dav2_ops& o, const dav2_device_buffer& w, std::uint64_t rows,
+                                         std::uint64_t columns, const char* what) {
+    if (rows == 0 || columns == 0 || columns % 4 != 0 || rows > 0xffffffffull || columns > 0xffffffffull)
+        throw std::invalid_argument(std::string("invalid ") + what + " dimensions");
+    if (w.data == nullptr || w.bytes < rows * columns) throw std::invalid_argument(std::string(what) + " is too small");
+    if (columns % 64 == 0) return v(w);
+    const std::uint64_t ld = ld64(columns);
+    if (o.padded_weight.size() < rows * ld) {
+        o.context->synchronize();  // work already queued may still read the old buffer
+        o.padded_weight.reset();
+        o.padded_weight = dav2::DeviceBuffer(rows * ld);
+    }
+    for (std::uint64_t r0 = 0; r0 < rows; r0 += 65535) {
+        const std::uint64_t n = std::min<std::uint64_t>(65535, rows - r0);
+        dav2::hip_check(dav2_hip_pad_rows_i8(static_cast<const std::int8_t*>(w.data) + r0 * columns,
+                                             static_cast<std::uint32_t>(n), static_cast<std::uint32_t>(columns),
+                                             o.padded_weight.as<std::int8_t>() + r0 * ld, static_cast<std::uint32_t>(ld),
+                                             o.ops->stream()),
+                        "pad int8 weight rows");
+    }
+    return dav2::DeviceBuffer::view(o.padded_weight.data(), rows * ld);
+}
 
 }  // namespace
 
@@ -74,7 +110,8 @@ dav2_status DAV2_CALL dav2_ops_linear_int8(dav2_ops* ops, dav2_device_buffer out
                                           uint32_t rows, uint32_t ic, uint32_t oc, int32_t gelu) {
     return guard(ops, [&](dav2::HipOperators& o) {
         auto out = v(output);
-        o.linear_int8(out, v(input), v(w8), v(ws), v(bias), rows, ic, oc, gelu != 0);
+        const auto w = reference_int8_weight(*ops, w8, oc, ic, "packed INT8 weight buffer");
+        o.linear_int8(out, v(input), w, v(ws), v(bias), rows, ic, oc, gelu != 0);
     });
 }
 
@@ -115,7 +152,8 @@ dav2_status DAV2_CALL dav2_ops_prepare_tokens(dav2_ops* ops, dav2_device_buffer 
                                              uint32_t height, uint32_t embedding) {
     return guard(ops, [&](dav2::HipOperators& o) {
         auto out = v(output);
-        o.prepare_tokens(out, v(image), dav2::DeviceBuffer(), dav2::DeviceBuffer(), v(w8), v(ws), v(bias), v(cls),
+        const auto w = reference_int8_weight(*ops, w8, embedding, 3 * 14 * 14, "INT8 patch weight buffer");
+        o.prepare_tokens(out, v(image), dav2::DeviceBuffer(), dav2::DeviceBuffer(), w, v(ws), v(bias), v(cls),
                          v(position), width, height, embedding, dav2::Precision::int8);
     });
 }
@@ -126,7 +164,8 @@ dav2_status DAV2_CALL dav2_ops_project_tokens_int8(dav2_ops* ops, dav2_device_bu
                                                   uint32_t height, uint32_t embedding, uint32_t channels) {
     return guard(ops, [&](dav2::HipOperators& o) {
         auto out = v(output);
-        o.project_tokens_int8(out, v(tokens), v(w8), v(ws), v(bias), width, height, embedding, channels);
+        const auto w = reference_int8_weight(*ops, w8, channels, embedding, "INT8 projection weight");
+        o.project_tokens_int8(out, v(tokens), w, v(ws), v(bias), width, height, embedding, channels);
     });
 }
 
@@ -136,7 +175,8 @@ dav2_status DAV2_CALL dav2_ops_conv2d_int8(dav2_ops* ops, dav2_device_buffer out
                                           uint32_t stride, uint32_t padding, int32_t has_bias) {
     return guard(ops, [&](dav2::HipOperators& o) {
         auto out = v(output);
-        o.conv2d_int8(out, v(input), v(w8), v(ws), v(bias), iw, ih, ic, oc, kernel, stride, padding, has_bias != 0);
+        const auto w = reference_int8_weight(*ops, w8, oc, std::uint64_t(ic) * kernel * kernel, "INT8 convolution weight");
+        o.conv2d_int8(out, v(input), w, v(ws), v(bias), iw, ih, ic, oc, kernel, stride, padding, has_bias != 0);
     });
 }
 
@@ -147,7 +187,9 @@ dav2_status DAV2_CALL dav2_ops_conv_transpose_nonoverlap_int8(dav2_ops* ops, dav
                                                              uint32_t kernel) {
     return guard(ops, [&](dav2::HipOperators& o) {
         auto out = v(output);
-        o.conv_transpose_nonoverlap_int8(out, v(input), v(w8), v(ws), v(bias), iw, ih, ic, oc, kernel);
+        const auto w =
+            reference_int8_weight(*ops, w8, std::uint64_t(kernel) * kernel * oc, ic, "INT8 transposed weight");
+        o.conv_transpose_nonoverlap_int8(out, v(input), w, v(ws), v(bias), iw, ih, ic, oc, kernel);
     });
 }
 

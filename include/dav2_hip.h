@@ -34,6 +34,13 @@ DAV2_API int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset
                                        uint32_t rows, uint32_t columns, int8_t* q,
                                        uint32_t ldq, float* scales, void* stream);
 
+/* int8 weight rows of `columns` bytes -- the reference GpuModel layout,
+ * [rows][columns/4] little-endian words (src/gpu_model.cpp:241-284) -- to the
+ * GEMM layout [rows][ld] (ld % 16 == 0, ld >= columns), bytes [columns, ld)
+ * zero. rows <= 65535. No reference counterpart (a layout conversion). */
+DAV2_API int dav2_hip_pad_rows_i8(const int8_t* src, uint32_t rows, uint32_t columns, int8_t* dst, uint32_t ld,
+                                  void* stream);
+
 /* Replaces im2col_quantize_int8.glsl:26-83 (src/operators.cpp:1284-1298,
  * :1787-1801, :1946-1960). CHW input; rows = output_width*output_height.
  * scratch (optional, dav2_hip_im2col_scratch_floats() floats) enables the

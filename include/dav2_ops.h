@@ -7,9 +7,14 @@
  * std::invalid_argument). Buffers are device memory described by
  * {pointer, bytes}; work is enqueued on the instance's stream.
  *
- * int8 weights use the GpuModel layout: [rows][ld] bytes with
- * ld = columns rounded up to 64 and zero padding (row r, column c = int8
- * weight of output r, input c; ConvTranspose rows are (ky*k+kx)*OC + oc).
+ * int8 weights use the reference GpuModel's layout (src/gpu_model.cpp:241-284):
+ * [rows][columns] bytes -- [rows][columns/4] little-endian words of four int8,
+ * as quantize_rows_int8_fused.glsl packs them -- with columns % 4 == 0 (row r,
+ * column c = int8 weight of output r, input c; convolution columns
+ * ic*k*k + ky*k + kx; ConvTranspose rows (ky*k+kx)*OC + oc, columns IC).
+ * Rows whose length is not a multiple of 64 (patch embedding 588, 3x3 over
+ * 48 channels 432, ...) are copied into a padded buffer of the instance on
+ * its stream before use.
  */
 #ifndef DAV2_OPS_H
 #define DAV2_OPS_H

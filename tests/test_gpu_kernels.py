@@ -580,6 +580,20 @@ def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
         assert np.array_equal(host(torch, out2).view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,cols,ld", [(384, 588, 640), (64, 432, 448), (1, 4, 16), (7, 36, 4096), (3, 64, 64)])
+def test_pad_rows_i8(gpu, lib, rows, cols, ld):
+    # reference GpuModel int8 rows ([rows][cols] bytes) to the GEMM layout
+    torch = gpu
+    rng = np.random.default_rng(rows + cols)
+    q = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+    src = dev(torch, q)
+    dst = torch.full((rows, ld), 0x55, dtype=torch.int8, device="cuda")
+    ok(lib, lib.dav2_hip_pad_rows_i8(ptr(src), rows, cols, ptr(dst), ld, stream(torch)))
+    got = host(torch, dst)
+    assert np.array_equal(got[:, :cols], q) and np.all(got[:, cols:] == 0)
+    assert lib.dav2_hip_pad_rows_i8(ptr(src), rows, cols, ptr(dst), cols - 4, stream(torch)) != 0
+
+
 # ---------------------------------------------------------------------------
 # attention: scores -> softmax -> values
 def _attention_mfma_gpu(torch, lib, qkv, tokens, heads):

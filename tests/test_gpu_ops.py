@@ -8,7 +8,6 @@ import pytest
 import torch.nn.functional as F
 
 from gpu_util import db, dev, empty, host
-from oracle_py import pad_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -30,12 +29,15 @@ def sync(lib, ops):
 
 
 def _weight(torch, oracle, w):
+    """int8 weights in the reference GpuModel layout: [rows][K] bytes
+    (gpu_model.cpp:241-284), exactly K bytes per row whatever K % 64."""
     q, s = oracle.quantize_weight_rows(w)
-    return dev(torch, pad_rows(q)), dev(torch, s), q, s
+    return dev(torch, np.ascontiguousarray(q)), dev(torch, s), q, s
 
 
 @pytest.mark.parametrize("rows,ic,oc,gelu", [(1370, 384, 1152, False), (1370, 1024, 4096, True), (5, 588, 384, False),
-                                             (1369, 1536, 384, False)])
+                                             (1369, 1536, 384, False), (1369, 588, 384, False), (77, 432, 48, True),
+                                             (3, 36, 5, False)])
 def test_linear_int8(gpu, pkg, lib, oracle, ops, rows, ic, oc, gelu):
     torch = gpu
     rng = np.random.default_rng(rows + ic + oc)
@@ -95,7 +97,7 @@ def test_conv2d_int8_reference_kat(gpu, pkg, lib, oracle, ops):
 @pytest.mark.parametrize("c,h,w,oc,k,stride,pad,bias", [
     (256, 37, 37, 256, 3, 1, 1, True), (1024, 19, 19, 256, 3, 1, 1, False), (1024, 37, 37, 1024, 3, 2, 1, True),
     (256, 74, 74, 256, 1, 1, 0, True), (128, 130, 130, 32, 3, 1, 1, True), (32, 130, 130, 1, 1, 1, 0, True),
-    (96, 23, 29, 64, 3, 1, 1, True)])
+    (96, 23, 29, 64, 3, 1, 1, True), (48, 37, 37, 64, 3, 1, 1, True), (48, 21, 17, 96, 3, 2, 1, False)])
 def test_conv2d_int8_vs_oracle(gpu, pkg, lib, oracle, ops, c, h, w, oc, k, stride, pad, bias):
     torch = gpu
     print("case: conv2d", c, h, w, oc, k, stride, pad, flush=True)
@@ -123,7 +125,7 @@ def test_conv_transpose_reference_kat(gpu, pkg, lib, oracle, ops):
     weights = ((np.arange(inputs * outputs * k * k) % 13 - 6) * 0.02).astype(np.float32).reshape(inputs, outputs, k, k)
     biases = np.zeros(outputs, np.float32)
     q, s = oracle.quantize_convT_weight(weights)
-    wd, sd, bd, xd = dev(torch, pad_rows(q)), dev(torch, s), dev(torch, biases), dev(torch, values)
+    wd, sd, bd, xd = dev(torch, q), dev(torch, s), dev(torch, biases), dev(torch, values)
     out = empty(torch, (outputs, height * k, width * k), torch.float32)
     run(lib, lib.dav2_ops_conv_transpose_nonoverlap_int8(ops, db(pkg, out), db(pkg, xd), db(pkg, wd), db(pkg, sd),
                                                          db(pkg, bd), width, height, inputs, outputs, k))
@@ -143,7 +145,7 @@ def test_conv_transpose_vs_oracle(gpu, pkg, lib, oracle, ops, c, h, w, k):
     wt = rng.uniform(-1, 1, (c, c, k, k)).astype(np.float32) / np.sqrt(c * k * k)
     b = rng.uniform(-0.1, 0.1, c).astype(np.float32)
     q, s = oracle.quantize_convT_weight(wt)
-    wd, sd, bd, xd = dev(torch, pad_rows(q)), dev(torch, s), dev(torch, b), dev(torch, x)
+    wd, sd, bd, xd = dev(torch, q), dev(torch, s), dev(torch, b), dev(torch, x)
     out = empty(torch, (c, h * k, w * k), torch.float32)
     run(lib, lib.dav2_ops_conv_transpose_nonoverlap_int8(ops, db(pkg, out), db(pkg, xd), db(pkg, wd), db(pkg, sd),
                                                          db(pkg, bd), w, h, c, c, k))
@@ -205,7 +207,7 @@ def test_prepare_tokens_reference_kat(gpu, pkg, lib, oracle, ops):
     # Every device tensor stays referenced until the call is synchronised: a
     # temporary would go back to torch's caching allocator and the next
     # upload could reuse its memory.
-    held = [dev(torch, a) for a in (image, pad_rows(wq), ws, bias, cls, pos)]
+    held = [dev(torch, a) for a in (image, wq, ws, bias, cls, pos)]
     run(lib, lib.dav2_ops_prepare_tokens(ops, db(pkg, out), *[db(pkg, t) for t in held], width, height, dim))
     sync(lib, ops)
     tokens = host(torch, out)
