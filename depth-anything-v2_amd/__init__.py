@@ -224,6 +224,7 @@ PROTOTYPES = {
     "dav2_ops_stream": (vp, [vp]),
     "dav2_ops_synchronize": (C.c_int, [vp]),
     "dav2_ops_linear_int8": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, i32]),
+    "dav2_ops_linear_int8_noalloc": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, i32]),
     "dav2_ops_layer_norm": (C.c_int, [vp, DB, DB, DB, DB, u32, u32, f32]),
     "dav2_ops_add_scaled": (C.c_int, [vp, DB, DB, DB, DB, u32, u32]),
     "dav2_ops_attention_head64": (C.c_int, [vp, DB, DB, u32, u32, DB, i32]),

@@ -50,6 +50,21 @@ DAV2_API dav2_status DAV2_CALL dav2_ops_linear_int8(dav2_ops* ops, dav2_device_b
                                                     dav2_device_buffer weight_scales, dav2_device_buffer bias,
                                                     uint32_t rows, uint32_t input_columns,
                                                     uint32_t output_columns, int32_t gelu);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments, checks and output bits as
+ * dav2_ops_linear_int8, but the quantized input rows (rows x roundup(K, 64)
+ * bytes), their scales and, when K % 64 != 0, the padded weight rows
+ * (N x roundup(K, 64) bytes) go into a fixed 32 MiB device array per GPU
+ * instead of the instance's growing workspace; the call allocates nothing.
+ * Sizes beyond the array -> DAV2_STATUS_INVALID_ARGUMENT. Calls that overlap
+ * on one GPU (two instances, two streams) race on the array: serialise them. */
+DAV2_API dav2_status DAV2_CALL dav2_ops_linear_int8_noalloc(dav2_ops* ops, dav2_device_buffer output,
+                                                            dav2_device_buffer input, dav2_device_buffer int8_weight,
+                                                            dav2_device_buffer weight_scales,
+                                                            dav2_device_buffer bias, uint32_t rows,
+                                                            uint32_t input_columns, uint32_t output_columns,
+                                                            int32_t gelu);
 /* src/operators.h:94-101 */
 DAV2_API dav2_status DAV2_CALL dav2_ops_layer_norm(dav2_ops* ops, dav2_device_buffer output,
                                                    dav2_device_buffer input, dav2_device_buffer weight,
