@@ -177,7 +177,7 @@ PROTOTYPES = {
     "dav2_hip_im2col_quantize_i8": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, vp, u32, vp, vp, u64, vp]),
     "dav2_hip_im2col_quantize_relu_i8": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, vp, u32, vp, vp, u64, vp]),
     "dav2_hip_conv2d_i8_supported": (C.c_int, [u32, u32, u32, u32, u32, u32, u32]),
-    "dav2_hip_conv_weights_tapmajor": (C.c_int, [vp, vp, u32, u32, u32, u64, vp]),
+    "dav2_hip_conv_weights_pack": (C.c_int, [vp, vp, u32, u32, u32, u64, vp]),
     "dav2_hip_conv2d_i8": (C.c_int, [C.POINTER(ConvArgs), vp]),
     "dav2_hip_conv1x1_narrow_i8": (C.c_int, [vp, u32, u32, u32, vp, u32, vp, vp, u32, vp, vp, u32, vp]),
     "dav2_hip_layer_norm": (C.c_int, [vp, vp, vp, vp, u32, u32, f32, vp]),

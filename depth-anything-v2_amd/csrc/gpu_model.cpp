@@ -127,11 +127,11 @@ GpuModel::GpuModel(const MappedModel& model, HipContext& context, bool fp32_weig
                 dav2_hip_conv2d_i8_supported(1, 1, static_cast<std::uint32_t>(src.shape[1]),
                                              dst.int8_rows, static_cast<std::uint32_t>(k), 1,
                                              static_cast<std::uint32_t>((k - 1) / 2))) {
-                dst.int8_tapmajor = context.create_device_buffer(rows * columns);
-                hip_check(dav2_hip_conv_weights_tapmajor(dst.int8_tapmajor.as<int8_t>(), dst.int8_buffer.as<int8_t>(),
-                                                         dst.int8_rows, static_cast<std::uint32_t>(src.shape[1]),
-                                                         static_cast<std::uint32_t>(k), dst.int8_ld, stream),
-                          "tap-major conv weights");
+                dst.int8_packed = context.create_device_buffer(rows * columns);
+                hip_check(dav2_hip_conv_weights_pack(dst.int8_packed.as<int8_t>(), dst.int8_buffer.as<int8_t>(),
+                                                     dst.int8_rows, static_cast<std::uint32_t>(src.shape[1]),
+                                                     static_cast<std::uint32_t>(k), dst.int8_ld, stream),
+                          "packed conv weights");
                 device_bytes_ += rows * columns;
             }
         }

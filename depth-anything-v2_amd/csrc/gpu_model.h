@@ -30,9 +30,10 @@ struct GpuTensor {
     DeviceBuffer int8_buffer;  // [int8_rows][int8_ld]
     DeviceBuffer int8_scales;  // [int8_rows]
     // Conv weights the implicit-GEMM convolution takes (kernel 1 or 3,
-    // IC % 64 == 0, OC % 32 == 0): the same int8 rows with columns reordered
-    // tap-major, [OC][(ky*k + kx)*IC + ic], no padding. Empty otherwise.
-    DeviceBuffer int8_tapmajor;
+    // IC % 64 == 0, OC % 32 == 0): the same int8 rows with K walked tap-major
+    // ((ky*k + kx)*IC + ic) and cut into the kernels' 16 x 64-byte operand
+    // fragments (dav2_hip_conv_weights_pack). Empty otherwise.
+    DeviceBuffer int8_packed;
     std::uint32_t int8_rows = 0;
     std::uint32_t int8_columns = 0;
     std::uint32_t int8_ld = 0;

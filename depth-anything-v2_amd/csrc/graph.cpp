@@ -220,7 +220,7 @@ FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::str
         f.emit_relu = emit == Emit::relu;
     }
     if (ops.conv2d_int8(*out.buffer, *in.buffer, w.int8_buffer, w.int8_scales, b, in.width, in.height, in.channels, oc,
-                        k, stride, pad, has_bias, &w.int8_tapmajor, f)) {
+                        k, stride, pad, has_bias, &w.int8_packed, f)) {
         out.maxima = maxima;
         out.maxima_relu = emit == Emit::relu;
     }

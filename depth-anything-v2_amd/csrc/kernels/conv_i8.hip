@@ -4,8 +4,10 @@
 // linear_int8_tiled.glsl:40-117 with the CHW store) in one kernel, without
 // the im2col matrix ever reaching HBM.
 //
-// Scope: kernel 3 (stride 1, padding 1) or kernel 1 (stride 1, no padding),
-// input channels a multiple of 64, output channels a multiple of 32.
+// Scope: kernel 1 (stride 1, no padding), and kernel 3 (stride 1, padding 1)
+// on maps conv3x3_i8.hip does not take (odd widths, inputs not 8-byte
+// aligned); input channels a multiple of 64, output channels a multiple of
+// 32.
 //
 // Arithmetic. Output pixel p's im2col row is quantized with the scale
 // s = max(absmax/127, 1e-8) of that whole row and q = rne(clamp(x * (1/s))),
@@ -13,7 +15,7 @@
 // the order in which K is walked is free. This kernel walks K tap-major
 // (k = tap * C + c, tap = ky * ks + kx) so that one 64-byte K step is 64
 // channels of one tap; the weights are stored in that order
-// (dav2_hip_conv_weights_tapmajor). The epilogue is the GEMM's CHW epilogue,
+// (packed by dav2_hip_conv_weights_pack). The epilogue is the GEMM's CHW epilogue,
 // ((float(acc) * s_pixel) * s_weight) + bias, so every output float equals
 // the im2col + GEMM path's bit for bit.
 //
@@ -38,66 +40,16 @@
 #include <type_traits>
 
 #include "common.h"
+#include "conv_common.h"
 #include "dav2_hip.h"
 
 using namespace dav2k;
 
 namespace {
 
-constexpr int kPix = 64;  // output pixels per workgroup
-constexpr int kCB = 64;   // input channels per block = one MFMA K step per tap
-
-struct ConvParams {
-    const float* x;        // CHW input
-    const float* partial;  // [groups][plane] channel-group |x| maxima
-    uint32_t groups;
-    uint32_t channels, height, width;
-    uint64_t plane;
-    uint32_t tiles_x;      // 3x3: pixel tiles per image row
-    const int8_t* w;       // [N][taps * channels], tap-major
-    const float* w_scales;
-    const float* bias;     // nullable
-    float* out;            // CHW [N][plane]
-    const float* residual; // nullable, CHW [N][plane]
-    uint32_t flags;        // DAV2_CONV_*
-    float* emit;           // channel-group maxima of the output (EMIT flags), [N/32][plane]
-};
-
 // Source of the 3x3 window positions outside the image (zero padding): the
 // copies of those positions read it instead of the input.
 __device__ float g_conv_zero_row[64];
-
-// Workgroup barrier that orders LDS only: waits for this wave's LDS
-// operations (lgkmcnt) but leaves global loads in flight.
-DAV2_DEV void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// rne(clamp(v * inv, -127, 127)) of four values packed little-endian, for
-// |v| <= absmax of the row and inv = 1 / max(absmax / 127, 1e-8): then
-// |v * inv| <= 127 * (1 + 3 * 2^-24) < 127.5 (or below 127 under the 1e-8
-// floor), so rounding alone lands in [-127, 127] and the clamp never acts.
-// Adding 1.5 * 2^23 rounds to an integer (round to nearest even, the ulp
-// there is 1) held in the low mantissa bits, so the low byte of the sum is the
-// two's-complement int8; v_perm gathers the bytes. (Finite inputs: the
-// reference leaves NaN and infinity to the shader's clamp.)
-DAV2_DEV uint32_t quant4(float a, float b, float c, float d, float inv) {
-    constexpr float kMagic = 12582912.0f;
-    const uint32_t qa = __float_as_uint(a * inv + kMagic);
-    const uint32_t qb = __float_as_uint(b * inv + kMagic);
-    const uint32_t qc = __float_as_uint(c * inv + kMagic);
-    const uint32_t qd = __float_as_uint(d * inv + kMagic);
-    const uint32_t lo = __builtin_amdgcn_perm(qb, qa, 0x00000400u);  // bytes: a, b, a, a
-    const uint32_t hi = __builtin_amdgcn_perm(qd, qc, 0x00000400u);  // bytes: c, d, c, c
-    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);               // bytes: a, b, c, d
-}
-
-// LDS byte offset of 16-byte chunk c (0..3) of pixel row p in a 64 x 64-byte
-// int8 tile: rows are 64 bytes, chunks XOR-swizzled by (p / 4) % 4 so the 16
-// rows one MFMA operand read touches cover all banks once.
-DAV2_DEV uint32_t a_offset(uint32_t p, uint32_t c) { return p * 64u + ((c ^ ((p >> 2) & 3u)) << 4); }
 
 template <int KS, int BN, int WM, int WN, bool RELU_IN>
 __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
@@ -292,17 +244,15 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
         }
     };
 
-    // ---- weight fragments ----------------------------------------------------
-    // Lane l supplies weight row n0 + 16i + l%16, bytes 16*(l/16) of the step.
-    const uint32_t kw = kTaps * g.channels;  // weight row length
-    const uint32_t wrow0 = (nb * BN + wn * NW) * kw;
-    const uint32_t wlane = (lane & 15u) * kw + (lane >> 4) * 16u;
+    // ---- weight fragments (packed: one contiguous 1 KiB per fragment) -------
+    const uint32_t ksteps = kTaps * (g.channels / kCB);
+    const uint32_t wbase = ((nb * BN + wn * NW) / 16u) * ksteps * 1024u + lane * 16u;
     auto load_w = [&](v4i (&b)[NB], uint32_t step) {
         const uint32_t cb = step / kTaps, tap = step - cb * kTaps;
-        const uint32_t k0 = tap * g.channels + cb * kCB;
+        const uint32_t ks = tap * (g.channels / kCB) + cb;
 #pragma unroll
         for (int i = 0; i < NB; ++i)
-            b[i] = *reinterpret_cast<const v4i*>(g.w + ((wrow0 + i * 16u * kw + k0) + wlane));
+            b[i] = *reinterpret_cast<const v4i*>(g.w + (wbase + (i * ksteps + ks) * 1024u));
     };
 
     v4i acc[NB][PB];
@@ -432,74 +382,11 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(ConvParams g) {
         }
     }
 
-    // ---- epilogue: out[ch][pixel] = ((acc * s_pixel) * s_weight) + bias,
-    // then + residual (add.glsl) and max(., 0) (relu.glsl) when asked; the
-    // flag tests sit outside the unrolled store loops.
-    // Accumulator r of lane l in block (i, j): channel 16i + 4(l/16) + r,
-    // pixel 16j + l%16 of the wave's sub-tile.
-    // Channels of a group: 16-channel blocks i of this lane (rows
-    // 4(l/16) + r) and of lanes l^16, l^32, l^48.
-    constexpr int kEmitGroups = (NW % 32 == 0) ? NW / 32 : 0;
-    const bool emit_relu = (g.flags & DAV2_CONV_EMIT_RELU_MAX) != 0;
-    float gmax[PB][kEmitGroups > 0 ? kEmitGroups : 1];
-#pragma unroll
-    for (int j = 0; j < PB; ++j)
-#pragma unroll
-        for (int q = 0; q < (kEmitGroups > 0 ? kEmitGroups : 1); ++q) gmax[j][q] = 0.0f;
-    auto epilogue = [&](auto residual_tag, auto relu_tag) {
-        constexpr bool kResidual = decltype(residual_tag)::value, kRelu = decltype(relu_tag)::value;
-#pragma unroll
-        for (int j = 0; j < PB; ++j) {
-            const uint32_t p = wm * PW + 16u * j + (lane & 15u);
-            if (p >= valid) continue;
-            const float sp = sc_lds[p];
-#pragma unroll
-            for (int i = 0; i < NB; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t cl = wn * NW + 16u * i + 4u * (lane >> 4) + r;
-                    float v = static_cast<float>(acc[i][j][r]);
-                    v = v * sp;
-                    v = v * wsc_lds[cl];
-                    v = v + bias_lds[cl];
-                    const uint64_t idx = static_cast<uint64_t>(nb * BN + cl) * g.plane + mbase + p;
-                    if (kResidual) v = v + g.residual[idx];
-                    if (kRelu) v = fmaxf(v, 0.0f);
-                    g.out[idx] = v;
-                    // group maxima for the next convolution: group gi of the
-                    // wave's channels holds blocks i of 32 channels
-                    if constexpr (kEmitGroups > 0) {
-                        const float m = emit_relu ? fmaxf(v, 0.0f) : fabsf(v);
-                        gmax[j][(16 * i) / 32] = fmaxf(gmax[j][(16 * i) / 32], m);
-                    }
-                }
-        }
-    };
-    auto emit_groups = [&]() {
-        if constexpr (kEmitGroups > 0) {
-#pragma unroll
-            for (int j = 0; j < PB; ++j) {
-                const uint32_t p = wm * PW + 16u * j + (lane & 15u);
-#pragma unroll
-                for (int q = 0; q < kEmitGroups; ++q) {
-                    float m = gmax[j][q];
-                    m = fmaxf(m, __shfl_xor(m, 16, kWave));
-                    m = fmaxf(m, __shfl_xor(m, 32, kWave));
-                    const uint32_t group = (nb * BN + wn * NW) / 32u + q;
-                    if (lane < 16u && p < valid) g.emit[static_cast<uint64_t>(group) * g.plane + mbase + p] = m;
-                }
-            }
-        }
-    };
-    const bool relu_out = (g.flags & DAV2_CONV_RELU_OUTPUT) != 0;
-    if (g.residual) {
-        if (relu_out) epilogue(std::true_type{}, std::true_type{});
-        else epilogue(std::true_type{}, std::false_type{});
-    } else {
-        if (relu_out) epilogue(std::false_type{}, std::true_type{});
-        else epilogue(std::false_type{}, std::false_type{});
-    }
-    if (g.emit) emit_groups();
+    store_tile<BN, WM, WN, kPix>(g, acc, wm, wn, lane, nb, sc_lds, wsc_lds, bias_lds,
+                                 [&](uint32_t p, uint64_t& pixel) {
+                                     pixel = mbase + p;
+                                     return p < valid;
+                                 });
 }
 
 // 1x1 convolution to at most kNarrowN output channels: one thread per pixel
@@ -545,15 +432,21 @@ __global__ __launch_bounds__(256) void conv1x1_narrow_kernel(const float* __rest
     }
 }
 
-// dst[n][tap*C + c] = src[n][c*taps + tap].
-__global__ __launch_bounds__(256) void weights_tapmajor_kernel(int8_t* __restrict__ dst, const int8_t* __restrict__ src,
-                                                               uint32_t n, uint32_t channels, uint32_t taps,
-                                                               uint64_t ldb) {
+// Packed convolution weights (conv_common.h): dst byte
+// ((nb * ksteps + ks) * 64 + l) * 16 + b holds weight row 16 nb + l % 16 at
+// tap-major K index k = 64 ks + 16 (l / 16) + b (k = tap * C + c), which is
+// src[row][c * taps + tap].
+__global__ __launch_bounds__(256) void weights_pack_kernel(int8_t* __restrict__ dst, const int8_t* __restrict__ src,
+                                                           uint32_t n, uint32_t channels, uint32_t taps, uint64_t ldb) {
     const uint64_t row_len = static_cast<uint64_t>(taps) * channels;
     const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
     if (idx >= row_len * n) return;
-    const uint64_t row = idx / row_len;
-    const uint32_t k = static_cast<uint32_t>(idx - row * row_len);
+    const uint32_t ksteps = static_cast<uint32_t>(row_len / 64u);
+    const uint32_t b = static_cast<uint32_t>(idx & 15u), l = static_cast<uint32_t>((idx >> 4) & 63u);
+    const uint64_t frag = idx >> 10;
+    const uint32_t nb = static_cast<uint32_t>(frag / ksteps), ks = static_cast<uint32_t>(frag - uint64_t(nb) * ksteps);
+    const uint64_t row = uint64_t(nb) * 16u + (l & 15u);
+    const uint32_t k = ks * 64u + (l >> 4) * 16u + b;
     const uint32_t tap = k / channels, c = k - tap * channels;
     dst[idx] = src[row * ldb + static_cast<uint64_t>(c) * taps + tap];
 }
@@ -581,13 +474,15 @@ void launch_ks(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
 
 extern "C" {
 
-int dav2_hip_conv_weights_tapmajor(int8_t* dst, const int8_t* src, uint32_t out_channels, uint32_t channels,
-                                   uint32_t kernel, uint64_t ldb, void* stream) {
+int dav2_hip_conv_weights_pack(int8_t* dst, const int8_t* src, uint32_t out_channels, uint32_t channels,
+                               uint32_t kernel, uint64_t ldb, void* stream) {
     if (out_channels == 0) return hipSuccess;
     const uint64_t taps = static_cast<uint64_t>(kernel) * kernel;
-    if (!dst || !src || kernel == 0 || channels == 0 || ldb < taps * channels) return hipErrorInvalidValue;
+    if (!dst || !src || kernel == 0 || channels == 0 || ldb < taps * channels || out_channels % 16 != 0 ||
+        (taps * channels) % 64 != 0)
+        return hipErrorInvalidValue;
     const uint64_t total = taps * channels * out_channels;
-    hipLaunchKernelGGL(weights_tapmajor_kernel, dim3(ceil_div(total, 256)), dim3(256), 0,
+    hipLaunchKernelGGL(weights_pack_kernel, dim3(ceil_div(total, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), dst, src, out_channels, channels,
                        static_cast<uint32_t>(taps), ldb);
     return hipGetLastError();
@@ -620,8 +515,9 @@ int dav2_hip_conv2d_i8(const dav2_conv_i8_args* a, void* stream) {
     if (emit == (DAV2_CONV_EMIT_ABSMAX | DAV2_CONV_EMIT_RELU_MAX) ||
         (emit && (!a->partial_out || !dav2_hip_conv2d_i8_emits(a->out_channels, a->kernel))))
         return hipErrorInvalidValue;
-    // The kernel addresses input and weights with 32-bit byte offsets.
-    if (plane * a->channels * sizeof(float) >= (1ull << 32) ||
+    // The kernels address input and weights with 32-bit byte offsets; the
+    // 3x3 kernel's buffer offsets of one channel block stay below 2^31.
+    if (plane * a->channels * sizeof(float) >= (1ull << 32) || plane * kCB * sizeof(float) >= (1ull << 31) ||
         static_cast<uint64_t>(a->out_channels) * a->kernel * a->kernel * a->channels >= (1ull << 32))
         return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -641,14 +537,19 @@ int dav2_hip_conv2d_i8(const dav2_conv_i8_args* a, void* stream) {
     g.height = a->height;
     g.width = a->width;
     g.plane = plane;
-    g.tiles_x = ceil_div(a->width, kPix);
+    // 3x3: the two-row kernel needs an even width and an 8-byte aligned
+    // input (8-byte column-pair loads); other maps take conv_i8_kernel.
+    const bool two_row = a->kernel == 3 && a->width % 2 == 0 && reinterpret_cast<uintptr_t>(a->input) % 8 == 0;
+    g.tiles_x = two_row ? ceil_div(a->width, kTileCols3) : ceil_div(a->width, kPix);
     g.w = a->weight;
+    g.n_out = a->out_channels;
     g.w_scales = a->weight_scales;
     g.bias = a->bias;
     g.out = a->out;
     g.residual = a->residual;
     g.flags = a->flags;
     g.emit = emit ? a->partial_out : nullptr;
+    if (two_row) return launch_conv3x3_i8(g, g.tiles_x * ceil_div(a->height, 2), a->out_channels, s);
     if (a->kernel == 3) launch_ks<3>(g, g.tiles_x * a->height, a->out_channels, s);
     else launch_ks<1>(g, ceil_div(plane, kPix), a->out_channels, s);
     return hipGetLastError();

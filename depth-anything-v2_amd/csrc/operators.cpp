@@ -629,7 +629,7 @@ bool HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
                                const DeviceBuffer& weight_scales, const DeviceBuffer& bias,
                                std::uint32_t input_width, std::uint32_t input_height, std::uint32_t input_channels,
                                std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
-                               std::uint32_t padding, bool has_bias, const DeviceBuffer* tapmajor_weight,
+                               std::uint32_t padding, bool has_bias, const DeviceBuffer* packed_weight,
                                const ConvFusion& fusion) {
     if (input_width == 0 || input_height == 0 || input_channels == 0 || output_channels == 0 || kernel == 0 ||
         stride == 0 || input_width + 2u * padding < kernel || input_height + 2u * padding < kernel)
@@ -649,16 +649,16 @@ bool HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
     const std::uint64_t scratch_floats = dav2_hip_im2col_scratch_floats(input_width, input_height, input_channels);
     // Implicit GEMM: same bits as im2col + GEMM, no im2col matrix.
     if (implicit_conv(input_width, input_height, input_channels, output_channels, kernel, stride, padding)) {
-        const DeviceBuffer* tapmajor = tapmajor_weight;
-        if (!tapmajor || !*tapmajor) {
+        const DeviceBuffer* packed = packed_weight;
+        if (!packed || !*packed) {
             grow(conv_weights_, std::uint64_t(output_channels) * inner);
-            hip_check(dav2_hip_conv_weights_tapmajor(conv_weights_.as<int8_t>(), int8_weight.as<int8_t>(),
-                                                     output_channels, input_channels, kernel, ld64(inner), s),
-                      "tap-major conv weights");
-            tapmajor = &conv_weights_;
+            hip_check(dav2_hip_conv_weights_pack(conv_weights_.as<int8_t>(), int8_weight.as<int8_t>(),
+                                                 output_channels, input_channels, kernel, ld64(inner), s),
+                      "packed conv weights");
+            packed = &conv_weights_;
         } else {
-            if (tapmajor->size() < std::uint64_t(output_channels) * inner)
-                throw std::invalid_argument("tap-major convolution weight is too small");
+            if (packed->size() < std::uint64_t(output_channels) * inner)
+                throw std::invalid_argument("packed convolution weight is too small");
         }
         grow(im2col_scratch_, scratch_floats * sizeof(float));
         ProfileScope prof(context_.profiler(), "conv2d_i8", 2.0 * rows * output_channels * inner, "OP", s);
@@ -668,7 +668,7 @@ bool HipOperators::conv2d_int8(DeviceBuffer& output, const DeviceBuffer& input, 
         a.height = input_height;
         a.channels = input_channels;
         a.kernel = kernel;
-        a.weight = tapmajor->as<int8_t>();
+        a.weight = packed->as<int8_t>();
         a.weight_scales = weight_scales.as<float>();
         a.bias = has_bias ? bias.as<float>() : nullptr;
         a.out_channels = output_channels;

@@ -102,7 +102,7 @@ public:
                      const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t input_width,
                      std::uint32_t input_height, std::uint32_t input_channels, std::uint32_t output_channels,
                      std::uint32_t kernel, std::uint32_t stride, std::uint32_t padding, bool has_bias,
-                     const DeviceBuffer* tapmajor_weight = nullptr, const ConvFusion& fusion = ConvFusion{});
+                     const DeviceBuffer* packed_weight = nullptr, const ConvFusion& fusion = ConvFusion{});
 
     // 1x1 convolution to at most 4 output channels from at most 64 (the DPT
     // head's last layer); pre_relu, when given, receives the output before
@@ -232,7 +232,7 @@ private:
     const void* interpolated_position_ = nullptr;
     std::uint32_t interpolated_pw_ = 0, interpolated_ph_ = 0, interpolated_dim_ = 0;
     DeviceBuffer im2col_scratch_;  // per-channel-group maxima for the tiled im2col kernels
-    DeviceBuffer conv_weights_;    // tap-major weights of a conv2d_int8 call that brought none
+    DeviceBuffer conv_weights_;    // packed weights of a conv2d_int8 call that brought none
     DeviceBuffer conv_act_;        // ReLU of a conv2d_int8 input on the im2col path
     DeviceBuffer gemm_split_;      // int32 slices of split-K channel-major GEMMs
     DeviceBuffer f32_cols_;        // fp32 im2col rows of the fp32 convolutions

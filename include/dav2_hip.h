@@ -181,8 +181,12 @@ DAV2_API uint64_t dav2_hip_gemm_i8_split_scratch_bytes(uint32_t m, uint32_t n, u
  * (dav2_hip_conv2d_i8_supported). Same output bits as
  * dav2_hip_im2col_quantize_i8 followed by dav2_hip_gemm_i8 with
  * DAV2_GEMM_EPI_TRANSPOSED; the im2col matrix is never stored. The weights are
- * the GpuModel int8 rows permuted tap-major by dav2_hip_conv_weights_tapmajor:
- * dst[n][(ky*k + kx)*channels + c] = src[n][c*k*k + ky*k + kx]. */
+ * the GpuModel int8 rows packed by dav2_hip_conv_weights_pack: K walked
+ * tap-major (k = (ky*k + kx)*channels + c holds src[n][c*k*k + ky*k + kx])
+ * and cut into 16-row x 64-byte MFMA operand fragments, fragment (rows
+ * 16 nb.., K step ks) at byte (nb * K/64 + ks) * 1024, lane l's 16 bytes at
+ * + 16 l (row 16 nb + l % 16, K bytes 64 ks + 16 (l / 16) ..). Needs
+ * out_channels % 16 == 0 and kernel*kernel*channels % 64 == 0. */
 enum {
     DAV2_CONV_RELU_INPUT = 1,   /* convolve max(input, 0) (relu.glsl before the conv)  */
     DAV2_CONV_RELU_OUTPUT = 2,  /* out = max(out, 0) after the residual (relu.glsl)     */
@@ -199,7 +203,7 @@ typedef struct dav2_conv_i8_args {
     const float* input;          /* CHW [channels][height][width]                  */
     uint32_t width, height, channels;
     uint32_t kernel;             /* 1 or 3                                         */
-    const int8_t* weight;        /* [out_channels][kernel*kernel*channels], tap-major */
+    const int8_t* weight;        /* packed (dav2_hip_conv_weights_pack)            */
     const float* weight_scales;  /* [out_channels]                                 */
     const float* bias;           /* [out_channels] or NULL = 0                     */
     uint32_t out_channels;
@@ -222,7 +226,7 @@ DAV2_API int dav2_hip_conv2d_i8_supported(uint32_t width, uint32_t height, uint3
  * output's channel-group maxima (DAV2_CONV_EMIT_*). No reference
  * counterpart (a fusion of channel_group maxima into the producer). */
 DAV2_API int dav2_hip_conv2d_i8_emits(uint32_t out_channels, uint32_t kernel);
-DAV2_API int dav2_hip_conv_weights_tapmajor(int8_t* dst, const int8_t* src, uint32_t out_channels,
+DAV2_API int dav2_hip_conv_weights_pack(int8_t* dst, const int8_t* src, uint32_t out_channels,
                                             uint32_t channels, uint32_t kernel, uint64_t ldb,
                                             void* stream);
 DAV2_API int dav2_hip_conv2d_i8(const dav2_conv_i8_args* args, void* stream);

@@ -414,6 +414,18 @@ class Oracle:
         return depth, logits, feats
 
 
+def pack_conv_weights(q: np.ndarray, n: int, c: int, k: int) -> np.ndarray:
+    """int8 conv weights [n][c*k*k] (reference order: c major, then tap) ->
+    the implicit convolution's packed layout: K walked tap-major
+    (tap * c + ic), cut into 16-row x 64-byte fragments [n/16][K/64], each
+    stored lane by lane (lane l: row l % 16, K bytes 16 (l // 16) .. + 15)."""
+    taps = k * k
+    kk = taps * c
+    tm = q[:, :kk].reshape(n, c, taps).transpose(0, 2, 1).reshape(n, kk)
+    frags = tm.reshape(n // 16, 16, kk // 64, 4, 16).transpose(0, 2, 3, 1, 4)
+    return np.ascontiguousarray(frags).reshape(n, kk)
+
+
 def pad_rows(q: np.ndarray, ld: int | None = None) -> np.ndarray:
     """int8 [rows][K] -> [rows][ld] with zero padding (the GPU int8 layout)."""
     rows, k = q.shape

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from gpu_util import dev, empty, host, ok, ptr, stream
-from oracle_py import pad_rows
+from oracle_py import pack_conv_weights, pad_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -122,13 +122,18 @@ def test_im2col_quantize_relu_bit_exact(gpu, lib, oracle, c, h, w, k):
 # ---------------------------------------------------------------------------
 # implicit-GEMM convolution == im2col_quantize_int8.glsl + linear_int8_tiled.glsl
 # (CHW store), bit for bit. Shapes cover every channel-tile configuration the
-# launcher picks (256/128/64/32 output channels per workgroup), maps narrower
-# than one 64-pixel tile, one-row maps and 1x1 kernels.
+# launchers pick (256/128/64/32 output channels per workgroup), the two-row
+# 3x3 kernel (even widths: tiles of 60 columns, an odd height leaving a tile's
+# second row outside, one and three channel blocks) and the one-row kernel
+# (odd widths), maps narrower than one tile, one-row maps and 1x1 kernels.
 @pytest.mark.parametrize("c,h,w,n,k,has_bias", [(64, 37, 37, 256, 3, True), (128, 9, 150, 32, 3, True),
                                                 (256, 166, 180, 256, 3, True), (64, 100, 300, 128, 3, False),
                                                 (64, 250, 128, 64, 3, True), (64, 1, 5, 32, 3, True),
                                                 (192, 19, 19, 96, 3, True), (64, 37, 37, 96, 1, True),
-                                                (128, 100, 330, 128, 1, True), (128, 518, 518, 32, 3, True)])
+                                                (128, 100, 330, 128, 1, True), (128, 518, 518, 32, 3, True),
+                                                (192, 19, 20, 96, 3, True), (64, 3, 6, 32, 3, True),
+                                                (64, 7, 121, 64, 3, True), (256, 75, 74, 256, 3, True),
+                                                (128, 4, 62, 128, 3, False), (64, 1, 64, 256, 3, True)])
 def test_conv2d_i8_matches_im2col_gemm(gpu, pkg, lib, oracle, c, h, w, n, k, has_bias):
     torch = gpu
     _announce("conv2d_i8", c, h, w, n, k, has_bias)
@@ -157,11 +162,11 @@ def test_conv2d_i8_matches_im2col_gemm(gpu, pkg, lib, oracle, c, h, w, n, k, has
                       out_row_stride=rows)
     ok(lib, lib.dav2_hip_gemm_i8(C.byref(args), s))
 
-    # tap-major weights: dst[o][t*c + ic] = src[o][ic*k*k + t]
+    # packed weights: tap-major K (dst k = t*c + ic holds src[o][ic*k*k + t])
+    # in 16 x 64-byte MFMA operand fragments
     wt = empty(torch, (n, kk), torch.int8)
-    ok(lib, lib.dav2_hip_conv_weights_tapmajor(ptr(wt), ptr(wqd), n, c, k, ld, s))
-    want_wt = wq.reshape(n, c, k * k).transpose(0, 2, 1).reshape(n, kk)
-    assert np.array_equal(host(torch, wt), want_wt)
+    ok(lib, lib.dav2_hip_conv_weights_pack(ptr(wt), ptr(wqd), n, c, k, ld, s))
+    assert np.array_equal(host(torch, wt), pack_conv_weights(wq, n, c, k))
 
     out = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
     a = pkg.ConvArgs(input=ptr(xd), width=w, height=h, channels=c, kernel=k, weight=ptr(wt), weight_scales=ptr(wsd),
@@ -183,7 +188,7 @@ def test_conv2d_i8_matches_oracle(gpu, pkg, lib, oracle):
     wq, ws = oracle.quantize_weight_rows(rng.standard_normal((n, c * 9)).astype(np.float32) * 0.05)
     bias = rng.standard_normal(n).astype(np.float32)
     want = oracle.conv2d_int8(x, wq, ws, bias, n, 3, 1, 1).reshape(n, h * w)
-    wt = wq.reshape(n, c, 9).transpose(0, 2, 1).reshape(n, c * 9)
+    wt = pack_conv_weights(wq, n, c, 3)
     n_scratch = lib.dav2_hip_im2col_scratch_floats(w, h, c)
     scratch = empty(torch, (n_scratch,), torch.float32)
     xd, wtd, wsd, bd = dev(torch, x), dev(torch, wt), dev(torch, ws), dev(torch, bias)
@@ -205,7 +210,7 @@ def test_conv2d_i8_fusions(gpu, pkg, lib, oracle, flags, with_residual):
     x = rng.standard_normal((c, h, w)).astype(np.float32)
     res = rng.standard_normal((n, h * w)).astype(np.float32)
     wq, ws = oracle.quantize_weight_rows(rng.standard_normal((n, c * 9)).astype(np.float32) * 0.05)
-    wt = wq.reshape(n, c, 9).transpose(0, 2, 1).reshape(n, c * 9)
+    wt = pack_conv_weights(wq, n, c, 3)
     bias = rng.standard_normal(n).astype(np.float32)
     xd, wtd, wsd, bd, rd = dev(torch, x), dev(torch, wt), dev(torch, ws), dev(torch, bias), dev(torch, res)
     s = stream(torch)
@@ -251,7 +256,7 @@ def test_conv2d_i8_group_maxima(gpu, pkg, lib, oracle, k, n, relu_in, emit):
     rng = np.random.default_rng(k * n + emit)
     x = rng.standard_normal((c, h, w)).astype(np.float32)
     wq, ws = oracle.quantize_weight_rows(rng.standard_normal((n, c * k * k)).astype(np.float32) * 0.05)
-    wt = wq.reshape(n, c, k * k).transpose(0, 2, 1).reshape(n, c * k * k)
+    wt = pack_conv_weights(wq, n, c, k)
     bias = rng.standard_normal(n).astype(np.float32)
     xd, wtd, wsd, bd = dev(torch, x), dev(torch, wt), dev(torch, ws), dev(torch, bias)
     s = stream(torch)
