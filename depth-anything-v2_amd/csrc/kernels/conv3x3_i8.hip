@@ -123,6 +123,60 @@ __global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
     const uint32_t y0 = 2u * ty, x0 = (pt - ty * g.tiles_x) * kTileCols3;
     const int H = static_cast<int>(g.height), W = static_cast<int>(g.width);
 
+    // ---- input loads -------------------------------------------------------
+    const uint32_t cp = lane >> 1, half = lane & 1u;
+    // Byte offsets within a channel block of the lane's column pair in
+    // window rows 0..3 (its channel half included); the channel goes into
+    // the scalar offset. With an even width both columns of a pair lie in
+    // or out of the image together.
+    const uint32_t plane4 = static_cast<uint32_t>(g.plane) * 4u;
+    const int col = static_cast<int>(x0) - 2 + 2 * static_cast<int>(cp);
+    const bool col_ok = col >= 0 && col < W;
+    uint32_t voff[4];
+#pragma unroll
+    for (int wr = 0; wr < 4; ++wr) {
+        const int gy = static_cast<int>(y0) + wr - 1;
+        const bool ok = col_ok && gy >= 0 && gy < H;
+        voff[wr] = ok ? (half * 8u * static_cast<uint32_t>(g.plane) + static_cast<uint32_t>(gy) * g.width +
+                         static_cast<uint32_t>(col)) * 4u
+                      : kOutside;
+    }
+    auto block_rsrc = [&](uint32_t cb) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.x) + static_cast<uint64_t>(cb) * kCB * g.plane,
+                                                 static_cast<short>(0), static_cast<int>(kCB * plane4), 0x00020000);
+    };
+    v2f xv[4][8];
+    auto issue_row = [&](uint32_t cb, int wr) {
+        const auto rs = block_rsrc(cb);
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            xv[wr][c] = __builtin_bit_cast(
+                v2f, __builtin_amdgcn_raw_buffer_load_b64(rs, voff[wr], (wave * 16u + c) * plane4, 0));
+    };
+
+    // ---- packed weight fragments (conv_common.h) ---------------------------
+    const uint32_t cblocks = g.channels / kCB, ksteps = kTaps * cblocks;
+    const auto wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(g.w), static_cast<short>(0),
+                                                       static_cast<int>(g.n_out * ksteps * 64u), 0x00020000);
+    const uint32_t wvoff = ((nb * BN + wn * NW) / 16u) * ksteps * 1024u + lane * 16u;
+    auto load_w = [&](v4i (&b)[NB], uint32_t step) {
+        const uint32_t cb = step / kTaps, tap = step - cb * kTaps;
+        const uint32_t ks = tap * cblocks + cb;
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            b[i] = __builtin_bit_cast(v4i,
+                                      __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff, (i * ksteps + ks) * 1024u, 0));
+    };
+
+    const uint32_t nblocks = cblocks, nsteps = ksteps;
+    v4i ring[kRing][NB];
+    // Block 0's values and the first weight fragments are in flight while
+    // the scales are formed.
+#pragma unroll
+    for (int wr = 0; wr < 4; ++wr) issue_row(0, wr);
+#pragma unroll
+    for (int d = 0; d < kRing; ++d) load_w(ring[d], min(static_cast<uint32_t>(d), nsteps - 1));
+
     // ---- per-pixel scales: window maxima of the channel-group maxima -----
     // Thread t: window row t / 64 (image row y0 - 1 + t/64), window column
     // t % 64 (image column x0 - 2 + t%64); positions outside the image are
@@ -167,7 +221,6 @@ __global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
     lds_barrier();
     // This lane's window columns w = 2 cp + t serve pixel w - 1 - dx as tap
     // column dx; 1 / scale of each such pixel, exactly the quantizer's 1.0f / s.
-    const uint32_t cp = lane >> 1, half = lane & 1u;
     float inv[2][2][3];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -178,36 +231,6 @@ __global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
                 const int p = static_cast<int>(2u * cp) + t - 1 - dx;
                 inv[i][t][dx] = 1.0f / sc_lds[i * 64 + (p >= 0 ? p : 0)];
             }
-
-    // ---- input loads -------------------------------------------------------
-    // Byte offsets within a channel block of the lane's column pair in
-    // window rows 0..3 (its channel half included); the channel goes into
-    // the scalar offset. With an even width both columns of a pair lie in
-    // or out of the image together.
-    const uint32_t plane4 = static_cast<uint32_t>(g.plane) * 4u;
-    const int col = static_cast<int>(x0) - 2 + 2 * static_cast<int>(cp);
-    const bool col_ok = col >= 0 && col < W;
-    uint32_t voff[4];
-#pragma unroll
-    for (int wr = 0; wr < 4; ++wr) {
-        const int gy = static_cast<int>(y0) + wr - 1;
-        const bool ok = col_ok && gy >= 0 && gy < H;
-        voff[wr] = ok ? (half * 8u * static_cast<uint32_t>(g.plane) + static_cast<uint32_t>(gy) * g.width +
-                         static_cast<uint32_t>(col)) * 4u
-                      : kOutside;
-    }
-    auto block_rsrc = [&](uint32_t cb) {
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.x) + static_cast<uint64_t>(cb) * kCB * g.plane,
-                                                 static_cast<short>(0), static_cast<int>(kCB * plane4), 0x00020000);
-    };
-    v2f xv[4][8];
-    auto issue_row = [&](uint32_t cb, int wr) {
-        const auto rs = block_rsrc(cb);
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-            xv[wr][c] = __builtin_bit_cast(
-                v2f, __builtin_amdgcn_raw_buffer_load_b64(rs, voff[wr], (wave * 16u + c) * plane4, 0));
-    };
 
     // ---- quantizer ---------------------------------------------------------
     // Unit u (0..7) of tap t's share: piece 2t + u / 4, window column
@@ -237,34 +260,13 @@ __global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
         }
     };
 
-    // ---- packed weight fragments (conv_common.h) ---------------------------
-    const uint32_t cblocks = g.channels / kCB, ksteps = kTaps * cblocks;
-    const auto wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(g.w), static_cast<short>(0),
-                                                       static_cast<int>(g.n_out * ksteps * 64u), 0x00020000);
-    const uint32_t wvoff = ((nb * BN + wn * NW) / 16u) * ksteps * 1024u + lane * 16u;
-    auto load_w = [&](v4i (&b)[NB], uint32_t step) {
-        const uint32_t cb = step / kTaps, tap = step - cb * kTaps;
-        const uint32_t ks = tap * cblocks + cb;
-#pragma unroll
-        for (int i = 0; i < NB; ++i)
-            b[i] = __builtin_bit_cast(v4i,
-                                      __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff, (i * ksteps + ks) * 1024u, 0));
-    };
-
     v4i acc[NB][PB];
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
         for (int j = 0; j < PB; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-    const uint32_t nblocks = cblocks, nsteps = ksteps;
-    v4i ring[kRing][NB];
-    // Prologue: block 0's values and tile, the first weight fragments, block
-    // 1's values in flight.
-#pragma unroll
-    for (int wr = 0; wr < 4; ++wr) issue_row(0, wr);
-#pragma unroll
-    for (int d = 0; d < kRing; ++d) load_w(ring[d], min(static_cast<uint32_t>(d), nsteps - 1));
+    // Prologue: block 0's tile, block 1's values in flight.
 #pragma unroll
     for (int tap = 0; tap < kTaps; ++tap)
 #pragma unroll
