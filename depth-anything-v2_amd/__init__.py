@@ -120,7 +120,7 @@ class GemmF32Args(C.Structure):
                 ("bias", C.c_void_p), ("out", C.c_void_p), ("out_row_offset", C.c_uint64),
                 ("out_row_stride", C.c_uint64), ("residual", C.c_void_p), ("gamma", C.c_void_p),
                 ("convt_kernel", C.c_uint32), ("convt_width", C.c_uint32), ("convt_height", C.c_uint32),
-                ("convt_channels", C.c_uint32), ("relu_output", C.c_uint32)]
+                ("convt_channels", C.c_uint32), ("relu_output", C.c_uint32), ("half_operands", C.c_uint32)]
 
 
 class ConvArgs(C.Structure):
@@ -189,6 +189,7 @@ PROTOTYPES = {
     "dav2_hip_add_scaled": (C.c_int, [vp, vp, vp, vp, u64, u32, vp]),
     "dav2_hip_add": (C.c_int, [vp, vp, vp, u64, vp]),
     "dav2_hip_relu": (C.c_int, [vp, vp, u64, vp]),
+    "dav2_hip_round_half": (C.c_int, [vp, u64, vp]),
     "dav2_hip_attention_scores": (C.c_int, [vp, vp, u32, u32, u32, C.c_int, vp]),
     "dav2_hip_softmax_rows": (C.c_int, [vp, u64, u32, u32, C.c_int, vp]),
     "dav2_hip_attention_values": (C.c_int, [vp, vp, vp, u32, u32, u32, C.c_int, vp]),
@@ -209,6 +210,7 @@ PROTOTYPES = {
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),
     "dav2_hip_normalize_relative": (C.c_int, [vp, vp, u64, vp]),
     "dav2_hip_gemm_f32": (C.c_int, [C.c_void_p, vp]),
+    "dav2_hip_gemm_h16_products": (C.c_int, [C.c_void_p, vp]),
     "dav2_hip_im2col_f32": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, u32, vp, u32, vp]),
     "dav2_hip_preprocess_bgr8": (C.c_int, [vp, u32, u32, u64, u32, u32, vp, vp]),
     "dav2_hip_preprocess_bgra8_nearest": (C.c_int, [vp, u32, u32, u64, u32, u32, vp, vp]),

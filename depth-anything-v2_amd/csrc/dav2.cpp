@@ -142,10 +142,9 @@ dav2_status DAV2_CALL dav2_create(const char* model_path_utf8, const dav2_create
         return fail(DAV2_STATUS_INVALID_ARGUMENT, "multiple DAV2 execution precisions were requested");
     if (options->vulkan_device_index < 0) return fail(DAV2_STATUS_INVALID_ARGUMENT, "invalid device index");
     // This build executes the int8 operator path (the default) and the fp32
-    // precision mode (FORCE_FP32). FORCE_FP32_WEIGHTS is accepted and has no
-    // further effect, as in the reference (dav2.cpp:182 is its only use).
-    if (options->flags & DAV2_CREATE_FORCE_FP16)
-        return fail(DAV2_STATUS_UNSUPPORTED, "the FP16 execution precision is not built for MI355X");
+    // and fp16 precision modes (FORCE_FP32, FORCE_FP16). FORCE_FP32_WEIGHTS is
+    // accepted and has no further effect, as in the reference (dav2.cpp:182
+    // is its only use).
     if (options->flags & DAV2_CREATE_FORCE_METAL)
         return fail(DAV2_STATUS_UNSUPPORTED, "the Metal executor is not available on this platform");
     return protect([&] {

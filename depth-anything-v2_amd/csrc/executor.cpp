@@ -28,13 +28,20 @@ private:
 };
 
 AttentionMode attention_mode_for(std::uint32_t flags) {
-    // src/encoder.cpp:389-396: int8 mode runs the reference's binary16
-    // attention unless FORCE_FP32(_ATTENTION) asks for fp32 scores. Here the
-    // int8-mode default is the integer-exact fused attention; the reference's
-    // binary16 arithmetic is DAV2_CREATE_REFERENCE_FP16_ATTENTION.
+    // src/encoder.cpp:389-396: int8 and fp16 modes run the reference's
+    // binary16 attention unless FORCE_FP32(_ATTENTION) asks for fp32 scores.
+    // Here the int8-mode default is the integer-exact fused attention; the
+    // reference's binary16 arithmetic is DAV2_CREATE_REFERENCE_FP16_ATTENTION
+    // (and the fp16 mode's default).
     if (flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP32_ATTENTION)) return AttentionMode::fp32;
-    if (flags & DAV2_CREATE_REFERENCE_FP16_ATTENTION) return AttentionMode::binary16;
+    if (flags & (DAV2_CREATE_REFERENCE_FP16_ATTENTION | DAV2_CREATE_FORCE_FP16)) return AttentionMode::binary16;
     return AttentionMode::exact;
+}
+
+Precision precision_for(std::uint32_t flags) {
+    if (flags & DAV2_CREATE_FORCE_FP32) return Precision::fp32;
+    if (flags & DAV2_CREATE_FORCE_FP16) return Precision::fp16;
+    return Precision::int8;
 }
 }  // namespace
 
@@ -43,9 +50,9 @@ HipExecutor::HipExecutor(const std::string& model_path, dav2_encoder encoder, in
     : encoder_(encoder),
       model_(model_path, encoder),
       context_(device_index),
-      precision_((flags & DAV2_CREATE_FORCE_FP32) != 0 ? Precision::fp32 : Precision::int8),
+      precision_(precision_for(flags)),
       attention_mode_(attention_mode_for(flags)),
-      weights_(model_, context_, precision_ == Precision::fp32),
+      weights_(model_, context_, precision_),
       operators_(context_),
       side_operators_(context_),
       dino_(encoder, weights_, operators_, attention_mode_, precision_),

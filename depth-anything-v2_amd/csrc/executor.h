@@ -99,7 +99,7 @@ private:
     dav2_encoder encoder_;
     MappedModel model_;  // validated before any HIP call, as the reference's member order does
     HipContext context_;
-    Precision precision_;  // int8, or fp32 under FORCE_FP32
+    Precision precision_;  // int8, or fp32 / fp16 under FORCE_FP32 / FORCE_FP16
     AttentionMode attention_mode_;
     GpuModel weights_;
     HipOperators operators_;

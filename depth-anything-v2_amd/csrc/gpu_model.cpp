@@ -54,7 +54,9 @@ bool use_int8_weight(std::string_view name, const WeightRecord& t) {
     return (t.count / t.shape[0]) % 4 == 0;
 }
 
-GpuModel::GpuModel(const MappedModel& model, HipContext& context, bool fp32_weights) {
+GpuModel::GpuModel(const MappedModel& model, HipContext& context, Precision precision) {
+    const bool fp32_weights = precision != Precision::int8;
+    const bool half_weights = precision == Precision::fp16;
     tensors_.reserve(model.records().size());
     DeviceBuffer staging;
     std::vector<std::unique_ptr<std::vector<float>>> host_keepalive;
@@ -71,6 +73,8 @@ GpuModel::GpuModel(const MappedModel& model, HipContext& context, bool fp32_weig
         if (!use_int8_weight(name, src)) {
             dst.buffer = context.create_device_buffer(bytes);
             context.upload(dst.buffer, src.values, bytes);
+            if (half_weights && quantizable_family(name))
+                hip_check(dav2_hip_round_half(dst.buffer.as<float>(), src.count, stream), "half weights");
             device_bytes_ += bytes;
         } else {
             const bool convT = transposed_convolution_weight(name);
@@ -99,6 +103,8 @@ GpuModel::GpuModel(const MappedModel& model, HipContext& context, bool fp32_weig
                 dst.f32_columns = static_cast<std::uint32_t>(columns);
                 dst.buffer = context.create_device_buffer(bytes);
                 context.upload(dst.buffer, rows_source, bytes);  // host copies live until the final sync
+                if (half_weights)
+                    hip_check(dav2_hip_round_half(dst.buffer.as<float>(), src.count, stream), "half weights");
                 device_bytes_ += bytes;
                 if (!tensors_.emplace(std::string(name), std::move(dst)).second)
                     throw std::runtime_error("duplicate GPU tensor name: " + std::string(name));

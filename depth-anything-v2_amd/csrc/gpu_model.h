@@ -2,7 +2,9 @@
 // (reference src/gpu_model.cpp:127-146). Tensors the reference quantizes for
 // its int8 mode (selection rule: src/gpu_model.cpp:16-44) are stored only as
 // per-output-row int8 + fp32 scales (quantizer: src/gpu_model.cpp:241-264),
-// everything else as fp32. The fp32 precision mode keeps every tensor fp32.
+// everything else as fp32. The fp32 precision mode keeps every tensor fp32;
+// the fp16 mode keeps them fp32 too, with the reference's half-weight family
+// (src/gpu_model.cpp:15-33) rounded to binary16 values.
 //
 // int8 layout: [rows][ld] bytes, ld = columns rounded up to 64, zero padding.
 // Conv weights [OC][IC][k][k] flatten to rows = OC, column ic*k*k + ky*k + kx
@@ -11,6 +13,7 @@
 #pragma once
 
 #include "model.h"
+#include "operators.h"
 #include "runtime.h"
 
 #include <array>
@@ -48,8 +51,9 @@ inline std::uint32_t padded_k(std::uint64_t columns) { return static_cast<std::u
 
 class GpuModel {
 public:
-    // fp32_weights: the fp32 precision mode (no int8 copies).
-    GpuModel(const MappedModel& model, HipContext& context, bool fp32_weights = false);
+    // precision: int8 (int8 copies of the quantized family), fp32 or fp16
+    // (no int8 copies; fp16 rounds the half family to binary16).
+    GpuModel(const MappedModel& model, HipContext& context, Precision precision = Precision::int8);
     const GpuTensor& tensor(std::string_view name) const;
     bool contains(std::string_view name) const { return tensors_.count(std::string(name)) != 0; }
     std::size_t tensor_count() const { return tensors_.size(); }

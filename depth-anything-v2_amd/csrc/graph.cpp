@@ -51,7 +51,6 @@ DinoEncoder::DinoEncoder(dav2_encoder encoder, GpuModel& weights, HipOperators& 
                          AttentionMode attention, Precision precision)
     : config_(encoder_config(encoder)), weights_(weights), ops_(operators),
       attention_(attention), precision_(precision) {
-    if (precision_ == Precision::fp16) throw std::invalid_argument("the fp16 encoder is not part of this build");
     if (weights_.tensor("pretrained.cls_token").elements != config_.embedding ||
         weights_.tensor("pretrained.pos_embed").elements != std::uint64_t(1370) * config_.embedding)
         throw std::runtime_error("encoder tensor dimensions do not match");
@@ -74,7 +73,7 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
     DeviceBuffer& qkv = arena.get("enc.qkv", tok_bytes * 3);
     DeviceBuffer& attn = arena.get("enc.attention", tok_bytes);
     DeviceBuffer& hidden = arena.get("enc.hidden", tok_bytes * 4);
-    const bool f32 = precision_ == Precision::fp32;
+    const bool f32 = precision_ != Precision::int8;  // fp32 or fp16 mode: the float path
     const bool fused = !f32 && attention_ == AttentionMode::exact;
     const Precision materialised = attention_ == AttentionMode::binary16 ? Precision::fp16 : Precision::fp32;
     DeviceBuffer& scores =
@@ -98,7 +97,7 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
                                               std::uint64_t(T) * D * sizeof(float));
         ops_.prepare_tokens(out, img, patch.buffer, DeviceBuffer(), patch.int8_buffer, patch.int8_scales,
                             fp32("pretrained.patch_embed.proj.bias"), fp32("pretrained.cls_token"),
-                            fp32("pretrained.pos_embed"), width, height, D, f32 ? Precision::fp32 : Precision::int8,
+                            fp32("pretrained.pos_embed"), width, height, D, precision_,
                             /*position_is_constant=*/true);
     }
     if (f32) {
@@ -156,22 +155,33 @@ void DinoEncoder::forward_fp32(std::uint32_t rows, std::uint32_t T, std::uint32_
     // encoder.cpp:407-597 in the fp32 precision mode: LayerNorm rows in fp32,
     // fp32 GEMMs (GELU and the LayerScale residual in their epilogues, the
     // arithmetic of the reference's separate gelu / add_scaled passes),
-    // materialised fp32 attention.
+    // materialised fp32 attention. The fp16 mode (encoder.cpp:428-546): the
+    // same with the GEMM operands rounded to binary16 (layer_norm_fp16 and
+    // pack_fp16 produce binary16 inputs, fc1's output is stored as binary16
+    // and fc2 reads it) and the reference's binary16 attention, or its fp32
+    // attention under FORCE_FP32_ATTENTION, both in the shaders' order.
     const std::uint32_t D = config_.embedding, H = config_.heads;
+    const bool half = precision_ == Precision::fp16;
     DeviceBuffer& normed = arena.get("enc.normed", std::uint64_t(rows) * D * sizeof(float));
     using E = HipOperators::Epilogue;
     std::uint32_t capture = 0;
     for (std::uint32_t blk = 0; blk < config_.blocks; ++blk) {
         const auto W = [&](const char* s) -> const DeviceBuffer& { return weights_.tensor(block_name(blk, s)).buffer; };
         ops_.layer_norm(normed, current, W(".norm1.weight"), W(".norm1.bias"), rows, D, 1.0e-6f);
-        ops_.linear_f32(qkv, normed, W(".attn.qkv.weight"), &W(".attn.qkv.bias"), rows, D, 3 * D, E::row);
-        ops_.attention_mfma_f32(attn, qkv, T, H, batch, scores);
+        ops_.linear_f32(qkv, normed, W(".attn.qkv.weight"), &W(".attn.qkv.bias"), rows, D, 3 * D, E::row, nullptr, 0,
+                        half);
+        if (!half)
+            ops_.attention_mfma_f32(attn, qkv, T, H, batch, scores);
+        else
+            ops_.attention_batched(attn, qkv, T, H, batch, scores,
+                                   attention_ == AttentionMode::fp32 ? Precision::fp32 : Precision::fp16);
         ops_.linear_f32(current, attn, W(".attn.proj.weight"), &W(".attn.proj.bias"), rows, D, D, E::row_layerscale,
-                        &W(".ls1.gamma"));
+                        &W(".ls1.gamma"), 0, half);
         ops_.layer_norm(normed, current, W(".norm2.weight"), W(".norm2.bias"), rows, D, 1.0e-6f);
-        ops_.linear_f32(hidden, normed, W(".mlp.fc1.weight"), &W(".mlp.fc1.bias"), rows, D, 4 * D, E::row_gelu);
+        ops_.linear_f32(hidden, normed, W(".mlp.fc1.weight"), &W(".mlp.fc1.bias"), rows, D, 4 * D, E::row_gelu,
+                        nullptr, 0, half);
         ops_.linear_f32(current, hidden, W(".mlp.fc2.weight"), &W(".mlp.fc2.bias"), rows, 4 * D, D, E::row_layerscale,
-                        &W(".ls2.gamma"));
+                        &W(".ls2.gamma"), 0, half);
         if (capture < 4 && blk == config_.capture[capture]) {
             ops_.layer_norm(*features[capture], current, fp32("pretrained.norm.weight"), fp32("pretrained.norm.bias"),
                             rows, D, 1.0e-6f);
@@ -186,7 +196,6 @@ void DinoEncoder::forward_fp32(std::uint32_t rows, std::uint32_t T, std::uint32_
 DptHead::DptHead(dav2_encoder encoder, GpuModel& weights, HipOperators& operators, Precision precision)
     : config_(dpt_config(encoder)), weights_(weights), ops_(operators), zero_bias_(sizeof(float)),
       precision_(precision) {
-    if (precision_ == Precision::fp16) throw std::invalid_argument("the fp16 DPT head is not part of this build");
     hip_check(hipMemsetAsync(zero_bias_.data(), 0, sizeof(float), ops_.context().active_stream()), "zero bias");
 }
 
@@ -201,7 +210,9 @@ FeatureMap DptHead::conv(HipOperators& ops, const FeatureMap& in, const std::str
     out.buffer = &arena.get(slot + suffix_, out.elements() * sizeof(float));
     const GpuTensor& w = weights_.tensor(weight);
     const DeviceBuffer& b = has_bias ? weights_.tensor(bias).buffer : zero_bias_;
-    if (precision_ == Precision::fp32) {
+    if (precision_ != Precision::int8) {
+        // fp32, or fp16 through the reference's conv2d route with half
+        // weights (dpt.cpp:507-517): fp32 arithmetic on binary16 weights
         ops.conv2d(*out.buffer, *in.buffer, w.buffer, b, in.width, in.height, in.channels, oc, k, stride, pad, has_bias,
                    fusion);
         return out;
@@ -232,7 +243,7 @@ FeatureMap DptHead::resize(HipOperators& ops, const FeatureMap& in, std::uint32_
     FeatureMap out{&arena.get(slot + suffix_, std::uint64_t(ow) * oh * in.channels * sizeof(float)), ow, oh,
                    in.channels};
     const std::uint32_t pad = (consumer_kernel - 1) / 2;
-    if (precision_ != Precision::fp32 && in.channels % 32 == 0 &&
+    if (precision_ == Precision::int8 && in.channels % 32 == 0 &&
         HipOperators::implicit_conv(ow, oh, in.channels, consumer_channels, consumer_kernel, 1, pad)) {
         out.maxima = &arena.get(slot + suffix_ + ".max", std::uint64_t(in.channels / 32) * ow * oh * sizeof(float));
         ops.bilinear_align_true_maxima(*out.buffer, *out.maxima, *in.buffer, in.width, in.height, ow, oh, in.channels);
@@ -294,6 +305,9 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
     if (precision_ == Precision::fp32)
         ops.project_tokens(*proj.buffer, tokens, w.buffer, weights_.tensor(prefix + ".bias").buffer, pw, ph, D,
                            config_.project[i]);
+    else if (precision_ == Precision::fp16)
+        ops.project_tokens_fp16(*proj.buffer, tokens, w.buffer, weights_.tensor(prefix + ".bias").buffer, pw, ph, D,
+                                config_.project[i]);
     else
         ops.project_tokens_int8(*proj.buffer, tokens, w.int8_buffer, w.int8_scales,
                                 weights_.tensor(prefix + ".bias").buffer, pw, ph, D, config_.project[i]);
@@ -308,6 +322,10 @@ FeatureMap DptHead::prepare_level(std::uint32_t i, const DeviceBuffer& feature, 
         if (precision_ == Precision::fp32)
             ops.conv_transpose_nonoverlap(*layer.buffer, *proj.buffer, rw.buffer, weights_.tensor(r + ".bias").buffer,
                                           pw, ph, proj.channels, proj.channels, k);
+        else if (precision_ == Precision::fp16)
+            ops.conv_transpose_nonoverlap_fp16(*layer.buffer, *proj.buffer, rw.buffer,
+                                               weights_.tensor(r + ".bias").buffer, pw, ph, proj.channels,
+                                               proj.channels, k);
         else
             ops.conv_transpose_nonoverlap_int8(*layer.buffer, *proj.buffer, rw.int8_buffer, rw.int8_scales,
                                                weights_.tensor(r + ".bias").buffer, pw, ph, proj.channels,
@@ -363,7 +381,7 @@ void DptHead::refine_and_head(const FeatureMap refined[4], std::uint32_t b, std:
     DeviceBuffer logits;
     if (pre_relu) logits = DeviceBuffer::view(pre_relu, pixels * sizeof(float));
     const GpuTensor& w3 = weights_.tensor("depth_head.scratch.output_conv2.2.weight");
-    if (precision_ == Precision::fp32) {
+    if (precision_ != Precision::int8) {
         const DeviceBuffer& b3 = weights_.tensor("depth_head.scratch.output_conv2.2.bias").buffer;
         if (logits) {
             ops.conv2d(logits, *head.buffer, w3.buffer, b3, head.width, head.height, head.channels, 1, 1, 1, 0, true);

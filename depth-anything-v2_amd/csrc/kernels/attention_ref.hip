@@ -29,8 +29,6 @@ using namespace dav2k;
 
 namespace {
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
 constexpr int kQueryTile = 128;  // score tile: 128 queries x 64 keys
 constexpr int kKeyTile = 64;
 constexpr int kValueRows = 64;   // value tile: 64 queries x 64 features
@@ -48,14 +46,6 @@ DAV2_DEV uint32_t pack_half2(float lo, float hi) {
 DAV2_DEV float half_lo(uint32_t w) { return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w))); }
 DAV2_DEV float half_hi(uint32_t w) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
-}
-
-// s + float(fp16(a * b)) for two pairs: one binary16 multiplication of
-// each pair (v_pk_mul_f16), each product widened and added in fp32.
-DAV2_DEV void add_half_products(float& s0, float& s1, h2 a, h2 b) {
-    const h2 p = a * b;
-    s0 = s0 + static_cast<float>(p.x);
-    s1 = s1 + static_cast<float>(p.y);
 }
 
 // ---------------------------------------------------------------------------

@@ -65,6 +65,21 @@ DAV2_DEV float keep_fp32(float v) {
     return v;
 }
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// s + float(fp16(a * b)) for two pairs: one binary16 multiplication of each
+// pair (v_pk_mul_f16), each product widened and added in fp32 (the native
+// binary16 shaders' sum += float(x16 * y16); no contraction under
+// -ffp-contract=off).
+DAV2_DEV void add_half_products(float& s0, float& s1, h2 a, h2 b) {
+    const h2 p = a * b;
+    s0 = s0 + static_cast<float>(p.x);
+    s1 = s1 + static_cast<float>(p.y);
+}
+
+// The binary16 value nearest v (round to nearest even), as a float.
+DAV2_DEV float round_half(float v) { return static_cast<float>(static_cast<_Float16>(keep_fp32(v))); }
+
 inline unsigned ceil_div(uint64_t a, uint64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;

@@ -56,6 +56,14 @@ __global__ __launch_bounds__(kBlock) void add_kernel(float* out, const float* l,
     for (; i < n; i += stride) out[i] = l[i] + r[i];
 }
 
+// data[i] = the binary16 value nearest data[i] (round to nearest even), as a
+// float: the reference's float_to_half weight conversion (gpu_model.cpp:51-98).
+__global__ __launch_bounds__(kBlock) void round_half_kernel(float* data, uint64_t n) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        data[i] = round_half(data[i]);
+}
+
 __global__ __launch_bounds__(kBlock) void relu_kernel(float* out, const float* in, uint64_t n) {
     const uint64_t n4 = n / 4;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kBlock;
@@ -275,6 +283,14 @@ int dav2_hip_add(float* out, const float* left, const float* right, uint64_t cou
     if (!out || !left || !right) return hipErrorInvalidValue;
     hipLaunchKernelGGL(add_kernel, dim3(grid_for((count + 3) / 4)), dim3(kBlock), 0,
                        static_cast<hipStream_t>(stream), out, left, right, count);
+    return hipGetLastError();
+}
+
+int dav2_hip_round_half(float* data, uint64_t count, void* stream) {
+    if (count == 0) return hipSuccess;
+    if (!data) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(round_half_kernel, dim3(grid_for(count)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                       data, count);
     return hipGetLastError();
 }
 

@@ -1,6 +1,18 @@
-// fp32 path of the precision modes (DAV2_CREATE_FORCE_FP32): the linear and
-// convolution GEMMs in float32 on the MFMA (v_mfma_f32_16x16x4_f32), with the
-// epilogues of the int8 GEMM, and the fp32 im2col that feeds convolutions.
+// fp32 and fp16 paths of the precision modes (DAV2_CREATE_FORCE_FP32 /
+// FORCE_FP16): the linear and convolution GEMMs in float32 on the MFMA
+// (v_mfma_f32_16x16x4_f32), with the epilogues of the int8 GEMM, and the
+// fp32 im2col that feeds convolutions.
+//
+// fp16 arithmetic comes in the reference's two forms. Cooperative-matrix
+// linears (linear_coop_fp16.glsl via linear_fp16* with cooperative_matrix_fp16,
+// src/operators.cpp:540-768): operands rounded to binary16, exact products,
+// fp32 accumulation. The fp32 GEMM does this with half_operands: both tiles
+// are rounded to binary16 as they are staged, and the product of two binary16
+// values is exact in fp32. Native binary16 shaders (prepare_tokens_fp16,
+// project_tokens_fp16, conv_transpose_nonoverlap_fp16): every product is a
+// binary16 multiplication, widened and added to an fp32 sum in k order;
+// gemm_h16p_kernel does exactly that on the VALU, so its results match the
+// oracle bit for bit.
 //
 // Reference: linear_tiled.glsl / linear_vec*.glsl (src/operators.cpp:882-955),
 // conv2d (:1528-1676), conv_transpose_nonoverlap (:1807-1861),
@@ -38,6 +50,7 @@ struct F32Params {
     const float* gamma;
     uint32_t relu_output;
     uint32_t convt_k, convt_w, convt_h, convt_c;
+    uint32_t half_operands;  // round both operands to binary16 when staged
 };
 
 template <int EPI>
@@ -104,8 +117,13 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(F32Params g) {
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i;
             const int off = (idx >> 3) * kLdsRow + 4 * (idx & 7);
-            *reinterpret_cast<float4*>(&as[s][off]) = ra[i];
-            *reinterpret_cast<float4*>(&bs[s][off]) = rb[i];
+            float4 va = ra[i], vb = rb[i];
+            if (g.half_operands) {
+                va = make_float4(round_half(va.x), round_half(va.y), round_half(va.z), round_half(va.w));
+                vb = make_float4(round_half(vb.x), round_half(vb.y), round_half(vb.z), round_half(vb.w));
+            }
+            *reinterpret_cast<float4*>(&as[s][off]) = va;
+            *reinterpret_cast<float4*>(&bs[s][off]) = vb;
         }
     };
 
@@ -160,6 +178,79 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(F32Params g) {
         }
 }
 
+// Native binary16 products: out[m][n] = sum over k = 0, 1, .. K-1 of
+// float(fp16(h(a[m][k]) * h(b[n][k]))) in fp32, h = round to binary16, then
+// the epilogue (+ bias): prepare_tokens_fp16.glsl:37-52,
+// project_tokens_common.glsl (NATIVE_FP16) and
+// conv_transpose_nonoverlap_common.glsl (NATIVE_FP16), whose sums run over
+// the inner index in ascending order. Thread (tx, ty) of 16 x 16 owns rows
+// 4 ty .. +3 and columns 4 tx .. +3 of a 64 x 64 tile; K goes in chunks of
+// 32, staged k-major in LDS as binary16 values held in floats (exact).
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_h16p_kernel(F32Params g) {
+    __shared__ __attribute__((aligned(16))) float as[kBK][kBM + 4];
+    __shared__ __attribute__((aligned(16))) float bs[kBK][kBN + 4];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const uint32_t row0 = blockIdx.x * kBM, col0 = blockIdx.y * kBN;
+    float s[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[r][c] = 0.0f;
+    for (uint32_t k0 = 0; k0 < g.k; k0 += kBK) {
+        // float4 idx = tid + 256 i of each 64 x 32 operand tile: row idx / 8,
+        // k 4 (idx % 8) .. +3 (K is a multiple of 4)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i;
+            const uint32_t r = static_cast<uint32_t>(idx >> 3), kq = 4u * (idx & 7), kk = k0 + kq;
+            const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 va = row0 + r < g.m && kk < g.k
+                                  ? *reinterpret_cast<const float4*>(g.a + static_cast<uint64_t>(row0 + r) * g.lda + kk)
+                                  : zero;
+            const float4 vb = col0 + r < g.n && kk < g.k
+                                  ? *reinterpret_cast<const float4*>(g.b + static_cast<uint64_t>(col0 + r) * g.ldb + kk)
+                                  : zero;
+            as[kq + 0][r] = round_half(va.x);
+            as[kq + 1][r] = round_half(va.y);
+            as[kq + 2][r] = round_half(va.z);
+            as[kq + 3][r] = round_half(va.w);
+            bs[kq + 0][r] = round_half(vb.x);
+            bs[kq + 1][r] = round_half(vb.y);
+            bs[kq + 2][r] = round_half(vb.z);
+            bs[kq + 3][r] = round_half(vb.w);
+        }
+        __syncthreads();
+        const uint32_t kc = min(static_cast<uint32_t>(kBK), g.k - k0);  // no terms past K
+#pragma unroll 4
+        for (uint32_t k = 0; k < kc; ++k) {
+            const float4 av = *reinterpret_cast<const float4*>(&as[k][ty * 4]);
+            const float4 bv = *reinterpret_cast<const float4*>(&bs[k][tx * 4]);
+            const h2 b01 = {static_cast<_Float16>(bv.x), static_cast<_Float16>(bv.y)};
+            const h2 b23 = {static_cast<_Float16>(bv.z), static_cast<_Float16>(bv.w)};
+            const float a[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const _Float16 ah = static_cast<_Float16>(a[r]);
+                const h2 aa = {ah, ah};
+                add_half_products(s[r][0], s[r][1], aa, b01);
+                add_half_products(s[r][2], s[r][3], aa, b23);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t m = row0 + 4u * ty + r;
+        if (m >= g.m) continue;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t n = col0 + 4u * tx + c;
+            if (n < g.n) store_f32<EPI>(g, m, n, s[r][c]);
+        }
+    }
+}
+
 // out[p][c] = input[ic][iy][ix] of tap c = ic k^2 + ky k + kx of output pixel
 // p (zero outside the image, max(., 0) first with relu); columns K .. ld-1 zero.
 __global__ __launch_bounds__(256) void im2col_f32_kernel(const float* __restrict__ input, uint32_t width,
@@ -191,28 +282,31 @@ void launch(const F32Params& g, hipStream_t s) {
     hipLaunchKernelGGL(gemm_f32_kernel<EPI>, dim3(ceil_div(g.m, kBM), ceil_div(g.n, kBN)), dim3(256), 0, s, g);
 }
 
-}  // namespace
+template <int EPI>
+void launch_h16p(const F32Params& g, hipStream_t s) {
+    hipLaunchKernelGGL(gemm_h16p_kernel<EPI>, dim3(ceil_div(g.m, kBM), ceil_div(g.n, kBN)), dim3(256), 0, s, g);
+}
 
-extern "C" {
-
-int dav2_hip_gemm_f32(const dav2_gemm_f32_args* a, void* stream) {
+// Checks a dav2_gemm_f32_args and fills the kernel parameters; false if the
+// call is invalid.
+bool f32_params(const dav2_gemm_f32_args* a, F32Params& g) {
     if (!a || !a->a || !a->b || !a->out || a->m == 0 || a->n == 0 || a->k == 0 || a->k % 4u || a->lda < a->k ||
         a->ldb < a->k || a->lda % 4u || a->ldb % 4u || (reinterpret_cast<uintptr_t>(a->a) & 15u) ||
-        (reinterpret_cast<uintptr_t>(a->b) & 15u) || ceil_div(a->n, kBN) > 65535u)
-        return hipErrorInvalidValue;
+        (reinterpret_cast<uintptr_t>(a->b) & 15u) || ceil_div(a->n, kBN) > 65535u || a->half_operands > 1u)
+        return false;
     const uint32_t e = a->epilogue;
     if (e != DAV2_GEMM_EPI_ROW && e != DAV2_GEMM_EPI_ROW_GELU && e != DAV2_GEMM_EPI_ROW_LAYERSCALE &&
         e != DAV2_GEMM_EPI_TRANSPOSED && e != DAV2_GEMM_EPI_CONVT)
-        return hipErrorInvalidValue;
-    if (e == DAV2_GEMM_EPI_ROW_LAYERSCALE && (!a->residual || !a->gamma)) return hipErrorInvalidValue;
-    if (e == DAV2_GEMM_EPI_TRANSPOSED && a->out_row_stride < a->m + a->out_row_offset) return hipErrorInvalidValue;
+        return false;
+    if (e == DAV2_GEMM_EPI_ROW_LAYERSCALE && (!a->residual || !a->gamma)) return false;
+    if (e == DAV2_GEMM_EPI_TRANSPOSED && a->out_row_stride < a->m + a->out_row_offset) return false;
     if (e == DAV2_GEMM_EPI_CONVT &&
         (a->convt_kernel == 0 || a->convt_channels == 0 || a->n != a->convt_kernel * a->convt_kernel * a->convt_channels ||
          a->m != a->convt_width * a->convt_height))
-        return hipErrorInvalidValue;
+        return false;
     if ((a->relu_output || (a->residual && e != DAV2_GEMM_EPI_ROW_LAYERSCALE)) && e != DAV2_GEMM_EPI_TRANSPOSED)
-        return hipErrorInvalidValue;
-    F32Params g{};
+        return false;
+    g = F32Params{};
     g.a = a->a;
     g.lda = a->lda;
     g.b = a->b;
@@ -231,13 +325,40 @@ int dav2_hip_gemm_f32(const dav2_gemm_f32_args* a, void* stream) {
     g.convt_w = a->convt_width;
     g.convt_h = a->convt_height;
     g.convt_c = a->convt_channels;
+    g.half_operands = a->half_operands;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dav2_hip_gemm_f32(const dav2_gemm_f32_args* a, void* stream) {
+    F32Params g;
+    if (!f32_params(a, g)) return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    switch (e) {
+    switch (a->epilogue) {
         case DAV2_GEMM_EPI_ROW: launch<DAV2_GEMM_EPI_ROW>(g, s); break;
         case DAV2_GEMM_EPI_ROW_GELU: launch<DAV2_GEMM_EPI_ROW_GELU>(g, s); break;
         case DAV2_GEMM_EPI_ROW_LAYERSCALE: launch<DAV2_GEMM_EPI_ROW_LAYERSCALE>(g, s); break;
         case DAV2_GEMM_EPI_TRANSPOSED: launch<DAV2_GEMM_EPI_TRANSPOSED>(g, s); break;
         default: launch<DAV2_GEMM_EPI_CONVT>(g, s); break;
+    }
+    return hipGetLastError();
+}
+
+int dav2_hip_gemm_h16_products(const dav2_gemm_f32_args* a, void* stream) {
+    F32Params g;
+    if (!f32_params(a, g)) return hipErrorInvalidValue;
+    const uint32_t e = a->epilogue;
+    if ((e != DAV2_GEMM_EPI_ROW && e != DAV2_GEMM_EPI_TRANSPOSED && e != DAV2_GEMM_EPI_CONVT) || a->residual ||
+        a->relu_output)
+        return hipErrorInvalidValue;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (e) {
+        case DAV2_GEMM_EPI_ROW: launch_h16p<DAV2_GEMM_EPI_ROW>(g, s); break;
+        case DAV2_GEMM_EPI_TRANSPOSED: launch_h16p<DAV2_GEMM_EPI_TRANSPOSED>(g, s); break;
+        default: launch_h16p<DAV2_GEMM_EPI_CONVT>(g, s); break;
     }
     return hipGetLastError();
 }

@@ -375,7 +375,6 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
                                   Precision precision, bool position_is_constant) {
     if (input_width == 0 || input_height == 0 || input_width % 14 != 0 || input_height % 14 != 0 || embedding == 0)
         throw std::invalid_argument("invalid patch embedding dimensions");
-    if (precision == Precision::fp16) throw std::runtime_error("the fp16 patch embedding is not part of this build");
     const std::uint32_t pw = input_width / 14, ph = input_height / 14, spatial = pw * ph;
     const std::uint64_t tokens = std::uint64_t(spatial) + 1;
     constexpr std::uint32_t patch_columns = 3u * 14u * 14u;
@@ -407,13 +406,32 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
                            patch_columns, embedding, 1u, static_cast<std::uint32_t>(tokens), false, true);
         workspace_ld_ = ld;
     } else {
-        // fp32: im2col rows of the 14x14 patches, GEMM into token rows 1..
+        // fp32 / fp16: im2col rows of the 14x14 patches, GEMM into token rows
+        // 1.. (fp16: prepare_tokens_fp16.glsl's binary16 products)
         DeviceBuffer& cols = grow(f32_cols_, std::uint64_t(spatial) * patch_columns * sizeof(float));
         hip_check(dav2_hip_im2col_f32(image.as<float>(), input_width, input_height, 3, pw, ph, 14, 14, 0, 0,
                                       cols.as<float>(), patch_columns, s),
                   "patch im2col");
-        linear_f32(output, cols, patch_weight, &patch_bias, spatial, patch_columns, embedding, Epilogue::row, nullptr,
-                   1);
+        if (precision == Precision::fp16) {
+            dav2_gemm_f32_args a{};
+            a.a = cols.as<float>();
+            a.lda = patch_columns;
+            a.b = patch_weight.as<float>();
+            a.ldb = patch_columns;
+            a.m = spatial;
+            a.n = embedding;
+            a.k = patch_columns;
+            a.epilogue = DAV2_GEMM_EPI_ROW;
+            a.bias = patch_bias.as<float>();
+            a.out = output.as<float>();
+            a.out_row_offset = 1;
+            ProfileScope prof(context_.profiler(), "gemm_h16_products", 2.0 * spatial * embedding * patch_columns,
+                              "OP", s);
+            hip_check(dav2_hip_gemm_h16_products(&a, s), "fp16 patch embedding");
+        } else {
+            linear_f32(output, cols, patch_weight, &patch_bias, spatial, patch_columns, embedding, Epilogue::row,
+                       nullptr, 1);
+        }
     }
     const void* before = interpolated_.data();
     grow(interpolated_, std::uint64_t(spatial) * embedding * sizeof(float));
@@ -436,7 +454,7 @@ void HipOperators::prepare_tokens(DeviceBuffer& output, const DeviceBuffer& imag
 void HipOperators::linear_f32(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
                               const DeviceBuffer* bias, std::uint32_t rows, std::uint32_t input_columns,
                               std::uint32_t output_columns, Epilogue epilogue, const DeviceBuffer* gamma,
-                              std::uint64_t output_row_offset) {
+                              std::uint64_t output_row_offset, bool half_operands) {
     if (rows == 0 || input_columns == 0 || output_columns == 0)
         throw std::invalid_argument("linear dimensions cannot be zero");
     if (input_columns % 4u) throw std::invalid_argument("fp32 linear input columns must be a multiple of four");
@@ -456,6 +474,7 @@ void HipOperators::linear_f32(DeviceBuffer& output, const DeviceBuffer& input, c
     a.bias = bias ? bias->as<float>() : nullptr;
     a.out = output.as<float>();
     a.out_row_offset = output_row_offset;
+    a.half_operands = half_operands ? 1u : 0u;
     switch (epilogue) {
         case Epilogue::row_gelu: a.epilogue = DAV2_GEMM_EPI_ROW_GELU; break;
         case Epilogue::row_layerscale:
@@ -483,6 +502,19 @@ void HipOperators::linear(DeviceBuffer& output, const DeviceBuffer& input, const
 void HipOperators::project_tokens(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& weight,
                                   const DeviceBuffer& bias, std::uint32_t width, std::uint32_t height,
                                   std::uint32_t embedding, std::uint32_t output_channels) {
+    project_tokens_float(output, tokens, weight, bias, width, height, embedding, output_channels, false);
+}
+
+// src/operators.cpp:1453-1481 (project_tokens_fp16.glsl)
+void HipOperators::project_tokens_fp16(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& weight,
+                                       const DeviceBuffer& bias, std::uint32_t width, std::uint32_t height,
+                                       std::uint32_t embedding, std::uint32_t output_channels) {
+    project_tokens_float(output, tokens, weight, bias, width, height, embedding, output_channels, true);
+}
+
+void HipOperators::project_tokens_float(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& weight,
+                                        const DeviceBuffer& bias, std::uint32_t width, std::uint32_t height,
+                                        std::uint32_t embedding, std::uint32_t output_channels, bool half_products) {
     const std::uint32_t spatial = width * height;
     if (width == 0 || height == 0 || embedding == 0 || output_channels == 0)
         throw std::invalid_argument("invalid token projection dimensions");
@@ -503,8 +535,10 @@ void HipOperators::project_tokens(DeviceBuffer& output, const DeviceBuffer& toke
     a.bias = bias.as<float>();
     a.out = output.as<float>();
     a.out_row_stride = spatial;
-    ProfileScope prof(context_.profiler(), "gemm_f32", 2.0 * spatial * output_channels * embedding, "OP", stream());
-    hip_check(dav2_hip_gemm_f32(&a, stream()), "fp32 token projection");
+    ProfileScope prof(context_.profiler(), half_products ? "gemm_h16_products" : "gemm_f32",
+                      2.0 * spatial * output_channels * embedding, "OP", stream());
+    hip_check(half_products ? dav2_hip_gemm_h16_products(&a, stream()) : dav2_hip_gemm_f32(&a, stream()),
+              "token projection");
 }
 
 // src/operators.cpp:1528-1676: im2col + GEMM, CHW output; fusion as conv2d_int8
@@ -557,6 +591,24 @@ void HipOperators::conv_transpose_nonoverlap(DeviceBuffer& output, const DeviceB
                                              std::uint32_t input_width, std::uint32_t input_height,
                                              std::uint32_t input_channels, std::uint32_t output_channels,
                                              std::uint32_t kernel) {
+    conv_transpose_float(output, input, weight, bias, input_width, input_height, input_channels, output_channels,
+                         kernel, false);
+}
+
+// src/operators.cpp:1862-1906 (conv_transpose_nonoverlap_fp16.glsl)
+void HipOperators::conv_transpose_nonoverlap_fp16(DeviceBuffer& output, const DeviceBuffer& input,
+                                                  const DeviceBuffer& weight, const DeviceBuffer& bias,
+                                                  std::uint32_t input_width, std::uint32_t input_height,
+                                                  std::uint32_t input_channels, std::uint32_t output_channels,
+                                                  std::uint32_t kernel) {
+    conv_transpose_float(output, input, weight, bias, input_width, input_height, input_channels, output_channels,
+                         kernel, true);
+}
+
+void HipOperators::conv_transpose_float(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                                        const DeviceBuffer& bias, std::uint32_t input_width,
+                                        std::uint32_t input_height, std::uint32_t input_channels,
+                                        std::uint32_t output_channels, std::uint32_t kernel, bool half_products) {
     if (input_width == 0 || input_height == 0 || input_channels == 0 || output_channels == 0 || kernel == 0)
         throw std::invalid_argument("invalid transposed convolution dimensions");
     if (input_channels % 4u) throw std::invalid_argument("fp32 transposed convolution channels must be a multiple of four");
@@ -586,8 +638,10 @@ void HipOperators::conv_transpose_nonoverlap(DeviceBuffer& output, const DeviceB
     a.convt_width = input_width;
     a.convt_height = input_height;
     a.convt_channels = output_channels;
-    ProfileScope prof(context_.profiler(), "gemm_f32", 2.0 * pixels * wrows * input_channels, "OP", s);
-    hip_check(dav2_hip_gemm_f32(&a, s), "fp32 transposed convolution");
+    ProfileScope prof(context_.profiler(), half_products ? "gemm_h16_products" : "gemm_f32",
+                      2.0 * pixels * wrows * input_channels, "OP", s);
+    hip_check(half_products ? dav2_hip_gemm_h16_products(&a, s) : dav2_hip_gemm_f32(&a, s),
+              "transposed convolution");
 }
 
 // src/operators.cpp:1483-1526

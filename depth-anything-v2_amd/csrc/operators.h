@@ -7,8 +7,10 @@
 // context's active stream. DeviceBuffer replaces VulkanBuffer; the int8 weight
 // buffers are the GpuModel layout ([rows][ld] bytes, ld = K rounded up to 64).
 // The fp32 variants (linear, project_tokens, conv2d, conv_transpose_nonoverlap,
-// prepare_tokens with Precision::fp32) serve the fp32 precision mode; fp16
-// variants are not part of this build.
+// prepare_tokens with Precision::fp32) serve the fp32 precision mode; the fp16
+// mode uses them with binary16-rounded weights, plus project_tokens_fp16,
+// conv_transpose_nonoverlap_fp16, prepare_tokens with Precision::fp16 (native
+// binary16 products) and linear_f32 with half operands.
 //
 // Fused variants (no reference counterpart) serve the encoder/DPT drivers:
 // they compute the same arithmetic as the reference's separate passes.
@@ -136,6 +138,26 @@ public:
                                    const DeviceBuffer& bias, std::uint32_t input_width, std::uint32_t input_height,
                                    std::uint32_t input_channels, std::uint32_t output_channels, std::uint32_t kernel);
 
+    // ---- fp16 precision mode (native binary16 products, k-order fp32 sums) --
+    // (the float variants behind project_tokens / conv_transpose_nonoverlap
+    // and their fp16 forms)
+    void project_tokens_float(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& weight,
+                              const DeviceBuffer& bias, std::uint32_t width, std::uint32_t height,
+                              std::uint32_t embedding, std::uint32_t output_channels, bool half_products);
+    void conv_transpose_float(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                              const DeviceBuffer& bias, std::uint32_t input_width, std::uint32_t input_height,
+                              std::uint32_t input_channels, std::uint32_t output_channels, std::uint32_t kernel,
+                              bool half_products);
+    // Weights as the fp32 variants take them (binary16 values or not: they
+    // are rounded to binary16 when staged).
+    void project_tokens_fp16(DeviceBuffer& output, const DeviceBuffer& tokens, const DeviceBuffer& weight,
+                             const DeviceBuffer& bias, std::uint32_t width, std::uint32_t height,
+                             std::uint32_t embedding, std::uint32_t output_channels);
+    void conv_transpose_nonoverlap_fp16(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
+                                        const DeviceBuffer& bias, std::uint32_t input_width,
+                                        std::uint32_t input_height, std::uint32_t input_channels,
+                                        std::uint32_t output_channels, std::uint32_t kernel);
+
     void bilinear_align_true(DeviceBuffer& output, const DeviceBuffer& input, std::uint32_t input_width,
                              std::uint32_t input_height, std::uint32_t output_width, std::uint32_t output_height,
                              std::uint32_t channels);
@@ -180,11 +202,12 @@ public:
                                   DeviceBuffer* col_absmax = nullptr, std::uint32_t col_absmax_begin = 0);
     static std::uint32_t gemm_row_tiles(std::uint32_t rows, std::uint32_t output_columns);
     // fp32 GEMM with the row epilogues (row_colmax excluded), for the fp32
-    // precision mode's encoder.
+    // precision mode's encoder; half_operands: both operands rounded to
+    // binary16 first (the fp16 mode's cooperative-matrix linears).
     void linear_f32(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& weight,
                     const DeviceBuffer* bias, std::uint32_t rows, std::uint32_t input_columns,
                     std::uint32_t output_columns, Epilogue epilogue, const DeviceBuffer* gamma = nullptr,
-                    std::uint64_t output_row_offset = 0);
+                    std::uint64_t output_row_offset = 0, bool half_operands = false);
     // Batched attention over `batch` token matrices of `tokens` rows each, in
     // the reference shaders' arithmetic order (fp32: bmm.glsl /
     // softmax_lastdim.glsl; fp16: the binary16 shaders), VALU kernels.

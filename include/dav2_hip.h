@@ -157,8 +157,19 @@ typedef struct dav2_gemm_f32_args {
     const float* gamma;
     uint32_t convt_kernel, convt_width, convt_height, convt_channels;
     uint32_t relu_output;   /* TRANSPOSED only                                 */
+    /* 1: both operands rounded to binary16 before the (exact) products, fp32
+     * accumulation: the fp16 mode's cooperative-matrix linears
+     * (linear_coop_fp16.glsl, src/operators.cpp:540-768). 0: fp32. */
+    uint32_t half_operands;
 } dav2_gemm_f32_args;
 DAV2_API int dav2_hip_gemm_f32(const dav2_gemm_f32_args* args, void* stream);
+/* Native binary16 products: out = sum over k ascending of
+ * float(fp16(h(a) * h(b))) in fp32 (h = round to binary16), then the ROW,
+ * TRANSPOSED or CONVT epilogue (+ bias; no residual / ReLU). Replaces the
+ * dot products of prepare_tokens_fp16.glsl:37-52, project_tokens_fp16.glsl
+ * and conv_transpose_nonoverlap_fp16.glsl (src/operators.cpp:1211-1406,
+ * :1453-1481, :1862-1906); the same bits as the CPU oracle. */
+DAV2_API int dav2_hip_gemm_h16_products(const dav2_gemm_f32_args* args, void* stream);
 
 /* fp32 im2col of conv2d (src/operators.cpp:1528-1676): out[p][c], p = oy*OW
  * + ox, c = ic*k*k + ky*k + kx, zero padding, columns C*k*k .. ld-1 zero;
@@ -251,6 +262,10 @@ DAV2_API int dav2_hip_add_scaled(float* out, const float* residual, const float*
 DAV2_API int dav2_hip_add(float* out, const float* left, const float* right, uint64_t count,
                           void* stream);
 DAV2_API int dav2_hip_relu(float* out, const float* input, uint64_t count, void* stream);
+/* Each float replaced by the nearest binary16 value (round to nearest even),
+ * kept as a float: the fp16 mode's half weights, the reference's float_to_half
+ * (src/gpu_model.cpp:51-98) applied on the device. */
+DAV2_API int dav2_hip_round_half(float* data, uint64_t count, void* stream);
 
 /* fp32 attention, head_dim 64, on the matrix cores (the fp32 precision
  * mode's path; src/operators.cpp:1169-1208 with bmm.glsl and

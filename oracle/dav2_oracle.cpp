@@ -229,7 +229,8 @@ struct orc_model {
     uint32_t capture[4] = {0, 0, 0, 0};
     uint32_t project[4] = {0, 0, 0, 0};
     std::unordered_map<std::string, Tensor> tensors;
-    bool fp32 = false;  // graph precision of the current inference (fp32 mode vs int8)
+    bool fp32 = false;  // graph precision of the current inference: fp32 mode,
+    bool fp16 = false;  // fp16 mode, or (neither) int8
 
     const Tensor& t(const std::string& name) const {
         auto it = tensors.find(name);
@@ -1218,6 +1219,125 @@ void orc_prepare_tokens_f32(const float* image, const float* weight, const float
 }
 
 // ---------------------------------------------------------------------------
+// fp16 precision mode (DAV2_CREATE_FORCE_FP16). Weights are the reference's
+// half buffers: every use_half_weight tensor rounded to binary16
+// (gpu_model.cpp:51-98, round to nearest even; f2h is that conversion).
+// Two kinds of arithmetic, as in the reference:
+// - cooperative-matrix linears (linear_coop_fp16.glsl, reached through
+//   linear_fp16* when the device has fp16 cooperative matrices,
+//   operators.cpp:540-768): operands rounded to binary16, exact products,
+//   fp32 sums (here in k order; a matrix unit's order is its own);
+// - native binary16 shaders (prepare_tokens_fp16.glsl:37-52,
+//   project_tokens_common.glsl and conv_transpose_nonoverlap_common.glsl
+//   with NATIVE_FP16): sum += float(x16 * w16) in k order, every product a
+//   binary16 multiplication.
+
+namespace {
+// fp16(h(a) * h(b)) widened: the product of two binary16 values is exact in
+// fp32, so rounding it once gives the binary16 multiplication.
+inline float half_product(float a, float b) { return round_half(round_half(a) * round_half(b)); }
+
+std::vector<float> rounded_half(const float* v, size_t count) {
+    std::vector<float> out(count);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) out[i] = round_half(v[i]);
+    return out;
+}
+}  // namespace
+
+void orc_gemm_h16_products(const float* a, uint64_t lda, const float* b, uint64_t ldb, uint32_t m, uint32_t n,
+                           uint32_t k, float* out) {
+    // out[i][j] = sum over kk ascending of float(h(a[i][kk]) * h(b[j][kk])), fp32
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(m); ++i)
+        for (uint32_t j = 0; j < n; ++j) {
+            const float* ai = a + static_cast<size_t>(i) * lda;
+            const float* bj = b + static_cast<size_t>(j) * ldb;
+            float sum = 0.0f;
+            for (uint32_t kk = 0; kk < k; ++kk) sum = sum + half_product(ai[kk], bj[kk]);
+            out[static_cast<size_t>(i) * n + j] = sum;
+        }
+}
+
+void orc_linear_f16(const float* input, const float* weight, const float* bias, uint32_t rows, uint32_t in_cols,
+                    uint32_t out_cols, int gelu, int half_output, float* out) {
+    // linear_coop_common.glsl: coopMatMulAdd of binary16 tiles into fp32,
+    // + bias, exact_gelu when fused, float16_t output with HALF_OUTPUT
+    const std::vector<float> x = rounded_half(input, static_cast<size_t>(rows) * in_cols);
+    const std::vector<float> w = rounded_half(weight, static_cast<size_t>(out_cols) * in_cols);
+    gemm_f32(x.data(), in_cols, w.data(), rows, out_cols, in_cols, out);
+    const size_t count = static_cast<size_t>(rows) * out_cols;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) {
+        float v = out[i] + (bias ? bias[static_cast<size_t>(i) % out_cols] : 0.0f);
+        if (gelu) v = gelu_value(v);
+        out[i] = half_output ? round_half(v) : v;
+    }
+}
+
+void orc_project_tokens_f16(const float* tokens, const float* weight, const float* bias, uint32_t width,
+                            uint32_t height, uint32_t D, uint32_t C, float* out) {
+    // project_tokens_common.glsl (NATIVE_FP16), operators.cpp:1453-1481: CLS
+    // skipped, channel-major output, sums + bias
+    const uint32_t spatial = width * height;
+    std::vector<float> acc(static_cast<size_t>(spatial) * C);
+    orc_gemm_h16_products(tokens + D, D, weight, D, spatial, C, D, acc.data());
+#pragma omp parallel for schedule(static)
+    for (int64_t c = 0; c < static_cast<int64_t>(C); ++c)
+        for (uint32_t p = 0; p < spatial; ++p)
+            out[static_cast<size_t>(c) * spatial + p] = acc[static_cast<size_t>(p) * C + c] + bias[c];
+}
+
+void orc_conv_transpose_f16(const float* input, const float* weight, const float* bias, uint32_t width,
+                            uint32_t height, uint32_t ic, uint32_t oc, uint32_t kernel, float* out) {
+    // conv_transpose_nonoverlap_common.glsl (NATIVE_FP16), operators.cpp:1862-1906:
+    // weight [IC][OC][k][k], one source pixel per output pixel, sum over the
+    // input channels in order, + bias
+    const uint32_t ow = width * kernel, oh = height * kernel;
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t o = 0; o < oc; ++o)
+        for (int64_t oy = 0; oy < oh; ++oy)
+            for (uint32_t ox = 0; ox < ow; ++ox) {
+                const uint32_t iy = static_cast<uint32_t>(oy) / kernel, ky = static_cast<uint32_t>(oy) % kernel;
+                const uint32_t ix = ox / kernel, kx = ox % kernel;
+                float sum = 0.0f;
+                for (uint32_t c = 0; c < ic; ++c)
+                    sum = sum + half_product(input[(static_cast<size_t>(c) * height + iy) * width + ix],
+                                             weight[((static_cast<size_t>(c) * oc + o) * kernel + ky) * kernel + kx]);
+                out[(static_cast<size_t>(o) * oh + oy) * ow + ox] = sum + bias[o];
+            }
+}
+
+void orc_prepare_tokens_f16(const float* image, const float* weight, const float* bias, const float* class_token,
+                            const float* position, uint32_t width, uint32_t height, uint32_t D, float* tokens) {
+    // prepare_tokens_fp16.glsl:37-52 (sum over channel, ky, kx of binary16
+    // products, + bias; the class token in row 0), then the position
+    // embedding as in the other precisions (operators.cpp:1322-1405)
+    const uint32_t pw = width / 14, ph = height / 14, spatial = pw * ph;
+    constexpr uint32_t K = 3 * 14 * 14;
+    std::vector<float> cols(static_cast<size_t>(spatial) * K);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < static_cast<int64_t>(spatial); ++r)
+        for (uint32_t c = 0; c < K; ++c)
+            cols[static_cast<size_t>(r) * K + c] =
+                im2col_read(image, width, height, pw, 14, 14, 0, static_cast<uint32_t>(r), c);
+    std::vector<float> acc(static_cast<size_t>(spatial) * D);
+    orc_gemm_h16_products(cols.data(), K, weight, K, spatial, D, K, acc.data());
+    std::memcpy(tokens, class_token, D * sizeof(float));
+    for (uint32_t p = 0; p < spatial; ++p)
+        for (uint32_t d = 0; d < D; ++d)
+            tokens[static_cast<size_t>(p + 1) * D + d] = acc[static_cast<size_t>(p) * D + d] + bias[d];
+    std::vector<float> interp(static_cast<size_t>(spatial) * D);
+    orc_position_bicubic(position, pw, ph, D, interp.data());
+    const size_t count = static_cast<size_t>(spatial + 1) * D;
+    for (size_t i = 0; i < count; ++i) {
+        const size_t token = i / D, feature = i % D;
+        const float p = token == 0 ? position[feature] : interp[feature * spatial + (token - 1)];
+        tokens[i] = tokens[i] + p;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Model
 
 static bool use_int8_weight(const std::string& name, const Tensor& t) {
@@ -1318,7 +1438,12 @@ void encoder_block(const orc_model& m, std::vector<float>& cur, uint32_t T, uint
     auto lin = [&](const std::vector<float>& in, const std::string& w, const std::string& bias,
                    uint32_t ic, uint32_t oc, bool gelu, std::vector<float>& out) {
         const Tensor& wt = m.t(w);
-        if (m.fp32)
+        if (m.fp16)
+            // encoder.cpp:428-546: layer_norm_fp16 / pack_fp16 inputs (the
+            // rounding is the operand rounding), fc1 with a half output
+            orc_linear_f16(in.data(), wt.data.data(), m.t(bias).data.data(), T, ic, oc, gelu, gelu ? 1 : 0,
+                           out.data());
+        else if (m.fp32)
             orc_linear_f32(in.data(), wt.data.data(), m.t(bias).data.data(), T, ic, oc, gelu, out.data());
         else
             orc_linear_int8(in.data(), wt.q.data(), wt.qscale.data(), m.t(bias).data.data(), T, ic, oc, gelu,
@@ -1352,6 +1477,14 @@ Map conv(const orc_model& m, const Map& in, const std::string& w, const std::str
     const Tensor& wt = m.t(w);
     if (m.fp32) {
         orc_conv2d_f32(in.v.data(), wt.data.data(), has_bias ? m.t(b).data.data() : nullptr, in.w, in.h, in.c, oc, k,
+                       stride, pad, has_bias ? 1 : 0, out.v.data());
+        return out;
+    }
+    if (m.fp16) {
+        // dpt.cpp:507-517, the conv2d route with the half weights: fp32
+        // input, products and sums (conv2d_common.glsl without NATIVE_FP16)
+        const std::vector<float> w16 = rounded_half(wt.data.data(), wt.data.size());
+        orc_conv2d_f32(in.v.data(), w16.data(), has_bias ? m.t(b).data.data() : nullptr, in.w, in.h, in.c, oc, k,
                        stride, pad, has_bias ? 1 : 0, out.v.data());
         return out;
     }
@@ -1410,6 +1543,16 @@ int orc_model_infer_fp32(orc_model* model, const float* chw, uint32_t width, uin
     return rc;
 }
 
+int orc_model_infer_fp16(orc_model* model, const float* chw, uint32_t width, uint32_t height, int attention_mode,
+                         float* depth, float* pre_relu, float* features) {
+    // FORCE_FP16: half weights, binary16 attention (encoder.cpp:389-403;
+    // attention_mode 0 with FORCE_FP32_ATTENTION)
+    model->fp16 = true;
+    const int rc = orc_model_infer(model, chw, width, height, attention_mode, depth, pre_relu, features);
+    model->fp16 = false;
+    return rc;
+}
+
 int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t height,
                     int attention_mode, float* depth, float* pre_relu, float* features) {
     try {
@@ -1418,7 +1561,11 @@ int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t
         const size_t n = static_cast<size_t>(T) * D;
         std::vector<float> cur(n);
         const Tensor& pe = m.t("pretrained.patch_embed.proj.weight");
-        if (m.fp32)
+        if (m.fp16)
+            orc_prepare_tokens_f16(chw, pe.data.data(), m.t("pretrained.patch_embed.proj.bias").data.data(),
+                                   m.t("pretrained.cls_token").data.data(), m.t("pretrained.pos_embed").data.data(),
+                                   width, height, D, cur.data());
+        else if (m.fp32)
             orc_prepare_tokens_f32(chw, pe.data.data(), m.t("pretrained.patch_embed.proj.bias").data.data(),
                                    m.t("pretrained.cls_token").data.data(), m.t("pretrained.pos_embed").data.data(),
                                    width, height, D, cur.data());
@@ -1448,7 +1595,10 @@ int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t
             proj.w = pw; proj.h = ph; proj.c = m.project[i];
             proj.v.resize(static_cast<size_t>(pw) * ph * proj.c);
             const Tensor& wt = m.t(prefix + ".weight");
-            if (m.fp32)
+            if (m.fp16)
+                orc_project_tokens_f16(feats[i].data(), wt.data.data(), m.t(prefix + ".bias").data.data(), pw, ph, D,
+                                       proj.c, proj.v.data());
+            else if (m.fp32)
                 orc_project_tokens_f32(feats[i].data(), wt.data.data(), m.t(prefix + ".bias").data.data(), pw, ph, D,
                                        proj.c, proj.v.data());
             else
@@ -1461,7 +1611,10 @@ int orc_model_infer(orc_model* model, const float* chw, uint32_t width, uint32_t
                 res.w = pw * k; res.h = ph * k; res.c = proj.c;
                 res.v.resize(static_cast<size_t>(res.w) * res.h * res.c);
                 const Tensor& rw = m.t(r + ".weight");
-                if (m.fp32)
+                if (m.fp16)
+                    orc_conv_transpose_f16(proj.v.data(), rw.data.data(), m.t(r + ".bias").data.data(), pw, ph,
+                                           proj.c, proj.c, k, res.v.data());
+                else if (m.fp32)
                     orc_conv_transpose_f32(proj.v.data(), rw.data.data(), m.t(r + ".bias").data.data(), pw, ph,
                                            proj.c, proj.c, k, res.v.data());
                 else

@@ -164,6 +164,38 @@ void orc_prepare_tokens_f32(const float* image, const float* weight,
                             const float* bias, const float* class_token,
                             const float* position, uint32_t width,
                             uint32_t height, uint32_t D, float* tokens);
+/* The graph in the fp16 precision mode (DAV2_CREATE_FORCE_FP16): half
+ * weights; cooperative-matrix linears (binary16 operands, exact products,
+ * fp32 sums) with layer_norm_fp16 / pack_fp16 inputs and fc1's half output;
+ * native binary16 patch embedding, projections and transposed convolutions;
+ * DPT convolutions through conv2d with half weights (fp32 arithmetic);
+ * attention_mode 1 (binary16, the default) or 0 (FORCE_FP32_ATTENTION). */
+int orc_model_infer_fp16(orc_model* model, const float* chw, uint32_t width,
+                         uint32_t height, int attention_mode, float* depth,
+                         float* pre_relu, float* features);
+/* fp16 operators. orc_gemm_h16_products: out[m][n] = sum over k ascending of
+ * float(fp16(h(a) * h(b))) in fp32, h = round to binary16 (the native
+ * binary16 shaders' dot products). orc_linear_f16: linear_coop_fp16.glsl
+ * (operators.cpp:540-768), optional GELU and half output. The others:
+ * prepare_tokens_fp16.glsl, project_tokens_fp16.glsl,
+ * conv_transpose_nonoverlap_fp16.glsl. Weights in the model file layout
+ * (fp32, rounded to binary16 inside). */
+void orc_gemm_h16_products(const float* a, uint64_t lda, const float* b, uint64_t ldb,
+                           uint32_t m, uint32_t n, uint32_t k, float* out);
+void orc_linear_f16(const float* input, const float* weight, const float* bias,
+                    uint32_t rows, uint32_t in_cols, uint32_t out_cols, int gelu,
+                    int half_output, float* out);
+void orc_project_tokens_f16(const float* tokens, const float* weight,
+                            const float* bias, uint32_t width, uint32_t height,
+                            uint32_t D, uint32_t C, float* out);
+void orc_conv_transpose_f16(const float* input, const float* weight,
+                            const float* bias, uint32_t width, uint32_t height,
+                            uint32_t in_channels, uint32_t out_channels,
+                            uint32_t kernel, float* out);
+void orc_prepare_tokens_f16(const float* image, const float* weight,
+                            const float* bias, const float* class_token,
+                            const float* position, uint32_t width,
+                            uint32_t height, uint32_t D, float* tokens);
 /* Encoder blocks [first, last) only, on tokens [T][D] in place (timing sample). */
 int orc_model_encoder_blocks(orc_model* model, float* tokens, uint32_t tokens_count,
                              uint32_t first, uint32_t last, int attention_mode);

@@ -51,6 +51,12 @@ _PROTO = {
     "orc_conv_transpose_f32": (None, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "orc_project_tokens_f32": (None, [vp, vp, vp, u32, u32, u32, u32, vp]),
     "orc_prepare_tokens_f32": (None, [vp, vp, vp, vp, vp, u32, u32, u32, vp]),
+    "orc_model_infer_fp16": (C.c_int, [vp, vp, u32, u32, C.c_int, vp, vp, vp]),
+    "orc_gemm_h16_products": (None, [vp, u64, vp, u64, u32, u32, u32, vp]),
+    "orc_linear_f16": (None, [vp, vp, vp, u32, u32, u32, C.c_int, C.c_int, vp]),
+    "orc_project_tokens_f16": (None, [vp, vp, vp, u32, u32, u32, u32, vp]),
+    "orc_conv_transpose_f16": (None, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
+    "orc_prepare_tokens_f16": (None, [vp, vp, vp, vp, vp, u32, u32, u32, vp]),
     "orc_network_shape": (C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "orc_preprocess_bgr8": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, vp]),
     "orc_preprocess_bgra8_nearest": (None, [vp, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, vp]),
@@ -389,6 +395,60 @@ class Oracle:
         t = (width // 14) * (height // 14) + 1
         out = np.empty((t, d), np.float32)
         self.lib.orc_prepare_tokens_f32(image.ctypes.data, w.ctypes.data, b.ctypes.data, cls.ctypes.data,
+                                        pos.ctypes.data, width, height, d, out.ctypes.data)
+        return out
+
+    # ---- fp16 precision mode ------------------------------------------------
+    def infer_fp16(self, h, chw, width: int, height: int, attention: str = "binary16"):
+        """The graph in the fp16 precision mode; returns (depth, pre-ReLU logits)."""
+        chw = _f32(chw)
+        depth = np.empty((height, width), np.float32)
+        logits = np.empty((height, width), np.float32)
+        if self.lib.orc_model_infer_fp16(h, chw.ctypes.data, width, height, self.ATTENTION_MODES[attention],
+                                         depth.ctypes.data, logits.ctypes.data, None) != 0:
+            raise RuntimeError("oracle inference failed")
+        return depth, logits
+
+    def gemm_h16_products(self, a, b):
+        a, b = _f32(a), _f32(b)
+        m, k = a.shape
+        n = b.shape[0]
+        out = np.empty((m, n), np.float32)
+        self.lib.orc_gemm_h16_products(a.ctypes.data, k, b.ctypes.data, k, m, n, k, out.ctypes.data)
+        return out
+
+    def linear_f16(self, x, w, b, gelu: bool = False, half_output: bool = False):
+        x, w = _f32(x), _f32(w)
+        rows, k = x.shape
+        n = w.shape[0]
+        out = np.empty((rows, n), np.float32)
+        self.lib.orc_linear_f16(x.ctypes.data, w.ctypes.data, _p(None if b is None else _f32(b)), rows, k, n,
+                                int(gelu), int(half_output), out.ctypes.data)
+        return out
+
+    def project_tokens_f16(self, tokens, w, b, pw: int, ph: int):
+        tokens, w, b = _f32(tokens), _f32(w), _f32(b)
+        c, d = w.shape
+        out = np.empty((c, ph, pw), np.float32)
+        self.lib.orc_project_tokens_f16(tokens.ctypes.data, w.ctypes.data, b.ctypes.data, pw, ph, d, c,
+                                        out.ctypes.data)
+        return out
+
+    def conv_transpose_f16(self, x, w, b):
+        x, w, b = _f32(x), _f32(w), _f32(b)
+        ic, ih, iw = x.shape
+        _, oc, k, _ = w.shape
+        out = np.empty((oc, ih * k, iw * k), np.float32)
+        self.lib.orc_conv_transpose_f16(x.ctypes.data, w.ctypes.data, b.ctypes.data, iw, ih, ic, oc, k,
+                                        out.ctypes.data)
+        return out
+
+    def prepare_tokens_f16(self, image, w, b, cls, pos, width: int, height: int):
+        image, w, b, cls, pos = _f32(image), _f32(w), _f32(b), _f32(cls), _f32(pos)
+        d = w.shape[0]
+        t = (width // 14) * (height // 14) + 1
+        out = np.empty((t, d), np.float32)
+        self.lib.orc_prepare_tokens_f16(image.ctypes.data, w.ctypes.data, b.ctypes.data, cls.ctypes.data,
                                         pos.ctypes.data, width, height, d, out.ctypes.data)
         return out
 

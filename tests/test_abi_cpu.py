@@ -99,8 +99,9 @@ def test_create_option_validation(pkg, lib, tmp_path):
     assert _create(pkg, lib, p, flags=1 << 9) == (1, "unsupported create flags")
     assert _create(pkg, lib, p, flags=pkg.FORCE_INT8 | pkg.FORCE_FP16)[0] == 1
     assert _create(pkg, lib, p, device=-1)[0] == 1
-    assert _create(pkg, lib, p, flags=pkg.FORCE_FP16)[0] == 8  # int8 and fp32 modes are built
-    # FORCE_FP32 and FORCE_FP32_WEIGHTS pass validation: the missing file then fails in the loader
+    # FORCE_FP32, FORCE_FP16 and FORCE_FP32_WEIGHTS pass validation: the missing file then fails in the loader
+    assert _create(pkg, lib, p, flags=pkg.FORCE_FP16)[0] == 9
+    assert _create(pkg, lib, p, flags=pkg.FORCE_FP16 | pkg.FORCE_FP32_ATTENTION)[0] == 9
     assert _create(pkg, lib, p, flags=pkg.FORCE_FP32)[0] == 9
     assert _create(pkg, lib, p, flags=pkg.FORCE_INT8 | 2)[0] == 9
     assert _create(pkg, lib, p, flags=pkg.FORCE_METAL)[0] == 8
