@@ -6,10 +6,12 @@
 //  - LayerNorm writes its quantized rows directly (no fp32 round trip), GELU
 //    is fused into the fc1 GEMM epilogue and the LayerScale residual into the
 //    proj/fc2 epilogues;
-//  - every DPT convolution, 3x3 and 1x1, runs as im2col + int8 GEMM (the
+//  - every DPT convolution, 3x3 and 1x1, runs as an int8 convolution (the
 //    reference's int8 mode sends only resize_layers.* through conv2d_int8 and
 //    the refinement convolutions through fp16); in the fp32 precision mode
-//    everything runs in fp32, as in the reference's;
+//    everything runs in fp32, as in the reference's, and the fp16 mode
+//    follows the reference's fp16 routing (half weights, cooperative-matrix
+//    linears, native binary16 projections, conv2d with half weights);
 //  - buffers come from a grow-only arena, so a fixed resolution allocates only
 //    on its first run.
 #pragma once
