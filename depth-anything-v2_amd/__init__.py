@@ -206,6 +206,7 @@ PROTOTYPES = {
     "dav2_hip_bilinear_align_true_maxima": (C.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "dav2_hip_conv2d_i8_emits": (C.c_int, [u32, u32]),
     "dav2_hip_gemm_i8_events": (None, [vp, vp]),
+    "dav2_hip_launch_events": (None, [vp, vp]),
     "dav2_hip_minmax_partials": (u32, [u64]),
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),
     "dav2_hip_normalize_relative": (C.c_int, [vp, vp, u64, vp]),

@@ -237,7 +237,7 @@ void launch_softmax(void* data, uint64_t rows, uint32_t columns, uint32_t stride
     const unsigned grid = ceil_div(rows, 4);
     const uint32_t ch = (columns + 63u) / 64u;
 #define DAV2_SM_CASE(N) \
-    hipLaunchKernelGGL((softmax_kernel<N>), dim3(grid), dim3(256), 0, s, data, rows, columns, stride)
+    dispatch((softmax_kernel<N>), dim3(grid), dim3(256), 0, s, data, rows, columns, stride)
     if (ch <= 4) DAV2_SM_CASE(4);
     else if (ch <= 8) DAV2_SM_CASE(8);
     else if (ch <= 16) DAV2_SM_CASE(16);
@@ -263,7 +263,7 @@ int dav2_hip_attention_scores(void* scores, const float* qkv, uint32_t tokens, u
         return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(ceil_div(tokens, 64), ceil_div(tokens, 64), heads * batch);
-    hipLaunchKernelGGL(attention_scores_kernel, grid, dim3(256), 0, s, qkv, static_cast<float*>(scores), tokens,
+    dispatch(attention_scores_kernel, grid, dim3(256), 0, s, qkv, static_cast<float*>(scores), tokens,
                        heads);
     return hipGetLastError();
 }
@@ -284,7 +284,7 @@ int dav2_hip_attention_values(float* out, const void* probabilities, const float
     if (!out || !probabilities || !qkv || (reinterpret_cast<uintptr_t>(qkv) & 15) || heads > 65535u / batch)
         return hipErrorInvalidValue;
     const dim3 grid(ceil_div(tokens, 128), 1, heads * batch);
-    hipLaunchKernelGGL(attention_values_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+    dispatch(attention_values_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<const float*>(probabilities), qkv, out, tokens, heads);
     return hipGetLastError();
 }

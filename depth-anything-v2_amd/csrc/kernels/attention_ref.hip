@@ -385,7 +385,7 @@ hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream
     const dim3 grid(static_cast<uint32_t>((rows + 3u) / 4u)), block(256);
 #define DAV2_SOFTMAX_CASE(N)                                                              \
     if (per_lane <= N) {                                                                  \
-        hipLaunchKernelGGL((ref_softmax_kernel<N, HALF>), grid, block, 0, s, data, rows, columns); \
+        dispatch((ref_softmax_kernel<N, HALF>), grid, block, 0, s, data, rows, columns); \
         return hipGetLastError();                                                         \
     }
     DAV2_SOFTMAX_CASE(4)
@@ -394,7 +394,7 @@ hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream
     DAV2_SOFTMAX_CASE(24)
     DAV2_SOFTMAX_CASE(48)
 #undef DAV2_SOFTMAX_CASE
-    hipLaunchKernelGGL((ref_softmax_kernel<0, HALF>), grid, block, 0, s, data, rows, columns);
+    dispatch((ref_softmax_kernel<0, HALF>), grid, block, 0, s, data, rows, columns);
     return hipGetLastError();
 }
 
@@ -418,9 +418,9 @@ int dav2_hip_attention_ref_scores(void* scores, const float* qkv, uint32_t token
     const dim3 grid(ceil_div(tokens, kKeyTile), ceil_div(tokens, kQueryTile), batch * heads);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (fp16)
-        hipLaunchKernelGGL(ref_scores_kernel<true>, grid, dim3(256), 0, s, qkv, scores, tokens, heads);
+        dispatch(ref_scores_kernel<true>, grid, dim3(256), 0, s, qkv, scores, tokens, heads);
     else
-        hipLaunchKernelGGL(ref_scores_kernel<false>, grid, dim3(256), 0, s, qkv, scores, tokens, heads);
+        dispatch(ref_scores_kernel<false>, grid, dim3(256), 0, s, qkv, scores, tokens, heads);
     return hipGetLastError();
 }
 
@@ -438,9 +438,9 @@ int dav2_hip_attention_ref_values(float* out, const void* probabilities, const f
     const dim3 grid(ceil_div(tokens, kValueRows), 1, batch * heads);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (fp16)
-        hipLaunchKernelGGL(ref_values_kernel<true>, grid, dim3(256), 0, s, out, probabilities, qkv, tokens, heads);
+        dispatch(ref_values_kernel<true>, grid, dim3(256), 0, s, out, probabilities, qkv, tokens, heads);
     else
-        hipLaunchKernelGGL(ref_values_kernel<false>, grid, dim3(256), 0, s, out, probabilities, qkv, tokens, heads);
+        dispatch(ref_values_kernel<false>, grid, dim3(256), 0, s, out, probabilities, qkv, tokens, heads);
     return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
 // Shared device helpers for the gfx950 kernels. Wave size is 64 throughout.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -104,6 +105,19 @@ DAV2_DEV void copy4_to_lds(const void* src, void* lds_base) {
 // quantize_rows_int8_fused.glsl:37 and im2col_quantize_int8.glsl:63.
 DAV2_DEV float row_scale(float absmax) { return fmaxf(absmax / 127.0f, 1.0e-8f); }
 
+// quantize_rne(x / s) (the IEEE quotient) for a row scale s from row_scale
+// (so |x / s| <= 127 (1 + 2^-23)), inv = div_rn(1, s). The product x * inv
+// is within 127 x (2^-23 + 2^-24 + 2^-47) < 2^-15.4 of the rounded quotient,
+// so both round to the same integer whenever the product is more than 2^-14
+// from a half-integer; the other lanes (about 1 in 8000) divide. NaN and
+// infinite x or s give the quotient's result as well (clamped NaN is -127).
+DAV2_DEV int quantize_div(float x, float s, float inv) {
+    const float y = x * inv;
+    const float n = __builtin_rintf(y);
+    if (__builtin_expect(fabsf(y - n) > 0.5f - 0x1p-14f, 0)) return quantize_rne(div_rn(x, s));
+    return static_cast<int>(fminf(fmaxf(n, -127.0f), 127.0f));
+}
+
 // Per-pixel |x| maxima of a CHW map over groups of kGroupChannels channels:
 // partial[g][p] = max over c in group g of |x[c][p]| (quantize.hip). The
 // window maximum of these is the absmax of an im2col row.
@@ -165,6 +179,28 @@ DAV2_DEV float gelu_erfcc(float value) {
     const float erfc_magnitude = t * exp_cw(-magnitude * magnitude + poly);
     const float erf_value = x >= 0.0f ? 1.0f - erfc_magnitude : erfc_magnitude - 1.0f;
     return 0.5f * value * (1.0f + erf_value);
+}
+
+// Timing hook for profiling (dav2_hip_launch_events): the calling thread's
+// next kernel launch records `start` when it begins, and every launch until
+// the hook is cleared records `stop` when it ends (an event keeps its last
+// record), so the pair spans all kernels of one operation. The dispatches
+// record them themselves (hipExtLaunchKernelGGL), so they time the kernels
+// and not the host's launch gaps before the first one.
+struct LaunchEvents {
+    hipEvent_t start, stop;
+};
+LaunchEvents& launch_events();
+
+template <typename Kernel, typename... Args>
+void dispatch(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+    LaunchEvents& e = launch_events();
+    if (e.start || e.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), stream, e.start, e.stop, 0, args...);
+        e.start = nullptr;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    }
 }
 
 }  // namespace dav2k

@@ -340,9 +340,9 @@ __global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
 template <int BN, int WM, int WN>
 void launch(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
     if (g.flags & DAV2_CONV_RELU_INPUT)
-        hipLaunchKernelGGL((conv3x3_i8_kernel<BN, WM, WN, true>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+        dispatch((conv3x3_i8_kernel<BN, WM, WN, true>), dim3(tiles, n / BN), dim3(256), 0, s, g);
     else
-        hipLaunchKernelGGL((conv3x3_i8_kernel<BN, WM, WN, false>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+        dispatch((conv3x3_i8_kernel<BN, WM, WN, false>), dim3(tiles, n / BN), dim3(256), 0, s, g);
 }
 
 }  // namespace

@@ -454,9 +454,9 @@ __global__ __launch_bounds__(256) void weights_pack_kernel(int8_t* __restrict__ 
 template <int KS, int BN, int WM, int WN>
 void launch(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
     if (g.flags & DAV2_CONV_RELU_INPUT)
-        hipLaunchKernelGGL((conv_i8_kernel<KS, BN, WM, WN, true>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+        dispatch((conv_i8_kernel<KS, BN, WM, WN, true>), dim3(tiles, n / BN), dim3(256), 0, s, g);
     else
-        hipLaunchKernelGGL((conv_i8_kernel<KS, BN, WM, WN, false>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+        dispatch((conv_i8_kernel<KS, BN, WM, WN, false>), dim3(tiles, n / BN), dim3(256), 0, s, g);
 }
 
 template <int KS>
@@ -482,7 +482,7 @@ int dav2_hip_conv_weights_pack(int8_t* dst, const int8_t* src, uint32_t out_chan
         (taps * channels) % 64 != 0)
         return hipErrorInvalidValue;
     const uint64_t total = taps * channels * out_channels;
-    hipLaunchKernelGGL(weights_pack_kernel, dim3(ceil_div(total, 256)), dim3(256), 0,
+    dispatch(weights_pack_kernel, dim3(ceil_div(total, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), dst, src, out_channels, channels,
                        static_cast<uint32_t>(taps), ldb);
     return hipGetLastError();
@@ -564,7 +564,7 @@ int dav2_hip_conv1x1_narrow_i8(const float* input, uint32_t width, uint32_t heig
         out_channels > kNarrowN || ldw < channels ||
         (flags & ~static_cast<uint32_t>(DAV2_CONV_RELU_INPUT | DAV2_CONV_RELU_OUTPUT)))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(conv1x1_narrow_kernel, dim3(ceil_div(plane, 256)), dim3(256), 0,
+    dispatch(conv1x1_narrow_kernel, dim3(ceil_div(plane, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), input, plane, channels, weight, ldw, weight_scales, bias,
                        out_channels, out, pre_relu, flags);
     return hipGetLastError();

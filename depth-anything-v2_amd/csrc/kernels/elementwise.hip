@@ -259,12 +259,21 @@ __global__ __launch_bounds__(kBlock) void finish_tokens_kernel(float* tokens, co
 
 }  // namespace
 
+LaunchEvents& dav2k::launch_events() {
+    thread_local LaunchEvents events{nullptr, nullptr};
+    return events;
+}
+
 extern "C" {
+
+void dav2_hip_launch_events(void* start, void* stop) {
+    launch_events() = LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
+}
 
 int dav2_hip_gelu(float* out, const float* input, uint64_t count, void* stream) {
     if (count == 0) return hipSuccess;
     if (!out || !input) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gelu_kernel, dim3(grid_for(count)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), out,
+    dispatch(gelu_kernel, dim3(grid_for(count)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), out,
                        input, count);
     return hipGetLastError();
 }
@@ -273,7 +282,7 @@ int dav2_hip_add_scaled(float* out, const float* residual, const float* addend, 
                         uint64_t count, uint32_t columns, void* stream) {
     if (count == 0) return hipSuccess;
     if (!out || !residual || !addend || !scale || columns == 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(add_scaled_kernel, dim3(grid_for(count)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+    dispatch(add_scaled_kernel, dim3(grid_for(count)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
                        out, residual, addend, scale, count, columns);
     return hipGetLastError();
 }
@@ -281,7 +290,7 @@ int dav2_hip_add_scaled(float* out, const float* residual, const float* addend, 
 int dav2_hip_add(float* out, const float* left, const float* right, uint64_t count, void* stream) {
     if (count == 0) return hipSuccess;
     if (!out || !left || !right) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(add_kernel, dim3(grid_for((count + 3) / 4)), dim3(kBlock), 0,
+    dispatch(add_kernel, dim3(grid_for((count + 3) / 4)), dim3(kBlock), 0,
                        static_cast<hipStream_t>(stream), out, left, right, count);
     return hipGetLastError();
 }
@@ -289,7 +298,7 @@ int dav2_hip_add(float* out, const float* left, const float* right, uint64_t cou
 int dav2_hip_round_half(float* data, uint64_t count, void* stream) {
     if (count == 0) return hipSuccess;
     if (!data) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(round_half_kernel, dim3(grid_for(count)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+    dispatch(round_half_kernel, dim3(grid_for(count)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
                        data, count);
     return hipGetLastError();
 }
@@ -297,7 +306,7 @@ int dav2_hip_round_half(float* data, uint64_t count, void* stream) {
 int dav2_hip_relu(float* out, const float* input, uint64_t count, void* stream) {
     if (count == 0) return hipSuccess;
     if (!out || !input) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(relu_kernel, dim3(grid_for((count + 3) / 4)), dim3(kBlock), 0,
+    dispatch(relu_kernel, dim3(grid_for((count + 3) / 4)), dim3(kBlock), 0,
                        static_cast<hipStream_t>(stream), out, input, count);
     return hipGetLastError();
 }
@@ -307,7 +316,7 @@ int dav2_hip_bilinear_align_true(float* out, const float* input, uint32_t iw, ui
     if (ow == 0 || oh == 0 || channels == 0) return hipSuccess;
     if (!out || !input || iw == 0 || ih == 0 || channels > 65535u) return hipErrorInvalidValue;
     const dim3 grid(ceil_div(ow, 64), ceil_div(oh, 4), ceil_div(channels, kBilinearChannels));
-    hipLaunchKernelGGL(bilinear_kernel<kBilinearChannels>, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+    dispatch(bilinear_kernel<kBilinearChannels>, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream),
                        out, input, iw, ih, ow, oh, channels, nullptr);
     return hipGetLastError();
 }
@@ -318,7 +327,7 @@ int dav2_hip_bilinear_align_true_maxima(float* out, float* partial, const float*
     if (!out || !partial || !input || iw == 0 || ih == 0 || channels % 32u || channels > 65535u)
         return hipErrorInvalidValue;
     const dim3 grid(ceil_div(ow, 64), ceil_div(oh, 4), channels / 32u);
-    hipLaunchKernelGGL(bilinear_kernel<32>, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), out, input, iw,
+    dispatch(bilinear_kernel<32>, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), out, input, iw,
                        ih, ow, oh, channels, partial);
     return hipGetLastError();
 }
@@ -332,15 +341,15 @@ int dav2_hip_reduce_minmax(const float* input, uint64_t count, float* range, flo
     if (!input || !range || !partials || count == 0) return hipErrorInvalidValue;
     const uint32_t groups = dav2_hip_minmax_partials(count);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(minmax_stage1, dim3(groups), dim3(kBlock), 0, s, input, count, partials);
-    hipLaunchKernelGGL(minmax_stage2, dim3(1), dim3(kBlock), 0, s, partials, groups, range);
+    dispatch(minmax_stage1, dim3(groups), dim3(kBlock), 0, s, input, count, partials);
+    dispatch(minmax_stage2, dim3(1), dim3(kBlock), 0, s, partials, groups, range);
     return hipGetLastError();
 }
 
 int dav2_hip_normalize_relative(float* depth, const float* range, uint64_t count, void* stream) {
     if (count == 0) return hipSuccess;
     if (!depth || !range) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(normalize_relative_kernel, dim3(grid_for(count)), dim3(kBlock), 0,
+    dispatch(normalize_relative_kernel, dim3(grid_for(count)), dim3(kBlock), 0,
                        static_cast<hipStream_t>(stream), depth, range, count);
     return hipGetLastError();
 }
@@ -355,7 +364,7 @@ int dav2_hip_position_bicubic(float* out, const float* position, uint32_t pw, ui
     const float sx = identity ? 1.0f : static_cast<float>(1.0 / ((static_cast<double>(pw) + 0.1) / 37.0));
     const float sy = identity ? 1.0f : static_cast<float>(1.0 / ((static_cast<double>(ph) + 0.1) / 37.0));
     const uint64_t total = static_cast<uint64_t>(pw) * ph * D;
-    hipLaunchKernelGGL(position_bicubic_kernel, dim3(grid_for(total)), dim3(kBlock), 0,
+    dispatch(position_bicubic_kernel, dim3(grid_for(total)), dim3(kBlock), 0,
                        static_cast<hipStream_t>(stream), out, position, pw, ph, D, sx, sy);
     return hipGetLastError();
 }
@@ -366,7 +375,7 @@ int dav2_hip_finish_tokens(float* tokens, const float* interpolated, const float
     if (D == 0 || batch == 0) return hipSuccess;
     if (!tokens || !interpolated || !position || !class_token) return hipErrorInvalidValue;
     const uint64_t total = (static_cast<uint64_t>(pw) * ph + 1u) * D * batch;
-    hipLaunchKernelGGL(finish_tokens_kernel, dim3(grid_for(total)), dim3(kBlock), 0,
+    dispatch(finish_tokens_kernel, dim3(grid_for(total)), dim3(kBlock), 0,
                        static_cast<hipStream_t>(stream), tokens, interpolated, position, class_token, pw * ph, D,
                        batch);
     return hipGetLastError();

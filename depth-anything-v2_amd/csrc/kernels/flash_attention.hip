@@ -715,13 +715,13 @@ int run_attention(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(tp / kBlock, heads, batch);
     if (col_absmax) {
-        hipLaunchKernelGGL(pack_qkv_kernel, dim3(tp / kBlock, heads, 3), dim3(256), 0, s, qkv, col_absmax,
+        dispatch(pack_qkv_kernel, dim3(tp / kBlock, heads, 3), dim3(256), 0, s, qkv, col_absmax,
                            partial_rows, qd, kd, vd, qe, ke, ve, tokens, heads, tp);
     } else {
-        hipLaunchKernelGGL(pack_q_kernel, grid, dim3(256), 0, s, qkv, qd, qe, kmax, vmax, tokens, heads, tp);
-        hipLaunchKernelGGL(pack_kv_kernel, grid, dim3(256), 0, s, qkv, kmax, vmax, kd, vd, ke, ve, tokens, heads, tp);
+        dispatch(pack_q_kernel, grid, dim3(256), 0, s, qkv, qd, qe, kmax, vmax, tokens, heads, tp);
+        dispatch(pack_kv_kernel, grid, dim3(256), 0, s, qkv, kmax, vmax, kd, vd, ke, ve, tokens, heads, tp);
     }
-    hipLaunchKernelGGL(attention_exact_kernel, dim3(tp / 32u, heads, batch), dim3(kAttnThreads), kAttnLds, s, qd,
+    dispatch(attention_exact_kernel, dim3(tp / 32u, heads, batch), dim3(kAttnThreads), kAttnLds, s, qd,
                        kd, vd, qe, ke, ve, out, tokens, heads, tp);
     return hipGetLastError();
 }

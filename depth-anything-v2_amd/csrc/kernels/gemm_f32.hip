@@ -279,12 +279,12 @@ __global__ __launch_bounds__(256) void im2col_f32_kernel(const float* __restrict
 
 template <int EPI>
 void launch(const F32Params& g, hipStream_t s) {
-    hipLaunchKernelGGL(gemm_f32_kernel<EPI>, dim3(ceil_div(g.m, kBM), ceil_div(g.n, kBN)), dim3(256), 0, s, g);
+    dispatch(gemm_f32_kernel<EPI>, dim3(ceil_div(g.m, kBM), ceil_div(g.n, kBN)), dim3(256), 0, s, g);
 }
 
 template <int EPI>
 void launch_h16p(const F32Params& g, hipStream_t s) {
-    hipLaunchKernelGGL(gemm_h16p_kernel<EPI>, dim3(ceil_div(g.m, kBM), ceil_div(g.n, kBN)), dim3(256), 0, s, g);
+    dispatch(gemm_h16p_kernel<EPI>, dim3(ceil_div(g.m, kBM), ceil_div(g.n, kBN)), dim3(256), 0, s, g);
 }
 
 // Checks a dav2_gemm_f32_args and fills the kernel parameters; false if the
@@ -372,7 +372,7 @@ int dav2_hip_im2col_f32(const float* input, uint32_t input_width, uint32_t input
     if (!input || !out || kernel == 0 || stride == 0 || padding < 0 || ld < columns || columns >= (1u << 24) ||
         rows * ld >= (1ull << 38))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(im2col_f32_kernel, dim3(ceil_div(rows * ld, 256)), dim3(256), 0,
+    dispatch(im2col_f32_kernel, dim3(ceil_div(rows * ld, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), input, input_width, input_height, input_channels,
                        output_width, kernel, stride, padding, relu, rows, static_cast<uint32_t>(columns), ld, out);
     return hipGetLastError();

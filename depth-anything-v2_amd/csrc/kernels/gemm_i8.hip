@@ -443,22 +443,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
     }
 }
 
-// Events for the calling thread's next GEMM launch (dav2_hip_gemm_i8_events):
-// the kernel dispatch itself records them (hipExtLaunchKernelGGL), so they
-// time the kernel and nothing else; consumed by that launch.
-thread_local hipEvent_t t_start_event = nullptr, t_stop_event = nullptr;
-
-template <typename Kernel, typename... Args>
-void launch_timed(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, bool first, bool last,
-                  Args... args) {
-    hipEvent_t start = first ? t_start_event : nullptr, stop = last ? t_stop_event : nullptr;
-    if (first) t_start_event = nullptr;
-    if (last) t_stop_event = nullptr;
-    if (start || stop)
-        hipExtLaunchKernelGGL(kernel, grid, block, lds, s, start, stop, 0, args...);
-    else
-        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
-}
+// dav2_hip_gemm_i8_events: the dispatch hook (dispatch() in common.h) set for
+// one dav2_hip_gemm_i8 call, cleared when that call returns.
+thread_local bool t_events_for_one_gemm = false;
 
 template <int BM, int BN, int WMW, int WNW, int BK, int STAGES, int EPI>
 void launch_cfg(const GemmParams& g, hipStream_t s, bool last = true) {
@@ -471,7 +458,8 @@ void launch_cfg(const GemmParams& g, hipStream_t s, bool last = true) {
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     (void)attr;
     const dim3 grid(ceil_div(g.rows_p, BM), ceil_div(g.rows_q, BN), ceil_div(g.k, g.k_split));
-    launch_timed(gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>, grid, dim3(64 * WMW * WNW), lds, s, true, last, g);
+    (void)last;
+    dispatch(gemm_i8_kernel<BM, BN, WMW, WNW, BK, STAGES, EPI>, grid, dim3(64 * WMW * WNW), lds, s, g);
 }
 
 // Rows of P from which launch_epi picks 64x128 tiles for the row-major
@@ -541,7 +529,9 @@ extern "C" uint64_t dav2_hip_gemm_i8_split_scratch_bytes(uint32_t m, uint32_t n,
     return static_cast<uint64_t>(split_k) * m * n * sizeof(int32_t);
 }
 
-extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
+namespace {
+
+int gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     if (!a) return hipErrorInvalidValue;
     if (a->m == 0 || a->n == 0) return hipSuccess;
     if (!a->a || !a->b || a->k == 0 || a->k % 64 || a->lda < a->k || a->ldb < a->k ||
@@ -607,7 +597,7 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     if (split && slices > 1) {
         launch_epi<kEpiSplitPartial>(g, s, false);
         const uint64_t total = static_cast<uint64_t>(a->m) * a->n;
-        launch_timed(split_reduce_transposed_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, false, true,
+        dispatch(split_reduce_transposed_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s,
                      a->split_scratch, slices, a->n, a->m, a->a_scales, a->b_scales, a->bias, a->residual,
                      a->relu_output, a->out, a->out_row_stride, a->out_row_offset);
         return hipGetLastError();
@@ -625,9 +615,20 @@ extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     return hipGetLastError();
 }
 
+}  // namespace
+
+extern "C" int dav2_hip_gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
+    const int status = gemm_i8(a, stream);
+    if (t_events_for_one_gemm) {
+        launch_events() = LaunchEvents{nullptr, nullptr};
+        t_events_for_one_gemm = false;
+    }
+    return status;
+}
+
 extern "C" void dav2_hip_gemm_i8_events(void* start, void* stop) {
-    t_start_event = static_cast<hipEvent_t>(start);
-    t_stop_event = static_cast<hipEvent_t>(stop);
+    launch_events() = LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
+    t_events_for_one_gemm = start || stop;
 }
 
 extern "C" uint32_t dav2_hip_gemm_i8_row_tiles(uint32_t m, uint32_t n, uint32_t epilogue) {

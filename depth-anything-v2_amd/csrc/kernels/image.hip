@@ -181,7 +181,7 @@ int dav2_hip_preprocess_bgr8(const uint8_t* bgr, uint32_t width, uint32_t height
         dst_height > kTileY * 65535u)
         return hipErrorInvalidValue;
     const dim3 grid(ceil_div(dst_width, kTileX), ceil_div(dst_height, kTileY));
-    hipLaunchKernelGGL(preprocess_bgr8_kernel, grid, dim3(kTileX * kTileY), 0, static_cast<hipStream_t>(stream), bgr,
+    dispatch(preprocess_bgr8_kernel, grid, dim3(kTileX * kTileY), 0, static_cast<hipStream_t>(stream), bgr,
                        width, height, stride, dst_width, dst_height,
                        static_cast<double>(width) / static_cast<double>(dst_width),
                        static_cast<double>(height) / static_cast<double>(dst_height), out);
@@ -195,7 +195,7 @@ int dav2_hip_preprocess_bgra8_nearest(const uint8_t* bgra, uint32_t width, uint3
         dst_width > (1u << 24) || dst_height > kTileY * 65535u)
         return hipErrorInvalidValue;
     const dim3 grid(ceil_div(dst_width, kTileX), ceil_div(dst_height, kTileY));
-    hipLaunchKernelGGL(preprocess_bgra8_nearest_kernel, grid, dim3(kTileX * kTileY), 0,
+    dispatch(preprocess_bgra8_nearest_kernel, grid, dim3(kTileX * kTileY), 0,
                        static_cast<hipStream_t>(stream), bgra, width, height, stride, dst_width, dst_height,
                        static_cast<float>(width) / static_cast<float>(dst_width),
                        static_cast<float>(height) / static_cast<float>(dst_height), out);
@@ -210,7 +210,7 @@ int dav2_hip_preprocess_rgba8(const uint32_t* pixels, uint32_t width, uint32_t h
         height > (1u << 24) || dst_width > (1u << 24) || dst_height > kTileY * 65535u)
         return hipErrorInvalidValue;
     const dim3 grid(ceil_div(dst_width, kTileX), ceil_div(dst_height, kTileY));
-    hipLaunchKernelGGL(preprocess_rgba8_kernel, grid, dim3(kTileX * kTileY), 0, static_cast<hipStream_t>(stream),
+    dispatch(preprocess_rgba8_kernel, grid, dim3(kTileX * kTileY), 0, static_cast<hipStream_t>(stream),
                        pixels, width, height, static_cast<uint32_t>(stride_bytes / 4u), dst_width, dst_height,
                        rgba_order, out);
     return hipGetLastError();
@@ -219,7 +219,7 @@ int dav2_hip_preprocess_rgba8(const uint32_t* pixels, uint32_t width, uint32_t h
 int dav2_hip_normalize_span(const float* depth, const float* range, uint64_t count, float* out, void* stream) {
     if (count == 0) return hipSuccess;
     if (!depth || !range || !out) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(normalize_span_kernel, dim3(ceil_div(count, 256)), dim3(256), 0,
+    dispatch(normalize_span_kernel, dim3(ceil_div(count, 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), depth, range, count, out);
     return hipGetLastError();
 }

@@ -490,7 +490,7 @@ hipError_t launch_layer_norm(const float* in, const float* w, const float* b, ui
     const size_t lds = QUANT ? static_cast<size_t>(kRowsPerBlock) * cols * sizeof(float) : 0;
     const uint32_t ch = (cols + 63u) / 64u;
 #define DAV2_LN_CASE(N)                                                                   \
-    hipLaunchKernelGGL((layer_norm_kernel<N, QUANT>), dim3(grid), dim3(64 * kRowsPerBlock), \
+    dispatch((layer_norm_kernel<N, QUANT>), dim3(grid), dim3(64 * kRowsPerBlock), \
                        lds, stream, in, w, b, rows, cols, eps, out, q, ldq, scales)
     if (ch <= 6) DAV2_LN_CASE(6);
     else if (ch <= 12) DAV2_LN_CASE(12);
@@ -505,8 +505,8 @@ hipError_t launch_layer_norm(const float* in, const float* w, const float* b, ui
 hipError_t dav2k::launch_channel_group_absmax(const float* x, uint32_t channels, uint64_t plane, float* partial,
                                               bool relu, hipStream_t stream) {
     const dim3 grid(ceil_div(plane, 256), channel_groups(channels));
-    if (relu) hipLaunchKernelGGL(channel_group_absmax_kernel<true>, grid, dim3(256), 0, stream, x, channels, plane, partial);
-    else hipLaunchKernelGGL(channel_group_absmax_kernel<false>, grid, dim3(256), 0, stream, x, channels, plane, partial);
+    if (relu) dispatch(channel_group_absmax_kernel<true>, grid, dim3(256), 0, stream, x, channels, plane, partial);
+    else dispatch(channel_group_absmax_kernel<false>, grid, dim3(256), 0, stream, x, channels, plane, partial);
     return hipGetLastError();
 }
 
@@ -541,7 +541,7 @@ int dav2_hip_pad_rows_i8(const int8_t* src, uint32_t rows, uint32_t columns, int
     if (!src || !dst || columns == 0 || ld < columns || ld % 16u || (reinterpret_cast<uintptr_t>(dst) & 15) ||
         rows > 65535u)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(pad_rows_kernel, dim3(ceil_div(ld, 256u * 16u), rows), dim3(256), 0,
+    dispatch(pad_rows_kernel, dim3(ceil_div(ld, 256u * 16u), rows), dim3(256), 0,
                        static_cast<hipStream_t>(stream), src, columns, dst, ld);
     return hipGetLastError();
 }
@@ -558,7 +558,7 @@ int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset, uint32_
     const uint32_t ch = (columns / 4u + 63u) / 64u;
     // Long rows are split over several waves (more loads in flight per row).
 #define DAV2_QR_CASE(N, W)                                                                                         \
-    hipLaunchKernelGGL((quantize_rows_kernel<N, W>), dim3(ceil_div(rows, kRowsPerBlock / W)), dim3(64 * kRowsPerBlock), \
+    dispatch((quantize_rows_kernel<N, W>), dim3(ceil_div(rows, kRowsPerBlock / W)), dim3(64 * kRowsPerBlock), \
                        0, s, input, input_offset, rows, columns, q, ldq, scales)
     if (ch <= 1) DAV2_QR_CASE(1, 1);
     else if (ch <= 2) DAV2_QR_CASE(2, 1);
@@ -566,7 +566,7 @@ int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset, uint32_
     else if (ch <= 8) DAV2_QR_CASE(4, 2);
     else if (ch <= 16) DAV2_QR_CASE(4, 4);
     else
-        hipLaunchKernelGGL(quantize_rows_long_kernel, dim3(grid), dim3(64 * kRowsPerBlock), 0, s,
+        dispatch(quantize_rows_long_kernel, dim3(grid), dim3(64 * kRowsPerBlock), 0, s,
                            input, input_offset, rows, columns, q, ldq, scales);
 #undef DAV2_QR_CASE
     return hipGetLastError();
@@ -628,10 +628,10 @@ int im2col_quantize(const float* input, uint32_t input_width, uint32_t input_hei
             const uint32_t per = (chunks + splits - 1) / splits;
             const dim3 grid(ceil_div(input_width, kTile), input_height, ceil_div(chunks, per));
             if (relu)
-                hipLaunchKernelGGL(im2col3x3_kernel<true>, grid, dim3(256), 0, s, input, scratch, groups,
+                dispatch(im2col3x3_kernel<true>, grid, dim3(256), 0, s, input, scratch, groups,
                                    input_channels, input_height, input_width, per, q, ldq, scales);
             else
-                hipLaunchKernelGGL(im2col3x3_kernel<false>, grid, dim3(256), 0, s, input, scratch, groups,
+                dispatch(im2col3x3_kernel<false>, grid, dim3(256), 0, s, input, scratch, groups,
                                    input_channels, input_height, input_width, per, q, ldq, scales);
         } else {
             const unsigned tiles = ceil_div(plane, kTile);
@@ -640,10 +640,10 @@ int im2col_quantize(const float* input, uint32_t input_width, uint32_t input_hei
             const uint32_t per = (chunks + splits - 1) / splits;
             const dim3 grid(tiles, ceil_div(chunks, per));
             if (relu)
-                hipLaunchKernelGGL(im2col1x1_kernel<true>, grid, dim3(256), 0, s, input, scratch, groups,
+                dispatch(im2col1x1_kernel<true>, grid, dim3(256), 0, s, input, scratch, groups,
                                    input_channels, plane, per, q, ldq, scales);
             else
-                hipLaunchKernelGGL(im2col1x1_kernel<false>, grid, dim3(256), 0, s, input, scratch, groups,
+                dispatch(im2col1x1_kernel<false>, grid, dim3(256), 0, s, input, scratch, groups,
                                    input_channels, plane, per, q, ldq, scales);
         }
         return hipGetLastError();
@@ -651,18 +651,18 @@ int im2col_quantize(const float* input, uint32_t input_width, uint32_t input_hei
     if (relu) return hipErrorInvalidValue;
     if (have_partial) {
         // Scales from the channel-group maxima (same values, one thread per row).
-        hipLaunchKernelGGL(channel_group_absmax_kernel<false>, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s,
+        dispatch(channel_group_absmax_kernel<false>, dim3(ceil_div(plane, 256), groups), dim3(256), 0, s,
                            input, input_channels, plane, scratch);
-        hipLaunchKernelGGL(window_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0, s,
+        dispatch(window_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0, s,
                            scratch, groups, plane, input_width, input_height, output_width, rows, kernel, stride,
                            padding, scales);
     } else {
-        hipLaunchKernelGGL(im2col_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
+        dispatch(im2col_scale_kernel, dim3(ceil_div(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
                            s, g, rows, scales);
     }
     const uint32_t ldq_words = ldq / 4u;
     const uint64_t total = rows64 * ldq_words;
-    hipLaunchKernelGGL(im2col_quantize_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, g, rows,
+    dispatch(im2col_quantize_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, g, rows,
                        ldq_words, scales, q);
     return hipGetLastError();
 }

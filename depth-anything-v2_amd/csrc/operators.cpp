@@ -173,7 +173,7 @@ void HipOperators::linear_int8_prequantized(DeviceBuffer& output, const DeviceBu
     a.residual = output.as<float>();
     a.gamma = gamma ? gamma->as<float>() : nullptr;
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
-                      stream(), /*dispatch_events=*/true);
+                      stream());
     hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
 }
 
@@ -215,7 +215,7 @@ void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& 
         }
     }
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
-                      stream(), /*dispatch_events=*/true);
+                      stream());
     hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
 }
 
@@ -855,8 +855,7 @@ void HipOperators::conv_transpose_nonoverlap_int8(DeviceBuffer& output, const De
     a.convt_width = input_width;
     a.convt_height = input_height;
     a.convt_channels = output_channels;
-    ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * input_rows * weight_rows * input_channels, "OP", s,
-                      /*dispatch_events=*/true);
+    ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * input_rows * weight_rows * input_channels, "OP", s);
     hip_check(dav2_hip_gemm_i8(&a, s), "transposed convolution GEMM");
 }
 

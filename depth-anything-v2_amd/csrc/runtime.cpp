@@ -74,7 +74,7 @@ int Profiler::begin(const char* name, double work, const char* unit, hipStream_t
     if (!enabled_) return -1;
     Record r{name, unit, work, take_event(), take_event(), dispatch_events};
     if (dispatch_events)
-        dav2_hip_gemm_i8_events(r.start, r.stop);
+        dav2_hip_launch_events(r.start, r.stop);
     else
         hip_check(hipEventRecord(r.start, stream), "hipEventRecord");
     pending_.push_back(r);
@@ -84,7 +84,7 @@ int Profiler::begin(const char* name, double work, const char* unit, hipStream_t
 void Profiler::end(int id, hipStream_t stream) {
     if (id < 0 || static_cast<std::size_t>(id) >= pending_.size()) return;
     if (pending_[id].dispatch)
-        dav2_hip_gemm_i8_events(nullptr, nullptr);  // a launch that did not happen leaves none behind
+        dav2_hip_launch_events(nullptr, nullptr);  // the operation's launches are done
     else
         (void)hipEventRecord(pending_[id].stop, stream);
 }

@@ -56,11 +56,13 @@ public:
     ~Profiler();
     void set_enabled(bool on) { enabled_ = on; }
     bool enabled() const { return enabled_; }
-    // Returns a record id, or -1 when disabled. With dispatch_events the
-    // events go to the next GEMM launch (dav2_hip_gemm_i8_events), which
-    // records them at the kernel's start and end; otherwise they are
-    // recorded on the stream around the enqueued work.
-    int begin(const char* name, double work, const char* unit, hipStream_t stream, bool dispatch_events = false);
+    // Returns a record id, or -1 when disabled. With dispatch_events (the
+    // default) the events go to the operation's kernel dispatches
+    // (dav2_hip_launch_events): the first kernel records the start as it
+    // begins, the last one the stop as it ends, so gaps before the first
+    // kernel are not counted; otherwise they are recorded on the stream
+    // around the enqueued work.
+    int begin(const char* name, double work, const char* unit, hipStream_t stream, bool dispatch_events = true);
     void end(int id, hipStream_t stream);
     // Synchronises, folds pending records into the totals and returns them as
     // a JSON object {name: {"launches", "ms", "work", "unit"}}; then clears.
@@ -89,7 +91,7 @@ private:
 class ProfileScope {
 public:
     ProfileScope(Profiler& p, const char* name, double work, const char* unit, hipStream_t s,
-                 bool dispatch_events = false)
+                 bool dispatch_events = true)
         : p_(p), s_(s), id_(p.begin(name, work, unit, s, dispatch_events)) {}
     ~ProfileScope() { p_.end(id_, s_); }
 

@@ -134,6 +134,11 @@ DAV2_API int dav2_hip_gemm_i8(const dav2_gemm_i8_args* args, void* stream);
  * calling thread's next dav2_hip_gemm_i8, recorded by its kernel dispatches
  * (the GEMM's start, the last kernel's end); NULL, NULL clears. */
 DAV2_API void dav2_hip_gemm_i8_events(void* start, void* stop);
+/* Timing hook, no reference counterpart: hipEvent_t start / stop for the
+ * calling thread's kernel dispatches: the next kernel launched records start
+ * when it begins, every launch until the hook is cleared (NULL, NULL) records
+ * stop when it ends, so the pair spans all kernels of an operation. */
+DAV2_API void dav2_hip_launch_events(void* start, void* stop);
 
 /* fp32 GEMM of the fp32 precision mode: out = a . b^T + bias with the
  * epilogues ROW, ROW_GELU, ROW_LAYERSCALE, TRANSPOSED (residual, relu_output)

@@ -25,7 +25,9 @@ def _announce(*what):
 # ---------------------------------------------------------------------------
 # quantize_rows_int8_fused.glsl
 @pytest.mark.parametrize("rows,cols,offset_rows", [(1370, 384, 0), (1370, 1024, 0), (1369, 4096, 0), (7, 8, 0),
-                                                   (3, 8192, 0), (1369, 1024, 1), (1, 1536, 0)])
+                                                   (3, 8192, 0), (1369, 1024, 1), (1, 1536, 0),
+                                                   # many rows: the row-looping kernel (odd wave tails)
+                                                   (10960, 1024, 0), (4099, 384, 2), (5000, 100, 0)])
 def test_quantize_rows_bit_exact(gpu, lib, oracle, rows, cols, offset_rows):
     torch = gpu
     _announce("quantize_rows", rows, cols, offset_rows)
@@ -56,6 +58,24 @@ def test_quantize_rows_packed_word_byte_order(gpu, lib):
     words = host(torch, qd).view(np.uint32)[0, :2]
     assert words.tolist() == [0x0201007F, 0x0002FF81]
     assert host(torch, sd)[0] == np.float32(2.0)
+
+
+@pytest.mark.parametrize("cols", [100, 1024, 2048, 4096, 20000])
+def test_quantize_rows_near_ties(gpu, lib, oracle, cols):
+    # quotients within a few ulps of half-integers: the kernels' product path
+    # must hand these to the IEEE division (bit-exact against the oracle)
+    from test_oracle_quant import near_tie_rows
+    torch = gpu
+    _announce("quantize_rows near ties", cols)
+    x = near_tie_rows(24, cols, cols)
+    q_ref, s_ref = oracle.quantize_rows(x)
+    ld = (cols + 63) // 64 * 64
+    xd = dev(torch, x)
+    qd = torch.full((24, ld), 0x55, dtype=torch.int8, device="cuda")
+    sd = empty(torch, (24,), torch.float32)
+    ok(lib, lib.dav2_hip_quantize_rows_i8(ptr(xd), 0, 24, cols, ptr(qd), ld, ptr(sd), stream(torch)))
+    assert np.array_equal(host(torch, qd)[:, :cols], q_ref)
+    assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
 
 
 # ---------------------------------------------------------------------------
@@ -583,6 +603,32 @@ def test_layer_norm_bit_exact(gpu, lib, oracle, rows, cols):
         assert np.array_equal(q[:, :cols], q_ref) and np.all(q[:, cols:] == 0)
         assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
         assert np.array_equal(host(torch, out2).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("cols", [384, 1024, 1536])
+def test_layer_norm_quantize_near_ties(gpu, lib, oracle, cols):
+    # weight 0 makes every normalised value the bias exactly, so the quantizer
+    # sees quotients within a few ulps of half-integers (CH path for 384 and
+    # 1024 columns, the re-reading path for 1536)
+    from test_oracle_quant import near_tie_rows
+    torch = gpu
+    _announce("layer_norm_quantize near ties", cols)
+    rows = 6
+    b = near_tie_rows(1, cols, cols + 1)[0]
+    x = np.random.default_rng(cols).standard_normal((rows, cols)).astype(np.float32)
+    w = np.zeros(cols, np.float32)
+    ref = oracle.layer_norm(x, w, b, 1e-6)
+    assert np.array_equal(ref, np.broadcast_to(b, ref.shape))
+    q_ref, s_ref = oracle.quantize_rows(ref)
+    ld = (cols + 63) // 64 * 64
+    xd, wd, bd = dev(torch, x), dev(torch, w), dev(torch, b)
+    qd = torch.full((rows, ld), 0x33, dtype=torch.int8, device="cuda")
+    sd = empty(torch, (rows,), torch.float32)
+    ok(lib, lib.dav2_hip_layer_norm_quantize_i8(ptr(qd), ld, ptr(sd), 0, ptr(xd), ptr(wd), ptr(bd), rows, cols, 1e-6,
+                                                 stream(torch)))
+    q = host(torch, qd)
+    assert np.array_equal(q[:, :cols], q_ref) and np.all(q[:, cols:] == 0)
+    assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("rows,cols,ld", [(384, 588, 640), (64, 432, 448), (1, 4, 16), (7, 36, 4096), (3, 64, 64)])

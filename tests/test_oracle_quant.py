@@ -27,6 +27,48 @@ def test_quantize_rows_hand_vectors(oracle):
     assert q[3].tolist() == [127, 0, 1, 2, -2, 4, -127, 0]
 
 
+def near_tie_rows(rows: int, cols: int, seed: int) -> np.ndarray:
+    """Rows whose quotients x / s fall within a few ulps of half-integers:
+    column 0 holds the row maximum A (s = A / 127), the others are
+    fl((k + 1/2) s) moved by -4..4 ulps, k in [-126, 125]."""
+    rng = np.random.default_rng(seed)
+    x = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        a = np.float32(rng.uniform(0.01, 50.0) * 2.0 ** rng.integers(-20, 20))
+        s = np.float32(max(a / np.float32(127.0), np.float32(1e-8)))
+        k = rng.integers(-126, 126, cols).astype(np.float32)
+        base = ((k + np.float32(0.5)) * s).astype(np.float32)
+        m = rng.integers(-4, 5, cols)
+        v = base.copy()
+        for step in range(4):
+            v = np.where(m > step, np.nextafter(v, np.float32(np.inf)), v)
+            v = np.where(m < -step, np.nextafter(v, np.float32(-np.inf)), v)
+        v = np.clip(v, -a, a)
+        v[0] = a
+        x[r] = v
+    return x
+
+
+def test_quantize_by_product_with_guard_equals_quotient():
+    # The GPU quantizers compute rne(clamp(x / s)) from x * fl(1 / s) and
+    # divide only where that product lies within 2^-14 of a half-integer
+    # (common.h quantize_div). Restated in float32 numpy against the IEEE
+    # quotient on rows built to sit at ties and a few ulps beside them.
+    x = near_tie_rows(64, 1024, 5)
+    absmax = np.abs(x).max(axis=1)
+    s = np.maximum(absmax / np.float32(127.0), np.float32(1e-8)).astype(np.float32)[:, None]
+    want = np.rint(np.clip(x / s, -127, 127))
+    inv = (np.float32(1.0) / s).astype(np.float32)
+    y = (x * inv).astype(np.float32)
+    n = np.rint(y)
+    slow = np.abs(y - n) > np.float32(0.5) - np.float32(2.0 ** -14)
+    got = np.where(slow, want, np.clip(n, -127, 127))
+    assert np.array_equal(got, want)
+    assert slow.mean() > 0.3  # the rows do exercise the division path
+    # without the guard the product alone rounds some of them the other way
+    assert not np.array_equal(np.clip(n, -127, 127), want)
+
+
 def test_quantize_rows_input_offset_skips_prefix(oracle):
     # project_tokens_int8 passes input_offset = D to skip the class token
     # (operators.cpp:1514-1522).
