@@ -154,20 +154,29 @@ __global__ __launch_bounds__(256) void ref_scores_kernel(const float* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Softmax, in place, one wave per row. The shader's 128 lanes become two
-// virtual lanes per thread (t and t + 64). Lane l visits items l, l + 128,
-// ... (columns, or packed words in binary16); a thread keeps up to CH items
-// per virtual lane in registers (CH = 0: the row is read again per pass).
-template <int CH, bool HALF>
+// Softmax, in place. The shader's 128 lanes L visit items L, L + 128, ...
+// (columns, or packed words in binary16). V = 2: one wave per row, each
+// thread holding virtual lanes t and t + 64; V = 1: two waves per row, wave
+// half h holding lane t + 64 h (long rows: half the registers per thread).
+// A thread keeps up to CH items per virtual lane in registers (CH = 0: the
+// row is read again per pass, and the exponentials are stored between the
+// passes as the shader does; with the row in registers that intermediate
+// store is never observable and is skipped).
+template <int CH, bool HALF, int V>
 __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t rows, uint32_t columns) {
-    const uint32_t t = threadIdx.x & 63u;
-    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 4u + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    static_assert(V == 1 || V == 2, "virtual lanes per thread");
+    constexpr uint32_t kRowsPerBlock = 2u * V;  // 4 waves
+    __shared__ float exchange[2][2][64];         // [row in block][max | partial][t]
+    const uint32_t t = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t slot = V == 2 ? wave : wave >> 1, half = V == 2 ? 0u : wave & 1u;
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * kRowsPerBlock + slot;
+    const bool live = row < rows;  // uniform per wave; both halves of a row agree
+    if (V == 2 && !live) return;
     const uint32_t items = HALF ? (columns + 1u) >> 1 : columns;
-    float* fr = HALF ? nullptr : static_cast<float*>(data) + row * items;
-    uint32_t* wr = HALF ? static_cast<uint32_t*>(data) + row * items : nullptr;
+    float* fr = HALF ? nullptr : static_cast<float*>(data) + (live ? row : 0u) * items;
+    uint32_t* wr = HALF ? static_cast<uint32_t*>(data) + (live ? row : 0u) * items : nullptr;
     constexpr int R = CH > 0 ? CH : 1;
-    float lo[2][R], hi[2][R];  // hi: the word's upper half (binary16)
+    float lo[V][R], hi[V][R];  // hi: the word's upper half (binary16)
 
     auto load = [&](uint32_t item, float& a, float& b) {
         if (HALF) {
@@ -185,72 +194,96 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
         if (HALF && item * 2u + 1u < columns) m = fmaxf(m, b);
         return m;
     };
+    auto lane_of = [&](int v) { return t + 64u * (V == 2 ? static_cast<uint32_t>(v) : half); };
 
     float maximum = -3.402823466e+38f;
+    if (live) {
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-        const uint32_t lane = t + 64u * v;
-        if (CH > 0) {
+        for (int v = 0; v < V; ++v) {
+            const uint32_t lane = lane_of(v);
+            if (CH > 0) {
 #pragma unroll
-            for (int k = 0; k < R; ++k) {
-                const uint32_t item = lane + 128u * k;
-                if (item < items) {
-                    load(item, lo[v][k], hi[v][k]);
-                    maximum = fold_max(maximum, item, lo[v][k], hi[v][k]);
+                for (int k = 0; k < R; ++k) {
+                    const uint32_t item = lane + 128u * k;
+                    if (item < items) {
+                        load(item, lo[v][k], hi[v][k]);
+                        maximum = fold_max(maximum, item, lo[v][k], hi[v][k]);
+                    }
                 }
-            }
-        } else {
-            for (uint32_t item = lane; item < items; item += 128u) {
-                float a, b;
-                load(item, a, b);
-                maximum = fold_max(maximum, item, a, b);
+            } else {
+                for (uint32_t item = lane; item < items; item += 128u) {
+                    float a, b;
+                    load(item, a, b);
+                    maximum = fold_max(maximum, item, a, b);
+                }
             }
         }
     }
     maximum = wave_max(maximum);  // order-free
+    if (V == 1) {
+        if (t == 0) exchange[slot][0][half] = maximum;
+        __syncthreads();
+        maximum = fmaxf(exchange[slot][0][0], exchange[slot][0][1]);
+    }
 
-    // exponentials, stored as they are produced; per-lane fp32 partials
-    float partial[2] = {0.0f, 0.0f};
+    // exponentials; per-lane fp32 partials
+    float partial[V];
     auto exponentials = [&](uint32_t item, float a, float b, float& ea, float& eb) {
         ea = exp_cw(a - maximum);
         if (HALF) {
             eb = item * 2u + 1u < columns ? exp_cw(b - maximum) : 0.0f;
-            wr[item] = pack_half2(ea, eb);
+            if (CH == 0) wr[item] = pack_half2(ea, eb);
             return ea + eb;
         }
-        fr[item] = ea;
+        if (CH == 0) fr[item] = ea;
         return ea;
     };
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-        const uint32_t lane = t + 64u * v;
+    for (int v = 0; v < V; ++v) {
+        const uint32_t lane = lane_of(v);
         float d = 0.0f;
-        if (CH > 0) {
+        if (live) {
+            if (CH > 0) {
 #pragma unroll
-            for (int k = 0; k < R; ++k) {
-                const uint32_t item = lane + 128u * k;
-                if (item < items) {
-                    float ea, eb;
-                    d = d + exponentials(item, lo[v][k], hi[v][k], ea, eb);
-                    lo[v][k] = ea;
-                    hi[v][k] = eb;
+                for (int k = 0; k < R; ++k) {
+                    const uint32_t item = lane + 128u * k;
+                    if (item < items) {
+                        float ea, eb;
+                        d = d + exponentials(item, lo[v][k], hi[v][k], ea, eb);
+                        lo[v][k] = ea;
+                        hi[v][k] = eb;
+                    }
                 }
-            }
-        } else {
-            for (uint32_t item = lane; item < items; item += 128u) {
-                float a, b, ea, eb;
-                load(item, a, b);
-                d = d + exponentials(item, a, b, ea, eb);
+            } else {
+                for (uint32_t item = lane; item < items; item += 128u) {
+                    float a, b, ea, eb;
+                    load(item, a, b);
+                    d = d + exponentials(item, a, b, ea, eb);
+                }
             }
         }
         partial[v] = d;
     }
-    // halving tree over the 128 partials: stride 64 inside the thread, then
-    // 32 .. 1 across lanes (lane t adds lane t + stride)
-    float sum = partial[0] + partial[1];
+    // halving tree over the 128 partials: stride 64 (lane t + lane t + 64),
+    // then 32 .. 1 across lanes (lane t adds lane t + stride)
+    float sum;
+    if (V == 2) {
+        sum = partial[0] + partial[V - 1];
+    } else {
+        if (half == 1) exchange[slot][1][t] = partial[0];
+        __syncthreads();
+        sum = partial[0] + exchange[slot][1][t];  // meaningful in half 0
+    }
 #pragma unroll
     for (int stride = 32; stride > 0; stride >>= 1) sum = sum + __shfl_down(sum, stride, kWave);
     sum = __shfl(sum, 0, kWave);
+    if (V == 1) {
+        __syncthreads();  // every partial has been read
+        if (half == 0 && t == 0) exchange[slot][1][0] = sum;
+        __syncthreads();
+        sum = exchange[slot][1][0];
+    }
+    if (!live) return;
     const float inverse = div_rn(1.0f, fmaxf(sum, 1.0e-20f));
 
     auto normalize = [&](uint32_t item, float ea, float eb) {
@@ -264,8 +297,8 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
         }
     };
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-        const uint32_t lane = t + 64u * v;
+    for (int v = 0; v < V; ++v) {
+        const uint32_t lane = lane_of(v);
         if (CH > 0) {
 #pragma unroll
             for (int k = 0; k < R; ++k) {
@@ -382,19 +415,21 @@ template <bool HALF>
 hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream_t s) {
     const uint32_t items = HALF ? (columns + 1u) >> 1 : columns;
     const uint32_t per_lane = (items + 127u) / 128u;
-    const dim3 grid(static_cast<uint32_t>((rows + 3u) / 4u)), block(256);
-#define DAV2_SOFTMAX_CASE(N)                                                              \
-    if (per_lane <= N) {                                                                  \
-        dispatch((ref_softmax_kernel<N, HALF>), grid, block, 0, s, data, rows, columns); \
-        return hipGetLastError();                                                         \
+    const dim3 grid(static_cast<uint32_t>((rows + 3u) / 4u)), grid2(static_cast<uint32_t>((rows + 1u) / 2u)),
+        block(256);
+    // rows of up to 12 items per lane: one wave per row; longer ones: two
+#define DAV2_SOFTMAX_CASE(N, V)                                                                        \
+    if (per_lane <= N) {                                                                               \
+        dispatch((ref_softmax_kernel<N, HALF, V>), V == 2 ? grid : grid2, block, 0, s, data, rows, columns); \
+        return hipGetLastError();                                                                      \
     }
-    DAV2_SOFTMAX_CASE(4)
-    DAV2_SOFTMAX_CASE(8)
-    DAV2_SOFTMAX_CASE(12)
-    DAV2_SOFTMAX_CASE(24)
-    DAV2_SOFTMAX_CASE(48)
+    DAV2_SOFTMAX_CASE(4, 2)
+    DAV2_SOFTMAX_CASE(8, 2)
+    DAV2_SOFTMAX_CASE(12, 2)
+    DAV2_SOFTMAX_CASE(24, 1)
+    DAV2_SOFTMAX_CASE(48, 1)
 #undef DAV2_SOFTMAX_CASE
-    dispatch((ref_softmax_kernel<0, HALF>), grid, block, 0, s, data, rows, columns);
+    dispatch((ref_softmax_kernel<0, HALF, 2>), grid, block, 0, s, data, rows, columns);
     return hipGetLastError();
 }
 
