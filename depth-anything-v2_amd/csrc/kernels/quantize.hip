@@ -19,7 +19,8 @@ namespace {
 constexpr int kRowsPerBlock = 4;
 
 // ---------------------------------------------------------------------------
-// Per-row quantization, quantize_rows_int8_fused.glsl:20-55. q = rne(clamp(x / s)).
+// Per-row quantization, quantize_rows_int8_fused.glsl:20-55. q = rne(clamp(x / s))
+// (the IEEE quotient, through quantize_div).
 // WPR waves share a row (kRowsPerBlock / WPR rows per workgroup): wave part
 // p owns float4 chunks p*64*CH + lane + 64j (j < CH) kept in VGPRs; the row
 // maximum is the maximum of the parts' maxima (exact, order-free).
@@ -52,15 +53,15 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_kernel(
         for (int i = 0; i < WPR; ++i) absmax = fmaxf(absmax, part_max[first + i]);
     }
     if (!live) return;
-    const float s = row_scale(absmax);
+    const float s = row_scale(absmax), inv = div_rn(1.0f, s);
     if (lane == 0 && part == 0) scales[row] = s;
     uint32_t* out = reinterpret_cast<uint32_t*>(q + static_cast<uint64_t>(row) * ldq);
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
         const uint32_t w = w0 + lane + 64u * j;
         if (w < words)
-            out[w] = pack4(quantize_rne(v[j].x / s), quantize_rne(v[j].y / s),
-                           quantize_rne(v[j].z / s), quantize_rne(v[j].w / s));
+            out[w] = pack4(quantize_div(v[j].x, s, inv), quantize_div(v[j].y, s, inv),
+                           quantize_div(v[j].z, s, inv), quantize_div(v[j].w, s, inv));
     }
     if (part == 0)
         for (uint32_t w = words + lane; w < (ldq >> 2); w += 64u) out[w] = 0u;
@@ -82,13 +83,13 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_long_kernel(
         absmax = fmaxf(absmax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
     absmax = wave_max(absmax);
-    const float s = row_scale(absmax);
+    const float s = row_scale(absmax), inv = div_rn(1.0f, s);
     if (lane == 0) scales[row] = s;
     uint32_t* out = reinterpret_cast<uint32_t*>(q + static_cast<uint64_t>(row) * ldq);
     for (uint32_t w = lane; w < words; w += 64u) {
         const float4 v = *reinterpret_cast<const float4*>(x + 4u * w);
-        out[w] = pack4(quantize_rne(v.x / s), quantize_rne(v.y / s), quantize_rne(v.z / s),
-                       quantize_rne(v.w / s));
+        out[w] = pack4(quantize_div(v.x, s, inv), quantize_div(v.y, s, inv), quantize_div(v.z, s, inv),
+                       quantize_div(v.w, s, inv));
     }
     for (uint32_t w = words + lane; w < (ldq >> 2); w += 64u) out[w] = 0u;
 }
@@ -464,7 +465,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
     }
     if (QUANT) {
         absmax = wave_max(absmax);
-        const float sc = row_scale(absmax);
+        const float sc = row_scale(absmax), inv_sc = div_rn(1.0f, sc);
         if (lane == 0) scales[row] = sc;
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -473,8 +474,8 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
         const uint32_t words = columns >> 2;
         for (uint32_t w = lane; w < words; w += 64u) {
             const float4 t = *reinterpret_cast<const float4*>(stage + 4u * w);
-            qo[w] = pack4(quantize_rne(t.x / sc), quantize_rne(t.y / sc), quantize_rne(t.z / sc),
-                          quantize_rne(t.w / sc));
+            qo[w] = pack4(quantize_div(t.x, sc, inv_sc), quantize_div(t.y, sc, inv_sc),
+                          quantize_div(t.z, sc, inv_sc), quantize_div(t.w, sc, inv_sc));
         }
         for (uint32_t w = words + lane; w < (ldq >> 2); w += 64u) qo[w] = 0u;
     }
