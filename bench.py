@@ -155,7 +155,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=30.0)
     ap.add_argument("--profile-json", default="")
-    ap.add_argument("--no-fp32-mode", action="store_true", help="skip the FORCE_FP32 comparison run")
+    ap.add_argument("--no-fp32-mode", action="store_true", help="skip the FORCE_FP32 / FORCE_FP16 / REFERENCE_FP16_ATTENTION comparison runs")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the batch-8 / 1036x1036 kernel measurements")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -299,23 +299,29 @@ def main() -> int:
         depth = out.cpu().numpy()
         ctx.close()
 
-        # The fp32 precision mode (FORCE_FP32) on the same model and input:
-        # a short run, reported beside the int8 headline.
-        fp32_rate = None
-        if args.batch == 1 and not args.no_fp32_mode:
-            with pkg.Context(str(model), args.encoder, pkg.FORCE_FP32) as ctx32:
-                def step32():
-                    ctx32.infer_device(x.data_ptr(), 1, args.size, args.size, out.data_ptr(), n_out, stream)
+        # The other precision / attention modes on the same model and input:
+        # short runs, reported beside the int8 headline (FORCE_FP32, FORCE_FP16,
+        # and the int8 graph with the reference's materialised binary16
+        # attention, REFERENCE_FP16_ATTENTION).
+        def mode_rate(flags, steps):
+            with pkg.Context(str(model), args.encoder, flags) as cm:
+                def stepm():
+                    cm.infer_device(x.data_ptr(), 1, args.size, args.size, out.data_ptr(), n_out, stream)
 
                 for _ in range(2):
-                    step32()
+                    stepm()
                 torch.cuda.synchronize()
                 f0 = time.perf_counter()
-                fp32_steps = 5
-                for _ in range(fp32_steps):
-                    step32()
+                for _ in range(steps):
+                    stepm()
                 torch.cuda.synchronize()
-                fp32_rate = fp32_steps / (time.perf_counter() - f0)
+                return steps / (time.perf_counter() - f0)
+
+        fp32_rate = fp16_rate = ref16_rate = None
+        if args.batch == 1 and not args.no_fp32_mode:
+            fp32_rate = mode_rate(pkg.FORCE_FP32, 5)
+            fp16_rate = mode_rate(pkg.FORCE_FP16, 5)
+            ref16_rate = mode_rate(pkg.REFERENCE_FP16_ATTENTION, 10)
 
         gemm = prof.get("gemm_i8", {})
         g_ms = gemm.get("ms", 0.0)
@@ -393,6 +399,8 @@ def main() -> int:
         "extra_configs": extra,
         "image_paths": image_paths,
         "fp32_mode_images_per_s": fp32_rate,
+        "fp16_mode_images_per_s": fp16_rate,
+        "reference_fp16_attention_images_per_s": ref16_rate,
         "depth_finite": bool(np.isfinite(depth).all()),
         "cpu_baseline": cpu,
     }
