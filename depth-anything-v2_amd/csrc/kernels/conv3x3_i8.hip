@@ -96,13 +96,18 @@ DAV2_DEV uint32_t quant4_bytes(float a, float b, float c, float d, float inv) {
     return w;
 }
 
-template <int BN, int WM, int WN, bool RELU_IN>
-__global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
+// SB (narrow channel tiles, whose registers allow two waves per SIMD): one
+// operand buffer instead of two, so that two workgroups share a CU; a block's
+// MFMAs and the next block's quantization then take turns inside a
+// workgroup, and the other workgroup's work (or its load latency) fills the
+// gaps.
+template <int BN, int WM, int WN, bool RELU_IN, bool SB = (BN <= 64)>
+__global__ __launch_bounds__(256, SB ? 2 : 1) void conv3x3_i8_kernel(ConvParams g) {
     constexpr int PW = kPixT / WM, NW = BN / WN, PB = PW / 16, NB = NW / 16;
     constexpr int kRing = 3;  // weight fragments three steps ahead (9 % 3 == 0)
     static_assert(WM * WN == 4 && PW % 16 == 0 && NW % 16 == 0, "wave tiling");
 
-    __shared__ __attribute__((aligned(16))) int8_t at[2 * kBufBytes];
+    __shared__ __attribute__((aligned(16))) int8_t at[(SB ? 1 : 2) * kBufBytes];
     __shared__ float amax_lds[4 * 64];
     __shared__ float sc_lds[kPixT];
     __shared__ float wsc_lds[BN], bias_lds[BN];
@@ -170,28 +175,38 @@ __global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
 
     const uint32_t nblocks = cblocks, nsteps = ksteps;
     v4i ring[kRing][NB];
-    // Block 0's values and the first weight fragments are in flight while
-    // the scales are formed.
+
+    // ---- per-pixel scales: window maxima of the channel-group maxima -----
+    // Thread t: window row t / 64 (image row y0 - 1 + t/64), window column
+    // t % 64 (image column x0 - 2 + t%64); positions outside the image read
+    // as zero (the padding: an offset past the buffer). The first eight
+    // groups' maxima are loaded before block 0's values and the first weight
+    // fragments, which then stay in flight while the scales are formed
+    // (loads return in issue order).
+    float gmax[8];
+    const int agy = static_cast<int>(y0) + static_cast<int>(tid >> 6) - 1;
+    const int agx = static_cast<int>(x0) + static_cast<int>(lane) - 2;
+    const bool a_in = agy >= 0 && agy < H && agx >= 0 && agx < W;
+    {
+        const auto prs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.partial), static_cast<short>(0),
+                                                           static_cast<int>(g.groups * plane4), 0x00020000);
+        const uint32_t aoff = a_in ? (static_cast<uint32_t>(agy) * g.width + static_cast<uint32_t>(agx)) * 4u
+                                   : kOutside;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            gmax[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                    prs, aoff, min(static_cast<uint32_t>(k), g.groups - 1u) * plane4, 0));
+    }
 #pragma unroll
     for (int wr = 0; wr < 4; ++wr) issue_row(0, wr);
 #pragma unroll
     for (int d = 0; d < kRing; ++d) load_w(ring[d], min(static_cast<uint32_t>(d), nsteps - 1));
-
-    // ---- per-pixel scales: window maxima of the channel-group maxima -----
-    // Thread t: window row t / 64 (image row y0 - 1 + t/64), window column
-    // t % 64 (image column x0 - 2 + t%64); positions outside the image are
-    // padding zeros. The group maxima are loaded together, then reduced.
     {
-        const int gy = static_cast<int>(y0) + static_cast<int>(tid >> 6) - 1;
-        const int gx = static_cast<int>(x0) + static_cast<int>(lane) - 2;
         float t = 0.0f;
-        if (gy >= 0 && gy < H && gx >= 0 && gx < W) {
-            const float* src = g.partial + static_cast<uint64_t>(gy) * g.width + gx;
-            float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = static_cast<uint32_t>(k) < g.groups ? src[k * g.plane] : 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) t = fmaxf(t, v[k]);
+        for (int k = 0; k < 8; ++k) t = fmaxf(t, gmax[k]);
+        if (a_in) {
+            const float* src = g.partial + static_cast<uint64_t>(agy) * g.width + agx;
             for (uint32_t k = 8; k < g.groups; ++k) t = fmaxf(t, src[k * g.plane]);
         }
         amax_lds[tid] = t;
@@ -288,7 +303,40 @@ __global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
     };
     constexpr int kUnitsPerChunk = 8 / PB;
     static_assert(PB * kUnitsPerChunk == 8, "quantizer units per MFMA chunk");
-    for (uint32_t cb = 0; cb < nblocks; ++cb) {
+    for (uint32_t cb = 0; SB && cb < nblocks; ++cb) {
+        // loads past the last block re-read it (unconditional prefetches)
+        const uint32_t ahead = min(cb + 2, nblocks - 1);
+#pragma unroll
+        for (int j = 0; j < PB; ++j) read_frag(j, at);
+#pragma unroll
+        for (int tap = 0; tap < kTaps; ++tap) {
+            const uint32_t step = cb * kTaps + tap;
+            v4i (&bw)[NB] = ring[tap % kRing];
+#pragma unroll
+            for (int j = 0; j < PB; ++j) {
+#pragma unroll
+                for (int i = 0; i < NB; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[i], bp[j], acc[i][j], 0, 0, 0);
+                if (tap + 1 < kTaps) read_frag(j, at + (tap + 1) * kTapBytes);
+            }
+            load_w(bw, min(step + kRing, nsteps - 1));
+        }
+        if (cb + 1 == nblocks) break;
+        lds_barrier();  // every wave has read block cb's tile
+        // block cb + 1's tile into the same buffer; a window row whose last
+        // piece is done takes block cb + 2's values
+#pragma unroll
+        for (int tap = 0; tap < kTaps; ++tap) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) quant_unit(at, tap, u);
+            if (tap == 1) issue_row(ahead, 0);
+            if (tap == 4) issue_row(ahead, 1);
+            if (tap == 7) issue_row(ahead, 2);
+            if (tap == 8) issue_row(ahead, 3);
+        }
+        lds_barrier();
+    }
+    for (uint32_t cb = 0; !SB && cb < nblocks; ++cb) {
         // loads past the last block re-read it (unconditional prefetches)
         const uint32_t ahead = min(cb + 2, nblocks - 1);
         const int8_t* cur = at + (cb & 1u) * kBufBytes;
@@ -337,6 +385,7 @@ __global__ __launch_bounds__(256, 1) void conv3x3_i8_kernel(ConvParams g) {
                                   });
 }
 
+// (BN <= 64: the single-buffered kernel, two workgroups per CU)
 template <int BN, int WM, int WN>
 void launch(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
     if (g.flags & DAV2_CONV_RELU_INPUT)

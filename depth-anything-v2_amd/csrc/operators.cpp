@@ -666,9 +666,12 @@ void HipOperators::project_tokens_int8(DeviceBuffer& output, const DeviceBuffer&
 bool HipOperators::implicit_conv(std::uint32_t width, std::uint32_t height, std::uint32_t channels,
                                  std::uint32_t output_channels, std::uint32_t kernel, std::uint32_t stride,
                                  std::uint32_t padding) {
-    // Maps narrower than the implicit GEMM's 64-pixel row tiles (37x37, 19x19
-    // in the DPT head) run faster as im2col + GEMM.
-    return width >= 64 &&
+    // 3x3 convolutions of maps narrower than the implicit GEMM's 64-pixel row
+    // tiles (37x37, 19x19 in the DPT head) run as fast or faster as im2col +
+    // GEMM with split K (ViT-L's 19x19 layer4_rn: 33 against 74 us); a 1x1
+    // convolution of such a map is faster implicit (37x37, 256 channels: 8.6
+    // against 23 us for channel maxima + im2col + GEMM).
+    return (width >= 64 || kernel == 1) &&
            dav2_hip_conv2d_i8_supported(width, height, channels, output_channels, kernel, stride, padding) != 0;
 }
 
