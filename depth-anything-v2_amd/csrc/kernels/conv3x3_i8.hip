@@ -96,12 +96,12 @@ DAV2_DEV uint32_t quant4_bytes(float a, float b, float c, float d, float inv) {
     return w;
 }
 
-// SB (narrow channel tiles, whose registers allow two waves per SIMD): one
-// operand buffer instead of two, so that two workgroups share a CU; a block's
-// MFMAs and the next block's quantization then take turns inside a
-// workgroup, and the other workgroup's work (or its load latency) fills the
-// gaps.
-template <int BN, int WM, int WN, bool RELU_IN, bool SB = (BN <= 64)>
+// SB (channel tiles of at most 128, whose registers then allow two waves
+// per SIMD): one operand buffer instead of two, so that two workgroups
+// share a CU; a block's MFMAs and the next block's quantization then take
+// turns inside a workgroup, and the other workgroup's work (or its load
+// latency) fills the gaps.
+template <int BN, int WM, int WN, bool RELU_IN, bool SB>
 __global__ __launch_bounds__(256, SB ? 2 : 1) void conv3x3_i8_kernel(ConvParams g) {
     constexpr int PW = kPixT / WM, NW = BN / WN, PB = PW / 16, NB = NW / 16;
     constexpr int kRing = 3;  // weight fragments three steps ahead (9 % 3 == 0)
@@ -385,23 +385,26 @@ __global__ __launch_bounds__(256, SB ? 2 : 1) void conv3x3_i8_kernel(ConvParams 
                                   });
 }
 
-// (BN <= 64: the single-buffered kernel, two workgroups per CU)
-template <int BN, int WM, int WN>
+template <int BN, int WM, int WN, bool SB>
 void launch(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
     if (g.flags & DAV2_CONV_RELU_INPUT)
-        dispatch((conv3x3_i8_kernel<BN, WM, WN, true>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+        dispatch((conv3x3_i8_kernel<BN, WM, WN, true, SB>), dim3(tiles, n / BN), dim3(256), 0, s, g);
     else
-        dispatch((conv3x3_i8_kernel<BN, WM, WN, false>), dim3(tiles, n / BN), dim3(256), 0, s, g);
+        dispatch((conv3x3_i8_kernel<BN, WM, WN, false, SB>), dim3(tiles, n / BN), dim3(256), 0, s, g);
 }
 
 }  // namespace
 
 // 256 output channels: each wave 128 pixels x 64 channels; narrower maps:
-// 2 x 2 waves of 64 pixels (one tile row) x BN/2 channels.
+// 2 x 2 waves of 64 pixels (one tile row) x BN/2 channels. 64 or 32 output
+// channels: single-buffered, two workgroups per CU; 128: single-buffered
+// from two workgroups per CU on (296x296, 256 -> 128: 86 -> 72 us), else
+// double-buffered (150x150: 29 against 30 us).
 hipError_t dav2k::launch_conv3x3_i8(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
-    if (n % 256 == 0) launch<256, 1, 4>(g, tiles, n, s);
-    else if (n % 128 == 0) launch<128, 2, 2>(g, tiles, n, s);
-    else if (n % 64 == 0) launch<64, 2, 2>(g, tiles, n, s);
-    else launch<32, 2, 2>(g, tiles, n, s);
+    if (n % 256 == 0) launch<256, 1, 4, false>(g, tiles, n, s);
+    else if (n % 128 == 0 && static_cast<uint64_t>(tiles) * (n / 128) >= 512) launch<128, 2, 2, true>(g, tiles, n, s);
+    else if (n % 128 == 0) launch<128, 2, 2, false>(g, tiles, n, s);
+    else if (n % 64 == 0) launch<64, 2, 2, true>(g, tiles, n, s);
+    else launch<32, 2, 2, true>(g, tiles, n, s);
     return hipGetLastError();
 }

@@ -153,7 +153,9 @@ def test_im2col_quantize_relu_bit_exact(gpu, lib, oracle, c, h, w, k):
                                                 (128, 100, 330, 128, 1, True), (128, 518, 518, 32, 3, True),
                                                 (192, 19, 20, 96, 3, True), (64, 3, 6, 32, 3, True),
                                                 (64, 7, 121, 64, 3, True), (256, 75, 74, 256, 3, True),
-                                                (128, 4, 62, 128, 3, False), (64, 1, 64, 256, 3, True)])
+                                                (128, 4, 62, 128, 3, False), (64, 1, 64, 256, 3, True),
+                                                # 128 output channels over >= 512 tiles: single-buffered
+                                                (128, 208, 244, 128, 3, False)])
 def test_conv2d_i8_matches_im2col_gemm(gpu, pkg, lib, oracle, c, h, w, n, k, has_bias):
     torch = gpu
     _announce("conv2d_i8", c, h, w, n, k, has_bias)
