@@ -395,15 +395,14 @@ void launch(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
 
 }  // namespace
 
-// 256 output channels: each wave 128 pixels x 64 channels; narrower maps:
-// 2 x 2 waves of 64 pixels (one tile row) x BN/2 channels. 64 or 32 output
-// channels: single-buffered, two workgroups per CU; 128: single-buffered
-// from two workgroups per CU on (296x296, 256 -> 128: 86 -> 72 us), else
-// double-buffered (150x150: 29 against 30 us).
+// 256 output channels over at least 128 tiles: each wave 128 pixels x 64
+// channels, double-buffered, one workgroup per CU. Otherwise 2 x 2 waves of
+// 64 pixels (one tile row) x BN/2 channels, single-buffered, two workgroups
+// per CU (296x296, 256 -> 128: 86 -> 72 us; 74x74, 256 -> 256 as two
+// 128-channel tiles: 31 -> 26 us; 518x518, 128 -> 32: 139 -> 88 us).
 hipError_t dav2k::launch_conv3x3_i8(const ConvParams& g, uint32_t tiles, uint32_t n, hipStream_t s) {
-    if (n % 256 == 0) launch<256, 1, 4, false>(g, tiles, n, s);
-    else if (n % 128 == 0 && static_cast<uint64_t>(tiles) * (n / 128) >= 512) launch<128, 2, 2, true>(g, tiles, n, s);
-    else if (n % 128 == 0) launch<128, 2, 2, false>(g, tiles, n, s);
+    if (n % 256 == 0 && tiles >= 128) launch<256, 1, 4, false>(g, tiles, n, s);
+    else if (n % 128 == 0) launch<128, 2, 2, true>(g, tiles, n, s);
     else if (n % 64 == 0) launch<64, 2, 2, true>(g, tiles, n, s);
     else launch<32, 2, 2, true>(g, tiles, n, s);
     return hipGetLastError();
