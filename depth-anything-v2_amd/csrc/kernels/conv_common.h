@@ -94,8 +94,26 @@ DAV2_DEV void store_tile(const ConvParams& g, const v4i (&acc)[BN / WN / 16][PIX
         for (int q = 0; q < (kEmitGroups > 0 ? kEmitGroups : 1); ++q) gmax[j][q] = 0.0f;
     auto epilogue = [&](auto residual_tag, auto relu_tag) {
         constexpr bool kResidual = decltype(residual_tag)::value, kRelu = decltype(relu_tag)::value;
+        // The residual of pixel block j + 1 is loaded while block j is
+        // stored (one round trip per two blocks instead of one per block);
+        // pixels outside the map load pixel 0 (never stored).
+        float res[2][kResidual ? NB : 1][4];
+        auto load_res = [&](int j, float (&dst)[kResidual ? NB : 1][4]) {
+            uint64_t pixel;
+            if (!locate(wm * PW + 16u * j + (lane & 15u), pixel)) pixel = 0;
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t cl = wn * NW + 16u * i + 4u * (lane >> 4) + r;
+                    dst[i][r] = g.residual[static_cast<uint64_t>(nb * BN + cl) * g.plane + pixel];
+                }
+        };
+        if constexpr (kResidual) load_res(0, res[0]);
 #pragma unroll
         for (int j = 0; j < PB; ++j) {
+            if constexpr (kResidual)
+                if (j + 1 < PB) load_res(j + 1, res[(j + 1) & 1]);
             const uint32_t p = wm * PW + 16u * j + (lane & 15u);
             uint64_t pixel;
             if (!locate(p, pixel)) continue;
@@ -110,7 +128,7 @@ DAV2_DEV void store_tile(const ConvParams& g, const v4i (&acc)[BN / WN / 16][PIX
                     v = v * wsc_lds[cl];
                     v = v + bias_lds[cl];
                     const uint64_t idx = static_cast<uint64_t>(nb * BN + cl) * g.plane + pixel;
-                    if (kResidual) v = v + g.residual[idx];
+                    if constexpr (kResidual) v = v + res[j & 1][i][r];
                     if (kRelu) v = fmaxf(v, 0.0f);
                     g.out[idx] = v;
                     if constexpr (kEmitGroups > 0) {
