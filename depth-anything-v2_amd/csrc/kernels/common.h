@@ -181,6 +181,16 @@ DAV2_DEV float gelu_erfcc(float value) {
     return 0.5f * value * (1.0f + erf_value);
 }
 
+// Nontemporal store for an output that the next kernel reads: it goes
+// straight to memory instead of waiting in this XCD's L2 for the write-back
+// at the kernel's end. (Measured per kernel: it helps the GEMM's row-major
+// outputs, and slows the convolutions and the resize, whose consumers read
+// part of their output back through the same L2.)
+DAV2_DEV void store_nt(float* dst, float4 v) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(f4{v.x, v.y, v.z, v.w}, reinterpret_cast<f4*>(dst));
+}
+
 // Timing hook for profiling (dav2_hip_launch_events): the calling thread's
 // next kernel launch records `start` when it begins, and every launch until
 // the hook is cleared records `stop` when it ends (an event keeps its last
