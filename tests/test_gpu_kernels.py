@@ -222,12 +222,14 @@ def test_conv2d_i8_matches_oracle(gpu, pkg, lib, oracle):
 
 
 @pytest.mark.parametrize("flags,with_residual", [(1, False), (2, False), (3, False), (0, True), (2, True)])
-def test_conv2d_i8_fusions(gpu, pkg, lib, oracle, flags, with_residual):
+@pytest.mark.parametrize("c,h,w,n", [(128, 20, 90, 128), (64, 90, 150, 256), (128, 9, 61, 64)])
+def test_conv2d_i8_fusions(gpu, pkg, lib, oracle, flags, with_residual, c, h, w, n):
     # relu(input) -> conv -> + residual -> relu, each step as its own kernel
-    # (relu.glsl, add.glsl), against the flags of the fused kernel.
+    # (relu.glsl, add.glsl), against the flags of the fused kernel: the
+    # single-buffered 128-channel tiles, the double-buffered 256-channel ones
+    # and the one-row kernel of odd widths.
     torch = gpu
-    _announce("conv2d_i8 fusions", flags, with_residual)
-    c, h, w, n = 128, 20, 90, 128
+    _announce("conv2d_i8 fusions", flags, with_residual, c, h, w, n)
     rng = np.random.default_rng(flags * 7 + with_residual)
     x = rng.standard_normal((c, h, w)).astype(np.float32)
     res = rng.standard_normal((n, h * w)).astype(np.float32)
