@@ -188,6 +188,18 @@ DAV2_DEV void store_one(const GemmParams& g, const EpilogueOperands<EPI, TM, TN>
     g.out[idx] = row_value<EPI, TM, TN>(e, i, j, r, v);
 }
 
+// Waits until at most `later` stages' copies (LPW per stage and wave) are
+// outstanding; later <= MAX (the counts must be immediates).
+template <int MAX, int LPW>
+DAV2_DEV void wait_stages(int later) {
+    if constexpr (MAX <= 0) {
+        DAV2_WAIT_VMCNT(0);
+    } else {
+        if (later >= MAX) DAV2_WAIT_VMCNT(MAX * LPW);
+        else wait_stages<MAX - 1, LPW>(later);
+    }
+}
+
 // Tile index of this workgroup. Workgroups are dealt to the 8 XCDs round
 // robin (id % 8); remap so that each XCD owns one contiguous run of tiles,
 // ordered along M first: the tiles of one weight-column band then share that
@@ -227,7 +239,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
     constexpr int LOADS = (BM + BN) / RPL;        // per stage, all waves
     constexpr int LOADS_PER_WAVE = LOADS / NW;
     static_assert(BK == 64 || BK == 128 || BK == 256, "stage depth");
-    static_assert(STAGES >= 2 && STAGES <= 4 && 2 * LOADS_PER_WAVE < 64, "pipeline depth / vmcnt range");
+    static_assert(STAGES >= 2 && STAGES <= 8 && (STAGES - 2) * LOADS_PER_WAVE < 64, "pipeline depth / vmcnt range");
     static_assert(LOADS % NW == 0 && BM % RPL == 0, "stage rows must split evenly over the waves");
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one MFMA block");
 
@@ -301,14 +313,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
         // outstanding
         // loads complete in order: after stage ks only the stages issued
         // after it (at most STAGES - 2 of them) may still be in flight
-        const int later = min(STAGES - 2, ksteps - 1 - ks);
-        if (later >= 2) {
-            DAV2_WAIT_VMCNT(2 * LOADS_PER_WAVE);
-        } else if (later == 1) {
-            DAV2_WAIT_VMCNT(LOADS_PER_WAVE);
-        } else {
-            DAV2_WAIT_VMCNT(0);
-        }
+        wait_stages<STAGES - 2, LOADS_PER_WAVE>(min(STAGES - 2, ksteps - 1 - ks));
         // Plain barrier: the wait above already covers this wave's copies of
         // stage ks, and the slot refilled next was last read by operands the
         // MFMAs of the previous stage consumed. (__syncthreads would also
