@@ -274,9 +274,7 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
         __syncthreads();
         sum = partial[0] + exchange[slot][1][t];  // meaningful in half 0
     }
-#pragma unroll
-    for (int stride = 32; stride > 0; stride >>= 1) sum = sum + __shfl_down(sum, stride, kWave);
-    sum = __shfl(sum, 0, kWave);
+    sum = wave_sum_tree(sum);
     if (V == 1) {
         __syncthreads();  // every partial has been read
         if (half == 0 && t == 0) exchange[slot][1][0] = sum;

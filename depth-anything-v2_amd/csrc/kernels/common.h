@@ -16,26 +16,37 @@ typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
-// Butterfly reductions. After the xor butterfly every lane holds the full
-// result, but each lane's association order differs; lane 0's order equals a
-// shared-memory tree reduction over widths 32,16,...,1 (partial[l] +=
-// partial[l+w]). Broadcasting lane 0 therefore reproduces the tree bit for bit.
+// Wave reductions as the halving tree partial[l] = op(partial[l],
+// partial[l + w]) for w = 32, 16, ..., 1, the order of a shared-memory tree
+// reduction; lane 0 ends with the result and every lane receives it. The
+// moves stay in the VALU: lanes 32-63 reach lanes 0-31 through
+// v_permlane32_swap, lanes 16-31 reach 0-15 through v_permlane16_swap, and
+// the steps within a row of 16 lanes are DPP row shifts (lanes that would
+// read past their row get 0, and only lanes whose results feed lane 0 are
+// meaningful). Every lane of the wave must be active.
+template <typename Op>
+DAV2_DEV float wave_tree(float v, Op op) {
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(v, __uint_as_float(p32[1]));
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(v, __uint_as_float(p16[1]));
+    v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, true)));  // row_shl:8
+    v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xF, 0xF, true)));  // row_shl:4
+    v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x102, 0xF, 0xF, true)));  // row_shl:2
+    v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xF, 0xF, true)));  // row_shl:1
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+
 DAV2_DEV float wave_sum_tree(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, kWave);
-    return __shfl(v, 0, kWave);
+    return wave_tree(v, [](float a, float b) { return a + b; });
 }
 
 DAV2_DEV float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    return wave_tree(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 DAV2_DEV float wave_min(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
-    return v;
+    return wave_tree(v, [](float a, float b) { return fminf(a, b); });
 }
 
 // Reference quantization step (quantize_rows_int8_fused.glsl:46-50 and
@@ -111,11 +122,20 @@ DAV2_DEV float row_scale(float absmax) { return fmaxf(absmax / 127.0f, 1.0e-8f);
 // so both round to the same integer whenever the product is more than 2^-14
 // from a half-integer; the other lanes (about 1 in 8000) divide. NaN and
 // infinite x or s give the quotient's result as well (clamped NaN is -127).
-DAV2_DEV int quantize_div(float x, float s, float inv) {
+// quantize_product is the first step alone: q = the clamped rint(x * inv),
+// and true where the product lies within 2^-14 of a half-integer, so that
+// only quantize_div's quotient may decide.
+DAV2_DEV bool quantize_product(float x, float inv, int& q) {
     const float y = x * inv;
     const float n = __builtin_rintf(y);
-    if (__builtin_expect(fabsf(y - n) > 0.5f - 0x1p-14f, 0)) return quantize_rne(div_rn(x, s));
-    return static_cast<int>(fminf(fmaxf(n, -127.0f), 127.0f));
+    q = static_cast<int>(fminf(fmaxf(n, -127.0f), 127.0f));
+    return fabsf(y - n) > 0.5f - 0x1p-14f;
+}
+
+DAV2_DEV int quantize_div(float x, float s, float inv) {
+    int q;
+    if (__builtin_expect(quantize_product(x, inv, q), 0)) return quantize_rne(div_rn(x, s));
+    return q;
 }
 
 // Per-pixel |x| maxima of a CHW map over groups of kGroupChannels channels:

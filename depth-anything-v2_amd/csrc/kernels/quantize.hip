@@ -385,14 +385,21 @@ __global__ __launch_bounds__(256) void im2col1x1_kernel(const float* __restrict_
 // tree, so sums, mean and variance match the reference order exactly.
 // CH = ceil(columns / 64) values kept per lane (0 = re-read from memory).
 // With QUANT the normalised row is also quantized (per-row rule above) into q/scales;
-// out may then be null.
-template <int CH, bool QUANT>
+// out may then be null. EXACT: columns == 64 * CH, a compile-time constant
+// (no partial column block, constant offsets, and for 1024 columns the
+// divisions by the width become exact multiplications). For CH > 0 the
+// quantized bytes go from registers straight to memory (lane l stores
+// columns l, l + 64, ...; a wave's 64 bytes form one segment); CH = 0
+// stages the normalised row in LDS.
+template <int CH, bool QUANT, bool EXACT>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
     const float* __restrict__ input, const float* __restrict__ weight,
-    const float* __restrict__ bias, uint32_t rows, uint32_t columns, float epsilon,
+    const float* __restrict__ bias, uint32_t rows, uint32_t width, float epsilon,
     float* __restrict__ out, int8_t* __restrict__ q, uint32_t ldq,
     float* __restrict__ scales) {
+    static_assert(!EXACT || CH > 0, "EXACT needs the row in registers");
     extern __shared__ float lds_rows[];
+    const uint32_t columns = EXACT ? 64u * CH : width;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t row = blockIdx.x * kRowsPerBlock + wave;
@@ -406,12 +413,13 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
         // first use, so the row, weight and bias arrive in one round trip;
         // columns past the row end are masked out of the sums by selects.
         const uint32_t last = columns - 1u;
+        auto at = [&](int j) { return EXACT ? lane + 64u * j : min(lane + 64u * j, last); };
 #pragma unroll
-        for (int j = 0; j < kKept; ++j) v[j] = x[min(lane + 64u * j, last)];
+        for (int j = 0; j < kKept; ++j) v[j] = x[at(j)];
 #pragma unroll
         for (int j = 0; j < kKept; ++j) {
-            wv[j] = weight[min(lane + 64u * j, last)];
-            bv[j] = bias[min(lane + 64u * j, last)];
+            wv[j] = weight[at(j)];
+            bv[j] = bias[at(j)];
         }
         // Tie the row values to the weight and bias loads so the compiler
         // cannot sink those loads below the reductions (a second memory
@@ -420,7 +428,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
         for (int j = 0; j < kKept; ++j) asm volatile("" : "+v"(v[j]) : "v"(wv[j]), "v"(bv[j]));
 #pragma unroll
         for (int j = 0; j < kKept; ++j) {
-            const bool in = lane + 64u * j < columns;
+            const bool in = EXACT || lane + 64u * j < columns;
             s = in ? s + v[j] : s;
             sq = in ? sq + v[j] * v[j] : sq;
         }
@@ -438,29 +446,48 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
     const float var = fmaxf(sq / denom - mean * mean, 0.0f);
     const float inv = 1.0f / sqrtf(var + epsilon);
     float* y = out ? out + static_cast<uint64_t>(row) * columns : nullptr;
-    float* stage = QUANT ? lds_rows + static_cast<size_t>(wave) * columns : nullptr;
     float absmax = 0.0f;
     if (CH > 0) {
 #pragma unroll
         for (int j = 0; j < kKept; ++j) {
             const uint32_t c = lane + 64u * j;
-            if (c < columns) {
-                const float r = (v[j] - mean) * inv * wv[j] + bv[j];
-                if (y) y[c] = r;
-                if (QUANT) {
-                    stage[c] = r;
-                    absmax = fmaxf(absmax, fabsf(r));
-                }
+            v[j] = (v[j] - mean) * inv * wv[j] + bv[j];
+            if (EXACT || c < columns) {
+                if (y) y[c] = v[j];
+                absmax = fmaxf(absmax, fabsf(v[j]));
             }
         }
-    } else {
-        for (uint32_t c = lane; c < columns; c += 64u) {
-            const float r = (x[c] - mean) * inv * weight[c] + bias[c];
-            if (y) y[c] = r;
-            if (QUANT) {
-                stage[c] = r;
-                absmax = fmaxf(absmax, fabsf(r));
+        if (QUANT) {
+            absmax = wave_max(absmax);
+            const float sc = row_scale(absmax), inv_sc = div_rn(1.0f, sc);
+            if (lane == 0) scales[row] = sc;
+            // Product form first; a lane with any value near a half-integer
+            // redoes its values with the guarded quotient (rare).
+            int qv[kKept];
+            bool near_tie = false;
+#pragma unroll
+            for (int j = 0; j < kKept; ++j) near_tie |= quantize_product(v[j], inv_sc, qv[j]);
+            if (__builtin_expect(near_tie, 0)) {
+#pragma unroll
+                for (int j = 0; j < kKept; ++j) qv[j] = quantize_div(v[j], sc, inv_sc);
             }
+            int8_t* qr = q + static_cast<uint64_t>(row) * ldq;
+#pragma unroll
+            for (int j = 0; j < kKept; ++j) {
+                const uint32_t c = lane + 64u * j;
+                if (EXACT || c < columns) qr[c] = static_cast<int8_t>(qv[j]);
+            }
+            for (uint32_t c = columns + lane; c < ldq; c += 64u) qr[c] = 0;
+        }
+        return;
+    }
+    float* stage = QUANT ? lds_rows + static_cast<size_t>(wave) * columns : nullptr;
+    for (uint32_t c = lane; c < columns; c += 64u) {
+        const float r = (x[c] - mean) * inv * weight[c] + bias[c];
+        if (y) y[c] = r;
+        if (QUANT) {
+            stage[c] = r;
+            absmax = fmaxf(absmax, fabsf(r));
         }
     }
     if (QUANT) {
@@ -488,15 +515,18 @@ hipError_t launch_layer_norm(const float* in, const float* w, const float* b, ui
                              uint32_t cols, float eps, float* out, int8_t* q, uint32_t ldq,
                              float* scales, hipStream_t stream) {
     const unsigned grid = ceil_div(rows, kRowsPerBlock);
-    const size_t lds = QUANT ? static_cast<size_t>(kRowsPerBlock) * cols * sizeof(float) : 0;
     const uint32_t ch = (cols + 63u) / 64u;
-#define DAV2_LN_CASE(N)                                                                   \
-    dispatch((layer_norm_kernel<N, QUANT>), dim3(grid), dim3(64 * kRowsPerBlock), \
+    const size_t lds = QUANT && ch > 16 ? static_cast<size_t>(kRowsPerBlock) * cols * sizeof(float) : 0;
+#define DAV2_LN_CASE(N, E)                                                                   \
+    dispatch((layer_norm_kernel<N, QUANT, E>), dim3(grid), dim3(64 * kRowsPerBlock), \
                        lds, stream, in, w, b, rows, cols, eps, out, q, ldq, scales)
-    if (ch <= 6) DAV2_LN_CASE(6);
-    else if (ch <= 12) DAV2_LN_CASE(12);
-    else if (ch <= 16) DAV2_LN_CASE(16);
-    else DAV2_LN_CASE(0);
+    if (cols == 384) DAV2_LN_CASE(6, true);
+    else if (cols == 768) DAV2_LN_CASE(12, true);
+    else if (cols == 1024) DAV2_LN_CASE(16, true);
+    else if (ch <= 6) DAV2_LN_CASE(6, false);
+    else if (ch <= 12) DAV2_LN_CASE(12, false);
+    else if (ch <= 16) DAV2_LN_CASE(16, false);
+    else DAV2_LN_CASE(0, false);
 #undef DAV2_LN_CASE
     return hipGetLastError();
 }
