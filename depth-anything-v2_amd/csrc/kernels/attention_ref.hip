@@ -162,9 +162,15 @@ __global__ __launch_bounds__(256) void ref_scores_kernel(const float* __restrict
 // row is read again per pass, and the exponentials are stored between the
 // passes as the shader does; with the row in registers that intermediate
 // store is never observable and is skipped).
-template <int CH, bool HALF, int V>
+// PAIR (V = 2, rows of an even number of items, held in registers): thread t
+// holds virtual lanes 2t and 2t + 1 instead, so each access moves two
+// adjacent items (8 bytes); the halving tree then splits into one tree per
+// parity over the 64 threads (strides 64 .. 2 of the 128 lanes) and the final
+// stride-1 sum of the two.
+template <int CH, bool HALF, int V, bool PAIR = false>
 __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t rows, uint32_t columns) {
     static_assert(V == 1 || V == 2, "virtual lanes per thread");
+    static_assert(!PAIR || (V == 2 && CH > 0), "pairs need one wave per row held in registers");
     constexpr uint32_t kRowsPerBlock = 2u * V;  // 4 waves
     __shared__ float exchange[2][2][64];         // [row in block][max | partial][t]
     const uint32_t t = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -194,10 +200,33 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
         if (HALF && item * 2u + 1u < columns) m = fmaxf(m, b);
         return m;
     };
-    auto lane_of = [&](int v) { return t + 64u * (V == 2 ? static_cast<uint32_t>(v) : half); };
+    auto lane_of = [&](int v) {
+        return PAIR ? 2u * t + static_cast<uint32_t>(v) : t + 64u * (V == 2 ? static_cast<uint32_t>(v) : half);
+    };
 
     float maximum = -3.402823466e+38f;
-    if (live) {
+    if (PAIR) {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const uint32_t item = 2u * t + 128u * k;  // even: item + 1 < items too
+            if (item < items) {
+                if (HALF) {
+                    const uint2 w = *reinterpret_cast<const uint2*>(wr + item);
+                    lo[0][k] = half_lo(w.x);
+                    hi[0][k] = half_hi(w.x);
+                    lo[1][k] = half_lo(w.y);
+                    hi[1][k] = half_hi(w.y);
+                } else {
+                    const float2 f = *reinterpret_cast<const float2*>(fr + item);
+                    lo[0][k] = f.x;
+                    lo[1][k] = f.y;
+                    hi[0][k] = hi[1][k] = 0.0f;
+                }
+                maximum = fold_max(maximum, item, lo[0][k], hi[0][k]);
+                maximum = fold_max(maximum, item + 1u, lo[1][k], hi[1][k]);
+            }
+        }
+    } else if (live) {
 #pragma unroll
         for (int v = 0; v < V; ++v) {
             const uint32_t lane = lane_of(v);
@@ -267,14 +296,18 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
     // halving tree over the 128 partials: stride 64 (lane t + lane t + 64),
     // then 32 .. 1 across lanes (lane t adds lane t + stride)
     float sum;
-    if (V == 2) {
-        sum = partial[0] + partial[V - 1];
+    if (PAIR) {
+        sum = wave_sum_tree(partial[0]) + wave_sum_tree(partial[V - 1]);
     } else {
-        if (half == 1) exchange[slot][1][t] = partial[0];
-        __syncthreads();
-        sum = partial[0] + exchange[slot][1][t];  // meaningful in half 0
+        if (V == 2) {
+            sum = partial[0] + partial[V - 1];
+        } else {
+            if (half == 1) exchange[slot][1][t] = partial[0];
+            __syncthreads();
+            sum = partial[0] + exchange[slot][1][t];  // meaningful in half 0
+        }
+        sum = wave_sum_tree(sum);
     }
-    sum = wave_sum_tree(sum);
     if (V == 1) {
         __syncthreads();  // every partial has been read
         if (half == 0 && t == 0) exchange[slot][1][0] = sum;
@@ -284,16 +317,30 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
     if (!live) return;
     const float inverse = div_rn(1.0f, fmaxf(sum, 1.0e-20f));
 
-    auto normalize = [&](uint32_t item, float ea, float eb) {
-        if (HALF) {
-            // p = fp16(float(fp16(e)) * inverse); the stored exponentials are fp16(e)
-            const float pa = static_cast<float>(static_cast<_Float16>(ea)) * inverse;
-            const float pb = static_cast<float>(static_cast<_Float16>(eb)) * inverse;  // pack_half2 keeps them fp32
-            wr[item] = pack_half2(pa, pb);
-        } else {
-            fr[item] = ea * inverse;
-        }
+    // p = fp16(float(fp16(e)) * inverse) in binary16 (the stored exponentials
+    // are fp16(e); pack_half2 keeps the products fp32 until it rounds them)
+    auto probability_word = [&](float ea, float eb) {
+        const float pa = static_cast<float>(static_cast<_Float16>(ea)) * inverse;
+        const float pb = static_cast<float>(static_cast<_Float16>(eb)) * inverse;
+        return pack_half2(pa, pb);
     };
+    auto normalize = [&](uint32_t item, float ea, float eb) {
+        if (HALF) wr[item] = probability_word(ea, eb);
+        else fr[item] = ea * inverse;
+    };
+    if (PAIR) {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const uint32_t item = 2u * t + 128u * k;
+            if (item >= items) continue;
+            if (HALF)
+                *reinterpret_cast<uint2*>(wr + item) =
+                    make_uint2(probability_word(lo[0][k], hi[0][k]), probability_word(lo[1][k], hi[1][k]));
+            else
+                *reinterpret_cast<float2*>(fr + item) = make_float2(lo[0][k] * inverse, lo[1][k] * inverse);
+        }
+        return;
+    }
 #pragma unroll
     for (int v = 0; v < V; ++v) {
         const uint32_t lane = lane_of(v);
@@ -416,9 +463,13 @@ hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream
     const dim3 grid(static_cast<uint32_t>((rows + 3u) / 4u)), grid2(static_cast<uint32_t>((rows + 1u) / 2u)),
         block(256);
     // rows of up to 12 items per lane: one wave per row; longer ones: two
+    // (rows of an even number of items: pairs of adjacent items per thread)
 #define DAV2_SOFTMAX_CASE(N, V)                                                                        \
     if (per_lane <= N) {                                                                               \
-        dispatch((ref_softmax_kernel<N, HALF, V>), V == 2 ? grid : grid2, block, 0, s, data, rows, columns); \
+        if (V == 2 && items % 2u == 0u)                                                                \
+            dispatch((ref_softmax_kernel<N, HALF, V, V == 2>), grid, block, 0, s, data, rows, columns); \
+        else                                                                                           \
+            dispatch((ref_softmax_kernel<N, HALF, V>), V == 2 ? grid : grid2, block, 0, s, data, rows, columns); \
         return hipGetLastError();                                                                      \
     }
     DAV2_SOFTMAX_CASE(4, 2)

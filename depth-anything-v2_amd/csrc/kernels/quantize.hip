@@ -23,8 +23,11 @@ constexpr int kRowsPerBlock = 4;
 // (the IEEE quotient, through quantize_div).
 // WPR waves share a row (kRowsPerBlock / WPR rows per workgroup): wave part
 // p owns float4 chunks p*64*CH + lane + 64j (j < CH) kept in VGPRs; the row
-// maximum is the maximum of the parts' maxima (exact, order-free).
-template <int CH, int WPR>
+// maximum is the maximum of the parts' maxima (exact, order-free). EXACT:
+// columns == 256 * CH * WPR (every chunk in the row). The products x * (1/s)
+// come first; a lane with a value near a half-integer redoes its chunks
+// with the guarded quotient (quantize_div).
+template <int CH, int WPR, bool EXACT>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_kernel(
     const float* __restrict__ input, uint64_t input_offset, uint32_t rows,
     uint32_t columns, int8_t* __restrict__ q, uint32_t ldq,
@@ -41,7 +44,8 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_kernel(
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
         const uint32_t w = w0 + lane + 64u * j;
-        v[j] = live && w < words ? *reinterpret_cast<const float4*>(x + 4u * w) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[j] = live && (EXACT || w < words) ? *reinterpret_cast<const float4*>(x + 4u * w)
+                                            : make_float4(0.f, 0.f, 0.f, 0.f);
         absmax = fmaxf(absmax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
     }
     absmax = wave_max(absmax);
@@ -56,12 +60,28 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_kernel(
     const float s = row_scale(absmax), inv = div_rn(1.0f, s);
     if (lane == 0 && part == 0) scales[row] = s;
     uint32_t* out = reinterpret_cast<uint32_t*>(q + static_cast<uint64_t>(row) * ldq);
+    int b[CH][4];
+    bool near_tie = false;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+        near_tie |= quantize_product(v[j].x, inv, b[j][0]);
+        near_tie |= quantize_product(v[j].y, inv, b[j][1]);
+        near_tie |= quantize_product(v[j].z, inv, b[j][2]);
+        near_tie |= quantize_product(v[j].w, inv, b[j][3]);
+    }
+    if (__builtin_expect(near_tie, 0)) {
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            b[j][0] = quantize_div(v[j].x, s, inv);
+            b[j][1] = quantize_div(v[j].y, s, inv);
+            b[j][2] = quantize_div(v[j].z, s, inv);
+            b[j][3] = quantize_div(v[j].w, s, inv);
+        }
+    }
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
         const uint32_t w = w0 + lane + 64u * j;
-        if (w < words)
-            out[w] = pack4(quantize_div(v[j].x, s, inv), quantize_div(v[j].y, s, inv),
-                           quantize_div(v[j].z, s, inv), quantize_div(v[j].w, s, inv));
+        if (EXACT || w < words) out[w] = pack4(b[j][0], b[j][1], b[j][2], b[j][3]);
     }
     if (part == 0)
         for (uint32_t w = words + lane; w < (ldq >> 2); w += 64u) out[w] = 0u;
@@ -588,14 +608,16 @@ int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset, uint32_
     const unsigned grid = ceil_div(rows, kRowsPerBlock);
     const uint32_t ch = (columns / 4u + 63u) / 64u;
     // Long rows are split over several waves (more loads in flight per row).
-#define DAV2_QR_CASE(N, W)                                                                                         \
-    dispatch((quantize_rows_kernel<N, W>), dim3(ceil_div(rows, kRowsPerBlock / W)), dim3(64 * kRowsPerBlock), \
+#define DAV2_QR_CASE(N, W, E)                                                                                         \
+    dispatch((quantize_rows_kernel<N, W, E>), dim3(ceil_div(rows, kRowsPerBlock / W)), dim3(64 * kRowsPerBlock), \
                        0, s, input, input_offset, rows, columns, q, ldq, scales)
-    if (ch <= 1) DAV2_QR_CASE(1, 1);
-    else if (ch <= 2) DAV2_QR_CASE(2, 1);
-    else if (ch <= 4) DAV2_QR_CASE(4, 1);
-    else if (ch <= 8) DAV2_QR_CASE(4, 2);
-    else if (ch <= 16) DAV2_QR_CASE(4, 4);
+    if (columns == 1024u) DAV2_QR_CASE(4, 1, true);
+    else if (columns == 4096u) DAV2_QR_CASE(4, 4, true);
+    else if (ch <= 1) DAV2_QR_CASE(1, 1, false);
+    else if (ch <= 2) DAV2_QR_CASE(2, 1, false);
+    else if (ch <= 4) DAV2_QR_CASE(4, 1, false);
+    else if (ch <= 8) DAV2_QR_CASE(4, 2, false);
+    else if (ch <= 16) DAV2_QR_CASE(4, 4, false);
     else
         dispatch(quantize_rows_long_kernel, dim3(grid), dim3(64 * kRowsPerBlock), 0, s,
                            input, input_offset, rows, columns, q, ldq, scales);

@@ -713,7 +713,8 @@ def test_attention_ref_fp32_bit_exact(gpu, lib, oracle, tokens, heads, batch):
 
 
 @pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (2, 1, 1), (5, 2, 1), (77, 4, 1), (258, 2, 2),
-                                                (1369, 3, 1), (1370, 16, 1), (3101, 1, 1), (6200, 1, 1)])
+                                                (1369, 3, 1), (1370, 16, 1), (3101, 1, 1), (6200, 1, 1),
+                                                (100, 2, 1), (1500, 1, 1)])
 def test_attention_ref_fp16_bit_exact(gpu, lib, oracle, tokens, heads, batch):
     # bmm_score_fp16 + softmax_lastdim_half + bmm_value_fp16 (mode 1 of the
     # oracle: every product rounded to binary16), bit for bit: the binary16
@@ -885,7 +886,7 @@ def test_attention_fused_peaked_and_zero_rows(gpu, lib, oracle, colmax):
 
 
 @pytest.mark.parametrize("rows,cols", [(16 * 1370, 1370), (7, 5477), (3, 64), (5, 9000), (4, 6144), (2, 1),
-                                       (3, 2500), (1, 1537)])
+                                       (3, 2500), (1, 1537), (5, 2), (3, 130), (6, 1024), (9, 1536), (4, 1000)])
 def test_softmax_fp32(gpu, lib, oracle, rows, cols):
     # softmax_lastdim.glsl in its lane/tree order: bit for bit (register and
     # streaming forms); the matrix-core path's row softmax within tolerance
