@@ -152,6 +152,101 @@ DAV2_DEV float im2col_value(const Im2colGeometry& g, uint32_t oy, uint32_t ox, u
     return g.input[ic * g.plane + static_cast<uint64_t>(iy) * g.iw + static_cast<uint32_t>(ix)];
 }
 
+// Small maps: one output pixel per WPR waves with its im2col row held in
+// registers, so the window absmax, the scale and the quantized bytes come
+// from one pass over the input and no channel-group maxima are needed (the
+// tiled paths below are built for many output pixels). Same bytes as the
+// other paths: the row absmax (of max(x, 0) with RELU), s = row_scale,
+// 1 / s, rne(clamp(x * (1 / s))). Wave part p of a row owns the words
+// p * 64 * kRowWords + lane + 64 j (four columns each), so a wave's stores
+// cover 256 contiguous bytes. The values come through raw buffer loads,
+// all issued before the first use; a column in the zero padding (or past
+// the row) loads from an offset beyond the buffer, which reads 0.
+constexpr int kRowWords = 9;            // words per lane and wave part
+constexpr uint32_t kSmallMapRows = 8192;  // output pixels up to which this path runs
+
+// Column c of an im2col row -> (input channel, ky, kx); KS = 3 divides by
+// constants (exact for c < 2^14: c * 58255 >> 19 = c / 9, t * 11 >> 5 = t / 3
+// for t < 9), KS = 0 by the geometry's reciprocals.
+template <int KS>
+DAV2_DEV void im2col_column(const Im2colGeometry& g, uint32_t c, uint32_t& ic, uint32_t& ky, uint32_t& kx) {
+    if (KS == 3) {
+        ic = __umul24(c, 58255u) >> 19;
+        const uint32_t t = c - __umul24(ic, 9u);
+        ky = __umul24(t, 11u) >> 5;
+        kx = t - __umul24(ky, 3u);
+    } else {
+        ic = g.div_area.div(c);
+        const uint32_t kidx = c - ic * g.div_area.d;
+        ky = g.div_k.div(kidx);
+        kx = kidx - ky * g.k;
+    }
+}
+
+template <int WPR, bool RELU, int KS>
+__global__ __launch_bounds__(256) void im2col_rows_kernel(Im2colGeometry g, uint32_t rows, uint32_t ldq,
+                                                          float* __restrict__ scales, int8_t* __restrict__ q) {
+    static_assert(4 % WPR == 0, "wave parts per row");
+    __shared__ float part_max[4];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t row = blockIdx.x * (4u / WPR) + wave / WPR, part = wave % WPR;
+    const bool live = row < rows;
+    // a row past the end (whole waves) reads the last row's window, stores nothing
+    const uint32_t r = min(row, rows - 1u);
+    const uint32_t oy = g.div_ow.div(r), ox = r - oy * g.ow;
+    const int32_t bx = static_cast<int32_t>(ox * g.stride) - g.pad, by = static_cast<int32_t>(oy * g.stride) - g.pad;
+    const uint32_t plane = static_cast<uint32_t>(g.plane);
+    const uint32_t words = ldq >> 2, w0 = part * 64u * kRowWords + lane;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.input), static_cast<short>(0),
+                                                      static_cast<int>(g.columns / (g.k * g.k) * plane * 4u),
+                                                      0x00020000);
+    float v[kRowWords][4];
+#pragma unroll
+    for (int j = 0; j < kRowWords; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = 4u * (w0 + 64u * j) + i;
+            uint32_t ic, ky, kx;
+            im2col_column<KS>(g, c, ic, ky, kx);
+            const uint32_t ix = static_cast<uint32_t>(bx + static_cast<int32_t>(kx));
+            const uint32_t iy = static_cast<uint32_t>(by + static_cast<int32_t>(ky));
+            // (negative coordinates wrap to large unsigned values)
+            const bool in = (c < g.columns) & (ix < g.iw) & (iy < g.ih);
+            // small maps: every index of the input fits 24 x 24 -> 32-bit
+            // products (checked by the launcher)
+            const uint32_t at = (__umul24(ic, plane) + __umul24(iy, g.iw) + ix) * 4u;
+            v[j][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, in ? at : 0x80000000u, 0, 0));
+        }
+    float absmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRowWords; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (RELU) v[j][i] = fmaxf(v[j][i], 0.0f);
+            absmax = fmaxf(absmax, fabsf(v[j][i]));
+        }
+    absmax = wave_max(absmax);
+    if (WPR > 1) {
+        if (lane == 0) part_max[wave] = absmax;
+        __syncthreads();
+        const uint32_t first = wave - part;
+#pragma unroll
+        for (int i = 0; i < WPR; ++i) absmax = fmaxf(absmax, part_max[first + i]);
+    }
+    if (!live) return;
+    const float s = row_scale(absmax);
+    const float inverse = 1.0f / s;
+    if (lane == 0 && part == 0) scales[row] = s;
+    uint32_t* out = reinterpret_cast<uint32_t*>(q + static_cast<uint64_t>(row) * ldq);
+#pragma unroll
+    for (int j = 0; j < kRowWords; ++j) {
+        const uint32_t w = w0 + 64u * j;
+        if (w < words)
+            out[w] = pack4(quantize_rne(v[j][0] * inverse), quantize_rne(v[j][1] * inverse),
+                           quantize_rne(v[j][2] * inverse), quantize_rne(v[j][3] * inverse));
+    }
+}
+
 // Pass 1: one wave per output row computes the row scale.
 __global__ __launch_bounds__(64 * kRowsPerBlock) void im2col_scale_kernel(
     Im2colGeometry g, uint32_t rows, float* __restrict__ scales) {
@@ -631,8 +726,9 @@ uint64_t dav2_hip_im2col_scratch_floats(uint32_t input_width, uint32_t input_hei
 
 namespace {
 
-// relu: quantize the rows of max(input, 0); only the tiled 3x3 / 1x1 paths
-// (with scratch) take it, other geometries return hipErrorInvalidValue.
+// relu: quantize the rows of max(input, 0); the single-pass path of small
+// maps and the tiled 3x3 / 1x1 paths (with scratch) take it, other calls
+// return hipErrorInvalidValue.
 int im2col_quantize(const float* input, uint32_t input_width, uint32_t input_height, uint32_t input_channels,
                     uint32_t output_width, uint32_t output_height, uint32_t kernel, uint32_t stride, int32_t padding,
                     int8_t* q, uint32_t ldq, float* scales, float* scratch, uint64_t scratch_floats, bool relu,
@@ -669,6 +765,28 @@ int im2col_quantize(const float* input, uint32_t input_width, uint32_t input_hei
     const bool fast1 = kernel == 1 && stride == 1 && padding == 0 && output_width == input_width &&
                        output_height == input_height;
     const bool have_partial = scratch && scratch_floats >= plane * groups;
+    const uint32_t row_words = ldq / 4u;
+    if (rows <= kSmallMapRows && row_words <= 4u * 64u * kRowWords && plane * input_channels < (1ull << 29) &&
+        plane < (1u << 24) && input_width < (1u << 24) && input_height < (1u << 24) && input_channels < (1u << 24)) {
+        const int wpr = row_words <= 64u * kRowWords ? 1 : (row_words <= 128u * kRowWords ? 2 : 4);
+#define DAV2_ROWS_CASE(W, K)                                                                                 \
+    do {                                                                                                     \
+        const dim3 grid(ceil_div(rows, 4u / (W)));                                                           \
+        if (relu) dispatch(im2col_rows_kernel<W, true, K>, grid, dim3(256), 0, s, g, rows, ldq, scales, q);  \
+        else dispatch(im2col_rows_kernel<W, false, K>, grid, dim3(256), 0, s, g, rows, ldq, scales, q);      \
+    } while (0)
+        if (kernel == 3) {
+            if (wpr == 1) DAV2_ROWS_CASE(1, 3);
+            else if (wpr == 2) DAV2_ROWS_CASE(2, 3);
+            else DAV2_ROWS_CASE(4, 3);
+        } else {
+            if (wpr == 1) DAV2_ROWS_CASE(1, 0);
+            else if (wpr == 2) DAV2_ROWS_CASE(2, 0);
+            else DAV2_ROWS_CASE(4, 0);
+        }
+#undef DAV2_ROWS_CASE
+        return hipGetLastError();
+    }
     if ((fast3 || fast1) && have_partial && input_height <= 65535u) {
         const hipError_t e = launch_channel_group_absmax(input, input_channels, plane, scratch, relu, s);
         if (e != hipSuccess) return e;

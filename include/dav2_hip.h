@@ -56,10 +56,11 @@ DAV2_API int dav2_hip_im2col_quantize_i8(const float* input, uint32_t input_widt
                                          int8_t* q, uint32_t ldq, float* scales,
                                          float* scratch, uint64_t scratch_floats, void* stream);
 /* The same for max(input, 0) (relu.glsl ahead of the convolution, as the DPT
- * residual units apply it), without materialising the ReLU; kernel 3 / stride
- * 1 / padding 1 (channels % 16 == 0) or kernel 1 / stride 1 / padding 0 with
- * scratch only, else hipErrorInvalidValue. No reference counterpart (a
- * fusion of two reference passes). */
+ * residual units apply it), without materialising the ReLU: any geometry on
+ * maps of up to 8192 output pixels (rows of up to 9216 columns), else kernel
+ * 3 / stride 1 / padding 1 (channels % 16 == 0) or kernel 1 / stride 1 /
+ * padding 0 with scratch only; other calls return hipErrorInvalidValue. No
+ * reference counterpart (a fusion of two reference passes). */
 DAV2_API int dav2_hip_im2col_quantize_relu_i8(const float* input, uint32_t input_width,
                                               uint32_t input_height, uint32_t input_channels,
                                               uint32_t output_width, uint32_t output_height,

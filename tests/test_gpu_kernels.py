@@ -84,7 +84,8 @@ def test_quantize_rows_near_ties(gpu, lib, oracle, cols):
                                          (96, 19, 19, 3, 2, 1), (32, 74, 74, 1, 1, 0), (5, 4, 4, 3, 1, 1),
                                          (128, 60, 52, 3, 1, 1), (1024, 10, 10, 3, 2, 1), (1024, 19, 19, 3, 1, 1),
                                          (128, 130, 141, 3, 1, 1), (16, 3, 70, 3, 1, 1), (512, 37, 37, 1, 1, 0),
-                                         (48, 5, 7, 1, 1, 0), (256, 150, 150, 3, 1, 1)])
+                                         (48, 5, 7, 1, 1, 0), (256, 150, 150, 3, 1, 1), (64, 100, 100, 1, 1, 0),
+                                         (8, 91, 93, 3, 2, 1), (2048, 9, 9, 3, 1, 1), (1024, 38, 38, 3, 1, 1)])
 def test_im2col_quantize_bit_exact(gpu, lib, oracle, c, h, w, k, s, p):
     torch = gpu
     _announce("im2col", c, h, w, k, s, p)
@@ -111,7 +112,7 @@ def test_im2col_quantize_bit_exact(gpu, lib, oracle, c, h, w, k, s, p):
 
 
 @pytest.mark.parametrize("c,h,w,k", [(256, 37, 37, 3), (1024, 19, 19, 3), (16, 3, 70, 3), (256, 37, 37, 1),
-                                     (48, 5, 7, 1)])
+                                     (48, 5, 7, 1), (64, 100, 100, 3), (64, 100, 100, 1)])
 def test_im2col_quantize_relu_bit_exact(gpu, lib, oracle, c, h, w, k):
     # the fused ReLU quantizes exactly the rows of max(x, 0)
     torch = gpu
@@ -133,10 +134,18 @@ def test_im2col_quantize_relu_bit_exact(gpu, lib, oracle, c, h, w, k):
     assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
     assert np.array_equal(q[:, :kk], q_ref)
     assert np.all(q[:, kk:] == 0)
-    # x itself is unchanged, and the geometries without a tiled kernel refuse
+    # x itself is unchanged. Without scratch, maps of up to 8192 output pixels
+    # (the single-pass path) give the same bytes; larger ones refuse.
     assert np.array_equal(host(torch, xd), x)
-    assert lib.dav2_hip_im2col_quantize_relu_i8(ptr(xd), w, h, c, w, h, k, 1, p, ptr(qd), ld, ptr(sd), None, 0,
-                                                stream(torch)) != 0
+    qd.fill_(0x55)
+    rc = lib.dav2_hip_im2col_quantize_relu_i8(ptr(xd), w, h, c, w, h, k, 1, p, ptr(qd), ld, ptr(sd), None, 0,
+                                              stream(torch))
+    if w * h <= 8192:
+        assert rc == 0
+        assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
+        assert np.array_equal(host(torch, qd)[:, :kk], q_ref)
+    else:
+        assert rc != 0
 
 
 # ---------------------------------------------------------------------------
