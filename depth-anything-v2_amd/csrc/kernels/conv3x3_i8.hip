@@ -54,7 +54,6 @@ constexpr int kPixT = 128;                             // pixel slots per tile (
 constexpr uint32_t kTapBytes = kPixT * 64u;            // one tap's operand tile
 constexpr uint32_t kBufBytes = kTaps * kTapBytes;      // one block's operand tile
 constexpr uint32_t kOutside = 0x80000000u;             // buffer offset past every block's range
-constexpr int kPieces = 18;
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 
