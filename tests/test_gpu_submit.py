@@ -3,11 +3,15 @@ submission (src/vulkan_executor.cpp:656-800, job API src/dav2.cpp:429-473):
 the float32 RGBA/BGRA preprocessing kernel (preprocess_rgba.glsl) bit for bit
 against the oracle, and whole submissions against the oracle's pipeline
 (preprocess, int8 graph, min/max normalisation, bilinear resize to the image).
-The cross-process (IPC handle) form is exercised by tests/ipc_submit_check.py,
-which starts its producer process before touching the GPU."""
+The cross-process (IPC handle) form is tests/ipc_submit_check.py, which
+starts its producer process before touching the GPU; the last test here runs
+it as a child process."""
 
 import ctypes as C
+import subprocess
+import sys
 import time
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -188,3 +192,14 @@ def test_submit_hip_cancel_and_checks(gpu, pkg, lib, vits_model):
         assert submit(struct_size=8)[0] == 1
         assert lib.dav2_submit_hip(None, None, None) == 1
         assert lib.dav2_gpu_job_poll(None, None) == 1
+
+
+def test_ipc_submit_cross_process():
+    # Producer and consumer in processes of their own (memory handles over
+    # IPC, the wait event over IPC where the runtime records interprocess
+    # events); the submission's output must equal the oracle's pipeline.
+    script = Path(__file__).resolve().parent / "ipc_submit_check.py"
+    r = subprocess.run([sys.executable, "-u", str(script)], capture_output=True, text=True, timeout=100)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    assert "ipc submit bit-exact vs oracle: True" in r.stdout
