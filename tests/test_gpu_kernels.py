@@ -85,7 +85,8 @@ def test_quantize_rows_near_ties(gpu, lib, oracle, cols):
                                          (128, 60, 52, 3, 1, 1), (1024, 10, 10, 3, 2, 1), (1024, 19, 19, 3, 1, 1),
                                          (128, 130, 141, 3, 1, 1), (16, 3, 70, 3, 1, 1), (512, 37, 37, 1, 1, 0),
                                          (48, 5, 7, 1, 1, 0), (256, 150, 150, 3, 1, 1), (64, 100, 100, 1, 1, 0),
-                                         (8, 91, 93, 3, 2, 1), (2048, 9, 9, 3, 1, 1), (1024, 38, 38, 3, 1, 1)])
+                                         (8, 91, 93, 3, 2, 1), (2048, 9, 9, 3, 1, 1), (1024, 38, 38, 3, 1, 1),
+                                         (512, 13, 11, 3, 1, 1), (700, 5, 9, 3, 2, 1)])
 def test_im2col_quantize_bit_exact(gpu, lib, oracle, c, h, w, k, s, p):
     torch = gpu
     _announce("im2col", c, h, w, k, s, p)
