@@ -463,10 +463,12 @@ hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream
     const dim3 grid(static_cast<uint32_t>((rows + 3u) / 4u)), grid2(static_cast<uint32_t>((rows + 1u) / 2u)),
         block(256);
     // rows of up to 12 items per lane: one wave per row; longer ones: two
-    // (rows of an even number of items: pairs of adjacent items per thread)
+    // (rows of an even number of items on an 8-byte aligned buffer: pairs
+    // of adjacent items per thread)
+    const bool pairs = items % 2u == 0u && (reinterpret_cast<uintptr_t>(data) & 7u) == 0u;
 #define DAV2_SOFTMAX_CASE(N, V)                                                                        \
     if (per_lane <= N) {                                                                               \
-        if (V == 2 && items % 2u == 0u)                                                                \
+        if (V == 2 && pairs)                                                                           \
             dispatch((ref_softmax_kernel<N, HALF, V, V == 2>), grid, block, 0, s, data, rows, columns); \
         else                                                                                           \
             dispatch((ref_softmax_kernel<N, HALF, V>), V == 2 ? grid : grid2, block, 0, s, data, rows, columns); \

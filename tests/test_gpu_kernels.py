@@ -895,6 +895,21 @@ def test_attention_fused_peaked_and_zero_rows(gpu, lib, oracle, colmax):
     assert np.all(out[:, 5] == 0.0)
 
 
+def test_softmax_fp32_buffer_off_8_bytes(gpu, lib, oracle):
+    # rows of an even number of items on a buffer 4 bytes past an 8-byte
+    # boundary: the single-item path, the same bits
+    torch = gpu
+    rows, cols = 6, 1024
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
+    ref = oracle.softmax_rows(x)
+    buf = torch.zeros(rows * cols + 2, dtype=torch.float32, device="cuda")
+    buf[1:1 + rows * cols] = torch.from_numpy(x.reshape(-1)).cuda()
+    ok(lib, lib.dav2_hip_attention_ref_softmax(ptr(buf) + 4, rows, cols, 0, stream(torch)))
+    got = host(torch, buf)[1:1 + rows * cols].reshape(rows, cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("rows,cols", [(16 * 1370, 1370), (7, 5477), (3, 64), (5, 9000), (4, 6144), (2, 1),
                                        (3, 2500), (1, 1537), (5, 2), (3, 130), (6, 1024), (9, 1536), (4, 1000)])
 def test_softmax_fp32(gpu, lib, oracle, rows, cols):
