@@ -2,11 +2,17 @@
 """Throughput of the int8 Depth-Anything-V2 path on one MI355X.
 
 Workload (default): ViT-L + DPT at 518x518, batch 1, int8 GEMMs and
-convolutions with the integer-exact fused attention (in place of the
+convolutions with this build's integer-exact fused attention (in place of the
 reference's binary16 attention of its int8 mode), seeded random weights in
-a .dav2 file and a seeded ImageNet-normalised input already resident in HBM,
-run through dav2_infer_tensor_f32_device. One step = one full inference of
-the batch. Prints one JSON line.
+a .dav2 file and a seeded ImageNet-normalised input. One step = one call of
+the public entry dav2_infer_tensor_f32 on one image (host buffers: the input's
+upload and the depth map's download are inside the step); `value` = 1 / the
+median step time. With --batch B > 1 a step is one call of the batched device
+entry dav2_infer_tensor_f32_device on B images already in HBM. Reported
+beside it: the same graph with the input already resident in HBM
+(dav2_infer_tensor_f32_device), and the int8 graph with the reference's own
+binary16 attention arithmetic (DAV2_CREATE_REFERENCE_FP16_ATTENTION) through
+the same host entry. Prints one JSON line.
 
 Roofline: the dominant kernel is the int8 MFMA GEMM. Its algorithmic work is
 2*M*N*K int8 ops per launch (unpadded K); achieved = total ops / total
@@ -59,7 +65,7 @@ def cpu_baseline(model_path: Path, encoder: str, size: int, budget_s: float) -> 
     try:
         x = fmt.imagenet_input(size, size, SEED + 3)[0]
         t0 = time.perf_counter()
-        oracle.infer(h, x, size, size, fp16_attention=True)
+        oracle.infer(h, x, size, size, attention="exact")
         dt = time.perf_counter() - t0
         return {"value": 1.0 / dt, "unit": "images/s", "cores": oracle.lib.orc_get_threads(), "kind": "port",
                 "sample": f"1 full {encoder} {size}x{size} image through the oracle's int8 graph ({dt:.2f} s)",
@@ -108,6 +114,31 @@ def cpu_preprocess_ms(width: int, height: int, input_size: int) -> float:
 BANDWIDTH_KERNELS = ("layer_norm_quantize_i8", "layer_norm", "softmax_f32", "quantize_rows_i8")
 
 
+def gemm_shape_table(prof: dict, steps: int) -> dict:
+    """Per GEMM shape (profiler keys "gemm_i8@MxNxK:epilogue"): average
+    launch time, int8 rate, and the attainable bound of that shape,
+    max(ops / 5 POP/s, bytes / 8 TB/s), with bytes = the int8 operands
+    (M*K + N*K), the fp32 output (4*M*N, plus 4*M*N read back by the
+    LayerScale-residual and residual epilogues) and the scales and bias."""
+    table = {}
+    for name, v in prof.items():
+        if not name.startswith("gemm_i8@") or not v["ms"]:
+            continue
+        dims, tag = name.split("@", 1)[1].split(":")
+        m, n, k = (int(t) for t in dims.split("x"))
+        ops = 2.0 * m * n * k
+        out_bytes = 4.0 * m * n * (2 if tag in ("row_layerscale", "transposed_residual") else 1)
+        nbytes = m * k + n * k + out_bytes + 4.0 * m + 8.0 * n
+        avg_s = v["ms"] * 1e-3 / v["launches"]
+        bound_s = max(ops / (PEAK_INT8_TOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9))
+        table[f"{dims}:{tag}"] = {"launches_per_step": v["launches"] / steps, "avg_us": 1e6 * avg_s,
+                                  "T/s": ops / avg_s / 1e12, "frac": ops / avg_s / 1e12 / PEAK_INT8_TOPS,
+                                  "attainable_us": 1e6 * bound_s, "frac_of_attainable": bound_s / avg_s,
+                                  "bound": "mfma" if ops / (PEAK_INT8_TOPS * 1e12) >= nbytes / (PEAK_HBM_GBS * 1e9)
+                                  else "hbm"}
+    return dict(sorted(table.items(), key=lambda kv: -kv[1]["avg_us"] * kv[1]["launches_per_step"]))
+
+
 def profile_config(pkg, fmt, torch, model: Path, size: int, batch: int, fp32_attention: bool, steps: int) -> dict:
     """A few profiled steps of one configuration: per-launch HIP events give
     each kernel's time; reported are the GEMM's int8 rate and the HBM rate of
@@ -133,6 +164,8 @@ def profile_config(pkg, fmt, torch, model: Path, size: int, batch: int, fp32_att
     if g and g["ms"]:
         rate = g["work"] / (g["ms"] * 1e-3) / 1e12
         res["gemm_i8"] = {"T/s": rate, "frac": rate / PEAK_INT8_TOPS, "avg_us": 1e3 * g["ms"] / g["launches"]}
+        # the encoder's GEMM shapes (the most time per step)
+        res["gemm_shapes"] = dict(list(gemm_shape_table(prof, steps).items())[:6])
     for name in BANDWIDTH_KERNELS:
         v = prof.get(name)
         if v and v["ms"]:
@@ -200,46 +233,57 @@ def main() -> int:
         out = torch.empty(n_out, dtype=torch.float32, device="cuda")
         stream = torch.cuda.current_stream().cuda_stream
 
-        def step():
+        def device_step():
             ctx.infer_device(x.data_ptr(), args.batch, args.size, args.size, out.data_ptr(), n_out, stream)
 
+        x_host = fmt.imagenet_input(args.size, args.size, SEED + 3)[0]
+
+        def host_step():
+            ctx.infer(x_host, args.size, args.size)  # synchronous: returns with the depth map on the host
+
+        step = host_step if args.batch == 1 else device_step
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
+        # The timed region: exactly K steps, each timed on its own (every step
+        # ends synchronised); value = batch / median step time.
+        calls = []
         t0 = time.perf_counter()
         for _ in range(args.steps):
+            h0 = time.perf_counter()
             step()
+            if args.batch > 1:
+                torch.cuda.synchronize()
+            calls.append(time.perf_counter() - h0)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
-        print(f"bench: {args.steps} steps in {elapsed:.3f} s", file=sys.stderr, flush=True)
+        median_s = float(np.median(calls))
+        print(f"bench: {args.steps} steps in {elapsed:.3f} s (median {1e3 * median_s:.3f} ms)", file=sys.stderr,
+              flush=True)
+        host_entry = {"entry": ("dav2_infer_tensor_f32 (host buffers, PCIe copies included)" if args.batch == 1
+                                else "dav2_infer_tensor_f32_device (batched device entry)"),
+                      "calls": len(calls), "median_ms": 1e3 * median_s, "mean_ms": 1e3 * float(np.mean(calls)),
+                      "min_ms": 1e3 * float(np.min(calls)), "images_per_s_median": args.batch / median_s}
 
-        # Per-step device-resident times (each step synchronised), for the
-        # median beside the K-step throughput.
+        # The same graph on an input already resident in HBM
+        # (dav2_infer_tensor_f32_device): K back-to-back steps, and the median
+        # of per-step synchronised times.
+        for _ in range(2):
+            device_step()
+        torch.cuda.synchronize()
+        d0 = time.perf_counter()
+        for _ in range(args.steps):
+            device_step()
+        torch.cuda.synchronize()
+        device_rate = args.batch * args.steps / (time.perf_counter() - d0)
         step_s = []
         for _ in range(max(20, args.steps)):
             s0 = time.perf_counter()
-            step()
+            device_step()
             torch.cuda.synchronize()
             step_s.append(time.perf_counter() - s0)
         device_median = args.batch / float(np.median(step_s))
-
-        # The host-buffer entry (dav2_infer_tensor_f32): H2D and D2H copies
-        # included; the median over >= 20 calls after one warm-up call.
-        host_rate = None
-        host_entry = None
         host_steps = min(args.steps, 10)
-        if args.batch == 1:
-            x_host = fmt.imagenet_input(args.size, args.size, SEED + 3)[0]
-            ctx.infer(x_host, args.size, args.size)
-            calls = []
-            for _ in range(max(20, args.steps)):
-                h0 = time.perf_counter()
-                ctx.infer(x_host, args.size, args.size)
-                calls.append(time.perf_counter() - h0)
-            host_rate = 1.0 / float(np.median(calls))
-            host_entry = {"entry": "dav2_infer_tensor_f32 (host buffers, PCIe copies included)",
-                          "calls": len(calls), "median_ms": 1e3 * float(np.median(calls)),
-                          "mean_ms": 1e3 * float(np.mean(calls)), "images_per_s_median": host_rate}
 
         # Host-image entries (dav2_infer_bgr8): a 518x518 BGR8 frame through
         # the GPU preprocessing and the same inference, PCIe copies included;
@@ -291,7 +335,7 @@ def main() -> int:
         torch.cuda.synchronize()
         p0 = time.perf_counter()
         for _ in range(args.steps):
-            step()
+            device_step()
         torch.cuda.synchronize()
         profiled_elapsed = time.perf_counter() - p0
         prof = ctx.profile_report()
@@ -317,11 +361,27 @@ def main() -> int:
                 torch.cuda.synchronize()
                 return steps / (time.perf_counter() - f0)
 
+        def host_entry_median(flags, calls_n):
+            with pkg.Context(str(model), args.encoder, flags) as cm:
+                cm.infer(x_host, args.size, args.size)
+                ts = []
+                for _ in range(calls_n):
+                    h0 = time.perf_counter()
+                    cm.infer(x_host, args.size, args.size)
+                    ts.append(time.perf_counter() - h0)
+            return {"calls": calls_n, "median_ms": 1e3 * float(np.median(ts)),
+                    "images_per_s_median": 1.0 / float(np.median(ts))}
+
         fp32_rate = fp16_rate = ref16_rate = None
+        ref16_host = None
         if args.batch == 1 and not args.no_fp32_mode:
             fp32_rate = mode_rate(pkg.FORCE_FP32, 5)
             fp16_rate = mode_rate(pkg.FORCE_FP16, 5)
             ref16_rate = mode_rate(pkg.REFERENCE_FP16_ATTENTION, 10)
+            ref16_host = host_entry_median(pkg.REFERENCE_FP16_ATTENTION, 20)
+            ref16_host["entry"] = ("dav2_infer_tensor_f32, int8 graph with the reference's binary16 attention "
+                                   "arithmetic (DAV2_CREATE_REFERENCE_FP16_ATTENTION)")
+            print("bench: reference-arithmetic attention " + json.dumps(ref16_host), file=sys.stderr, flush=True)
 
         gemm = prof.get("gemm_i8", {})
         g_ms = gemm.get("ms", 0.0)
@@ -337,7 +397,10 @@ def main() -> int:
             except (ValueError, OSError):
                 traffic = None
         kernels = {}
+        gemm_shapes = gemm_shape_table(prof, args.steps)
         for name, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+            if "@" in name:
+                continue
             rate = v["work"] / (v["ms"] * 1e-3) if v["ms"] else 0.0
             if v["unit"] == "B":
                 kernels[name] = {"ms_per_step": v["ms"] / args.steps, "avg_us": 1e3 * v["ms"] / v["launches"],
@@ -367,10 +430,10 @@ def main() -> int:
             if image_paths is not None:
                 cpu["preprocess_bgr8_1080p_ms"] = cpu_preprocess_ms(1920, 1080, 518)
 
-    ms = 1e3 * elapsed / args.steps
+    ms = 1e3 * median_s
     result = {
         "metric": "images/sec ViT-L 518² bs1 on 1 MI355X; int8 GEMM % MFMA peak; LN/softmax % HBM",
-        "value": args.batch * args.steps / elapsed,
+        "value": args.batch / median_s,
         "unit": "images/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -383,7 +446,8 @@ def main() -> int:
         "data": "synthetic (seeded random-init weights in a .dav2 file, seeded ImageNet-normalised input)",
         "config": {"workload": f"{args.encoder} + DPT {args.size}x{args.size} batch {args.batch}, int8 GEMMs and "
                                f"convolutions, {'fp32' if args.fp32_attention else 'integer-exact'} attention, "
-                               "dav2_infer_tensor_f32_device",
+                               + ("dav2_infer_tensor_f32 (host buffers)" if args.batch == 1
+                                  else "dav2_infer_tensor_f32_device (batched)"),
                    "size": args.size, "global_batch": args.batch,
                    "parallelism": "single GPU"},
         "roofline": {"kernel": "gemm_i8", "bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS,
@@ -392,10 +456,12 @@ def main() -> int:
                      "avg_launch_us": 1e3 * g_ms / g_launches, "launches_per_step": g_launches / args.steps,
                      "traffic": traffic},
         "kernels": {k: kernels[k] for k in list(kernels)[:8]},
+        "gemm_shapes": gemm_shapes,
         "profiled_ms_per_step": 1e3 * profiled_elapsed / args.steps,
-        "device_median_images_per_s": device_median,
-        "host_entry_images_per_s": host_rate,
         "host_entry": host_entry,
+        "device_resident_images_per_s": device_rate,
+        "device_median_images_per_s": device_median,
+        "reference_arithmetic_host_entry": ref16_host,
         "extra_configs": extra,
         "image_paths": image_paths,
         "fp32_mode_images_per_s": fp32_rate,

@@ -199,6 +199,9 @@ PROTOTYPES = {
     "dav2_hip_attention_ref_scores": (C.c_int, [vp, vp, u32, u32, u32, C.c_int, vp]),
     "dav2_hip_attention_ref_softmax": (C.c_int, [vp, u64, u32, C.c_int, vp]),
     "dav2_hip_attention_ref_values": (C.c_int, [vp, vp, vp, u32, u32, u32, C.c_int, vp]),
+    "dav2_hip_attention_ref16_fused_scratch_bytes": (u64, [u32, u32, u32]),
+    "dav2_hip_attention_ref16_fused": (C.c_int, [vp, vp, u32, u32, u32, vp, u64, vp]),
+    "dav2_hip_transpose_rows_i8": (C.c_int, [vp, u32, u32, vp, u32, vp]),
     "dav2_hip_attention_fused_scratch_bytes": (u64, [u32, u32, u32]),
     "dav2_hip_attention_fused": (C.c_int, [vp, vp, u32, u32, u32, vp, u64, vp]),
     "dav2_hip_attention_fused_colmax": (C.c_int, [vp, vp, u32, u32, vp, u32, vp, u64, vp]),
@@ -206,7 +209,7 @@ PROTOTYPES = {
     "dav2_hip_bilinear_align_true_maxima": (C.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "dav2_hip_conv2d_i8_emits": (C.c_int, [u32, u32]),
     "dav2_hip_gemm_i8_events": (None, [vp, vp]),
-    "dav2_hip_launch_events": (None, [vp, vp]),
+    "dav2_hip_launch_events": (C.c_int, [vp, vp]),
     "dav2_hip_minmax_partials": (u32, [u64]),
     "dav2_hip_reduce_minmax": (C.c_int, [vp, u64, vp, vp, vp]),
     "dav2_hip_normalize_relative": (C.c_int, [vp, vp, u64, vp]),
@@ -226,8 +229,8 @@ PROTOTYPES = {
     "dav2_ops_last_error": (C.c_char_p, []),
     "dav2_ops_stream": (vp, [vp]),
     "dav2_ops_synchronize": (C.c_int, [vp]),
-    "dav2_ops_linear_int8": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, i32]),
-    "dav2_ops_linear_int8_noalloc": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, i32]),
+    "dav2_ops_linear_int8": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, i32, i32]),
+    "dav2_ops_linear_int8_noalloc": (C.c_int, [vp, DB, DB, DB, DB, DB, u32, u32, u32, i32, i32]),
     "dav2_ops_layer_norm": (C.c_int, [vp, DB, DB, DB, DB, u32, u32, f32]),
     "dav2_ops_add_scaled": (C.c_int, [vp, DB, DB, DB, DB, u32, u32]),
     "dav2_ops_attention_head64": (C.c_int, [vp, DB, DB, u32, u32, DB, i32]),

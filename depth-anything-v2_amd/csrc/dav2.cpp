@@ -301,6 +301,13 @@ dav2_status DAV2_CALL dav2_submit_hip(dav2_context* context, const dav2_hip_subm
             (r.pixel_format != DAV2_GPU_PIXEL_BGRA8 && r.pixel_format != DAV2_GPU_PIXEL_RGBA8) ||
             (r.flags & ~static_cast<uint32_t>(DAV2_HIP_SUBMIT_WAIT_EVENT_IPC)) != 0)
             throw std::invalid_argument("invalid HIP GPU inference request");
+        // Waiting on another process's event: hipEventRecord of an
+        // interprocess event was refused by the runtime on the hardware this
+        // was built for, so the form could never be exercised; it is
+        // reported as unsupported rather than shipped untested. Producers in
+        // another process synchronise before publishing their handles.
+        if (r.flags & DAV2_HIP_SUBMIT_WAIT_EVENT_IPC)
+            throw ApiError(DAV2_STATUS_UNSUPPORTED, "waiting on an interprocess HIP event is not supported");
         if (static_cast<uint64_t>(r.row_stride_bytes) * r.height > r.input_byte_size ||
             r.width > static_cast<uint32_t>(INT32_MAX) || r.height > static_cast<uint32_t>(INT32_MAX))
             throw std::invalid_argument("HIP GPU input dimensions exceed the buffer");

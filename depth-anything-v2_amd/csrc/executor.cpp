@@ -249,7 +249,6 @@ HipJob::~HipJob() {
         (void)hipEventSynchronize(done_);
         (void)hipEventDestroy(done_);
     }
-    if (ipc_wait_) (void)hipEventDestroy(ipc_wait_);
     if (mapped_input_) (void)hipIpcCloseMemHandle(mapped_input_);
     if (mapped_output_) (void)hipIpcCloseMemHandle(mapped_output_);
     if (previous >= 0) (void)hipSetDevice(previous);
@@ -294,12 +293,7 @@ std::unique_ptr<HipJob> HipExecutor::submit_hip(const dav2_hip_submit_request& r
                   "open output IPC handle");
         output = reinterpret_cast<float*>(static_cast<std::uint8_t*>(job->mapped_output_) + r.output_offset);
     }
-    if (r.flags & DAV2_HIP_SUBMIT_WAIT_EVENT_IPC) {
-        hipIpcEventHandle_t h;
-        std::memcpy(&h, r.wait_event_ipc, sizeof(h));
-        hip_check(hipIpcOpenEventHandle(&job->ipc_wait_, h), "open wait event IPC handle");
-        hip_check(hipStreamWaitEvent(main, job->ipc_wait_, 0), "wait for the producer");
-    } else if (r.wait_event) {
+    if (r.wait_event) {
         hip_check(hipStreamWaitEvent(main, static_cast<hipEvent_t>(r.wait_event), 0), "wait for the producer");
     }
     // vulkan_executor.cpp:694-787: GPU preprocessing, inference, min/max

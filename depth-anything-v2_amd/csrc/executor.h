@@ -28,7 +28,6 @@ private:
     friend class HipExecutor;
     int device_ = 0;
     hipEvent_t done_ = nullptr;
-    hipEvent_t ipc_wait_ = nullptr;
     void* mapped_input_ = nullptr;
     void* mapped_output_ = nullptr;
     std::atomic<bool> cancelled_{false};

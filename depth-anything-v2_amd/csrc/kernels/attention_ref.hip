@@ -456,6 +456,264 @@ __global__ __launch_bounds__(256) void ref_values_kernel(float* __restrict__ out
     }
 }
 
+// ---------------------------------------------------------------------------
+// The binary16 pipeline fused per block of R query rows: the same arithmetic
+// as the three kernels above, and the same bits, without the score round trip
+// through memory. A workgroup computes its rows' binary16 scores against every
+// key into LDS, runs the softmax on them there and then the value sums.
+//
+// Keys and values are first rounded to binary16 once (ref16_pack_kernel)
+// into chunks of 64 tokens laid out the way the LDS reads want them:
+//   keys   chunk c: word (p, kk) = (k[64c+kk][2p], k[64c+kk][2p+1]), p < 32
+//   values chunk c: word (q, f)  = (v[64c+2q][f], v[64c+2q+1][f]),   q < 32
+// (64 x 32 words = 8 KB each, zero past the last token). One v_pk_mul_f16 on
+// a q pair and a key word gives the binary16 products of features 2p and
+// 2p+1 of one score, in feature order; on a probability pair and a value word
+// the products of keys 2q and 2q+1 of one output, in key order. Each product
+// is then added to its fp32 sum by v_fma_mix_f32 (the binary16 half widened
+// exactly, times 1.0, plus the sum, one rounding): the shaders'
+// sum += float(a16 * b16) at 1.5 VALU instructions per product.
+constexpr uint32_t kChunkWords = 32u * 64u;  // one 64-token chunk of keys or values
+
+// acc = (acc + float(lo(prod))) + float(hi(prod)), two IEEE fp32 additions.
+DAV2_DEV void add_product_pair(float& acc, uint32_t prod, float one) {
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "+v"(acc)
+        : "v"(prod), "v"(one));
+}
+
+DAV2_DEV uint32_t mul_half2(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
+}
+
+__global__ __launch_bounds__(256) void ref16_pack_kernel(const float* __restrict__ qkv, uint32_t* __restrict__ k16,
+                                                         uint32_t* __restrict__ v16, uint32_t tokens, uint32_t heads,
+                                                         uint32_t chunks) {
+    const uint32_t c = blockIdx.x, bh = blockIdx.y;
+    const uint32_t b = bh / heads, h = bh - b * heads;
+    const uint32_t D = heads * 64u;
+    const float* base = qkv + static_cast<uint64_t>(b) * tokens * 3u * D + h * 64u;
+    const uint32_t lane = threadIdx.x & 63u, part = threadIdx.x >> 6;
+    const uint64_t chunk = (static_cast<uint64_t>(bh) * chunks + c) * kChunkWords;
+    // keys: lane = token of the chunk, part = features 16*part .. +15
+    const uint32_t j = c * 64u + lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j < tokens)
+            v = *reinterpret_cast<const float4*>(base + static_cast<uint64_t>(j) * 3u * D + D + 16u * part + 4u * i);
+        const uint32_t p = 8u * part + 2u * i;
+        k16[chunk + p * 64u + lane] = pack_half2(v.x, v.y);
+        k16[chunk + (p + 1u) * 64u + lane] = pack_half2(v.z, v.w);
+    }
+    // values: lane = feature, part = token pairs 8*part .. +7
+    const float* vb = base + 2u * D + lane;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t q = 8u * part + i, j0 = c * 64u + 2u * q;
+        const float lo = j0 < tokens ? vb[static_cast<uint64_t>(j0) * 3u * D] : 0.0f;
+        const float hi = j0 + 1u < tokens ? vb[static_cast<uint64_t>(j0 + 1u) * 3u * D] : 0.0f;
+        v16[chunk + q * 64u + lane] = pack_half2(lo, hi);
+    }
+}
+
+// R query rows per workgroup of 256 threads; thread t owns row t % R and, of
+// each 64-token chunk, keys (for the scores) or features (for the values)
+// G*(t / R) .. +G-1, G = R / 4. LDS: the chunk double buffer (16 KB), then the
+// rows' binary16 scores / probabilities, `stride` words per row (4 more than
+// a multiple of 32, so the 16 rows' 16-byte reads fall on different banks).
+template <int R>
+__global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ out, const float* __restrict__ qkv,
+                                                          const uint32_t* __restrict__ k16,
+                                                          const uint32_t* __restrict__ v16, uint32_t tokens,
+                                                          uint32_t heads, uint32_t chunks, uint32_t row_blocks,
+                                                          uint32_t stride) {
+    constexpr int G = R / 4;  // keys or features per thread and chunk
+    static_assert(G == 2 || G == 4, "two or four keys per thread");
+    typedef uint32_t wordsG __attribute__((ext_vector_type(G)));
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    uint32_t* const kv = lds;                     // [2][kChunkWords]
+    uint32_t* const srows = lds + 2 * kChunkWords;  // [R][stride]
+
+    // XCD-banded order: workgroup L runs on XCD L % 8, and each XCD takes a
+    // contiguous range of (head, row block) items, so a head's keys and
+    // values stay in one L2.
+    const uint32_t L = blockIdx.x, n = gridDim.x;
+    const uint32_t xcd = L & 7u, per = n >> 3, extra = n & 7u;
+    const uint32_t work = xcd * per + min(xcd, extra) + (L >> 3);
+    const uint32_t bh = work / row_blocks, rb = work - bh * row_blocks;
+    const uint32_t b = bh / heads, h = bh - b * heads;
+    const uint32_t D = heads * 64u;
+    const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
+    const uint32_t r = t % R, grp = t / R;
+    const uint32_t i = rb * R + r;
+    const uint32_t* kbase = k16 + static_cast<uint64_t>(bh) * chunks * kChunkWords;
+    const uint32_t* vbase = v16 + static_cast<uint64_t>(bh) * chunks * kChunkWords;
+    const float one = 1.0f;
+
+    // chunk c of src into buffer buf: 8 KB, two 1 KB blocks per wave
+    auto stage = [&](const uint32_t* src, uint32_t c, uint32_t buf) {
+        const uint32_t* s0 = src + static_cast<uint64_t>(c) * kChunkWords;
+#pragma unroll
+        for (uint32_t it = 0; it < 2; ++it) {
+            const uint32_t blk = wave * 2u + it;
+            copy16_to_lds(s0 + blk * 256u + lane * 4u, kv + buf * kChunkWords + blk * 256u);
+        }
+    };
+
+    stage(kbase, 0, 0);
+    // q row i as binary16 pairs of q * 0.125 (bmm_score_fp16.glsl:32)
+    uint32_t qp[32];
+    {
+        const float* q = qkv + (static_cast<uint64_t>(b) * tokens + (i < tokens ? i : 0u)) * 3u * D + h * 64u;
+#pragma unroll
+        for (int f4 = 0; f4 < 16; ++f4) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < tokens) v = *reinterpret_cast<const float4*>(q + 4 * f4);
+            qp[2 * f4] = pack_half2(v.x * 0.125f, v.y * 0.125f);
+            qp[2 * f4 + 1] = pack_half2(v.z * 0.125f, v.w * 0.125f);
+        }
+    }
+
+    // scores: s = sum over features 0..63 of float(q16 * k16), stored binary16
+    uint32_t* const myrow = srows + r * stride;
+    for (uint32_t c = 0; c < chunks; ++c) {
+        if (c + 1u < chunks) {
+            stage(kbase, c + 1u, (c + 1u) & 1u);
+            DAV2_WAIT_VMCNT(2);
+        } else {
+            DAV2_WAIT_VMCNT(0);
+        }
+        __syncthreads();
+        const uint32_t* kc = kv + (c & 1u) * kChunkWords + grp * G;
+        float acc[G];
+#pragma unroll
+        for (int kk = 0; kk < G; ++kk) acc[kk] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 32; ++p) {
+            const wordsG kw = *reinterpret_cast<const wordsG*>(kc + p * 64);
+#pragma unroll
+            for (int kk = 0; kk < G; ++kk) add_product_pair(acc[kk], mul_half2(qp[p], kw[kk]), one);
+        }
+        // keys 64c + G*grp + kk -> words 32c + G*grp/2 + kk/2 (packHalf2x16)
+        if (G == 4) {
+            *reinterpret_cast<uint2*>(myrow + 32u * c + 2u * grp) =
+                make_uint2(pack_half2(acc[0], acc[1]), pack_half2(acc[G - 2], acc[G - 1]));
+        } else {
+            myrow[32u * c + grp] = pack_half2(acc[0], acc[1]);
+        }
+        __syncthreads();
+    }
+
+    // the first value chunk arrives during the softmax
+    stage(vbase, 0, 0);
+
+    // softmax_lastdim_half.glsl:19-65 on each row: the maximum; e = exp(s -
+    // max) stored binary16 while virtual lane L (words L, L + 128, ...; lane
+    // holds L and L + 64) sums (e.x + e.y) in fp32; the 128 partials by the
+    // halving tree; p = binary16(float(binary16(e)) * (1 / max(sum, 1e-20))).
+    const uint32_t words = (tokens + 1u) >> 1;
+    for (uint32_t rr = wave; rr < static_cast<uint32_t>(R); rr += 4u) {
+        uint32_t* row = srows + rr * stride;
+        float maximum = -3.402823466e+38f;
+        for (uint32_t w = lane; w < words; w += 64u) {
+            const uint32_t pair = row[w];
+            maximum = fmaxf(maximum, half_lo(pair));
+            if (2u * w + 1u < tokens) maximum = fmaxf(maximum, half_hi(pair));
+        }
+        maximum = wave_max(maximum);
+        float partial[2];
+#pragma unroll
+        for (uint32_t v = 0; v < 2; ++v) {
+            float d = 0.0f;
+            for (uint32_t w = lane + 64u * v; w < words; w += 128u) {
+                const uint32_t pair = row[w];
+                const float ea = exp_cw(half_lo(pair) - maximum);
+                const float eb = 2u * w + 1u < tokens ? exp_cw(half_hi(pair) - maximum) : 0.0f;
+                row[w] = pack_half2(ea, eb);
+                d = d + (ea + eb);
+            }
+            partial[v] = d;
+        }
+        const float sum = wave_sum_tree(partial[0] + partial[1]);
+        const float inverse = div_rn(1.0f, fmaxf(sum, 1.0e-20f));
+        for (uint32_t w = lane; w < words; w += 64u) {
+            const uint32_t pair = row[w];
+            row[w] = pack_half2(half_lo(pair) * inverse, half_hi(pair) * inverse);
+        }
+    }
+
+    // values: out = sum over tokens 0..T-1 of float(p16 * v16), in order
+    float acc[G];
+#pragma unroll
+    for (int f = 0; f < G; ++f) acc[f] = 0.0f;
+    for (uint32_t c = 0; c < chunks; ++c) {
+        if (c + 1u < chunks) {
+            stage(vbase, c + 1u, (c + 1u) & 1u);
+            DAV2_WAIT_VMCNT(2);
+        } else {
+            DAV2_WAIT_VMCNT(0);
+        }
+        __syncthreads();  // (c = 0: also the end of every row's softmax)
+        const uint32_t* vc = kv + (c & 1u) * kChunkWords + grp * G;
+        const uint32_t* pc = myrow + 32u * c;
+        if (64u * c + 64u <= tokens) {
+#pragma unroll 2
+            for (int q4 = 0; q4 < 32; q4 += 4) {
+                const uint4 pw = *reinterpret_cast<const uint4*>(pc + q4);
+                const uint32_t pq[4] = {pw.x, pw.y, pw.z, pw.w};
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) {
+                    const wordsG vw = *reinterpret_cast<const wordsG*>(vc + (q4 + qq) * 64);
+#pragma unroll
+                    for (int f = 0; f < G; ++f) add_product_pair(acc[f], mul_half2(pq[qq], vw[f]), one);
+                }
+            }
+        } else {
+            // the last, partial chunk: tokens 64c .. T-1 only
+            const uint32_t left = tokens - 64u * c;
+            for (uint32_t q = 0; 2u * q < left; ++q) {
+                const uint32_t pw = pc[q];
+                const wordsG vw = *reinterpret_cast<const wordsG*>(vc + q * 64u);
+                if (2u * q + 1u < left) {
+#pragma unroll
+                    for (int f = 0; f < G; ++f) add_product_pair(acc[f], mul_half2(pw, vw[f]), one);
+                } else {
+#pragma unroll
+                    for (int f = 0; f < G; ++f) acc[f] = acc[f] + half_lo(mul_half2(pw, vw[f]));
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (i < tokens) {
+        float* o = out + (static_cast<uint64_t>(b) * tokens + i) * D + h * 64u + grp * G;
+        if (G == 4)
+            *reinterpret_cast<float4*>(o) = make_float4(acc[0], acc[1], acc[G - 2], acc[G - 1]);
+        else
+            *reinterpret_cast<float2*>(o) = make_float2(acc[0], acc[1]);
+    }
+}
+
+uint32_t ref16_chunks(uint32_t tokens) { return (tokens + 63u) / 64u; }
+
+// Rows per workgroup and the LDS they need: 16 rows while two workgroups fit
+// a CU (T up to 1984), 8 rows up to the 160 KB of one workgroup.
+struct Ref16Shape {
+    int rows;
+    uint32_t stride;
+    uint32_t lds;
+};
+
+Ref16Shape ref16_shape(uint32_t tokens) {
+    const uint32_t stride = ref16_chunks(tokens) * 32u + 4u;
+    const uint32_t kv_bytes = 2u * kChunkWords * 4u;
+    if (kv_bytes + 16u * stride * 4u <= 80u * 1024u) return {16, stride, kv_bytes + 16u * stride * 4u};
+    if (kv_bytes + 8u * stride * 4u <= 160u * 1024u) return {8, stride, kv_bytes + 8u * stride * 4u};
+    return {0, stride, 0};
+}
+
 template <bool HALF>
 hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream_t s) {
     const uint32_t items = HALF ? (columns + 1u) >> 1 : columns;
@@ -515,6 +773,42 @@ int dav2_hip_attention_ref_softmax(void* scores, uint64_t rows, uint32_t columns
     if (rows == 0) return hipSuccess;
     hipStream_t s = static_cast<hipStream_t>(stream);
     return fp16 ? launch_softmax<true>(scores, rows, columns, s) : launch_softmax<false>(scores, rows, columns, s);
+}
+
+uint64_t dav2_hip_attention_ref16_fused_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch) {
+    if (ref16_shape(tokens).rows == 0) return 0;
+    return 2ull * batch * heads * ref16_chunks(tokens) * kChunkWords * 4u;
+}
+
+int dav2_hip_attention_ref16_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads, uint32_t batch,
+                                   void* scratch, uint64_t scratch_bytes, void* stream) {
+    if (!out || !qkv || !scratch || !valid(tokens, heads, batch)) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(scratch)) &
+        15)
+        return hipErrorInvalidValue;
+    const Ref16Shape shape = ref16_shape(tokens);
+    const uint64_t need = dav2_hip_attention_ref16_fused_scratch_bytes(tokens, heads, batch);
+    if (shape.rows == 0 || scratch_bytes < need) return hipErrorInvalidValue;
+    const uint32_t chunks = ref16_chunks(tokens), bh = batch * heads;
+    const uint32_t row_blocks = (tokens + shape.rows - 1u) / shape.rows;
+    const uint64_t items = static_cast<uint64_t>(row_blocks) * bh;
+    if (items > 0x7fffffffull) return hipErrorInvalidValue;
+    uint32_t* k16 = static_cast<uint32_t*>(scratch);
+    uint32_t* v16 = k16 + static_cast<uint64_t>(bh) * chunks * kChunkWords;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    dispatch(ref16_pack_kernel, dim3(chunks, bh), dim3(256), 0, s, qkv, k16, v16, tokens, heads, chunks);
+#define DAV2_REF16_CASE(R)                                                                                         \
+    {                                                                                                              \
+        static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(ref16_fused_kernel<R>), \
+                                                             hipFuncAttributeMaxDynamicSharedMemorySize,          \
+                                                             static_cast<int>(160u * 1024u));                     \
+        if (lds_ok != hipSuccess) return lds_ok;                                                                   \
+        dispatch(ref16_fused_kernel<R>, dim3(static_cast<uint32_t>(items)), dim3(256), shape.lds, s, out, qkv, k16, \
+                 v16, tokens, heads, chunks, row_blocks, shape.stride);                                            \
+    }
+    if (shape.rows == 16) DAV2_REF16_CASE(16) else DAV2_REF16_CASE(8)
+#undef DAV2_REF16_CASE
+    return hipGetLastError();
 }
 
 int dav2_hip_attention_ref_values(float* out, const void* probabilities, const float* qkv, uint32_t tokens,

@@ -219,6 +219,7 @@ DAV2_DEV void store_nt(float* dst, float4 v) {
 // and not the host's launch gaps before the first one.
 struct LaunchEvents {
     hipEvent_t start, stop;
+    bool launched;  // a kernel recorded the pair since it was set
 };
 LaunchEvents& launch_events();
 
@@ -228,6 +229,7 @@ void dispatch(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stre
     if (e.start || e.stop) {
         hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), stream, e.start, e.stop, 0, args...);
         e.start = nullptr;
+        e.launched = true;
     } else {
         hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
     }

@@ -260,14 +260,17 @@ __global__ __launch_bounds__(kBlock) void finish_tokens_kernel(float* tokens, co
 }  // namespace
 
 LaunchEvents& dav2k::launch_events() {
-    thread_local LaunchEvents events{nullptr, nullptr};
+    thread_local LaunchEvents events{nullptr, nullptr, false};
     return events;
 }
 
 extern "C" {
 
-void dav2_hip_launch_events(void* start, void* stop) {
-    launch_events() = LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
+int dav2_hip_launch_events(void* start, void* stop) {
+    LaunchEvents& e = launch_events();
+    const int launched = e.launched ? 1 : 0;
+    e = LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop), false};
+    return launched;
 }
 
 int dav2_hip_gelu(float* out, const float* input, uint64_t count, void* stream) {

@@ -679,7 +679,40 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(const int8_t* __restrict_
     *reinterpret_cast<uint4*>(dst + row * ld + c0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// int8 weights in the reference's transposed layout ([K][N] bytes, element
+// (k, n) = weight of output n, input k; src/gpu_model.cpp:241-258) to the GEMM
+// layout ([N][ld] bytes, zero for k >= K): 64x64 byte tiles through LDS, the
+// reads coalesced along n, the writes along k.
+__global__ __launch_bounds__(256) void transpose_rows_kernel(const int8_t* __restrict__ src, uint32_t k_rows,
+                                                             uint32_t n_columns, int8_t* __restrict__ dst,
+                                                             uint32_t ld) {
+    __shared__ int8_t tile[64][65];
+    const uint32_t n0 = blockIdx.x * 64u, k0 = blockIdx.y * 64u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t idx = threadIdx.x + 256u * i, r = idx / 64u, c = idx % 64u;
+        const uint32_t k = k0 + r, n = n0 + c;
+        tile[r][c] = (k < k_rows && n < n_columns) ? src[uint64_t(k) * n_columns + n] : int8_t(0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t idx = threadIdx.x + 256u * i, r = idx / 64u, c = idx % 64u;
+        const uint32_t n = n0 + r;
+        if (n < n_columns) dst[uint64_t(n) * ld + k0 + c] = tile[c][r];
+    }
+}
+
 extern "C" {
+
+int dav2_hip_transpose_rows_i8(const int8_t* src, uint32_t k_rows, uint32_t n_columns, int8_t* dst, uint32_t ld,
+                               void* stream) {
+    if (k_rows == 0 || n_columns == 0) return hipSuccess;
+    if (!src || !dst || ld < k_rows || ld % 64u || ld / 64u > 65535u) return hipErrorInvalidValue;
+    dispatch(transpose_rows_kernel, dim3(ceil_div(n_columns, 64u), ld / 64u), dim3(256), 0,
+             static_cast<hipStream_t>(stream), src, k_rows, n_columns, dst, ld);
+    return hipGetLastError();
+}
 
 int dav2_hip_pad_rows_i8(const int8_t* src, uint32_t rows, uint32_t columns, int8_t* dst, uint32_t ld,
                          void* stream) {

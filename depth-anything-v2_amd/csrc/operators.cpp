@@ -42,24 +42,42 @@ DeviceBuffer& grow(DeviceBuffer& buffer, std::uint64_t bytes) {
 
 DeviceBuffer& Int8Workspace::packed(std::uint64_t bytes) { return grow(packed_, bytes); }
 DeviceBuffer& Int8Workspace::scales(std::uint64_t bytes) { return grow(scales_, bytes); }
+DeviceBuffer& Int8Workspace::weight(std::uint64_t bytes) { return grow(weight_, bytes); }
 
 HipOperators::HipOperators(HipContext& context) : context_(context) {}
 
 // ---------------------------------------------------------------------------
-// src/operators.cpp:770-845
+// src/operators.cpp:770-845. weight_transposed: int8_weight is the
+// reference's [K][N] byte layout (int8_transposed_buffer, gpu_model.cpp:
+// 241-258), turned into the GEMM's rows on this stream first; the result is
+// the same as for the [N][K] weight.
 void HipOperators::linear_int8(DeviceBuffer& output, const DeviceBuffer& input, const DeviceBuffer& int8_weight,
                                const DeviceBuffer& weight_scales, const DeviceBuffer& bias, std::uint32_t rows,
                                std::uint32_t input_columns, std::uint32_t output_columns, bool gelu,
-                               bool /*weight_transposed: the NV cooperative-matrix layout is not used*/) {
+                               bool weight_transposed) {
     if (rows == 0 || input_columns == 0 || output_columns == 0 || input_columns % 4 != 0)
         throw std::invalid_argument("invalid INT8 linear dimensions");
     require_bytes(input, std::uint64_t(rows) * input_columns, "input");
-    require_int8_weight(int8_weight, output_columns, input_columns, "packed INT8 weight buffer");
+    const DeviceBuffer* weight = &int8_weight;
+    if (weight_transposed) {
+        if (int8_weight.size() < std::uint64_t(output_columns) * input_columns)
+            throw std::invalid_argument("transposed INT8 weight buffer is too small");
+    } else {
+        require_int8_weight(int8_weight, output_columns, input_columns, "packed INT8 weight buffer");
+    }
     require_bytes(weight_scales, output_columns, "weight scale");
     require_bytes(bias, output_columns, "bias");
     require_bytes(output, std::uint64_t(rows) * output_columns, "output");
+    if (weight_transposed) {
+        const std::uint32_t ld = ld64(input_columns);
+        DeviceBuffer& rows_layout = workspace_.weight(std::uint64_t(output_columns) * ld);
+        hip_check(dav2_hip_transpose_rows_i8(int8_weight.as<int8_t>(), input_columns, output_columns,
+                                             rows_layout.as<int8_t>(), ld, stream()),
+                  "transpose int8 weight");
+        weight = &rows_layout;
+    }
     quantize_rows(input, 0, rows, input_columns);
-    linear_int8_prequantized(output, int8_weight, weight_scales, &bias, rows, input_columns, output_columns,
+    linear_int8_prequantized(output, *weight, weight_scales, &bias, rows, input_columns, output_columns,
                              gelu ? Epilogue::row_gelu : Epilogue::row);
 }
 
@@ -174,6 +192,11 @@ void HipOperators::linear_int8_prequantized(DeviceBuffer& output, const DeviceBu
     a.gamma = gamma ? gamma->as<float>() : nullptr;
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
                       stream());
+    prof.shape(rows, output_columns, input_columns,
+               epilogue == Epilogue::row        ? "row"
+               : epilogue == Epilogue::row_gelu ? "row_gelu"
+               : epilogue == Epilogue::row_colmax ? "row_colmax"
+                                                  : "row_layerscale");
     hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
 }
 
@@ -216,6 +239,9 @@ void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& 
     }
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * rows * output_columns * input_columns, "OP",
                       stream());
+    prof.shape(rows, output_columns, input_columns, output_transposed ? (residual ? "transposed_residual"
+                                                                                  : "transposed")
+                                                                      : "row");
     hip_check(dav2_hip_gemm_i8(&a, stream()), "int8 GEMM");
 }
 
@@ -285,6 +311,18 @@ void HipOperators::attention_batched(DeviceBuffer& output, const DeviceBuffer& q
     const double flops = 2.0 * batch * heads * double(tokens) * tokens * 64.0;
     const double score_bytes = double(dav2_hip_attention_ref_scratch_bytes(tokens, heads, batch, fp16));
     Profiler& prof = context_.profiler();
+    if (fp16) {
+        // the same bits in one pass per query block, when the scratch holds
+        // its binary16 keys and values (all but the shortest sequences)
+        const std::uint64_t fused = dav2_hip_attention_ref16_fused_scratch_bytes(tokens, heads, batch);
+        if (fused != 0 && scores.size() >= fused) {
+            ProfileScope p(prof, "attention_ref16_fused", 2.0 * flops, "FLOP", s);
+            hip_check(dav2_hip_attention_ref16_fused(output.as<float>(), qkv.as<float>(), tokens, heads, batch,
+                                                     scores.data(), scores.size(), s),
+                      "fused binary16 attention");
+            return;
+        }
+    }
     {
         ProfileScope p(prof, fp16 ? "attention_scores_ref_f16" : "attention_scores_ref_f32", flops, "FLOP", s);
         hip_check(dav2_hip_attention_ref_scores(scores.data(), qkv.as<float>(), tokens, heads, batch, fp16, s),
@@ -859,6 +897,7 @@ void HipOperators::conv_transpose_nonoverlap_int8(DeviceBuffer& output, const De
     a.convt_height = input_height;
     a.convt_channels = output_channels;
     ProfileScope prof(context_.profiler(), "gemm_i8", 2.0 * input_rows * weight_rows * input_channels, "OP", s);
+    prof.shape(input_rows, weight_rows, input_channels, "convt");
     hip_check(dav2_hip_gemm_i8(&a, s), "transposed convolution GEMM");
 }
 

@@ -49,10 +49,14 @@ class Int8Workspace {
 public:
     DeviceBuffer& packed(std::uint64_t bytes);
     DeviceBuffer& scales(std::uint64_t bytes);
+    // weights handed over in the reference's transposed [K][N] layout,
+    // turned into the GEMM's [N][ld] rows
+    DeviceBuffer& weight(std::uint64_t bytes);
 
 private:
     DeviceBuffer packed_;
     DeviceBuffer scales_;
+    DeviceBuffer weight_;
 };
 
 class HipOperators {

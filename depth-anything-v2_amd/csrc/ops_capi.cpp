@@ -20,8 +20,6 @@ struct dav2_ops {
     // int8 weights of the reference layout repacked to the GEMM layout when
     // their row length is not a multiple of 64 (grown on demand)
     dav2::DeviceBuffer padded_weight;
-    // this device's copy of the no-allocation scratch array (below)
-    std::uint8_t* noalloc_scratch = nullptr;
 };
 
 namespace {
@@ -87,14 +85,29 @@ dav2::DeviceBuffer reference_int8_weight(dav2_ops& o, const dav2_device_buffer& 
 // Scratch of dav2_ops_linear_int8_noalloc: a file-scope device array, one
 // copy per GPU, held from module load until the process ends. Host code
 // never passes the array's name to a kernel (in host code it is a stand-in,
-// not a device address): dav2_ops_create looks up this device's address of it
-// once per device with hipGetSymbolAddress, and the entry point passes that.
+// not a device address): the entry point's first call on a device looks up
+// that device's address of it with hipGetSymbolAddress, and every call
+// passes that.
 constexpr std::uint64_t kNoAllocScratchBytes = 32ull << 20;
 static __device__ __align__(256) std::uint8_t scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
 std::atomic<std::uint8_t*> scratch_address[kMaxDevices];
 std::mutex scratch_lookup;
+
+// Order of the no-allocation calls on one GPU: every instance has its own
+// stream, and all of them share the device's scratch, so each call makes its
+// stream wait for the previous call's last kernel (an event per device,
+// created with the first instance on that device) and records the event
+// after its own. The mutex keeps wait + enqueue + record of one call
+// together. Streams under graph capture are left alone (their work runs when
+// the graph is launched, and a wait on an event recorded outside the capture
+// is not allowed there).
+struct NoAllocOrder {
+    std::mutex mutex;
+    hipEvent_t done = nullptr;
+};
+NoAllocOrder noalloc_order[kMaxDevices];
 
 // Address of the current device's copy of `scratch` (the caller made
 // `device` current).
@@ -130,7 +143,13 @@ dav2_ops* DAV2_CALL dav2_ops_create(int32_t device_index) {
         o->context = std::make_unique<dav2::HipContext>(device_index);
         o->ops = std::make_unique<dav2::HipOperators>(*o->context);
         o->context->make_current();
-        o->noalloc_scratch = device_scratch(o->context->device());
+        const int device = o->context->device();
+        if (device >= 0 && device < kMaxDevices) {
+            std::lock_guard<std::mutex> lock(noalloc_order[device].mutex);
+            if (!noalloc_order[device].done)
+                dav2::hip_check(hipEventCreateWithFlags(&noalloc_order[device].done, hipEventDisableTiming),
+                                "no-allocation call order event");
+        }
         return o.release();
     } catch (const std::exception& e) {
         ops_error = e.what();
@@ -148,55 +167,80 @@ dav2_status DAV2_CALL dav2_ops_synchronize(dav2_ops* ops) {
 
 dav2_status DAV2_CALL dav2_ops_linear_int8(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
                                           dav2_device_buffer w8, dav2_device_buffer ws, dav2_device_buffer bias,
-                                          uint32_t rows, uint32_t ic, uint32_t oc, int32_t gelu) {
+                                          uint32_t rows, uint32_t ic, uint32_t oc, int32_t gelu,
+                                          int32_t weight_transposed) {
     return guard(ops, [&](dav2::HipOperators& o) {
         auto out = v(output);
+        if (weight_transposed) {
+            // [ic][oc] bytes, turned into rows by the operator itself
+            o.linear_int8(out, v(input), v(w8), v(ws), v(bias), rows, ic, oc, gelu != 0, true);
+            return;
+        }
         const auto w = reference_int8_weight(*ops, w8, oc, ic, "packed INT8 weight buffer");
         o.linear_int8(out, v(input), w, v(ws), v(bias), rows, ic, oc, gelu != 0);
     });
 }
 
 // linear_int8 without allocating: the quantized rows (rows x roundup(ic, 64)
-// bytes), their scales and, when ic % 64 != 0, the padded weight rows live in
-// this GPU's copy of `scratch`, laid out [packed][scales][weight], each part
-// 256-byte aligned. Every byte a kernel reads there was written earlier in the
-// same call (the quantizer writes the zero padding of each row itself), so
-// nothing needs clearing; calls that overlap on one GPU race on the array.
+// bytes), their scales and, when ic % 64 != 0 or the weight comes transposed,
+// the weight rows in the GEMM layout live in this GPU's copy of `scratch`,
+// laid out [packed][scales][weight], each part 256-byte aligned. Every byte a
+// kernel reads there was written earlier in the same call (the quantizer
+// writes the zero padding of each row itself), so nothing needs clearing.
+// Calls on one GPU are ordered through the device's event (NoAllocOrder);
+// calls under graph capture are not, and captured graphs replayed while
+// another call runs on the same GPU race on the array.
 dav2_status DAV2_CALL dav2_ops_linear_int8_noalloc(dav2_ops* ops, dav2_device_buffer output, dav2_device_buffer input,
                                                   dav2_device_buffer w8, dav2_device_buffer ws,
                                                   dav2_device_buffer bias, uint32_t rows, uint32_t ic, uint32_t oc,
-                                                  int32_t gelu) {
+                                                  int32_t gelu, int32_t weight_transposed) {
     return guard(ops, [&](dav2::HipOperators& o) {
         if (rows == 0 || ic == 0 || oc == 0 || ic % 4 != 0)
             throw std::invalid_argument("invalid INT8 linear dimensions");
         if (w8.data == nullptr || w8.bytes < std::uint64_t(oc) * ic)
-            throw std::invalid_argument("packed INT8 weight buffer is too small");
+            throw std::invalid_argument(weight_transposed ? "transposed INT8 weight buffer is too small"
+                                                          : "packed INT8 weight buffer is too small");
         const std::uint64_t ld = ld64(ic);
         const std::uint64_t packed_bytes = align256(std::uint64_t(rows) * ld);
         const std::uint64_t scale_bytes = align256(std::uint64_t(rows) * sizeof(float));
-        const std::uint64_t weight_bytes = ic % 64 ? align256(std::uint64_t(oc) * ld) : 0;
+        const std::uint64_t weight_bytes = (ic % 64 || weight_transposed) ? align256(std::uint64_t(oc) * ld) : 0;
         if (packed_bytes + scale_bytes + weight_bytes > kNoAllocScratchBytes)
             throw std::invalid_argument(
                 "linear_int8_noalloc: rows x roundup(input_columns, 64) bytes of quantized rows, their scales and "
-                "the padded weight exceed the 32 MiB scratch");
-        std::uint8_t* base = ops->noalloc_scratch;
+                "the weight rows exceed the 32 MiB scratch");
+        const int device = ops->context->device();
+        std::uint8_t* base = device_scratch(device);
+        NoAllocOrder& order = noalloc_order[device];
+        std::lock_guard<std::mutex> lock(order.mutex);
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        dav2::hip_check(hipStreamIsCapturing(o.stream(), &capture), "capture status");
+        const bool ordered = capture == hipStreamCaptureStatusNone && order.done != nullptr;
+        if (ordered) dav2::hip_check(hipStreamWaitEvent(o.stream(), order.done, 0), "wait for the previous call");
         auto weight = v(w8);
         if (weight_bytes) {
-            std::uint8_t* padded = base + packed_bytes + scale_bytes;
-            for (std::uint64_t r0 = 0; r0 < oc; r0 += 65535) {
-                const std::uint64_t n = std::min<std::uint64_t>(65535, oc - r0);
-                dav2::hip_check(dav2_hip_pad_rows_i8(static_cast<const std::int8_t*>(w8.data) + r0 * ic,
-                                                     static_cast<std::uint32_t>(n), ic,
-                                                     reinterpret_cast<std::int8_t*>(padded + r0 * ld),
-                                                     static_cast<std::uint32_t>(ld), o.stream()),
-                                "pad int8 weight rows");
+            std::uint8_t* rows_layout = base + packed_bytes + scale_bytes;
+            if (weight_transposed) {
+                dav2::hip_check(dav2_hip_transpose_rows_i8(static_cast<const std::int8_t*>(w8.data), ic, oc,
+                                                           reinterpret_cast<std::int8_t*>(rows_layout),
+                                                           static_cast<std::uint32_t>(ld), o.stream()),
+                                "transpose int8 weight");
+            } else {
+                for (std::uint64_t r0 = 0; r0 < oc; r0 += 65535) {
+                    const std::uint64_t n = std::min<std::uint64_t>(65535, oc - r0);
+                    dav2::hip_check(dav2_hip_pad_rows_i8(static_cast<const std::int8_t*>(w8.data) + r0 * ic,
+                                                         static_cast<std::uint32_t>(n), ic,
+                                                         reinterpret_cast<std::int8_t*>(rows_layout + r0 * ld),
+                                                         static_cast<std::uint32_t>(ld), o.stream()),
+                                    "pad int8 weight rows");
+                }
             }
-            weight = dav2::DeviceBuffer::view(padded, std::uint64_t(oc) * ld);
+            weight = dav2::DeviceBuffer::view(rows_layout, std::uint64_t(oc) * ld);
         }
         auto out = v(output);
         o.linear_int8_in(out, v(input), weight, v(ws), v(bias), rows, ic, oc, gelu != 0,
                          dav2::DeviceBuffer::view(base, std::uint64_t(rows) * ld),
                          dav2::DeviceBuffer::view(base + packed_bytes, std::uint64_t(rows) * sizeof(float)));
+        if (ordered) dav2::hip_check(hipEventRecord(order.done, o.stream()), "record the call's end");
     });
 }
 

@@ -72,7 +72,7 @@ hipEvent_t Profiler::take_event() {
 
 int Profiler::begin(const char* name, double work, const char* unit, hipStream_t stream, bool dispatch_events) {
     if (!enabled_) return -1;
-    Record r{name, unit, work, take_event(), take_event(), dispatch_events};
+    Record r{name, unit, work, take_event(), take_event(), dispatch_events, true, {}};
     if (dispatch_events)
         dav2_hip_launch_events(r.start, r.stop);
     else
@@ -84,17 +84,27 @@ int Profiler::begin(const char* name, double work, const char* unit, hipStream_t
 void Profiler::end(int id, hipStream_t stream) {
     if (id < 0 || static_cast<std::size_t>(id) >= pending_.size()) return;
     if (pending_[id].dispatch)
-        dav2_hip_launch_events(nullptr, nullptr);  // the operation's launches are done
+        // the operation's launches are done; an operation that launched
+        // nothing (an empty range) left the events as an earlier one set them
+        pending_[id].launched = dav2_hip_launch_events(nullptr, nullptr) != 0;
     else
         (void)hipEventRecord(pending_[id].stop, stream);
+}
+
+void Profiler::set_shape(int id, std::uint32_t m, std::uint32_t n, std::uint32_t k, const char* tag) {
+    if (id < 0 || static_cast<std::size_t>(id) >= pending_.size()) return;
+    char buf[96];
+    std::snprintf(buf, sizeof(buf), "%ux%ux%u:%s", m, n, k, tag);
+    pending_[id].shape = buf;
 }
 
 std::string Profiler::report() {
     hip_check(hipDeviceSynchronize(), "profile synchronize");
     for (auto& r : pending_) {
         float ms = 0.0f;
-        // an event pair a launch never recorded (it failed) has no time
-        if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) {
+        // an event pair a launch never recorded (it failed, or the operation
+        // launched nothing) has no time
+        if (!r.launched || hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) {
             (void)hipGetLastError();
             free_.push_back(r.start);
             free_.push_back(r.stop);
@@ -105,6 +115,13 @@ std::string Profiler::report() {
         t.ms += ms;
         t.work += r.work;
         t.unit = r.unit;
+        if (!r.shape.empty()) {
+            Total& ts = totals_[r.name + "@" + r.shape];
+            ts.launches += 1;
+            ts.ms += ms;
+            ts.work += r.work;
+            ts.unit = r.unit;
+        }
         free_.push_back(r.start);
         free_.push_back(r.stop);
     }

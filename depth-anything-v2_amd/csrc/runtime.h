@@ -64,6 +64,9 @@ public:
     // around the enqueued work.
     int begin(const char* name, double work, const char* unit, hipStream_t stream, bool dispatch_events = true);
     void end(int id, hipStream_t stream);
+    // Adds a per-shape total "name@MxNxK:tag" for record `id` (GEMMs), beside
+    // the family total.
+    void set_shape(int id, std::uint32_t m, std::uint32_t n, std::uint32_t k, const char* tag);
     // Synchronises, folds pending records into the totals and returns them as
     // a JSON object {name: {"launches", "ms", "work", "unit"}}; then clears.
     std::string report();
@@ -75,6 +78,8 @@ private:
         double work;
         hipEvent_t start, stop;
         bool dispatch;
+        bool launched;  // false: the operation launched no kernel, nothing to time
+        std::string shape;
     };
     struct Total {
         std::uint64_t launches = 0;
@@ -94,6 +99,9 @@ public:
                  bool dispatch_events = true)
         : p_(p), s_(s), id_(p.begin(name, work, unit, s, dispatch_events)) {}
     ~ProfileScope() { p_.end(id_, s_); }
+    void shape(std::uint32_t m, std::uint32_t n, std::uint32_t k, const char* tag) {
+        if (id_ >= 0) p_.set_shape(id_, m, n, k, tag);
+    }
 
 private:
     Profiler& p_;

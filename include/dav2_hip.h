@@ -40,6 +40,13 @@ DAV2_API int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset
  * zero. rows <= 65535. No reference counterpart (a layout conversion). */
 DAV2_API int dav2_hip_pad_rows_i8(const int8_t* src, uint32_t rows, uint32_t columns, int8_t* dst, uint32_t ld,
                                   void* stream);
+/* The reference's transposed int8 weight layout (src/gpu_model.cpp:241-258,
+ * int8_transposed_buffer: [K][N] bytes, byte k*N + n = weight of output n,
+ * input k), consumed by linear_int8(..., weight_transposed=true)
+ * (src/operators.cpp:819-832), to the GEMM layout: N rows of ld bytes
+ * (ld % 64 == 0, ld >= K), zero beyond K. */
+DAV2_API int dav2_hip_transpose_rows_i8(const int8_t* src, uint32_t k_rows, uint32_t n_columns, int8_t* dst,
+                                        uint32_t ld, void* stream);
 
 /* Replaces im2col_quantize_int8.glsl:26-83 (src/operators.cpp:1284-1298,
  * :1787-1801, :1946-1960). CHW input; rows = output_width*output_height.
@@ -138,8 +145,10 @@ DAV2_API void dav2_hip_gemm_i8_events(void* start, void* stop);
 /* Timing hook, no reference counterpart: hipEvent_t start / stop for the
  * calling thread's kernel dispatches: the next kernel launched records start
  * when it begins, every launch until the hook is cleared (NULL, NULL) records
- * stop when it ends, so the pair spans all kernels of an operation. */
-DAV2_API void dav2_hip_launch_events(void* start, void* stop);
+ * stop when it ends, so the pair spans all kernels of an operation. Returns 1
+ * when a kernel launched under the pair being replaced, 0 when none did (its
+ * events then hold no record of that operation). */
+DAV2_API int dav2_hip_launch_events(void* start, void* stop);
 
 /* fp32 GEMM of the fp32 precision mode: out = a . b^T + bias with the
  * epilogues ROW, ROW_GELU, ROW_LAYERSCALE, TRANSPOSED (residual, relu_output)
@@ -309,6 +318,18 @@ DAV2_API int dav2_hip_attention_ref_softmax(void* scores, uint64_t rows, uint32_
 DAV2_API int dav2_hip_attention_ref_values(float* out, const void* probabilities, const float* qkv,
                                            uint32_t tokens, uint32_t heads, uint32_t batch, int fp16,
                                            void* stream);
+
+/* The binary16 pipeline above (bmm_score_fp16.glsl, softmax_lastdim_half.glsl,
+ * bmm_value_fp16.glsl) fused per block of query rows, the same bits as the
+ * three kernels: keys and values are rounded to binary16 once into the
+ * scratch (dav2_hip_attention_ref16_fused_scratch_bytes() bytes, 0 when T is
+ * beyond the fused kernel's LDS, above about 9000 tokens: then use the three
+ * kernels), then each workgroup keeps its rows' binary16 scores in LDS
+ * through the softmax and the value sums. No reference counterpart as one
+ * kernel; reference: src/operators.cpp:1132-1167. */
+DAV2_API uint64_t dav2_hip_attention_ref16_fused_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch);
+DAV2_API int dav2_hip_attention_ref16_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
+                                            uint32_t batch, void* scratch, uint64_t scratch_bytes, void* stream);
 
 /* Fused attention (int8-mode default): replaces the materialised binary16
  * path of src/operators.cpp:1132-1167 (bmm_score_fp16.glsl,

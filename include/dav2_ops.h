@@ -44,27 +44,37 @@ DAV2_API const char* DAV2_CALL dav2_ops_last_error(void);
 DAV2_API void* DAV2_CALL dav2_ops_stream(dav2_ops* ops);
 DAV2_API dav2_status DAV2_CALL dav2_ops_synchronize(dav2_ops* ops);
 
-/* src/operators.h:82-92 */
+/* src/operators.h:82-92 (VulkanOperators::linear_int8, same argument order).
+ * weight_transposed == 0: int8_weight is the GpuModel's int8_buffer,
+ * [output_columns][input_columns] bytes. weight_transposed != 0: it is the
+ * int8_transposed_buffer (src/gpu_model.cpp:241-258), [input_columns]
+ * [output_columns] bytes, byte k*N + n = weight of output n, input k; it is
+ * turned into rows on the instance's stream before the GEMM, and the output
+ * is bit-identical to the untransposed call's. */
 DAV2_API dav2_status DAV2_CALL dav2_ops_linear_int8(dav2_ops* ops, dav2_device_buffer output,
                                                     dav2_device_buffer input, dav2_device_buffer int8_weight,
                                                     dav2_device_buffer weight_scales, dav2_device_buffer bias,
                                                     uint32_t rows, uint32_t input_columns,
-                                                    uint32_t output_columns, int32_t gelu);
+                                                    uint32_t output_columns, int32_t gelu,
+                                                    int32_t weight_transposed);
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). Same arguments, checks and output bits as
  * dav2_ops_linear_int8, but the quantized input rows (rows x roundup(K, 64)
- * bytes), their scales and, when K % 64 != 0, the padded weight rows
- * (N x roundup(K, 64) bytes) go into a fixed 32 MiB device array per GPU
- * instead of the instance's growing workspace; the call allocates nothing.
- * Sizes beyond the array -> DAV2_STATUS_INVALID_ARGUMENT. Calls that overlap
- * on one GPU (two instances, two streams) race on the array: serialise them. */
+ * bytes), their scales and, when K % 64 != 0 or the weight is transposed, the
+ * weight rows (N x roundup(K, 64) bytes) go into a fixed 32 MiB device array
+ * per GPU instead of the instance's growing workspace; the call allocates
+ * nothing. Sizes beyond the array -> DAV2_STATUS_INVALID_ARGUMENT. Calls on
+ * one GPU from several instances (several streams) are ordered through a
+ * per-device event, each waiting for the previous call; calls enqueued under
+ * HIP graph capture are not, so a captured graph replayed while another call
+ * runs on the same GPU races on the array: serialise those. */
 DAV2_API dav2_status DAV2_CALL dav2_ops_linear_int8_noalloc(dav2_ops* ops, dav2_device_buffer output,
                                                             dav2_device_buffer input, dav2_device_buffer int8_weight,
                                                             dav2_device_buffer weight_scales,
                                                             dav2_device_buffer bias, uint32_t rows,
                                                             uint32_t input_columns, uint32_t output_columns,
-                                                            int32_t gelu);
+                                                            int32_t gelu, int32_t weight_transposed);
 /* src/operators.h:94-101 */
 DAV2_API dav2_status DAV2_CALL dav2_ops_layer_norm(dav2_ops* ops, dav2_device_buffer output,
                                                    dav2_device_buffer input, dav2_device_buffer weight,

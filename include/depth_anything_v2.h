@@ -370,8 +370,10 @@ DAV2_API dav2_status DAV2_CALL dav2_infer_tensor_f32_device(
  * pixels and the output a device buffer of width*height float32, each given
  * as a pointer in this process or, when the pointer is NULL, as a HIP IPC
  * memory handle exported by another process (plus a byte offset into that
- * allocation). The work waits for an optional HIP event (wait_event, or the
- * IPC event handle when DAV2_HIP_SUBMIT_WAIT_EVENT_IPC is set), then runs the
+ * allocation). The work waits for an optional HIP event of this process
+ * (wait_event; DAV2_HIP_SUBMIT_WAIT_EVENT_IPC, a wait on another process's
+ * event, returns DAV2_STATUS_UNSUPPORTED: a producer in another process
+ * finishes its writes before it publishes the handles), then runs the
  * GPU preprocessing (float32 cubic resize to network_shape(width, height,
  * input_size)), the inference, min/max normalisation and the bilinear resize
  * back to width x height, on the device and without host copies. The returned
@@ -398,7 +400,7 @@ typedef struct dav2_hip_submit_request {
     uint64_t output_offset;
     uint8_t input_ipc[64];      /* hipIpcMemHandle_t */
     uint8_t output_ipc[64];     /* hipIpcMemHandle_t */
-    uint8_t wait_event_ipc[64]; /* hipIpcEventHandle_t */
+    uint8_t wait_event_ipc[64]; /* reserved: DAV2_HIP_SUBMIT_WAIT_EVENT_IPC is unsupported */
     uint64_t source_frame_id;
     uint64_t timestamp_ns;
 } dav2_hip_submit_request;

@@ -104,6 +104,43 @@ inline int32_t dot_i8(const int8_t* a, const int8_t* b, uint32_t k) {
     return s;
 }
 
+inline int32_t hsum_epi32(__m256i v) {
+    __m128i x = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+    x = _mm_add_epi32(x, _mm_shuffle_epi32(x, 0x4e));
+    x = _mm_add_epi32(x, _mm_shuffle_epi32(x, 0xb1));
+    return _mm_cvtsi128_si32(x);
+}
+
+// 2 rows of a x 4 rows of b over k: 32 bytes at a time, |a| as unsigned bytes
+// times b carrying a's sign (_mm256_sign_epi8) in _mm256_maddubs_epi16 (pairs
+// of products: |sum| <= 2 * 128 * 127 < 2^15 for operands in [-128, 127]
+// that are not both -128; the quantizers only produce [-127, 127]), then
+// widened by _mm256_madd_epi16 with ones into int32. Every sum is exact, so
+// the order does not matter.
+inline void dot_i8_2x4(const int8_t* a0, const int8_t* a1, const int8_t* const* bj, uint32_t k, int32_t out[2][4]) {
+    const __m256i ones = _mm256_set1_epi16(1);
+    __m256i acc[2][4];
+    for (int r = 0; r < 2; ++r)
+        for (int c = 0; c < 4; ++c) acc[r][c] = _mm256_setzero_si256();
+    uint32_t kk = 0;
+    for (; kk + 32 <= k; kk += 32) {
+        const __m256i x0 = _mm256_loadu_si256(reinterpret_cast<const __m256i*>(a0 + kk));
+        const __m256i x1 = _mm256_loadu_si256(reinterpret_cast<const __m256i*>(a1 + kk));
+        const __m256i u0 = _mm256_abs_epi8(x0), u1 = _mm256_abs_epi8(x1);
+        for (int c = 0; c < 4; ++c) {
+            const __m256i y = _mm256_loadu_si256(reinterpret_cast<const __m256i*>(bj[c] + kk));
+            acc[0][c] = _mm256_add_epi32(acc[0][c],
+                                         _mm256_madd_epi16(_mm256_maddubs_epi16(u0, _mm256_sign_epi8(y, x0)), ones));
+            acc[1][c] = _mm256_add_epi32(acc[1][c],
+                                         _mm256_madd_epi16(_mm256_maddubs_epi16(u1, _mm256_sign_epi8(y, x1)), ones));
+        }
+    }
+    for (int c = 0; c < 4; ++c) {
+        out[0][c] = hsum_epi32(acc[0][c]) + (kk < k ? dot_i8(a0 + kk, bj[c] + kk, k - kk) : 0);
+        out[1][c] = hsum_epi32(acc[1][c]) + (kk < k ? dot_i8(a1 + kk, bj[c] + kk, k - kk) : 0);
+    }
+}
+
 void gemm_i8_blocked(const int8_t* a, const int8_t* b, uint32_t m, uint32_t n,
                      uint32_t k, int32_t* acc) {
     constexpr uint32_t MB = 32, NB = 64;
@@ -115,12 +152,25 @@ void gemm_i8_blocked(const int8_t* a, const int8_t* b, uint32_t m, uint32_t n,
         const uint32_t nb = static_cast<uint32_t>(t % nblocks);
         const uint32_t m0 = mb * MB, m1 = std::min(m, m0 + MB);
         const uint32_t n0 = nb * NB, n1 = std::min(n, n0 + NB);
-        for (uint32_t j = n0; j < n1; ++j) {
-            const int8_t* bj = b + static_cast<size_t>(j) * k;
-            for (uint32_t i = m0; i < m1; ++i) {
-                acc[static_cast<size_t>(i) * n + j] =
-                    dot_i8(a + static_cast<size_t>(i) * k, bj, k);
+        uint32_t j = n0;
+        for (; j + 4 <= n1; j += 4) {
+            const int8_t* bj[4];
+            for (int c = 0; c < 4; ++c) bj[c] = b + static_cast<size_t>(j + c) * k;
+            uint32_t i = m0;
+            for (; i + 2 <= m1; i += 2) {
+                int32_t o[2][4];
+                dot_i8_2x4(a + static_cast<size_t>(i) * k, a + static_cast<size_t>(i + 1) * k, bj, k, o);
+                for (int r = 0; r < 2; ++r)
+                    for (int c = 0; c < 4; ++c) acc[static_cast<size_t>(i + r) * n + j + c] = o[r][c];
             }
+            for (; i < m1; ++i)
+                for (int c = 0; c < 4; ++c)
+                    acc[static_cast<size_t>(i) * n + j + c] = dot_i8(a + static_cast<size_t>(i) * k, bj[c], k);
+        }
+        for (; j < n1; ++j) {
+            const int8_t* bj = b + static_cast<size_t>(j) * k;
+            for (uint32_t i = m0; i < m1; ++i)
+                acc[static_cast<size_t>(i) * n + j] = dot_i8(a + static_cast<size_t>(i) * k, bj, k);
         }
     }
 }

@@ -3,10 +3,12 @@ pytest): a producer process allocates the BGRA input and the depth output
 with hipMalloc, records an interprocess event and passes the IPC handles to
 this process, which submits through them (input = output = NULL) and
 releases the job; the producer then reads the output back. The result must
-equal the oracle's pipeline bit for bit. Where the runtime refuses to record
-an interprocess event (hipEventRecord returned hipErrorInvalidValue on the
-MI355X pool this was run on), the producer synchronises its uploads before
-publishing the memory handles and the submission runs without a wait event.
+equal the oracle's pipeline bit for bit. The producer synchronises its
+uploads before publishing the memory handles; a submission that asks to wait
+on an interprocess event (DAV2_HIP_SUBMIT_WAIT_EVENT_IPC) must be refused
+with DAV2_STATUS_UNSUPPORTED (the runtime refused hipEventRecord of an
+interprocess event on the MI355X it was tried on, so that form is not
+offered).
 
 The producer is started before this process makes any HIP call, so no
 process that has initialised the GPU starts another program.
@@ -29,29 +31,18 @@ W, H, STRIDE, INPUT_SIZE, SEED = 180, 120, 184, 112, 0xDA20000
 def producer(out_path: str) -> int:
     hip = C.CDLL("libamdhip64.so")
     words = np.random.default_rng(SEED).integers(0, 2**32, size=H * STRIDE, dtype=np.uint32)
-    pin, pout, ev = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    pin, pout = C.c_void_p(), C.c_void_p()
     out_bytes = 4 * W * H
     assert hip.hipMalloc(C.byref(pin), C.c_size_t(words.nbytes)) == 0
     assert hip.hipMalloc(C.byref(pout), C.c_size_t(out_bytes)) == 0
     assert hip.hipMemcpy(pin, C.c_void_p(words.ctypes.data), C.c_size_t(words.nbytes), 1) == 0
     assert hip.hipMemset(pout, 0, C.c_size_t(out_bytes)) == 0
-    h_in, h_out, h_ev = (C.c_uint8 * 64)(), (C.c_uint8 * 64)(), (C.c_uint8 * 64)()
+    h_in, h_out = (C.c_uint8 * 64)(), (C.c_uint8 * 64)()
     assert hip.hipIpcGetMemHandle(h_in, pin) == 0
     assert hip.hipIpcGetMemHandle(h_out, pout) == 0
-    # An interprocess event the consumer waits on, recorded on a stream of
-    # this process after the uploads; without event IPC the uploads are
-    # complete (synchronised) before the handles are published.
-    use_event = hip.hipEventCreateWithFlags(C.byref(ev), 0x2 | 0x4) == 0  # disable timing | interprocess
-    strm = C.c_void_p()
-    if use_event:
-        rc_s = hip.hipStreamCreate(C.byref(strm))
-        rc_r = hip.hipEventRecord(ev, strm) if rc_s == 0 else -1
-        rc_h = hip.hipIpcGetEventHandle(h_ev, ev) if rc_r == 0 else -1
-        use_event = rc_s == 0 and rc_r == 0 and rc_h == 0
-        print(f"producer: event ipc stream={rc_s} record={rc_r} handle={rc_h}", file=sys.stderr, flush=True)
+    # The uploads are complete (synchronised) before the handles are published.
     assert hip.hipDeviceSynchronize() == 0
-    print(json.dumps({"in": bytes(h_in).hex(), "out": bytes(h_out).hex(), "ev": bytes(h_ev).hex() if use_event else "",
-                      "bytes": words.nbytes}), flush=True)
+    print(json.dumps({"in": bytes(h_in).hex(), "out": bytes(h_out).hex(), "bytes": words.nbytes}), flush=True)
     line = sys.stdin.readline()  # the consumer has released its job (or gave up)
     rc = 1
     if line.strip() == "done":
@@ -60,10 +51,6 @@ def producer(out_path: str) -> int:
         np.save(out_path, host)
         rc = 0
     print("saved" if rc == 0 else "skipped", flush=True)
-    if ev:
-        hip.hipEventDestroy(ev)
-    if strm:
-        hip.hipStreamDestroy(strm)
     hip.hipFree(pin)
     hip.hipFree(pout)
     return rc
@@ -91,13 +78,17 @@ def consumer() -> int:
             r.struct_size, r.abi_version = C.sizeof(r), pkg.DAV2_ABI_VERSION
             r.width, r.height, r.row_stride_bytes, r.pixel_format = W, H, 4 * STRIDE, pkg.GPU_PIXEL_BGRA8
             r.input_size = INPUT_SIZE
-            r.flags = pkg.HIP_SUBMIT_WAIT_EVENT_IPC if handles["ev"] else 0
-            print("wait event over IPC:", bool(handles["ev"]), flush=True)
             r.input_byte_size, r.output_byte_size = handles["bytes"], 4 * W * H
-            for field, key in (("input_ipc", "in"), ("output_ipc", "out"), ("wait_event_ipc", "ev")):
-                if handles[key]:
-                    C.memmove(getattr(r, field), bytes.fromhex(handles[key]), 64)
+            for field, key in (("input_ipc", "in"), ("output_ipc", "out")):
+                C.memmove(getattr(r, field), bytes.fromhex(handles[key]), 64)
             job = C.c_void_p()
+            # A wait on another process's event is refused before anything runs.
+            r.flags = pkg.HIP_SUBMIT_WAIT_EVENT_IPC
+            st = lib.dav2_submit_hip(ctx.handle, C.byref(r), C.byref(job))
+            print("interprocess wait event status", st, (lib.dav2_last_error() or b"").decode(), flush=True)
+            if st != 8 or job.value is not None:  # DAV2_STATUS_UNSUPPORTED
+                return 1
+            r.flags = 0
             st = lib.dav2_submit_hip(ctx.handle, C.byref(r), C.byref(job))
             print("submit status", st, (lib.dav2_last_error() or b"").decode(), flush=True)
             if st != 0:

@@ -454,12 +454,13 @@ class Oracle:
 
     ATTENTION_MODES = {"fp32": 0, "binary16": 1, "exact": 2}
 
-    def infer(self, h, chw, width: int, height: int, fp16_attention: bool = True, dim: int | None = None,
-              attention: str | None = None):
-        """The int8 graph. attention: "exact" (the int8-mode default, also
-        fp16_attention=True), "binary16" (the reference's binary16 pipeline)
-        or "fp32" (FORCE_FP32_ATTENTION, also fp16_attention=False)."""
-        mode = self.ATTENTION_MODES[attention or ("exact" if fp16_attention else "fp32")]
+    def infer(self, h, chw, width: int, height: int, attention: str = "exact", dim: int | None = None):
+        """The int8 graph. attention: "exact" (this build's integer-exact
+        attention, the int8-mode default of the GPU path; not the reference's
+        arithmetic), "binary16" (the reference's int8-mode attention
+        arithmetic: bmm_score_fp16 / softmax_lastdim_half / bmm_value_fp16) or
+        "fp32" (FORCE_FP32_ATTENTION: bmm.glsl / softmax_lastdim.glsl)."""
+        mode = self.ATTENTION_MODES[attention]
         chw = _f32(chw)
         depth = np.empty((height, width), np.float32)
         logits = np.empty((height, width), np.float32)

@@ -95,7 +95,7 @@ def vits_model(pkg, tmp_path_factory):
 def _oracle_depth(oracle, model, chw, width, height):
     h = oracle.load_model(model, 0)
     try:
-        depth, _, _ = oracle.infer(h, chw, width, height, fp16_attention=True)
+        depth, _, _ = oracle.infer(h, chw, width, height, attention="exact")
     finally:
         oracle.free_model(h)
     return depth

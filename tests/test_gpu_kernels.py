@@ -677,9 +677,10 @@ def _attention_mfma_gpu(torch, lib, qkv, tokens, heads):
     return host(torch, out), probs
 
 
-def _attention_ref_gpu(torch, lib, qkv, tokens, heads, fp16, batch=1):
+def _attention_ref_gpu(torch, lib, qkv, tokens, heads, fp16, batch=1, unpacked=True):
     """The reference-order kernels; returns the output, the probabilities
-    ([batch*H][T][T] as float32) and the scores before the softmax."""
+    ([batch*H][T][T] as float32) and the scores before the softmax (None,
+    None without `unpacked`)."""
     qd = dev(torch, qkv)
     nbytes = lib.dav2_hip_attention_ref_scratch_bytes(tokens, heads, batch, int(fp16))
     words = (tokens + 1) // 2
@@ -695,13 +696,16 @@ def _attention_ref_gpu(torch, lib, qkv, tokens, heads, fp16, batch=1):
             return w[:, :, :tokens].astype(np.float32), w[:, :, tokens:]
         return host(torch, buf.view(torch.float32)).reshape(batch * heads, tokens, tokens), None
 
-    scores, pad = unpack()
-    if fp16 and tokens % 2:
-        assert np.all(pad == 0)  # the high half of a row's last word is 0
+    scores = probs = None
+    if unpacked:
+        scores, pad = unpack()
+        if fp16 and tokens % 2:
+            assert np.all(pad == 0)  # the high half of a row's last word is 0
     ok(lib, lib.dav2_hip_attention_ref_softmax(ptr(buf), batch * heads * tokens, tokens, int(fp16), s))
-    probs, pad = unpack()
-    if fp16 and tokens % 2:
-        assert np.all(pad == 0)
+    if unpacked:
+        probs, pad = unpack()
+        if fp16 and tokens % 2:
+            assert np.all(pad == 0)
     ok(lib, lib.dav2_hip_attention_ref_values(ptr(out), ptr(buf), ptr(qd), tokens, heads, batch, int(fp16), s))
     return host(torch, out), probs, scores
 
@@ -742,6 +746,63 @@ def test_attention_ref_fp16_bit_exact(gpu, lib, oracle, tokens, heads, batch):
         ref, p_ref = oracle.attention(qkv[rows], tokens, heads, fp16=True, probabilities=True)
         assert np.array_equal(p[hs].view(np.uint32), p_ref.view(np.uint32))
         assert np.array_equal(out[rows].view(np.uint32), ref.view(np.uint32))
+
+
+def _attention_ref16_fused_gpu(torch, lib, qkv, tokens, heads, batch=1):
+    qd = dev(torch, qkv)
+    nbytes = lib.dav2_hip_attention_ref16_fused_scratch_bytes(tokens, heads, batch)
+    assert nbytes == 2 * batch * heads * ((tokens + 63) // 64) * 8192
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    out = empty(torch, (batch * tokens, heads * 64), torch.float32)
+    out.fill_(float("nan"))
+    ok(lib, lib.dav2_hip_attention_ref16_fused(ptr(out), ptr(qd), tokens, heads, batch, ptr(buf), nbytes,
+                                               stream(torch)))
+    # one byte short of the binary16 keys and values is rejected before any launch
+    assert lib.dav2_hip_attention_ref16_fused(ptr(out), ptr(qd), tokens, heads, batch, ptr(buf), nbytes - 1,
+                                              stream(torch)) == 1
+    return host(torch, out)
+
+
+@pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (2, 1, 1), (5, 2, 1), (63, 1, 1), (64, 2, 1), (65, 3, 1),
+                                                (77, 4, 2), (129, 2, 1), (1369, 3, 1), (1370, 16, 1), (1984, 2, 1),
+                                                (1985, 2, 1), (3101, 1, 1), (6200, 1, 1)])
+def test_attention_ref16_fused_bit_exact(gpu, lib, oracle, tokens, heads, batch):
+    # The fused binary16 kernel (16 query rows per workgroup up to T = 1984,
+    # 8 beyond) against the oracle's mode 1 (bmm_score_fp16 +
+    # softmax_lastdim_half + bmm_value_fp16), bit for bit
+    torch = gpu
+    _announce("attention ref16 fused", tokens, heads, batch)
+    rng = np.random.default_rng(tokens * 5 + heads + batch)
+    qkv = (rng.standard_normal((batch * tokens, 3 * heads * 64)) * 1.5).astype(np.float32)
+    out = _attention_ref16_fused_gpu(torch, lib, qkv, tokens, heads, batch)
+    for b in range(batch):
+        rows = slice(b * tokens, (b + 1) * tokens)
+        ref = oracle.attention(qkv[rows], tokens, heads, fp16=True)
+        assert np.array_equal(out[rows].view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("tokens,heads,batch,sigma", [(1370, 16, 2, 0.64), (5477, 16, 1, 0.64), (5477, 4, 1, 3.0),
+                                                      (9152, 1, 1, 1.0)])
+def test_attention_ref16_fused_matches_three_kernels(gpu, lib, tokens, heads, batch, sigma):
+    # Long sequences (the 1036x1036 token count, the fused kernel's longest)
+    # against the three materialised kernels, themselves bit-exact with the
+    # oracle's mode 1 up to 6200 tokens: the same bits
+    torch = gpu
+    _announce("attention ref16 fused vs three kernels", tokens, heads, batch, sigma)
+    rng = np.random.default_rng(tokens + heads + int(10 * sigma))
+    qkv = (rng.standard_normal((batch * tokens, 3 * heads * 64)) * sigma).astype(np.float32)
+    out = _attention_ref16_fused_gpu(torch, lib, qkv, tokens, heads, batch)
+    ref, _, _ = _attention_ref_gpu(torch, lib, qkv, tokens, heads, True, batch, unpacked=False)
+    assert np.isfinite(out).all()
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_attention_ref16_fused_limits(gpu, lib):
+    # beyond the fused kernel's LDS (about 9000 tokens) it reports no scratch
+    # size and refuses to run; the three kernels serve those lengths
+    assert lib.dav2_hip_attention_ref16_fused_scratch_bytes(9152, 1, 1) > 0
+    assert lib.dav2_hip_attention_ref16_fused_scratch_bytes(9153, 1, 1) == 0
+    assert lib.dav2_hip_attention_ref16_fused(None, None, 9153, 1, 1, None, 0, None) == 1
 
 
 def test_attention_ref_hand_vectors(gpu, lib):
@@ -893,6 +954,57 @@ def test_attention_fused_peaked_and_zero_rows(gpu, lib, oracle, colmax):
     assert np.isfinite(out).all()
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
     assert np.all(out[:, 5] == 0.0)
+
+
+def _attention_f64_gpu(torch, qkv, tokens, heads):
+    # float64 attention on the device (head by head), the exact reference
+    q = torch.from_numpy(qkv).to("cuda", torch.float64)
+    d = heads * 64
+    out = torch.empty((tokens, d), dtype=torch.float64, device="cuda")
+    for h in range(heads):
+        qh = q[:, h * 64:(h + 1) * 64] * 0.125
+        kh = q[:, d + h * 64:d + (h + 1) * 64].contiguous()
+        vh = q[:, 2 * d + h * 64:2 * d + (h + 1) * 64].contiguous()
+        p = torch.softmax(qh @ kh.T.contiguous(), dim=-1)
+        out[:, h * 64:(h + 1) * 64] = p @ vh
+    return host(torch, out)
+
+
+@pytest.mark.parametrize("tokens,heads,sigma", [(1370, 16, 0.64), (1370, 16, 2.0), (5477, 16, 0.64)])
+def test_attention_fused_against_reference_arithmetic(gpu, lib, tokens, heads, sigma):
+    # The int8 mode's default attention (integer-exact, this build's own
+    # arithmetic) against the reference's int8-mode arithmetic
+    # (bmm_score_fp16.glsl / softmax_lastdim_half.glsl / bmm_value_fp16.glsl:
+    # the binary16 kernels, bit-exact with the oracle's mode 1 in
+    # test_attention_ref_fp16_bit_exact) and float64 attention, on the same
+    # qkv at ViT-L width (16 heads) for 518x518 (T = 1370) and 1036x1036
+    # (T = 5477). sigma 0.64 is the spread of a random-init ViT-L's qkv; 2.0
+    # gives peaked rows. Asserted:
+    #   max|fused - f64| <= max|binary16 - f64| (the default is no less
+    #     accurate than the reference's arithmetic), and so is the per-row
+    #     maximum on at least 98% of the (token, head) rows;
+    #   max|fused - binary16| <= 1.25 max|binary16 - f64|: the default departs
+    #     from the reference's arithmetic by no more than that arithmetic
+    #     departs from exact attention.
+    torch = gpu
+    _announce("attention fused vs binary16 vs f64", tokens, heads, sigma)
+    rng = np.random.default_rng(tokens + int(sigma * 100))
+    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * sigma).astype(np.float32)
+    fused = _attention_fused_gpu(torch, lib, qkv, tokens, heads, 1).astype(np.float64)
+    ref16, _, _ = _attention_ref_gpu(torch, lib, qkv, tokens, heads, True, unpacked=False)
+    ref16 = ref16.astype(np.float64)
+    exact = _attention_f64_gpu(torch, qkv, tokens, heads)
+    e_fused, e_ref = np.abs(fused - exact), np.abs(ref16 - exact)
+    rows_fused = e_fused.reshape(tokens, heads, 64).max(-1)
+    rows_ref = e_ref.reshape(tokens, heads, 64).max(-1)
+    gap = np.abs(fused - ref16).max()
+    share = float((rows_fused <= rows_ref).mean())
+    print(f"attention T={tokens} H={heads} sigma={sigma}: max|fused-f64| {e_fused.max():.3g}, "
+          f"max|binary16-f64| {e_ref.max():.3g}, max|fused-binary16| {gap:.3g}, "
+          f"rows with fused <= binary16 error {share:.4f}", flush=True)
+    assert e_fused.max() <= e_ref.max()
+    assert share >= 0.98
+    assert gap <= 1.25 * e_ref.max()
 
 
 def test_softmax_fp32_buffer_off_8_bytes(gpu, lib, oracle):

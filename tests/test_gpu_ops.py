@@ -48,11 +48,40 @@ def test_linear_int8(gpu, pkg, lib, oracle, ops, rows, ic, oc, gelu):
     xd, bd = dev(torch, x), dev(torch, b)
     out = empty(torch, (rows, oc), torch.float32)
     run(lib, lib.dav2_ops_linear_int8(ops, db(pkg, out), db(pkg, xd), db(pkg, wd), db(pkg, sd), db(pkg, bd), rows, ic,
-                                      oc, int(gelu)))
+                                      oc, int(gelu), 0))
     sync(lib, ops)
     ref = oracle.linear_int8(x, q, s, b, gelu=gelu)
     got = host(torch, out)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,ic,oc,gelu", [(1370, 1024, 3072, False), (1370, 1024, 4096, True),
+                                             (300, 4096, 1024, False), (130, 588, 100, True), (3, 36, 5, False)])
+def test_linear_int8_weight_transposed(gpu, pkg, lib, oracle, ops, rows, ic, oc, gelu):
+    # linear_int8(..., weight_transposed=true) with the reference's
+    # int8_transposed_buffer ([K][N] bytes, gpu_model.cpp:241-258): the same
+    # bits as the oracle's linear on the [N][K] weight.
+    torch = gpu
+    print("case: linear_int8 transposed", rows, ic, oc, gelu, flush=True)
+    rng = np.random.default_rng(rows * 7 + ic + oc)
+    x = rng.standard_normal((rows, ic)).astype(np.float32)
+    w = (rng.standard_normal((oc, ic)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(oc) * 0.01).astype(np.float32)
+    q, s = oracle.quantize_weight_rows(w)
+    qt = dev(torch, np.ascontiguousarray(q.T))  # [K][N] bytes
+    xd, bd, sd = dev(torch, x), dev(torch, b), dev(torch, s)
+    out = empty(torch, (rows, oc), torch.float32)
+    out.fill_(float("nan"))
+    torch.cuda.current_stream().synchronize()
+    run(lib, lib.dav2_ops_linear_int8(ops, db(pkg, out), db(pkg, xd), db(pkg, qt), db(pkg, sd), db(pkg, bd), rows, ic,
+                                      oc, int(gelu), 1))
+    sync(lib, ops)
+    ref = oracle.linear_int8(x, q, s, b, gelu=gelu)
+    assert np.array_equal(host(torch, out).view(np.uint32), ref.view(np.uint32))
+    # a transposed buffer one byte short is rejected
+    run_rc = lib.dav2_ops_linear_int8(ops, db(pkg, out), db(pkg, xd), db(pkg, qt, ic * oc - 1), db(pkg, sd),
+                                      db(pkg, bd), rows, ic, oc, int(gelu), 1)
+    assert run_rc == 1 and b"transposed INT8 weight" in lib.dav2_ops_last_error()
 
 
 def test_linear_int8_validation(gpu, pkg, lib, ops):
@@ -62,13 +91,15 @@ def test_linear_int8_validation(gpu, pkg, lib, ops):
     s = empty(torch, (8,), torch.float32)
     out = empty(torch, (4, 8), torch.float32)
     # K not a multiple of 4 (operators.cpp:785-788)
-    assert lib.dav2_ops_linear_int8(ops, db(pkg, out), db(pkg, x), db(pkg, w), db(pkg, s), db(pkg, s), 4, 62, 8, 0) == 1
+    assert lib.dav2_ops_linear_int8(ops, db(pkg, out), db(pkg, x), db(pkg, w), db(pkg, s), db(pkg, s), 4, 62, 8, 0,
+                                    0) == 1
     # output buffer too small (require_bytes)
     assert lib.dav2_ops_linear_int8(ops, db(pkg, out, 64), db(pkg, x), db(pkg, w), db(pkg, s), db(pkg, s), 4, 64, 8,
-                                    0) == 1
+                                    0, 0) == 1
     assert b"too small" in lib.dav2_ops_last_error()
     # zero rows
-    assert lib.dav2_ops_linear_int8(ops, db(pkg, out), db(pkg, x), db(pkg, w), db(pkg, s), db(pkg, s), 0, 64, 8, 0) == 1
+    assert lib.dav2_ops_linear_int8(ops, db(pkg, out), db(pkg, x), db(pkg, w), db(pkg, s), db(pkg, s), 0, 64, 8, 0,
+                                    0) == 1
 
 
 def test_conv2d_int8_reference_kat(gpu, pkg, lib, oracle, ops):

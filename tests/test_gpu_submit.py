@@ -67,7 +67,7 @@ def oracle_submit(oracle, model, words, width, height, stride, input_size, rgba)
     chw = oracle.preprocess_rgba8(words, width, height, stride, nw, nh, rgba)
     h = oracle.load_model(model, 0)
     try:
-        depth, _, _ = oracle.infer(h, chw, nw, nh, fp16_attention=True)
+        depth, _, _ = oracle.infer(h, chw, nw, nh, attention="exact")
     finally:
         oracle.free_model(h)
     norm = oracle.normalize_relative(depth, oracle.reduce_minmax(depth))

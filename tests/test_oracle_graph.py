@@ -161,7 +161,7 @@ def graph_case(pkg, oracle, tmp_path_factory):
     image = pkg.dav2_format.imagenet_input(width, height, SEED + 5)[0]
     h = oracle.load_model(Path(path), ENC[enc])
     try:
-        depth, logits, feats = oracle.infer(h, image, width, height, fp16_attention=True, dim=384)
+        depth, logits, feats = oracle.infer(h, image, width, height, attention="exact", dim=384)
     finally:
         oracle.free_model(h)
     return st, enc, image, width, height, feats, logits
