@@ -475,12 +475,24 @@ __global__ __launch_bounds__(256) void ref_values_kernel(float* __restrict__ out
 // sum += float(a16 * b16) at 1.5 VALU instructions per product.
 constexpr uint32_t kChunkWords = 32u * 64u;  // one 64-token chunk of keys or values
 
-// acc = (acc + float(lo(prod))) + float(hi(prod)), two IEEE fp32 additions.
-DAV2_DEV void add_product_pair(float& acc, uint32_t prod, float one) {
-    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,0,0]\n\t"
-        "v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-        : "+v"(acc)
-        : "v"(prod), "v"(one));
+// acc = acc + float(lo(prod)), one IEEE fp32 addition (the binary16 half
+// widened exactly, times 1.0, plus acc: v_fma_mix_f32 rounds once).
+DAV2_DEV void add_product_lo(float& acc, uint32_t prod, float one) {
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(prod), "v"(one));
+}
+// acc = acc + float(hi(prod))
+DAV2_DEV void add_product_hi(float& acc, uint32_t prod, float one) {
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(prod), "v"(one));
+}
+
+// acc[n] = (acc[n] + float(lo(prod[n]))) + float(hi(prod[n])) for N sums;
+// the low halves of all N first, so that dependent additions are N apart.
+template <int N>
+DAV2_DEV void add_product_pairs(float (&acc)[N], const uint32_t (&prod)[N], float one) {
+#pragma unroll
+    for (int n = 0; n < N; ++n) add_product_lo(acc[n], prod[n], one);
+#pragma unroll
+    for (int n = 0; n < N; ++n) add_product_hi(acc[n], prod[n], one);
 }
 
 DAV2_DEV uint32_t mul_half2(uint32_t a, uint32_t b) {
@@ -520,9 +532,10 @@ __global__ __launch_bounds__(256) void ref16_pack_kernel(const float* __restrict
 
 // R query rows per workgroup of 256 threads; thread t owns row t % R and, of
 // each 64-token chunk, keys (for the scores) or features (for the values)
-// G*(t / R) .. +G-1, G = R / 4. LDS: the chunk double buffer (16 KB), then the
-// rows' binary16 scores / probabilities, `stride` words per row (4 more than
-// a multiple of 32, so the 16 rows' 16-byte reads fall on different banks).
+// G*(t / R) .. +G-1, G = R / 4. LDS: the chunk buffer (8 KB), then the rows'
+// binary16 scores / probabilities, `stride` words per row (4 more than a
+// multiple of 32, so the 16 rows' 16-byte reads fall on different banks).
+// At T = 1370 that is 53.5 KB: three workgroups per CU.
 template <int R>
 __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ out, const float* __restrict__ qkv,
                                                           const uint32_t* __restrict__ k16,
@@ -533,8 +546,8 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
     static_assert(G == 2 || G == 4, "two or four keys per thread");
     typedef uint32_t wordsG __attribute__((ext_vector_type(G)));
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-    uint32_t* const kv = lds;                     // [2][kChunkWords]
-    uint32_t* const srows = lds + 2 * kChunkWords;  // [R][stride]
+    uint32_t* const kv = lds;                 // [kChunkWords]
+    uint32_t* const srows = lds + kChunkWords;  // [R][stride]
 
     // XCD-banded order: workgroup L runs on XCD L % 8, and each XCD takes a
     // contiguous range of (head, row block) items, so a head's keys and
@@ -552,49 +565,64 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
     const uint32_t* vbase = v16 + static_cast<uint64_t>(bh) * chunks * kChunkWords;
     const float one = 1.0f;
 
-    // chunk c of src into buffer buf: 8 KB, two 1 KB blocks per wave
-    auto stage = [&](const uint32_t* src, uint32_t c, uint32_t buf) {
-        const uint32_t* s0 = src + static_cast<uint64_t>(c) * kChunkWords;
-#pragma unroll
-        for (uint32_t it = 0; it < 2; ++it) {
-            const uint32_t blk = wave * 2u + it;
-            copy16_to_lds(s0 + blk * 256u + lane * 4u, kv + buf * kChunkWords + blk * 256u);
+    // Chunks go through registers: chunk c + 1 is loaded (two 16-byte loads
+    // per thread) while chunk c is multiplied, and written to the buffer once
+    // every wave is done with chunk c. (Copies straight into LDS would make
+    // the compiler wait for them before every LDS read of the loop.)
+    uint4 staged0, staged1;
+    auto fetch = [t](const uint32_t* src, uint32_t c, uint4& a, uint4& b) {
+        const uint4* s0 = reinterpret_cast<const uint4*>(src + static_cast<uint64_t>(c) * kChunkWords);
+        a = s0[t];
+        b = s0[t + 256u];
+    };
+    auto put = [t, kv](const uint4& a, const uint4& b) {
+        uint4* d = reinterpret_cast<uint4*>(kv);
+        d[t] = a;
+        d[t + 256u] = b;
+    };
+    auto next_chunk = [&](uint32_t c) {
+        if (c + 1u < chunks) {
+            __syncthreads();  // every wave is done with chunk c
+            put(staged0, staged1);
+            __syncthreads();
         }
     };
 
-    stage(kbase, 0, 0);
-    // q row i as binary16 pairs of q * 0.125 (bmm_score_fp16.glsl:32)
+    fetch(kbase, 0, staged0, staged1);
+    // q row i as binary16 pairs of q * 0.125 (bmm_score_fp16.glsl:32); rows
+    // past T compute on zeros and are never stored
     uint32_t qp[32];
     {
-        const float* q = qkv + (static_cast<uint64_t>(b) * tokens + (i < tokens ? i : 0u)) * 3u * D + h * 64u;
+        const float* q = qkv + (static_cast<uint64_t>(b) * tokens + min(i, tokens - 1u)) * 3u * D + h * 64u;
+        float4 v[16];
+#pragma unroll
+        for (int f4 = 0; f4 < 16; ++f4) v[f4] = *reinterpret_cast<const float4*>(q + 4 * f4);
+        const float scale = i < tokens ? 0.125f : 0.0f;
 #pragma unroll
         for (int f4 = 0; f4 < 16; ++f4) {
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (i < tokens) v = *reinterpret_cast<const float4*>(q + 4 * f4);
-            qp[2 * f4] = pack_half2(v.x * 0.125f, v.y * 0.125f);
-            qp[2 * f4 + 1] = pack_half2(v.z * 0.125f, v.w * 0.125f);
+            qp[2 * f4] = pack_half2(v[f4].x * scale, v[f4].y * scale);
+            qp[2 * f4 + 1] = pack_half2(v[f4].z * scale, v[f4].w * scale);
         }
     }
+
+    put(staged0, staged1);
+    __syncthreads();
 
     // scores: s = sum over features 0..63 of float(q16 * k16), stored binary16
     uint32_t* const myrow = srows + r * stride;
     for (uint32_t c = 0; c < chunks; ++c) {
-        if (c + 1u < chunks) {
-            stage(kbase, c + 1u, (c + 1u) & 1u);
-            DAV2_WAIT_VMCNT(2);
-        } else {
-            DAV2_WAIT_VMCNT(0);
-        }
-        __syncthreads();
-        const uint32_t* kc = kv + (c & 1u) * kChunkWords + grp * G;
+        if (c + 1u < chunks) fetch(kbase, c + 1u, staged0, staged1);
+        const uint32_t* kc = kv + grp * G;
         float acc[G];
 #pragma unroll
         for (int kk = 0; kk < G; ++kk) acc[kk] = 0.0f;
 #pragma unroll
         for (int p = 0; p < 32; ++p) {
             const wordsG kw = *reinterpret_cast<const wordsG*>(kc + p * 64);
+            uint32_t prod[G];
 #pragma unroll
-            for (int kk = 0; kk < G; ++kk) add_product_pair(acc[kk], mul_half2(qp[p], kw[kk]), one);
+            for (int kk = 0; kk < G; ++kk) prod[kk] = mul_half2(qp[p], kw[kk]);
+            add_product_pairs(acc, prod, one);
         }
         // keys 64c + G*grp + kk -> words 32c + G*grp/2 + kk/2 (packHalf2x16)
         if (G == 4) {
@@ -603,11 +631,12 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
         } else {
             myrow[32u * c + grp] = pack_half2(acc[0], acc[1]);
         }
-        __syncthreads();
+        next_chunk(c);
     }
+    __syncthreads();  // every row's scores are in LDS; the chunk buffer is free
 
     // the first value chunk arrives during the softmax
-    stage(vbase, 0, 0);
+    fetch(vbase, 0, staged0, staged1);
 
     // softmax_lastdim_half.glsl:19-65 on each row: the maximum; e = exp(s -
     // max) stored binary16 while virtual lane L (words L, L + 128, ...; lane
@@ -648,15 +677,11 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
     float acc[G];
 #pragma unroll
     for (int f = 0; f < G; ++f) acc[f] = 0.0f;
+    put(staged0, staged1);
+    __syncthreads();  // every row's probabilities and the first value chunk are in LDS
     for (uint32_t c = 0; c < chunks; ++c) {
-        if (c + 1u < chunks) {
-            stage(vbase, c + 1u, (c + 1u) & 1u);
-            DAV2_WAIT_VMCNT(2);
-        } else {
-            DAV2_WAIT_VMCNT(0);
-        }
-        __syncthreads();  // (c = 0: also the end of every row's softmax)
-        const uint32_t* vc = kv + (c & 1u) * kChunkWords + grp * G;
+        if (c + 1u < chunks) fetch(vbase, c + 1u, staged0, staged1);
+        const uint32_t* vc = kv + grp * G;
         const uint32_t* pc = myrow + 32u * c;
         if (64u * c + 64u <= tokens) {
 #pragma unroll 2
@@ -666,8 +691,10 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
 #pragma unroll
                 for (int qq = 0; qq < 4; ++qq) {
                     const wordsG vw = *reinterpret_cast<const wordsG*>(vc + (q4 + qq) * 64);
+                    uint32_t prod[G];
 #pragma unroll
-                    for (int f = 0; f < G; ++f) add_product_pair(acc[f], mul_half2(pq[qq], vw[f]), one);
+                    for (int f = 0; f < G; ++f) prod[f] = mul_half2(pq[qq], vw[f]);
+                    add_product_pairs(acc, prod, one);
                 }
             }
         } else {
@@ -677,15 +704,17 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
                 const uint32_t pw = pc[q];
                 const wordsG vw = *reinterpret_cast<const wordsG*>(vc + q * 64u);
                 if (2u * q + 1u < left) {
+                    uint32_t prod[G];
 #pragma unroll
-                    for (int f = 0; f < G; ++f) add_product_pair(acc[f], mul_half2(pw, vw[f]), one);
+                    for (int f = 0; f < G; ++f) prod[f] = mul_half2(pw, vw[f]);
+                    add_product_pairs(acc, prod, one);
                 } else {
 #pragma unroll
                     for (int f = 0; f < G; ++f) acc[f] = acc[f] + half_lo(mul_half2(pw, vw[f]));
                 }
             }
         }
-        __syncthreads();
+        next_chunk(c);
     }
     if (i < tokens) {
         float* o = out + (static_cast<uint64_t>(b) * tokens + i) * D + h * 64u + grp * G;
@@ -698,20 +727,20 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
 
 uint32_t ref16_chunks(uint32_t tokens) { return (tokens + 63u) / 64u; }
 
-// Rows per workgroup and the LDS they need: 16 rows while two workgroups fit
-// a CU (T up to 1984), 8 rows up to the 160 KB of one workgroup.
+// The fused kernel runs 16 query rows per workgroup while at least two
+// workgroups fit a CU's 160 KB of LDS (T up to 2240; three at T = 1370).
+// Longer rows would leave one workgroup per CU, slower than the three
+// materialised kernels (measured at T = 5477), which serve them instead.
+constexpr int kRef16Rows = 16;
 struct Ref16Shape {
-    int rows;
-    uint32_t stride;
-    uint32_t lds;
+    uint32_t stride;  // words per score row
+    uint32_t lds;     // bytes, 0: T too long for the fused kernel
 };
 
 Ref16Shape ref16_shape(uint32_t tokens) {
     const uint32_t stride = ref16_chunks(tokens) * 32u + 4u;
-    const uint32_t kv_bytes = 2u * kChunkWords * 4u;
-    if (kv_bytes + 16u * stride * 4u <= 80u * 1024u) return {16, stride, kv_bytes + 16u * stride * 4u};
-    if (kv_bytes + 8u * stride * 4u <= 160u * 1024u) return {8, stride, kv_bytes + 8u * stride * 4u};
-    return {0, stride, 0};
+    const uint32_t lds = kChunkWords * 4u + kRef16Rows * stride * 4u;
+    return {stride, lds <= 80u * 1024u ? lds : 0u};
 }
 
 template <bool HALF>
@@ -776,7 +805,7 @@ int dav2_hip_attention_ref_softmax(void* scores, uint64_t rows, uint32_t columns
 }
 
 uint64_t dav2_hip_attention_ref16_fused_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch) {
-    if (ref16_shape(tokens).rows == 0) return 0;
+    if (ref16_shape(tokens).lds == 0) return 0;
     return 2ull * batch * heads * ref16_chunks(tokens) * kChunkWords * 4u;
 }
 
@@ -788,26 +817,21 @@ int dav2_hip_attention_ref16_fused(float* out, const float* qkv, uint32_t tokens
         return hipErrorInvalidValue;
     const Ref16Shape shape = ref16_shape(tokens);
     const uint64_t need = dav2_hip_attention_ref16_fused_scratch_bytes(tokens, heads, batch);
-    if (shape.rows == 0 || scratch_bytes < need) return hipErrorInvalidValue;
+    if (shape.lds == 0 || scratch_bytes < need) return hipErrorInvalidValue;
     const uint32_t chunks = ref16_chunks(tokens), bh = batch * heads;
-    const uint32_t row_blocks = (tokens + shape.rows - 1u) / shape.rows;
+    const uint32_t row_blocks = (tokens + kRef16Rows - 1u) / kRef16Rows;
     const uint64_t items = static_cast<uint64_t>(row_blocks) * bh;
     if (items > 0x7fffffffull) return hipErrorInvalidValue;
     uint32_t* k16 = static_cast<uint32_t*>(scratch);
     uint32_t* v16 = k16 + static_cast<uint64_t>(bh) * chunks * kChunkWords;
     hipStream_t s = static_cast<hipStream_t>(stream);
     dispatch(ref16_pack_kernel, dim3(chunks, bh), dim3(256), 0, s, qkv, k16, v16, tokens, heads, chunks);
-#define DAV2_REF16_CASE(R)                                                                                         \
-    {                                                                                                              \
-        static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(ref16_fused_kernel<R>), \
-                                                             hipFuncAttributeMaxDynamicSharedMemorySize,          \
-                                                             static_cast<int>(160u * 1024u));                     \
-        if (lds_ok != hipSuccess) return lds_ok;                                                                   \
-        dispatch(ref16_fused_kernel<R>, dim3(static_cast<uint32_t>(items)), dim3(256), shape.lds, s, out, qkv, k16, \
-                 v16, tokens, heads, chunks, row_blocks, shape.stride);                                            \
-    }
-    if (shape.rows == 16) DAV2_REF16_CASE(16) else DAV2_REF16_CASE(8)
-#undef DAV2_REF16_CASE
+    static const hipError_t lds_ok =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(ref16_fused_kernel<kRef16Rows>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(80u * 1024u));
+    if (lds_ok != hipSuccess) return lds_ok;
+    dispatch(ref16_fused_kernel<kRef16Rows>, dim3(static_cast<uint32_t>(items)), dim3(256), shape.lds, s, out, qkv, k16,
+             v16, tokens, heads, chunks, row_blocks, shape.stride);
     return hipGetLastError();
 }
 

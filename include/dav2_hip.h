@@ -322,10 +322,10 @@ DAV2_API int dav2_hip_attention_ref_values(float* out, const void* probabilities
 /* The binary16 pipeline above (bmm_score_fp16.glsl, softmax_lastdim_half.glsl,
  * bmm_value_fp16.glsl) fused per block of query rows, the same bits as the
  * three kernels: keys and values are rounded to binary16 once into the
- * scratch (dav2_hip_attention_ref16_fused_scratch_bytes() bytes, 0 when T is
- * beyond the fused kernel's LDS, above about 9000 tokens: then use the three
- * kernels), then each workgroup keeps its rows' binary16 scores in LDS
- * through the softmax and the value sums. No reference counterpart as one
+ * scratch (dav2_hip_attention_ref16_fused_scratch_bytes() bytes; 0 above
+ * 2240 tokens, where the three kernels are faster: use them), then each
+ * workgroup keeps its 16 rows' binary16 scores in LDS through the softmax
+ * and the value sums. No reference counterpart as one
  * kernel; reference: src/operators.cpp:1132-1167. */
 DAV2_API uint64_t dav2_hip_attention_ref16_fused_scratch_bytes(uint32_t tokens, uint32_t heads, uint32_t batch);
 DAV2_API int dav2_hip_attention_ref16_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads,

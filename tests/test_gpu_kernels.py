@@ -764,12 +764,12 @@ def _attention_ref16_fused_gpu(torch, lib, qkv, tokens, heads, batch=1):
 
 
 @pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (2, 1, 1), (5, 2, 1), (63, 1, 1), (64, 2, 1), (65, 3, 1),
-                                                (77, 4, 2), (129, 2, 1), (1369, 3, 1), (1370, 16, 1), (1984, 2, 1),
-                                                (1985, 2, 1), (3101, 1, 1), (6200, 1, 1)])
+                                                (77, 4, 2), (129, 2, 1), (1369, 3, 1), (1370, 16, 1), (1407, 2, 1),
+                                                (1409, 2, 1), (2240, 2, 1)])
 def test_attention_ref16_fused_bit_exact(gpu, lib, oracle, tokens, heads, batch):
-    # The fused binary16 kernel (16 query rows per workgroup up to T = 1984,
-    # 8 beyond) against the oracle's mode 1 (bmm_score_fp16 +
-    # softmax_lastdim_half + bmm_value_fp16), bit for bit
+    # The fused binary16 kernel (16 query rows per workgroup, T up to 2240)
+    # against the oracle's mode 1 (bmm_score_fp16 + softmax_lastdim_half +
+    # bmm_value_fp16), bit for bit
     torch = gpu
     _announce("attention ref16 fused", tokens, heads, batch)
     rng = np.random.default_rng(tokens * 5 + heads + batch)
@@ -781,12 +781,11 @@ def test_attention_ref16_fused_bit_exact(gpu, lib, oracle, tokens, heads, batch)
         assert np.array_equal(out[rows].view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("tokens,heads,batch,sigma", [(1370, 16, 2, 0.64), (5477, 16, 1, 0.64), (5477, 4, 1, 3.0),
-                                                      (9152, 1, 1, 1.0)])
+@pytest.mark.parametrize("tokens,heads,batch,sigma", [(1370, 16, 2, 0.64), (1370, 16, 8, 3.0), (2240, 16, 1, 1.0)])
 def test_attention_ref16_fused_matches_three_kernels(gpu, lib, tokens, heads, batch, sigma):
-    # Long sequences (the 1036x1036 token count, the fused kernel's longest)
-    # against the three materialised kernels, themselves bit-exact with the
-    # oracle's mode 1 up to 6200 tokens: the same bits
+    # Batches of ViT-L rows and the fused kernel's longest rows against the
+    # three materialised kernels, themselves bit-exact with the oracle's mode
+    # 1 up to 6200 tokens: the same bits
     torch = gpu
     _announce("attention ref16 fused vs three kernels", tokens, heads, batch, sigma)
     rng = np.random.default_rng(tokens + heads + int(10 * sigma))
@@ -798,11 +797,11 @@ def test_attention_ref16_fused_matches_three_kernels(gpu, lib, tokens, heads, ba
 
 
 def test_attention_ref16_fused_limits(gpu, lib):
-    # beyond the fused kernel's LDS (about 9000 tokens) it reports no scratch
-    # size and refuses to run; the three kernels serve those lengths
-    assert lib.dav2_hip_attention_ref16_fused_scratch_bytes(9152, 1, 1) > 0
-    assert lib.dav2_hip_attention_ref16_fused_scratch_bytes(9153, 1, 1) == 0
-    assert lib.dav2_hip_attention_ref16_fused(None, None, 9153, 1, 1, None, 0, None) == 1
+    # beyond 2240 tokens the fused kernel reports no scratch size and refuses
+    # to run; the three kernels serve those lengths
+    assert lib.dav2_hip_attention_ref16_fused_scratch_bytes(2240, 1, 1) > 0
+    assert lib.dav2_hip_attention_ref16_fused_scratch_bytes(2241, 1, 1) == 0
+    assert lib.dav2_hip_attention_ref16_fused(None, None, 2241, 1, 1, None, 0, None) == 1
 
 
 def test_attention_ref_hand_vectors(gpu, lib):
