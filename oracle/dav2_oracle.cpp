@@ -545,6 +545,26 @@ float numerator21(float x) {
     return std::nearbyint(v);
 }
 
+// numerator21 of eight values at once, the same operations: round to nearest
+// even (vroundps), fused multiply-adds (vfmadd), and ldexp(p, n) for n in
+// [-100, 0] as the product with 2^n, exact because p * 2^n stays a normal
+// float (p is near 2^21). Pinned against numerator21 in the oracle tests.
+inline __m256 numerator21_x8(__m256 x) {
+    constexpr float k21 = 2097152.0f;
+    const __m256 xc = _mm256_max_ps(x, _mm256_set1_ps(-100.0f));
+    const __m256 n = _mm256_round_ps(xc, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+    const __m256 f = _mm256_sub_ps(xc, n);
+    __m256 p = _mm256_set1_ps(1.327647245e-3f * k21);
+    p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(9.675540961e-3f * k21));
+    p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(5.550713092e-2f * k21));
+    p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(2.402212024e-1f * k21));
+    p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(6.931469440e-1f * k21));
+    p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(1.000000119e+0f * k21));
+    const __m256i e = _mm256_slli_epi32(_mm256_add_epi32(_mm256_cvtps_epi32(n), _mm256_set1_epi32(127)), 23);
+    const __m256 v = _mm256_min_ps(_mm256_mul_ps(p, _mm256_castsi256_ps(e)), _mm256_set1_ps(2097151.0f));
+    return _mm256_round_ps(v, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+}
+
 // Integer-exact attention (the int8-mode kernel): q*0.125 in 15-bit block
 // floating point per token row, k per head (one exponent over all tokens),
 // v per feature column over the tokens; X = 128 d1 + d0 (d1 in [-128, 127],
@@ -585,53 +605,105 @@ void attention_exact(const float* qkv, uint32_t tokens, uint32_t heads, float* o
             block_fixed15(qkv + 2 * D + h * 64 + f, T, D * 3, X.data(), &ve[f]);
             for (size_t t = 0; t < T; ++t) vd[t * 64 + f] = X[t];
         }
-        std::vector<float> u(T);
-        std::vector<double> E(T);
-        for (size_t i = 0; i < T; ++i) {
-            const double* qi = &qd[i * 64];
-            const double* qhi = &qh[i * 64];
-            float maximum = -std::numeric_limits<float>::infinity();
+        // Blocks of QB query rows: each key and value row is loaded once per
+        // block. Every sum below is an exact integer in double (products <
+        // 2^28, score sums < 2^34, value sums < 2^52), so the order of the
+        // additions does not change any result.
+        constexpr size_t QB = 4;
+        std::vector<float> u(QB * T);
+        std::vector<double> E(QB * T);
+        for (size_t i0 = 0; i0 < T; i0 += QB) {
+            const size_t nb = std::min(QB, T - i0);
+            float maximum[QB];
+            for (size_t b = 0; b < QB; ++b) maximum[b] = -std::numeric_limits<float>::infinity();
+            // rows past T repeat the last row (computed, never stored)
+            const double* qi[QB];
+            const double* qhi[QB];
+            for (size_t b = 0; b < QB; ++b) {
+                const size_t i = i0 + std::min(b, nb - 1);
+                qi[b] = &qd[i * 64];
+                qhi[b] = &qh[i * 64];
+            }
             for (size_t j = 0; j < T; ++j) {
-                // products < 2^28, sums < 2^34: every double operation is exact
                 const double* kj = &kd[j * 64];
                 const double* khj = &kh[j * 64];
-                __m256d acc = _mm256_setzero_pd(), acch = _mm256_setzero_pd();
+                __m256d acc[QB], acch[QB];
+                for (size_t b = 0; b < QB; ++b) acc[b] = acch[b] = _mm256_setzero_pd();
                 for (int f = 0; f < 64; f += 4) {
-                    acc = _mm256_fmadd_pd(_mm256_loadu_pd(qi + f), _mm256_loadu_pd(kj + f), acc);
-                    acch = _mm256_fmadd_pd(_mm256_loadu_pd(qhi + f), _mm256_loadu_pd(khj + f), acch);
+                    const __m256d kv = _mm256_loadu_pd(kj + f), khv = _mm256_loadu_pd(khj + f);
+                    for (size_t b = 0; b < QB; ++b) {
+                        acc[b] = _mm256_fmadd_pd(_mm256_loadu_pd(qi[b] + f), kv, acc[b]);
+                        acch[b] = _mm256_fmadd_pd(_mm256_loadu_pd(qhi[b] + f), khv, acch[b]);
+                    }
                 }
-                alignas(32) double lanes[4], lanesh[4];
-                _mm256_store_pd(lanes, acc);
-                _mm256_store_pd(lanesh, acch);
-                const double dot = (lanes[0] + lanes[1]) + (lanes[2] + lanes[3]);
-                const double hi = (lanesh[0] + lanesh[1]) + (lanesh[2] + lanesh[3]);
-                const int32_t rest = static_cast<int32_t>(dot - hi * 16384.0);
-                u[j] = std::fmaf(static_cast<float>(hi), 16384.0f, static_cast<float>(rest));
-                maximum = std::max(maximum, u[j]);
+                for (size_t b = 0; b < QB; ++b) {
+                    alignas(32) double lanes[4], lanesh[4];
+                    _mm256_store_pd(lanes, acc[b]);
+                    _mm256_store_pd(lanesh, acch[b]);
+                    const double dot = (lanes[0] + lanes[1]) + (lanes[2] + lanes[3]);
+                    const double hi = (lanesh[0] + lanesh[1]) + (lanesh[2] + lanesh[3]);
+                    const int32_t rest = static_cast<int32_t>(dot - hi * 16384.0);
+                    const float uj = std::fmaf(static_cast<float>(hi), 16384.0f, static_cast<float>(rest));
+                    u[b * T + j] = uj;
+                    maximum[b] = std::max(maximum[b], uj);
+                }
             }
-            const float row_scale = std::ldexp(1.44269504f, qe[i] + ke);
-            const float neg_ms = -(maximum * row_scale);
-            double L = 0.0;
-            for (size_t j = 0; j < T; ++j) {
-                E[j] = numerator21(std::fmaf(u[j], row_scale, neg_ms));
-                L += E[j];
+            double L[QB];
+            for (size_t b = 0; b < nb; ++b) {
+                const size_t i = i0 + b;
+                const float row_scale = std::ldexp(1.44269504f, qe[i] + ke);
+                const float neg_ms = -(maximum[b] * row_scale);
+                const float* ub = &u[b * T];
+                double* Eb = &E[b * T];
+                double Lb = 0.0;
+                size_t j8 = 0;
+                for (; j8 + 8 <= T; j8 += 8) {
+                    alignas(32) float e8[8];
+                    _mm256_store_ps(e8, numerator21_x8(_mm256_fmadd_ps(_mm256_loadu_ps(ub + j8),
+                                                                       _mm256_set1_ps(row_scale),
+                                                                       _mm256_set1_ps(neg_ms))));
+                    for (int l = 0; l < 8; ++l) {
+                        Eb[j8 + l] = e8[l];
+                        Lb += e8[l];
+                    }
+                }
+                for (size_t j = j8; j < T; ++j) {
+                    Eb[j] = numerator21(std::fmaf(ub[j], row_scale, neg_ms));
+                    Lb += Eb[j];
+                }
+                L[b] = Lb;
             }
-            // E < 2^21, |V| < 2^14, T < 2^17: sums stay below 2^52 (exact)
-            __m256d o[16];
-            for (int c = 0; c < 16; ++c) o[c] = _mm256_setzero_pd();
-            for (size_t j = 0; j < T; ++j) {
-                const __m256d e = _mm256_set1_pd(E[j]);
-                const double* vj = &vd[j * 64];
-                for (int c = 0; c < 16; ++c) o[c] = _mm256_fmadd_pd(e, _mm256_loadu_pd(vj + 4 * c), o[c]);
+            for (size_t b = nb; b < QB; ++b)
+                std::fill(E.begin() + static_cast<ptrdiff_t>(b * T), E.begin() + static_cast<ptrdiff_t>((b + 1) * T),
+                          0.0);
+            // values, eight features at a time for the block's rows
+            alignas(32) double ov[QB][64];
+            for (int f0 = 0; f0 < 64; f0 += 8) {
+                __m256d o[QB][2];
+                for (size_t b = 0; b < QB; ++b) o[b][0] = o[b][1] = _mm256_setzero_pd();
+                for (size_t j = 0; j < T; ++j) {
+                    const double* vj = &vd[j * 64 + f0];
+                    const __m256d v0 = _mm256_loadu_pd(vj), v1 = _mm256_loadu_pd(vj + 4);
+                    for (size_t b = 0; b < QB; ++b) {
+                        const __m256d e = _mm256_set1_pd(E[b * T + j]);
+                        o[b][0] = _mm256_fmadd_pd(e, v0, o[b][0]);
+                        o[b][1] = _mm256_fmadd_pd(e, v1, o[b][1]);
+                    }
+                }
+                for (size_t b = 0; b < QB; ++b) {
+                    _mm256_store_pd(&ov[b][f0], o[b][0]);
+                    _mm256_store_pd(&ov[b][f0 + 4], o[b][1]);
+                }
             }
-            alignas(32) double ov[64];
-            for (int c = 0; c < 16; ++c) _mm256_store_pd(ov + 4 * c, o[c]);
-            const float Lf = static_cast<float>(L);
-            float* dst = out + i * D + h * 64;
-            for (int f = 0; f < 64; ++f) dst[f] = std::ldexp(static_cast<float>(ov[f]) / Lf, ve[f]);
-            if (probabilities)
-                for (size_t j = 0; j < T; ++j)
-                    probabilities[(h * T + i) * T + j] = static_cast<float>(E[j]) / Lf;
+            for (size_t b = 0; b < nb; ++b) {
+                const size_t i = i0 + b;
+                const float Lf = static_cast<float>(L[b]);
+                float* dst = out + i * D + h * 64;
+                for (int f = 0; f < 64; ++f) dst[f] = std::ldexp(static_cast<float>(ov[b][f]) / Lf, ve[f]);
+                if (probabilities)
+                    for (size_t j = 0; j < T; ++j)
+                        probabilities[(h * T + i) * T + j] = static_cast<float>(E[b * T + j]) / Lf;
+            }
         }
     }
 }
@@ -640,6 +712,12 @@ void attention_exact(const float* qkv, uint32_t tokens, uint32_t heads, float* o
 
 void orc_numerator21(const float* x, uint64_t count, float* out) {
     for (uint64_t i = 0; i < count; ++i) out[i] = numerator21(x[i]);
+}
+
+void orc_numerator21_x8(const float* x, uint64_t count, float* out) {
+    uint64_t i = 0;
+    for (; i + 8 <= count; i += 8) _mm256_storeu_ps(out + i, numerator21_x8(_mm256_loadu_ps(x + i)));
+    for (; i < count; ++i) out[i] = numerator21(x[i]);
 }
 
 // Binary16 attention, the reference's int8-mode default (encoder.cpp:389-396

@@ -92,6 +92,8 @@ void orc_attention_scores_binary16(const float* qkv, uint32_t tokens, uint32_t h
 void orc_round_half_product(const float* a, const float* b, uint64_t count, float* out);
 /* The 21-bit softmax numerator of mode 2 for each x (as a float integer). */
 void orc_numerator21(const float* x, uint64_t count, float* out);
+// the same function eight values at a time (the form the attention uses)
+void orc_numerator21_x8(const float* x, uint64_t count, float* out);
 void orc_bilinear_align_true(const float* input, uint32_t input_width,
                              uint32_t input_height, uint32_t output_width,
                              uint32_t output_height, uint32_t channels,

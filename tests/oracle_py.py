@@ -24,6 +24,7 @@ _PROTO = {
     "orc_linear_int8": (None, [vp, vp, vp, vp, u32, u32, u32, C.c_int, vp]),
     "orc_gelu": (None, [vp, u64, vp]),
     "orc_numerator21": (None, [vp, u64, vp]),
+    "orc_numerator21_x8": (None, [vp, u64, vp]),
     "orc_exp": (None, [vp, u64, vp]),
     "orc_round_half_product": (None, [vp, vp, u64, vp]),
     "orc_attention_scores_binary16": (None, [vp, u32, u32, vp]),

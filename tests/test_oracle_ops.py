@@ -289,6 +289,22 @@ def test_numerator21_vs_float64(oracle):
     assert np.all(oracle.numerator21(np.array([0.0, 1e-6, 0.03], np.float32)) == 2097151.0)
 
 
+def test_numerator21_vector_form_matches_scalar(oracle):
+    # The eight-wide form the oracle's attention uses for speed gives the
+    # scalar numerator21's bits: dense and random arguments, half-integers
+    # (ties of the rounding to an integer exponent), the clamp at -100,
+    # -inf and NaN.
+    rng = np.random.default_rng(21)
+    x = np.concatenate([np.linspace(-101.0, 0.5, 2000003), rng.uniform(-110.0, 0.6, 2000000),
+                        np.arange(-100.5, 1.0, 0.5), np.nextafter(np.arange(-100.5, 1.0, 0.5), 0.0),
+                        np.nextafter(np.arange(-100.5, 1.0, 0.5), -1.0),
+                        [-np.inf, np.nan, -3e38, 0.0, -0.0, 1e-30]]).astype(np.float32)
+    scalar = oracle.numerator21(x)
+    vec = np.empty_like(x)
+    oracle.lib.orc_numerator21_x8(x.ctypes.data, x.size, vec.ctypes.data)
+    assert np.array_equal(vec.view(np.uint32), scalar.view(np.uint32))
+
+
 def test_attention_exact_mode_uniform_keys(oracle):
     # identical keys: every probability is 1/T, the output is the mean of the
     # (15-bit block floating point) values
