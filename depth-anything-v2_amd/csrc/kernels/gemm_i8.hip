@@ -471,11 +471,14 @@ void launch_cfg(const GemmParams& g, hipStream_t s, bool last = true) {
 // epilogues other than the column-maxima one.
 constexpr uint32_t kWideTileRows = 4096;
 
-// Rows of P per tile of the configuration launch_epi picks: 64 for the
-// 64x128 tiles of the large row-major GEMMs without column maxima
+// Columns of Q from which those GEMMs take 128x128 tiles on eight waves.
+constexpr uint32_t kWideTileCols = 3072;
+
+// Rows of P per tile of the configuration launch_epi picks: 128 / 64 for the
+// 128x128 / 64x128 tiles of the large row-major GEMMs without column maxima
 // (rows_p >= kWideTileRows), else 32, 96 or 64 as in the switch below.
 inline uint32_t tile_rows(uint32_t rows_p, uint32_t rows_q, bool row_major, bool col_max) {
-    if (row_major && !col_max && rows_p >= kWideTileRows) return 64;
+    if (row_major && !col_max && rows_p >= kWideTileRows) return rows_q >= kWideTileCols ? 128 : 64;
     if (rows_p <= 32) return 32;
     if (row_major && rows_q >= 2048 && rows_p >= 512) return 96;
     return 64;
@@ -492,11 +495,16 @@ void launch_epi(const GemmParams& g, hipStream_t s, bool last = true) {
     // From M = 4096 rows on (ViT-L 518 batch 8: M = 10960) 64x128 tiles
     // with a two-stage ring are fastest for the row-major GEMMs without
     // column maxima (proj / fc1 / fc2: 35 / 126 / 106 us with the tiles
-    // below, 29 / 97 / 73 us with these); the column-maxima epilogue needs
+    // below, 29 / 97 / 73 us with these), and from N = 3072 on 128x128 tiles
+    // on eight waves of 32x64 (qkv / fc1 at batch 8: 68 -> 64 / 125 -> 115
+    // us; fewer columns measured slower); the column-maxima epilogue needs
     // 64-column tiles.
     if constexpr (row_major_epi<EPI>() && EPI != DAV2_GEMM_EPI_ROW_COLMAX) {
         if (g.rows_p >= kWideTileRows) {
-            launch_cfg<64, 128, 2, 2, 128, 2, EPI>(g, s, last);
+            if (g.rows_q >= kWideTileCols)
+                launch_cfg<128, 128, 4, 2, 128, 2, EPI>(g, s, last);
+            else
+                launch_cfg<64, 128, 2, 2, 128, 2, EPI>(g, s, last);
             return;
         }
     }

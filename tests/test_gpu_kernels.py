@@ -429,12 +429,15 @@ def _random_gemm_case(rng, m, n, k):
     return a, b, sa, sb, bias
 
 
-# the last three take the 64x128 tiles of M >= 4096: ragged M, N not a multiple
-# of 128 (200) and not of 4 (1001, element stores), a partial K stage (192)
+# (4100, 200, 192) and (4097, 1001, 128) take the 64x128 tiles of M >= 4096:
+# ragged M, N not a multiple of 128 (200) and not of 4 (1001, element stores),
+# a partial K stage (192); (4100, 3100, 192), (4097, 3073, 128) and
+# (6000, 4096, 1024) the 128x128 eight-wave tiles of N >= 3072;
 # (1370, 1024, 4096) and (300, 96, 2112): long K (fc2), the second with a
 # partial last stage
 @pytest.mark.parametrize("m,n,k", [(1370, 384, 384), (1369, 96, 640), (300, 1024, 1024), (5477, 384, 384),
-                                   (4100, 200, 192), (4097, 1001, 128), (1370, 1024, 4096), (300, 96, 2112)])
+                                   (4100, 200, 192), (4097, 1001, 128), (4100, 3100, 192), (4097, 3073, 128),
+                                   (6000, 4096, 1024), (1370, 1024, 4096), (300, 96, 2112)])
 def test_gemm_row_epilogues(gpu, pkg, lib, oracle, m, n, k):
     torch = gpu
     _announce("gemm epilogues", m, n, k)
