@@ -432,6 +432,63 @@ __global__ __launch_bounds__(256) void conv1x1_narrow_kernel(const float* __rest
     }
 }
 
+// The same for a compile-time channel count on planes of an even number of
+// pixels: each thread takes two adjacent pixels (8-byte loads and stores),
+// the same arithmetic per pixel.
+template <int C>
+__global__ __launch_bounds__(256) void conv1x1_narrow_pairs_kernel(const float* __restrict__ x, uint64_t plane,
+                                                                   const int8_t* __restrict__ w, uint32_t ldw,
+                                                                   const float* __restrict__ w_scales,
+                                                                   const float* __restrict__ bias, uint32_t n,
+                                                                   float* __restrict__ out,
+                                                                   float* __restrict__ pre_relu, uint32_t flags) {
+    const uint64_t p = 2u * (static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x);
+    if (p >= plane) return;
+    const bool relu_in = (flags & DAV2_CONV_RELU_INPUT) != 0, relu_out = (flags & DAV2_CONV_RELU_OUTPUT) != 0;
+    float2 v[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) v[c] = *reinterpret_cast<const float2*>(x + c * plane + p);
+    float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        if (relu_in) {
+            v[c].x = fmaxf(v[c].x, 0.0f);
+            v[c].y = fmaxf(v[c].y, 0.0f);
+        }
+        m0 = fmaxf(m0, fabsf(v[c].x));
+        m1 = fmaxf(m1, fabsf(v[c].y));
+    }
+    const float s0 = row_scale(m0), inv0 = 1.0f / s0;
+    const float s1 = row_scale(m1), inv1 = 1.0f / s1;
+    int q0[C], q1[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        q0[c] = quantize_rne(v[c].x * inv0);
+        q1[c] = quantize_rne(v[c].y * inv1);
+    }
+    for (uint32_t o = 0; o < n; ++o) {
+        int32_t a0 = 0, a1 = 0;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int32_t wc = static_cast<int32_t>(w[static_cast<uint64_t>(o) * ldw + c]);
+            a0 += q0[c] * wc;
+            a1 += q1[c] * wc;
+        }
+        const float ws = w_scales[o], b = bias ? bias[o] : 0.0f;
+        float r0 = static_cast<float>(a0);
+        r0 = r0 * s0;
+        r0 = r0 * ws;
+        r0 = r0 + b;
+        float r1 = static_cast<float>(a1);
+        r1 = r1 * s1;
+        r1 = r1 * ws;
+        r1 = r1 + b;
+        if (pre_relu) *reinterpret_cast<float2*>(pre_relu + o * plane + p) = make_float2(r0, r1);
+        *reinterpret_cast<float2*>(out + o * plane + p) =
+            relu_out ? make_float2(fmaxf(r0, 0.0f), fmaxf(r1, 0.0f)) : make_float2(r0, r1);
+    }
+}
+
 // Packed convolution weights (conv_common.h): dst byte
 // ((nb * ksteps + ks) * 64 + l) * 16 + b holds weight row 16 nb + l % 16 at
 // tap-major K index k = 64 ks + 16 (l / 16) + b (k = tap * C + c), which is
@@ -564,9 +621,17 @@ int dav2_hip_conv1x1_narrow_i8(const float* input, uint32_t width, uint32_t heig
         out_channels > kNarrowN || ldw < channels ||
         (flags & ~static_cast<uint32_t>(DAV2_CONV_RELU_INPUT | DAV2_CONV_RELU_OUTPUT)))
         return hipErrorInvalidValue;
-    dispatch(conv1x1_narrow_kernel, dim3(ceil_div(plane, 256)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), input, plane, channels, weight, ldw, weight_scales, bias,
-                       out_channels, out, pre_relu, flags);
+    const bool pairs = channels == 32u && plane % 2u == 0u &&
+                       ((reinterpret_cast<uintptr_t>(input) | reinterpret_cast<uintptr_t>(out) |
+                         reinterpret_cast<uintptr_t>(pre_relu)) & 7u) == 0u;
+    if (pairs)
+        dispatch(conv1x1_narrow_pairs_kernel<32>, dim3(ceil_div(plane / 2u, 256)), dim3(256), 0,
+                 static_cast<hipStream_t>(stream), input, plane, weight, ldw, weight_scales, bias, out_channels, out,
+                 pre_relu, flags);
+    else
+        dispatch(conv1x1_narrow_kernel, dim3(ceil_div(plane, 256)), dim3(256), 0,
+                 static_cast<hipStream_t>(stream), input, plane, channels, weight, ldw, weight_scales, bias,
+                 out_channels, out, pre_relu, flags);
     return hipGetLastError();
 }
 

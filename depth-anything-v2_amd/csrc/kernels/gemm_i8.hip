@@ -477,8 +477,13 @@ constexpr uint32_t kWideTileCols = 3072;
 // Rows of P per tile of the configuration launch_epi picks: 128 / 64 for the
 // 128x128 / 64x128 tiles of the large row-major GEMMs without column maxima
 // (rows_p >= kWideTileRows), else 32, 96 or 64 as in the switch below.
+// Columns of Q from which the smaller row-major GEMMs without column maxima
+// (fc1 at batch 1) take 128x64 tiles on eight waves.
+constexpr uint32_t kTallTileCols = 4096;
+
 inline uint32_t tile_rows(uint32_t rows_p, uint32_t rows_q, bool row_major, bool col_max) {
     if (row_major && !col_max && rows_p >= kWideTileRows) return rows_q >= kWideTileCols ? 128 : 64;
+    if (row_major && !col_max && rows_q >= kTallTileCols && rows_p >= 512) return 128;
     if (rows_p <= 32) return 32;
     if (row_major && rows_q >= 2048 && rows_p >= 512) return 96;
     return 64;
@@ -499,12 +504,19 @@ void launch_epi(const GemmParams& g, hipStream_t s, bool last = true) {
     // on eight waves of 32x64 (qkv / fc1 at batch 8: 68 -> 64 / 125 -> 115
     // us; fewer columns measured slower); the column-maxima epilogue needs
     // 64-column tiles.
+    // Below that, from N = 4096 on (fc1 at batch 1), 128x64 tiles on eight
+    // waves of 32x32 (20.4 -> 18.3 us at M = 1370): twice the waves of the
+    // 96x64 tiles on the same CUs to hide the operand waits.
     if constexpr (row_major_epi<EPI>() && EPI != DAV2_GEMM_EPI_ROW_COLMAX) {
         if (g.rows_p >= kWideTileRows) {
             if (g.rows_q >= kWideTileCols)
                 launch_cfg<128, 128, 4, 2, 128, 2, EPI>(g, s, last);
             else
                 launch_cfg<64, 128, 2, 2, 128, 2, EPI>(g, s, last);
+            return;
+        }
+        if (g.rows_q >= kTallTileCols && g.rows_p >= 512) {
+            launch_cfg<128, 64, 4, 2, 128, 2, EPI>(g, s, last);
             return;
         }
     }

@@ -503,9 +503,10 @@ __global__ __launch_bounds__(256) void im2col1x1_kernel(const float* __restrict_
 // out may then be null. EXACT: columns == 64 * CH, a compile-time constant
 // (no partial column block, constant offsets, and for 1024 columns the
 // divisions by the width become exact multiplications). For CH > 0 the
-// quantized bytes go from registers straight to memory (lane l stores
-// columns l, l + 64, ...; a wave's 64 bytes form one segment); CH = 0
-// stages the normalised row in LDS.
+// quantized bytes go from registers to memory: with EXACT regrouped through
+// LDS so that lane l stores bytes 16 l .. 16 l + 15 (one store of the whole
+// row per wave), else lane l stores columns l, l + 64, ... (64-byte
+// segments); CH = 0 stages the normalised row in LDS.
 template <int CH, bool QUANT, bool EXACT>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
     const float* __restrict__ input, const float* __restrict__ weight,
@@ -514,6 +515,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
     float* __restrict__ scales) {
     static_assert(!EXACT || CH > 0, "EXACT needs the row in registers");
     extern __shared__ float lds_rows[];
+    __shared__ __attribute__((aligned(16))) int8_t qstage[EXACT && QUANT ? kRowsPerBlock : 1][EXACT ? 64 * CH : 16];
     const uint32_t columns = EXACT ? 64u * CH : width;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
@@ -587,10 +589,22 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void layer_norm_kernel(
                 for (int j = 0; j < kKept; ++j) qv[j] = quantize_div(v[j], sc, inv_sc);
             }
             int8_t* qr = q + static_cast<uint64_t>(row) * ldq;
+            if (EXACT && (reinterpret_cast<uintptr_t>(qr) & 15u) == 0) {
+                int8_t* st = qstage[EXACT && QUANT ? wave : 0];
 #pragma unroll
-            for (int j = 0; j < kKept; ++j) {
-                const uint32_t c = lane + 64u * j;
-                if (EXACT || c < columns) qr[c] = static_cast<int8_t>(qv[j]);
+                for (int j = 0; j < kKept; ++j) st[lane + 64u * j] = static_cast<int8_t>(qv[j]);
+                // this wave's bytes are in LDS before its lanes read them back
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (16u * lane < columns)
+                    *reinterpret_cast<uint4*>(qr + 16u * lane) = *reinterpret_cast<const uint4*>(st + 16u * lane);
+            } else {
+#pragma unroll
+                for (int j = 0; j < kKept; ++j) {
+                    const uint32_t c = lane + 64u * j;
+                    if (EXACT || c < columns) qr[c] = static_cast<int8_t>(qv[j]);
+                }
             }
             for (uint32_t c = columns + lane; c < ldq; c += 64u) qr[c] = 0;
         }

@@ -338,14 +338,18 @@ DAV2_API dav2_status DAV2_CALL dav2_infer_tensor_f32(
  * ------------------------------------------------------------------------ */
 
 /*
- * Create flag (int8 mode): run the attention with the reference's binary16
- * arithmetic -- bmm_score_fp16.glsl, softmax_lastdim_half.glsl and
- * bmm_value_fp16.glsl, every product rounded to binary16 and every sum in
- * the shaders' order (the reference's int8-mode default on devices without
+ * Create flag (int8 mode): run the attention in the reference shaders'
+ * binary16 arithmetic order -- bmm_score_fp16.glsl, softmax_lastdim_half.glsl
+ * and bmm_value_fp16.glsl, every product rounded to binary16 and every sum in
+ * the shaders' order (the reference's int8-mode attention on devices without
  * its cooperative-matrix score shader, src/encoder.cpp:389-396) -- instead of
- * this build's default integer-exact fused attention. Slower; for callers
- * that need the reference's int8-mode depth maps bit for bit. Not combinable
- * with FORCE_FP32 / FORCE_FP32_ATTENTION.
+ * this build's default integer-exact fused attention. The results equal the
+ * CPU oracle's restatement of those shaders bit for bit; that restatement
+ * uses this build's own exp (exp_cw) where the shaders call the Vulkan
+ * driver's exp, and devices with the cooperative-matrix score shader sum the
+ * scores in another order, so bit equality with a given Vulkan device is not
+ * established. Slower than the default (about half the images per second).
+ * Not combinable with FORCE_FP32 / FORCE_FP32_ATTENTION.
  */
 enum { DAV2_CREATE_REFERENCE_FP16_ATTENTION = 1u << 16u };
 

@@ -342,7 +342,10 @@ def test_bilinear_maxima(gpu, lib, c, ih, iw, oh, ow):
     assert np.array_equal(host(torch, maxima), _group_max(ref, relu=False))
 
 
-@pytest.mark.parametrize("c,h,w,n,flags", [(32, 518, 518, 1, 2), (32, 20, 33, 1, 0), (64, 7, 9, 3, 1), (12, 5, 5, 4, 3)])
+# 32 channels on an even plane take the two-pixel kernel (also with three
+# outputs and both ReLUs); odd planes and other channel counts the other
+@pytest.mark.parametrize("c,h,w,n,flags", [(32, 518, 518, 1, 2), (32, 20, 33, 1, 0), (32, 6, 10, 3, 3), (32, 7, 9, 4, 3),
+                                           (64, 7, 9, 3, 1), (12, 5, 5, 4, 3)])
 def test_conv1x1_narrow_matches_im2col_gemm(gpu, pkg, lib, oracle, c, h, w, n, flags):
     torch = gpu
     _announce("conv1x1 narrow", c, h, w, n, flags)
@@ -432,12 +435,15 @@ def _random_gemm_case(rng, m, n, k):
 # (4100, 200, 192) and (4097, 1001, 128) take the 64x128 tiles of M >= 4096:
 # ragged M, N not a multiple of 128 (200) and not of 4 (1001, element stores),
 # a partial K stage (192); (4100, 3100, 192), (4097, 3073, 128) and
-# (6000, 4096, 1024) the 128x128 eight-wave tiles of N >= 3072;
+# (6000, 4096, 1024) the 128x128 eight-wave tiles of N >= 3072; (1370, 4096,
+# 256) and (700, 4100, 192) the 128x64 eight-wave tiles of N >= 4096 below
+# M = 4096;
 # (1370, 1024, 4096) and (300, 96, 2112): long K (fc2), the second with a
 # partial last stage
 @pytest.mark.parametrize("m,n,k", [(1370, 384, 384), (1369, 96, 640), (300, 1024, 1024), (5477, 384, 384),
                                    (4100, 200, 192), (4097, 1001, 128), (4100, 3100, 192), (4097, 3073, 128),
-                                   (6000, 4096, 1024), (1370, 1024, 4096), (300, 96, 2112)])
+                                   (6000, 4096, 1024), (1370, 4096, 256), (700, 4100, 192), (1370, 1024, 4096),
+                                   (300, 96, 2112)])
 def test_gemm_row_epilogues(gpu, pkg, lib, oracle, m, n, k):
     torch = gpu
     _announce("gemm epilogues", m, n, k)
