@@ -883,7 +883,8 @@ def _attention_fused_gpu(torch, lib, qkv, tokens, heads, batch):
 
 
 @pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (5, 2, 1), (64, 3, 1), (77, 4, 2), (257, 6, 1),
-                                                (1370, 16, 1), (1370, 6, 3), (2000, 2, 1)])
+                                                (1370, 16, 1), (1370, 6, 3), (1500, 3, 2), (1536, 2, 1),
+                                                (1537, 2, 1), (2000, 2, 1)])
 def test_attention_fused(gpu, lib, oracle, tokens, heads, batch):
     # Integer-exact kernel vs the oracle's restatement: every sum is an exact
     # integer and every rounding the same IEEE operation, so bit for bit; and
