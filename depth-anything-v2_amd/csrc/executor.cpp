@@ -191,9 +191,9 @@ void HipExecutor::infer(const float* input, int width, int height, float* output
     const std::uint64_t out_elems = std::uint64_t(width) * height;
     DeviceBuffer& in = arena_.get("io.input", in_elems * sizeof(float));
     DeviceBuffer& out = arena_.get("io.output", out_elems * sizeof(float));
-    context_.upload(in, input, in_elems * sizeof(float));
+    context_.upload_staged(in, input, in_elems * sizeof(float));
     run_graph(in.as<float>(), 1, width, height, out.as<float>(), nullptr);
-    context_.download(out, output, out_elems * sizeof(float));
+    context_.download_staged(out, output, out_elems * sizeof(float));
 }
 
 void HipExecutor::infer_device(const float* input, int batch, int width, int height, float* output,
@@ -220,23 +220,19 @@ void HipExecutor::normalize_relative_device(float* depth, std::uint64_t count, h
 std::size_t HipExecutor::upload_image(const char* slot, const std::uint8_t* image, std::size_t row_bytes,
                                       int height, std::size_t stride, bool keep_stride, DeviceBuffer*& device) {
     // One host-to-device copy either way (a pitched copy from pageable memory
-    // goes row by row): the rows with their padding when it is small, else
-    // the rows packed on the host first.
+    // goes row by row), through the context's pinned input buffer: the rows
+    // with their padding when it is small, else the rows packed.
     const std::size_t rows = static_cast<std::size_t>(height);
     const std::size_t span = (rows - 1) * stride + row_bytes, packed = rows * row_bytes;
     if (keep_stride && span <= packed + packed / 4) {
         device = &arena_.get(slot, span);
-        context_.upload(*device, image, span);
+        context_.upload_staged(*device, image, span);
         return stride;
     }
-    image_stage_.resize(packed);
-    for (std::size_t r = 0; r < rows; ++r)
-        std::memcpy(image_stage_.data() + r * row_bytes, image + r * stride, row_bytes);
+    auto* stage = static_cast<std::uint8_t*>(context_.input_staging(packed));
+    for (std::size_t r = 0; r < rows; ++r) std::memcpy(stage + r * row_bytes, image + r * stride, row_bytes);
     device = &arena_.get(slot, packed);
-    context_.upload(*device, image_stage_.data(), packed);
-    // the copy reads the staging rows asynchronously: wait before they can
-    // be reused by the next call
-    context_.synchronize();
+    context_.upload_staged(*device, packed);
     return row_bytes;
 }
 
@@ -339,7 +335,7 @@ void HipExecutor::infer_bgr8(const std::uint8_t* bgr, int width, int height, std
               "preprocess_bgr8");
     run_graph(in.as<float>(), 1, network_width, network_height, depth.as<float>(), nullptr);
     if (network_width == width && network_height == height) {
-        context_.download(depth, output, pixels * sizeof(float));
+        context_.download_staged(depth, output, pixels * sizeof(float));
         return;
     }
     // vulkan_executor.cpp:586-598: bilinear (align corners) back to the image
@@ -347,7 +343,7 @@ void HipExecutor::infer_bgr8(const std::uint8_t* bgr, int width, int height, std
     operators_.bilinear_align_true(resized, depth, static_cast<std::uint32_t>(network_width),
                                    static_cast<std::uint32_t>(network_height), static_cast<std::uint32_t>(width),
                                    static_cast<std::uint32_t>(height), 1);
-    context_.download(resized, output, pixels * sizeof(float));
+    context_.download_staged(resized, output, pixels * sizeof(float));
 }
 
 void HipExecutor::infer_bgra8_normalized(const std::uint8_t* bgra, int width, int height, std::size_t stride,
@@ -377,7 +373,7 @@ void HipExecutor::infer_bgra8_normalized(const std::uint8_t* bgra, int width, in
     hip_check(dav2_hip_normalize_span(depth.as<float>(), range.as<float>(), net, normalized.as<float>(),
                                       context_.active_stream()),
               "normalize_span");
-    context_.download(normalized, output, net * sizeof(float));
+    context_.download_staged(normalized, output, net * sizeof(float));
 }
 
 }  // namespace dav2

@@ -128,7 +128,6 @@ private:
     GraphKey warm_key_;   // last eager run (buffers sized for it)
     GraphKey graph_key_;  // what graph_exec_ replays
     hipGraphExec_t graph_exec_ = nullptr;
-    std::vector<std::uint8_t> image_stage_;  // host rows of a strided image, packed before the upload
     DinoEncoder dino_;
     DptHead dpt_;
     Arena arena_;

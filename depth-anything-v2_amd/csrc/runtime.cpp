@@ -1,5 +1,8 @@
 #include "runtime.h"
 
+#include <algorithm>
+#include <cstring>
+
 #include "dav2_hip.h"
 
 #include <cstdio>
@@ -154,14 +157,75 @@ HipContext::HipContext(int device_index) : device_(device_index) {
     // Default priority, non-blocking with respect to the null stream.
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
     active_ = stream_;
+    hip_check(hipEventCreateWithFlags(&in_copied_, hipEventDisableTiming), "staging event");
 }
 
 HipContext::~HipContext() {
-    if (stream_) {
-        (void)hipSetDevice(device_);
-        (void)hipStreamSynchronize(stream_);
-        (void)hipStreamDestroy(stream_);
+    (void)hipSetDevice(device_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (in_copied_) {
+        (void)hipEventSynchronize(in_copied_);
+        (void)hipEventDestroy(in_copied_);
     }
+    if (in_stage_.data) (void)hipHostFree(in_stage_.data);
+    if (out_stage_.data) (void)hipHostFree(out_stage_.data);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void* HipContext::pinned(Pinned& buffer, std::size_t bytes) {
+    if (buffer.bytes >= bytes) return buffer.data;
+    if (buffer.data) hip_check(hipHostFree(buffer.data), "hipHostFree");
+    buffer.data = nullptr;
+    buffer.bytes = 0;
+    const std::size_t grow = (bytes + (std::size_t(1) << 20) - 1) & ~((std::size_t(1) << 20) - 1);
+    hip_check(hipHostMalloc(&buffer.data, grow, hipHostMallocDefault), "hipHostMalloc (staging)");
+    buffer.bytes = grow;
+    return buffer.data;
+}
+
+void* HipContext::input_staging(std::size_t bytes) {
+    if (in_pending_) hip_check(hipEventSynchronize(in_copied_), "staging wait");
+    in_pending_ = false;
+    return pinned(in_stage_, bytes);
+}
+
+void HipContext::upload_staged(DeviceBuffer& destination, std::size_t bytes) {
+    if (bytes > destination.size() || bytes > in_stage_.bytes) throw std::invalid_argument("staged upload too large");
+    if (bytes == 0) return;
+    hip_check(hipMemcpyAsync(destination.data(), in_stage_.data, bytes, hipMemcpyHostToDevice, active_), "upload");
+    hip_check(hipEventRecord(in_copied_, active_), "staging event");
+    in_pending_ = true;
+    upload_bytes_ += bytes;
+}
+
+void HipContext::upload_staged(DeviceBuffer& destination, const void* source, std::size_t bytes) {
+    if (bytes > destination.size()) throw std::invalid_argument("upload exceeds device buffer");
+    if (bytes == 0) return;
+    // In pieces of about 1 MiB: the DMA of one piece runs while the host
+    // copies the next into pinned memory.
+    auto* stage = static_cast<std::uint8_t*>(input_staging(bytes));
+    const auto* src = static_cast<const std::uint8_t*>(source);
+    auto* dst = static_cast<std::uint8_t*>(destination.data());
+    const std::size_t pieces = std::min<std::size_t>(8, (bytes + (std::size_t(1) << 20) - 1) >> 20);
+    const std::size_t piece = ((bytes + pieces - 1) / pieces + 63) & ~std::size_t(63);
+    for (std::size_t off = 0; off < bytes; off += piece) {
+        const std::size_t n = std::min(piece, bytes - off);
+        std::memcpy(stage + off, src + off, n);
+        hip_check(hipMemcpyAsync(dst + off, stage + off, n, hipMemcpyHostToDevice, active_), "upload");
+    }
+    hip_check(hipEventRecord(in_copied_, active_), "staging event");
+    in_pending_ = true;
+    upload_bytes_ += bytes;
+}
+
+void HipContext::download_staged(const DeviceBuffer& source, void* destination, std::size_t bytes) {
+    if (bytes > source.size()) throw std::invalid_argument("download exceeds device buffer");
+    if (bytes == 0) return;
+    void* stage = pinned(out_stage_, bytes);
+    hip_check(hipMemcpyAsync(stage, source.data(), bytes, hipMemcpyDeviceToHost, active_), "download");
+    hip_check(hipStreamSynchronize(active_), "download synchronize");
+    std::memcpy(destination, stage, bytes);
+    download_bytes_ += bytes;
 }
 
 void HipContext::make_current() const { hip_check(hipSetDevice(device_), "hipSetDevice"); }

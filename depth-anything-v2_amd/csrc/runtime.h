@@ -125,6 +125,21 @@ public:
     DeviceBuffer create_device_buffer(std::size_t bytes) { return DeviceBuffer(bytes); }
     void upload(DeviceBuffer& destination, const void* source, std::size_t bytes);
     void download(const DeviceBuffer& source, void* destination, std::size_t bytes);
+    // Host I/O of the inference entries through pinned buffers owned by the
+    // context. A pageable hipMemcpyAsync stages the data itself and returns
+    // only when the copy is done; a host copy into pinned memory takes a few
+    // microseconds per MB and the DMA from it runs on the stream, so the
+    // kernels are enqueued while the input is in flight (ViT-L 518: 3.2 MB
+    // up 0.12 -> 0.08 ms, 1.1 MB down 0.08 -> 0.04 ms).
+    // input_staging: the pinned input buffer, at least `bytes` long, once the
+    // previous staged upload has left it; upload_staged(destination, bytes)
+    // then copies its first `bytes` to the device on the active stream.
+    void* input_staging(std::size_t bytes);
+    void upload_staged(DeviceBuffer& destination, std::size_t bytes);
+    void upload_staged(DeviceBuffer& destination, const void* source, std::size_t bytes);
+    // Copies to the pinned output buffer on the active stream, synchronises
+    // the stream, then copies to `destination`.
+    void download_staged(const DeviceBuffer& source, void* destination, std::size_t bytes);
     void synchronize();
     void make_current() const;
 
@@ -135,10 +150,19 @@ public:
     Profiler& profiler() { return profiler_; }
 
 private:
+    struct Pinned {
+        void* data = nullptr;
+        std::size_t bytes = 0;
+    };
+    void* pinned(Pinned& buffer, std::size_t bytes);
+
     Profiler profiler_;
     int device_ = 0;
     hipStream_t stream_ = nullptr;
     hipStream_t active_ = nullptr;
+    Pinned in_stage_, out_stage_;
+    hipEvent_t in_copied_ = nullptr;  // recorded after each staged upload
+    bool in_pending_ = false;
     std::uint64_t upload_bytes_ = 0;
     std::uint64_t download_bytes_ = 0;
     std::string device_name_;
