@@ -44,6 +44,7 @@ STATUS = {0: "OK", 1: "INVALID_ARGUMENT", 2: "MODEL_IO", 3: "MODEL_FORMAT", 4: "
 FORCE_FP32, FORCE_FP32_WEIGHTS, FORCE_FP32_ATTENTION, FORCE_FP16, FORCE_INT8, FORCE_METAL, FORCE_VULKAN = (
     1, 2, 4, 8, 16, 32, 64)
 REFERENCE_FP16_ATTENTION = 1 << 16  # extension: the reference's binary16 attention in int8 mode
+REFERENCE_FP16_COOP_ATTENTION = 1 << 17  # extension: the same with the cooperative-matrix score shader
 ENCODER = {"vits": 0, "vitb": 1, "vitl": 2}
 GEMM_EPI = {"raw": 0, "row": 1, "row_gelu": 2, "row_layerscale": 3, "transposed": 4, "convt": 5}
 
@@ -201,6 +202,8 @@ PROTOTYPES = {
     "dav2_hip_attention_ref_values": (C.c_int, [vp, vp, vp, u32, u32, u32, C.c_int, vp]),
     "dav2_hip_attention_ref16_fused_scratch_bytes": (u64, [u32, u32, u32]),
     "dav2_hip_attention_ref16_fused": (C.c_int, [vp, vp, u32, u32, u32, vp, u64, vp]),
+    "dav2_hip_attention_ref16_fused_coop": (C.c_int, [vp, vp, u32, u32, u32, vp, u64, vp]),
+    "dav2_hip_attention_ref_scores_coop": (C.c_int, [vp, vp, u32, u32, u32, vp]),
     "dav2_hip_transpose_rows_i8": (C.c_int, [vp, u32, u32, vp, u32, vp]),
     "dav2_hip_attention_fused_scratch_bytes": (u64, [u32, u32, u32]),
     "dav2_hip_attention_fused": (C.c_int, [vp, vp, u32, u32, u32, vp, u64, vp]),

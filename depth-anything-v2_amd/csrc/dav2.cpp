@@ -132,9 +132,9 @@ dav2_status DAV2_CALL dav2_create(const char* model_path_utf8, const dav2_create
     constexpr uint32_t supported = DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP32_WEIGHTS |
                                    DAV2_CREATE_FORCE_FP32_ATTENTION | DAV2_CREATE_FORCE_FP16 |
                                    DAV2_CREATE_FORCE_INT8 | DAV2_CREATE_FORCE_METAL | DAV2_CREATE_FORCE_VULKAN |
-                                   DAV2_CREATE_REFERENCE_FP16_ATTENTION;
+                                   DAV2_CREATE_REFERENCE_FP16_ATTENTION | DAV2_CREATE_REFERENCE_FP16_COOP_ATTENTION;
     if ((options->flags & ~supported) != 0) return fail(DAV2_STATUS_INVALID_ARGUMENT, "unsupported create flags");
-    if ((options->flags & DAV2_CREATE_REFERENCE_FP16_ATTENTION) &&
+    if ((options->flags & (DAV2_CREATE_REFERENCE_FP16_ATTENTION | DAV2_CREATE_REFERENCE_FP16_COOP_ATTENTION)) &&
         (options->flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP32_ATTENTION)))
         return fail(DAV2_STATUS_INVALID_ARGUMENT, "binary16 attention needs the int8 execution precision");
     const uint32_t precision = options->flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP16 | DAV2_CREATE_FORCE_INT8);

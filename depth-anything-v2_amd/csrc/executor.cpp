@@ -34,6 +34,9 @@ AttentionMode attention_mode_for(std::uint32_t flags) {
     // reference's binary16 arithmetic is DAV2_CREATE_REFERENCE_FP16_ATTENTION
     // (and the fp16 mode's default).
     if (flags & (DAV2_CREATE_FORCE_FP32 | DAV2_CREATE_FORCE_FP32_ATTENTION)) return AttentionMode::fp32;
+    // operators.cpp:1137-1148: devices with cooperative_matrix_fp16 take the
+    // scores from bmm_score_coop_fp16.glsl
+    if (flags & DAV2_CREATE_REFERENCE_FP16_COOP_ATTENTION) return AttentionMode::binary16_coop;
     if (flags & (DAV2_CREATE_REFERENCE_FP16_ATTENTION | DAV2_CREATE_FORCE_FP16)) return AttentionMode::binary16;
     return AttentionMode::exact;
 }

@@ -75,7 +75,9 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
     DeviceBuffer& hidden = arena.get("enc.hidden", tok_bytes * 4);
     const bool f32 = precision_ != Precision::int8;  // fp32 or fp16 mode: the float path
     const bool fused = !f32 && attention_ == AttentionMode::exact;
-    const Precision materialised = attention_ == AttentionMode::binary16 ? Precision::fp16 : Precision::fp32;
+    const bool coop = attention_ == AttentionMode::binary16_coop;
+    const Precision materialised =
+        attention_ == AttentionMode::binary16 || coop ? Precision::fp16 : Precision::fp32;
     DeviceBuffer& scores =
         arena.get("enc.scores", fused ? HipOperators::attention_fused_scratch_bytes(T, H, batch)
                                       : HipOperators::attention_score_bytes(T, H, batch, materialised));
@@ -121,7 +123,7 @@ void DinoEncoder::forward(const float* image, std::uint32_t width, std::uint32_t
         if (fused)
             ops_.attention_fused(attn, qkv, T, H, batch, scores, col_absmax, qkv_tiles);
         else
-            ops_.attention_batched(attn, qkv, T, H, batch, scores, materialised);
+            ops_.attention_batched(attn, qkv, T, H, batch, scores, materialised, coop);
         // proj + LayerScale residual (encoder.cpp:478-491), in place
         ops_.quantize_rows(attn, 0, rows, D);
         const GpuTensor& wproj = W(".attn.proj.weight");
@@ -174,7 +176,8 @@ void DinoEncoder::forward_fp32(std::uint32_t rows, std::uint32_t T, std::uint32_
             ops_.attention_mfma_f32(attn, qkv, T, H, batch, scores);
         else
             ops_.attention_batched(attn, qkv, T, H, batch, scores,
-                                   attention_ == AttentionMode::fp32 ? Precision::fp32 : Precision::fp16);
+                                   attention_ == AttentionMode::fp32 ? Precision::fp32 : Precision::fp16,
+                                   attention_ == AttentionMode::binary16_coop);
         ops_.linear_f32(current, attn, W(".attn.proj.weight"), &W(".attn.proj.bias"), rows, D, D, E::row_layerscale,
                         &W(".ls1.gamma"), 0, half);
         ops_.layer_norm(normed, current, W(".norm2.weight"), W(".norm2.bias"), rows, D, 1.0e-6f);

@@ -48,7 +48,7 @@ private:
 // Attention of the int8 graph: the integer-exact fused kernel (default), the
 // reference's binary16 pipeline, or fp32 scores (FORCE_FP32_ATTENTION; also
 // the fp32 precision mode, which uses the matrix-core fp32 kernels).
-enum class AttentionMode { exact, binary16, fp32 };
+enum class AttentionMode { exact, binary16, binary16_coop, fp32 };
 
 class DinoEncoder {
 public:

@@ -17,6 +17,13 @@
 // sequential per output, so they run on the VALU (a matrix core's
 // accumulation order is its own).
 //
+// Cooperative-matrix scores (bmm_score_coop_fp16.glsl:12-33, the reference's
+// int8-mode scores on devices with cooperative_matrix_fp16): the same binary16
+// operands, every product exact, summed in fp32 by the matrix unit in its own
+// order (coopMatMulAdd), the sum stored as binary16. Here that is
+// v_mfma_f32_16x16x32_f16 (two K steps of 32 features per 16 x 16 block);
+// softmax and values as above.
+//
 // Layouts: qkv [batch*T][3*H*64] token-major (q | k | v, head h at h*64);
 // fp32 scores [batch][H][T][T] floats; binary16 scores [batch][H][T][words]
 // packed half2 words, words = ceil(T/2) (the reference's layout and size);
@@ -150,6 +157,70 @@ __global__ __launch_bounds__(256) void ref_scores_kernel(const float* __restrict
             for (int c = 0; c < 4; ++c)
                 if (j + c < tokens) out[(plane + i) * tokens + j + c] = s[r][c];
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Cooperative-matrix scores. v_mfma_f32_16x16x32_f16 operands: lane l holds
+// row (A) or column (B) l % 16, K elements 8 (l / 16) .. + 7; the result
+// element (row 4 (l / 16) + i, column l % 16) is lane l's i-th value.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+DAV2_DEV h8 half8(const float4& a, const float4& b, float scale) {
+    return h8{static_cast<_Float16>(keep_fp32(a.x * scale)), static_cast<_Float16>(keep_fp32(a.y * scale)),
+              static_cast<_Float16>(keep_fp32(a.z * scale)), static_cast<_Float16>(keep_fp32(a.w * scale)),
+              static_cast<_Float16>(keep_fp32(b.x * scale)), static_cast<_Float16>(keep_fp32(b.y * scale)),
+              static_cast<_Float16>(keep_fp32(b.z * scale)), static_cast<_Float16>(keep_fp32(b.w * scale))};
+}
+
+// A operand of the two K steps for query row i (features 32 s + 8 g ..):
+// binary16(q * 0.125); rows past T are zeros.
+DAV2_DEV void coop_query(const float* qkv, uint32_t b, uint32_t tokens, uint32_t D, uint32_t h, uint32_t i, uint32_t g,
+                         h8 (&qa)[2]) {
+    const float* q = qkv + (static_cast<uint64_t>(b) * tokens + min(i, tokens - 1u)) * 3u * D + h * 64u + 8u * g;
+    const float scale = i < tokens ? 0.125f : 0.0f;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+        qa[st] = half8(*reinterpret_cast<const float4*>(q + 32 * st), *reinterpret_cast<const float4*>(q + 32 * st + 4),
+                       scale);
+}
+
+DAV2_DEV f4v coop_block(const h8 (&qa)[2], const h8 (&kb)[2]) {
+    f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0], kb[0], acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1], kb[1], acc, 0, 0, 0);
+}
+
+DAV2_DEV uint16_t half_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(keep_fp32(v))); }
+
+// Materialised binary16 scores [batch][H][T][words]: workgroup = 16 queries x
+// 64 keys, wave w keys 16 w ..; keys from T on are zeros (so the second half
+// of an odd row's last word is 0, as packHalf2x16 writes it).
+__global__ __launch_bounds__(256) void ref_scores_coop_kernel(const float* __restrict__ qkv,
+                                                              uint16_t* __restrict__ scores, uint32_t tokens,
+                                                              uint32_t heads) {
+    const uint32_t bh = blockIdx.z, b = bh / heads, h = bh - b * heads;
+    const uint32_t D = heads * 64u;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, g = lane >> 4, col = lane & 15u;
+    const uint32_t i0 = blockIdx.y * 16u, j = blockIdx.x * 64u + wave * 16u + col;
+    h8 qa[2], kb[2];
+    coop_query(qkv, b, tokens, D, h, i0 + col, g, qa);
+    {
+        const float* k = qkv + (static_cast<uint64_t>(b) * tokens + min(j, tokens - 1u)) * 3u * D + D + h * 64u + 8u * g;
+        const float one = j < tokens ? 1.0f : 0.0f;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+            kb[st] = half8(*reinterpret_cast<const float4*>(k + 32 * st), *reinterpret_cast<const float4*>(k + 32 * st + 4),
+                           one);
+    }
+    const f4v acc = coop_block(qa, kb);
+    const uint32_t words = (tokens + 1u) >> 1;
+    if (j >= 2u * words) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t i = i0 + 4u * g + r;
+        if (i < tokens) scores[(static_cast<uint64_t>(bh) * tokens + i) * 2u * words + j] = half_bits(acc[r]);
     }
 }
 
@@ -536,7 +607,7 @@ __global__ __launch_bounds__(256) void ref16_pack_kernel(const float* __restrict
 // binary16 scores / probabilities, `stride` words per row (4 more than a
 // multiple of 32, so the 16 rows' 16-byte reads fall on different banks).
 // At T = 1370 that is 53.5 KB: three workgroups per CU.
-template <int R>
+template <int R, bool COOP>
 __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ out, const float* __restrict__ qkv,
                                                           const uint32_t* __restrict__ k16,
                                                           const uint32_t* __restrict__ v16, uint32_t tokens,
@@ -590,9 +661,14 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
 
     fetch(kbase, 0, staged0, staged1);
     // q row i as binary16 pairs of q * 0.125 (bmm_score_fp16.glsl:32); rows
-    // past T compute on zeros and are never stored
-    uint32_t qp[32];
-    {
+    // past T compute on zeros and are never stored. Cooperative-matrix
+    // scores: the MFMA A operand of query row rb*16 + l%16 instead.
+    uint32_t qp[COOP ? 1 : 32];
+    h8 qa[2];
+    if constexpr (COOP) {
+        static_assert(R == 16, "one 16-row MFMA block of queries");
+        coop_query(qkv, b, tokens, D, h, rb * R + (lane & 15u), lane >> 4, qa);
+    } else {
         const float* q = qkv + (static_cast<uint64_t>(b) * tokens + min(i, tokens - 1u)) * 3u * D + h * 64u;
         float4 v[16];
 #pragma unroll
@@ -608,9 +684,31 @@ __global__ __launch_bounds__(256) void ref16_fused_kernel(float* __restrict__ ou
     put(staged0, staged1);
     __syncthreads();
 
+    if constexpr (COOP) {
+        // bmm_score_coop_fp16.glsl: wave w scores keys 16w .. 16w+15 of each
+        // chunk for the 16 rows; B operand words (16 st + 4 g + e, key) of
+        // the chunk buffer are features 32 st + 8 g + 2e, +1. Each result is
+        // stored as one binary16 half of its row's packed word.
+        uint16_t* const halves = reinterpret_cast<uint16_t*>(srows);
+        const uint32_t key = 16u * wave + (lane & 15u), g = lane >> 4;
+        for (uint32_t c = 0; c < chunks; ++c) {
+            if (c + 1u < chunks) fetch(kbase, c + 1u, staged0, staged1);
+            h8 kb[2];
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const uint32_t* w = kv + (16u * st + 4u * g) * 64u + key;
+                kb[st] = __builtin_bit_cast(h8, make_uint4(w[0], w[64], w[128], w[192]));
+            }
+            const f4v acc = coop_block(qa, kb);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                halves[((4u * g + rr) * stride + 32u * c) * 2u + key] = half_bits(acc[rr]);
+            next_chunk(c);
+        }
+    }
     // scores: s = sum over features 0..63 of float(q16 * k16), stored binary16
     uint32_t* const myrow = srows + r * stride;
-    for (uint32_t c = 0; c < chunks; ++c) {
+    for (uint32_t c = 0; !COOP && c < chunks; ++c) {
         if (c + 1u < chunks) fetch(kbase, c + 1u, staged0, staged1);
         const uint32_t* kc = kv + grp * G;
         float acc[G];
@@ -809,8 +907,13 @@ uint64_t dav2_hip_attention_ref16_fused_scratch_bytes(uint32_t tokens, uint32_t 
     return 2ull * batch * heads * ref16_chunks(tokens) * kChunkWords * 4u;
 }
 
-int dav2_hip_attention_ref16_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads, uint32_t batch,
-                                   void* scratch, uint64_t scratch_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+template <bool COOP>
+int run_ref16_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads, uint32_t batch, void* scratch,
+                    uint64_t scratch_bytes, void* stream) {
     if (!out || !qkv || !scratch || !valid(tokens, heads, batch)) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(scratch)) &
         15)
@@ -827,11 +930,35 @@ int dav2_hip_attention_ref16_fused(float* out, const float* qkv, uint32_t tokens
     hipStream_t s = static_cast<hipStream_t>(stream);
     dispatch(ref16_pack_kernel, dim3(chunks, bh), dim3(256), 0, s, qkv, k16, v16, tokens, heads, chunks);
     static const hipError_t lds_ok =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(ref16_fused_kernel<kRef16Rows>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(ref16_fused_kernel<kRef16Rows, COOP>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(80u * 1024u));
     if (lds_ok != hipSuccess) return lds_ok;
-    dispatch(ref16_fused_kernel<kRef16Rows>, dim3(static_cast<uint32_t>(items)), dim3(256), shape.lds, s, out, qkv, k16,
-             v16, tokens, heads, chunks, row_blocks, shape.stride);
+    dispatch((ref16_fused_kernel<kRef16Rows, COOP>), dim3(static_cast<uint32_t>(items)), dim3(256), shape.lds, s, out,
+             qkv, k16, v16, tokens, heads, chunks, row_blocks, shape.stride);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+int dav2_hip_attention_ref16_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads, uint32_t batch,
+                                   void* scratch, uint64_t scratch_bytes, void* stream) {
+    return run_ref16_fused<false>(out, qkv, tokens, heads, batch, scratch, scratch_bytes, stream);
+}
+
+int dav2_hip_attention_ref16_fused_coop(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
+                                        uint32_t batch, void* scratch, uint64_t scratch_bytes, void* stream) {
+    return run_ref16_fused<true>(out, qkv, tokens, heads, batch, scratch, scratch_bytes, stream);
+}
+
+int dav2_hip_attention_ref_scores_coop(void* scores, const float* qkv, uint32_t tokens, uint32_t heads,
+                                       uint32_t batch, void* stream) {
+    if (!scores || !qkv || !valid(tokens, heads, batch)) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(qkv) & 15) || (reinterpret_cast<uintptr_t>(scores) & 1)) return hipErrorInvalidValue;
+    const dim3 grid(ceil_div(tokens, 64), ceil_div(tokens, 16), batch * heads);
+    dispatch(ref_scores_coop_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), qkv,
+             static_cast<uint16_t*>(scores), tokens, heads);
     return hipGetLastError();
 }
 

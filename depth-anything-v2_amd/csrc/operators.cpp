@@ -302,9 +302,10 @@ void HipOperators::attention_head64(DeviceBuffer& output, const DeviceBuffer& qk
 
 void HipOperators::attention_batched(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
                                      std::uint32_t heads, std::uint32_t batch, DeviceBuffer& scores,
-                                     Precision precision) {
+                                     Precision precision, bool cooperative) {
     if (tokens == 0 || heads == 0 || batch == 0) throw std::invalid_argument("invalid attention dimensions");
     const int fp16 = precision == Precision::fp16 ? 1 : 0;
+    if (cooperative && !fp16) throw std::invalid_argument("cooperative-matrix scores are binary16");
     if (scores.size() < attention_score_bytes(tokens, heads, batch, precision))
         throw std::invalid_argument("attention score scratch device buffer is too small");
     const hipStream_t s = stream();
@@ -316,14 +317,19 @@ void HipOperators::attention_batched(DeviceBuffer& output, const DeviceBuffer& q
         // its binary16 keys and values (all but the shortest sequences)
         const std::uint64_t fused = dav2_hip_attention_ref16_fused_scratch_bytes(tokens, heads, batch);
         if (fused != 0 && scores.size() >= fused) {
-            ProfileScope p(prof, "attention_ref16_fused", 2.0 * flops, "FLOP", s);
-            hip_check(dav2_hip_attention_ref16_fused(output.as<float>(), qkv.as<float>(), tokens, heads, batch,
-                                                     scores.data(), scores.size(), s),
+            ProfileScope p(prof, cooperative ? "attention_ref16_coop_fused" : "attention_ref16_fused", 2.0 * flops,
+                           "FLOP", s);
+            const auto run = cooperative ? dav2_hip_attention_ref16_fused_coop : dav2_hip_attention_ref16_fused;
+            hip_check(run(output.as<float>(), qkv.as<float>(), tokens, heads, batch, scores.data(), scores.size(), s),
                       "fused binary16 attention");
             return;
         }
     }
-    {
+    if (cooperative) {
+        ProfileScope p(prof, "attention_scores_coop_f16", flops, "FLOP", s);
+        hip_check(dav2_hip_attention_ref_scores_coop(scores.data(), qkv.as<float>(), tokens, heads, batch, s),
+                  "cooperative-matrix attention scores");
+    } else {
         ProfileScope p(prof, fp16 ? "attention_scores_ref_f16" : "attention_scores_ref_f32", flops, "FLOP", s);
         hip_check(dav2_hip_attention_ref_scores(scores.data(), qkv.as<float>(), tokens, heads, batch, fp16, s),
                   "attention scores");

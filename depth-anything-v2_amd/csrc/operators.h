@@ -215,9 +215,11 @@ public:
     // Batched attention over `batch` token matrices of `tokens` rows each, in
     // the reference shaders' arithmetic order (fp32: bmm.glsl /
     // softmax_lastdim.glsl; fp16: the binary16 shaders), VALU kernels.
+    // cooperative (fp16 only): the scores of bmm_score_coop_fp16.glsl on the
+    // matrix cores instead of bmm_score_fp16.glsl.
     void attention_batched(DeviceBuffer& output, const DeviceBuffer& qkv, std::uint32_t tokens,
                            std::uint32_t heads, std::uint32_t batch, DeviceBuffer& score_scratch,
-                           Precision precision);
+                           Precision precision, bool cooperative = false);
     static std::uint64_t attention_score_bytes(std::uint32_t tokens, std::uint32_t heads, std::uint32_t batch,
                                                Precision precision);
     // fp32 attention on the matrix cores (fp32 precision mode): the same

@@ -331,6 +331,25 @@ DAV2_API uint64_t dav2_hip_attention_ref16_fused_scratch_bytes(uint32_t tokens, 
 DAV2_API int dav2_hip_attention_ref16_fused(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
                                             uint32_t batch, void* scratch, uint64_t scratch_bytes, void* stream);
 
+/* The reference's int8-mode scores on devices with cooperative_matrix_fp16
+ * (src/operators.cpp:1137-1148 selects bmm_score_coop_fp16.glsl:12-33):
+ * binary16(q * 0.125) and binary16(k) operands, every product exact, the fp32
+ * sums in the matrix unit's order (v_mfma_f32_16x16x32_f16, two K steps of
+ * 32 features), each score stored as binary16 in the packed
+ * [batch][H][T][ceil(T/2)] layout of dav2_hip_attention_ref_scores (fp16 = 1);
+ * the softmax and values then run as above. The shader leaves the sum order
+ * to the device, so these scores are held to the oracle's mode 3 (exact
+ * products summed in double, rounded to fp32 and then binary16) within one
+ * binary16 rounding, not bit for bit. */
+DAV2_API int dav2_hip_attention_ref_scores_coop(void* scores, const float* qkv, uint32_t tokens, uint32_t heads,
+                                                uint32_t batch, void* stream);
+/* dav2_hip_attention_ref16_fused with the cooperative-matrix scores above
+ * (same scratch); the same bits as dav2_hip_attention_ref_scores_coop +
+ * _ref_softmax + _ref_values with fp16 = 1. */
+DAV2_API int dav2_hip_attention_ref16_fused_coop(float* out, const float* qkv, uint32_t tokens, uint32_t heads,
+                                                 uint32_t batch, void* scratch, uint64_t scratch_bytes,
+                                                 void* stream);
+
 /* Fused attention (int8-mode default): replaces the materialised binary16
  * path of src/operators.cpp:1132-1167 (bmm_score_fp16.glsl,
  * softmax_lastdim_half.glsl, bmm_value_fp16.glsl) with an integer-exact

@@ -354,6 +354,21 @@ DAV2_API dav2_status DAV2_CALL dav2_infer_tensor_f32(
 enum { DAV2_CREATE_REFERENCE_FP16_ATTENTION = 1u << 16u };
 
 /*
+ * Create flag (int8 or fp16 mode): the reference's binary16 attention as it
+ * runs on devices with cooperative_matrix_fp16 (src/operators.cpp:1137-1148):
+ * the scores of bmm_score_coop_fp16.glsl -- binary16 operands, exact
+ * products, fp32 sums in the matrix unit's order (here the MFMA's), each
+ * score stored as binary16 -- then softmax_lastdim_half.glsl and
+ * bmm_value_fp16.glsl as under DAV2_CREATE_REFERENCE_FP16_ATTENTION. The
+ * shader leaves the order of the sums to the device, so the results are held
+ * to the CPU oracle's restatement (products summed exactly) within a
+ * tolerance, not bit for bit. Takes precedence over
+ * DAV2_CREATE_REFERENCE_FP16_ATTENTION; not combinable with FORCE_FP32 /
+ * FORCE_FP32_ATTENTION.
+ */
+enum { DAV2_CREATE_REFERENCE_FP16_COOP_ATTENTION = 1u << 17u };
+
+/*
  * Device-resident, batched variant of dav2_infer_tensor_f32 for callers whose
  * images already live in HBM (serving loops, benchmarks). device_input holds
  * batch images, each 3*H*W float32 CHW, back to back; device_output receives

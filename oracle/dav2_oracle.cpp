@@ -771,7 +771,24 @@ void binary16_score_row(const float* q16, const std::vector<float>& kt, size_t T
     }
 }
 
-void attention_binary16(const float* qkv, uint32_t tokens, uint32_t heads, float* out, float* probabilities) {
+// One row of bmm_score_coop_fp16.glsl:12-33: s = sum over features 0..63 of
+// q16[f] * k16[j][f], every product exact, summed in double in feature order,
+// rounded to fp32 (the accumulator's type), then stored as binary16
+// (packHalf2x16). Four keys per vector.
+void coop_score_row(const float* q16, const std::vector<float>& kt, size_t T, uint16_t* hrow) {
+    const size_t T8 = (T + 7) & ~size_t(7);
+    for (size_t j = 0; j < T; j += 4) {
+        __m256d s = _mm256_setzero_pd();
+        for (int f = 0; f < 64; ++f)
+            s = _mm256_add_pd(s, _mm256_mul_pd(_mm256_set1_pd(q16[f]), _mm256_cvtps_pd(_mm_loadu_ps(&kt[f * T8 + j]))));
+        alignas(16) float lanes[4];
+        _mm_store_ps(lanes, _mm256_cvtpd_ps(s));
+        for (size_t l = 0; l < 4 && j + l < T; ++l) hrow[j + l] = f2h(lanes[l]);
+    }
+}
+
+void attention_binary16(const float* qkv, uint32_t tokens, uint32_t heads, float* out, float* probabilities,
+                        bool coop) {
     const size_t D = static_cast<size_t>(heads) * 64;
     const size_t T = tokens;
     // Per head: keys feature-major and values token-major [T][64], rounded to
@@ -794,7 +811,10 @@ void attention_binary16(const float* qkv, uint32_t tokens, uint32_t heads, float
                 const float* q = qkv + static_cast<size_t>(i) * D * 3 + h * 64;
                 float q16[64];
                 for (int f = 0; f < 64; ++f) q16[f] = round_half(q[f] * 0.125f);
-                binary16_score_row(q16, keys_t[h], T, hrow.data());
+                if (coop)
+                    coop_score_row(q16, keys_t[h], T, hrow.data());
+                else
+                    binary16_score_row(q16, keys_t[h], T, hrow.data());
                 // softmax over the packed row
                 float maximum = -3.402823466e+38f;
                 for (size_t j = 0; j < T; ++j) maximum = std::max(maximum, h2f(hrow[j]));
@@ -846,6 +866,19 @@ void orc_attention_scores_binary16(const float* qkv, uint32_t tokens, uint32_t h
     }
 }
 
+void orc_attention_scores_coop(const float* qkv, uint32_t tokens, uint32_t heads, uint16_t* scores) {
+    const size_t D = static_cast<size_t>(heads) * 64, T = tokens;
+    for (size_t h = 0; h < heads; ++h) {
+        const std::vector<float> kt = binary16_keys(qkv, T, D, h);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < static_cast<int64_t>(T); ++i) {
+            float q16[64];
+            for (int f = 0; f < 64; ++f) q16[f] = round_half(qkv[i * D * 3 + h * 64 + f] * 0.125f);
+            coop_score_row(q16, kt, T, scores + (h * T + i) * T);
+        }
+    }
+}
+
 void orc_round_half_product(const float* a, const float* b, uint64_t count, float* out) {
     uint64_t i = 0;
     for (; i + 8 <= count; i += 8)
@@ -861,8 +894,8 @@ void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads, int
     }
     const size_t D = static_cast<size_t>(heads) * 64;
     const size_t T = tokens;
-    if (mode == 1) {
-        attention_binary16(qkv, tokens, heads, out, probabilities);
+    if (mode == 1 || mode == 3) {
+        attention_binary16(qkv, tokens, heads, out, probabilities, mode == 3);
         return;
     }
 #pragma omp parallel
@@ -1581,7 +1614,8 @@ void encoder_block(const orc_model& m, std::vector<float>& cur, uint32_t T, uint
                    T, D, 1.0e-6f, norm.data());
     lin(norm, blk(b, ".attn.qkv.weight"), blk(b, ".attn.qkv.bias"), D, 3 * D, false, qkv);
     // attention_mode as orc_attention_head64: 0 fp32 scores, 1 the reference's
-    // binary16 pipeline, 2 integer-exact (this build's int8-mode default)
+    // binary16 pipeline, 2 integer-exact (this build's int8-mode default), 3
+    // the binary16 pipeline with cooperative-matrix scores
     orc_attention_head64(qkv.data(), T, m.heads, attention_mode, attn.data(), nullptr);
     lin(attn, blk(b, ".attn.proj.weight"), blk(b, ".attn.proj.bias"), D, D, false, tmp);
     orc_add_scaled(cur.data(), tmp.data(), m.t(blk(b, ".ls1.gamma")).data.data(), n, D, next.data());

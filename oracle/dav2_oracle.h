@@ -81,12 +81,19 @@ void orc_softmax_rows(const float* input, uint64_t rows, uint32_t columns,
  * mode 2: integer-exact (the int8-mode kernel): 15-bit block floating point
  *         q*0.125 (per token), k (per head) and v (per feature), exact
  *         integer dot products, 21-bit softmax numerators.
+ * mode 3: mode 1 with the scores of bmm_score_coop_fp16.glsl (devices with
+ *         cooperative_matrix_fp16): binary16 operands, exact products summed
+ *         in double (feature order) and rounded to fp32, then to binary16.
+ *         The shader leaves the order of the fp32 sums to the matrix unit,
+ *         so a GPU result is held to this within a tolerance.
  * probabilities (optional) receives [H][T][T]. */
 void orc_attention_head64(const float* qkv, uint32_t tokens, uint32_t heads,
                           int mode, float* out, float* probabilities);
 /* The binary16 scores of mode 1 before the softmax (bmm_score_fp16.glsl):
  * scores [H][T][T] binary16 bit patterns. */
 void orc_attention_scores_binary16(const float* qkv, uint32_t tokens, uint32_t heads, uint16_t* scores);
+/* The binary16 scores of mode 3 (bmm_score_coop_fp16.glsl, sums as above). */
+void orc_attention_scores_coop(const float* qkv, uint32_t tokens, uint32_t heads, uint16_t* scores);
 /* out[i] = fp16(a[i] * b[i]) for binary16 values a, b (the vector path the
  * mode-1 attention uses; the tail uses the scalar conversion). */
 void orc_round_half_product(const float* a, const float* b, uint64_t count, float* out);
@@ -133,8 +140,10 @@ orc_model* orc_model_load(const char* path, int encoder, char* error,
 void orc_model_free(orc_model* model);
 /* attention_mode selects orc_attention_head64's mode for every block: 2 (the
  * integer-exact attention, this build's int8-mode default), 1 (the
- * reference's binary16 pipeline, DAV2_CREATE_REFERENCE_FP16_ATTENTION) or 0
- * (fp32 scores, FORCE_FP32_ATTENTION).
+ * reference's binary16 pipeline, DAV2_CREATE_REFERENCE_FP16_ATTENTION), 3
+ * (the same with cooperative-matrix scores,
+ * DAV2_CREATE_REFERENCE_FP16_COOP_ATTENTION) or 0 (fp32 scores,
+ * FORCE_FP32_ATTENTION).
  * depth: W*H raw ReLU depth. pre_relu (nullable): W*H before the final ReLU.
  * features (nullable): 4*T*D captured encoder features.
  * Returns 0 on success. */

@@ -28,6 +28,7 @@ _PROTO = {
     "orc_exp": (None, [vp, u64, vp]),
     "orc_round_half_product": (None, [vp, vp, u64, vp]),
     "orc_attention_scores_binary16": (None, [vp, u32, u32, vp]),
+    "orc_attention_scores_coop": (None, [vp, u32, u32, vp]),
     "orc_layer_norm": (None, [vp, vp, vp, u32, u32, f32, vp]),
     "orc_add_scaled": (None, [vp, vp, vp, u64, u32, vp]),
     "orc_add": (None, [vp, vp, u64, vp]),
@@ -220,14 +221,23 @@ class Oracle:
         self.lib.orc_attention_scores_binary16(qkv.ctypes.data, tokens, heads, out.ctypes.data)
         return out
 
+    def scores_coop(self, qkv, tokens: int, heads: int):
+        """Binary16 scores [H][T][T] as float16 (bmm_score_coop_fp16.glsl: exact
+        products summed in double, rounded to fp32, then binary16)."""
+        qkv = _f32(qkv)
+        out = np.empty((heads, tokens, tokens), np.float16)
+        self.lib.orc_attention_scores_coop(qkv.ctypes.data, tokens, heads, out.ctypes.data)
+        return out
+
     def attention(self, qkv, tokens: int, heads: int, fp16: bool = False, probabilities: bool = False,
-                  fused: bool = False):
-        """fp16=False: fp32 path; fp16=True: materialised binary16 scores;
+                  fused: bool = False, coop: bool = False):
+        """fp16=False: fp32 path; fp16=True: materialised binary16 scores
+        (coop=True: the cooperative-matrix score shader's arithmetic);
         fused=True: the integer-exact kernel of int8 mode."""
         qkv = _f32(qkv)
         out = np.empty((tokens, heads * 64), np.float32)
         p = np.empty((heads, tokens, tokens), np.float32) if probabilities else None
-        mode = 2 if fused else int(fp16)
+        mode = 2 if fused else (3 if coop else int(fp16))
         self.lib.orc_attention_head64(qkv.ctypes.data, tokens, heads, mode, out.ctypes.data, _p(p))
         return (out, p) if probabilities else out
 
@@ -453,14 +463,15 @@ class Oracle:
                                         pos.ctypes.data, width, height, d, out.ctypes.data)
         return out
 
-    ATTENTION_MODES = {"fp32": 0, "binary16": 1, "exact": 2}
+    ATTENTION_MODES = {"fp32": 0, "binary16": 1, "exact": 2, "coop": 3}
 
     def infer(self, h, chw, width: int, height: int, attention: str = "exact", dim: int | None = None):
         """The int8 graph. attention: "exact" (this build's integer-exact
         attention, the int8-mode default of the GPU path; not the reference's
         arithmetic), "binary16" (the reference's int8-mode attention
-        arithmetic: bmm_score_fp16 / softmax_lastdim_half / bmm_value_fp16) or
-        "fp32" (FORCE_FP32_ATTENTION: bmm.glsl / softmax_lastdim.glsl)."""
+        arithmetic: bmm_score_fp16 / softmax_lastdim_half / bmm_value_fp16),
+        "coop" (the same with bmm_score_coop_fp16's scores) or "fp32"
+        (FORCE_FP32_ATTENTION: bmm.glsl / softmax_lastdim.glsl)."""
         mode = self.ATTENTION_MODES[attention]
         chw = _f32(chw)
         depth = np.empty((height, width), np.float32)

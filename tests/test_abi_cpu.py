@@ -105,6 +105,14 @@ def test_create_option_validation(pkg, lib, tmp_path):
     assert _create(pkg, lib, p, flags=pkg.FORCE_FP32)[0] == 9
     assert _create(pkg, lib, p, flags=pkg.FORCE_INT8 | 2)[0] == 9
     assert _create(pkg, lib, p, flags=pkg.FORCE_METAL)[0] == 8
+    # the binary16 attention flags need the int8 or fp16 precision
+    for att in (pkg.REFERENCE_FP16_ATTENTION, pkg.REFERENCE_FP16_COOP_ATTENTION):
+        assert _create(pkg, lib, p, flags=att)[0] == 9
+        assert _create(pkg, lib, p, flags=pkg.FORCE_FP16 | att)[0] == 9
+        assert _create(pkg, lib, p, flags=pkg.FORCE_FP32 | att) == (
+            1, "binary16 attention needs the int8 execution precision")
+        assert _create(pkg, lib, p, flags=pkg.FORCE_FP32_ATTENTION | att)[0] == 1
+    assert _create(pkg, lib, p, flags=1 << 18) == (1, "unsupported create flags")
     assert lib.dav2_create(str(p).encode(), C.byref(opts), None) == 1
     # a missing file fails in the loader (std::runtime_error -> INTERNAL_ERROR)
     st, msg = _create(pkg, lib, p)

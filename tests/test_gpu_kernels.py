@@ -686,18 +686,23 @@ def _attention_mfma_gpu(torch, lib, qkv, tokens, heads):
     return host(torch, out), probs
 
 
-def _attention_ref_gpu(torch, lib, qkv, tokens, heads, fp16, batch=1, unpacked=True):
-    """The reference-order kernels; returns the output, the probabilities
-    ([batch*H][T][T] as float32) and the scores before the softmax (None,
-    None without `unpacked`)."""
+def _attention_ref_gpu(torch, lib, qkv, tokens, heads, fp16, batch=1, unpacked=True, coop=False):
+    """The reference-order kernels (coop: the cooperative-matrix scores);
+    returns the output, the probabilities ([batch*H][T][T] as float32) and
+    the scores before the softmax (None, None without `unpacked`)."""
     qd = dev(torch, qkv)
     nbytes = lib.dav2_hip_attention_ref_scratch_bytes(tokens, heads, batch, int(fp16))
     words = (tokens + 1) // 2
     assert nbytes == batch * heads * tokens * (words * 4 if fp16 else tokens * 4)  # the reference's size
     buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    if coop:
+        buf.fill_(0xFF)  # every half of the score buffer is written (NaN pattern otherwise)
     out = empty(torch, (batch * tokens, heads * 64), torch.float32)
     s = stream(torch)
-    ok(lib, lib.dav2_hip_attention_ref_scores(ptr(buf), ptr(qd), tokens, heads, batch, int(fp16), s))
+    if coop:
+        ok(lib, lib.dav2_hip_attention_ref_scores_coop(ptr(buf), ptr(qd), tokens, heads, batch, s))
+    else:
+        ok(lib, lib.dav2_hip_attention_ref_scores(ptr(buf), ptr(qd), tokens, heads, batch, int(fp16), s))
 
     def unpack():
         if fp16:
@@ -757,18 +762,17 @@ def test_attention_ref_fp16_bit_exact(gpu, lib, oracle, tokens, heads, batch):
         assert np.array_equal(out[rows].view(np.uint32), ref.view(np.uint32))
 
 
-def _attention_ref16_fused_gpu(torch, lib, qkv, tokens, heads, batch=1):
+def _attention_ref16_fused_gpu(torch, lib, qkv, tokens, heads, batch=1, coop=False):
     qd = dev(torch, qkv)
     nbytes = lib.dav2_hip_attention_ref16_fused_scratch_bytes(tokens, heads, batch)
     assert nbytes == 2 * batch * heads * ((tokens + 63) // 64) * 8192
     buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     out = empty(torch, (batch * tokens, heads * 64), torch.float32)
     out.fill_(float("nan"))
-    ok(lib, lib.dav2_hip_attention_ref16_fused(ptr(out), ptr(qd), tokens, heads, batch, ptr(buf), nbytes,
-                                               stream(torch)))
+    run = lib.dav2_hip_attention_ref16_fused_coop if coop else lib.dav2_hip_attention_ref16_fused
+    ok(lib, run(ptr(out), ptr(qd), tokens, heads, batch, ptr(buf), nbytes, stream(torch)))
     # one byte short of the binary16 keys and values is rejected before any launch
-    assert lib.dav2_hip_attention_ref16_fused(ptr(out), ptr(qd), tokens, heads, batch, ptr(buf), nbytes - 1,
-                                              stream(torch)) == 1
+    assert run(ptr(out), ptr(qd), tokens, heads, batch, ptr(buf), nbytes - 1, stream(torch)) == 1
     return host(torch, out)
 
 
@@ -803,6 +807,101 @@ def test_attention_ref16_fused_matches_three_kernels(gpu, lib, tokens, heads, ba
     ref, _, _ = _attention_ref_gpu(torch, lib, qkv, tokens, heads, True, batch, unpacked=False)
     assert np.isfinite(out).all()
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def _f16_steps(a, b):
+    """Distance in binary16 steps between two float16 arrays."""
+    def key(x):
+        u = x.view(np.uint16).astype(np.int32)
+        return np.where(u & 0x8000, -(u & 0x7FFF), u)
+    return np.abs(key(a) - key(b))
+
+
+@pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (2, 1, 1), (5, 2, 1), (77, 4, 2), (258, 2, 1),
+                                                (1370, 16, 1), (2241, 2, 1), (5477, 1, 1)])
+def test_attention_coop_scores(gpu, lib, oracle, tokens, heads, batch):
+    # bmm_score_coop_fp16.glsl on v_mfma_f32_16x16x32_f16 against the oracle's
+    # mode-3 scores (exact products summed in double, rounded to fp32, then
+    # binary16). The shader leaves the fp32 sum order to the matrix unit, and
+    # any fp32 order of 64 terms is within 63 * 2^-24 * sum|q16 k16| of the
+    # exact sum; so a score may differ from the oracle's by one binary16 step
+    # plus that bound (near zero, where binary16 steps are finer than the
+    # fp32 sums' rounding, that can be several steps), and differs at all only
+    # rarely. The scores differ from the per-product shader's (mode 1) in
+    # many places.
+    torch = gpu
+    _announce("attention coop scores", tokens, heads, batch)
+    rng = np.random.default_rng(tokens * 13 + heads + batch)
+    qkv = (rng.standard_normal((batch * tokens, 3 * heads * 64)) * 1.5).astype(np.float32)
+    _, _, scores = _attention_ref_gpu(torch, lib, qkv, tokens, heads, True, batch, coop=True)
+    d = heads * 64
+    outside = moved = several = total = 0
+    for b in range(batch):
+        rows = slice(b * tokens, (b + 1) * tokens)
+        got = scores[b * heads:(b + 1) * heads].astype(np.float16)
+        ref = oracle.scores_coop(qkv[rows], tokens, heads)
+        for h in range(heads):
+            q16 = (qkv[rows, h * 64:h * 64 + 64] * np.float32(0.125)).astype(np.float16).astype(np.float64)
+            k16 = qkv[rows, d + h * 64:d + h * 64 + 64].astype(np.float16).astype(np.float64)
+            bound = 63 * 2.0 ** -24 * (np.abs(q16) @ np.abs(k16).T)
+            step = np.spacing(np.abs(ref[h])).astype(np.float64)
+            diff = np.abs(got[h].astype(np.float64) - ref[h].astype(np.float64))
+            outside += int((diff > step + bound).sum())
+        steps = _f16_steps(got, ref)
+        moved += int((steps > 0).sum())
+        several += int((steps > 1).sum())
+        total += steps.size
+        if tokens >= 64:
+            assert (got != oracle.scores_binary16(qkv[rows], tokens, heads)).any()
+    print(f"coop scores T={tokens}: {moved} of {total} differ from the oracle ({several} by more than one "
+          f"binary16 step)", flush=True)
+    assert outside == 0
+    assert moved <= max(2, 1e-3 * total)
+
+
+@pytest.mark.parametrize("tokens,heads,batch,sigma", [(1, 1, 1, 1.0), (65, 3, 1, 1.5), (77, 3, 2, 1.5),
+                                                      (1370, 16, 2, 0.64), (1370, 16, 1, 3.0), (2240, 16, 1, 1.0)])
+def test_attention_coop_fused_matches_three_kernels(gpu, lib, tokens, heads, batch, sigma):
+    # the fused kernel issues the same two MFMAs per 16 x 16 score block as
+    # the materialised score kernel, then the binary16 softmax and values of
+    # the fused binary16 kernel: the same bits as scores + softmax + values
+    torch = gpu
+    _announce("attention coop fused vs three kernels", tokens, heads, batch, sigma)
+    rng = np.random.default_rng(tokens + 7 * heads + int(10 * sigma))
+    qkv = (rng.standard_normal((batch * tokens, 3 * heads * 64)) * sigma).astype(np.float32)
+    out = _attention_ref16_fused_gpu(torch, lib, qkv, tokens, heads, batch, coop=True)
+    ref, _, _ = _attention_ref_gpu(torch, lib, qkv, tokens, heads, True, batch, unpacked=False, coop=True)
+    assert np.isfinite(out).all()
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("tokens,heads,sigma", [(77, 4, 1.5), (1370, 16, 0.64), (1370, 16, 2.0), (5477, 2, 0.64)])
+def test_attention_coop_against_oracle(gpu, lib, oracle, tokens, heads, sigma):
+    # The whole cooperative-matrix pipeline against the oracle's mode 3 and
+    # against float64 attention. Only scores one binary16 step apart
+    # (test_attention_coop_scores) separate it from mode 3, so the outputs
+    # agree to a few binary16 steps of the values; both stay within the
+    # per-product pipeline's distance of float64 attention.
+    torch = gpu
+    _announce("attention coop vs oracle", tokens, heads, sigma)
+    rng = np.random.default_rng(tokens * 17 + heads + int(10 * sigma))
+    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * sigma).astype(np.float32)
+    if lib.dav2_hip_attention_ref16_fused_scratch_bytes(tokens, heads, 1):
+        out = _attention_ref16_fused_gpu(torch, lib, qkv, tokens, heads, coop=True)
+    else:
+        out, _, _ = _attention_ref_gpu(torch, lib, qkv, tokens, heads, True, unpacked=False, coop=True)
+    ref = oracle.attention(qkv, tokens, heads, fp16=True, coop=True)
+    per_product = oracle.attention(qkv, tokens, heads, fp16=True)
+    f64 = _attention_f64_gpu(torch, qkv, tokens, heads)
+    d = np.abs(out.astype(np.float64) - ref)
+    scale = float(np.abs(qkv[:, 2 * heads * 64:]).max())
+    e_coop, e_mode1 = np.abs(out - f64).max(), np.abs(per_product - f64).max()
+    print(f"coop vs oracle T={tokens} sigma={sigma}: max {d.max():.3g}, mean {d.mean():.3g}, "
+          f"equal {np.mean(out == ref):.4f}; max|coop - f64| {e_coop:.3g}, max|per-product - f64| {e_mode1:.3g}",
+          flush=True)
+    assert d.max() <= 4e-3 * scale
+    assert d.mean() <= 1e-5 * scale
+    assert e_coop <= 1.25 * e_mode1
 
 
 def test_attention_ref16_fused_limits(gpu, lib):

@@ -84,6 +84,56 @@ def test_depth_parity(gpu, pkg, lib, oracle, models, enc, width, height, flags):
     assert np.array_equal(depth.view(np.uint32), ref_depth.view(np.uint32))
 
 
+@pytest.mark.parametrize("enc", ["vits", "vitl"])
+def test_coop_attention_graph(gpu, pkg, lib, oracle, models, enc):
+    # DAV2_CREATE_REFERENCE_FP16_COOP_ATTENTION: the reference's int8 graph as
+    # it runs on devices with cooperative_matrix_fp16 (bmm_score_coop_fp16
+    # scores on the MFMA). The score shader leaves its fp32 sum order to the
+    # device, so the graph is held to the oracle's graph with mode-3
+    # attention (exact products) within a tolerance: a score one binary16
+    # step away moves an attention output by an ulp, which can flip an int8
+    # requantization downstream (single pixels move by up to a few percent of
+    # the logit range, as between the default and the binary16 graph), while
+    # the map as a whole moves by far less. Bounds: relative L1 <= 0.2%,
+    # largest single-pixel gap <= 3% of the logit range, against the oracle
+    # and against the per-product binary16 graph; and the reference's 1%
+    # relative L1 contract against the fp32 precision mode.
+    torch = gpu
+    width = height = 518
+    print("case: coop attention graph", enc, flush=True)
+    x = pkg.dav2_format.imagenet_input(width, height, seed=SEED + 47)[0]
+    xd = dev(torch, x)
+    logits = {}
+    for name, fl in (("coop", pkg.FORCE_INT8 | pkg.REFERENCE_FP16_COOP_ATTENTION),
+                     ("binary16", pkg.FORCE_INT8 | pkg.REFERENCE_FP16_ATTENTION), ("fp32", pkg.FORCE_FP32)):
+        d = empty(torch, (height, width), torch.float32)
+        lg = empty(torch, (height, width), torch.float32)
+        with pkg.Context(str(models[enc]), enc, fl) as ctx:
+            assert lib.dav2_infer_tensor_f32_device_logits(ctx.handle, xd.data_ptr(), width, height, d.data_ptr(),
+                                                           lg.data_ptr(), torch.cuda.current_stream().cuda_stream) == 0
+            if name == "coop":
+                assert np.array_equal(ctx.infer(x, width, height), host(torch, d))
+            logits[name] = host(torch, lg).astype(np.float64)
+    h = oracle.load_model(models[enc], ENC[enc])
+    try:
+        _, ref_logits, _ = oracle.infer(h, x, width, height, attention="coop")
+    finally:
+        oracle.free_model(h)
+
+    def gap(a, b):
+        diff = np.abs(a - b)
+        return diff.sum() / np.abs(b).sum(), diff.max() / (b.max() - b.min())
+
+    vs_oracle, vs_b16 = gap(logits["coop"], ref_logits.astype(np.float64)), gap(logits["coop"], logits["binary16"])
+    vs_fp32 = gap(logits["coop"], logits["fp32"])
+    print(f"coop graph {enc}: vs oracle rel L1 {vs_oracle[0]:.4%} max {vs_oracle[1]:.4g}; vs binary16 rel L1 "
+          f"{vs_b16[0]:.4%} max {vs_b16[1]:.4g}; vs fp32 mode rel L1 {vs_fp32[0]:.4%}", flush=True)
+    for l1, mx in (vs_oracle, vs_b16):
+        assert l1 <= 2e-3
+        assert mx <= 0.03
+    assert vs_fp32[0] < 0.01
+
+
 @pytest.mark.parametrize("enc", ["vits", "vitb", "vitl"])
 def test_int8_modes_against_fp32_mode(gpu, pkg, lib, models, enc):
     # The reference's accuracy contract (docs/architecture.md:38-47): relative

@@ -152,12 +152,22 @@ def test_attention_exact_mode_is_order_free(oracle):
 F16, F32 = np.float16, np.float32
 
 
-def _binary16_attention_numpy(oracle, qkv, tokens, heads):
-    """bmm_score_fp16.glsl, softmax_lastdim_half.glsl and bmm_value_fp16.glsl
-    written loop for loop with numpy's IEEE float16 / float32 types (one
-    query row at a time, every sum in the shaders' order). exp is the
-    oracle's exp_cw (GLSL leaves exp's precision open; exp_cw is pinned
-    against float64 in test_exp_cw_*)."""
+def _coop_scores_numpy(q16_row, k16):
+    """bmm_score_coop_fp16.glsl as the oracle states it: the exact products
+    q16 * k16 summed in float64 in feature order, rounded to float32 (the
+    accumulator's type), then to binary16."""
+    s = np.zeros(k16.shape[0], np.float64)
+    for f in range(64):
+        s = s + np.float64(q16_row[f]) * k16[:, f].astype(np.float64)
+    return s.astype(F32).astype(F16)
+
+
+def _binary16_attention_numpy(oracle, qkv, tokens, heads, coop=False):
+    """bmm_score_fp16.glsl (coop: bmm_score_coop_fp16.glsl as above),
+    softmax_lastdim_half.glsl and bmm_value_fp16.glsl written loop for loop
+    with numpy's IEEE float16 / float32 types (one query row at a time, every
+    sum in the shaders' order). exp is the oracle's exp_cw (GLSL leaves exp's
+    precision open; exp_cw is pinned against float64 in test_exp_cw_*)."""
     d = heads * 64
     out = np.zeros((tokens, d), F32)
     for h in range(heads):
@@ -165,11 +175,14 @@ def _binary16_attention_numpy(oracle, qkv, tokens, heads):
         k16 = qkv[:, d + h * 64:d + h * 64 + 64].astype(F16)
         v16 = qkv[:, 2 * d + h * 64:2 * d + h * 64 + 64].astype(F16)
         for i in range(tokens):
-            # scores: s[j] += float(q16 * k16) for features 0..63 in order
-            s = np.zeros(tokens, F32)
-            for f in range(64):
-                s = (s + (q16[i, f].astype(F32) * k16[:, f].astype(F32)).astype(F16).astype(F32)).astype(F32)
-            row = s.astype(F16).astype(F32)
+            if coop:
+                row = _coop_scores_numpy(q16[i], k16).astype(F32)
+            else:
+                # scores: s[j] += float(q16 * k16) for features 0..63 in order
+                s = np.zeros(tokens, F32)
+                for f in range(64):
+                    s = (s + (q16[i, f].astype(F32) * k16[:, f].astype(F32)).astype(F16).astype(F32)).astype(F32)
+                row = s.astype(F16).astype(F32)
             # softmax: 128 lanes over words (2w, 2w+1), then the halving tree
             m = row.max()
             e = oracle.exp((row - m).astype(F32))
@@ -246,6 +259,49 @@ def test_binary16_attention_matches_shader_restatement(oracle, tokens, heads):
     want = _binary16_attention_numpy(oracle, qkv, tokens, heads)
     got = oracle.attention(qkv, tokens, heads, fp16=True)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_coop_scores_keep_exact_products(oracle):
+    # bmm_score_coop_fp16.glsl multiplies binary16 operands without rounding
+    # the products: (1 + 2^-10)^2 - (1 + 2^-9) = 2^-20, a binary16 subnormal
+    # the stored score keeps (the per-product shader gives 0 here)
+    qkv = _qkv_with([1 + 2.0 ** -10, -1.0], [1 + 2.0 ** -10, 1 + 2.0 ** -9])
+    assert oracle.scores_coop(qkv, 2, 1)[0, 0, 1] == F16(2.0 ** -20)
+    assert oracle.scores_binary16(qkv, 2, 1)[0, 0, 1] == 0.0
+    # the sum passes through the fp32 accumulator before binary16: 1 + 2^-11
+    # + 2^-30 is 1 + 2^-11 in fp32, a binary16 tie that rounds to even (1.0);
+    # rounding the exact sum straight to binary16 would give 1 + 2^-10
+    qkv = _qkv_with([1.0, 2.0 ** -11, 2.0 ** -15], [1.0, 1.0, 2.0 ** -15])
+    assert oracle.scores_coop(qkv, 2, 1)[0, 0, 1] == F16(1.0)
+    assert np.float64(1 + 2.0 ** -11 + 2.0 ** -30).astype(F16) == F16(1 + 2.0 ** -10)
+    # the sign of a cancelling product pair: exact products cancel to 0
+    qkv = _qkv_with([3.0, -3.0], [1 + 2.0 ** -10, 1 + 2.0 ** -10])
+    assert oracle.scores_coop(qkv, 2, 1)[0, 0, 1] == 0.0
+
+
+@pytest.mark.parametrize("tokens,heads", [(5, 1), (37, 2), (129, 1)])
+def test_coop_scores_match_numpy(oracle, tokens, heads):
+    rng = np.random.default_rng(tokens * 11 + heads)
+    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * 2.0).astype(F32)
+    got = oracle.scores_coop(qkv, tokens, heads)
+    d = heads * 64
+    for h in range(heads):
+        q16 = (qkv[:, h * 64:h * 64 + 64] * F32(0.125)).astype(F16)
+        k16 = qkv[:, d + h * 64:d + h * 64 + 64].astype(F16)
+        want = np.stack([_coop_scores_numpy(q16[i], k16) for i in range(tokens)])
+        assert np.array_equal(got[h].view(np.uint16), want.view(np.uint16))
+    # scores of magnitude ~10 differ from the per-product shader's somewhere
+    assert (got != oracle.scores_binary16(qkv, tokens, heads)).any()
+
+
+@pytest.mark.parametrize("tokens,heads", [(2, 1), (37, 2), (258, 1)])
+def test_coop_attention_matches_shader_restatement(oracle, tokens, heads):
+    rng = np.random.default_rng(tokens + 300 * heads)
+    qkv = (rng.standard_normal((tokens, 3 * heads * 64)) * 1.5).astype(F32)
+    want = _binary16_attention_numpy(oracle, qkv, tokens, heads, coop=True)
+    got = oracle.attention(qkv, tokens, heads, fp16=True, coop=True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.abs(got - _attention_f64(qkv, tokens, heads)).max() <= 2e-2
 
 
 def test_binary16_attention_differs_from_exact_products(oracle):
