@@ -372,8 +372,8 @@ def main() -> int:
             return {"calls": calls_n, "median_ms": 1e3 * float(np.median(ts)),
                     "images_per_s_median": 1.0 / float(np.median(ts))}
 
-        fp32_rate = fp16_rate = ref16_rate = None
-        ref16_host = None
+        fp32_rate = fp16_rate = ref16_rate = coop_rate = None
+        ref16_host = coop_host = None
         if args.batch == 1 and not args.no_fp32_mode:
             fp32_rate = mode_rate(pkg.FORCE_FP32, 5)
             fp16_rate = mode_rate(pkg.FORCE_FP16, 5)
@@ -382,6 +382,13 @@ def main() -> int:
             ref16_host["entry"] = ("dav2_infer_tensor_f32, int8 graph with the reference's binary16 attention "
                                    "arithmetic (DAV2_CREATE_REFERENCE_FP16_ATTENTION)")
             print("bench: reference-arithmetic attention " + json.dumps(ref16_host), file=sys.stderr, flush=True)
+            coop_rate = mode_rate(pkg.REFERENCE_FP16_COOP_ATTENTION, 10)
+            coop_host = host_entry_median(pkg.REFERENCE_FP16_COOP_ATTENTION, 20)
+            coop_host["entry"] = ("dav2_infer_tensor_f32, int8 graph with the reference's binary16 attention as on "
+                                  "cooperative-matrix devices: bmm_score_coop_fp16 scores on the f16 MFMA "
+                                  "(DAV2_CREATE_REFERENCE_FP16_COOP_ATTENTION)")
+            print("bench: cooperative-matrix reference attention " + json.dumps(coop_host), file=sys.stderr,
+                  flush=True)
 
         gemm = prof.get("gemm_i8", {})
         g_ms = gemm.get("ms", 0.0)
@@ -462,11 +469,13 @@ def main() -> int:
         "device_resident_images_per_s": device_rate,
         "device_median_images_per_s": device_median,
         "reference_arithmetic_host_entry": ref16_host,
+        "reference_arithmetic_coop_host_entry": coop_host,
         "extra_configs": extra,
         "image_paths": image_paths,
         "fp32_mode_images_per_s": fp32_rate,
         "fp16_mode_images_per_s": fp16_rate,
         "reference_fp16_attention_images_per_s": ref16_rate,
+        "reference_fp16_coop_attention_images_per_s": coop_rate,
         "depth_finite": bool(np.isfinite(depth).all()),
         "cpu_baseline": cpu,
     }
