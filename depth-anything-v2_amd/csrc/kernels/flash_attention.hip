@@ -274,6 +274,8 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
     const int tid = threadIdx.x, hi4 = tid >> 2, c16 = (tid & 3) * 16;
     const uint32_t t = j0 + hi4;
 
+    // The row's values and (k, v) the first four partial maxima of the
+    // lane's column are loaded together, so that their latencies overlap.
     float x[16];
     {
         const float* src = qkv + static_cast<uint64_t>(t) * 3u * D + part * D + h * 64u + c16;
@@ -287,7 +289,32 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
             x[4 * i + 3] = v.w;
         }
     }
+    // Head maximum of |k| (part 1) or column maxima of |v| (part 2) from the
+    // partials: wave w folds row tiles w, w + 4, ...; lane = feature. The
+    // first 16 row tiles are loaded at once (indices clamped: a repeated row
+    // leaves a maximum unchanged), further ones in a loop.
+    const uint32_t f = static_cast<uint32_t>(tid & 63);
+    const float* cols = col_absmax + (part == 0 ? 0u : (part - 1u) * D) + h * 64u + f;
+    float pm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (part != 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = min(static_cast<uint32_t>(tid >> 6) + 4u * i, partial_rows - 1u);
+            pm[i] = cols[static_cast<uint64_t>(r) * 2u * D];
+        }
+    }
+    // digits of every value (a zero maximum means zero values; the select
+    // keeps NaN inputs at 0 digits there, as before)
     int8_t d1[16], d0[16];
+    auto digits_of = [&](const float (&v)[16], float maximum, int e) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int8_t a1, a0;
+            digits15(v[i], 14 - e, a1, a0);
+            d1[i] = maximum != 0.0f ? a1 : int8_t(0);
+            d0[i] = maximum != 0.0f ? a0 : int8_t(0);
+        }
+    };
     if (part == 0) {  // q * 0.125: exponent of the row maximum over the four lanes of the row
         float a = 0.0f;
 #pragma unroll
@@ -299,12 +326,7 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
         a = fmaxf(a, __shfl_xor(a, 2, kWave));
         int e = 0;
         if (a != 0.0f) frexpf(a, &e);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            d1[i] = 0;
-            d0[i] = 0;
-            if (a != 0.0f) digits15(x[i], 14 - e, d1[i], d0[i]);
-        }
+        digits_of(x, a, e);
         int8_t* p0 = qd + (static_cast<uint64_t>(h) * 2u * tp + t) * 64u + c16;
         store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
         if ((tid & 3) == 0) qe[static_cast<uint64_t>(h) * tp + t] = a != 0.0f ? e - 14 : 0;
@@ -314,19 +336,7 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
 #pragma unroll
         for (int i = 0; i < 16; ++i) tile[hi4][c16 + i] = x[i];
     }
-    // Head maximum of |k| (part 1) or column maxima of |v| (part 2) from the
-    // partials: wave w folds row tiles w, w + 4, ...; lane = feature. The
-    // first 16 row tiles are loaded at once (indices clamped: a repeated row
-    // leaves a maximum unchanged), further ones in a loop.
     {
-        const uint32_t f = static_cast<uint32_t>(tid & 63);
-        const float* cols = col_absmax + (part - 1u) * D + h * 64u + f;
-        float pm[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = min(static_cast<uint32_t>(tid >> 6) + 4u * i, partial_rows - 1u);
-            pm[i] = cols[static_cast<uint64_t>(r) * 2u * D];
-        }
         float m = fmaxf(fmaxf(pm[0], pm[1]), fmaxf(pm[2], pm[3]));
         for (uint32_t r = static_cast<uint32_t>(tid >> 6) + 16u; r < partial_rows; r += 4u)
             m = fmaxf(m, cols[static_cast<uint64_t>(r) * 2u * D]);
@@ -338,27 +348,20 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
         const float a = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
         int e = 0;
         if (a != 0.0f) frexpf(a, &e);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            d1[i] = 0;
-            d0[i] = 0;
-            if (a != 0.0f) digits15(x[i], 14 - e, d1[i], d0[i]);
-        }
+        digits_of(x, a, e);
         int8_t* p0 = kd + (static_cast<uint64_t>(h) * 2u * tp + t) * 64u + c16;
         store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
         if (blockIdx.x == 0 && tid == 0) ke[h] = a != 0.0f ? e - 14 : 0;
         return;
     }
-    {  // v: feature hi4, block positions c16..c16+15
+    {  // v: feature hi4, block positions c16..c16+15 (all 16 read before use)
         const float mv = fmaxf(fmaxf(red[0][hi4], red[1][hi4]), fmaxf(red[2][hi4], red[3][hi4]));
         int e = 0;
         if (mv != 0.0f) frexpf(mv, &e);
+        float vv[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            d1[i] = 0;
-            d0[i] = 0;
-            if (mv != 0.0f) digits15(tile[perm64(c16 + i)][hi4], 14 - e, d1[i], d0[i]);
-        }
+        for (int i = 0; i < 16; ++i) vv[i] = tile[perm64(c16 + i)][hi4];
+        digits_of(vv, mv, e);
         int8_t* p0 = vd + (static_cast<uint64_t>(h) * 2u * 64u + hi4) * tp + j0 + c16;
         store_digits16(p0 + static_cast<uint64_t>(tp) * 64u, p0, d1, d0);
         if (blockIdx.x == 0 && (tid & 3) == 0) ve[static_cast<uint64_t>(h) * 64u + hi4] = mv != 0.0f ? e - 14 : 0;
