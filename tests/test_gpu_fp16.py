@@ -138,11 +138,15 @@ def _span_err(got, ref):
 
 @pytest.mark.parametrize("enc,width,height,attention", [
     ("vits", 266, 266, "binary16"), ("vits", 350, 266, "binary16"), ("vits", 266, 266, "fp32"),
-    ("vitb", 196, 252, "binary16"), ("vitl", 518, 518, "binary16")])
+    ("vitb", 196, 252, "binary16"), ("vitl", 518, 518, "binary16"), ("vits", 350, 266, "coop"),
+    ("vitl", 518, 518, "coop")])
 def test_fp16_mode_depth_parity(gpu, pkg, lib, oracle, models, enc, width, height, attention):
+    # coop: the fp16 mode with the cooperative-matrix score shader
+    # (REFERENCE_FP16_COOP_ATTENTION) against the oracle's fp16 graph with
+    # mode-3 attention, the same 1e-3 bound
     torch = gpu
     _announce("fp16 model", enc, width, height, attention)
-    flags = pkg.FORCE_FP16 | (pkg.FORCE_FP32_ATTENTION if attention == "fp32" else 0)
+    flags = pkg.FORCE_FP16 | {"fp32": pkg.FORCE_FP32_ATTENTION, "coop": pkg.REFERENCE_FP16_COOP_ATTENTION}.get(attention, 0)
     x = pkg.dav2_format.imagenet_input(width, height, seed=SEED + width + 1)[0]
     with pkg.Context(str(models[enc]), enc, flags) as ctx:
         depth = ctx.infer(x, width, height)

@@ -325,8 +325,13 @@ def test_conv2d_i8_group_maxima(gpu, pkg, lib, oracle, k, n, relu_in, emit):
     assert conv(got, fl | 4) != 0
 
 
-@pytest.mark.parametrize("c,ih,iw,oh,ow", [(128, 296, 296, 518, 518), (256, 37, 37, 74, 74), (32, 5, 7, 9, 13)])
+@pytest.mark.parametrize("c,ih,iw,oh,ow", [(128, 296, 296, 518, 518), (256, 37, 37, 74, 74), (32, 5, 7, 9, 13),
+                                           (64, 148, 148, 296, 296), (32, 19, 19, 37, 37), (32, 9, 13, 17, 25),
+                                           (32, 10, 10, 10, 10), (32, 1, 1, 5, 3), (32, 7, 3, 7, 200),
+                                           (32, 40, 40, 20, 20), (32, 30, 5, 7, 50)])
 def test_bilinear_maxima(gpu, lib, c, ih, iw, oh, ow):
+    # the 32-channel resize with maxima: the same bits as the plain resize
+    # (up- and downsampling, ragged tiles, one-pixel sources)
     torch = gpu
     _announce("bilinear maxima", c, ih, iw, oh, ow)
     x = np.random.default_rng(c + oh).standard_normal((c, ih, iw)).astype(np.float32)
