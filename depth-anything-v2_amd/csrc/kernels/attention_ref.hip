@@ -431,6 +431,67 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
     }
 }
 
+// fp32 softmax of long rows, in place: one workgroup of NT threads per row,
+// thread t holding items t + NT j (J of them), so that each thread moves few
+// bytes and a row's loads are spread over NT / 64 waves (a row held by one
+// or two waves keeps too few rows in flight per byte: T = 1370, 175360 rows:
+// 0.59 -> 0.68 of 8 TB/s; T = 5477: 0.51 -> 0.67). The maximum is
+// order-free. The shader's sums are not: lane L adds items L, L + 128, ...
+// in order, so the exponentials go to LDS and threads 0..127 run those 128
+// chains from there, then the stride-64 step and the in-wave halving tree
+// as in ref_softmax_kernel; the exponentials stay in registers for the
+// final products.
+template <int NT, int J>
+__global__ __launch_bounds__(NT) void ref_softmax_spread_kernel(float* __restrict__ data, uint32_t columns) {
+    static_assert(NT % 64 == 0 && NT >= 128, "whole waves, at least the shader's 128 lanes");
+    extern __shared__ float exps[];  // [columns]
+    __shared__ float wave_maxima[NT / 64];
+    __shared__ float upper[64];      // lanes 64..127's partial sums
+    __shared__ float inverse_lds;
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    float* row = data + static_cast<uint64_t>(blockIdx.x) * columns;
+    float v[J];
+    const uint32_t last = columns - 1u;
+    // clamped indices: every load issued before the first use
+#pragma unroll
+    for (int j = 0; j < J; ++j) v[j] = row[min(t + NT * j, last)];
+    float maximum = -3.402823466e+38f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) maximum = t + NT * j < columns ? fmaxf(maximum, v[j]) : maximum;
+    maximum = wave_max(maximum);
+    if (lane == 0) wave_maxima[wave] = maximum;
+    __syncthreads();
+    maximum = wave_maxima[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) maximum = fmaxf(maximum, wave_maxima[w]);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t c = t + NT * j;
+        if (c < columns) {
+            v[j] = exp_cw(v[j] - maximum);
+            exps[c] = v[j];
+        }
+    }
+    __syncthreads();
+    float partial = 0.0f;  // softmax_lastdim.glsl:45-55, lane t's chain
+    if (t < 128u) {
+        for (uint32_t c = t; c < columns; c += 128u) partial = partial + exps[c];
+        if (t >= 64u) upper[t - 64u] = partial;
+    }
+    __syncthreads();
+    if (t < 64u) {
+        const float sum = wave_sum_tree(partial + upper[t]);  // strides 64, then 32 .. 1
+        if (t == 0) inverse_lds = div_rn(1.0f, fmaxf(sum, 1.0e-20f));
+    }
+    __syncthreads();
+    const float inverse = inverse_lds;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t c = t + NT * j;
+        if (c < columns) row[c] = v[j] * inverse;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Values. Thread (tx, ty) of 16 x 16 owns queries ty*4 .. +3 and features
 // tx*4 .. +3 of a 64 x 64 tile; the source tokens advance in chunks of 32,
@@ -851,7 +912,23 @@ hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream
     // (rows of an even number of items on an 8-byte aligned buffer: pairs
     // of adjacent items per thread)
     const bool pairs = items % 2u == 0u && (reinterpret_cast<uintptr_t>(data) & 7u) == 0u;
-#define DAV2_SOFTMAX_CASE(N, V)                                                                        \
+    // fp32 rows of 961 .. 11264 items: a workgroup per row (256 threads up
+    // to 3072 items, 512 beyond; measured best at 1370 and 5477). Fraction of
+    // 8 TB/s against the kernel below, at 1000 / 1370 / 2000 / 5477 / 8000
+    // items: 0.72 / 0.72 / 0.69 / 0.67 / 0.66 against 0.62 / 0.60 / 0.48 /
+    // 0.51 / 0.23; rows of 300-700 items measured faster below.
+    if (!HALF && items > 960u && items <= 11264u && rows <= 0x7fffffffu) {
+        const dim3 one_row(static_cast<uint32_t>(rows));
+        const size_t lds = static_cast<size_t>(items) * sizeof(float);
+        float* f = static_cast<float*>(data);
+        if (items <= 1024u) dispatch((ref_softmax_spread_kernel<256, 4>), one_row, dim3(256), lds, s, f, columns);
+        else if (items <= 1536u) dispatch((ref_softmax_spread_kernel<256, 6>), one_row, dim3(256), lds, s, f, columns);
+        else if (items <= 3072u) dispatch((ref_softmax_spread_kernel<256, 12>), one_row, dim3(256), lds, s, f, columns);
+        else if (items <= 5632u) dispatch((ref_softmax_spread_kernel<512, 11>), one_row, dim3(512), lds, s, f, columns);
+        else dispatch((ref_softmax_spread_kernel<512, 22>), one_row, dim3(512), lds, s, f, columns);
+        return hipGetLastError();
+    }
+#define DAV2_SOFTMAX_CASE(N, V)                                                                     \
     if (per_lane <= N) {                                                                               \
         if (V == 2 && pairs)                                                                           \
             dispatch((ref_softmax_kernel<N, HALF, V, V == 2>), grid, block, 0, s, data, rows, columns); \

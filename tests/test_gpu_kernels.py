@@ -1136,7 +1136,9 @@ def test_softmax_fp32_buffer_off_8_bytes(gpu, lib, oracle):
 
 
 @pytest.mark.parametrize("rows,cols", [(16 * 1370, 1370), (7, 5477), (3, 64), (5, 9000), (4, 6144), (2, 1),
-                                       (3, 2500), (1, 1537), (5, 2), (3, 130), (6, 1024), (9, 1536), (4, 1000)])
+                                       (3, 2500), (1, 1537), (5, 2), (3, 130), (6, 1024), (9, 1536), (4, 1000),
+                                       (3, 1025), (2, 3072), (2, 3073), (2, 5632), (2, 5633), (2, 11264),
+                                       (2, 11265), (64 * 5477, 5477), (5, 961), (3, 960), (4, 700)])
 def test_softmax_fp32(gpu, lib, oracle, rows, cols):
     # softmax_lastdim.glsl in its lane/tree order: bit for bit (register and
     # streaming forms); the matrix-core path's row softmax within tolerance
