@@ -431,33 +431,55 @@ __global__ __launch_bounds__(256) void ref_softmax_kernel(void* data, uint64_t r
     }
 }
 
-// fp32 softmax of long rows, in place: one workgroup of NT threads per row,
-// thread t holding items t + NT j (J of them), so that each thread moves few
-// bytes and a row's loads are spread over NT / 64 waves (a row held by one
-// or two waves keeps too few rows in flight per byte: T = 1370, 175360 rows:
+// Softmax of long rows, in place: one workgroup of NT threads per row,
+// thread t holding items t + NT j (J of them: columns in fp32, packed words
+// of two binary16 values with HALF), so that each thread moves few bytes and
+// a row's loads are spread over NT / 64 waves (a row held by one or two
+// waves keeps too few rows in flight per byte: fp32, T = 1370, 175360 rows:
 // 0.59 -> 0.68 of 8 TB/s; T = 5477: 0.51 -> 0.67). The maximum is
-// order-free. The shader's sums are not: lane L adds items L, L + 128, ...
-// in order, so the exponentials go to LDS and threads 0..127 run those 128
-// chains from there, then the stride-64 step and the in-wave halving tree
-// as in ref_softmax_kernel; the exponentials stay in registers for the
-// final products.
-template <int NT, int J>
-__global__ __launch_bounds__(NT) void ref_softmax_spread_kernel(float* __restrict__ data, uint32_t columns) {
+// order-free. The shader's sums are not: lane L adds the exponentials of
+// items L, L + 128, ... in order (binary16: each word's two exponentials
+// added first, softmax_lastdim_half.glsl:48-49), so those per-item terms go
+// to LDS and threads 0..127 run the 128 chains from there, then the
+// stride-64 step and the in-wave halving tree as in ref_softmax_kernel; the
+// exponentials stay in registers for the final products.
+template <int NT, int J, bool HALF>
+__global__ __launch_bounds__(NT) void ref_softmax_spread_kernel(void* __restrict__ data, uint32_t columns) {
     static_assert(NT % 64 == 0 && NT >= 128, "whole waves, at least the shader's 128 lanes");
-    extern __shared__ float exps[];  // [columns]
+    extern __shared__ float terms[];  // [items]
     __shared__ float wave_maxima[NT / 64];
-    __shared__ float upper[64];      // lanes 64..127's partial sums
+    __shared__ float upper[64];       // lanes 64..127's partial sums
     __shared__ float inverse_lds;
     const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    float* row = data + static_cast<uint64_t>(blockIdx.x) * columns;
-    float v[J];
-    const uint32_t last = columns - 1u;
+    const uint32_t items = HALF ? (columns + 1u) >> 1 : columns;
+    float* frow = HALF ? nullptr : static_cast<float*>(data) + static_cast<uint64_t>(blockIdx.x) * items;
+    uint32_t* wrow = HALF ? static_cast<uint32_t*>(data) + static_cast<uint64_t>(blockIdx.x) * items : nullptr;
+    float lo[J], hi[J];  // hi: a word's upper half (binary16)
+    const uint32_t last = items - 1u;
     // clamped indices: every load issued before the first use
 #pragma unroll
-    for (int j = 0; j < J; ++j) v[j] = row[min(t + NT * j, last)];
+    for (int j = 0; j < J; ++j) {
+        const uint32_t item = min(t + NT * j, last);
+        if (HALF) {
+            const uint32_t w = wrow[item];
+            lo[j] = half_lo(w);
+            hi[j] = half_hi(w);
+        } else {
+            lo[j] = frow[item];
+            hi[j] = 0.0f;
+        }
+    }
+    // a word's upper half counts unless it pads an odd row
+    auto has_hi = [&](uint32_t item) { return HALF && item * 2u + 1u < columns; };
     float maximum = -3.402823466e+38f;
 #pragma unroll
-    for (int j = 0; j < J; ++j) maximum = t + NT * j < columns ? fmaxf(maximum, v[j]) : maximum;
+    for (int j = 0; j < J; ++j) {
+        const uint32_t item = t + NT * j;
+        if (item < items) {
+            maximum = fmaxf(maximum, lo[j]);
+            if (has_hi(item)) maximum = fmaxf(maximum, hi[j]);
+        }
+    }
     maximum = wave_max(maximum);
     if (lane == 0) wave_maxima[wave] = maximum;
     __syncthreads();
@@ -466,16 +488,17 @@ __global__ __launch_bounds__(NT) void ref_softmax_spread_kernel(float* __restric
     for (int w = 1; w < NT / 64; ++w) maximum = fmaxf(maximum, wave_maxima[w]);
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t c = t + NT * j;
-        if (c < columns) {
-            v[j] = exp_cw(v[j] - maximum);
-            exps[c] = v[j];
+        const uint32_t item = t + NT * j;
+        if (item < items) {
+            lo[j] = exp_cw(lo[j] - maximum);
+            hi[j] = has_hi(item) ? exp_cw(hi[j] - maximum) : 0.0f;
+            terms[item] = HALF ? lo[j] + hi[j] : lo[j];
         }
     }
     __syncthreads();
-    float partial = 0.0f;  // softmax_lastdim.glsl:45-55, lane t's chain
+    float partial = 0.0f;  // lane t's chain (softmax_lastdim.glsl:45-55, _half.glsl:41-50)
     if (t < 128u) {
-        for (uint32_t c = t; c < columns; c += 128u) partial = partial + exps[c];
+        for (uint32_t item = t; item < items; item += 128u) partial = partial + terms[item];
         if (t >= 64u) upper[t - 64u] = partial;
     }
     __syncthreads();
@@ -487,8 +510,16 @@ __global__ __launch_bounds__(NT) void ref_softmax_spread_kernel(float* __restric
     const float inverse = inverse_lds;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t c = t + NT * j;
-        if (c < columns) row[c] = v[j] * inverse;
+        const uint32_t item = t + NT * j;
+        if (item >= items) continue;
+        if (HALF) {
+            // p = fp16(float(fp16(e)) * inverse): the stored exponentials are fp16(e)
+            const float pa = static_cast<float>(static_cast<_Float16>(lo[j])) * inverse;
+            const float pb = static_cast<float>(static_cast<_Float16>(hi[j])) * inverse;
+            wrow[item] = pack_half2(pa, pb);
+        } else {
+            frow[item] = lo[j] * inverse;
+        }
     }
 }
 
@@ -912,20 +943,22 @@ hipError_t launch_softmax(void* data, uint64_t rows, uint32_t columns, hipStream
     // (rows of an even number of items on an 8-byte aligned buffer: pairs
     // of adjacent items per thread)
     const bool pairs = items % 2u == 0u && (reinterpret_cast<uintptr_t>(data) & 7u) == 0u;
-    // fp32 rows of 961 .. 11264 items: a workgroup per row (256 threads up
-    // to 3072 items, 512 beyond; measured best at 1370 and 5477). Fraction of
-    // 8 TB/s against the kernel below, at 1000 / 1370 / 2000 / 5477 / 8000
-    // items: 0.72 / 0.72 / 0.69 / 0.67 / 0.66 against 0.62 / 0.60 / 0.48 /
-    // 0.51 / 0.23; rows of 300-700 items measured faster below.
-    if (!HALF && items > 960u && items <= 11264u && rows <= 0x7fffffffu) {
+    // Rows of 961 .. 11264 fp32 columns or 1537 .. 5632 binary16 words: a
+    // workgroup per row (256 threads up to 3072 items, 512 beyond; measured
+    // best at 1370 and 5477). Fraction of 8 TB/s against the kernels below,
+    // fp32 rows of 1000 / 1370 / 2000 / 5477 / 8000 items: 0.72 / 0.72 / 0.69
+    // / 0.67 / 0.66 against 0.62 / 0.60 / 0.48 / 0.51 / 0.23 (rows of 300-700
+    // items measured faster below); binary16 rows of 2739 / 3100 / 5500
+    // words: 0.60 / 0.51 / 0.64 against 0.31 / 0.26 / 0.27 (1000 words: 0.50
+    // against 0.57 below).
+    if (items > (HALF ? 1536u : 960u) && items <= (HALF ? 5632u : 11264u) && rows <= 0x7fffffffu) {
         const dim3 one_row(static_cast<uint32_t>(rows));
         const size_t lds = static_cast<size_t>(items) * sizeof(float);
-        float* f = static_cast<float*>(data);
-        if (items <= 1024u) dispatch((ref_softmax_spread_kernel<256, 4>), one_row, dim3(256), lds, s, f, columns);
-        else if (items <= 1536u) dispatch((ref_softmax_spread_kernel<256, 6>), one_row, dim3(256), lds, s, f, columns);
-        else if (items <= 3072u) dispatch((ref_softmax_spread_kernel<256, 12>), one_row, dim3(256), lds, s, f, columns);
-        else if (items <= 5632u) dispatch((ref_softmax_spread_kernel<512, 11>), one_row, dim3(512), lds, s, f, columns);
-        else dispatch((ref_softmax_spread_kernel<512, 22>), one_row, dim3(512), lds, s, f, columns);
+        if (items <= 1024u) dispatch((ref_softmax_spread_kernel<256, 4, HALF>), one_row, dim3(256), lds, s, data, columns);
+        else if (items <= 1536u) dispatch((ref_softmax_spread_kernel<256, 6, HALF>), one_row, dim3(256), lds, s, data, columns);
+        else if (items <= 3072u) dispatch((ref_softmax_spread_kernel<256, 12, HALF>), one_row, dim3(256), lds, s, data, columns);
+        else if (items <= 5632u) dispatch((ref_softmax_spread_kernel<512, 11, HALF>), one_row, dim3(512), lds, s, data, columns);
+        else dispatch((ref_softmax_spread_kernel<512, 22, HALF>), one_row, dim3(512), lds, s, data, columns);
         return hipGetLastError();
     }
 #define DAV2_SOFTMAX_CASE(N, V)                                                                     \

@@ -747,7 +747,8 @@ def test_attention_ref_fp32_bit_exact(gpu, lib, oracle, tokens, heads, batch):
 
 @pytest.mark.parametrize("tokens,heads,batch", [(1, 1, 1), (2, 1, 1), (5, 2, 1), (77, 4, 1), (258, 2, 2),
                                                 (1369, 3, 1), (1370, 16, 1), (3101, 1, 1), (6200, 1, 1),
-                                                (100, 2, 1), (1500, 1, 1)])
+                                                (100, 2, 1), (1500, 1, 1), (3073, 1, 1), (3074, 2, 1),
+                                                (5477, 1, 1)])
 def test_attention_ref_fp16_bit_exact(gpu, lib, oracle, tokens, heads, batch):
     # bmm_score_fp16 + softmax_lastdim_half + bmm_value_fp16 (mode 1 of the
     # oracle: every product rounded to binary16), bit for bit: the binary16
