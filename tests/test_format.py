@@ -141,3 +141,41 @@ def test_oracle_rejects_bad_crc(oracle, pkg, tmp_path):
     path.write_bytes(bytes(data))
     with pytest.raises(RuntimeError, match="crc"):
         oracle.load_model(path, 0)
+
+
+def test_mutated_files_match_reference_loader(pkg, lib, ref_lib, tmp_path):
+    # Differential check of the header / index parser: 400 seeded mutations of
+    # the metadata fixtures (bit flips, truncations, 32- and 64-bit boundary
+    # values at aligned offsets, appended bytes); this build's verdict and
+    # message equal the reference loader's (src/model.cpp) on every one.
+    import random
+    rng = random.Random(20261202)
+    fixtures = sorted(GOLDEN.glob("*.dav2"))
+    verdicts = {"accept": 0, "reject": 0}
+    for it in range(400):
+        b = bytearray(rng.choice(fixtures).read_bytes())
+        kind = it % 5
+        if kind == 0:
+            for _ in range(rng.randint(1, 4)):
+                i = rng.randrange(len(b))
+                b[i] ^= 1 << rng.randrange(8)
+        elif kind == 1:
+            b = b[:rng.randrange(len(b))]
+        elif kind == 2:
+            i = rng.randrange(0, len(b) - 4) & ~3
+            b[i:i + 4] = struct.pack("<I", rng.choice([0, 1, 0x7FFFFFFF, 0x80000000, 0xFFFFFFFF, len(b), 64, 4096]))
+        elif kind == 3:
+            i = rng.randrange(0, len(b) - 8) & ~7
+            b[i:i + 8] = struct.pack("<Q", rng.choice([0, 1, 2**63, 2**64 - 1, len(b), 2**32, 2**40]))
+        else:
+            b += bytes(rng.randrange(256) for _ in range(rng.randint(1, 64)))
+        path = tmp_path / f"mutated_{it % 4}.dav2"
+        path.write_bytes(bytes(b))
+        rc, msg, *_ = ref_verdict(ref_lib, path)
+        want = "accept" if rc == 0 else "reject"
+        got, why = our_verdict(pkg, lib, path)
+        assert got == want, (it, kind, msg, why)
+        if want == "reject":
+            assert why == msg, (it, kind)
+        verdicts[want] += 1
+    assert verdicts["accept"] > 20 and verdicts["reject"] > 200
