@@ -383,12 +383,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
             }
             float* dst = g.out + (static_cast<uint64_t>(row) + g.out_row_offset) * g.n + col;
             if (col + 3 < g.rows_q) {
-                // Nontemporal (ViT-L qkv at batch 1: 13.3 -> 11.4 us), except
-                // the LayerScale residual stream, which the LayerNorm that
-                // follows reads back: kept in the caches there (batch 1:
-                // LayerNorm+quantize 5.5 -> 5.0 us, fc2 19.3 -> 18.6, proj
-                // 7.7 -> 8.2; the pass 0.2% faster).
-                if constexpr (EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE)
+                // Nontemporal (nothing left in L2 to write back when the
+                // kernel ends), except where the next kernel reads the
+                // output straight back and gains more from finding it in
+                // the caches than the GEMM loses: the LayerScale residual
+                // stream (LayerNorm+quantize 5.5 -> 5.0 us, fc2 19.3 ->
+                // 18.6, proj 7.7 -> 8.2 at batch 1; pass +0.2%) and the
+                // batch-1 qkv with column maxima (digit packing + attention
+                // 53.0 -> 51.6 us, the GEMM unchanged; pass +0.5%). fc1's
+                // GELU output stays nontemporal (plain: fc1 +1.5 us against
+                // -0.7 us for the row quantizer).
+                if constexpr (EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE || EPI == DAV2_GEMM_EPI_ROW_COLMAX)
                     *reinterpret_cast<float4*>(dst) = v;
                 else
                     store_nt(dst, v);
