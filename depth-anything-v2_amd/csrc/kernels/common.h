@@ -201,11 +201,12 @@ DAV2_DEV float gelu_erfcc(float value) {
     return 0.5f * value * (1.0f + erf_value);
 }
 
-// Nontemporal store for an output that the next kernel reads: it goes
-// straight to memory instead of waiting in this XCD's L2 for the write-back
-// at the kernel's end. (Measured per kernel: it helps the GEMM's row-major
-// outputs, and slows the convolutions and the resize, whose consumers read
-// part of their output back through the same L2.)
+// Nontemporal store: the data goes straight to memory instead of waiting in
+// this XCD's L2 for the write-back at the kernel's end. It speeds up the
+// storing kernel and slows a consumer that would have found the data in the
+// caches; measured per use, it pays only for fc1's GELU output at batch 1
+// (the GEMM's other row-major outputs, the convolutions and the resize keep
+// plain stores).
 DAV2_DEV void store_nt(float* dst, float4 v) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     __builtin_nontemporal_store(f4{v.x, v.y, v.z, v.w}, reinterpret_cast<f4*>(dst));

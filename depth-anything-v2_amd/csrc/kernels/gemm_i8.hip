@@ -45,6 +45,7 @@ struct GemmParams {
     const float* gamma;
     uint32_t convt_k, convt_w, convt_h, convt_c;
     uint32_t coalesced_out;  // row-major output rows 16-byte aligned (n % 4 == 0, out aligned)
+    uint32_t nontemporal_out;  // coalesced row-major stores bypass the caches (see the store)
     float* col_absmax;       // ROW_COLMAX partial maxima [row tile][n - col_absmax_begin]
     uint32_t col_absmax_begin;
     uint32_t relu_output;    // TRANSPOSED: max(out, 0) after the residual
@@ -383,20 +384,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
             }
             float* dst = g.out + (static_cast<uint64_t>(row) + g.out_row_offset) * g.n + col;
             if (col + 3 < g.rows_q) {
-                // Nontemporal (nothing left in L2 to write back when the
-                // kernel ends), except where the next kernel reads the
-                // output straight back and gains more from finding it in
-                // the caches than the GEMM loses: the LayerScale residual
-                // stream (LayerNorm+quantize 5.5 -> 5.0 us, fc2 19.3 ->
-                // 18.6, proj 7.7 -> 8.2 at batch 1; pass +0.2%) and the
-                // batch-1 qkv with column maxima (digit packing + attention
-                // 53.0 -> 51.6 us, the GEMM unchanged; pass +0.5%). fc1's
-                // GELU output stays nontemporal (plain: fc1 +1.5 us against
-                // -0.7 us for the row quantizer).
-                if constexpr (EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE || EPI == DAV2_GEMM_EPI_ROW_COLMAX)
-                    *reinterpret_cast<float4*>(dst) = v;
-                else
+                if (g.nontemporal_out)
                     store_nt(dst, v);
+                else
+                    *reinterpret_cast<float4*>(dst) = v;
             } else {
                 if (col < g.rows_q) dst[0] = v.x;
                 if (col + 1 < g.rows_q) dst[1] = v.y;
@@ -620,6 +611,17 @@ int gemm_i8(const dav2_gemm_i8_args* a, void* stream) {
     g.convt_h = a->convt_height;
     g.convt_c = a->convt_channels;
     g.coalesced_out = !swapped && a->n % 4 == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0;
+    // The next kernel reads a row-major output straight back (LayerNorm the
+    // LayerScale residual stream, the digit packing qkv, the row quantizer
+    // fc1's GELU output), and finding it in the caches gains it more than
+    // the GEMM's own nontemporal stores would (nothing left in L2 to write
+    // back at the kernel's end). Measured, same-process A/Bs: batch 1,
+    // LayerScale +0.2% and qkv with column maxima +0.5% per pass; batch 8,
+    // every row-major output +1.0% (digit packing + attention -11 us, row
+    // quantizer -1.8 us); except fc1's GELU output below 4096 rows (batch
+    // 1: fc1 +1.5 us against -0.7 us for the row quantizer), kept
+    // nontemporal.
+    g.nontemporal_out = e == DAV2_GEMM_EPI_ROW_GELU && a->m < 4096u;
     g.col_absmax = a->col_absmax;
     g.col_absmax_begin = a->col_absmax_begin;
     g.relu_output = a->relu_output;
