@@ -228,10 +228,11 @@ void HipOperators::linear_int8_packed(DeviceBuffer& output, const DeviceBuffer& 
     if (output_transposed) {
         // Few output tiles (the DPT's 37x37 / 19x19 maps): split K so that
         // about 384 workgroups run, each slice at least six 128-byte stages.
-        // Measured per shape (M x N x K, us, split 1 / old rule / this rule):
-        // 1369x512x1024 7.8 / 11.5 / 7.8, 1369x256x9216 32.7 / 18.0 / 15.7,
-        // 361x1024x9216 33.8 / 18.9 / 17.3, 361x256x2304 11.3 / 8.8 / 8.4;
-        // the int32 partial sums make every split bit-identical.
+        // Measured per shape (M x N x K, us: unsplit / about 256 workgroups
+        // with two-stage slices / this rule): 1369x512x1024 7.8 / 11.5 / 7.8,
+        // 1369x256x9216 32.7 / 18.0 / 15.7, 361x1024x9216 33.8 / 18.9 / 17.3,
+        // 361x256x2304 11.3 / 8.8 / 8.4; the int32 partial sums make every
+        // split bit-identical.
         const std::uint32_t tiles = ((output_columns + 63) / 64) * ((rows + 63) / 64);
         const std::uint32_t ksteps = (a.k + 127) / 128;
         const std::uint32_t split = std::min({8u, (384u + tiles - 1) / tiles, ksteps / 6});
