@@ -456,6 +456,170 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_kernel(GemmPar
 // one dav2_hip_gemm_i8 call, cleared when that call returns.
 thread_local bool t_events_for_one_gemm = false;
 
+// Long-K row-major GEMMs of many rows (fc2 at batch 8: 10960 x 1024 x 4096)
+// on v_mfma_i32_32x32x32_i8, whose operand fragments carry half the LDS bytes
+// per operation of the 16x16x64 form. Lane l holds row l % 32 of each operand
+// with K bytes 16 (l / 32) .. + 15; result register r is row 8 (r / 4) +
+// 4 (l / 32) + r % 4 of column l % 32 (checked on gfx950 with a one-wave
+// probe). BM x 256 tiles (BM 256 or 192) on BM / 16 waves (BM / 64 x 4,
+// each 64 x 64 as 2 x 2 blocks of 32 x 32), the same XCD-banded tile order
+// and global -> LDS stage ring (two 128-byte stages) as gemm_i8_kernel; K a
+// multiple of 128.
+// Epilogues ROW and ROW_LAYERSCALE with gemm_i8_kernel's arithmetic. Each
+// wave stages its int32 sums in LDS, 32 rows at a time, and reads them back
+// row-major, so that one a_scale per row and float4 column operands
+// dequantize them and the residual loads and stores are 256-byte row pieces
+// (16 lanes x float4): output rows (and the residual's) 16-byte aligned.
+typedef int v16i __attribute__((ext_vector_type(16)));
+constexpr int kWideBN = 256;
+constexpr int kWideOutStride = 72;  // int32 per staged row: rows 4 apart start 32 banks apart
+
+template <int BM>
+constexpr size_t wide_lds() {
+    constexpr size_t ring = 2u * (BM + kWideBN) * 128u;
+    constexpr size_t out = static_cast<size_t>(BM / 16) * 32u * kWideOutStride * 4u;
+    return ring > out ? ring : out;
+}
+
+template <int BM, int EPI>
+__global__ __launch_bounds__(4 * BM) void gemm_i8_wide_kernel(GemmParams g) {
+    static_assert(EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE, "row-major epilogues");
+    static_assert(BM % 64 == 0 && wide_lds<BM>() <= 160u * 1024u, "64-row waves, LDS per CU");
+    constexpr int BK = 128, CPR = BK / 16, RPL = 1024 / BK, STAGES = 2;
+    constexpr int NW = BM / 16, WAVES_N = 4, WM = 64, WN = 64, TM = WM / 32, TN = WN / 32;
+    constexpr int COPIES = (BM + kWideBN) / RPL;  // 1 KiB global -> LDS copies per stage
+    constexpr int LPW = (COPIES + NW - 1) / NW;  // copy i * NW + wave of each stage, if < COPIES
+    constexpr int STAGE_BYTES = (BM + kWideBN) * BK;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    uint32_t tm, tn;
+    tile_of(tm, tn);
+    const uint32_t row0 = tm * BM, col0 = tn * kWideBN;
+    const int ksteps = static_cast<int>(g.k / BK);
+    const int8_t* src[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+        const int copy = min(i * NW + wave, COPIES - 1);  // uniform per wave
+        const uint32_t srow = RPL * copy + lane / CPR;  // stage row
+        const uint32_t chunk = ((lane % CPR) ^ ((srow / (256 / BK)) & (CPR - 1))) * 16u;
+        if (srow < static_cast<uint32_t>(BM))  // uniform per instruction
+            src[i] = g.p + min(row0 + srow, g.rows_p - 1) * g.ldp + chunk;
+        else
+            src[i] = g.q + min(col0 + srow - BM, g.rows_q - 1) * g.ldq + chunk;
+    }
+    auto issue = [&](int ks) {
+#pragma unroll
+        for (int i = 0; i < LPW; ++i)
+            if (i * NW + wave < COPIES)
+                copy16_to_lds(src[i] + static_cast<uint32_t>(ks) * BK,
+                              smem + (ks % STAGES) * STAGE_BYTES + (i * NW + wave) * 1024);
+    };
+    v16i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = v16i{};
+    issue(0);
+    const int fr = lane & 31, fc = lane >> 5;
+    for (int ks = 0; ks < ksteps; ++ks) {
+        DAV2_WAIT_VMCNT(0);  // stage ks (the only one in flight)
+        __builtin_amdgcn_s_barrier();  // every wave's copies of it have landed; the other slot is free
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + 1 < ksteps) issue(ks + 1);
+        const int8_t* st = smem + (ks % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk) {
+            v4i af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                af[i] = *reinterpret_cast<const v4i*>(st + swz<BK>(wm * WM + i * 32 + fr, kk * 2 + fc));
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                bf[j] = *reinterpret_cast<const v4i*>(st + swz<BK>(BM + wn * WN + j * 32 + fr, kk * 2 + fc));
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // every wave is done with the last stage's operands
+    int32_t* stage = reinterpret_cast<int32_t*>(smem) + wave * (32 * kWideOutStride);
+    const int c4 = (lane & 15) * 4;
+    const uint32_t col = col0 + wn * WN + c4;
+    float s_w[4], b[4], gam[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t c = min(col + e, g.rows_q - 1);
+        s_w[e] = g.b_scales[c];
+        b[e] = g.bias ? g.bias[c] : 0.0f;
+        gam[e] = EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE ? g.gamma[c] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                stage[(8 * (r / 4) + 4 * fc + (r % 4)) * kWideOutStride + j * 32 + fr] = acc[i][j][r];
+        __syncthreads();  // this wave's rows are staged (waves share no rows)
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int lr = it * 4 + (lane >> 4);
+            const uint32_t row = row0 + wm * WM + i * 32 + lr;
+            if (row >= g.rows_p || col >= g.rows_q) break;  // n % 4 == 0: col + 3 < n as well
+            const int4 a = *reinterpret_cast<const int4*>(stage + lr * kWideOutStride + c4);
+            const float s_in = g.a_scales[row];
+            const int32_t av[4] = {a.x, a.y, a.z, a.w};
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = dequant(av[e], s_in, s_w[e], b[e]);
+            const uint64_t idx = (static_cast<uint64_t>(row) + g.out_row_offset) * g.n + col;
+            if (EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE) {
+                // add_scaled.glsl:26-30: residual + (addend * gamma)
+                const float4 res = *reinterpret_cast<const float4*>(g.residual + idx);
+                const float rv[4] = {res.x, res.y, res.z, res.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float scaled = v[e] * gam[e];
+                    v[e] = rv[e] + scaled;
+                }
+            }
+            *reinterpret_cast<float4*>(g.out + idx) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        if (i + 1 < TM) __syncthreads();  // the reads are done before the next block overwrites the stage
+    }
+}
+
+template <int BM, int EPI>
+void launch_wide_bm(const GemmParams& g, hipStream_t s) {
+    constexpr size_t lds = wide_lds<BM>();
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_i8_wide_kernel<BM, EPI>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    (void)attr;
+    const dim3 grid(ceil_div(g.rows_p, BM), ceil_div(g.rows_q, kWideBN), 1);
+    dispatch(gemm_i8_wide_kernel<BM, EPI>, grid, dim3(4 * BM), lds, s, g);
+}
+
+// One workgroup per CU (MI355X: 256 CUs), so the time goes as the rounds of
+// workgroups times the tile height: 192-row tiles unless 256 takes no longer.
+// fc2 (N = 1024, K = 4096, LayerScale), us for gemm_i8_kernel / 256-row /
+// 192-row tiles on one box: 10960 rows (one round of 172 or 232 tiles)
+// 84.3 / 75.0 / 69.8; 21908 rows (two rounds either way) 162.6 / 150.6 / 137.1.
+template <int EPI>
+void launch_wide(const GemmParams& g, hipStream_t s) {
+    constexpr uint32_t kCus = 256;
+    const uint32_t tn = ceil_div(g.rows_q, kWideBN);
+    auto cost = [&](uint32_t bm) { return ceil_div(static_cast<uint64_t>(ceil_div(g.rows_p, bm)) * tn, kCus) * bm; };
+    if (cost(192) < cost(256))
+        launch_wide_bm<192, EPI>(g, s);
+    else
+        launch_wide_bm<256, EPI>(g, s);
+}
+
 template <int BM, int BN, int WMW, int WNW, int BK, int STAGES, int EPI>
 void launch_cfg(const GemmParams& g, hipStream_t s, bool last = true) {
     // LDS: the stage ring, or the row-major output tile if that is larger.
@@ -511,6 +675,15 @@ void launch_epi(const GemmParams& g, hipStream_t s, bool last = true) {
     // Below that, from N = 4096 on (fc1 at batch 1), 128x64 tiles on eight
     // waves of 32x32 (20.4 -> 18.3 us at M = 1370): twice the waves of the
     // 96x64 tiles on the same CUs to hide the operand waits.
+    if constexpr (EPI == DAV2_GEMM_EPI_ROW || EPI == DAV2_GEMM_EPI_ROW_LAYERSCALE) {
+        // many rows and long K (fc2 from batch 8): the 32x32x32 kernel, whose
+        // float4 epilogue needs 16-byte aligned output and residual rows
+        if (g.rows_p >= kWideTileRows && g.k >= 4096 && g.k % 128 == 0 && g.k_split == g.k && g.coalesced_out &&
+            (EPI != DAV2_GEMM_EPI_ROW_LAYERSCALE || (reinterpret_cast<uintptr_t>(g.residual) & 15) == 0)) {
+            launch_wide<EPI>(g, s);
+            return;
+        }
+    }
     if constexpr (row_major_epi<EPI>() && EPI != DAV2_GEMM_EPI_ROW_COLMAX) {
         if (g.rows_p >= kWideTileRows) {
             if (g.rows_q >= kWideTileCols)

@@ -444,11 +444,16 @@ def _random_gemm_case(rng, m, n, k):
 # 256) and (700, 4100, 192) the 128x64 eight-wave tiles of N >= 4096 below
 # M = 4096;
 # (1370, 1024, 4096) and (300, 96, 2112): long K (fc2), the second with a
-# partial last stage
+# partial last stage; (4100, 1024, 4096) and (4097, 1020, 4224): the
+# 32x32x32 kernel of M >= 4096, K >= 4096 on 192-row tiles (ROW and
+# LayerScale; ragged M and N), (4100, 3000, 4096) on 256-row tiles (one round
+# of 204 tiles against two of 264); (4097, 1001, 4224): N % 4 != 0, which it
+# leaves to gemm_i8_kernel
 @pytest.mark.parametrize("m,n,k", [(1370, 384, 384), (1369, 96, 640), (300, 1024, 1024), (5477, 384, 384),
                                    (4100, 200, 192), (4097, 1001, 128), (4100, 3100, 192), (4097, 3073, 128),
                                    (6000, 4096, 1024), (1370, 4096, 256), (700, 4100, 192), (1370, 1024, 4096),
-                                   (300, 96, 2112)])
+                                   (300, 96, 2112), (4100, 1024, 4096), (4097, 1020, 4224),
+                                   (4100, 3000, 4096), (4097, 1001, 4224)])
 def test_gemm_row_epilogues(gpu, pkg, lib, oracle, m, n, k):
     torch = gpu
     _announce("gemm epilogues", m, n, k)
