@@ -174,6 +174,7 @@ PROTOTYPES = {
     "dav2_profile_report": (C.c_int, [vp, C.c_char_p, sz]),
     # HIP launcher layer
     "dav2_hip_quantize_rows_i8": (C.c_int, [vp, u64, u32, u32, vp, u32, vp, vp]),
+    "dav2_hip_gelu_quantize_rows_i8": (C.c_int, [vp, u64, u32, u32, vp, u32, vp, vp]),
     "dav2_hip_im2col_scratch_floats": (u64, [u32, u32, u32]),
     "dav2_hip_im2col_quantize_i8": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, vp, u32, vp, vp, u64, vp]),
     "dav2_hip_im2col_quantize_relu_i8": (C.c_int, [vp, u32, u32, u32, u32, u32, u32, u32, i32, vp, u32, vp, vp, u64, vp]),

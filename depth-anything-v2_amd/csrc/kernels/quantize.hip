@@ -26,8 +26,10 @@ constexpr int kRowsPerBlock = 4;
 // maximum is the maximum of the parts' maxima (exact, order-free). EXACT:
 // columns == 256 * CH * WPR (every chunk in the row). The products x * (1/s)
 // come first; a lane with a value near a half-integer redoes its chunks
-// with the guarded quotient (quantize_div).
-template <int CH, int WPR, bool EXACT>
+// with the guarded quotient (quantize_div). GELU: the row is gelu(x)
+// (gelu.glsl:16-49, gelu_erfcc) of the loaded values, as if a GELU pass had
+// written it first.
+template <int CH, int WPR, bool EXACT, bool GELU = false>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_kernel(
     const float* __restrict__ input, uint64_t input_offset, uint32_t rows,
     uint32_t columns, int8_t* __restrict__ q, uint32_t ldq,
@@ -46,6 +48,8 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void quantize_rows_kernel(
         const uint32_t w = w0 + lane + 64u * j;
         v[j] = live && (EXACT || w < words) ? *reinterpret_cast<const float4*>(x + 4u * w)
                                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (GELU)  // gelu(0) == 0, so the zero padding stays out of the maximum
+            v[j] = make_float4(gelu_erfcc(v[j].x), gelu_erfcc(v[j].y), gelu_erfcc(v[j].z), gelu_erfcc(v[j].w));
         absmax = fmaxf(absmax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
     }
     absmax = wave_max(absmax);
@@ -763,6 +767,26 @@ int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset, uint32_
     else
         dispatch(quantize_rows_long_kernel, dim3(grid), dim3(64 * kRowsPerBlock), 0, s,
                            input, input_offset, rows, columns, q, ldq, scales);
+#undef DAV2_QR_CASE
+    return hipGetLastError();
+}
+
+int dav2_hip_gelu_quantize_rows_i8(const float* input, uint64_t input_offset, uint32_t rows, uint32_t columns,
+                                   int8_t* q, uint32_t ldq, float* scales, void* stream) {
+    if (rows == 0) return hipSuccess;
+    if (!input || !q || !scales || columns == 0 || columns % 4u || columns > 4096u || ldq < columns ||
+        ldq % 64u || input_offset % 4u)
+        return hipErrorInvalidValue;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t ch = (columns / 4u + 63u) / 64u;
+#define DAV2_QR_CASE(N, W, E)                                                                    \
+    dispatch((quantize_rows_kernel<N, W, E, true>), dim3(ceil_div(rows, kRowsPerBlock / W)),     \
+             dim3(64 * kRowsPerBlock), 0, s, input, input_offset, rows, columns, q, ldq, scales)
+    if (columns == 4096u) DAV2_QR_CASE(4, 4, true);
+    else if (ch <= 2) DAV2_QR_CASE(2, 1, false);
+    else if (ch <= 4) DAV2_QR_CASE(4, 1, false);
+    else if (ch <= 8) DAV2_QR_CASE(4, 2, false);
+    else DAV2_QR_CASE(4, 4, false);
 #undef DAV2_QR_CASE
     return hipGetLastError();
 }

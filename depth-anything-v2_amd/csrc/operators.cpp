@@ -115,14 +115,15 @@ void HipOperators::linear_int8_in(DeviceBuffer& output, const DeviceBuffer& inpu
 }
 
 void HipOperators::quantize_rows(const DeviceBuffer& input, std::uint64_t input_offset, std::uint32_t rows,
-                                 std::uint32_t columns) {
+                                 std::uint32_t columns, bool gelu) {
     const std::uint32_t ld = ld64(columns);
     DeviceBuffer& packed = workspace_.packed(std::uint64_t(rows) * ld);
     DeviceBuffer& scales = workspace_.scales(std::uint64_t(rows) * sizeof(float));
-    ProfileScope prof(context_.profiler(), "quantize_rows_i8", 5.0 * rows * columns + 4.0 * rows, "B",
-                      stream());
-    hip_check(dav2_hip_quantize_rows_i8(input.as<float>(), input_offset, rows, columns, packed.as<int8_t>(), ld,
-                                        scales.as<float>(), stream()),
+    ProfileScope prof(context_.profiler(), gelu ? "gelu_quantize_rows_i8" : "quantize_rows_i8",
+                      5.0 * rows * columns + 4.0 * rows, "B", stream());
+    const auto quantize = gelu ? dav2_hip_gelu_quantize_rows_i8 : dav2_hip_quantize_rows_i8;
+    hip_check(quantize(input.as<float>(), input_offset, rows, columns, packed.as<int8_t>(), ld, scales.as<float>(),
+                       stream()),
               "quantize_rows_int8");
     workspace_ld_ = ld;
 }

@@ -191,9 +191,11 @@ public:
     // (layer_norm + quantize_rows of linear_int8); fp32 row optional.
     void layer_norm_quantize(const DeviceBuffer& input, const DeviceBuffer& weight, const DeviceBuffer& bias,
                              std::uint32_t rows, std::uint32_t columns, float epsilon, DeviceBuffer* fp32_out);
-    // quantize_rows of linear_int8 into the workspace.
+    // quantize_rows of linear_int8 into the workspace; gelu: of gelu(input)
+    // (the GELU pass of a linear_int8 with gelu, then the next linear's
+    // quantization), columns <= 4096.
     void quantize_rows(const DeviceBuffer& input, std::uint64_t input_offset, std::uint32_t rows,
-                       std::uint32_t columns);
+                       std::uint32_t columns, bool gelu = false);
     // GEMM on the rows currently held by the workspace.
     // row_colmax: row, and per GEMM row tile the maxima of |out| of the
     // columns from col_absmax_begin on into col_absmax

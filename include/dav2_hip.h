@@ -34,6 +34,16 @@ DAV2_API int dav2_hip_quantize_rows_i8(const float* input, uint64_t input_offset
                                        uint32_t rows, uint32_t columns, int8_t* q,
                                        uint32_t ldq, float* scales, void* stream);
 
+/* gelu.glsl:16-49 followed by quantize_rows_int8_fused.glsl:20-55 in one pass:
+ * the row quantized is gelu(input row), bit for bit what the reference's
+ * GELU pass after fc1 (linear_int8 with gelu, src/operators.cpp:837-843,
+ * called from src/encoder.cpp:525-528) and fc2's input quantization
+ * (src/operators.cpp:810-818) produce. Arguments as dav2_hip_quantize_rows_i8;
+ * columns <= 4096. */
+DAV2_API int dav2_hip_gelu_quantize_rows_i8(const float* input, uint64_t input_offset,
+                                            uint32_t rows, uint32_t columns, int8_t* q,
+                                            uint32_t ldq, float* scales, void* stream);
+
 /* int8 weight rows of `columns` bytes -- the reference GpuModel layout,
  * [rows][columns/4] little-endian words (src/gpu_model.cpp:241-284) -- to the
  * GEMM layout [rows][ld] (ld % 16 == 0, ld >= columns), bytes [columns, ld)

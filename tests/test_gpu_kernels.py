@@ -47,6 +47,33 @@ def test_quantize_rows_bit_exact(gpu, lib, oracle, rows, cols, offset_rows):
     assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,cols,offset_rows", [(37, 4096, 2), (300, 4096, 0), (9, 3072, 1), (17, 1536, 0),
+                                                   (5, 1000, 3), (3, 100, 0)])
+def test_gelu_quantize_rows_bit_exact(gpu, lib, oracle, rows, cols, offset_rows):
+    # the row quantized is gelu(x): the oracle's GELU pass, then its row quantizer
+    torch = gpu
+    _announce("gelu quantize_rows", rows, cols, offset_rows)
+    rng = np.random.default_rng(rows * cols + 7)
+    x = (rng.standard_normal((rows + offset_rows, cols)) * rng.uniform(0.01, 12, (rows + offset_rows, 1))).astype(np.float32)
+    x[offset_rows] = 0.0  # an all-zero row
+    if rows > 2:
+        x[offset_rows + 1] = -np.abs(x[offset_rows + 1]) - 20.0  # gelu flushes the whole row to (almost) zero
+    g = oracle.gelu(x)
+    q_ref, s_ref = oracle.quantize_rows(g, rows, cols, offset_rows * cols)
+    ld = (cols + 63) // 64 * 64
+    xd = dev(torch, x)
+    qd = torch.full((rows, ld), 0x55, dtype=torch.int8, device="cuda")
+    sd = empty(torch, (rows,), torch.float32)
+    ok(lib, lib.dav2_hip_gelu_quantize_rows_i8(ptr(xd), offset_rows * cols, rows, cols, ptr(qd), ld, ptr(sd),
+                                              stream(torch)))
+    q = host(torch, qd)
+    assert np.array_equal(q[:, :cols], q_ref)
+    assert np.all(q[:, cols:] == 0)
+    assert np.array_equal(host(torch, sd).view(np.uint32), s_ref.view(np.uint32))
+    # rows longer than the register-resident kernel holds are rejected
+    assert lib.dav2_hip_gelu_quantize_rows_i8(ptr(xd), 0, 1, 4100, ptr(qd), 4160, ptr(sd), stream(torch)) != 0
+
+
 def test_quantize_rows_packed_word_byte_order(gpu, lib):
     # quantize_rows_int8_fused.glsl:51: byte k of word w is column 4w+k.
     torch = gpu
