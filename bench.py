@@ -111,7 +111,10 @@ def cpu_preprocess_ms(width: int, height: int, input_size: int) -> float:
     return 1e3 * best
 
 
-BANDWIDTH_KERNELS = ("layer_norm_quantize_i8", "layer_norm", "softmax_f32", "quantize_rows_i8")
+# gelu_quantize_rows_i8 (fc2's input quantization with fc1's GELU, from 4096
+# rows) moves the bytes of quantize_rows_i8 but is bound by its GELU's VALU
+# work; its HBM rate is reported all the same.
+BANDWIDTH_KERNELS = ("layer_norm_quantize_i8", "layer_norm", "softmax_f32", "quantize_rows_i8", "gelu_quantize_rows_i8")
 
 
 def gemm_shape_table(prof: dict, steps: int) -> dict:
