@@ -3,7 +3,7 @@ im2col kernels against float64 products and torch's unfold, the fp32
 operators (src/operators.cpp:882-955, :1211-1452, :1528-1676, :1807-1861)
 against the oracle, and whole models against the oracle's fp32 graph.
 
-fp32 sums in a different order than the oracle's: the gate is the north-star
+fp32 sums in a different order than the oracle's: the gate is the depth
 tolerance, max|gpu - cpu| <= 1e-3 of the depth range; the operators are held
 to 1e-5 of their output's magnitude."""
 

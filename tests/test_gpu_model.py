@@ -2,7 +2,7 @@
 dav2_infer_tensor_f32 (src/dav2.cpp:158-213, :603-628) on seeded synthetic
 models, against the CPU oracle's int8 graph on the same inputs.
 
-Gate (north star): max|gpu - cpu| / (max(cpu) - min(cpu)) <= 1e-3 on the depth
+Gate: max|gpu - cpu| / (max(cpu) - min(cpu)) <= 1e-3 on the depth
 map, and on the pre-ReLU logits (random weights can zero most of the depth).
 """
 
